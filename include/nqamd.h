@@ -1,0 +1,151 @@
+/*
+ * nqamd.h — C ABI of the MI355X (gfx950) packed binary low-rank linear.
+ *
+ *   y = s_out ⊙ (U±1 · (s_mid ⊙ (V±1ᵀ · (s_in ⊙ x))))
+ *       + Σ_k x[:, idx_k] · W_sal[:, k] (· scale_k)      salient input columns
+ *       + patch_left · (patch_right · x)                  float low-rank patch
+ *       + scatter(row_idx, row_scale · (Q_rows · x))      int8 output-row sidecar
+ *       + bias
+ *
+ * U and V are sign matrices in layout llama.cpp-i32-lsb-v1: int32 words, column c
+ * in word c/32 at bit c%32, bit set = -1, pad bits 0.
+ *
+ * Conventions shared by every entry point:
+ *   - every pointer argument except `desc` and `out` parameters of the query
+ *     functions is a DEVICE pointer owned by the caller;
+ *   - `stream` is a hipStream_t passed as void*; kernels are enqueued on it and
+ *     nothing synchronises, allocates or frees device memory;
+ *   - the return value is an nq_status; nothing throws across the ABI.
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to the NanoQuant repository).
+ */
+#ifndef NQAMD_H
+#define NQAMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NQ_ABI_VERSION 1
+
+typedef enum nq_dtype {
+    NQ_DTYPE_F32 = 0,
+    NQ_DTYPE_F16 = 1,
+    NQ_DTYPE_BF16 = 2,
+    NQ_DTYPE_I8 = 3,
+    NQ_DTYPE_I32 = 4
+} nq_dtype;
+
+typedef enum nq_status {
+    NQ_OK = 0,
+    NQ_ERR_ARGUMENT = -1,    /* null pointer or inconsistent sizes          */
+    NQ_ERR_DTYPE = -2,       /* dtype code not accepted for that operand     */
+    NQ_ERR_SHAPE = -3,       /* dimension out of the supported range         */
+    NQ_ERR_ALIGNMENT = -4,   /* pointer alignment the kernel needs is missing */
+    NQ_ERR_WORKSPACE = -5,   /* workspace smaller than nq_linear_workspace_bytes */
+    NQ_ERR_LAUNCH = -6,      /* hipLaunchKernel / hipGetLastError failure    */
+    NQ_ERR_DEVICE = -7,      /* no HIP device or wrong architecture          */
+    NQ_ERR_UNSUPPORTED = -8  /* valid request this build does not implement  */
+} nq_status;
+
+/* Device facts used by the backend's capability check.
+ * Replaces the CUDA capability probe of CudaPackedBackend.supports
+ * (src/nanoquant/runtime/cuda_backend.py:174-197). */
+typedef struct nq_device_caps {
+    char arch[64];            /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+    int32_t compute_units;
+    int32_t wavefront_size;
+    int64_t lds_bytes_per_block;
+    int64_t global_mem_bytes;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width_bits;
+    int32_t is_gfx950;        /* 1 when the kernels in this library can run */
+} nq_device_caps;
+
+/* One packed linear. Sizes are element counts; word rows are contiguous.
+ * Replaces the operand list of launch_packed_linear
+ * (src/nanoquant/runtime/cuda_kernels.py:816-874) and the payload of
+ * CudaPackedBackend (src/nanoquant/runtime/cuda_backend.py:35-48). */
+typedef struct nq_linear_desc {
+    int64_t in_features;
+    int64_t out_features;
+    int64_t rank;
+    const int32_t* right_words;   /* V: [rank, ceil(in/32)]            */
+    const int32_t* left_words;    /* U: [out,  ceil(rank/32)]          */
+    const void* scale_pre;        /* [in]   (zero at salient columns)  */
+    const void* scale_mid;        /* [rank]                            */
+    const void* scale_post;       /* [out]                             */
+    int32_t scale_dtype;          /* F32/F16/BF16: scales, salient and row scales */
+    int32_t bias_dtype;           /* F32/F16/BF16                      */
+    const void* bias;             /* [out] or NULL                     */
+    int64_t salient_count;        /* k; 0 when absent                  */
+    const int32_t* salient_indices; /* [k] strictly increasing, < in  */
+    const void* salient_values;   /* [out, k]                          */
+    int32_t salient_dtype;        /* I8/F16/BF16/F32                   */
+    const void* salient_scales;   /* [k] (scale_dtype) when I8, else NULL */
+    int64_t patch_rank;           /* p; 0 when absent                  */
+    const void* patch_left;       /* [out, p]                          */
+    const void* patch_right;      /* [p, in]                           */
+    int32_t patch_dtype;          /* F32/F16/BF16                      */
+    int64_t row_count;            /* output-row sidecar rows; 0 when absent */
+    const int32_t* row_indices;   /* [row_count] strictly increasing, < out */
+    const int8_t* row_values;     /* [row_count, in]                   */
+    const void* row_scales;       /* [row_count] (scale_dtype)         */
+    const void* tiles;            /* GPU layout from nq_prepare_tiles, or NULL */
+    int64_t tiles_bytes;
+} nq_linear_desc;
+
+/* Library ABI version (NQ_ABI_VERSION). No reference counterpart. */
+int nq_abi_version(void);
+
+/* Human-readable text for a status code. No reference counterpart. */
+const char* nq_status_string(int status);
+
+/* Device query; see nq_device_caps. */
+int nq_query_device(int device, nq_device_caps* out);
+
+/* Bit-exact unpack of sign words to dense ±1 in F32/F16/BF16, row-major
+ * [rows, cols]. Replaces unpack_sign_matrix
+ * (src/nanoquant/runtime/packed.py:204-218) for device tensors. */
+int nq_unpack_signs(const int32_t* words, int64_t rows, int64_t cols,
+                    int64_t row_stride_words, int32_t out_dtype, void* out,
+                    void* stream);
+
+/* Count rows whose pad bits (columns >= cols in the last word) are non-zero;
+ * writes one int32 to *bad_rows (device). Device form of the padding check in
+ * _validate_packed_matrix (src/nanoquant/runtime/packed.py:189-201). */
+int nq_count_bad_padding(const int32_t* words, int64_t rows, int64_t cols,
+                         int64_t row_stride_words, int32_t* bad_rows, void* stream);
+
+/* Size in bytes of the GPU-private tiled weight layout for one linear. */
+int64_t nq_tiles_bytes(int64_t in_features, int64_t out_features, int64_t rank);
+
+/* Re-tile the canonical U and V words of `desc` into the GPU-private decode
+ * layout at `tiles` (nq_tiles_bytes bytes). Prepare-time; replaces the
+ * one-time device copy in CudaPackedBackend.prepare
+ * (src/nanoquant/runtime/cuda_backend.py:199-241). */
+int nq_prepare_tiles(const nq_linear_desc* desc, void* tiles, int64_t tiles_bytes,
+                     void* stream);
+
+/* Workspace bytes nq_linear needs for `tokens` token slots. */
+int64_t nq_linear_workspace_bytes(const nq_linear_desc* desc, int64_t tokens);
+
+/* y[tokens, out] = linear(x[tokens, in]). x dtype F32/F16/BF16; y dtype F32
+ * (the reference backend's output) or BF16/F16. Decode kernels for
+ * tokens <= 16, the MFMA prefill kernel above. Replaces launch_packed_linear
+ * (src/nanoquant/runtime/cuda_kernels.py:816-874) and CudaPackedBackend.linear
+ * (src/nanoquant/runtime/cuda_backend.py:243-278). */
+int nq_linear(const nq_linear_desc* desc, const void* x, int32_t x_dtype,
+              int64_t tokens, void* y, int32_t y_dtype, void* workspace,
+              int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NQAMD_H */

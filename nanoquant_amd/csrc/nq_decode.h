@@ -1,0 +1,18 @@
+// Tiled-layout decode path (token counts the fused MFMA kernel covers).
+#pragma once
+
+#include "nq_common.h"
+
+namespace nq {
+
+// Extra workspace bytes the tiled decode path needs for `tokens` slots.
+int64_t decode_scratch_bytes(const nq_linear_desc* d, int64_t tokens);
+
+// True when desc->tiles is set and the tiled decode kernel handles `tokens`.
+bool decode_path_applies(const nq_linear_desc* d, int64_t tokens);
+
+// Launch the tiled decode path; scratch is decode_scratch_bytes(d, tokens) bytes.
+int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y,
+                  int y_dtype, void* scratch, hipStream_t stream);
+
+}  // namespace nq

@@ -1,0 +1,298 @@
+"""HIP backend for the packed binary low-rank linear on MI355X (gfx950).
+
+Drop-in for the reference's GPU packed backend ``CudaPackedBackend``
+(src/nanoquant/runtime/cuda_backend.py:151-278): same protocol, capability
+declaration, error convention (misuse raises ``ValueError``/``TypeError``;
+capability gaps are returned as ``SupportResult.rejected`` codes) and the same
+fp32 output boundary. ``linear`` validates, allocates the output and workspace
+from torch's caching allocator and enqueues the HIP kernels on torch's current
+stream through the C ABI; it never synchronises, transfers or unpacks.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, field, replace
+
+import torch
+
+from nanoquant_amd.runtime import _native
+from nanoquant_amd.runtime.backend import (
+    BackendCapabilities,
+    DeviceLike,
+    PreparedLayer,
+    QuantizedLinearSpec,
+    RuntimeLayerState,
+    SupportResult,
+    WorkloadSpec,
+    evaluate_capabilities,
+)
+from nanoquant_amd.runtime.logical import canonical_torch_dtype
+from nanoquant_amd.runtime.packed import PACKED_LAYOUT_VERSION, PackedLayerState
+from nanoquant_amd.runtime.row_sidecar import RowSidecarLayerState
+
+HIP_PACKED_BACKEND_NAME = "rocm-packed-hip"
+HIP_PACKED_BACKEND_VERSION = "1"
+_FLOAT_DTYPES = ("float16", "bfloat16", "float32")
+_REQUIRED_ARCH = "gfx950"
+
+
+@dataclass(frozen=True, slots=True)
+class _HipPackedPayload:
+    device: torch.device
+    left_words: torch.Tensor
+    right_words: torch.Tensor
+    scale_pre: torch.Tensor
+    scale_mid: torch.Tensor
+    scale_post: torch.Tensor
+    bias: torch.Tensor | None
+    outlier_indices: torch.Tensor | None
+    outlier_values: torch.Tensor | None
+    outlier_scales: torch.Tensor | None
+    patch_left: torch.Tensor | None
+    patch_right: torch.Tensor | None
+    row_indices: torch.Tensor | None
+    row_values: torch.Tensor | None
+    row_scales: torch.Tensor | None
+    tiles: torch.Tensor | None
+    desc: _native.LinearDesc = field(repr=False)
+
+
+def _to_device(tensor: torch.Tensor | None, device: torch.device) -> torch.Tensor | None:
+    return None if tensor is None else tensor.to(device=device).contiguous()
+
+
+def _device_arch(index: int) -> str:
+    return str(getattr(torch.cuda.get_device_properties(index), "gcnArchName", ""))
+
+
+def _describe(
+    p: _HipPackedPayload, spec: QuantizedLinearSpec, desc: _native.LinearDesc
+) -> None:
+    """Fill the C descriptor with the payload's device pointers."""
+
+    ptr = _native.pointer
+    desc.in_features = spec.in_features
+    desc.out_features = spec.out_features
+    desc.rank = spec.rank
+    desc.right_words = ptr(p.right_words)
+    desc.left_words = ptr(p.left_words)
+    desc.scale_pre = ptr(p.scale_pre)
+    desc.scale_mid = ptr(p.scale_mid)
+    desc.scale_post = ptr(p.scale_post)
+    desc.scale_dtype = _native.dtype_code(p.scale_pre.dtype)
+    if p.bias is not None:
+        desc.bias = ptr(p.bias)
+        desc.bias_dtype = _native.dtype_code(p.bias.dtype)
+    if p.outlier_indices is not None and p.outlier_values is not None:
+        desc.salient_count = int(p.outlier_indices.numel())
+        desc.salient_indices = ptr(p.outlier_indices)
+        desc.salient_values = ptr(p.outlier_values)
+        desc.salient_dtype = _native.dtype_code(p.outlier_values.dtype)
+        desc.salient_scales = ptr(p.outlier_scales)
+    if p.patch_left is not None and p.patch_right is not None:
+        desc.patch_rank = int(p.patch_left.shape[1])
+        desc.patch_left = ptr(p.patch_left)
+        desc.patch_right = ptr(p.patch_right)
+        desc.patch_dtype = _native.dtype_code(p.patch_left.dtype)
+    if p.row_indices is not None:
+        desc.row_count = int(p.row_indices.numel())
+        desc.row_indices = ptr(p.row_indices)
+        desc.row_values = ptr(p.row_values)
+        desc.row_scales = ptr(p.row_scales)
+
+
+class HipPackedBackend:
+    """gfx950 HIP kernels behind the reference backend protocol."""
+
+    name = HIP_PACKED_BACKEND_NAME
+    version = HIP_PACKED_BACKEND_VERSION
+    packed_layout = PACKED_LAYOUT_VERSION
+
+    def __init__(self, *, tiled_decode: bool = True) -> None:
+        self._tiled_decode = tiled_decode
+
+    def capabilities(self) -> BackendCapabilities:
+        return BackendCapabilities(
+            logical_formats=("nanoquant-v1",),
+            device_types=("cuda",),
+            input_dtypes=_FLOAT_DTYPES,
+            factor_dtypes=_FLOAT_DTYPES,
+            scale_dtypes=_FLOAT_DTYPES,
+            outlier_value_dtypes=(*_FLOAT_DTYPES, "int8"),
+            workload_kinds=("prefill", "decode"),
+            supports_bias=True,
+            supports_outliers=True,
+            supports_deterministic=True,
+            patch_value_dtypes=_FLOAT_DTYPES,
+        )
+
+    def supports(self, op: QuantizedLinearSpec, workload: WorkloadSpec) -> SupportResult:
+        result = evaluate_capabilities(self.capabilities(), op, workload)
+        if not result.supported:
+            return result
+        if not _native.library_available():
+            return SupportResult.rejected(
+                "NQ-INF-HIP-KERNEL", "the HIP library libnqamd.so is not built"
+            )
+        if not torch.cuda.is_available():
+            return SupportResult.rejected(
+                "NQ-INF-DEVICE-UNAVAILABLE", "CUDA is not available in this runtime"
+            )
+        arch = _device_arch(torch.cuda.current_device())
+        if not arch.startswith(_REQUIRED_ARCH):
+            return SupportResult.rejected(
+                "NQ-INF-HIP-ARCH", f"device architecture {arch!r} is not {_REQUIRED_ARCH}"
+            )
+        return result
+
+    def prepare(self, state: RuntimeLayerState, device: DeviceLike) -> PreparedLayer:
+        if isinstance(state, RowSidecarLayerState):
+            packed, rows = state.base, state.rows
+        elif isinstance(state, PackedLayerState):
+            packed, rows = state, None
+        else:
+            raise TypeError("HIP packed backend requires PackedLayerState or RowSidecarLayerState")
+        target = torch.device(device)
+        if target.type != "cuda":
+            raise ValueError("HIP packed backend preparation requires a CUDA (HIP) device")
+        if not torch.cuda.is_available():
+            raise RuntimeError("CUDA is not available in this runtime")
+        if target.index is None:
+            target = torch.device("cuda", torch.cuda.current_device())
+        lib = _native.load()
+        payload = _HipPackedPayload(
+            target,
+            _to_device(packed.left_words, target),
+            _to_device(packed.right_words, target),
+            _to_device(packed.scale_pre, target),
+            _to_device(packed.scale_mid, target),
+            _to_device(packed.scale_post, target),
+            _to_device(packed.bias, target),
+            _to_device(packed.outlier_indices, target),
+            _to_device(packed.outlier_values, target),
+            _to_device(packed.outlier_scales, target),
+            _to_device(packed.patch_left, target),
+            _to_device(packed.patch_right, target),
+            None if rows is None else _to_device(rows.indices, target),
+            None if rows is None else _to_device(rows.values, target),
+            None if rows is None else _to_device(rows.scales, target),
+            None,
+            _native.LinearDesc(),
+        )
+        _describe(payload, packed.spec, payload.desc)
+        spec = packed.spec
+        size = int(lib.nq_tiles_bytes(spec.in_features, spec.out_features, spec.rank))
+        if self._tiled_decode and size > 0:
+            tiles = torch.empty(size, dtype=torch.uint8, device=target)
+            with torch.cuda.device(target):
+                _native.check(
+                    "nq_prepare_tiles",
+                    lib.nq_prepare_tiles(
+                        ctypes.byref(payload.desc),
+                        tiles.data_ptr(),
+                        size,
+                        _native.current_stream_handle(target),
+                    ),
+                )
+            payload = replace(payload, tiles=tiles)
+            payload.desc.tiles = tiles.data_ptr()
+            payload.desc.tiles_bytes = size
+        return PreparedLayer(self.name, self.version, packed.spec, payload)
+
+    def linear(self, value: torch.Tensor, layer: PreparedLayer) -> torch.Tensor:
+        return self.linear_into(value, layer, output_dtype=torch.float32)
+
+    def linear_into(
+        self,
+        value: torch.Tensor,
+        layer: PreparedLayer,
+        *,
+        output_dtype: torch.dtype = torch.float32,
+        out: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """``linear`` with an explicit output dtype (fp32 boundary by default;
+        bf16/f16 stores fuse the cast) and an optional preallocated output."""
+
+        if (layer.backend_name, layer.backend_version) != (self.name, self.version):
+            raise ValueError("prepared runtime layer belongs to a different backend")
+        payload = layer.payload
+        if not isinstance(payload, _HipPackedPayload):
+            raise TypeError("prepared runtime layer has an invalid HIP packed payload")
+        spec = layer.spec
+        if value.device != payload.device:
+            raise ValueError("HIP packed input and prepared layer must use the same device")
+        if canonical_torch_dtype(value.dtype) not in _FLOAT_DTYPES:
+            raise ValueError(f"HIP packed input dtype is unsupported: {value.dtype}")
+        if value.ndim == 0 or value.shape[-1] != spec.in_features:
+            raise ValueError("HIP packed input feature dimension differs from the layer")
+        if value.numel() == 0:
+            raise ValueError("HIP packed input must contain at least one token")
+        if not value.is_contiguous():
+            raise ValueError("HIP packed input must be contiguous")
+        if value.requires_grad:
+            raise ValueError("HIP packed runtime does not support autograd")
+        if output_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise ValueError(f"HIP packed output dtype is unsupported: {output_dtype}")
+        tokens = value.numel() // spec.in_features
+        shape = (*value.shape[:-1], spec.out_features)
+        if out is None:
+            out = torch.empty(shape, dtype=output_dtype, device=value.device)
+        elif tuple(out.shape) != shape or out.dtype != output_dtype or not out.is_contiguous():
+            raise ValueError("HIP packed output tensor shape, dtype or layout differs")
+        lib = _native.load()
+        desc = payload.desc
+        ws_bytes = int(lib.nq_linear_workspace_bytes(ctypes.byref(desc), tokens))
+        if ws_bytes < 0:
+            raise ValueError("HIP packed layer descriptor was rejected")
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=value.device)
+        status = lib.nq_linear(
+            ctypes.byref(desc),
+            value.data_ptr(),
+            _native.dtype_code(value.dtype),
+            tokens,
+            out.data_ptr(),
+            _native.dtype_code(output_dtype),
+            workspace.data_ptr(),
+            ws_bytes,
+            _native.current_stream_handle(value.device),
+        )
+        _native.check("nq_linear", status)
+        return out
+
+
+def unpack_sign_matrix_device(
+    words: torch.Tensor,
+    rows: int,
+    columns: int,
+    *,
+    dtype: torch.dtype = torch.float32,
+) -> torch.Tensor:
+    """Bit-exact HIP unpack of device sign words to dense +/-1
+    (device form of src/nanoquant/runtime/packed.py:204-218)."""
+
+    if words.device.type != "cuda":
+        raise ValueError("device unpack requires words on a HIP device")
+    stride = -(-columns // 32)
+    if words.dtype != torch.int32 or tuple(words.shape) != (rows, stride) or not words.is_contiguous():
+        raise ValueError(
+            f"packed sign matrix must be contiguous int32 with shape {(rows, stride)}, got "
+            f"{words.dtype} {tuple(words.shape)}"
+        )
+    out = torch.empty(rows, columns, dtype=dtype, device=words.device)
+    lib = _native.load()
+    bad = torch.empty(1, dtype=torch.int32, device=words.device)
+    stream = _native.current_stream_handle(words.device)
+    _native.check(
+        "nq_count_bad_padding",
+        lib.nq_count_bad_padding(words.data_ptr(), rows, columns, stride, bad.data_ptr(), stream),
+    )
+    if int(bad.item()) != 0:
+        raise ValueError("packed sign matrix has a non-zero padding bit")
+    _native.check(
+        "nq_unpack_signs",
+        lib.nq_unpack_signs(
+            words.data_ptr(), rows, columns, stride, _native.dtype_code(dtype), out.data_ptr(), stream
+        ),
+    )
+    return out

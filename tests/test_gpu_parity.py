@@ -1,0 +1,311 @@
+"""HIP parity against the CPU oracle (run on an MI355X: ``pytest -m gpu``).
+
+Bar: bit-exact for unpacked signs; fp outputs within the reference tests'
+``rtol=2e-5, atol=2e-4`` on the small fixtures and within relative L2 2e-3 of
+the oracle's fp32 forward at the benchmark shapes; bit-exact replay.
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+from dataclasses import replace
+from itertools import product
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from nanoquant_amd import synthetic as syn
+from nanoquant_amd.runtime import (
+    HipPackedBackend,
+    LogicalLayerState,
+    PreparedLinear,
+    QuantizedLinearSpec,
+    WorkloadSpec,
+    execution_workload,
+    pack_logical_layer,
+    pack_sign_matrix,
+    plan_execution_workloads,
+    prepare_execution_workloads,
+    unpack_sign_matrix_device,
+)
+from oracle import nq_oracle as orc
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a HIP device"),
+]
+
+REL_L2 = 2e-3  # north-star tolerance against the fp32 reference forward
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_fixtures.json").read_text())
+_FLOATS = (torch.float16, torch.bfloat16, torch.float32)
+
+
+def _say(*parts) -> None:
+    print("[case]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def backend() -> HipPackedBackend:
+    return HipPackedBackend()
+
+
+def _run(backend, state, x):
+    layer = backend.prepare(state, "cuda")
+    return backend.linear(x.cuda(), layer), layer
+
+
+# --- unpack ------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 1), (3, 31), (2, 32), (5, 33), (4, 65), (819, 4096), (3072, 819)])
+@pytest.mark.parametrize("dtype", _FLOATS)
+def test_device_unpack_bit_exact(rows, cols, dtype):
+    _say("unpack", rows, cols, dtype)
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    signs = torch.where(torch.rand(rows, cols, generator=g) < 0.5, -1.0, 1.0)
+    words = pack_sign_matrix(signs)
+    out = unpack_sign_matrix_device(words.cuda(), rows, cols, dtype=dtype)
+    expected = orc.unpack_signs(words.numpy(), rows, cols)
+    assert out.dtype == dtype
+    assert np.array_equal(out.float().cpu().numpy(), expected.astype(np.float32))
+    # Bit patterns, not just values: +1 / -1 exactly.
+    assert torch.equal(out.cpu(), torch.from_numpy(expected).to(dtype))
+
+
+def test_device_unpack_rejects_padding():
+    words = pack_sign_matrix(torch.ones(4, 33))
+    words[2, -1] = 2
+    with pytest.raises(ValueError, match="non-zero padding bit"):
+        unpack_sign_matrix_device(words.cuda(), 4, 33)
+
+
+# --- reference fixtures ----------------------------------------------------------------
+
+
+def test_golden_fixture_on_gpu(backend):
+    f = next(f for f in GOLDEN["fixtures"] if f["name"].startswith("packed_35x3"))
+    _say("golden", f["name"])
+    spec = QuantizedLinearSpec("blocks.0.linear", "nanoquant-v1", 35, 3, 33, "float32", "float32",
+                               outlier_count=2, outlier_value_dtype="int8",
+                               has_outlier_scales=True, has_bias=True)
+    logical = LogicalLayerState(
+        spec,
+        torch.tensor(f["left"], dtype=torch.float32),
+        torch.tensor(f["right"], dtype=torch.float32),
+        torch.tensor(f["scale_pre"], dtype=torch.float32),
+        torch.tensor(f["scale_mid"], dtype=torch.float32),
+        torch.tensor(f["scale_post"], dtype=torch.float32),
+        torch.tensor(f["bias"], dtype=torch.float32),
+        torch.tensor(f["outlier_indices"], dtype=torch.int32),
+        torch.tensor(f["outlier_values"], dtype=torch.int8),
+        torch.tensor(f["outlier_scales"], dtype=torch.float32),
+    )
+    packed = pack_logical_layer(logical)
+    assert packed.left_words.tolist() == f["left_words"]
+    y, _ = _run(backend, packed, torch.tensor(f["x"], dtype=torch.float32))
+    torch.testing.assert_close(y.cpu().double(), torch.tensor(f["expected_y"], dtype=torch.float64),
+                               rtol=2e-5, atol=2e-4)
+
+
+def _matrix_state(factor_dtype, scale_dtype, outlier_dtype, bias) -> LogicalLayerState:
+    """35->17, rank 33 word-tail geometry with salient columns {0, 17, 34}
+    (geometry of tests/unit/test_runtime_cuda_matrix.py:37-113)."""
+
+    in_f, out_f, rank = 35, 17, 33
+    count = 0 if outlier_dtype is None else 3
+    spec = QuantizedLinearSpec(
+        "blocks.0.self_attn.q_proj", "nanoquant-v1", in_f, out_f, rank,
+        str(factor_dtype).removeprefix("torch."), str(scale_dtype).removeprefix("torch."),
+        outlier_count=count,
+        outlier_value_dtype=None if outlier_dtype is None else str(outlier_dtype).removeprefix("torch."),
+        has_outlier_scales=outlier_dtype is torch.int8, has_bias=bias,
+    )
+    g = torch.Generator().manual_seed(20260715)
+    left = torch.where(torch.rand(out_f, rank, generator=g) > 0.5, 1.0, -1.0).to(factor_dtype)
+    right = torch.where(torch.rand(rank, in_f, generator=g) > 0.5, 1.0, -1.0).to(factor_dtype)
+    pre = torch.randn(in_f, generator=g).to(scale_dtype)
+    idx = torch.tensor((0, 17, 34), dtype=torch.int32) if count else None
+    if idx is not None:
+        pre[idx.long()] = 0
+    if outlier_dtype is None:
+        values = None
+    elif outlier_dtype is torch.int8:
+        values = torch.randint(-8, 8, (out_f, count), generator=g, dtype=torch.int8)
+    else:
+        values = torch.randn(out_f, count, generator=g).to(outlier_dtype)
+    return LogicalLayerState(
+        spec, left, right, pre,
+        torch.randn(rank, generator=g).to(scale_dtype),
+        torch.randn(out_f, generator=g).to(scale_dtype),
+        bias=torch.randn(out_f, generator=g).to(scale_dtype) if bias else None,
+        outlier_indices=idx, outlier_values=values,
+        outlier_scales=torch.tensor((0.125, 0.25, 0.375), dtype=scale_dtype) if outlier_dtype is torch.int8 else None,
+    )
+
+
+def test_full_dtype_salient_workload_matrix(backend):
+    """Every factor x scale x salient x bias x input dtype x workload combination."""
+
+    executed = 0
+    for factor, scale, outlier, bias in product(_FLOATS, _FLOATS, (None, *_FLOATS, torch.int8), (False, True)):
+        logical = _matrix_state(factor, scale, outlier, bias)
+        packed = pack_logical_layer(logical)
+        layer = backend.prepare(packed, "cuda:0")
+        oracle_fwd = orc.CpuPackedForward(orc.operands_from_state(packed))
+        for input_dtype, kind in product(_FLOATS, ("prefill", "decode")):
+            shape = (2, 3) if kind == "prefill" else (2,)
+            work = WorkloadSpec(kind, "cuda", str(input_dtype).removeprefix("torch."), 2,
+                                3 if kind == "prefill" else 1, deterministic=True)
+            assert backend.supports(packed.spec, work).supported
+            x = torch.linspace(-0.75, 0.875, 35 * (6 if kind == "prefill" else 2), dtype=input_dtype)
+            x = x.reshape(*shape, 35)
+            actual = backend.linear(x.cuda(), layer)
+            repeated = backend.linear(x.cuda(), layer)
+            case = (factor, scale, outlier, bias, input_dtype, kind)
+            assert actual.dtype == torch.float32
+            torch.testing.assert_close(actual.cpu(), oracle_fwd(x), rtol=2e-5, atol=2e-4,
+                                       msg=lambda m, case=case: f"{case}: {m}")
+            assert torch.equal(actual, repeated), case
+            executed += 1
+    assert executed == 540
+
+
+def test_more_than_one_salient_tile_and_patch(backend):
+    logical = _matrix_state(torch.float32, torch.float32, torch.float32, False)
+    g = torch.Generator().manual_seed(99)
+    spec = replace(logical.spec, outlier_count=33, patch_rank=2, patch_value_dtype="float32")
+    idx = torch.arange(33, dtype=torch.int32)
+    pre = logical.scale_pre.clone()
+    pre[:33] = 0
+    state = LogicalLayerState(
+        spec, logical.left_binary, logical.right_binary, pre, logical.scale_mid, logical.scale_post,
+        None, idx, torch.randn(17, 33, generator=g), None,
+        torch.randn(17, 2, generator=g), torch.randn(2, 35, generator=g),
+    )
+    packed = pack_logical_layer(state)
+    x = torch.linspace(-0.5, 0.75, 70, dtype=torch.float32).reshape(2, 35)
+    y, _ = _run(backend, packed, x)
+    torch.testing.assert_close(y.cpu(), orc.packed_forward(orc.operands_from_state(packed), x),
+                               rtol=2e-5, atol=2e-4)
+
+
+@pytest.mark.parametrize("shape", [(32, 16, 24, 1, 0), (33, 17, 25, 1, 3), (64, 32, 48, 4, 4),
+                                   (64, 32, 48, 8, 2), (96, 64, 64, 8, 7)])
+def test_llama_cpp_backend_ops_cases(backend, shape):
+    """Shapes of the llama.cpp test-backend-ops NanoQuant cases with their
+    deterministic F16 salient weights ((o*5 + s*3) % 19 - 9) / 128."""
+
+    in_f, rank, out_f, cols, k = shape
+    _say("backend-ops", shape)
+    base = syn.synthetic_packed_layer(syn.LinearShape("blocks.0.t", in_f, out_f, rank), seed=sum(shape),
+                                      salient=k, salient_dtype=torch.float16 if k else None)
+    if k:
+        o = torch.arange(out_f).reshape(-1, 1)
+        s = torch.arange(k).reshape(1, -1)
+        values = (((o * 5 + s * 3) % 19 - 9) * 0.0078125).to(torch.float16)
+        base = replace(base, outlier_values=values.contiguous())
+    x = syn.synthetic_activations(cols, in_f, seed=1, dtype=torch.float32)
+    y, _ = _run(backend, base, x)
+    torch.testing.assert_close(y.cpu(), orc.packed_forward(orc.operands_from_state(base), x), rtol=2e-5, atol=2e-4)
+
+
+# --- benchmark shapes ----------------------------------------------------------------
+
+
+def _check_shape(backend, state, tokens, seed):
+    x = syn.synthetic_activations(tokens, state.spec.in_features, seed=seed)
+    layer = backend.prepare(state, "cuda")
+    y = backend.linear(x.cuda(), layer)
+    y2 = backend.linear(x.cuda(), layer)
+    expected = orc.packed_forward(orc.operands_from_state(state), x)
+    err = orc.relative_l2(y, expected)
+    assert err <= REL_L2, (state.spec.name, tokens, err)
+    assert torch.equal(y, y2)
+    return err
+
+
+def test_gemma3_1b_gate_decode(backend):
+    shape = syn.gemma3_1b_gate()
+    _say("gemma gate", shape)
+    state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 0)
+    _check_shape(backend, state, 1, seed=1)
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 16])
+def test_qwen3_8b_layer_decode(backend, tokens):
+    for i, shape in enumerate(syn.qwen3_8b_layer()):
+        _say("qwen", shape.name, tokens)
+        state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 1 + i)
+        _check_shape(backend, state, tokens, seed=tokens + i)
+
+
+@pytest.mark.parametrize("tokens", [64])
+def test_llama3_8b_prefill(backend, tokens):
+    for i, shape in enumerate(syn.llama3_8b_layer()):
+        _say("llama", shape.name, tokens)
+        state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 2 + i)
+        _check_shape(backend, state, tokens, seed=tokens + i)
+
+
+@pytest.mark.parametrize("tokens", [1, 8])
+def test_gemma3_4b_down_with_sidecars(backend, tokens):
+    shape = syn.gemma3_4b_down()
+    _say("gemma down sidecars", tokens)
+    column = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 3, salient=26, bias=True)
+    _check_shape(backend, column, tokens, seed=tokens)
+    plain = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 3)
+    rows = syn.synthetic_row_sidecar(plain, 26, seed=syn.BASE_SEED + 4)
+    _check_shape(backend, rows, tokens, seed=tokens)
+
+
+# --- integration ---------------------------------------------------------------------
+
+
+def test_planner_and_module_on_gpu(backend):
+    logical = _matrix_state(torch.float32, torch.bfloat16, torch.bfloat16, True)
+    packed = pack_logical_layer(logical)
+    plans = plan_execution_workloads(
+        (packed.spec,),
+        prefill=WorkloadSpec("prefill", "cuda", "bfloat16", 1, 4, deterministic=True),
+        decode=WorkloadSpec("decode", "cuda", "bfloat16", 1, 1, deterministic=True),
+        prefill_backends=(backend,), decode_backends=(backend,), strict=True,
+    )
+    prepared = prepare_execution_workloads(plans, {packed.spec.name: packed}, (backend,), "cuda")
+    assert prepared.prefill.dispatches[0].layer is prepared.decode.dispatches[0].layer
+    prefill = torch.linspace(-1, 1, 140, dtype=torch.bfloat16).reshape(1, 4, 35).cuda()
+    decode = prefill[:, -1, :].contiguous()
+    fwd = orc.CpuPackedForward(orc.operands_from_state(packed))
+    torch.testing.assert_close(prepared.prefill.linear_at(0, prefill).cpu(), fwd(prefill.cpu()), rtol=2e-5, atol=2e-4)
+    torch.testing.assert_close(prepared.decode.linear_at(0, decode).cpu(), fwd(decode.cpu()), rtol=2e-5, atol=2e-4)
+    module = PreparedLinear(prepared, 0)
+    with execution_workload("decode"):
+        out = module(decode)
+    assert out.dtype == torch.bfloat16
+
+
+def test_hip_graph_capture_replays_match_eager(backend):
+    shape = syn.qwen3_8b_layer()[1]
+    state = syn.synthetic_packed_layer(shape, seed=7)
+    layer = backend.prepare(state, "cuda")
+    x = syn.synthetic_activations(1, shape.in_features, seed=3, device="cuda")
+    eager = backend.linear(x, layer)
+    static_out = torch.empty_like(eager)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        backend.linear_into(x, layer, out=static_out)  # warm the allocator off-graph
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        backend.linear_into(x, layer, out=static_out)
+    for _ in range(3):
+        static_out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager)
+        _ = backend.linear(x, layer)  # eager work between replays
+        torch.cuda.synchronize()

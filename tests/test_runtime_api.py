@@ -1,0 +1,326 @@
+"""Host-side runtime API: layout helpers, layer-state invariants, capability
+codes, planner behaviour and the module binding. Mirrors the reference's
+tests/unit/test_runtime_{packed,backend,execution_plans}.py behaviour with
+fake backends; no GPU needed."""
+
+from __future__ import annotations
+
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from nanoquant_amd.runtime import (
+    GGUF_TENSOR_SUFFIXES,
+    PACKED_LAYOUT_VERSION,
+    PACKED_REFERENCE_COMMIT,
+    PACKED_REFERENCE_CUDA_SHA256,
+    BackendCapabilities,
+    BackendPlanningError,
+    ExecutionPlans,
+    HipPackedBackend,
+    LogicalLayerState,
+    PackedLayerState,
+    PackedLayoutMetadata,
+    PreparedLayer,
+    PreparedLinear,
+    QuantizedLinearSpec,
+    SupportResult,
+    WorkloadSpec,
+    bind_prepared_linears,
+    evaluate_capabilities,
+    execution_workload,
+    pack_logical_layer,
+    pack_sign_matrix,
+    packed_row_stride_bytes,
+    packed_word_count,
+    plan_backends,
+    plan_execution_workloads,
+    prepare_execution_workloads,
+    prepare_plan,
+    summarize_benchmark,
+    supports_vector_word_loads,
+    unpack_sign_matrix,
+)
+from nanoquant_amd.runtime import _native
+from nanoquant_amd.synthetic import qwen3_8b_layer, synthetic_packed_layer, synthetic_row_sidecar
+from oracle import nq_oracle as orc
+
+# --- layout ----------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("columns", (1, 31, 32, 33, 65, 128))
+def test_host_pack_unpack_is_bit_exact_with_oracle(columns):
+    values = torch.where(torch.arange(3 * columns).reshape(3, columns) % 3 == 0, -1.0, 1.0)
+    packed = pack_sign_matrix(values)
+    assert packed.dtype == torch.int32 and packed.shape == (3, packed_word_count(columns))
+    assert np.array_equal(packed.numpy(), orc.pack_signs(values.numpy().astype(np.int8)))
+    assert torch.equal(unpack_sign_matrix(packed, 3, columns), values)
+
+
+def test_host_pack_known_answer_words():
+    values = torch.ones(2, 32)
+    values[0, (0, 1, 31)] = -1
+    values[1] = -1
+    packed = pack_sign_matrix(values)
+    assert int(packed[0, 0]) == -(2**31) + 3
+    assert int(packed[1, 0]) == -1
+
+
+def test_host_unpack_rejects_padding():
+    packed = pack_sign_matrix(torch.ones(1, 33))
+    packed[0, -1] = 2
+    with pytest.raises(ValueError, match="non-zero padding bit"):
+        unpack_sign_matrix(packed, 1, 33)
+
+
+def test_row_stride_and_vector_predicate():
+    assert packed_row_stride_bytes(33) == 8
+    assert packed_row_stride_bytes(128) == 16
+    assert not supports_vector_word_loads(pack_sign_matrix(torch.ones(2, 33)))
+    assert supports_vector_word_loads(pack_sign_matrix(torch.ones(2, 128)))
+
+
+def test_layout_metadata_contract():
+    layout = PackedLayoutMetadata()
+    assert layout.version == "llama.cpp-i32-lsb-v1" == PACKED_LAYOUT_VERSION
+    assert (layout.positive_bit, layout.negative_bit, layout.padding_bit) == (0, 1, 0)
+    assert layout.bit_order == "least-significant-bit-first"
+    assert (layout.right_sidecar_name, layout.left_sidecar_name) == ("nq_v", "nq_u")
+    assert dict(GGUF_TENSOR_SUFFIXES)["outlier_scales"] == "nq_salient_scale"
+    assert layout.reference.commit == PACKED_REFERENCE_COMMIT
+    assert layout.reference.cuda_sha256 == PACKED_REFERENCE_CUDA_SHA256
+    with pytest.raises(ValueError, match="bit order"):
+        PackedLayoutMetadata(bit_order="most-significant-bit-first")
+
+
+# --- layer state -----------------------------------------------------------------
+
+
+def _logical(factor_dtype=torch.float32) -> LogicalLayerState:
+    spec = QuantizedLinearSpec(
+        "blocks.0.linear", "nanoquant-v1", 35, 3, 33,
+        str(factor_dtype).removeprefix("torch."), "float32",
+        outlier_count=2, outlier_value_dtype="int8", has_outlier_scales=True, has_bias=True,
+    )
+    left = torch.where(torch.arange(99).reshape(3, 33) % 2 == 0, 1.0, -1.0).to(factor_dtype)
+    right = torch.where(torch.arange(33 * 35).reshape(33, 35) % 5 == 0, -1.0, 1.0).to(factor_dtype)
+    return LogicalLayerState(
+        spec, left, right,
+        torch.cat((torch.tensor([0.5, 0.0]), torch.linspace(0.5, 1.5, 32), torch.zeros(1))),
+        torch.linspace(0.75, 1.25, 33), torch.linspace(1.0, 1.5, 3), torch.tensor([0.1, -0.2, 0.3]),
+        torch.tensor([1, 34], dtype=torch.int32),
+        torch.tensor([[1, -2], [3, -4], [5, -6]], dtype=torch.int8), torch.tensor([0.25, 0.5]),
+    )
+
+
+@pytest.mark.parametrize("factor_dtype", (torch.float16, torch.bfloat16, torch.float32))
+def test_packed_round_trip_preserves_logical_state(factor_dtype):
+    logical = _logical(factor_dtype)
+    packed = pack_logical_layer(logical)
+    restored = packed.to_logical()
+    assert packed.left_words.shape == (3, 2) and packed.right_words.shape == (33, 2)
+    for a, b in ((logical.left_binary, restored.left_binary), (logical.right_binary, restored.right_binary),
+                 (logical.scale_pre, restored.scale_pre), (logical.outlier_values, restored.outlier_values)):
+        assert torch.equal(a, b)
+
+
+def test_packed_state_rejects_nonzero_scale_pre_at_salient_column():
+    logical = _logical()
+    pre = logical.scale_pre.clone()
+    pre[1] = 1
+    with pytest.raises(ValueError, match="exactly zero scale_pre"):
+        PackedLayerState(
+            logical.spec, PACKED_LAYOUT_VERSION, pack_sign_matrix(logical.left_binary),
+            pack_sign_matrix(logical.right_binary), pre, logical.scale_mid, logical.scale_post,
+            logical.bias, logical.outlier_indices, logical.outlier_values, logical.outlier_scales,
+        )
+
+
+def test_packed_state_rejects_scales_on_float_salient_values():
+    packed = pack_logical_layer(_logical())
+    with pytest.raises(ValueError, match="scales require int8"):
+        PackedLayerState(
+            replace(packed.spec, outlier_value_dtype="float32"), packed.layout, packed.left_words,
+            packed.right_words, packed.scale_pre, packed.scale_mid, packed.scale_post, packed.bias,
+            packed.outlier_indices, packed.outlier_values.float(), packed.outlier_scales,
+        )
+
+
+def test_logical_state_rejects_non_sign_and_unsorted_outliers():
+    state = _logical()
+    bad = state.left_binary.clone()
+    bad[0, 0] = 0
+    with pytest.raises(ValueError, match=r"other than -1 or \+1"):
+        LogicalLayerState(state.spec, bad, state.right_binary, state.scale_pre, state.scale_mid,
+                          state.scale_post, state.bias, state.outlier_indices, state.outlier_values,
+                          state.outlier_scales)
+    with pytest.raises(ValueError, match="strictly increasing"):
+        LogicalLayerState(state.spec, state.left_binary, state.right_binary, state.scale_pre,
+                          state.scale_mid, state.scale_post, state.bias,
+                          torch.tensor([34, 1], dtype=torch.int32), state.outlier_values,
+                          state.outlier_scales)
+
+
+def test_row_sidecar_state_folds_into_reference_patch():
+    shape = qwen3_8b_layer()[1]
+    small = replace(shape, in_features=96, out_features=40, rank=19)
+    base = synthetic_packed_layer(small, seed=1)
+    state = synthetic_row_sidecar(base, 4, seed=2)
+    logical = state.to_logical()
+    assert logical.spec.patch_rank == 4 and logical.patch_left.shape == (40, 4)
+    x = torch.randn(2, 96)
+    op = orc.operands_from_state(state)
+    direct = orc.packed_forward(orc.operands_from_state(base), x, dtype=torch.float64)
+    rows = state.rows
+    direct.index_add_(1, rows.indices.long(), (x.double() @ rows.values.double().T) * rows.scales.double())
+    torch.testing.assert_close(orc.packed_forward(op, x, dtype=torch.float64), direct)
+
+
+# --- capabilities and planning -----------------------------------------------------
+
+
+def _spec(name="blocks.0.mlp.proj") -> QuantizedLinearSpec:
+    return QuantizedLinearSpec(name, "nanoquant-v1", 4, 3, 2, "float32", "float32",
+                               outlier_count=1, outlier_value_dtype="int8",
+                               has_outlier_scales=True, has_bias=True)
+
+
+def test_capability_first_failure_is_stable():
+    caps = BackendCapabilities(
+        logical_formats=("nanoquant-v1",), device_types=("cuda",), input_dtypes=("bfloat16",),
+        factor_dtypes=("float32",), scale_dtypes=("float32",), outlier_value_dtypes=("int8",),
+        workload_kinds=("decode",), supports_bias=True, supports_outliers=True,
+        supports_deterministic=True, in_feature_alignment=8,
+    )
+    op = QuantizedLinearSpec("blocks.0.attn.q_proj", "nanoquant-v1", 12, 8, 8, "float32", "float32")
+    work = WorkloadSpec("decode", "cuda", "bfloat16", 1, 1, deterministic=True)
+    assert evaluate_capabilities(caps, op, work) == SupportResult.rejected(
+        "NQ-INF-IN-ALIGNMENT", "input features must be aligned to 8")
+    assert evaluate_capabilities(caps, op, replace(work, kind="prefill")).code == "NQ-INF-WORKLOAD"
+    assert evaluate_capabilities(caps, replace(op, logical_format="x"), work).code == "NQ-INF-FORMAT"
+
+
+def test_hip_backend_reports_missing_device_and_library(monkeypatch):
+    backend = HipPackedBackend()
+    work = WorkloadSpec("decode", "cuda", "bfloat16", 1, 1, deterministic=True)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    assert backend.supports(_spec(), work).code == "NQ-INF-DEVICE-UNAVAILABLE"
+    monkeypatch.setattr(_native, "library_available", lambda: False)
+    assert backend.supports(_spec(), work).code == "NQ-INF-HIP-KERNEL"
+    assert backend.supports(_spec(), replace(work, device_type="cpu")).code == "NQ-INF-DEVICE"
+
+
+def test_hip_backend_declares_reference_capabilities():
+    caps = HipPackedBackend().capabilities()
+    assert caps.device_types == ("cuda",)
+    assert caps.workload_kinds == ("prefill", "decode")
+    assert caps.supports_outliers and caps.supports_bias and caps.supports_deterministic
+    assert set(caps.outlier_value_dtypes) == {"float16", "bfloat16", "float32", "int8"}
+
+
+class _KindBackend:
+    version = "1"
+
+    def __init__(self, name, kinds, reject_code=None):
+        self.name, self.kinds, self.reject_code = name, kinds, reject_code
+        self.prepare_count = 0
+
+    def capabilities(self):
+        return HipPackedBackend().capabilities()
+
+    def supports(self, op, workload):
+        if self.reject_code:
+            return SupportResult.rejected(self.reject_code, "rank must be aligned to 32")
+        if workload.kind not in self.kinds:
+            return SupportResult.rejected("NQ-INF-WORKLOAD", f"{workload.kind} is not selected")
+        return SupportResult.accepted()
+
+    def prepare(self, state, device):
+        self.prepare_count += 1
+        return PreparedLayer(self.name, self.version, state.spec, state)
+
+    def linear(self, value, layer):
+        return torch.zeros(*value.shape[:-1], layer.spec.out_features, dtype=torch.float32)
+
+
+def _state(name):
+    spec = QuantizedLinearSpec(name, "nanoquant-v1", 4, 3, 2, "float32", "float32")
+    return LogicalLayerState(spec, torch.tensor([[1.0, -1.0], [-1.0, 1.0], [1.0, 1.0]]),
+                             torch.tensor([[1.0, -1.0, 1.0, -1.0], [-1.0, -1.0, 1.0, 1.0]]),
+                             torch.ones(4), torch.ones(2), torch.ones(3))
+
+
+def test_planner_fallback_strict_and_named_rejections():
+    states = {n: _state(n) for n in ("blocks.0.proj", "blocks.1.proj")}
+    rejecting = _KindBackend("rejecting", ("prefill", "decode"), reject_code="NQ-INF-RANK-ALIGNMENT")
+    fallback = _KindBackend("fallback", ("prefill", "decode"))
+    work = WorkloadSpec("decode", "cpu", "float32", 1, 1, deterministic=True)
+    plan = plan_backends(tuple(s.spec for s in states.values()), work, (rejecting, fallback), strict=False)
+    assert plan.fallback_count == 2
+    assert [d.rejected_backends[0].support.code for d in plan.layers] == ["NQ-INF-RANK-ALIGNMENT"] * 2
+    prepared = prepare_plan(plan, states, (rejecting, fallback), "cpu")
+    assert prepared[0].linear(torch.ones(1, 4)).shape == (1, 3)
+    with pytest.raises(BackendPlanningError, match="strict runtime plan rejected fallback.*NQ-INF-RANK-ALIGNMENT"):
+        plan_backends((_spec(),), work, (rejecting, fallback), strict=True)
+    with pytest.raises(ValueError, match="missing=.*blocks.0.proj"):
+        prepare_plan(plan, {}, (fallback,), "cpu")
+
+
+def test_execution_plans_share_payloads_and_fix_decode_geometry():
+    states = {n: _state(n) for n in ("blocks.0.proj", "blocks.1.proj")}
+    backend = _KindBackend("both", ("prefill", "decode"))
+    plans = plan_execution_workloads(
+        tuple(s.spec for s in states.values()),
+        prefill=WorkloadSpec("prefill", "cpu", "float32", 2, 3, deterministic=True),
+        decode=WorkloadSpec("decode", "cpu", "float32", 2, 1, deterministic=True),
+        prefill_backends=(backend,), decode_backends=(backend,), strict=True,
+    )
+    prepared = prepare_execution_workloads(plans, states, (backend,), "cpu")
+    assert backend.prepare_count == 2
+    assert all(p.layer is d.layer for p, d in zip(prepared.prefill.dispatches, prepared.decode.dispatches))
+    assert prepared.prefill.linear_at(0, torch.ones(2, 1, 4)).shape == (2, 1, 3)
+    with pytest.raises(ValueError, match="prefill input has 8 token slots, expected at most 6"):
+        prepared.prefill.linear_at(0, torch.ones(2, 4, 4))
+    with pytest.raises(ValueError, match="decode input has 6 token slots, expected exactly 2"):
+        prepared.decode.linear_at(0, torch.ones(2, 3, 4))
+    with pytest.raises(ValueError, match="prefill input dtype differs"):
+        prepared.prefill.linear_at(0, torch.ones(2, 3, 4, dtype=torch.float16))
+    with pytest.raises(IndexError, match="outside the inventory"):
+        prepared.decode.linear_at(2, torch.ones(2, 4))
+    with pytest.raises(ValueError, match="decode plans require exactly one token"):
+        ExecutionPlans(plans.prefill, replace(plans.decode, workload=WorkloadSpec("decode", "cpu", "float32", 1, 2)))
+    with pytest.raises(ValueError, match="preparation device 'cuda' differs"):
+        prepare_execution_workloads(plans, states, (backend,), "cuda")
+
+
+def test_prepared_linear_binding_and_context():
+    states = {"blocks.0.mlp.up": _state("blocks.0.mlp.up")}
+    backend = _KindBackend("both", ("prefill", "decode"))
+    plans = plan_execution_workloads(
+        (states["blocks.0.mlp.up"].spec,),
+        prefill=WorkloadSpec("prefill", "cpu", "float32", 1, 4),
+        decode=WorkloadSpec("decode", "cpu", "float32", 1, 1),
+        prefill_backends=(backend,), decode_backends=(backend,), strict=True,
+    )
+    prepared = prepare_execution_workloads(plans, states, (backend,), "cpu")
+    model = nn.Module()
+    model.mlp = nn.Module()
+    model.mlp.up = nn.Linear(4, 3)
+    assert bind_prepared_linears(model, prepared, {"blocks.0.mlp.up": "mlp.up"}) == 1
+    assert isinstance(model.mlp.up, PreparedLinear)
+    with pytest.raises(RuntimeError, match="outside an execution_workload"):
+        model.mlp.up(torch.ones(1, 4))
+    with execution_workload("decode"):
+        assert model.mlp.up(torch.ones(1, 4)).shape == (1, 3)
+
+
+def test_benchmark_summary_percentiles():
+    dist = summarize_benchmark([0.4, 0.1, 0.2, 0.3], unit_name="tokens", units_per_sample=2)
+    assert dist.samples_seconds == (0.4, 0.1, 0.2, 0.3)
+    assert dist.latency_seconds["p50"] == pytest.approx(0.25)
+    assert dist.throughput_per_second["max"] == pytest.approx(20.0)
+    with pytest.raises(ValueError):
+        summarize_benchmark([0.0], unit_name="t", units_per_sample=1)
