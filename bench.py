@@ -237,7 +237,7 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "nq_linear decode launch sequence (per packed-linear call)",
+            "kernel": "k_decode_fused (one launch per packed linear)",
             "bytes_per_launch": round(mean_bytes),
             "mean_launch_us": round(mean_launch_ms * 1e3, 3),
         },
