@@ -122,6 +122,14 @@ int nq_unpack_signs(const int32_t* words, int64_t rows, int64_t cols,
 int nq_count_bad_padding(const int32_t* words, int64_t rows, int64_t cols,
                          int64_t row_stride_words, int32_t* bad_rows, void* stream);
 
+/* Bytes of the synchronisation header at the start of a tiles buffer. Between
+ * launches every header word is zero except the last 256-byte line, whose
+ * word 0 is a sticky error flag (set if a decode launch ever timed out
+ * waiting for its stage-1 results) and words 1-2 hold a magic value and
+ * max|s_in|. The header is per layer: calls on one prepared layer must not
+ * overlap in time (one stream, or ordered streams). No reference counterpart. */
+int64_t nq_tiles_header_bytes(void);
+
 /* Size in bytes of the GPU-private tiled weight layout for one linear. */
 int64_t nq_tiles_bytes(int64_t in_features, int64_t out_features, int64_t rank);
 

@@ -41,12 +41,34 @@ constexpr int kWaves = 4;
 constexpr int kTileRows = 16;
 constexpr int kSuperCols = 128;
 constexpr int kMaxTokens = 16;
-constexpr int kHeaderWords = 64;  // 256-byte sync header at the start of the tiles buffer
 constexpr uint32_t kTilesMagic = 0x4e515431u;  // "NQT1"
-constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kSpinLimit = 1u << 22;
 
-// Sync header words.
-enum : int { kHdrCounter = 0, kHdrDone = 1, kHdrError = 2, kHdrMagic = 3, kHdrPreMax = 4 };
+// Sync header at the start of the tiles buffer: every counter and flag lives
+// on its own 256-byte line so no address is hit by more than a few dozen
+// workgroups per launch.
+//   ready tree: stage-1 workgroup b bumps slot b % kReadySlots; the workgroup
+//     completing a slot bumps the root; the one completing the root raises the
+//     kReplicas ready flags (and zeroes the slots and root).
+//   done tree: the same for stage-2 workgroups; the one completing its root
+//     lowers the ready flags and zeroes the done tree for the next launch.
+// Stage-2 workgroup i polls ready flag i % kReplicas.
+constexpr int kLine = 64;  // words per line
+constexpr int kReadySlots = 16;
+constexpr int kDoneSlots = 32;
+constexpr int kReplicas = 32;
+constexpr int kReadySlot0 = 0;
+constexpr int kReadyRoot = kReadySlots;
+constexpr int kDoneSlot0 = kReadyRoot + 1;
+constexpr int kDoneRoot = kDoneSlot0 + kDoneSlots;
+constexpr int kReplica0 = kDoneRoot + 1;
+constexpr int kMiscLine = kReplica0 + kReplicas;
+constexpr int kHeaderLines = kMiscLine + 1;
+constexpr int kHeaderWords = kHeaderLines * kLine;
+// Words on the misc line.
+enum : int { kMiscError = 0, kMiscMagic = 1, kMiscPreMax = 2 };
+
+__host__ __device__ constexpr int line_word(int line) { return line * kLine; }
 
 __host__ __device__ inline int64_t tiles_of(int64_t rows) { return (rows + kTileRows - 1) / kTileRows; }
 __host__ __device__ inline int64_t supers_of(int64_t cols) { return (cols + kSuperCols - 1) / kSuperCols; }
@@ -87,7 +109,7 @@ __global__ __launch_bounds__(kBlock) void k_build_tiles(const uint32_t* __restri
 }
 
 __global__ void k_init_header(uint32_t* header, const void* s_in, int scale_dtype, int64_t in) {
-    // One block: header words plus max|s_in| (used to bound x * s_in).
+    // One block: zero the sync header, record max|s_in| (bounds x * s_in).
     __shared__ float red[kBlock];
     float m = 0.0f;
     for (int64_t i = threadIdx.x; i < in; i += kBlock) m = fmaxf(m, fabsf(nq::load_f32(s_in, scale_dtype, i)));
@@ -97,11 +119,11 @@ __global__ void k_init_header(uint32_t* header, const void* s_in, int scale_dtyp
         if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
         __syncthreads();
     }
-    if (threadIdx.x < kHeaderWords) header[threadIdx.x] = 0;
+    for (int i = threadIdx.x; i < kHeaderWords; i += kBlock) header[i] = 0;
     __syncthreads();
     if (threadIdx.x == 0) {
-        header[kHdrMagic] = kTilesMagic;
-        header[kHdrPreMax] = __float_as_uint(red[0]);
+        header[line_word(kMiscLine) + kMiscMagic] = kTilesMagic;
+        header[line_word(kMiscLine) + kMiscPreMax] = __float_as_uint(red[0]);
     }
 }
 
@@ -134,6 +156,7 @@ struct FusedArgs {
     int y_dtype;
     float* lm;      // [16][n1*16]
     float* wgmax;   // [n1][16]
+    int x_vec;      // x rows and s_in are 16-byte aligned with in % 8 == 0
 };
 
 // 2^e for an integer e in the fp32 normal range.
@@ -152,6 +175,30 @@ __device__ __forceinline__ float range_scale(float bound) {
     int e = 13 - exponent_of(bound);
     e = e > 100 ? 100 : (e < -100 ? -100 : e);
     return exp2i(e);
+}
+
+__device__ __forceinline__ void store_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void hdr_store(uint32_t* header, int word, uint32_t v) {
+    __hip_atomic_store(header + word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrive at a two-level counter tree for `count` participants; participant
+// `index` uses slot index % slots. Returns true for exactly one caller: the
+// last arrival overall.
+__device__ __forceinline__ bool tree_arrive(uint32_t* header, int slot0, int slots, int root,
+                                            int64_t index, int64_t count) {
+    const int slot = static_cast<int>(index % slots);
+    const uint32_t slot_total = static_cast<uint32_t>(count / slots + (slot < count % slots ? 1 : 0));
+    const uint32_t before = __hip_atomic_fetch_add(header + line_word(slot0 + slot), 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+    if (before + 1 != slot_total) return false;
+    const uint32_t used_slots = static_cast<uint32_t>(count < slots ? count : slots);
+    const uint32_t root_before =
+        __hip_atomic_fetch_add(header + line_word(root), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return root_before + 1 == used_slots;
 }
 
 template <int MT>
@@ -179,17 +226,104 @@ __device__ __forceinline__ v8h expand_signs(uint32_t word, int m) {
     return r.v;
 }
 
-// Stage activation columns [c0, c0 + ncols) into LDS: act[t][c - c0] = fp16(a(t, c) * scale[t]).
-template <int MT, typename Fn>
-__device__ __forceinline__ void stage_columns(Lds<MT>& lds, int64_t c0, int ncols, int64_t col_limit,
-                                              int tokens, Fn value) {
-    for (int e = threadIdx.x; e < MT * ncols; e += kBlock) {
-        const int t = e / ncols;
-        const int c = e - t * ncols;
-        const int64_t col = c0 + c;
-        float v = 0.0f;
-        if (t < tokens && col < col_limit) v = value(t, col) * lds.tokscale[t];
-        lds.act[t * Lds<MT>::kStride + c] = static_cast<_Float16>(v);
+// Eight consecutive elements [i, i + 8) of a typed buffer as fp32. The caller
+// guarantees 16-byte alignment of element i (rows of length % 8 == 0 on
+// 256-byte aligned allocations).
+__device__ __forceinline__ void load8(const void* __restrict__ p, int dtype, int64_t i, float (&v)[8]) {
+    if (dtype == NQ_DTYPE_F32) {
+        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        const float4 lo = q[0], hi = q[1];
+        v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
+        v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
+    } else {
+        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+        if (dtype == NQ_DTYPE_BF16) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                v[2 * k] = __uint_as_float(w[k] << 16);
+                v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                union { uint32_t u; _Float16 h[2]; } c;
+                c.u = w[k];
+                v[2 * k] = static_cast<float>(c.h[0]);
+                v[2 * k + 1] = static_cast<float>(c.h[1]);
+            }
+        }
+    }
+}
+
+// Elements [i, i + 8) of a row of length `limit`, zero past the end.
+__device__ __forceinline__ void load8_tail(const void* __restrict__ p, int dtype, int64_t row_base,
+                                           int64_t i, int64_t limit, float (&v)[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = i + k < limit ? nq::load_f32(p, dtype, row_base + i + k) : 0.0f;
+}
+
+__device__ __forceinline__ uint4 pack8_f16(const float (&v)[8]) {
+    union { _Float16 h[8]; uint4 u; } r;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) r.h[k] = static_cast<_Float16>(v[k]);
+    return r.u;
+}
+
+// Stage columns [c0, c0 + ncols) of the activation rows into LDS as
+// fp16(a * s * tokscale[t]); `s` (a per-column scale) may be null.
+// act[t][c - c0]; rows t >= tokens are zero.
+template <int MT>
+__device__ __forceinline__ void stage_rows(Lds<MT>& lds, const void* __restrict__ act, int act_dtype,
+                                           int64_t row_len, const void* __restrict__ colscale,
+                                           int colscale_dtype, int tokens, int64_t c0, int ncols,
+                                           bool vec) {
+    const int nv = ncols >> 3;
+    for (int t = 0; t < MT; ++t) {
+        uint4* dst = reinterpret_cast<uint4*>(&lds.act[t * Lds<MT>::kStride]);
+        if (t >= tokens) {
+            for (int j = threadIdx.x; j < nv; j += kBlock) dst[j] = make_uint4(0, 0, 0, 0);
+            continue;
+        }
+        const float scale = lds.tokscale[t];
+#pragma unroll 4
+        for (int j = threadIdx.x; j < nv; j += kBlock) {
+            const int64_t col = c0 + 8 * j;
+            float v[8], w[8];
+            if (vec && col + 8 <= row_len) {
+                load8(act, act_dtype, t * row_len + col, v);
+                if (colscale) load8(colscale, colscale_dtype, col, w);
+            } else {
+                load8_tail(act, act_dtype, t * row_len, col, row_len, v);
+                if (colscale) load8_tail(colscale, colscale_dtype, 0, col, row_len, w);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] *= (colscale ? w[k] : 1.0f) * scale;
+            dst[j] = pack8_f16(v);
+        }
+    }
+}
+
+// max |a[t, :]| for each token t < tokens, accumulated into lds.tokscale[t]
+// (non-negative floats compare like their bit patterns).
+template <int MT>
+__device__ __forceinline__ void row_absmax(Lds<MT>& lds, const void* __restrict__ act, int act_dtype,
+                                           int64_t row_len, int64_t row_stride, int tokens, bool vec) {
+    const int64_t nv = (row_len + 7) >> 3;
+    for (int t = 0; t < MT && t < tokens; ++t) {
+        float m = 0.0f;
+#pragma unroll 4
+        for (int64_t j = threadIdx.x; j < nv; j += kBlock) {
+            float v[8];
+            if (vec) load8(act, act_dtype, t * row_stride + 8 * j, v);
+            else load8_tail(act, act_dtype, t * row_stride, 8 * j, row_len, v);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(v[k]));
+        }
+        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        if ((threadIdx.x & 63) == 0 && m > 0.0f) {
+            atomicMax(reinterpret_cast<unsigned int*>(&lds.tokscale[t]), __float_as_uint(m));
+        }
     }
 }
 
@@ -245,7 +379,7 @@ __device__ __forceinline__ float reduce_waves(Lds<MT>& lds, v4f acc) {
 }
 
 template <int MT, int SCMAX>
-__device__ void stage1_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
+__device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
     const uint32_t* tile = a.v_tiles + rt * a.nsc1 * 64;
     constexpr int kWindowSc = 4 * SCMAX;
     uint32_t words[SCMAX];
@@ -254,20 +388,9 @@ __device__ void stage1_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
     // Per-token range scale: bound |x * s_in| by max|x| * max|s_in|.
     if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
     __syncthreads();
-    {
-        const int t = threadIdx.x % MT;     // kBlock / MT threads cooperate per token
-        const int part = threadIdx.x / MT;
-        float m = 0.0f;
-        if (t < a.tokens) {
-            for (int64_t i = part; i < a.in; i += kBlock / MT) {
-                m = fmaxf(m, fabsf(nq::load_f32(a.x, a.x_dtype, t * a.in + i)));
-            }
-        }
-        // Non-negative floats order like their bit patterns.
-        if (m > 0.0f) atomicMax(reinterpret_cast<unsigned int*>(&lds.tokscale[t]), __float_as_uint(m));
-    }
+    row_absmax<MT>(lds, a.x, a.x_dtype, a.in, a.in, a.tokens, a.x_vec != 0);
     __syncthreads();
-    const float premax = __uint_as_float(a.header[kHdrPreMax]);
+    const float premax = __uint_as_float(a.header[line_word(kMiscLine) + kMiscPreMax]);
     if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = range_scale(lds.tokscale[threadIdx.x] * premax);
     __syncthreads();
 
@@ -276,11 +399,8 @@ __device__ void stage1_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
         if (w0 > 0) load_words<SCMAX>(words, tile, w0, a.nsc1);
         const int64_t c0 = w0 * kSuperCols;
         const int64_t cend = (w0 + kWindowSc < a.nsc1 ? w0 + kWindowSc : a.nsc1) * kSuperCols;
-        stage_columns<MT>(lds, c0, static_cast<int>(cend - c0), a.in, a.tokens,
-                          [&](int t, int64_t col) {
-                              return nq::load_f32(a.x, a.x_dtype, t * a.in + col) *
-                                     nq::load_f32(a.s_in, a.scale_dtype, col);
-                          });
+        stage_rows<MT>(lds, a.x, a.x_dtype, a.in, a.s_in, a.scale_dtype, a.tokens, c0,
+                       static_cast<int>(cend - c0), a.x_vec != 0);
         __syncthreads();
         acc = tile_mfma<MT, SCMAX>(lds, words, w0, a.nsc1, w0, acc);
         __syncthreads();
@@ -291,44 +411,51 @@ __device__ void stage1_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
     const int n = threadIdx.x & 15;
     const int64_t r = rt * kTileRows + n;
     float lmv = 0.0f;
-    if (t < a.tokens && r < a.rank) {
-        lmv = sum / lds.tokscale[t] * nq::load_f32(a.s_mid, a.scale_dtype, r);
-        a.lm[t * (a.n1 * kTileRows) + r] = lmv;
-    }
+    if (t < a.tokens && r < a.rank) lmv = sum / lds.tokscale[t] * nq::load_f32(a.s_mid, a.scale_dtype, r);
+    // Pad ranks [rank, 16 * n1) are written as zero: stage 2 stages whole rows and
+    // its pad sign bits decode to +1.
     // Per-token max over the 16 tile rows (lanes n = 0..15 of this group).
     float am = fabsf(lmv);
     for (int off = 8; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 16));
-    if (n == 0) a.wgmax[rt * kMaxTokens + t] = am;
-
-    // Publish: every wave makes its stores visible at agent scope, then one
-    // release increment.
-    __threadfence();
+    // lm and the maxima are stored write-through at agent scope (no L2
+    // writeback needed); the wait makes them complete before the signal.
+    if (t < a.tokens) store_agent(&a.lm[t * (a.n1 * kTileRows) + r], lmv);
+    if (n == 0) store_agent(&a.wgmax[rt * kMaxTokens + t], am);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-        __hip_atomic_fetch_add(a.header + kHdrCounter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        if (tree_arrive(a.header, kReadySlot0, kReadySlots, kReadyRoot, rt, a.n1)) {
+            // Last stage-1 workgroup: clear the ready tree, raise the flags.
+            for (int i = 0; i < kReadySlots; ++i) hdr_store(a.header, line_word(kReadySlot0 + i), 0u);
+            hdr_store(a.header, line_word(kReadyRoot), 0u);
+            __builtin_amdgcn_s_waitcnt(0);
+            for (int i = 0; i < kReplicas; ++i) hdr_store(a.header, line_word(kReplica0 + i), 1u);
+        }
     }
 }
 
 template <int MT, int SCMAX>
-__device__ void stage2_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
+__device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
     const uint32_t* tile = a.u_tiles + rt * a.nsc2 * 64;
     constexpr int kWindowSc = 4 * SCMAX;
     uint32_t words[SCMAX];
     load_words<SCMAX>(words, tile, 0, a.nsc2);  // prefetch before waiting
 
+    // Poll this workgroup's ready flag with relaxed agent-scope loads, then one
+    // acquire fence (L2 invalidate) before reading stage-1 results.
     if (threadIdx.x == 0) {
+        const uint32_t* flag = a.header + line_word(kReplica0 + static_cast<int>(rt % kReplicas));
         uint32_t spins = 0;
-        while (__hip_atomic_load(a.header + kHdrCounter, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) <
-               static_cast<uint32_t>(a.n1)) {
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
             if (++spins > kSpinLimit) {
-                __hip_atomic_store(a.header + kHdrError, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                hdr_store(a.header, line_word(kMiscLine) + kMiscError, 1u);
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
         }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
     // Per-token |lm| maximum over all stage-1 workgroups -> range scale.
     if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
@@ -352,8 +479,9 @@ __device__ void stage2_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
         if (w0 > 0) load_words<SCMAX>(words, tile, w0, a.nsc2);
         const int64_t c0 = w0 * kSuperCols;
         const int64_t cend = (w0 + kWindowSc < a.nsc2 ? w0 + kWindowSc : a.nsc2) * kSuperCols;
-        stage_columns<MT>(lds, c0, static_cast<int>(cend - c0), a.rank, a.tokens,
-                          [&](int t, int64_t col) { return a.lm[t * lm_ld + col]; });
+        // lm rows have stride lm_ld (a multiple of 16, zeros past `rank`).
+        stage_rows<MT>(lds, a.lm, NQ_DTYPE_F32, lm_ld, nullptr, 0, a.tokens, c0,
+                       static_cast<int>(cend - c0), true);
         __syncthreads();
         acc = tile_mfma<MT, SCMAX>(lds, words, w0, a.nsc2, w0, acc);
         __syncthreads();
@@ -376,11 +504,12 @@ __device__ void stage2_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
 
     __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t done =
-            __hip_atomic_fetch_add(a.header + kHdrDone, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        if (done + 1 == static_cast<uint32_t>(a.n2)) {
-            __hip_atomic_store(a.header + kHdrCounter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(a.header + kHdrDone, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        if (tree_arrive(a.header, kDoneSlot0, kDoneSlots, kDoneRoot, rt, a.n2)) {
+            // Last workgroup of the launch: every stage-2 workgroup has passed
+            // its flag, so lower the flags and clear the done tree.
+            for (int i = 0; i < kReplicas; ++i) hdr_store(a.header, line_word(kReplica0 + i), 0u);
+            for (int i = 0; i < kDoneSlots; ++i) hdr_store(a.header, line_word(kDoneSlot0 + i), 0u);
+            hdr_store(a.header, line_word(kDoneRoot), 0u);
         }
     }
 }
@@ -465,6 +594,8 @@ int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t t
     const int64_t lm_bytes = kMaxTokens * g.rt1 * kTileRows * 4;
     a.lm = reinterpret_cast<float*>(ws);
     a.wgmax = reinterpret_cast<float*>(ws + ((lm_bytes + 255) & ~int64_t(255)));
+    const auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    a.x_vec = (d->in_features % 8 == 0 && aligned16(x) && aligned16(d->scale_pre)) ? 1 : 0;
     const dim3 grid(static_cast<unsigned>(g.rt1 + g.rt2));
     if (tokens == 1) {
         hipLaunchKernelGGL((k_decode_fused<1, 24>), grid, dim3(kBlock), 0, stream, a);
@@ -477,6 +608,8 @@ int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t t
 }
 
 }  // namespace nq
+
+extern "C" int64_t nq_tiles_header_bytes(void) { return static_cast<int64_t>(kHeaderWords) * 4; }
 
 extern "C" int64_t nq_tiles_bytes(int64_t in_features, int64_t out_features, int64_t rank) {
     if (in_features <= 0 || out_features <= 0 || rank <= 0) return -1;

@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "nq_query_device",
     "nq_unpack_signs",
     "nq_count_bad_padding",
+    "nq_tiles_header_bytes",
     "nq_tiles_bytes",
     "nq_prepare_tiles",
     "nq_linear_workspace_bytes",
@@ -120,6 +121,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "nq_query_device": (c_int, [c_int, ctypes.POINTER(DeviceCaps)]),
         "nq_unpack_signs": (c_int, [vp, c_i64, c_i64, c_i64, ctypes.c_int32, vp, vp]),
         "nq_count_bad_padding": (c_int, [vp, c_i64, c_i64, c_i64, vp, vp]),
+        "nq_tiles_header_bytes": (c_i64, []),
         "nq_tiles_bytes": (c_i64, [c_i64, c_i64, c_i64]),
         "nq_prepare_tiles": (c_int, [desc_p, vp, c_i64, vp]),
         "nq_linear_workspace_bytes": (c_i64, [desc_p, c_i64]),

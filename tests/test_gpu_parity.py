@@ -31,6 +31,7 @@ from nanoquant_amd.runtime import (
     prepare_execution_workloads,
     unpack_sign_matrix_device,
 )
+from nanoquant_amd.runtime import _native
 from oracle import nq_oracle as orc
 
 pytestmark = [
@@ -73,11 +74,17 @@ def _assert_parity(backend, actual, expected, case=None):
 
 
 def _sync_header_clean(layer) -> bool:
+    """Between launches the decode sync header is all zero except its last
+    line, whose word 0 (sticky timeout flag) must also be zero."""
+
     tiles = layer.payload.tiles
     if tiles is None:
         return True
-    words = tiles[:16].view(torch.int32).cpu()
-    return int(words[0]) == 0 and int(words[1]) == 0 and int(words[2]) == 0
+    torch.cuda.synchronize()
+    size = int(_native.load().nq_tiles_header_bytes())
+    words = tiles[:size].view(torch.int32).cpu()
+    counters, misc = words[:-64], words[-64:]
+    return bool((counters == 0).all()) and int(misc[0]) == 0
 
 
 def _run(backend, state, x):
