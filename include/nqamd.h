@@ -122,12 +122,13 @@ int nq_unpack_signs(const int32_t* words, int64_t rows, int64_t cols,
 int nq_count_bad_padding(const int32_t* words, int64_t rows, int64_t cols,
                          int64_t row_stride_words, int32_t* bad_rows, void* stream);
 
-/* Bytes of the synchronisation header at the start of a tiles buffer. Between
- * launches every header word is zero except the last 256-byte line, whose
- * word 0 is a sticky error flag (set if a decode launch ever timed out
- * waiting for its stage-1 results) and words 1-2 hold a magic value and
- * max|s_in|. The header is per layer: calls on one prepared layer must not
- * overlap in time (one stream, or ordered streams). No reference counterpart. */
+/* Bytes of the synchronisation header at the start of a tiles buffer. It holds
+ * monotonic launch counters (never reset; graph replays are safe) and, on its
+ * last 256-byte line, word 0 = sticky error flag (set if a decode launch ever
+ * timed out waiting for its stage-1 results), word 1 = magic 0x4E515432,
+ * word 2 = max|s_in| as fp32 bits. The header is per layer: launches that use
+ * one prepared layer must not overlap in time (one stream, or ordered
+ * streams). No reference counterpart. */
 int64_t nq_tiles_header_bytes(void);
 
 /* Size in bytes of the GPU-private tiled weight layout for one linear. */
@@ -151,6 +152,18 @@ int64_t nq_linear_workspace_bytes(const nq_linear_desc* desc, int64_t tokens);
 int nq_linear(const nq_linear_desc* desc, const void* x, int32_t x_dtype,
               int64_t tokens, void* y, int32_t y_dtype, void* workspace,
               int64_t workspace_bytes, void* stream);
+
+/* One launch for `count` (1..8) packed linears with the same token count
+ * (1..16) and dtypes: y_i = linear_i(x_i). Inputs may alias (Q/K/V or gate/up
+ * share x); every descriptor must carry tiles and no two may share them.
+ * workspaces[i] holds nq_linear_workspace_bytes(descs[i], tokens) bytes.
+ * Replaces launch_grouped_packed_linears / grouped_cuda_projection
+ * (src/nanoquant/runtime/cuda_kernels.py:301-374,
+ * src/nanoquant/runtime/cuda_backend.py:123-144), generalised to distinct
+ * inputs, any rank (no multiple-of-8 limit) and sidecars. */
+int nq_linear_batch(const nq_linear_desc* const* descs, int32_t count, const void* const* xs,
+                    int32_t x_dtype, int64_t tokens, void* const* ys, int32_t y_dtype,
+                    void* const* workspaces, const int64_t* workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -15,4 +15,9 @@ bool decode_path_applies(const nq_linear_desc* d, int64_t tokens);
 int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y,
                   int y_dtype, void* scratch, hipStream_t stream);
 
+// One launch for `count` (1..8) linears sharing the token count and dtypes.
+int launch_decode_batch(const nq_linear_desc* const* descs, int count, const void* const* xs, int x_dtype,
+                        int64_t tokens, void* const* ys, int y_dtype, void* const* scratch,
+                        hipStream_t stream);
+
 }  // namespace nq

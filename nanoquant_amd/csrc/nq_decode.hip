@@ -1,5 +1,6 @@
 // Fused single-launch decode path (tokens <= 16) for the packed binary
-// low-rank linear on gfx950.
+// low-rank linear on gfx950, for one linear or a batch of up to 8 linears in
+// one launch.
 //
 //   lm[t, r] = s_mid[r] * Σ_i sgn(V[r, i]) * x[t, i] * s_in[i]     (stage 1)
 //   y[t, o]  = s_out[o] * Σ_r sgn(U[o, r]) * lm[t, r] + salient + bias (stage 2)
@@ -15,20 +16,19 @@
 // is two fp16 ±1 values in one shift + one and_or. A wave reads one word per
 // lane per superchunk: 256 contiguous bytes, fully coalesced.
 //
-// Grid: one launch. Workgroups [0, n1) are stage-1 tiles (16 ranks each, the
-// four waves split the columns); workgroups [n1, n1 + n2) are stage-2 tiles
-// (16 output rows each). Stage-1 workgroups write lm (fp32) and a per-token
-// |lm| maximum to the workspace, then release a counter (agent scope).
-// Stage-2 workgroups first issue the loads of their U tile, then acquire the
-// counter (bounded spin), so the U stream overlaps stage 1. Workgroups are
-// dispatched in index order, so every stage-1 workgroup is resident or done
-// before any stage-2 workgroup can occupy its slot; stage-1 workgroups never
-// wait. The last stage-2 workgroup resets the counters for the next launch.
+// Grid: one launch. The first workgroups are stage-1 tiles (16 ranks each, the
+// four waves split the columns) of every linear in the batch, the rest are
+// stage-2 tiles (16 output rows each). Stage-1 workgroups store lm (fp32)
+// write-through at agent scope and then signal; stage-2 workgroups issue the
+// loads of their U tile first, then wait for their linear's signal (bounded
+// spin), so the U stream overlaps stage 1. Workgroups are dispatched in index
+// order, so every stage-1 workgroup is resident or finished before a stage-2
+// workgroup can take its slot, and stage-1 workgroups never wait.
 //
 // Activations enter the fp16 MFMA scaled by an exact per-token power of two
-// (from the maximum |x| exponent times max|s_in|, and from the stage-1 |lm|
-// maximum), so the fp16 range cannot overflow; products are accumulated in
-// fp32.
+// (from the exact max |x * s_in| for one token, else max|x| * max|s_in|, and
+// from the |lm| maximum), so the fp16 range cannot overflow; products are
+// accumulated in fp32.
 #include "nq_decode.h"
 
 namespace {
@@ -41,27 +41,32 @@ constexpr int kWaves = 4;
 constexpr int kTileRows = 16;
 constexpr int kSuperCols = 128;
 constexpr int kMaxTokens = 16;
-constexpr uint32_t kTilesMagic = 0x4e515431u;  // "NQT1"
+constexpr int kMaxBatch = 8;
+constexpr uint32_t kTilesMagic = 0x4e515432u;  // "NQT2"
 constexpr uint32_t kSpinLimit = 1u << 22;
 
-// Sync header at the start of the tiles buffer: every counter and flag lives
-// on its own 256-byte line so no address is hit by more than a few dozen
-// workgroups per launch.
-//   ready tree: stage-1 workgroup b bumps slot b % kReadySlots; the workgroup
-//     completing a slot bumps the root; the one completing the root raises the
-//     kReplicas ready flags (and zeroes the slots and root).
-//   done tree: the same for stage-2 workgroups; the one completing its root
-//     lowers the ready flags and zeroes the done tree for the next launch.
-// Stage-2 workgroup i polls ready flag i % kReplicas.
+// Sync header at the start of each linear's tiles buffer. Every word lives on
+// its own 256-byte line. All counters only ever increase, so nothing is reset
+// between launches (graph replays included):
+//   Counters are 64-bit (first two words of their line); flags are 32-bit and
+//   compared wrap-safely.
+//   ready slots: stage-1 workgroup b adds 1 to slot b % kReadySlots; with
+//     c = that slot's participant count, the value it saw, v, gives the
+//     launch index k = v / c, and v % c == c - 1 marks the slot complete.
+//   ready root: each slot completer adds 1; the root completer of launch k
+//     (old value == (k + 1) * used_slots - 1) writes k + 1 into every ready
+//     flag.
+//   arrive slots: stage-2 workgroup i adds 1 to slot i % kArriveSlots at its
+//     start, which yields its own launch index k the same way; it then waits
+//     until ready flag i % kReplicas reaches k + 1 (wrap-safe compare).
 constexpr int kLine = 64;  // words per line
 constexpr int kReadySlots = 16;
-constexpr int kDoneSlots = 32;
-constexpr int kReplicas = 32;
+constexpr int kArriveSlots = 32;
+constexpr int kReplicas = 64;
 constexpr int kReadySlot0 = 0;
 constexpr int kReadyRoot = kReadySlots;
-constexpr int kDoneSlot0 = kReadyRoot + 1;
-constexpr int kDoneRoot = kDoneSlot0 + kDoneSlots;
-constexpr int kReplica0 = kDoneRoot + 1;
+constexpr int kArriveSlot0 = kReadyRoot + 1;
+constexpr int kReplica0 = kArriveSlot0 + kArriveSlots;
 constexpr int kMiscLine = kReplica0 + kReplicas;
 constexpr int kHeaderLines = kMiscLine + 1;
 constexpr int kHeaderWords = kHeaderLines * kLine;
@@ -69,6 +74,22 @@ constexpr int kHeaderWords = kHeaderLines * kLine;
 enum : int { kMiscError = 0, kMiscMagic = 1, kMiscPreMax = 2 };
 
 __host__ __device__ constexpr int line_word(int line) { return line * kLine; }
+
+// Optional phase tracing (build with -DNQ_DECODE_TRACE): thread 0 of every
+// workgroup stamps the 100 MHz real-time counter at each phase boundary into
+// g_nq_trace[block * 8 + phase]. Compiled out of the shipped library.
+#ifdef NQ_DECODE_TRACE
+__device__ uint64_t* g_nq_trace;
+#define NQ_TRACE(phase)                                                              \
+    do {                                                                             \
+        if (threadIdx.x == 0 && g_nq_trace)                                          \
+            g_nq_trace[blockIdx.x * 8 + (phase)] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define NQ_TRACE(phase) \
+    do {                \
+    } while (0)
+#endif
 
 __host__ __device__ inline int64_t tiles_of(int64_t rows) { return (rows + kTileRows - 1) / kTileRows; }
 __host__ __device__ inline int64_t supers_of(int64_t cols) { return (cols + kSuperCols - 1) / kSuperCols; }
@@ -159,6 +180,13 @@ struct FusedArgs {
     int x_vec;      // x rows and s_in are 16-byte aligned with in % 8 == 0
 };
 
+struct FusedBatch {
+    int count;
+    int64_t first1[kMaxBatch + 1];  // stage-1 workgroup prefix per linear
+    int64_t first2[kMaxBatch + 1];  // stage-2 workgroup prefix (after all stage-1)
+    FusedArgs p[kMaxBatch];
+};
+
 // 2^e for an integer e in the fp32 normal range.
 __device__ __forceinline__ float exp2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
 
@@ -168,8 +196,7 @@ __device__ __forceinline__ int exponent_of(float v) {
     return e < -126 ? -126 : e;
 }
 
-// Scale that maps values bounded by `bound` below 2^14 (fp16-safe with headroom
-// for the sum of 32 terms the MFMA never rounds to fp16 anyway).
+// Exact power of two mapping values bounded by `bound` below 2^14 (fp16-safe).
 __device__ __forceinline__ float range_scale(float bound) {
     if (!(bound > 0.0f)) return 1.0f;
     int e = 13 - exponent_of(bound);
@@ -185,32 +212,30 @@ __device__ __forceinline__ void hdr_store(uint32_t* header, int word, uint32_t v
     __hip_atomic_store(header + word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Arrive at a two-level counter tree for `count` participants; participant
-// `index` uses slot index % slots. Returns true for exactly one caller: the
-// last arrival overall.
-__device__ __forceinline__ bool tree_arrive(uint32_t* header, int slot0, int slots, int root,
-                                            int64_t index, int64_t count) {
-    const int slot = static_cast<int>(index % slots);
-    const uint32_t slot_total = static_cast<uint32_t>(count / slots + (slot < count % slots ? 1 : 0));
-    const uint32_t before = __hip_atomic_fetch_add(header + line_word(slot0 + slot), 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-    if (before + 1 != slot_total) return false;
-    const uint32_t used_slots = static_cast<uint32_t>(count < slots ? count : slots);
-    const uint32_t root_before =
-        __hip_atomic_fetch_add(header + line_word(root), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return root_before + 1 == used_slots;
+// 64-bit monotonic counter at the start of a header line (never wraps in practice).
+__device__ __forceinline__ uint64_t hdr_add(uint32_t* header, int word) {
+    return __hip_atomic_fetch_add(reinterpret_cast<uint64_t*>(header + word), uint64_t{1}, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int MT>
+// Participants of slot `slot` when `count` participants are spread over `slots`.
+__device__ __forceinline__ uint64_t slot_count(int slot, int slots, int64_t count) {
+    return static_cast<uint64_t>(count / slots + (slot < count % slots ? 1 : 0));
+}
+
+// LDS of one workgroup for MT token rows and a column window of 4 * SC
+// superchunks (SC per wave).
+template <int MT, int SC>
 struct alignas(16) Lds {
+    static constexpr int kMT = MT;
     // Activation staging: MT rows of fp16, row stride padded by 8 halfs so the
     // 16 token rows of a ds_read_b128 land in different banks.
-    static constexpr int kStageCols = MT == 1 ? 12288 : (MT <= 4 ? 3072 : 2048);
+    static constexpr int kStageCols = 4 * SC * kSuperCols;
     static constexpr int kStride = kStageCols + 8;
     _Float16 act[MT * kStride];
     float red[kWaves][kMaxTokens][kTileRows];
     float tokscale[kMaxTokens];
-    uint32_t flag;
+    float wmax[kWaves];
 };
 
 __device__ __forceinline__ v8h expand_signs(uint32_t word, int m) {
@@ -273,14 +298,14 @@ __device__ __forceinline__ uint4 pack8_f16(const float (&v)[8]) {
 // Stage columns [c0, c0 + ncols) of the activation rows into LDS as
 // fp16(a * s * tokscale[t]); `s` (a per-column scale) may be null.
 // act[t][c - c0]; rows t >= tokens are zero.
-template <int MT>
-__device__ __forceinline__ void stage_rows(Lds<MT>& lds, const void* __restrict__ act, int act_dtype,
+template <typename L>
+__device__ __forceinline__ void stage_rows(L& lds, const void* __restrict__ act, int act_dtype,
                                            int64_t row_len, const void* __restrict__ colscale,
                                            int colscale_dtype, int tokens, int64_t c0, int ncols,
                                            bool vec) {
     const int nv = ncols >> 3;
-    for (int t = 0; t < MT; ++t) {
-        uint4* dst = reinterpret_cast<uint4*>(&lds.act[t * Lds<MT>::kStride]);
+    for (int t = 0; t < L::kMT; ++t) {
+        uint4* dst = reinterpret_cast<uint4*>(&lds.act[t * L::kStride]);
         if (t >= tokens) {
             for (int j = threadIdx.x; j < nv; j += kBlock) dst[j] = make_uint4(0, 0, 0, 0);
             continue;
@@ -306,11 +331,11 @@ __device__ __forceinline__ void stage_rows(Lds<MT>& lds, const void* __restrict_
 
 // max |a[t, :]| for each token t < tokens, accumulated into lds.tokscale[t]
 // (non-negative floats compare like their bit patterns).
-template <int MT>
-__device__ __forceinline__ void row_absmax(Lds<MT>& lds, const void* __restrict__ act, int act_dtype,
+template <typename L>
+__device__ __forceinline__ void row_absmax(L& lds, const void* __restrict__ act, int act_dtype,
                                            int64_t row_len, int64_t row_stride, int tokens, bool vec) {
     const int64_t nv = (row_len + 7) >> 3;
-    for (int t = 0; t < MT && t < tokens; ++t) {
+    for (int t = 0; t < L::kMT && t < tokens; ++t) {
         float m = 0.0f;
 #pragma unroll 4
         for (int64_t j = threadIdx.x; j < nv; j += kBlock) {
@@ -327,10 +352,60 @@ __device__ __forceinline__ void row_absmax(Lds<MT>& lds, const void* __restrict_
     }
 }
 
+// One-token staging in a single memory round trip: every thread loads its
+// NV vectors of a[col] * s[col] into registers, the block reduces max |value|
+// into a range scale (lds.tokscale[0]), then the scaled fp16 values go to LDS
+// row 0. Columns [n, ncols_pad) are zero. Requires ncols_pad <= 2048 * NV.
+template <typename L>
+__device__ __forceinline__ void stage_row_single(L& lds, const void* __restrict__ act, int act_dtype,
+                                                 const void* __restrict__ colscale, int colscale_dtype,
+                                                 int64_t n, int ncols_pad, bool vec) {
+    constexpr int NV = L::kStageCols / (8 * kBlock);
+    float v[NV][8];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int64_t col = 8 * (static_cast<int64_t>(threadIdx.x) + i * kBlock);
+        float w[8];
+        if (col < ncols_pad) {
+            if (vec && col + 8 <= n) {
+                load8(act, act_dtype, col, v[i]);
+                if (colscale) load8(colscale, colscale_dtype, col, w);
+            } else {
+                load8_tail(act, act_dtype, 0, col, n, v[i]);
+                if (colscale) load8_tail(colscale, colscale_dtype, 0, col, n, w);
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[i][k] = 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (colscale && col < ncols_pad) v[i][k] *= w[k];
+            m = fmaxf(m, fabsf(v[i][k]));
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) lds.wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const float scale = range_scale(fmaxf(fmaxf(lds.wmax[0], lds.wmax[1]), fmaxf(lds.wmax[2], lds.wmax[3])));
+    if (threadIdx.x == 0) lds.tokscale[0] = scale;
+    uint4* dst = reinterpret_cast<uint4*>(&lds.act[0]);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int j = threadIdx.x + i * kBlock;
+        if (8 * j < ncols_pad) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[i][k] *= scale;
+            dst[j] = pack8_f16(v[i]);
+        }
+    }
+}
+
 // One wave's share of a 16-row tile: superchunks sc = w, w + 4, ... of the
 // current stage window. Returns the partial D (token rows x 16 tile rows).
 template <int MT, int SCMAX>
-__device__ __forceinline__ v4f tile_mfma(const Lds<MT>& lds, const uint32_t (&words)[SCMAX],
+__device__ __forceinline__ v4f tile_mfma(const Lds<MT, SCMAX>& lds, const uint32_t (&words)[SCMAX],
                                          int64_t sc_first, int64_t nsc, int64_t window_sc0, v4f acc) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -344,7 +419,7 @@ __device__ __forceinline__ v4f tile_mfma(const Lds<MT>& lds, const uint32_t (&wo
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 v8h a = {};
-                if (t < MT) a = *reinterpret_cast<const v8h*>(&lds.act[t * Lds<MT>::kStride + base + 32 * m]);
+                if (t < MT) a = *reinterpret_cast<const v8h*>(&lds.act[t * Lds<MT, SCMAX>::kStride + base + 32 * m]);
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, expand_signs(words[i], m), acc, 0, 0, 0);
             }
         }
@@ -366,8 +441,8 @@ __device__ __forceinline__ void load_words(uint32_t (&words)[SCMAX], const uint3
 
 // Sum the four waves' partial tiles (fixed order: deterministic). Returns the
 // value for (t = tid / 16, n = tid % 16).
-template <int MT>
-__device__ __forceinline__ float reduce_waves(Lds<MT>& lds, v4f acc) {
+template <typename L>
+__device__ __forceinline__ float reduce_waves(L& lds, v4f acc) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
 #pragma unroll
@@ -379,42 +454,52 @@ __device__ __forceinline__ float reduce_waves(Lds<MT>& lds, v4f acc) {
 }
 
 template <int MT, int SCMAX>
-__device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
+__device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT, SCMAX>& lds, int64_t rt) {
+    NQ_TRACE(0);
     const uint32_t* tile = a.v_tiles + rt * a.nsc1 * 64;
     constexpr int kWindowSc = 4 * SCMAX;
     uint32_t words[SCMAX];
     load_words<SCMAX>(words, tile, 0, a.nsc1);
 
-    // Per-token range scale: bound |x * s_in| by max|x| * max|s_in|.
-    if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
-    __syncthreads();
-    row_absmax<MT>(lds, a.x, a.x_dtype, a.in, a.in, a.tokens, a.x_vec != 0);
-    __syncthreads();
-    const float premax = __uint_as_float(a.header[line_word(kMiscLine) + kMiscPreMax]);
-    if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = range_scale(lds.tokscale[threadIdx.x] * premax);
-    __syncthreads();
-
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int64_t w0 = 0; w0 < a.nsc1; w0 += kWindowSc) {
-        if (w0 > 0) load_words<SCMAX>(words, tile, w0, a.nsc1);
-        const int64_t c0 = w0 * kSuperCols;
-        const int64_t cend = (w0 + kWindowSc < a.nsc1 ? w0 + kWindowSc : a.nsc1) * kSuperCols;
-        stage_rows<MT>(lds, a.x, a.x_dtype, a.in, a.s_in, a.scale_dtype, a.tokens, c0,
+    if (MT == 1 && a.nsc1 <= kWindowSc) {
+        // One token, one window: x * s_in loaded once, exact range scale.
+        stage_row_single(lds, a.x, a.x_dtype, a.s_in, a.scale_dtype, a.in,
+                         static_cast<int>(a.nsc1 * kSuperCols), a.x_vec != 0);
+        __syncthreads();
+        NQ_TRACE(1);
+        acc = tile_mfma<MT, SCMAX>(lds, words, 0, a.nsc1, 0, acc);
+    } else {
+        // Per-token range scale: bound |x * s_in| by max|x| * max|s_in|.
+        if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
+        __syncthreads();
+        row_absmax(lds, a.x, a.x_dtype, a.in, a.in, a.tokens, a.x_vec != 0);
+        __syncthreads();
+        const float premax = __uint_as_float(a.header[line_word(kMiscLine) + kMiscPreMax]);
+        if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = range_scale(lds.tokscale[threadIdx.x] * premax);
+        __syncthreads();
+        NQ_TRACE(1);
+        for (int64_t w0 = 0; w0 < a.nsc1; w0 += kWindowSc) {
+            if (w0 > 0) load_words<SCMAX>(words, tile, w0, a.nsc1);
+            const int64_t c0 = w0 * kSuperCols;
+            const int64_t cend = (w0 + kWindowSc < a.nsc1 ? w0 + kWindowSc : a.nsc1) * kSuperCols;
+            stage_rows(lds, a.x, a.x_dtype, a.in, a.s_in, a.scale_dtype, a.tokens, c0,
                        static_cast<int>(cend - c0), a.x_vec != 0);
-        __syncthreads();
-        acc = tile_mfma<MT, SCMAX>(lds, words, w0, a.nsc1, w0, acc);
-        __syncthreads();
+            __syncthreads();
+            acc = tile_mfma<MT, SCMAX>(lds, words, w0, a.nsc1, w0, acc);
+            __syncthreads();
+        }
     }
 
-    const float sum = reduce_waves<MT>(lds, acc);
+    NQ_TRACE(2);
+    const float sum = reduce_waves(lds, acc);
     const int t = threadIdx.x >> 4;
     const int n = threadIdx.x & 15;
     const int64_t r = rt * kTileRows + n;
-    float lmv = 0.0f;
-    if (t < a.tokens && r < a.rank) lmv = sum / lds.tokscale[t] * nq::load_f32(a.s_mid, a.scale_dtype, r);
     // Pad ranks [rank, 16 * n1) are written as zero: stage 2 stages whole rows and
     // its pad sign bits decode to +1.
-    // Per-token max over the 16 tile rows (lanes n = 0..15 of this group).
+    float lmv = 0.0f;
+    if (t < a.tokens && r < a.rank) lmv = sum / lds.tokscale[t] * nq::load_f32(a.s_mid, a.scale_dtype, r);
     float am = fabsf(lmv);
     for (int off = 8; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 16));
     // lm and the maxima are stored write-through at agent scope (no L2
@@ -423,30 +508,41 @@ __device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT>& lds, in
     if (n == 0) store_agent(&a.wgmax[rt * kMaxTokens + t], am);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    NQ_TRACE(3);
     if (threadIdx.x == 0) {
-        if (tree_arrive(a.header, kReadySlot0, kReadySlots, kReadyRoot, rt, a.n1)) {
-            // Last stage-1 workgroup: clear the ready tree, raise the flags.
-            for (int i = 0; i < kReadySlots; ++i) hdr_store(a.header, line_word(kReadySlot0 + i), 0u);
-            hdr_store(a.header, line_word(kReadyRoot), 0u);
-            __builtin_amdgcn_s_waitcnt(0);
-            for (int i = 0; i < kReplicas; ++i) hdr_store(a.header, line_word(kReplica0 + i), 1u);
+        const int slot = static_cast<int>(rt % kReadySlots);
+        const uint64_t c = slot_count(slot, kReadySlots, a.n1);
+        const uint64_t v = hdr_add(a.header, line_word(kReadySlot0 + slot));
+        if (v % c == c - 1) {
+            const uint64_t used = static_cast<uint64_t>(a.n1 < kReadySlots ? a.n1 : kReadySlots);
+            const uint64_t k = v / c;
+            const uint64_t w = hdr_add(a.header, line_word(kReadyRoot));
+            if (w + 1 == (k + 1) * used) {
+                const uint32_t flag = static_cast<uint32_t>(k + 1);
+                for (int i = 0; i < kReplicas; ++i) hdr_store(a.header, line_word(kReplica0 + i), flag);
+            }
         }
     }
+    NQ_TRACE(4);
 }
 
 template <int MT, int SCMAX>
-__device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT>& lds, int64_t rt) {
+__device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT, SCMAX>& lds, int64_t rt) {
+    NQ_TRACE(0);
     const uint32_t* tile = a.u_tiles + rt * a.nsc2 * 64;
     constexpr int kWindowSc = 4 * SCMAX;
     uint32_t words[SCMAX];
     load_words<SCMAX>(words, tile, 0, a.nsc2);  // prefetch before waiting
 
-    // Poll this workgroup's ready flag with relaxed agent-scope loads, then one
-    // acquire fence (L2 invalidate) before reading stage-1 results.
+    // Launch index from this workgroup's arrival, then poll its ready flag with
+    // relaxed agent-scope loads; one acquire fence (L2 invalidate) at the end.
     if (threadIdx.x == 0) {
+        const int slot = static_cast<int>(rt % kArriveSlots);
+        const uint64_t c = slot_count(slot, kArriveSlots, a.n2);
+        const uint32_t target = static_cast<uint32_t>(hdr_add(a.header, line_word(kArriveSlot0 + slot)) / c + 1);
         const uint32_t* flag = a.header + line_word(kReplica0 + static_cast<int>(rt % kReplicas));
         uint32_t spins = 0;
-        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+        while (static_cast<int32_t>(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
             if (++spins > kSpinLimit) {
                 hdr_store(a.header, line_word(kMiscLine) + kMiscError, 1u);
                 break;
@@ -456,38 +552,47 @@ __device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT>& lds, in
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
-
-    // Per-token |lm| maximum over all stage-1 workgroups -> range scale.
-    if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
-    __syncthreads();
-    {
-        const int t = threadIdx.x % MT;
-        const int part = threadIdx.x / MT;
-        float m = 0.0f;
-        if (t < a.tokens) {
-            for (int64_t b = part; b < a.n1; b += kBlock / MT) m = fmaxf(m, a.wgmax[b * kMaxTokens + t]);
-        }
-        if (m > 0.0f) atomicMax(reinterpret_cast<unsigned int*>(&lds.tokscale[t]), __float_as_uint(m));
-    }
-    __syncthreads();
-    if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = range_scale(lds.tokscale[threadIdx.x]);
-    __syncthreads();
+    NQ_TRACE(1);
 
     const int64_t lm_ld = a.n1 * kTileRows;
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int64_t w0 = 0; w0 < a.nsc2; w0 += kWindowSc) {
-        if (w0 > 0) load_words<SCMAX>(words, tile, w0, a.nsc2);
-        const int64_t c0 = w0 * kSuperCols;
-        const int64_t cend = (w0 + kWindowSc < a.nsc2 ? w0 + kWindowSc : a.nsc2) * kSuperCols;
-        // lm rows have stride lm_ld (a multiple of 16, zeros past `rank`).
-        stage_rows<MT>(lds, a.lm, NQ_DTYPE_F32, lm_ld, nullptr, 0, a.tokens, c0,
-                       static_cast<int>(cend - c0), true);
+    if (MT == 1 && a.nsc2 <= kWindowSc) {
+        // One token, one window: lm loaded once, range scale from its own max.
+        stage_row_single(lds, a.lm, NQ_DTYPE_F32, nullptr, 0, lm_ld, static_cast<int>(a.nsc2 * kSuperCols),
+                         true);
         __syncthreads();
-        acc = tile_mfma<MT, SCMAX>(lds, words, w0, a.nsc2, w0, acc);
+        acc = tile_mfma<MT, SCMAX>(lds, words, 0, a.nsc2, 0, acc);
+    } else {
+        // Per-token |lm| maximum over all stage-1 workgroups -> range scale.
+        if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
         __syncthreads();
+        {
+            const int t = threadIdx.x % MT;
+            const int part = threadIdx.x / MT;
+            float m = 0.0f;
+            if (t < a.tokens) {
+                for (int64_t b = part; b < a.n1; b += kBlock / MT) m = fmaxf(m, a.wgmax[b * kMaxTokens + t]);
+            }
+            if (m > 0.0f) atomicMax(reinterpret_cast<unsigned int*>(&lds.tokscale[t]), __float_as_uint(m));
+        }
+        __syncthreads();
+        if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = range_scale(lds.tokscale[threadIdx.x]);
+        __syncthreads();
+        for (int64_t w0 = 0; w0 < a.nsc2; w0 += kWindowSc) {
+            if (w0 > 0) load_words<SCMAX>(words, tile, w0, a.nsc2);
+            const int64_t c0 = w0 * kSuperCols;
+            const int64_t cend = (w0 + kWindowSc < a.nsc2 ? w0 + kWindowSc : a.nsc2) * kSuperCols;
+            // lm rows have stride lm_ld (a multiple of 16, zeros past `rank`).
+            stage_rows(lds, a.lm, NQ_DTYPE_F32, lm_ld, nullptr, 0, a.tokens, c0, static_cast<int>(cend - c0),
+                       true);
+            __syncthreads();
+            acc = tile_mfma<MT, SCMAX>(lds, words, w0, a.nsc2, w0, acc);
+            __syncthreads();
+        }
     }
 
-    const float sum = reduce_waves<MT>(lds, acc);
+    NQ_TRACE(2);
+    const float sum = reduce_waves(lds, acc);
     const int t = threadIdx.x >> 4;
     const int n = threadIdx.x & 15;
     const int64_t o = rt * kTileRows + n;
@@ -501,27 +606,21 @@ __device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT>& lds, in
         if (a.bias) v += nq::load_f32(a.bias, a.bias_dtype, o);
         nq::store_f32_as(a.y, a.y_dtype, t * a.out + o, v);
     }
-
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        if (tree_arrive(a.header, kDoneSlot0, kDoneSlots, kDoneRoot, rt, a.n2)) {
-            // Last workgroup of the launch: every stage-2 workgroup has passed
-            // its flag, so lower the flags and clear the done tree.
-            for (int i = 0; i < kReplicas; ++i) hdr_store(a.header, line_word(kReplica0 + i), 0u);
-            for (int i = 0; i < kDoneSlots; ++i) hdr_store(a.header, line_word(kDoneSlot0 + i), 0u);
-            hdr_store(a.header, line_word(kDoneRoot), 0u);
-        }
-    }
+    NQ_TRACE(3);
 }
 
 template <int MT, int SCMAX>
-__global__ __launch_bounds__(kBlock) void k_decode_fused(const FusedArgs a) {
-    __shared__ Lds<MT> lds;
+__global__ __launch_bounds__(kBlock) void k_decode_fused(const FusedBatch batch) {
+    __shared__ Lds<MT, SCMAX> lds;
     const int64_t b = blockIdx.x;
-    if (b < a.n1) {
-        stage1_tile<MT, SCMAX>(a, lds, b);
+    if (b < batch.first1[batch.count]) {
+        int p = 0;
+        while (p + 1 < batch.count && b >= batch.first1[p + 1]) ++p;
+        stage1_tile<MT, SCMAX>(batch.p[p], lds, b - batch.first1[p]);
     } else {
-        stage2_tile<MT, SCMAX>(a, lds, b - a.n1);
+        int p = 0;
+        while (p + 1 < batch.count && b >= batch.first2[p + 1]) ++p;
+        stage2_tile<MT, SCMAX>(batch.p[p], lds, b - batch.first2[p]);
     }
 }
 
@@ -541,28 +640,23 @@ TilesGeometry geometry(int64_t in, int64_t out, int64_t rank) {
     return g;
 }
 
-}  // namespace
-
-namespace nq {
-
-int64_t decode_scratch_bytes(const nq_linear_desc* d, int64_t tokens) {
-    (void)tokens;
-    if (!d->tiles) return 0;
-    const TilesGeometry g = geometry(d->in_features, d->out_features, d->rank);
-    const int64_t lm = kMaxTokens * g.rt1 * kTileRows * 4;
-    const int64_t wgmax = g.rt1 * kMaxTokens * 4;
-    return ((lm + 255) & ~int64_t(255)) + ((wgmax + 255) & ~int64_t(255));
+int64_t scratch_lm_bytes(const TilesGeometry& g) {
+    return (kMaxTokens * g.rt1 * kTileRows * 4 + 255) & ~int64_t(255);
 }
 
-bool decode_path_applies(const nq_linear_desc* d, int64_t tokens) {
-    return d->tiles != nullptr && tokens >= 1 && tokens <= kMaxTokens;
+int64_t scratch_bytes(const TilesGeometry& g) {
+    return scratch_lm_bytes(g) + ((g.rt1 * kMaxTokens * 4 + 255) & ~int64_t(255));
 }
 
-int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y,
-                  int y_dtype, void* scratch, hipStream_t stream) {
-    const TilesGeometry g = geometry(d->in_features, d->out_features, d->rank);
-    if (d->tiles_bytes < static_cast<int64_t>(kHeaderWords + g.v_words + g.u_words) * 4) return NQ_ERR_ARGUMENT;
-    FusedArgs a{};
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Fill one problem of a batch; NQ_OK or an error status.
+int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y, int y_dtype,
+             void* scratch, FusedArgs& a, TilesGeometry& g) {
+    g = geometry(d->in_features, d->out_features, d->rank);
+    if (!d->tiles) return NQ_ERR_ARGUMENT;
+    if (d->tiles_bytes < (kHeaderWords + g.v_words + g.u_words) * 4) return NQ_ERR_ARGUMENT;
+    a = FusedArgs{};
     a.in = d->in_features;
     a.rank = d->rank;
     a.out = d->out_features;
@@ -591,23 +685,84 @@ int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t t
     a.y = y;
     a.y_dtype = y_dtype;
     char* ws = static_cast<char*>(scratch);
-    const int64_t lm_bytes = kMaxTokens * g.rt1 * kTileRows * 4;
     a.lm = reinterpret_cast<float*>(ws);
-    a.wgmax = reinterpret_cast<float*>(ws + ((lm_bytes + 255) & ~int64_t(255)));
-    const auto aligned16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    a.wgmax = reinterpret_cast<float*>(ws + scratch_lm_bytes(g));
     a.x_vec = (d->in_features % 8 == 0 && aligned16(x) && aligned16(d->scale_pre)) ? 1 : 0;
-    const dim3 grid(static_cast<unsigned>(g.rt1 + g.rt2));
-    if (tokens == 1) {
-        hipLaunchKernelGGL((k_decode_fused<1, 24>), grid, dim3(kBlock), 0, stream, a);
+    return NQ_OK;
+}
+
+int launch_batch(FusedBatch& batch, int64_t tokens, int64_t max_nsc, hipStream_t stream) {
+    const int64_t n = batch.first2[batch.count];
+    if (n <= 0 || n > 0x7fffffff) return NQ_ERR_SHAPE;
+    const dim3 grid(static_cast<unsigned>(n));
+    if (tokens == 1 && max_nsc <= 32) {
+        // in, rank <= 4096: one 4096-column window per stage, small register file.
+        hipLaunchKernelGGL((k_decode_fused<1, 8>), grid, dim3(kBlock), 0, stream, batch);
+    } else if (tokens == 1) {
+        hipLaunchKernelGGL((k_decode_fused<1, 24>), grid, dim3(kBlock), 0, stream, batch);
     } else if (tokens <= 4) {
-        hipLaunchKernelGGL((k_decode_fused<4, 6>), grid, dim3(kBlock), 0, stream, a);
+        hipLaunchKernelGGL((k_decode_fused<4, 6>), grid, dim3(kBlock), 0, stream, batch);
     } else {
-        hipLaunchKernelGGL((k_decode_fused<16, 4>), grid, dim3(kBlock), 0, stream, a);
+        hipLaunchKernelGGL((k_decode_fused<16, 4>), grid, dim3(kBlock), 0, stream, batch);
     }
-    return launch_status();
+    return nq::launch_status();
+}
+
+}  // namespace
+
+namespace nq {
+
+int64_t decode_scratch_bytes(const nq_linear_desc* d, int64_t tokens) {
+    (void)tokens;
+    if (!d->tiles) return 0;
+    return scratch_bytes(geometry(d->in_features, d->out_features, d->rank));
+}
+
+bool decode_path_applies(const nq_linear_desc* d, int64_t tokens) {
+    return d->tiles != nullptr && tokens >= 1 && tokens <= kMaxTokens;
+}
+
+int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y,
+                  int y_dtype, void* scratch, hipStream_t stream) {
+    return launch_decode_batch(&d, 1, &x, x_dtype, tokens, &y, y_dtype, &scratch, stream);
+}
+
+int launch_decode_batch(const nq_linear_desc* const* descs, int count, const void* const* xs, int x_dtype,
+                        int64_t tokens, void* const* ys, int y_dtype, void* const* scratch,
+                        hipStream_t stream) {
+    if (count < 1 || count > kMaxBatch) return NQ_ERR_SHAPE;
+    if (tokens < 1 || tokens > kMaxTokens) return NQ_ERR_SHAPE;
+    FusedBatch batch{};
+    batch.count = count;
+    int64_t max_nsc = 0;
+    int64_t stage1 = 0;
+    for (int i = 0; i < count; ++i) {
+        TilesGeometry g{};
+        const int st = describe(descs[i], xs[i], x_dtype, tokens, ys[i], y_dtype, scratch[i], batch.p[i], g);
+        if (st != NQ_OK) return st;
+        batch.first1[i] = stage1;
+        stage1 += g.rt1;
+        max_nsc = g.nsc1 > max_nsc ? g.nsc1 : max_nsc;
+        max_nsc = g.nsc2 > max_nsc ? g.nsc2 : max_nsc;
+    }
+    batch.first1[count] = stage1;
+    int64_t stage2 = stage1;
+    for (int i = 0; i < count; ++i) {
+        batch.first2[i] = stage2;
+        stage2 += batch.p[i].n2;
+    }
+    batch.first2[count] = stage2;
+    return launch_batch(batch, tokens, max_nsc, stream);
 }
 
 }  // namespace nq
+
+#ifdef NQ_DECODE_TRACE
+extern "C" int nq_debug_set_trace(uint64_t* buffer) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(g_nq_trace), &buffer, sizeof(buffer)) == hipSuccess ? NQ_OK
+                                                                                             : NQ_ERR_LAUNCH;
+}
+#endif
 
 extern "C" int64_t nq_tiles_header_bytes(void) { return static_cast<int64_t>(kHeaderWords) * 4; }
 

@@ -280,6 +280,53 @@ WorkspaceLayout workspace_layout(const nq_linear_desc* d, int64_t tokens) {
     return w;
 }
 
+// Float patch and output-row sidecar, accumulated into fp32 y after stage 2.
+int apply_extras(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y, char* patch_ws,
+                 hipStream_t s) {
+    int st = NQ_OK;
+    if (d->patch_rank > 0) {
+        float* tmp = reinterpret_cast<float*>(patch_ws);
+        DenseRowsArgs p1{};
+        p1.w = d->patch_right;
+        p1.w_dtype = d->patch_dtype;
+        p1.rows = d->patch_rank;
+        p1.act = ActSource{x, x_dtype, nullptr, 0, d->in_features, d->in_features};
+        p1.tokens = tokens;
+        p1.out = tmp;
+        p1.out_ld = d->patch_rank;
+        st = launch_dense_rows(p1, s);
+        if (st != NQ_OK) return st;
+        DenseRowsArgs p2{};
+        p2.w = d->patch_left;
+        p2.w_dtype = d->patch_dtype;
+        p2.rows = d->out_features;
+        p2.act = ActSource{tmp, NQ_DTYPE_F32, nullptr, 0, d->patch_rank, d->patch_rank};
+        p2.tokens = tokens;
+        p2.out = static_cast<float*>(y);
+        p2.out_ld = d->out_features;
+        p2.accumulate = 1;
+        st = launch_dense_rows(p2, s);
+        if (st != NQ_OK) return st;
+    }
+    if (d->row_count > 0) {
+        DenseRowsArgs r{};
+        r.w = d->row_values;
+        r.w_dtype = NQ_DTYPE_I8;
+        r.rows = d->row_count;
+        r.act = ActSource{x, x_dtype, nullptr, 0, d->in_features, d->in_features};
+        r.tokens = tokens;
+        r.row_scale = d->row_scales;
+        r.row_scale_dtype = d->scale_dtype;
+        r.dst_rows = d->row_indices;
+        r.out = static_cast<float*>(y);
+        r.out_ld = d->out_features;
+        r.accumulate = 1;
+        st = launch_dense_rows(r, s);
+        if (st != NQ_OK) return st;
+    }
+    return NQ_OK;
+}
+
 }  // namespace
 
 extern "C" int64_t nq_linear_workspace_bytes(const nq_linear_desc* desc, int64_t tokens) {
@@ -345,44 +392,37 @@ extern "C" int nq_linear(const nq_linear_desc* d, const void* x, int32_t x_dtype
         if (st != NQ_OK) return st;
     }
 
-    if (d->patch_rank > 0) {
-        float* tmp = reinterpret_cast<float*>(ws + wl.patch_offset);
-        DenseRowsArgs p1{};
-        p1.w = d->patch_right;
-        p1.w_dtype = d->patch_dtype;
-        p1.rows = d->patch_rank;
-        p1.act = ActSource{x, x_dtype, nullptr, 0, d->in_features, d->in_features};
-        p1.tokens = tokens;
-        p1.out = tmp;
-        p1.out_ld = d->patch_rank;
-        st = launch_dense_rows(p1, s);
+    return apply_extras(d, x, x_dtype, tokens, y, ws + wl.patch_offset, s);
+}
+
+extern "C" int nq_linear_batch(const nq_linear_desc* const* descs, int32_t count, const void* const* xs,
+                               int32_t x_dtype, int64_t tokens, void* const* ys, int32_t y_dtype,
+                               void* const* workspaces, const int64_t* workspace_bytes, void* stream) {
+    if (!descs || !xs || !ys || !workspaces || !workspace_bytes) return NQ_ERR_ARGUMENT;
+    if (count < 1 || count > 8) return NQ_ERR_SHAPE;
+    if (tokens < 1 || tokens > 16) return NQ_ERR_SHAPE;
+    if (!nq::is_float_dtype(x_dtype) || !nq::is_float_dtype(y_dtype)) return NQ_ERR_DTYPE;
+    void* scratch[8];
+    for (int i = 0; i < count; ++i) {
+        const nq_linear_desc* d = descs[i];
+        int st = validate(d);
         if (st != NQ_OK) return st;
-        DenseRowsArgs p2{};
-        p2.w = d->patch_left;
-        p2.w_dtype = d->patch_dtype;
-        p2.rows = d->out_features;
-        p2.act = ActSource{tmp, NQ_DTYPE_F32, nullptr, 0, d->patch_rank, d->patch_rank};
-        p2.tokens = tokens;
-        p2.out = static_cast<float*>(y);
-        p2.out_ld = d->out_features;
-        p2.accumulate = 1;
-        st = launch_dense_rows(p2, s);
-        if (st != NQ_OK) return st;
+        if (!d->tiles || !xs[i] || !ys[i]) return NQ_ERR_ARGUMENT;
+        if (y_dtype != NQ_DTYPE_F32 && (d->patch_rank > 0 || d->row_count > 0)) return NQ_ERR_UNSUPPORTED;
+        for (int j = 0; j < i; ++j) {
+            if (descs[j]->tiles == d->tiles) return NQ_ERR_ARGUMENT;  // one sync header per launch
+        }
+        const WorkspaceLayout wl = workspace_layout(d, tokens);
+        if (!workspaces[i] || workspace_bytes[i] < wl.total) return NQ_ERR_WORKSPACE;
+        scratch[i] = static_cast<char*>(workspaces[i]) + wl.decode_offset;
     }
-    if (d->row_count > 0) {
-        DenseRowsArgs r{};
-        r.w = d->row_values;
-        r.w_dtype = NQ_DTYPE_I8;
-        r.rows = d->row_count;
-        r.act = ActSource{x, x_dtype, nullptr, 0, d->in_features, d->in_features};
-        r.tokens = tokens;
-        r.row_scale = d->row_scales;
-        r.row_scale_dtype = d->scale_dtype;
-        r.dst_rows = d->row_indices;
-        r.out = static_cast<float*>(y);
-        r.out_ld = d->out_features;
-        r.accumulate = 1;
-        st = launch_dense_rows(r, s);
+    auto s = static_cast<hipStream_t>(stream);
+    int st = nq::launch_decode_batch(descs, count, xs, x_dtype, tokens, ys, y_dtype, scratch, s);
+    if (st != NQ_OK) return st;
+    for (int i = 0; i < count; ++i) {
+        const WorkspaceLayout wl = workspace_layout(descs[i], tokens);
+        st = apply_extras(descs[i], xs[i], x_dtype, tokens, ys[i],
+                          static_cast<char*>(workspaces[i]) + wl.patch_offset, s);
         if (st != NQ_OK) return st;
     }
     return NQ_OK;

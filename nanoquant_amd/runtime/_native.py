@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "nq_prepare_tiles",
     "nq_linear_workspace_bytes",
     "nq_linear",
+    "nq_linear_batch",
 )
 
 
@@ -128,6 +129,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         "nq_linear": (
             c_int,
             [desc_p, vp, ctypes.c_int32, c_i64, vp, ctypes.c_int32, vp, c_i64, vp],
+        ),
+        "nq_linear_batch": (
+            c_int,
+            [ctypes.POINTER(desc_p), ctypes.c_int32, ctypes.POINTER(vp), ctypes.c_int32, c_i64,
+             ctypes.POINTER(vp), ctypes.c_int32, ctypes.POINTER(vp), ctypes.POINTER(c_i64), vp],
         ),
     }
     for name, (restype, argtypes) in table.items():

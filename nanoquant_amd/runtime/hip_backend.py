@@ -200,8 +200,75 @@ class HipPackedBackend:
             payload.desc.tiles_bytes = size
         return PreparedLayer(self.name, self.version, packed.spec, payload)
 
+    def _payload(self, layer: PreparedLayer) -> _HipPackedPayload:
+        if (layer.backend_name, layer.backend_version) != (self.name, self.version):
+            raise ValueError("prepared runtime layer belongs to a different backend")
+        if not isinstance(layer.payload, _HipPackedPayload):
+            raise TypeError("prepared runtime layer has an invalid HIP packed payload")
+        return layer.payload
+
     def linear(self, value: torch.Tensor, layer: PreparedLayer) -> torch.Tensor:
         return self.linear_into(value, layer, output_dtype=torch.float32)
+
+    def linear_batch(
+        self,
+        values: list[torch.Tensor] | tuple[torch.Tensor, ...],
+        layers: list[PreparedLayer] | tuple[PreparedLayer, ...],
+        *,
+        output_dtype: torch.dtype = torch.float32,
+        outs: list[torch.Tensor] | None = None,
+    ) -> list[torch.Tensor]:
+        """Run up to 8 prepared layers in ONE decode launch (1-16 token slots).
+
+        Generalises the reference's grouped Q/K/V and gate/up projection
+        (src/nanoquant/runtime/cuda_backend.py:65-144): members may have distinct
+        inputs and any rank; inputs may be the same tensor."""
+
+        if len(values) != len(layers) or not 1 <= len(layers) <= 8:
+            raise ValueError("HIP packed batch needs 1-8 layers with one input each")
+        if len({id(layer) for layer in layers}) != len(layers):
+            raise ValueError("HIP packed batch members must be distinct prepared layers")
+        payloads = [self._payload(layer) for layer in layers]
+        if any(p.tiles is None for p in payloads):
+            raise ValueError("HIP packed batch requires layers prepared with tiled decode")
+        tokens = {v.numel() // layer.spec.in_features for v, layer in zip(values, layers)}
+        dtypes = {v.dtype for v in values}
+        if len(tokens) != 1 or len(dtypes) != 1:
+            raise ValueError("HIP packed batch members must share token count and input dtype")
+        (count,) = tokens
+        if not 1 <= count <= 16:
+            raise ValueError("HIP packed batch supports 1-16 token slots")
+        for value, layer, payload in zip(values, layers, payloads):
+            _check_value(value, layer.spec, payload.device)
+        if output_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise ValueError(f"HIP packed output dtype is unsupported: {output_dtype}")
+        device = payloads[0].device
+        if outs is None:
+            outs = [
+                torch.empty((*v.shape[:-1], layer.spec.out_features), dtype=output_dtype, device=device)
+                for v, layer in zip(values, layers)
+            ]
+        for out, value, layer in zip(outs, values, layers):
+            shape = (*value.shape[:-1], layer.spec.out_features)
+            if tuple(out.shape) != shape or out.dtype != output_dtype or not out.is_contiguous():
+                raise ValueError("HIP packed output tensor shape, dtype or layout differs")
+        lib = _native.load()
+        n = len(layers)
+        sizes = [int(lib.nq_linear_workspace_bytes(ctypes.byref(p.desc), count)) for p in payloads]
+        if min(sizes) < 0:
+            raise ValueError("HIP packed layer descriptor was rejected")
+        workspaces = [torch.empty(max(b, 1), dtype=torch.uint8, device=device) for b in sizes]
+        desc_ptrs = (ctypes.POINTER(_native.LinearDesc) * n)(*[ctypes.pointer(p.desc) for p in payloads])
+        x_ptrs = (ctypes.c_void_p * n)(*[v.data_ptr() for v in values])
+        y_ptrs = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+        w_ptrs = (ctypes.c_void_p * n)(*[w.data_ptr() for w in workspaces])
+        w_sizes = (ctypes.c_int64 * n)(*sizes)
+        status = lib.nq_linear_batch(
+            desc_ptrs, n, x_ptrs, _native.dtype_code(values[0].dtype), count, y_ptrs,
+            _native.dtype_code(output_dtype), w_ptrs, w_sizes, _native.current_stream_handle(device),
+        )
+        _native.check("nq_linear_batch", status)
+        return list(outs)
 
     def linear_into(
         self,
@@ -214,24 +281,9 @@ class HipPackedBackend:
         """``linear`` with an explicit output dtype (fp32 boundary by default;
         bf16/f16 stores fuse the cast) and an optional preallocated output."""
 
-        if (layer.backend_name, layer.backend_version) != (self.name, self.version):
-            raise ValueError("prepared runtime layer belongs to a different backend")
-        payload = layer.payload
-        if not isinstance(payload, _HipPackedPayload):
-            raise TypeError("prepared runtime layer has an invalid HIP packed payload")
+        payload = self._payload(layer)
         spec = layer.spec
-        if value.device != payload.device:
-            raise ValueError("HIP packed input and prepared layer must use the same device")
-        if canonical_torch_dtype(value.dtype) not in _FLOAT_DTYPES:
-            raise ValueError(f"HIP packed input dtype is unsupported: {value.dtype}")
-        if value.ndim == 0 or value.shape[-1] != spec.in_features:
-            raise ValueError("HIP packed input feature dimension differs from the layer")
-        if value.numel() == 0:
-            raise ValueError("HIP packed input must contain at least one token")
-        if not value.is_contiguous():
-            raise ValueError("HIP packed input must be contiguous")
-        if value.requires_grad:
-            raise ValueError("HIP packed runtime does not support autograd")
+        _check_value(value, spec, payload.device)
         if output_dtype not in (torch.float32, torch.bfloat16, torch.float16):
             raise ValueError(f"HIP packed output dtype is unsupported: {output_dtype}")
         tokens = value.numel() // spec.in_features
@@ -259,6 +311,21 @@ class HipPackedBackend:
         )
         _native.check("nq_linear", status)
         return out
+
+
+def _check_value(value: torch.Tensor, spec: QuantizedLinearSpec, device: torch.device) -> None:
+    if value.device != device:
+        raise ValueError("HIP packed input and prepared layer must use the same device")
+    if canonical_torch_dtype(value.dtype) not in _FLOAT_DTYPES:
+        raise ValueError(f"HIP packed input dtype is unsupported: {value.dtype}")
+    if value.ndim == 0 or value.shape[-1] != spec.in_features:
+        raise ValueError("HIP packed input feature dimension differs from the layer")
+    if value.numel() == 0:
+        raise ValueError("HIP packed input must contain at least one token")
+    if not value.is_contiguous():
+        raise ValueError("HIP packed input must be contiguous")
+    if value.requires_grad:
+        raise ValueError("HIP packed runtime does not support autograd")
 
 
 def unpack_sign_matrix_device(

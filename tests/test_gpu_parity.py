@@ -74,17 +74,16 @@ def _assert_parity(backend, actual, expected, case=None):
 
 
 def _sync_header_clean(layer) -> bool:
-    """Between launches the decode sync header is all zero except its last
-    line, whose word 0 (sticky timeout flag) must also be zero."""
+    """The decode sync header's last line holds the sticky timeout flag (word 0,
+    must be 0: no launch ever timed out waiting for stage 1) and the magic."""
 
     tiles = layer.payload.tiles
     if tiles is None:
         return True
     torch.cuda.synchronize()
     size = int(_native.load().nq_tiles_header_bytes())
-    words = tiles[:size].view(torch.int32).cpu()
-    counters, misc = words[:-64], words[-64:]
-    return bool((counters == 0).all()) and int(misc[0]) == 0
+    misc = tiles[:size].view(torch.int32).cpu()[-64:]
+    return int(misc[0]) == 0 and int(misc[1]) == 0x4E515432
 
 
 def _run(backend, state, x):
@@ -344,3 +343,45 @@ def test_hip_graph_capture_replays_match_eager(backend):
         assert torch.equal(static_out, eager)
         _ = backend.linear(x, layer)  # eager work between replays
         torch.cuda.synchronize()
+
+
+# --- batched launches ----------------------------------------------------------------
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 16])
+def test_qkv_and_layer_batches_match_oracle(tokens):
+    """One launch for Q/K/V (shared x) and one for all seven Qwen3-8B linears of
+    a layer (four distinct inputs); every member against the oracle."""
+
+    backend = HipPackedBackend()
+    shapes = syn.qwen3_8b_layer()
+    states = [syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 40 + i) for i, s in enumerate(shapes)]
+    layers = [backend.prepare(st, "cuda") for st in states]
+    xa = syn.synthetic_activations(tokens, 4096, seed=1, device="cuda")
+    xo = syn.synthetic_activations(tokens, 4096, seed=2, device="cuda")
+    xm = syn.synthetic_activations(tokens, 4096, seed=3, device="cuda")
+    xd = syn.synthetic_activations(tokens, 12288, seed=4, device="cuda")
+    inputs = [xa, xa, xa, xo, xm, xm, xd]
+    _say("qkv batch", tokens)
+    qkv = backend.linear_batch(inputs[:3], layers[:3])
+    _say("layer batch", tokens)
+    whole = backend.linear_batch(inputs, layers)
+    again = backend.linear_batch(inputs, layers)
+    for i, (state, x) in enumerate(zip(states, inputs)):
+        expected = orc.packed_forward(orc.operands_from_state(state), x.cpu())
+        assert orc.relative_l2(whole[i], expected) <= REL_L2, (state.spec.name, tokens)
+        assert torch.equal(whole[i], again[i])
+        if i < 3:
+            assert torch.equal(qkv[i], whole[i])
+        single = backend.linear(x, layers[i])
+        assert torch.equal(single, whole[i])
+    assert all(_sync_header_clean(layer) for layer in layers)
+
+
+def test_batch_rejects_duplicate_members():
+    backend = HipPackedBackend()
+    state = syn.synthetic_packed_layer(syn.qwen3_8b_layer()[1], seed=3)
+    layer = backend.prepare(state, "cuda")
+    x = syn.synthetic_activations(1, 4096, seed=1, device="cuda")
+    with pytest.raises(ValueError, match="distinct"):
+        backend.linear_batch([x, x], [layer, layer])
