@@ -53,8 +53,19 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+# Launch grouping per decoder layer (indices into the seven projections):
+#   grouped: decode dependency order - Q/K/V share x, O, gate/up share x, down;
+#   single:  one launch per linear;
+#   layer:   the seven linears of a layer with independent inputs in one launch.
+GROUPINGS = {
+    "grouped": ((0, 1, 2), (3,), (4, 5), (6,)),
+    "single": ((0,), (1,), (2,), (3,), (4,), (5,), (6,)),
+    "layer": ((0, 1, 2, 3, 4, 5, 6),),
+}
+
+
 def build_stack(layers: int, tokens: int, device):
-    """Prepared layers plus resident inputs/outputs for every linear call of a step."""
+    """Prepared layers plus resident inputs/outputs for every linear of a step."""
 
     import torch
 
@@ -62,10 +73,11 @@ def build_stack(layers: int, tokens: int, device):
     from nanoquant_amd.runtime import HipPackedBackend
 
     backend = HipPackedBackend()
-    calls = []
+    stack = []
     for layer in range(layers):
         shapes = syn.qwen3_8b_layer(layer)
         inputs = {}
+        entries = []
         for i, shape in enumerate(shapes):
             state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 1000 * layer + i, device=device)
             prepared = backend.prepare(state, device)
@@ -76,13 +88,69 @@ def build_stack(layers: int, tokens: int, device):
                 inputs[key] = syn.synthetic_activations(
                     tokens, shape.in_features, seed=layer * 10 + i, device=device)
             out = torch.empty(tokens, shape.out_features, dtype=torch.float32, device=device)
-            calls.append((shape, prepared, inputs[key], out))
-    return backend, calls
+            entries.append((shape, prepared, inputs[key], out))
+        stack.append(entries)
+    return backend, stack
+
+
+def step_calls(stack, mode: str):
+    """The launches of one step: a list of member lists."""
+
+    return [[entries[i] for i in group] for entries in stack for group in GROUPINGS[mode]]
 
 
 def run_step(backend, calls):
-    for _shape, prepared, x, out in calls:
-        backend.linear_into(x, prepared, out=out)
+    for members in calls:
+        if len(members) == 1:
+            _shape, prepared, x, out = members[0]
+            backend.linear_into(x, prepared, out=out)
+        else:
+            backend.linear_batch([m[2] for m in members], [m[1] for m in members],
+                                 outs=[m[3] for m in members])
+
+
+def time_mode(backend, stack, mode: str, steps: int, warmup: int, use_graph: bool) -> dict:
+    """Capture one step of `mode` in a HIP graph, replay `warmup` + `steps` times;
+    events bracket the timed region."""
+
+    import torch
+
+    calls = step_calls(stack, mode)
+    replay = lambda: run_step(backend, calls)  # noqa: E731
+    if use_graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            run_step(backend, calls)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_step(backend, calls)
+        replay = graph.replay
+    for _ in range(warmup):
+        replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        replay()
+    stop.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - wall0) * 1e3
+    ms_per_step = max(start.elapsed_time(stop), wall_ms) / steps
+    tokens = calls[0][0][2].shape[0]
+    step_bytes = sum(algorithmic_bytes(m[0], tokens) for members in calls for m in members)
+    launch_ms = ms_per_step / len(calls)
+    return {
+        "ms_per_step": ms_per_step,
+        "launches_per_step": len(calls),
+        "step_bytes": step_bytes,
+        "mean_launch_us": launch_ms * 1e3,
+        "bytes_per_launch": step_bytes / len(calls),
+        "achieved_gbs": step_bytes / len(calls) / (launch_ms * 1e-3) / 1e9,
+    }
 
 
 def algorithmic_bytes(shape, tokens: int) -> int:
@@ -151,49 +219,15 @@ def main(argv=None) -> int:
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
     print(f"[bench] building {args.layers}-layer stack, M={args.tokens}", file=sys.stderr, flush=True)
-    backend, calls = build_stack(args.layers, args.tokens, device)
+    backend, stack = build_stack(args.layers, args.tokens, device)
     torch.cuda.synchronize()
-    step_bytes = sum(algorithmic_bytes(shape, args.tokens) for shape, *_ in calls)
-
-    # Capture the step once (outputs/workspaces live in the graph's pool).
-    replay = lambda: run_step(backend, calls)  # noqa: E731
-    graph = None
-    if not args.no_graph:
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            run_step(backend, calls)
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            run_step(backend, calls)
-        replay = graph.replay
-
-    for _ in range(args.warmup):
-        replay()
-    torch.cuda.synchronize()
-    print(f"[bench] warmup done; timing {args.steps} steps", file=sys.stderr, flush=True)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    start.record()
-    for _ in range(args.steps):
-        replay()
-    stop.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    gpu_ms = start.elapsed_time(stop)
-    ms_per_step = max(gpu_ms, wall * 1e3) / args.steps
-
-    # Every launch inside the timed graph is the fused decode kernel (outputs and
-    # workspaces are preallocated in the graph pool), so the event-timed region
-    # divided by the launch count is its average launch duration, inter-kernel
-    # gaps included.
-    launches = args.steps * len(calls)
-    mean_launch_ms = ms_per_step * args.steps / launches
-    mean_bytes = step_bytes / len(calls)
-    achieved = mean_bytes / (mean_launch_ms * 1e-3) / 1e9
+    modes = {}
+    for mode in ("grouped", "single", "layer"):
+        print(f"[bench] mode {mode}: timing {args.steps} steps", file=sys.stderr, flush=True)
+        modes[mode] = time_mode(backend, stack, mode, args.steps, args.warmup, not args.no_graph)
+    head = modes["grouped"]
+    ms_per_step = head["ms_per_step"]
+    achieved = head["achieved_gbs"]
 
     result = {
         "metric": METRIC,
@@ -211,12 +245,13 @@ def main(argv=None) -> int:
         "config": {
             "workload": (
                 f"qwen3-8b-shape packed-linear decode stack: {args.layers} layers x 7 linears "
-                f"(q/o r2048, k/v r819, gate/up/down r3072), M={args.tokens}, HIP-graph step"
+                f"(q/o r2048, k/v r819, gate/up/down r3072), M={args.tokens}, one HIP-graph step = "
+                f"per layer 4 launches (QKV batch, O, gate/up batch, down)"
             ),
             "global_batch": args.tokens,
             "layers": args.layers,
-            "linears_per_step": len(calls),
-            "weight_bytes_per_step": sum(s.weight_bytes for s, *_ in calls),
+            "linears_per_step": 7 * args.layers,
+            "weight_bytes_per_step": sum(e[0].weight_bytes for entries in stack for e in entries),
             "parallelism": "single-gpu",
         },
         "roofline": {
@@ -226,11 +261,23 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "k_decode_fused (one launch per packed linear)",
-            "bytes_per_launch": round(mean_bytes),
-            "mean_launch_us": round(mean_launch_ms * 1e3, 3),
+            "kernel": "k_decode_fused (fused two-stage decode launch; QKV and gate/up batched)",
+            "bytes_per_launch": round(head["bytes_per_launch"]),
+            "mean_launch_us": round(head["mean_launch_us"], 3),
         },
-        "launches_per_step": len(calls),
+        "launches_per_step": head["launches_per_step"],
+        "modes": {
+            name: {
+                "launches_per_step": m["launches_per_step"],
+                "ms_per_step": round(m["ms_per_step"], 4),
+                "tok_per_s": round(args.tokens * 1000.0 / m["ms_per_step"], 2),
+                "mean_launch_us": round(m["mean_launch_us"], 3),
+                "bytes_per_launch": round(m["bytes_per_launch"]),
+                "achieved_gbs": round(m["achieved_gbs"], 1),
+                "frac_of_hbm_peak": round(m["achieved_gbs"] / HBM_PEAK_GBS, 4),
+            }
+            for name, m in modes.items()
+        },
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

@@ -352,38 +352,55 @@ __device__ __forceinline__ void row_absmax(L& lds, const void* __restrict__ act,
     }
 }
 
-// One-token staging in a single memory round trip: every thread loads its
-// NV vectors of a[col] * s[col] into registers, the block reduces max |value|
-// into a range scale (lds.tokscale[0]), then the scaled fp16 values go to LDS
-// row 0. Columns [n, ncols_pad) are zero. Requires ncols_pad <= 2048 * NV.
-template <typename L>
-__device__ __forceinline__ void stage_row_single(L& lds, const void* __restrict__ act, int act_dtype,
-                                                 const void* __restrict__ colscale, int colscale_dtype,
-                                                 int64_t n, int ncols_pad, bool vec) {
-    constexpr int NV = L::kStageCols / (8 * kBlock);
+// One-token staging in a single memory round trip, split in two so the caller
+// can issue other loads (the weight words) after the activation loads:
+//   row_single_load:   every thread loads its NV vectors of a[col] * s[col];
+//   row_single_stage:  the block reduces max |value| into a range scale
+//                      (lds.tokscale[0]) and writes the scaled fp16 values to
+//                      LDS row 0. Columns [n, ncols_pad) are zero.
+// Requires ncols_pad <= 2048 * NV.
+template <int NV>
+struct RowRegs {
     float v[NV][8];
-    float m = 0.0f;
+};
+
+template <typename L>
+__device__ __forceinline__ RowRegs<L::kStageCols / (8 * kBlock)> row_single_load(
+    const void* __restrict__ act, int act_dtype, const void* __restrict__ colscale, int colscale_dtype,
+    int64_t n, int ncols_pad, bool vec) {
+    constexpr int NV = L::kStageCols / (8 * kBlock);
+    RowRegs<NV> r;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int64_t col = 8 * (static_cast<int64_t>(threadIdx.x) + i * kBlock);
         float w[8];
         if (col < ncols_pad) {
             if (vec && col + 8 <= n) {
-                load8(act, act_dtype, col, v[i]);
+                load8(act, act_dtype, col, r.v[i]);
                 if (colscale) load8(colscale, colscale_dtype, col, w);
             } else {
-                load8_tail(act, act_dtype, 0, col, n, v[i]);
+                load8_tail(act, act_dtype, 0, col, n, r.v[i]);
                 if (colscale) load8_tail(colscale, colscale_dtype, 0, col, n, w);
+            }
+            if (colscale) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) r.v[i][k] *= w[k];
             }
         } else {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[i][k] = 0.0f;
+            for (int k = 0; k < 8; ++k) r.v[i][k] = 0.0f;
         }
+    }
+    return r;
+}
+
+template <typename L, int NV>
+__device__ __forceinline__ void row_single_stage(L& lds, RowRegs<NV>& r, int ncols_pad) {
+    float m = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (colscale && col < ncols_pad) v[i][k] *= w[k];
-            m = fmaxf(m, fabsf(v[i][k]));
-        }
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(r.v[i][k]));
     }
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if ((threadIdx.x & 63) == 0) lds.wmax[threadIdx.x >> 6] = m;
@@ -396,8 +413,8 @@ __device__ __forceinline__ void stage_row_single(L& lds, const void* __restrict_
         const int j = threadIdx.x + i * kBlock;
         if (8 * j < ncols_pad) {
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[i][k] *= scale;
-            dst[j] = pack8_f16(v[i]);
+            for (int k = 0; k < 8; ++k) r.v[i][k] *= scale;
+            dst[j] = pack8_f16(r.v[i]);
         }
     }
 }
@@ -459,17 +476,22 @@ __device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
     const uint32_t* tile = a.v_tiles + rt * a.nsc1 * 64;
     constexpr int kWindowSc = 4 * SCMAX;
     uint32_t words[SCMAX];
-    load_words<SCMAX>(words, tile, 0, a.nsc1);
 
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if (MT == 1 && a.nsc1 <= kWindowSc) {
-        // One token, one window: x * s_in loaded once, exact range scale.
-        stage_row_single(lds, a.x, a.x_dtype, a.s_in, a.scale_dtype, a.in,
-                         static_cast<int>(a.nsc1 * kSuperCols), a.x_vec != 0);
+        // One token, one window: x * s_in loaded once (issued before the weight
+        // words, so the in-order load counter lets staging start early), exact
+        // range scale.
+        const int ncols = static_cast<int>(a.nsc1 * kSuperCols);
+        auto xr = row_single_load<Lds<MT, SCMAX>>(a.x, a.x_dtype, a.s_in, a.scale_dtype, a.in, ncols,
+                                                  a.x_vec != 0);
+        load_words<SCMAX>(words, tile, 0, a.nsc1);
+        row_single_stage(lds, xr, ncols);
         __syncthreads();
         NQ_TRACE(1);
         acc = tile_mfma<MT, SCMAX>(lds, words, 0, a.nsc1, 0, acc);
     } else {
+        load_words<SCMAX>(words, tile, 0, a.nsc1);
         // Per-token range scale: bound |x * s_in| by max|x| * max|s_in|.
         if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
         __syncthreads();
@@ -558,8 +580,9 @@ __device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if (MT == 1 && a.nsc2 <= kWindowSc) {
         // One token, one window: lm loaded once, range scale from its own max.
-        stage_row_single(lds, a.lm, NQ_DTYPE_F32, nullptr, 0, lm_ld, static_cast<int>(a.nsc2 * kSuperCols),
-                         true);
+        const int ncols = static_cast<int>(a.nsc2 * kSuperCols);
+        auto lr = row_single_load<Lds<MT, SCMAX>>(a.lm, NQ_DTYPE_F32, nullptr, 0, lm_ld, ncols, true);
+        row_single_stage(lds, lr, ncols);
         __syncthreads();
         acc = tile_mfma<MT, SCMAX>(lds, words, 0, a.nsc2, 0, acc);
     } else {
