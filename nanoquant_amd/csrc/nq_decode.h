@@ -5,6 +5,9 @@
 
 namespace nq {
 
+// Words of the sync header in front of the V tiles in a tiles buffer.
+int64_t tiles_header_words();
+
 // Extra workspace bytes the tiled decode path needs for `tokens` slots.
 int64_t decode_scratch_bytes(const nq_linear_desc* d, int64_t tokens);
 

@@ -735,6 +735,8 @@ int launch_batch(FusedBatch& batch, int64_t tokens, int64_t max_nsc, hipStream_t
 
 namespace nq {
 
+int64_t tiles_header_words() { return kHeaderWords; }
+
 int64_t decode_scratch_bytes(const nq_linear_desc* d, int64_t tokens) {
     (void)tokens;
     if (!d->tiles) return 0;

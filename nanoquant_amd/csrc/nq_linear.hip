@@ -17,6 +17,7 @@
 // four groups of a wave read the same addresses (broadcast).
 #include "nq_common.h"
 #include "nq_decode.h"
+#include "nq_prefill.h"
 
 namespace {
 
@@ -276,7 +277,9 @@ WorkspaceLayout workspace_layout(const nq_linear_desc* d, int64_t tokens) {
     w.lm_offset = 0;
     w.patch_offset = align256(tokens * d->rank * 4);
     w.decode_offset = w.patch_offset + align256(tokens * d->patch_rank * 4);
-    w.total = w.decode_offset + nq::decode_scratch_bytes(d, tokens);
+    const int64_t tiled = nq::decode_path_applies(d, tokens) ? nq::decode_scratch_bytes(d, tokens)
+                                                             : nq::prefill_scratch_bytes(d, tokens);
+    w.total = w.decode_offset + tiled;
     return w;
 }
 
@@ -351,6 +354,9 @@ extern "C" int nq_linear(const nq_linear_desc* d, const void* x, int32_t x_dtype
 
     if (d->tiles && nq::decode_path_applies(d, tokens)) {
         st = nq::launch_decode(d, x, x_dtype, tokens, y, y_dtype, ws + wl.decode_offset, s);
+        if (st != NQ_OK) return st;
+    } else if (nq::prefill_path_applies(d, tokens)) {
+        st = nq::launch_prefill(d, x, x_dtype, tokens, y, y_dtype, ws + wl.decode_offset, s);
         if (st != NQ_OK) return st;
     } else {
         float* lm = reinterpret_cast<float*>(ws + wl.lm_offset);

@@ -1,0 +1,329 @@
+// Prefill path (tokens > 16) for the packed binary low-rank linear on gfx950:
+// two dense sign GEMMs on v_mfma_f32_16x16x32_f16.
+//
+//   k_prep_rows:  xs16[t, :] = fp16(x[t, :] * s_in * 2^e_t)       (exact power of
+//                 two per row from max |x * s_in|, so fp16 cannot overflow)
+//   GEMM 1:       lm[t, r]   = s_mid[r] * (xs16 · V±1ᵀ)[t, r] / 2^e_t   (fp32)
+//   k_prep_rows:  lm16[t, :] = fp16(lm[t, :] * 2^f_t)
+//   GEMM 2:       y[t, o]    = s_out[o] * (lm16 · U±1ᵀ)[t, o] / 2^f_t
+//                              + Σ_k x[t, idx_k] W_sal[o, k] (* scale_k) + bias[o]
+//
+// The sign operand comes straight from the decode tile layout (16-row tiles x
+// 128-column superchunks, one word per lane per superchunk, bits in MFMA
+// B-operand order): a wave loads the words of its four 16-row tiles for one
+// superchunk (256 contiguous bytes each), expands them in registers to fp16
+// ±1 (one shift + one and_or per pair) and reuses every expanded operand for
+// its four 16-row M tiles. The activation tile (128 rows x 128 columns fp16)
+// is staged in LDS with a padded row stride and read as ds_read_b128.
+//
+// Block tile 128 (tokens) x 128 (sign rows), 4 waves in a 2 x 2 grid, each
+// wave 64 x 64 = 4 x 4 MFMA tiles of 16 x 16 accumulated in fp32.
+#include "nq_prefill.h"
+
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kBlock = 256;
+constexpr int kBM = 128;
+constexpr int kBN = 128;
+constexpr int kBK = 128;                 // one superchunk per K step
+constexpr int kAStride = kBK + 8;        // halfs; rows land in different banks
+constexpr int kTileRows = 16;
+constexpr int kParkStride = 65;          // floats per parked accumulator row
+constexpr int kALdsBytes = kBM * kAStride * 2;
+constexpr int kParkBytes = 4 * 64 * kParkStride * 4;
+constexpr int kLdsBytes = kALdsBytes > kParkBytes ? kALdsBytes : kParkBytes;
+
+__device__ __forceinline__ float exp2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
+
+__device__ __forceinline__ float range_scale(float bound) {
+    if (!(bound > 0.0f)) return 1.0f;
+    int e = static_cast<int>((__float_as_uint(bound) >> 23) & 0xff) - 127;
+    e = 13 - (e < -126 ? -126 : e);
+    e = e > 100 ? 100 : (e < -100 ? -100 : e);
+    return exp2i(e);
+}
+
+// One workgroup per row: out16[t, c] = fp16(a[t, c] * s[c] * scale_t) for
+// c < cols, zero for cols <= c < cols_pad; scale_out[t] = scale_t.
+__global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ act, int act_dtype, int64_t ld,
+                                                      const void* __restrict__ colscale, int colscale_dtype,
+                                                      int64_t cols, int64_t cols_pad,
+                                                      _Float16* __restrict__ out16, float* __restrict__ scale_out) {
+    __shared__ float wmax[kBlock / 64];
+    const int64_t t = blockIdx.x;
+    float m = 0.0f;
+    for (int64_t c = threadIdx.x; c < cols; c += kBlock) {
+        float v = nq::load_f32(act, act_dtype, t * ld + c);
+        if (colscale) v *= nq::load_f32(colscale, colscale_dtype, c);
+        m = fmaxf(m, fabsf(v));
+    }
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const float scale = range_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+    for (int64_t c = threadIdx.x; c < cols_pad; c += kBlock) {
+        float v = 0.0f;
+        if (c < cols) {
+            v = nq::load_f32(act, act_dtype, t * ld + c);
+            if (colscale) v *= nq::load_f32(colscale, colscale_dtype, c);
+        }
+        out16[t * cols_pad + c] = static_cast<_Float16>(v * scale);
+    }
+    if (threadIdx.x == 0) scale_out[t] = scale;
+}
+
+__device__ __forceinline__ v8h expand_signs(uint32_t word, int m) {
+    union {
+        uint32_t u[4];
+        v8h v;
+    } r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const int s = 4 * m + d;
+        r.u[d] = ((word << s) & 0x80008000u) | 0x3C003C00u;
+    }
+    return r.v;
+}
+
+struct GemmArgs {
+    const _Float16* a;        // [M, kpad] fp16 activations (row-scaled)
+    int64_t m;                // tokens
+    int64_t kpad;             // nsc * 128
+    const uint32_t* tiles;    // sign tiles [rt][nsc][64]
+    int64_t n;                // sign rows (rank or out)
+    int64_t nsc;
+    const float* row_scale;   // [M]: divide accumulators by this
+    const void* col_scale;    // [n] s_mid or s_out
+    int col_scale_dtype;
+    // epilogue (GEMM 2 only; salient_count == 0 and bias == null for GEMM 1)
+    const void* x;
+    int x_dtype;
+    int64_t in;
+    int64_t salient_count;
+    const int32_t* salient_indices;
+    const void* salient_values;
+    int salient_dtype;
+    const void* salient_scales;
+    int scale_dtype;
+    const void* bias;
+    int bias_dtype;
+    void* out;                // [M, n]
+    int out_dtype;
+};
+
+__global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
+    __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+    _Float16* const a_lds = reinterpret_cast<_Float16*>(lds);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1;  // wave row in the 2 x 2 grid
+    const int wn = wave & 1;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kBN;
+    const int64_t rt_count = (g.n + kTileRows - 1) / kTileRows;
+    const int64_t rt0 = n0 / kTileRows + 4 * wn;  // first 16-row tile of this wave
+
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Software pipeline: the sign words and the activation tile of superchunk
+    // sc + 1 are loaded into registers while superchunk sc runs on the MFMAs.
+    uint32_t words[4], next_words[4];
+    uint4 next_a[8];
+    // Plain locals (not the by-value kernel argument) so the loader stays in registers.
+    const uint32_t* const tiles = g.tiles;
+    const _Float16* const act = g.a;
+    const int64_t nsc = g.nsc, kpad = g.kpad, mrows = g.m;
+    auto load_step = [&](int64_t sc) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t rt = rt0 + j;
+            next_words[j] = rt < rt_count ? tiles[(rt * nsc + sc) * 64 + lane] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int v = threadIdx.x + i * kBlock;
+            const int64_t row = m0 + (v >> 4);
+            next_a[i] = row < mrows ? *reinterpret_cast<const uint4*>(act + row * kpad + sc * kBK + (v & 15) * 8)
+                                    : make_uint4(0, 0, 0, 0);
+        }
+    };
+    load_step(0);
+    for (int64_t sc = 0; sc < nsc; ++sc) {
+        __syncthreads();  // previous step's LDS reads are done
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int v = threadIdx.x + i * kBlock;
+            *reinterpret_cast<uint4*>(&a_lds[(v >> 4) * kAStride + (v & 15) * 8]) = next_a[i];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) words[j] = next_words[j];
+        __syncthreads();
+        if (sc + 1 < nsc) load_step(sc + 1);
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) {
+            v8h b[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = expand_signs(words[j], kc);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 64 * wm + 16 * i + (lane & 15);
+                const v8h a = *reinterpret_cast<const v8h*>(&a_lds[r * kAStride + 32 * kc + 8 * (lane >> 4)]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+
+    // Epilogue through LDS: each wave parks its 64 x 64 fp32 tile (lane holds
+    // D[4*(lane/16) + q][lane % 16] of each 16 x 16 MFMA tile), then walks it
+    // row by row with lane = column, so every output row segment is one
+    // coalesced 64-wide store and the salient sum joins before the single
+    // rounding to the output dtype.
+    __syncthreads();  // every wave is done reading the activation tile
+    float* park = reinterpret_cast<float*>(lds) + wave * (64 * kParkStride);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                park[(16 * i + 4 * (lane >> 4) + q) * kParkStride + 16 * j + (lane & 15)] = acc[i][j][q];
+    __syncthreads();
+    const int64_t col = n0 + 64 * wn + lane;
+    if (col >= g.n) return;
+    const float cs = nq::load_f32(g.col_scale, g.col_scale_dtype, col);
+    const float bias = g.bias ? nq::load_f32(g.bias, g.bias_dtype, col) : 0.0f;
+    const int64_t salient = g.salient_count;
+    const int64_t row0 = m0 + 64 * wm;
+    const int rows = static_cast<int>(g.m - row0 < 64 ? g.m - row0 : 64);
+    for (int e = 0; e < rows; ++e) {
+        const int64_t row = row0 + e;
+        float v = park[e * kParkStride + lane] / g.row_scale[row] * cs + bias;
+        for (int64_t k = 0; k < salient; ++k) {
+            float w = nq::load_f32(g.salient_values, g.salient_dtype, col * salient + k);
+            if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
+            v += w * nq::load_f32(g.x, g.x_dtype, row * g.in + g.salient_indices[k]);
+        }
+        nq::store_f32_as(g.out, g.out_dtype, row * g.n + col, v);
+    }
+}
+
+struct Geometry {
+    int64_t rt1, nsc1, rt2, nsc2, v_words, u_words;
+};
+
+Geometry geometry(const nq_linear_desc* d) {
+    Geometry g{};
+    g.rt1 = (d->rank + kTileRows - 1) / kTileRows;
+    g.nsc1 = (d->in_features + kBK - 1) / kBK;
+    g.rt2 = (d->out_features + kTileRows - 1) / kTileRows;
+    g.nsc2 = (d->rank + kBK - 1) / kBK;
+    g.v_words = g.rt1 * g.nsc1 * 64;
+    g.u_words = g.rt2 * g.nsc2 * 64;
+    return g;
+}
+
+int64_t a256(int64_t n) { return (n + 255) & ~int64_t(255); }
+
+struct Scratch {
+    int64_t xs16, scale1, lm, lm16, scale2, total;
+};
+
+Scratch scratch_layout(const nq_linear_desc* d, int64_t tokens) {
+    const Geometry g = geometry(d);
+    Scratch s{};
+    s.xs16 = 0;
+    s.scale1 = s.xs16 + a256(tokens * g.nsc1 * kBK * 2);
+    s.lm = s.scale1 + a256(tokens * 4);
+    s.lm16 = s.lm + a256(tokens * d->rank * 4);
+    s.scale2 = s.lm16 + a256(tokens * g.nsc2 * kBK * 2);
+    s.total = s.scale2 + a256(tokens * 4);
+    return s;
+}
+
+}  // namespace
+
+namespace nq {
+
+int64_t prefill_scratch_bytes(const nq_linear_desc* d, int64_t tokens) {
+    if (!d->tiles) return 0;
+    return scratch_layout(d, tokens).total;
+}
+
+bool prefill_path_applies(const nq_linear_desc* d, int64_t tokens) {
+    return d->tiles != nullptr && tokens > 16 && tokens <= 65535 * int64_t(kBM);
+}
+
+int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y, int y_dtype,
+                   void* scratch, hipStream_t stream) {
+    const Geometry geo = geometry(d);
+    const int64_t header_words = tiles_header_words();
+    if (d->tiles_bytes < (header_words + geo.v_words + geo.u_words) * 4) return NQ_ERR_ARGUMENT;
+    // The GEMMs read the fp16 staging buffers with 16-byte vector loads.
+    if ((reinterpret_cast<uintptr_t>(scratch) & 15) != 0) return NQ_ERR_ALIGNMENT;
+    const Scratch sl = scratch_layout(d, tokens);
+    char* ws = static_cast<char*>(scratch);
+    auto* xs16 = reinterpret_cast<_Float16*>(ws + sl.xs16);
+    auto* scale1 = reinterpret_cast<float*>(ws + sl.scale1);
+    auto* lm = reinterpret_cast<float*>(ws + sl.lm);
+    auto* lm16 = reinterpret_cast<_Float16*>(ws + sl.lm16);
+    auto* scale2 = reinterpret_cast<float*>(ws + sl.scale2);
+    const auto* base = static_cast<const uint32_t*>(d->tiles);
+    const dim3 rows(static_cast<unsigned>(tokens));
+
+    hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, x, x_dtype, d->in_features, d->scale_pre,
+                       d->scale_dtype, d->in_features, geo.nsc1 * kBK, xs16, scale1);
+    GemmArgs g1{};
+    g1.a = xs16;
+    g1.m = tokens;
+    g1.kpad = geo.nsc1 * kBK;
+    g1.tiles = base + header_words;
+    g1.n = d->rank;
+    g1.nsc = geo.nsc1;
+    g1.row_scale = scale1;
+    g1.col_scale = d->scale_mid;
+    g1.col_scale_dtype = d->scale_dtype;
+    g1.out = lm;
+    g1.out_dtype = NQ_DTYPE_F32;
+    const dim3 grid1(static_cast<unsigned>((d->rank + kBN - 1) / kBN), static_cast<unsigned>((tokens + kBM - 1) / kBM));
+    hipLaunchKernelGGL(k_sign_gemm, grid1, dim3(kBlock), 0, stream, g1);
+
+    hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, lm, NQ_DTYPE_F32, d->rank, nullptr, 0, d->rank,
+                       geo.nsc2 * kBK, lm16, scale2);
+    GemmArgs g2{};
+    g2.a = lm16;
+    g2.m = tokens;
+    g2.kpad = geo.nsc2 * kBK;
+    g2.tiles = base + header_words + geo.v_words;
+    g2.n = d->out_features;
+    g2.nsc = geo.nsc2;
+    g2.row_scale = scale2;
+    g2.col_scale = d->scale_post;
+    g2.col_scale_dtype = d->scale_dtype;
+    g2.x = x;
+    g2.x_dtype = x_dtype;
+    g2.in = d->in_features;
+    g2.salient_count = d->salient_count;
+    g2.salient_indices = d->salient_indices;
+    g2.salient_values = d->salient_values;
+    g2.salient_dtype = d->salient_dtype;
+    g2.salient_scales = d->salient_scales;
+    g2.scale_dtype = d->scale_dtype;
+    g2.bias = d->bias;
+    g2.bias_dtype = d->bias_dtype;
+    g2.out = y;
+    g2.out_dtype = y_dtype;
+    const dim3 grid2(static_cast<unsigned>((d->out_features + kBN - 1) / kBN),
+                     static_cast<unsigned>((tokens + kBM - 1) / kBM));
+    hipLaunchKernelGGL(k_sign_gemm, grid2, dim3(kBlock), 0, stream, g2);
+    return launch_status();
+}
+
+}  // namespace nq

@@ -296,6 +296,66 @@ def test_gemma3_4b_down_with_sidecars(backend, tokens):
     _check_shape(backend, rows, tokens, seed=tokens)
 
 
+# --- prefill: tokens > 16 run two MFMA sign GEMMs ------------------------------------
+
+
+@pytest.mark.parametrize("tokens", [17, 40, 129, 300])
+@pytest.mark.parametrize("geometry", [(35, 17, 33, 3), (200, 130, 129, 5), (1152, 864, 768, 0),
+                                      (640, 257, 96, 31)])
+def test_prefill_ragged_geometries(tokens, geometry):
+    """Word tails, partial 16-row tiles, partial 128-token blocks, salient
+    columns (int8 with scales) and bias on the MFMA prefill kernels."""
+
+    in_f, out_f, rank, k = geometry
+    backend = HipPackedBackend()
+    _say("prefill ragged", geometry, tokens)
+    shape = syn.LinearShape("blocks.0.mlp.gate_proj", in_f, out_f, rank)
+    state = syn.synthetic_packed_layer(shape, seed=tokens + sum(geometry), salient=k, bias=True)
+    _check_shape(backend, state, tokens, seed=tokens)
+
+
+@pytest.mark.parametrize("x_dtype", _FLOATS)
+def test_prefill_input_dtypes_and_patch(x_dtype):
+    logical = _matrix_state(torch.bfloat16, torch.float16, torch.float16, True)
+    packed = pack_logical_layer(logical)
+    backend = HipPackedBackend()
+    _say("prefill dtype", x_dtype)
+    layer = backend.prepare(packed, "cuda")
+    x = torch.linspace(-2.0, 1.5, 35 * 70, dtype=x_dtype).reshape(2, 35, 35)
+    y = backend.linear(x.cuda(), layer)
+    assert y.shape == (2, 35, 17) and y.dtype == torch.float32
+    err = orc.relative_l2(y, orc.CpuPackedForward(orc.operands_from_state(packed))(x))
+    assert err <= REL_L2, (x_dtype, err)
+    shape = syn.gemma3_4b_down()
+    rows = syn.synthetic_row_sidecar(syn.synthetic_packed_layer(shape, seed=5), 26, seed=6)
+    _check_shape(backend, rows, 64, seed=7)
+
+
+def test_prefill_output_dtypes():
+    backend = HipPackedBackend()
+    shape = syn.LinearShape("blocks.0.mlp.down_proj", 512, 384, 200)
+    state = syn.synthetic_packed_layer(shape, seed=11, salient=4, bias=True)
+    layer = backend.prepare(state, "cuda")
+    x = syn.synthetic_activations(96, 512, seed=12, device="cuda")
+    y32 = backend.linear(x, layer)
+    for dtype in (torch.bfloat16, torch.float16):
+        _say("prefill out dtype", dtype)
+        out = torch.empty(96, 384, dtype=dtype, device="cuda")
+        backend.linear_into(x, layer, output_dtype=dtype, out=out)
+        torch.testing.assert_close(out, y32.to(dtype), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("tokens", [256, 512, 2048])
+def test_llama3_8b_prefill_sweep(tokens):
+    backend = HipPackedBackend()
+    shapes = syn.llama3_8b_layer()
+    picks = shapes if tokens == 256 else [shapes[1], shapes[4], shapes[6]]
+    for shape in picks:
+        _say("llama sweep", shape.name, tokens)
+        state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 60 + tokens)
+        _check_shape(backend, state, tokens, seed=tokens)
+
+
 # --- integration ---------------------------------------------------------------------
 
 
