@@ -40,6 +40,12 @@ def parse_args(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a graph")
+    p.add_argument("--modes", default="grouped,grouped-fused,single,layer",
+                   help="comma-separated decode launch groupings to time (first one is the headline)")
+    p.add_argument("--prefill-tokens", default="64,256,512,2048",
+                   help="token counts of the Llama-3-8B prefill sweep ('' to skip)")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB 10 times (byte-counter calibration) and exit")
     return p.parse_args(argv)
 
 
@@ -57,11 +63,17 @@ def _cpu_model() -> str:
 #   grouped: decode dependency order - Q/K/V share x, O, gate/up share x, down;
 #   single:  one launch per linear;
 #   layer:   the seven linears of a layer with independent inputs in one launch.
+# A "-fused" suffix runs the same grouping with the single-kernel decode
+# launch (in-kernel grid handoff) instead of the default two-kernel split.
 GROUPINGS = {
     "grouped": ((0, 1, 2), (3,), (4, 5), (6,)),
     "single": ((0,), (1,), (2,), (3,), (4,), (5,), (6,)),
     "layer": ((0, 1, 2, 3, 4, 5, 6),),
 }
+
+
+def _grouping(mode: str):
+    return GROUPINGS[mode.removesuffix("-fused")]
 
 
 def build_stack(layers: int, tokens: int, device):
@@ -93,10 +105,14 @@ def build_stack(layers: int, tokens: int, device):
     return backend, stack
 
 
-def step_calls(stack, mode: str):
-    """The launches of one step: a list of member lists."""
+def step_calls(stack, mode: str, backend=None):
+    """The calls of one step: a list of member lists."""
 
-    return [[entries[i] for i in group] for entries in stack for group in GROUPINGS[mode]]
+    calls = [[entries[i] for i in group] for entries in stack for group in _grouping(mode)]
+    if mode.endswith("-fused"):
+        calls = [[(shape, backend.with_decode_launch(prepared, "fused"), x, out)
+                  for shape, prepared, x, out in members] for members in calls]
+    return calls
 
 
 def run_step(backend, calls):
@@ -115,7 +131,7 @@ def time_mode(backend, stack, mode: str, steps: int, warmup: int, use_graph: boo
 
     import torch
 
-    calls = step_calls(stack, mode)
+    calls = step_calls(stack, mode, backend)
     replay = lambda: run_step(backend, calls)  # noqa: E731
     if use_graph:
         side = torch.cuda.Stream()
@@ -142,14 +158,15 @@ def time_mode(backend, stack, mode: str, steps: int, warmup: int, use_graph: boo
     ms_per_step = max(start.elapsed_time(stop), wall_ms) / steps
     tokens = calls[0][0][2].shape[0]
     step_bytes = sum(algorithmic_bytes(m[0], tokens) for members in calls for m in members)
-    launch_ms = ms_per_step / len(calls)
+    call_ms = ms_per_step / len(calls)
     return {
         "ms_per_step": ms_per_step,
-        "launches_per_step": len(calls),
+        "calls_per_step": len(calls),
+        "kernels_per_step": len(calls) * (1 if mode.endswith("-fused") else 2),
         "step_bytes": step_bytes,
-        "mean_launch_us": launch_ms * 1e3,
-        "bytes_per_launch": step_bytes / len(calls),
-        "achieved_gbs": step_bytes / len(calls) / (launch_ms * 1e-3) / 1e9,
+        "mean_call_us": call_ms * 1e3,
+        "bytes_per_call": step_bytes / len(calls),
+        "achieved_gbs": step_bytes / len(calls) / (call_ms * 1e-3) / 1e9,
     }
 
 
@@ -188,7 +205,7 @@ def cpu_baseline(tokens: int, budget_s: float, layers: int) -> dict:
     samples.sort()
     median = samples[len(samples) // 2]
     return {
-        "value": tokens / (median * layers),
+        "value": round(tokens / (median * layers), 4),
         "unit": "tok/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
@@ -198,6 +215,74 @@ def cpu_baseline(tokens: int, budget_s: float, layers: int) -> dict:
             f"{median * 1e3:.1f} ms/layer), scaled x{layers} layers; cpu={_cpu_model()}"
         ),
     }
+
+
+FP16_DENSE_PEAK_TFLOPS = 2500.0
+
+
+def prefill_sweep(token_counts, steps: int, warmup: int) -> dict:
+    """Config: the seven Llama-3-8B linears (~0.8 bpw) at each token count, each
+    linear launched eagerly on the current stream; events bracket `steps`
+    repetitions of the whole layer. TFLOP/s counts the two sign GEMMs
+    (2*M*(in*r + r*out)) against the fp16 dense MFMA peak."""
+
+    import torch
+
+    from nanoquant_amd import synthetic as syn
+    from nanoquant_amd.runtime import HipPackedBackend
+
+    device = torch.device("cuda", 0)
+    backend = HipPackedBackend()
+    shapes = syn.llama3_8b_layer()
+    layers = [backend.prepare(syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 500 + i, device=device), device)
+              for i, s in enumerate(shapes)]
+    sweep = {}
+    for tokens in token_counts:
+        xs = {s.in_features: syn.synthetic_activations(tokens, s.in_features, seed=tokens, device=device)
+              for s in shapes}
+        outs = [torch.empty(tokens, s.out_features, dtype=torch.float32, device=device) for s in shapes]
+
+        def layer_pass():
+            for s, layer, out in zip(shapes, layers, outs):
+                backend.linear_into(xs[s.in_features], layer, out=out)
+
+        for _ in range(warmup):
+            layer_pass()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            layer_pass()
+        stop.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(stop) / steps
+        flops = sum(2 * tokens * (s.in_features * s.rank + s.rank * s.out_features) for s in shapes)
+        tflops = flops / (ms * 1e-3) / 1e12
+        sweep[str(tokens)] = {
+            "ms_per_layer": round(ms, 4),
+            "tok_per_s": round(tokens * 1000.0 / ms, 1),
+            "tflops": round(tflops, 2),
+            "frac_of_fp16_peak": round(tflops / FP16_DENSE_PEAK_TFLOPS, 4),
+        }
+    return {
+        "workload": "llama-3-8b-shape packed linears (q/o r1638, k/v r655, gate/up/down r2549), one layer",
+        "peak_tflops": FP16_DENSE_PEAK_TFLOPS,
+        "points": sweep,
+    }
+
+
+def copy_calibration(mib: int) -> int:
+    """A plain device-to-device copy of known size, for scaling HBM byte counters."""
+
+    import torch
+
+    src = torch.ones(mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": src.numel() * 4, "written": dst.numel() * 4}))
+    return 0
 
 
 def main(argv=None) -> int:
@@ -214,6 +299,13 @@ def main(argv=None) -> int:
         print("--tokens must be in 1..16 (decode path)", file=sys.stderr)
         return 2
 
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
+    modes_wanted = [m for m in args.modes.split(",") if m]
+    if not modes_wanted or any(m.removesuffix("-fused") not in GROUPINGS for m in modes_wanted):
+        print(f"--modes must name some of {sorted(GROUPINGS)} (optionally with -fused)", file=sys.stderr)
+        return 2
+
     import torch
 
     device = torch.device("cuda", 0)
@@ -222,10 +314,11 @@ def main(argv=None) -> int:
     backend, stack = build_stack(args.layers, args.tokens, device)
     torch.cuda.synchronize()
     modes = {}
-    for mode in ("grouped", "single", "layer"):
+    for mode in modes_wanted:
         print(f"[bench] mode {mode}: timing {args.steps} steps", file=sys.stderr, flush=True)
         modes[mode] = time_mode(backend, stack, mode, args.steps, args.warmup, not args.no_graph)
-    head = modes["grouped"]
+    head_mode = modes_wanted[0]
+    head = modes[head_mode]
     ms_per_step = head["ms_per_step"]
     achieved = head["achieved_gbs"]
 
@@ -245,8 +338,8 @@ def main(argv=None) -> int:
         "config": {
             "workload": (
                 f"qwen3-8b-shape packed-linear decode stack: {args.layers} layers x 7 linears "
-                f"(q/o r2048, k/v r819, gate/up/down r3072), M={args.tokens}, one HIP-graph step = "
-                f"per layer 4 launches (QKV batch, O, gate/up batch, down)"
+                f"(q/o r2048, k/v r819, gate/up/down r3072), M={args.tokens}, one HIP-graph step, "
+                f"launch grouping '{head_mode}'"
             ),
             "global_batch": args.tokens,
             "layers": args.layers,
@@ -261,25 +354,33 @@ def main(argv=None) -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "k_decode_fused (fused two-stage decode launch; QKV and gate/up batched)",
-            "bytes_per_launch": round(head["bytes_per_launch"]),
-            "mean_launch_us": round(head["mean_launch_us"], 3),
+            "kernel": (f"one decode call = k_decode_fused" if head_mode.endswith("-fused") else
+                       "one decode call = k_decode_stage1 + k_decode_stage2") + f" (grouping '{head_mode}')",
+            "bytes_per_call": round(head["bytes_per_call"]),
+            "mean_call_us": round(head["mean_call_us"], 3),
         },
-        "launches_per_step": head["launches_per_step"],
+        "calls_per_step": head["calls_per_step"],
+        "kernels_per_step": head["kernels_per_step"],
         "modes": {
             name: {
-                "launches_per_step": m["launches_per_step"],
+                "calls_per_step": m["calls_per_step"],
+                "kernels_per_step": m["kernels_per_step"],
                 "ms_per_step": round(m["ms_per_step"], 4),
                 "tok_per_s": round(args.tokens * 1000.0 / m["ms_per_step"], 2),
-                "mean_launch_us": round(m["mean_launch_us"], 3),
-                "bytes_per_launch": round(m["bytes_per_launch"]),
+                "mean_call_us": round(m["mean_call_us"], 3),
+                "bytes_per_call": round(m["bytes_per_call"]),
                 "achieved_gbs": round(m["achieved_gbs"], 1),
                 "frac_of_hbm_peak": round(m["achieved_gbs"] / HBM_PEAK_GBS, 4),
             }
             for name, m in modes.items()
         },
+        "prefill": None,
         "cpu_baseline": None,
     }
+    prefill_tokens = [int(t) for t in args.prefill_tokens.split(",") if t]
+    if prefill_tokens:
+        print(f"[bench] prefill sweep M={prefill_tokens}", file=sys.stderr, flush=True)
+        result["prefill"] = prefill_sweep(prefill_tokens, max(args.steps // 2, 3), 2)
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.tokens, args.cpu_seconds, args.layers)

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 1
+#define NQ_ABI_VERSION 2
 
 typedef enum nq_dtype {
     NQ_DTYPE_F32 = 0,
@@ -51,6 +51,18 @@ typedef enum nq_status {
     NQ_ERR_DEVICE = -7,      /* no HIP device or wrong architecture          */
     NQ_ERR_UNSUPPORTED = -8  /* valid request this build does not implement  */
 } nq_status;
+
+/* Launch structure of the tiled decode path (tokens <= 16).
+ *   NQ_DECODE_SPLIT: two kernels per call (stage 1 writes the rank-r
+ *     intermediate, the kernel boundary publishes it, stage 2 reads it).
+ *   NQ_DECODE_FUSED: one kernel; stage-2 workgroups wait on a grid-wide
+ *     counter in the tiles header that stage-1 workgroups signal.
+ * Both give bit-identical results. No reference counterpart (the reference
+ * always launches two Triton kernels, cuda_kernels.py:816-874). */
+typedef enum nq_decode_launch {
+    NQ_DECODE_SPLIT = 0,
+    NQ_DECODE_FUSED = 1
+} nq_decode_launch;
 
 /* Device facts used by the backend's capability check.
  * Replaces the CUDA capability probe of CudaPackedBackend.supports
@@ -98,6 +110,7 @@ typedef struct nq_linear_desc {
     const void* row_scales;       /* [row_count] (scale_dtype)         */
     const void* tiles;            /* GPU layout from nq_prepare_tiles, or NULL */
     int64_t tiles_bytes;
+    int32_t decode_launch;        /* nq_decode_launch; batch members must agree */
 } nq_linear_desc;
 
 /* Library ABI version (NQ_ABI_VERSION). No reference counterpart. */

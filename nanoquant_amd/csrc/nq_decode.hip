@@ -16,14 +16,21 @@
 // is two fp16 ±1 values in one shift + one and_or. A wave reads one word per
 // lane per superchunk: 256 contiguous bytes, fully coalesced.
 //
-// Grid: one launch. The first workgroups are stage-1 tiles (16 ranks each, the
-// four waves split the columns) of every linear in the batch, the rest are
-// stage-2 tiles (16 output rows each). Stage-1 workgroups store lm (fp32)
-// write-through at agent scope and then signal; stage-2 workgroups issue the
-// loads of their U tile first, then wait for their linear's signal (bounded
-// spin), so the U stream overlaps stage 1. Workgroups are dispatched in index
-// order, so every stage-1 workgroup is resident or finished before a stage-2
-// workgroup can take its slot, and stage-1 workgroups never wait.
+// Launch structure (nq_linear_desc.decode_launch):
+//   split (default): kernel 1 runs the stage-1 tiles (16 ranks each, the four
+//     waves split the columns) of every linear in the batch and stores lm;
+//     kernel 2 runs the stage-2 tiles (16 output rows each). The kernel
+//     boundary is the grid-wide barrier.
+//   fused: one kernel whose first workgroups are the stage-1 tiles and the
+//     rest the stage-2 tiles. Stage-1 workgroups store lm write-through at
+//     agent scope and then signal; stage-2 workgroups issue the loads of
+//     their U tile first, then wait for their linear's signal (bounded spin),
+//     so the U stream overlaps stage 1. Workgroups are dispatched in index
+//     order, so every stage-1 workgroup is resident or finished before a
+//     stage-2 workgroup can take its slot, and stage-1 workgroups never wait.
+// On gfx950 the eight XCDs have separate L2s, so the fused signal and its
+// polls travel through the fabric (agent-scope atomics); measured, that costs
+// more than a graph-launched kernel boundary, hence split is the default.
 //
 // Activations enter the fp16 MFMA scaled by an exact per-token power of two
 // (from the exact max |x * s_in| for one token, else max|x| * max|s_in|, and
@@ -470,7 +477,7 @@ __device__ __forceinline__ float reduce_waves(L& lds, v4f acc) {
     return ((lds.red[0][t][n] + lds.red[1][t][n]) + lds.red[2][t][n]) + lds.red[3][t][n];
 }
 
-template <int MT, int SCMAX>
+template <int MT, int SCMAX, bool FUSED>
 __device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT, SCMAX>& lds, int64_t rt) {
     NQ_TRACE(0);
     const uint32_t* tile = a.v_tiles + rt * a.nsc1 * 64;
@@ -524,6 +531,14 @@ __device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
     if (t < a.tokens && r < a.rank) lmv = sum / lds.tokscale[t] * nq::load_f32(a.s_mid, a.scale_dtype, r);
     float am = fabsf(lmv);
     for (int off = 8; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 16));
+    if (!FUSED) {
+        // Split launch: the kernel boundary publishes lm to the stage-2 kernel.
+        if (t < a.tokens) a.lm[t * (a.n1 * kTileRows) + r] = lmv;
+        if (n == 0) a.wgmax[rt * kMaxTokens + t] = am;
+        NQ_TRACE(3);
+        NQ_TRACE(4);
+        return;
+    }
     // lm and the maxima are stored write-through at agent scope (no L2
     // writeback needed); the wait makes them complete before the signal.
     if (t < a.tokens) store_agent(&a.lm[t * (a.n1 * kTileRows) + r], lmv);
@@ -548,7 +563,7 @@ __device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
     NQ_TRACE(4);
 }
 
-template <int MT, int SCMAX>
+template <int MT, int SCMAX, bool FUSED>
 __device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT, SCMAX>& lds, int64_t rt) {
     NQ_TRACE(0);
     const uint32_t* tile = a.u_tiles + rt * a.nsc2 * 64;
@@ -556,9 +571,11 @@ __device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
     uint32_t words[SCMAX];
     load_words<SCMAX>(words, tile, 0, a.nsc2);  // prefetch before waiting
 
-    // Launch index from this workgroup's arrival, then poll its ready flag with
-    // relaxed agent-scope loads; one acquire fence (L2 invalidate) at the end.
-    if (threadIdx.x == 0) {
+    // Fused launch: launch index from this workgroup's arrival, then poll its
+    // ready flag with relaxed agent-scope loads; one acquire fence (L2
+    // invalidate) at the end. Split launch: stage 1 finished in the previous
+    // kernel.
+    if (FUSED && threadIdx.x == 0) {
         const int slot = static_cast<int>(rt % kArriveSlots);
         const uint64_t c = slot_count(slot, kArriveSlots, a.n2);
         const uint32_t target = static_cast<uint32_t>(hdr_add(a.header, line_word(kArriveSlot0 + slot)) / c + 1);
@@ -573,7 +590,7 @@ __device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
-    __syncthreads();
+    if (FUSED) __syncthreads();
     NQ_TRACE(1);
 
     const int64_t lm_ld = a.n1 * kTileRows;
@@ -639,12 +656,33 @@ __global__ __launch_bounds__(kBlock) void k_decode_fused(const FusedBatch batch)
     if (b < batch.first1[batch.count]) {
         int p = 0;
         while (p + 1 < batch.count && b >= batch.first1[p + 1]) ++p;
-        stage1_tile<MT, SCMAX>(batch.p[p], lds, b - batch.first1[p]);
+        stage1_tile<MT, SCMAX, true>(batch.p[p], lds, b - batch.first1[p]);
     } else {
         int p = 0;
         while (p + 1 < batch.count && b >= batch.first2[p + 1]) ++p;
-        stage2_tile<MT, SCMAX>(batch.p[p], lds, b - batch.first2[p]);
+        stage2_tile<MT, SCMAX, true>(batch.p[p], lds, b - batch.first2[p]);
     }
+}
+
+// Split launch, kernel 1: the stage-1 tiles of every linear in the batch.
+template <int MT, int SCMAX>
+__global__ __launch_bounds__(kBlock) void k_decode_stage1(const FusedBatch batch) {
+    __shared__ Lds<MT, SCMAX> lds;
+    const int64_t b = blockIdx.x;
+    int p = 0;
+    while (p + 1 < batch.count && b >= batch.first1[p + 1]) ++p;
+    stage1_tile<MT, SCMAX, false>(batch.p[p], lds, b - batch.first1[p]);
+}
+
+// Split launch, kernel 2: the stage-2 tiles (block index offset by the
+// stage-1 count so first2[] is shared with the fused grid).
+template <int MT, int SCMAX>
+__global__ __launch_bounds__(kBlock) void k_decode_stage2(const FusedBatch batch) {
+    __shared__ Lds<MT, SCMAX> lds;
+    const int64_t b = blockIdx.x + batch.first1[batch.count];
+    int p = 0;
+    while (p + 1 < batch.count && b >= batch.first2[p + 1]) ++p;
+    stage2_tile<MT, SCMAX, false>(batch.p[p], lds, b - batch.first2[p]);
 }
 
 struct TilesGeometry {
@@ -714,19 +752,33 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
     return NQ_OK;
 }
 
-int launch_batch(FusedBatch& batch, int64_t tokens, int64_t max_nsc, hipStream_t stream) {
+template <int MT, int SCMAX>
+void enqueue(const FusedBatch& batch, bool fused, hipStream_t stream) {
+    const int64_t n1 = batch.first1[batch.count];
+    const int64_t n = batch.first2[batch.count];
+    if (fused) {
+        hipLaunchKernelGGL((k_decode_fused<MT, SCMAX>), dim3(static_cast<unsigned>(n)), dim3(kBlock), 0, stream,
+                           batch);
+    } else {
+        hipLaunchKernelGGL((k_decode_stage1<MT, SCMAX>), dim3(static_cast<unsigned>(n1)), dim3(kBlock), 0, stream,
+                           batch);
+        hipLaunchKernelGGL((k_decode_stage2<MT, SCMAX>), dim3(static_cast<unsigned>(n - n1)), dim3(kBlock), 0,
+                           stream, batch);
+    }
+}
+
+int launch_batch(FusedBatch& batch, int64_t tokens, int64_t max_nsc, bool fused, hipStream_t stream) {
     const int64_t n = batch.first2[batch.count];
     if (n <= 0 || n > 0x7fffffff) return NQ_ERR_SHAPE;
-    const dim3 grid(static_cast<unsigned>(n));
     if (tokens == 1 && max_nsc <= 32) {
         // in, rank <= 4096: one 4096-column window per stage, small register file.
-        hipLaunchKernelGGL((k_decode_fused<1, 8>), grid, dim3(kBlock), 0, stream, batch);
+        enqueue<1, 8>(batch, fused, stream);
     } else if (tokens == 1) {
-        hipLaunchKernelGGL((k_decode_fused<1, 24>), grid, dim3(kBlock), 0, stream, batch);
+        enqueue<1, 24>(batch, fused, stream);
     } else if (tokens <= 4) {
-        hipLaunchKernelGGL((k_decode_fused<4, 6>), grid, dim3(kBlock), 0, stream, batch);
+        enqueue<4, 6>(batch, fused, stream);
     } else {
-        hipLaunchKernelGGL((k_decode_fused<16, 4>), grid, dim3(kBlock), 0, stream, batch);
+        enqueue<16, 4>(batch, fused, stream);
     }
     return nq::launch_status();
 }
@@ -762,6 +814,7 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
     int64_t max_nsc = 0;
     int64_t stage1 = 0;
     for (int i = 0; i < count; ++i) {
+        if (descs[i]->decode_launch != descs[0]->decode_launch) return NQ_ERR_ARGUMENT;
         TilesGeometry g{};
         const int st = describe(descs[i], xs[i], x_dtype, tokens, ys[i], y_dtype, scratch[i], batch.p[i], g);
         if (st != NQ_OK) return st;
@@ -777,7 +830,7 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
         stage2 += batch.p[i].n2;
     }
     batch.first2[count] = stage2;
-    return launch_batch(batch, tokens, max_nsc, stream);
+    return launch_batch(batch, tokens, max_nsc, descs[0]->decode_launch == NQ_DECODE_FUSED, stream);
 }
 
 }  // namespace nq

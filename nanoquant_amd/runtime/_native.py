@@ -24,6 +24,9 @@ NQ_ERR_LAUNCH = -6
 NQ_ERR_DEVICE = -7
 NQ_ERR_UNSUPPORTED = -8
 
+NQ_DECODE_SPLIT = 0
+NQ_DECODE_FUSED = 1
+
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
     torch.float16: 1,
@@ -103,6 +106,7 @@ class LinearDesc(ctypes.Structure):
         ("row_scales", ctypes.c_void_p),
         ("tiles", ctypes.c_void_p),
         ("tiles_bytes", ctypes.c_int64),
+        ("decode_launch", ctypes.c_int32),
     ]
 
 

@@ -102,6 +102,9 @@ def _describe(
         desc.row_scales = ptr(p.row_scales)
 
 
+_DECODE_LAUNCH = {"split": _native.NQ_DECODE_SPLIT, "fused": _native.NQ_DECODE_FUSED}
+
+
 class HipPackedBackend:
     """gfx950 HIP kernels behind the reference backend protocol."""
 
@@ -109,8 +112,16 @@ class HipPackedBackend:
     version = HIP_PACKED_BACKEND_VERSION
     packed_layout = PACKED_LAYOUT_VERSION
 
-    def __init__(self, *, tiled_decode: bool = True) -> None:
+    def __init__(self, *, tiled_decode: bool = True, decode_launch: str = "split") -> None:
+        """``tiled_decode`` prepares the MFMA tile layout (decode and prefill
+        kernels); without it every call takes the canonical-word fp32 path.
+        ``decode_launch``: ``"split"`` runs the two decode stages as two
+        kernels, ``"fused"`` as one kernel with an in-kernel grid handoff."""
+
+        if decode_launch not in _DECODE_LAUNCH:
+            raise ValueError(f"decode_launch must be one of {sorted(_DECODE_LAUNCH)}")
         self._tiled_decode = tiled_decode
+        self._decode_launch = _DECODE_LAUNCH[decode_launch]
 
     def capabilities(self) -> BackendCapabilities:
         return BackendCapabilities(
@@ -181,6 +192,7 @@ class HipPackedBackend:
             _native.LinearDesc(),
         )
         _describe(payload, packed.spec, payload.desc)
+        payload.desc.decode_launch = self._decode_launch
         spec = packed.spec
         size = int(lib.nq_tiles_bytes(spec.in_features, spec.out_features, spec.rank))
         if self._tiled_decode and size > 0:
@@ -199,6 +211,17 @@ class HipPackedBackend:
             payload.desc.tiles = tiles.data_ptr()
             payload.desc.tiles_bytes = size
         return PreparedLayer(self.name, self.version, packed.spec, payload)
+
+    def with_decode_launch(self, layer: PreparedLayer, decode_launch: str) -> PreparedLayer:
+        """The same prepared layer (device tensors shared, no copies) with another
+        decode launch structure. Layers sharing tiles must not run concurrently."""
+
+        payload = self._payload(layer)
+        if decode_launch not in _DECODE_LAUNCH:
+            raise ValueError(f"decode_launch must be one of {sorted(_DECODE_LAUNCH)}")
+        desc = _native.LinearDesc.from_buffer_copy(payload.desc)
+        desc.decode_launch = _DECODE_LAUNCH[decode_launch]
+        return PreparedLayer(layer.backend_name, layer.backend_version, layer.spec, replace(payload, desc=desc))
 
     def _payload(self, layer: PreparedLayer) -> _HipPackedPayload:
         if (layer.backend_name, layer.backend_version) != (self.name, self.version):

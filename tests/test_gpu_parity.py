@@ -49,23 +49,26 @@ def _say(*parts) -> None:
     sys.stdout.flush()
 
 
-@pytest.fixture(scope="module", params=["fused", "general"])
+@pytest.fixture(scope="module", params=["split", "fused", "general"])
 def backend(request) -> HipPackedBackend:
-    """``fused``: the tiled single-launch MFMA decode path (tokens <= 16);
+    """``split`` / ``fused``: the tiled MFMA kernels (decode as two kernels or
+    as one kernel with an in-kernel handoff; prefill above 16 tokens);
     ``general``: the canonical-word fp32 path used for every token count."""
 
-    return HipPackedBackend(tiled_decode=request.param == "fused")
+    if request.param == "general":
+        return HipPackedBackend(tiled_decode=False)
+    return HipPackedBackend(decode_launch=request.param)
 
 
-def _fused(backend) -> bool:
+def _tiled(backend) -> bool:
     return backend._tiled_decode
 
 
 def _assert_parity(backend, actual, expected, case=None):
-    """fp32 path: the reference tests' rtol=2e-5/atol=2e-4. Fused fp16-MFMA
+    """fp32 path: the reference tests' rtol=2e-5/atol=2e-4. fp16-MFMA tiled
     path: the north-star bar, relative L2 <= 2e-3 against the fp32 forward."""
 
-    if _fused(backend):
+    if _tiled(backend):
         err = orc.relative_l2(actual, expected)
         assert err <= REL_L2, (case, err)
     else:
@@ -408,12 +411,13 @@ def test_hip_graph_capture_replays_match_eager(backend):
 # --- batched launches ----------------------------------------------------------------
 
 
+@pytest.mark.parametrize("launch", ["split", "fused"])
 @pytest.mark.parametrize("tokens", [1, 4, 16])
-def test_qkv_and_layer_batches_match_oracle(tokens):
+def test_qkv_and_layer_batches_match_oracle(tokens, launch):
     """One launch for Q/K/V (shared x) and one for all seven Qwen3-8B linears of
     a layer (four distinct inputs); every member against the oracle."""
 
-    backend = HipPackedBackend()
+    backend = HipPackedBackend(decode_launch=launch)
     shapes = syn.qwen3_8b_layer()
     states = [syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 40 + i) for i, s in enumerate(shapes)]
     layers = [backend.prepare(st, "cuda") for st in states]
@@ -436,6 +440,30 @@ def test_qkv_and_layer_batches_match_oracle(tokens):
         single = backend.linear(x, layers[i])
         assert torch.equal(single, whole[i])
     assert all(_sync_header_clean(layer) for layer in layers)
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 16])
+def test_split_and_fused_launches_are_bit_identical(tokens):
+    """The two decode launch structures run the same tile arithmetic in the
+    same order, so their outputs agree bit for bit (including salient and bias)."""
+
+    split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
+    for i, shape in enumerate(syn.qwen3_8b_layer()):
+        _say("split vs fused", shape.name, tokens)
+        state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 70 + i, salient=3 * i, bias=i % 2 == 1)
+        x = syn.synthetic_activations(tokens, shape.in_features, seed=i, device="cuda")
+        a = split.linear(x, split.prepare(state, "cuda"))
+        b = fused.linear(x, fused.prepare(state, "cuda"))
+        assert torch.equal(a, b), shape.name
+
+
+def test_batch_rejects_mixed_launch_structures():
+    state = syn.synthetic_packed_layer(syn.qwen3_8b_layer()[1], seed=3)
+    split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
+    a, b = split.prepare(state, "cuda"), fused.prepare(state, "cuda")
+    x = syn.synthetic_activations(1, 4096, seed=1, device="cuda")
+    with pytest.raises(_native.NativeCallError):
+        split.linear_batch([x, x], [a, b])
 
 
 def test_batch_rejects_duplicate_members():
