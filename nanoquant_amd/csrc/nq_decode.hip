@@ -1,6 +1,5 @@
-// Fused single-launch decode path (tokens <= 16) for the packed binary
-// low-rank linear on gfx950, for one linear or a batch of up to 8 linears in
-// one launch.
+// Tiled decode path (tokens <= 16) for the packed binary low-rank linear on
+// gfx950, for one linear or a batch of up to 8 linears per launch.
 //
 //   lm[t, r] = s_mid[r] * Σ_i sgn(V[r, i]) * x[t, i] * s_in[i]     (stage 1)
 //   y[t, o]  = s_out[o] * Σ_r sgn(U[o, r]) * lm[t, r] + salient + bias (stage 2)
@@ -16,32 +15,40 @@
 // is two fp16 ±1 values in one shift + one and_or. A wave reads one word per
 // lane per superchunk: 256 contiguous bytes, fully coalesced.
 //
+// One workgroup computes one 16-row tile (16 ranks in stage 1, 16 output rows
+// in stage 2). Its four waves split the K superchunks into contiguous ranges
+// and work independently until the final cross-wave sum:
+//   - a wave issues the loads of its activation window (x and s_in, or lm)
+//     first and its sign words second, so the activations arrive first;
+//   - it scales the window into fp16 with an exact per-token power of two
+//     taken from the window's own max |value| (no block-wide reduction), parks
+//     it in its private LDS rows and runs the MFMAs on it;
+//   - the window result is divided by that power of two (exact) and added to
+//     an fp32 total; the four wave totals are summed in a fixed order.
+// Epilogue operands (s_mid, s_out, bias) are loaded at kernel start.
+//
 // Launch structure (nq_linear_desc.decode_launch):
-//   split (default): kernel 1 runs the stage-1 tiles (16 ranks each, the four
-//     waves split the columns) of every linear in the batch and stores lm;
-//     kernel 2 runs the stage-2 tiles (16 output rows each). The kernel
+//   split (default): kernel 1 runs the stage-1 tiles of every linear in the
+//     batch and stores lm; kernel 2 runs the stage-2 tiles. The kernel
 //     boundary is the grid-wide barrier.
 //   fused: one kernel whose first workgroups are the stage-1 tiles and the
 //     rest the stage-2 tiles. Stage-1 workgroups store lm write-through at
-//     agent scope and then signal; stage-2 workgroups issue the loads of
-//     their U tile first, then wait for their linear's signal (bounded spin),
-//     so the U stream overlaps stage 1. Workgroups are dispatched in index
-//     order, so every stage-1 workgroup is resident or finished before a
-//     stage-2 workgroup can take its slot, and stage-1 workgroups never wait.
+//     agent scope and then signal; stage-2 workgroups touch their first U
+//     words, then wait for their linear's signal (bounded spin) and only then
+//     load lm. Workgroups are dispatched in index order, so every stage-1
+//     workgroup is resident or finished before a stage-2 workgroup can take
+//     its slot, and stage-1 workgroups never wait.
 // On gfx950 the eight XCDs have separate L2s, so the fused signal and its
 // polls travel through the fabric (agent-scope atomics); measured, that costs
-// more than a graph-launched kernel boundary, hence split is the default.
-//
-// Activations enter the fp16 MFMA scaled by an exact per-token power of two
-// (from the exact max |x * s_in| for one token, else max|x| * max|s_in|, and
-// from the |lm| maximum), so the fp16 range cannot overflow; products are
-// accumulated in fp32.
+// more than a graph-launched kernel boundary, hence split is the default. Both
+// run the same tile arithmetic in the same order: their outputs are identical.
 #include "nq_decode.h"
 
 namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kBlock = 256;
 constexpr int kWaves = 4;
@@ -51,10 +58,11 @@ constexpr int kMaxTokens = 16;
 constexpr int kMaxBatch = 8;
 constexpr uint32_t kTilesMagic = 0x4e515432u;  // "NQT2"
 constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr int kAny = -1;  // dtype template tag: runtime dtype, element loads
 
-// Sync header at the start of each linear's tiles buffer. Every word lives on
-// its own 256-byte line. All counters only ever increase, so nothing is reset
-// between launches (graph replays included):
+// Sync header at the start of each linear's tiles buffer (used by the fused
+// launch only). Every word lives on its own 256-byte line. All counters only
+// ever increase, so nothing is reset between launches (graph replays included):
 //   Counters are 64-bit (first two words of their line); flags are 32-bit and
 //   compared wrap-safely.
 //   ready slots: stage-1 workgroup b adds 1 to slot b % kReadySlots; with
@@ -78,19 +86,20 @@ constexpr int kMiscLine = kReplica0 + kReplicas;
 constexpr int kHeaderLines = kMiscLine + 1;
 constexpr int kHeaderWords = kHeaderLines * kLine;
 // Words on the misc line.
-enum : int { kMiscError = 0, kMiscMagic = 1, kMiscPreMax = 2 };
+enum : int { kMiscError = 0, kMiscMagic = 1 };
 
 __host__ __device__ constexpr int line_word(int line) { return line * kLine; }
 
 // Optional phase tracing (build with -DNQ_DECODE_TRACE): thread 0 of every
 // workgroup stamps the 100 MHz real-time counter at each phase boundary into
-// g_nq_trace[block * 8 + phase]. Compiled out of the shipped library.
+// g_nq_trace[gblock * 8 + phase], gblock = the workgroup's index in the fused
+// grid numbering. Compiled out of the shipped library.
 #ifdef NQ_DECODE_TRACE
 __device__ uint64_t* g_nq_trace;
-#define NQ_TRACE(phase)                                                              \
-    do {                                                                             \
-        if (threadIdx.x == 0 && g_nq_trace)                                          \
-            g_nq_trace[blockIdx.x * 8 + (phase)] = __builtin_amdgcn_s_memrealtime(); \
+#define NQ_TRACE(phase)                                                          \
+    do {                                                                         \
+        if (threadIdx.x == 0 && g_nq_trace)                                      \
+            g_nq_trace[gblock * 8 + (phase)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define NQ_TRACE(phase) \
@@ -136,27 +145,14 @@ __global__ __launch_bounds__(kBlock) void k_build_tiles(const uint32_t* __restri
     }
 }
 
-__global__ void k_init_header(uint32_t* header, const void* s_in, int scale_dtype, int64_t in) {
-    // One block: zero the sync header, record max|s_in| (bounds x * s_in).
-    __shared__ float red[kBlock];
-    float m = 0.0f;
-    for (int64_t i = threadIdx.x; i < in; i += kBlock) m = fmaxf(m, fabsf(nq::load_f32(s_in, scale_dtype, i)));
-    red[threadIdx.x] = m;
-    __syncthreads();
-    for (int s = kBlock / 2; s > 0; s >>= 1) {
-        if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
-    }
+__global__ void k_init_header(uint32_t* header) {
     for (int i = threadIdx.x; i < kHeaderWords; i += kBlock) header[i] = 0;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        header[line_word(kMiscLine) + kMiscMagic] = kTilesMagic;
-        header[line_word(kMiscLine) + kMiscPreMax] = __float_as_uint(red[0]);
-    }
+    if (threadIdx.x == 0) header[line_word(kMiscLine) + kMiscMagic] = kTilesMagic;
 }
 
 // ---------------------------------------------------------------------------
-// Fused kernel.
+// Decode kernels.
 // ---------------------------------------------------------------------------
 
 struct FusedArgs {
@@ -182,9 +178,7 @@ struct FusedArgs {
     int bias_dtype;
     void* y;
     int y_dtype;
-    float* lm;      // [16][n1*16]
-    float* wgmax;   // [n1][16]
-    int x_vec;      // x rows and s_in are 16-byte aligned with in % 8 == 0
+    float* lm;      // [16][n1 * 16], ranks >= rank hold zero
 };
 
 struct FusedBatch {
@@ -197,18 +191,13 @@ struct FusedBatch {
 // 2^e for an integer e in the fp32 normal range.
 __device__ __forceinline__ float exp2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
 
-// Exponent e with 2^e <= v < 2^(e+1) for finite v > 0 (normals only; tiny values clamp).
-__device__ __forceinline__ int exponent_of(float v) {
-    const int e = static_cast<int>((__float_as_uint(v) >> 23) & 0xff) - 127;
-    return e < -126 ? -126 : e;
-}
-
-// Exact power of two mapping values bounded by `bound` below 2^14 (fp16-safe).
-__device__ __forceinline__ float range_scale(float bound) {
-    if (!(bound > 0.0f)) return 1.0f;
-    int e = 13 - exponent_of(bound);
-    e = e > 100 ? 100 : (e < -100 ? -100 : e);
-    return exp2i(e);
+// Exponent e of a power of two mapping values bounded by `bound` below 2^14
+// (fp16-safe); 0 when the bound is zero or not finite-positive.
+__device__ __forceinline__ int range_exponent(float bound) {
+    if (!(bound > 0.0f)) return 0;
+    int e = static_cast<int>((__float_as_uint(bound) >> 23) & 0xff) - 127;
+    e = 13 - (e < -126 ? -126 : e);
+    return e > 100 ? 100 : (e < -100 ? -100 : e);
 }
 
 __device__ __forceinline__ void store_agent(float* p, float v) {
@@ -230,21 +219,6 @@ __device__ __forceinline__ uint64_t slot_count(int slot, int slots, int64_t coun
     return static_cast<uint64_t>(count / slots + (slot < count % slots ? 1 : 0));
 }
 
-// LDS of one workgroup for MT token rows and a column window of 4 * SC
-// superchunks (SC per wave).
-template <int MT, int SC>
-struct alignas(16) Lds {
-    static constexpr int kMT = MT;
-    // Activation staging: MT rows of fp16, row stride padded by 8 halfs so the
-    // 16 token rows of a ds_read_b128 land in different banks.
-    static constexpr int kStageCols = 4 * SC * kSuperCols;
-    static constexpr int kStride = kStageCols + 8;
-    _Float16 act[MT * kStride];
-    float red[kWaves][kMaxTokens][kTileRows];
-    float tokscale[kMaxTokens];
-    float wmax[kWaves];
-};
-
 __device__ __forceinline__ v8h expand_signs(uint32_t word, int m) {
     union {
         uint32_t u[4];
@@ -258,291 +232,403 @@ __device__ __forceinline__ v8h expand_signs(uint32_t word, int m) {
     return r.v;
 }
 
-// Eight consecutive elements [i, i + 8) of a typed buffer as fp32. The caller
-// guarantees 16-byte alignment of element i (rows of length % 8 == 0 on
-// 256-byte aligned allocations).
-__device__ __forceinline__ void load8(const void* __restrict__ p, int dtype, int64_t i, float (&v)[8]) {
-    if (dtype == NQ_DTYPE_F32) {
-        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
-        const float4 lo = q[0], hi = q[1];
-        v[0] = lo.x; v[1] = lo.y; v[2] = lo.z; v[3] = lo.w;
-        v[4] = hi.x; v[5] = hi.y; v[6] = hi.z; v[7] = hi.w;
-    } else {
-        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-        if (dtype == NQ_DTYPE_BF16) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                v[2 * k] = __uint_as_float(w[k] << 16);
-                v[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                union { uint32_t u; _Float16 h[2]; } c;
-                c.u = w[k];
-                v[2 * k] = static_cast<float>(c.h[0]);
-                v[2 * k + 1] = static_cast<float>(c.h[1]);
-            }
-        }
-    }
-}
+// --- activation vectors: 8 consecutive elements -------------------------------
 
-// Elements [i, i + 8) of a row of length `limit`, zero past the end.
-__device__ __forceinline__ void load8_tail(const void* __restrict__ p, int dtype, int64_t row_base,
-                                           int64_t i, int64_t limit, float (&v)[8]) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = i + k < limit ? nq::load_f32(p, dtype, row_base + i + k) : 0.0f;
-}
-
-__device__ __forceinline__ uint4 pack8_f16(const float (&v)[8]) {
-    union { _Float16 h[8]; uint4 u; } r;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) r.h[k] = static_cast<_Float16>(v[k]);
-    return r.u;
-}
-
-// Stage columns [c0, c0 + ncols) of the activation rows into LDS as
-// fp16(a * s * tokscale[t]); `s` (a per-column scale) may be null.
-// act[t][c - c0]; rows t >= tokens are zero.
-template <typename L>
-__device__ __forceinline__ void stage_rows(L& lds, const void* __restrict__ act, int act_dtype,
-                                           int64_t row_len, const void* __restrict__ colscale,
-                                           int colscale_dtype, int tokens, int64_t c0, int ncols,
-                                           bool vec) {
-    const int nv = ncols >> 3;
-    for (int t = 0; t < L::kMT; ++t) {
-        uint4* dst = reinterpret_cast<uint4*>(&lds.act[t * L::kStride]);
-        if (t >= tokens) {
-            for (int j = threadIdx.x; j < nv; j += kBlock) dst[j] = make_uint4(0, 0, 0, 0);
-            continue;
-        }
-        const float scale = lds.tokscale[t];
-#pragma unroll 4
-        for (int j = threadIdx.x; j < nv; j += kBlock) {
-            const int64_t col = c0 + 8 * j;
-            float v[8], w[8];
-            if (vec && col + 8 <= row_len) {
-                load8(act, act_dtype, t * row_len + col, v);
-                if (colscale) load8(colscale, colscale_dtype, col, w);
-            } else {
-                load8_tail(act, act_dtype, t * row_len, col, row_len, v);
-                if (colscale) load8_tail(colscale, colscale_dtype, 0, col, row_len, w);
-            }
-#pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] *= (colscale ? w[k] : 1.0f) * scale;
-            dst[j] = pack8_f16(v);
-        }
-    }
-}
-
-// max |a[t, :]| for each token t < tokens, accumulated into lds.tokscale[t]
-// (non-negative floats compare like their bit patterns).
-template <typename L>
-__device__ __forceinline__ void row_absmax(L& lds, const void* __restrict__ act, int act_dtype,
-                                           int64_t row_len, int64_t row_stride, int tokens, bool vec) {
-    const int64_t nv = (row_len + 7) >> 3;
-    for (int t = 0; t < L::kMT && t < tokens; ++t) {
-        float m = 0.0f;
-#pragma unroll 4
-        for (int64_t j = threadIdx.x; j < nv; j += kBlock) {
-            float v[8];
-            if (vec) load8(act, act_dtype, t * row_stride + 8 * j, v);
-            else load8_tail(act, act_dtype, t * row_stride, 8 * j, row_len, v);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(v[k]));
-        }
-        for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        if ((threadIdx.x & 63) == 0 && m > 0.0f) {
-            atomicMax(reinterpret_cast<unsigned int*>(&lds.tokscale[t]), __float_as_uint(m));
-        }
-    }
-}
-
-// One-token staging in a single memory round trip, split in two so the caller
-// can issue other loads (the weight words) after the activation loads:
-//   row_single_load:   every thread loads its NV vectors of a[col] * s[col];
-//   row_single_stage:  the block reduces max |value| into a range scale
-//                      (lds.tokscale[0]) and writes the scaled fp16 values to
-//                      LDS row 0. Columns [n, ncols_pad) are zero.
-// Requires ncols_pad <= 2048 * NV.
-template <int NV>
-struct RowRegs {
-    float v[NV][8];
+// Raw bits of 8 elements of dtype D (kAny: already fp32, loaded element-wise).
+template <int D>
+struct Raw8 {
+    v4u u[D == NQ_DTYPE_F32 ? 2 : 1];
+};
+template <>
+struct Raw8<kAny> {
+    float f[8];
 };
 
-template <typename L>
-__device__ __forceinline__ RowRegs<L::kStageCols / (8 * kBlock)> row_single_load(
-    const void* __restrict__ act, int act_dtype, const void* __restrict__ colscale, int colscale_dtype,
-    int64_t n, int ncols_pad, bool vec) {
-    constexpr int NV = L::kStageCols / (8 * kBlock);
-    RowRegs<NV> r;
+// Elements [i, i + 8) of a row whose valid part ends at `limit`. Typed D: the
+// caller guarantees i + 8 <= limit and 16-byte alignment (rows of length % 8 ==
+// 0 on 16-byte aligned buffers). kAny: bounds-checked element loads.
+template <int D>
+__device__ __forceinline__ void raw_load(Raw8<D>& r, const void* __restrict__ p, int64_t row_base, int64_t i,
+                                         int64_t limit, int rt_dtype) {
+    if constexpr (D == kAny) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int64_t col = 8 * (static_cast<int64_t>(threadIdx.x) + i * kBlock);
-        float w[8];
-        if (col < ncols_pad) {
-            if (vec && col + 8 <= n) {
-                load8(act, act_dtype, col, r.v[i]);
-                if (colscale) load8(colscale, colscale_dtype, col, w);
-            } else {
-                load8_tail(act, act_dtype, 0, col, n, r.v[i]);
-                if (colscale) load8_tail(colscale, colscale_dtype, 0, col, n, w);
-            }
-            if (colscale) {
+        for (int k = 0; k < 8; ++k) r.f[k] = i + k < limit ? nq::load_f32(p, rt_dtype, row_base + i + k) : 0.0f;
+    } else if constexpr (D == NQ_DTYPE_F32) {
+        const v4u* q = reinterpret_cast<const v4u*>(static_cast<const float*>(p) + row_base + i);
+        r.u[0] = q[0];
+        r.u[1] = q[1];
+    } else {
+        r.u[0] = *reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(p) + row_base + i);
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void raw_zero(Raw8<D>& r) {
+    if constexpr (D == kAny) {
 #pragma unroll
-                for (int k = 0; k < 8; ++k) r.v[i][k] *= w[k];
-            }
+        for (int k = 0; k < 8; ++k) r.f[k] = 0.0f;
+    } else {
+#pragma unroll
+        for (int k = 0; k < (D == NQ_DTYPE_F32 ? 2 : 1); ++k) r.u[k] = v4u{0u, 0u, 0u, 0u};
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void raw_unpack(const Raw8<D>& r, float (&v)[8]) {
+    if constexpr (D == kAny) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = r.f[k];
+    } else if constexpr (D == NQ_DTYPE_F32) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = __uint_as_float(r.u[k >> 2][k & 3]);
+    } else if constexpr (D == NQ_DTYPE_BF16) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            v[2 * k] = __uint_as_float(r.u[0][k] << 16);
+            v[2 * k + 1] = __uint_as_float(r.u[0][k] & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            union {
+                uint32_t u;
+                _Float16 h[2];
+            } c;
+            c.u = r.u[0][k];
+            v[2 * k] = static_cast<float>(c.h[0]);
+            v[2 * k + 1] = static_cast<float>(c.h[1]);
+        }
+    }
+}
+
+// One element of a typed buffer as fp32 (kAny: runtime dtype switch).
+template <int D>
+__device__ __forceinline__ float load_one(const void* __restrict__ p, int64_t i, int rt_dtype) {
+    if constexpr (D == kAny) {
+        return nq::load_f32(p, rt_dtype, i);
+    } else if constexpr (D == NQ_DTYPE_F32) {
+        return static_cast<const float*>(p)[i];
+    } else if constexpr (D == NQ_DTYPE_BF16) {
+        return __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(p)[i]) << 16);
+    } else {
+        return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+    }
+}
+
+// --- one wave's window ----------------------------------------------------------
+
+// A window is KW superchunks (128 * KW columns) of MT token rows. Vector e =
+// lane + 64 * j (j < NV) covers token t = e / CV and columns 8 * (e % CV) of
+// the window. When 64 % CV == 0 the column (and so its column scale) is the
+// same for every j of a lane.
+template <int MT, int KW>
+struct Win {
+    static constexpr int CW = KW * kSuperCols;      // columns per window
+    static constexpr int CV = CW / 8;               // 8-column vectors per token row
+    static constexpr int NV = MT * CV / 64;         // vectors per lane
+    static constexpr bool kSameCol = (CV <= 64) && (64 % CV == 0);
+    static constexpr int NS = kSameCol ? 1 : NV;    // column-scale vectors per lane
+    static constexpr int kStride = CW + 8;          // LDS row stride (halfs)
+    static_assert((MT * CV) % 64 == 0, "window must split evenly over a wave");
+};
+
+template <int MT, int KW, int XD, int SD>
+struct WinRegs {
+    Raw8<XD> x[Win<MT, KW>::NV];
+    Raw8<SD> s[Win<MT, KW>::NS];
+    bool live[Win<MT, KW>::NV];
+    uint32_t w[KW];
+};
+
+// Where the activations of a window come from.
+struct ActRef {
+    const void* p;        // [tokens][ld]
+    int dtype;            // runtime dtype (kAny loads)
+    int64_t ld;           // row stride (elements)
+    int64_t limit;        // valid columns (typed dtypes: a multiple of 8, >= 8)
+    const void* colscale; // [limit] or null
+    int colscale_dtype;
+    int tokens;
+};
+
+// Issue the activation loads of a window. Typed dtypes load unconditionally
+// from clamped addresses (no branches, so the compiler can count outstanding
+// loads exactly) and record which vectors are live; dead vectors are zeroed
+// when unpacked. Columns past the wave's range are dead, so their MFMAs add 0.
+template <int MT, int KW, int XD, int SD>
+__device__ __forceinline__ void load_acts(WinRegs<MT, KW, XD, SD>& r, const ActRef& a, int64_t sc0, int64_t sc_end,
+                                          int lane) {
+    using W = Win<MT, KW>;
+#pragma unroll
+    for (int j = 0; j < W::NV; ++j) {
+        const int e = lane + 64 * j;
+        const int t = e / W::CV;
+        const int64_t col = sc0 * kSuperCols + 8 * (e % W::CV);
+        r.live[j] = t < a.tokens && col < a.limit && sc0 + (8 * (e % W::CV)) / kSuperCols < sc_end;
+        if constexpr (XD == kAny) {
+            if (r.live[j]) raw_load<XD>(r.x[j], a.p, t * a.ld, col, a.limit, a.dtype);
+            else raw_zero<XD>(r.x[j]);
         } else {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) r.v[i][k] = 0.0f;
+            const int64_t tc = t < a.tokens ? t : a.tokens - 1;
+            const int64_t cc = col < a.limit - 8 ? col : a.limit - 8;
+            raw_load<XD>(r.x[j], a.p, tc * a.ld, cc, a.limit, a.dtype);
         }
     }
-    return r;
-}
-
-template <typename L, int NV>
-__device__ __forceinline__ void row_single_stage(L& lds, RowRegs<NV>& r, int ncols_pad) {
-    float m = 0.0f;
+    if (a.colscale) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(r.v[i][k]));
-    }
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if ((threadIdx.x & 63) == 0) lds.wmax[threadIdx.x >> 6] = m;
-    __syncthreads();
-    const float scale = range_scale(fmaxf(fmaxf(lds.wmax[0], lds.wmax[1]), fmaxf(lds.wmax[2], lds.wmax[3])));
-    if (threadIdx.x == 0) lds.tokscale[0] = scale;
-    uint4* dst = reinterpret_cast<uint4*>(&lds.act[0]);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int j = threadIdx.x + i * kBlock;
-        if (8 * j < ncols_pad) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) r.v[i][k] *= scale;
-            dst[j] = pack8_f16(r.v[i]);
-        }
-    }
-}
-
-// One wave's share of a 16-row tile: superchunks sc = w, w + 4, ... of the
-// current stage window. Returns the partial D (token rows x 16 tile rows).
-template <int MT, int SCMAX>
-__device__ __forceinline__ v4f tile_mfma(const Lds<MT, SCMAX>& lds, const uint32_t (&words)[SCMAX],
-                                         int64_t sc_first, int64_t nsc, int64_t window_sc0, v4f acc) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int t = lane & 15;
-    const int g = lane >> 4;
-#pragma unroll
-    for (int i = 0; i < SCMAX; ++i) {
-        const int64_t sc = sc_first + 4 * i + wave;
-        if (sc < nsc) {
-            const int base = static_cast<int>(sc - window_sc0) * kSuperCols + 8 * g;
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                v8h a = {};
-                if (t < MT) a = *reinterpret_cast<const v8h*>(&lds.act[t * Lds<MT, SCMAX>::kStride + base + 32 * m]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, expand_signs(words[i], m), acc, 0, 0, 0);
+        for (int j = 0; j < W::NS; ++j) {
+            const int e = lane + 64 * j;
+            const int64_t col = sc0 * kSuperCols + 8 * (e % W::CV);
+            if constexpr (SD == kAny) {
+                if (col < a.limit) raw_load<SD>(r.s[j], a.colscale, 0, col, a.limit, a.colscale_dtype);
+                else raw_zero<SD>(r.s[j]);
+            } else {
+                const int64_t cc = col < a.limit - 8 ? col : a.limit - 8;
+                raw_load<SD>(r.s[j], a.colscale, 0, cc, a.limit, a.colscale_dtype);
             }
         }
     }
-    return acc;
 }
 
-template <int SCMAX>
-__device__ __forceinline__ void load_words(uint32_t (&words)[SCMAX], const uint32_t* __restrict__ tile,
-                                           int64_t sc_first, int64_t nsc) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+// Sign words of a window; superchunks past the tile's last load a valid word
+// (their activations are zero).
+template <int MT, int KW, int XD, int SD>
+__device__ __forceinline__ void load_words(WinRegs<MT, KW, XD, SD>& r, const uint32_t* __restrict__ tile,
+                                           int64_t sc0, int64_t nsc, int lane) {
 #pragma unroll
-    for (int i = 0; i < SCMAX; ++i) {
-        const int64_t sc = sc_first + 4 * i + wave;
-        words[i] = sc < nsc ? __builtin_nontemporal_load(tile + sc * 64 + lane) : 0u;
+    for (int i = 0; i < KW; ++i) {
+        const int64_t sc = sc0 + i < nsc ? sc0 + i : nsc - 1;
+        r.w[i] = __builtin_nontemporal_load(tile + sc * 64 + lane);
     }
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float x) {
+    const int y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false);
+    return fmaxf(x, __int_as_float(y));
+}
+
+// Max over the 16 lanes of each row of the wave (every lane gets its row's max).
+__device__ __forceinline__ float row16_max(float v) {
+    v = dpp_max<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_max<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_max<0x141>(v);  // row_half_mirror
+    v = dpp_max<0x140>(v);  // row_mirror
+    return v;
+}
+
+// Scale the window into fp16 (per-token exact power of two from the window's
+// max |value|), write it to this wave's LDS rows act[t][c], and return the
+// per-token exponents (uniform; tokens >= MT unused).
+template <int MT, int KW, int XD, int SD>
+__device__ __forceinline__ void stage_window(const WinRegs<MT, KW, XD, SD>& r, bool has_colscale,
+                                             _Float16* __restrict__ act, int lane, int (&expo)[MT]) {
+    using W = Win<MT, KW>;
+    // Two passes over the raw registers (max, then scale + pack) keep only one
+    // vector unpacked at a time.
+    auto values = [&](int j, float (&v)[8]) {
+        raw_unpack<XD>(r.x[j], v);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = r.live[j] ? v[k] : 0.0f;
+        if (has_colscale) {
+            float s[8];
+            raw_unpack<SD>(r.s[W::kSameCol ? 0 : j], s);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] *= s[k];
+        }
+    };
+    float m[W::NV];
+#pragma unroll
+    for (int j = 0; j < W::NV; ++j) {
+        float v[8];
+        values(j, v);
+        m[j] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) m[j] = fmaxf(m[j], fabsf(v[k]));
+    }
+    // Per-token maxima: reduce each j over 16-lane rows, then combine rows.
+    float tmax[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) tmax[t] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < W::NV; ++j) {
+        const float rm = row16_max(m[j]);
+#pragma unroll
+        for (int row = 0; row < 4; ++row) {
+            const int t = (16 * row + 64 * j) / W::CV;
+            const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 16 * row));
+            tmax[t] = fmaxf(tmax[t], rv);
+        }
+    }
+    float scale[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        expo[t] = range_exponent(tmax[t]);
+        scale[t] = exp2i(expo[t]);
+    }
+#pragma unroll
+    for (int j = 0; j < W::NV; ++j) {
+        const int e = lane + 64 * j;
+        // Token of this vector; uniform per j unless a token row spans less than a wave.
+        float sc;
+        if constexpr (W::CV >= 64) {
+            sc = scale[(64 * j) / W::CV];
+        } else {
+            sc = scale[0];
+#pragma unroll
+            for (int t = 1; t < MT; ++t) sc = (e / W::CV == t) ? scale[t] : sc;
+        }
+        float v[8];
+        values(j, v);
+        union {
+            _Float16 h[8];
+            v4u u;
+        } pk;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) pk.h[k] = static_cast<_Float16>(v[k] * sc);
+        *reinterpret_cast<v4u*>(act + (e / W::CV) * W::kStride + 8 * (e % W::CV)) = pk.u;
+    }
+}
+
+// MFMAs of one window (KW superchunks). Every lane reads an A row: lanes of
+// token rows >= MT read row t % MT, which only feeds D rows that are never
+// used. One accumulator per 32-column chunk keeps the MFMA chains short; they
+// are summed in a fixed order.
+template <int MT, int KW, int XD, int SD>
+__device__ __forceinline__ v4f window_mfma(const WinRegs<MT, KW, XD, SD>& r, const _Float16* __restrict__ act,
+                                           int lane) {
+    using W = Win<MT, KW>;
+    const int g = lane >> 4;
+    const _Float16* row = act + ((lane & 15) % MT) * W::kStride + 8 * g;
+    v4f acc[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < KW; ++i) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const v8h a = *reinterpret_cast<const v8h*>(row + i * kSuperCols + 32 * m);
+            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, expand_signs(r.w[i], m), acc[m], 0, 0, 0);
+        }
+    }
+    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+}
+
+// Order this wave's LDS writes before its own reads (waves never share rows).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
+
+// D row of MFMA register q in this lane is token 4 * (lane / 16) + q.
+template <int MT>
+__device__ __forceinline__ void add_scaled(v4f& tot, const v4f& acc, const int (&expo)[MT], int lane) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        int e;
+        if constexpr (MT <= 4) {
+            e = expo[q < MT ? q : 0];
+        } else {
+            const int grp = lane >> 4;
+            e = expo[q];
+#pragma unroll
+            for (int gg = 1; gg < 4; ++gg) e = (grp == gg && 4 * gg + q < MT) ? expo[4 * gg + q] : e;
+        }
+        tot[q] += acc[q] * exp2i(-e);
+    }
+}
+
+// Shared memory of one workgroup.
+template <int MT, int KW>
+struct alignas(16) TileLds {
+    _Float16 act[kWaves][MT * Win<MT, KW>::kStride];
+    float red[kWaves][kMaxTokens][kTileRows];
+};
+
+// One wave's share of a 16-row tile: superchunks [s_begin, s_end) in windows
+// of KW. Returns the wave's fp32 partial D (tokens x 16 rows).
+template <int MT, int KW, int XD, int SD, bool WORDS_FIRST>
+__device__ __forceinline__ v4f wave_tile(const ActRef& act_ref, const uint32_t* __restrict__ tile, int64_t nsc,
+                                         int64_t s_begin, int64_t s_end, _Float16* __restrict__ act, int lane) {
+    v4f tot = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t sc0 = s_begin; sc0 < s_end; sc0 += KW) {
+        WinRegs<MT, KW, XD, SD> r;
+        if (WORDS_FIRST) {
+            load_words(r, tile, sc0, nsc, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            load_acts(r, act_ref, sc0, s_end, lane);
+        } else {
+            load_acts(r, act_ref, sc0, s_end, lane);
+            __builtin_amdgcn_sched_barrier(0);
+            load_words(r, tile, sc0, nsc, lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load is issued before any use
+        int expo[MT];
+        stage_window(r, act_ref.colscale != nullptr, act, lane, expo);
+        wave_lds_sync();
+        const v4f acc = window_mfma(r, act, lane);
+        add_scaled<MT>(tot, acc, expo, lane);
+        wave_lds_sync();  // the next window rewrites the rows this one read
+    }
+    return tot;
+}
+
+// Contiguous superchunk range of wave `w` out of nsc.
+__device__ __forceinline__ void wave_range(int64_t nsc, int w, int64_t& b, int64_t& e) {
+    const int64_t q = (nsc + kWaves - 1) / kWaves;
+    b = q * w < nsc ? q * w : nsc;
+    e = b + q < nsc ? b + q : nsc;
 }
 
 // Sum the four waves' partial tiles (fixed order: deterministic). Returns the
 // value for (t = tid / 16, n = tid % 16).
-template <typename L>
-__device__ __forceinline__ float reduce_waves(L& lds, v4f acc) {
+template <int MT, int KW>
+__device__ __forceinline__ float reduce_waves(TileLds<MT, KW>& lds, v4f tot) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lds.red[wave][4 * (lane >> 4) + i][lane & 15] = acc[i];
+    for (int i = 0; i < 4; ++i) lds.red[wave][4 * (lane >> 4) + i][lane & 15] = tot[i];
     __syncthreads();
     const int t = threadIdx.x >> 4;
     const int n = threadIdx.x & 15;
     return ((lds.red[0][t][n] + lds.red[1][t][n]) + lds.red[2][t][n]) + lds.red[3][t][n];
 }
 
-template <int MT, int SCMAX, bool FUSED>
-__device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT, SCMAX>& lds, int64_t rt) {
+template <int MT, int KW, int XD, int SD, bool FUSED>
+__device__ __forceinline__ void stage1_tile(const FusedArgs& a, TileLds<MT, KW>& lds, int64_t rt,
+                                            [[maybe_unused]] int64_t gblock) {
     NQ_TRACE(0);
-    const uint32_t* tile = a.v_tiles + rt * a.nsc1 * 64;
-    constexpr int kWindowSc = 4 * SCMAX;
-    uint32_t words[SCMAX];
-
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (MT == 1 && a.nsc1 <= kWindowSc) {
-        // One token, one window: x * s_in loaded once (issued before the weight
-        // words, so the in-order load counter lets staging start early), exact
-        // range scale.
-        const int ncols = static_cast<int>(a.nsc1 * kSuperCols);
-        auto xr = row_single_load<Lds<MT, SCMAX>>(a.x, a.x_dtype, a.s_in, a.scale_dtype, a.in, ncols,
-                                                  a.x_vec != 0);
-        load_words<SCMAX>(words, tile, 0, a.nsc1);
-        row_single_stage(lds, xr, ncols);
-        __syncthreads();
-        NQ_TRACE(1);
-        acc = tile_mfma<MT, SCMAX>(lds, words, 0, a.nsc1, 0, acc);
-    } else {
-        load_words<SCMAX>(words, tile, 0, a.nsc1);
-        // Per-token range scale: bound |x * s_in| by max|x| * max|s_in|.
-        if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
-        __syncthreads();
-        row_absmax(lds, a.x, a.x_dtype, a.in, a.in, a.tokens, a.x_vec != 0);
-        __syncthreads();
-        const float premax = __uint_as_float(a.header[line_word(kMiscLine) + kMiscPreMax]);
-        if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = range_scale(lds.tokscale[threadIdx.x] * premax);
-        __syncthreads();
-        NQ_TRACE(1);
-        for (int64_t w0 = 0; w0 < a.nsc1; w0 += kWindowSc) {
-            if (w0 > 0) load_words<SCMAX>(words, tile, w0, a.nsc1);
-            const int64_t c0 = w0 * kSuperCols;
-            const int64_t cend = (w0 + kWindowSc < a.nsc1 ? w0 + kWindowSc : a.nsc1) * kSuperCols;
-            stage_rows(lds, a.x, a.x_dtype, a.in, a.s_in, a.scale_dtype, a.tokens, c0,
-                       static_cast<int>(cend - c0), a.x_vec != 0);
-            __syncthreads();
-            acc = tile_mfma<MT, SCMAX>(lds, words, w0, a.nsc1, w0, acc);
-            __syncthreads();
-        }
-    }
-
-    NQ_TRACE(2);
-    const float sum = reduce_waves(lds, acc);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int t = threadIdx.x >> 4;
     const int n = threadIdx.x & 15;
     const int64_t r = rt * kTileRows + n;
-    // Pad ranks [rank, 16 * n1) are written as zero: stage 2 stages whole rows and
-    // its pad sign bits decode to +1.
-    float lmv = 0.0f;
-    if (t < a.tokens && r < a.rank) lmv = sum / lds.tokscale[t] * nq::load_f32(a.s_mid, a.scale_dtype, r);
-    float am = fabsf(lmv);
-    for (int off = 8; off >= 1; off >>= 1) am = fmaxf(am, __shfl_xor(am, off, 16));
+    // Epilogue operand first (typed, unconditional): its latency hides under
+    // the main loads.
+    const float smid = load_one<SD>(a.s_mid, r < a.rank ? r : a.rank - 1, a.scale_dtype);
+
+    int64_t sb, se;
+    wave_range(a.nsc1, wave, sb, se);
+    const ActRef xr{a.x, a.x_dtype, a.in, a.in, a.s_in, a.scale_dtype, a.tokens};
+    const v4f tot =
+        wave_tile<MT, KW, XD, SD, false>(xr, a.v_tiles + rt * a.nsc1 * 64, a.nsc1, sb, se, lds.act[wave], lane);
+    NQ_TRACE(1);
+    const float sum = reduce_waves(lds, tot);
+    NQ_TRACE(2);
+    // Pad ranks [rank, 16 * n1) are written as zero: stage 2 reads whole rows
+    // and their sign bits decode to +1.
+    const float lmv = (t < a.tokens && r < a.rank) ? sum * smid : 0.0f;
+    float* dst = &a.lm[t * (a.n1 * kTileRows) + r];
     if (!FUSED) {
         // Split launch: the kernel boundary publishes lm to the stage-2 kernel.
-        if (t < a.tokens) a.lm[t * (a.n1 * kTileRows) + r] = lmv;
-        if (n == 0) a.wgmax[rt * kMaxTokens + t] = am;
+        if (t < a.tokens) *dst = lmv;
         NQ_TRACE(3);
-        NQ_TRACE(4);
         return;
     }
-    // lm and the maxima are stored write-through at agent scope (no L2
-    // writeback needed); the wait makes them complete before the signal.
-    if (t < a.tokens) store_agent(&a.lm[t * (a.n1 * kTileRows) + r], lmv);
-    if (n == 0) store_agent(&a.wgmax[rt * kMaxTokens + t], am);
+    // lm is stored write-through at agent scope (no L2 writeback needed); the
+    // wait makes it complete before the signal.
+    if (t < a.tokens) store_agent(dst, lmv);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     NQ_TRACE(3);
@@ -560,22 +646,11 @@ __device__ __forceinline__ void stage1_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
             }
         }
     }
-    NQ_TRACE(4);
 }
 
-template <int MT, int SCMAX, bool FUSED>
-__device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT, SCMAX>& lds, int64_t rt) {
-    NQ_TRACE(0);
-    const uint32_t* tile = a.u_tiles + rt * a.nsc2 * 64;
-    constexpr int kWindowSc = 4 * SCMAX;
-    uint32_t words[SCMAX];
-    load_words<SCMAX>(words, tile, 0, a.nsc2);  // prefetch before waiting
-
-    // Fused launch: launch index from this workgroup's arrival, then poll its
-    // ready flag with relaxed agent-scope loads; one acquire fence (L2
-    // invalidate) at the end. Split launch: stage 1 finished in the previous
-    // kernel.
-    if (FUSED && threadIdx.x == 0) {
+// Fused launch: wait until every stage-1 workgroup of this launch has signalled.
+__device__ __forceinline__ void wait_ready(const FusedArgs& a, int64_t rt) {
+    if (threadIdx.x == 0) {
         const int slot = static_cast<int>(rt % kArriveSlots);
         const uint64_t c = slot_count(slot, kArriveSlots, a.n2);
         const uint32_t target = static_cast<uint32_t>(hdr_add(a.header, line_word(kArriveSlot0 + slot)) / c + 1);
@@ -590,54 +665,44 @@ __device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
-    if (FUSED) __syncthreads();
-    NQ_TRACE(1);
+    __syncthreads();
+}
 
-    const int64_t lm_ld = a.n1 * kTileRows;
-    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (MT == 1 && a.nsc2 <= kWindowSc) {
-        // One token, one window: lm loaded once, range scale from its own max.
-        const int ncols = static_cast<int>(a.nsc2 * kSuperCols);
-        auto lr = row_single_load<Lds<MT, SCMAX>>(a.lm, NQ_DTYPE_F32, nullptr, 0, lm_ld, ncols, true);
-        row_single_stage(lds, lr, ncols);
-        __syncthreads();
-        acc = tile_mfma<MT, SCMAX>(lds, words, 0, a.nsc2, 0, acc);
-    } else {
-        // Per-token |lm| maximum over all stage-1 workgroups -> range scale.
-        if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = 0.0f;
-        __syncthreads();
-        {
-            const int t = threadIdx.x % MT;
-            const int part = threadIdx.x / MT;
-            float m = 0.0f;
-            if (t < a.tokens) {
-                for (int64_t b = part; b < a.n1; b += kBlock / MT) m = fmaxf(m, a.wgmax[b * kMaxTokens + t]);
-            }
-            if (m > 0.0f) atomicMax(reinterpret_cast<unsigned int*>(&lds.tokscale[t]), __float_as_uint(m));
-        }
-        __syncthreads();
-        if (threadIdx.x < kMaxTokens) lds.tokscale[threadIdx.x] = range_scale(lds.tokscale[threadIdx.x]);
-        __syncthreads();
-        for (int64_t w0 = 0; w0 < a.nsc2; w0 += kWindowSc) {
-            if (w0 > 0) load_words<SCMAX>(words, tile, w0, a.nsc2);
-            const int64_t c0 = w0 * kSuperCols;
-            const int64_t cend = (w0 + kWindowSc < a.nsc2 ? w0 + kWindowSc : a.nsc2) * kSuperCols;
-            // lm rows have stride lm_ld (a multiple of 16, zeros past `rank`).
-            stage_rows(lds, a.lm, NQ_DTYPE_F32, lm_ld, nullptr, 0, a.tokens, c0, static_cast<int>(cend - c0),
-                       true);
-            __syncthreads();
-            acc = tile_mfma<MT, SCMAX>(lds, words, w0, a.nsc2, w0, acc);
-            __syncthreads();
-        }
-    }
-
-    NQ_TRACE(2);
-    const float sum = reduce_waves(lds, acc);
+template <int MT, int KW, int SD, bool FUSED>
+__device__ __forceinline__ void stage2_tile(const FusedArgs& a, TileLds<MT, KW>& lds, int64_t rt,
+                                            [[maybe_unused]] int64_t gblock) {
+    NQ_TRACE(0);
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int t = threadIdx.x >> 4;
     const int n = threadIdx.x & 15;
     const int64_t o = rt * kTileRows + n;
-    if (t < a.tokens && o < a.out) {
-        float v = sum / lds.tokscale[t] * nq::load_f32(a.s_out, a.scale_dtype, o);
+    const bool store = t < a.tokens && o < a.out;
+    const float sout = load_one<SD>(a.s_out, o < a.out ? o : a.out - 1, a.scale_dtype);
+
+    int64_t sb, se;
+    wave_range(a.nsc2, wave, sb, se);
+    const int64_t lm_ld = a.n1 * kTileRows;
+    // lm rows have stride lm_ld (a multiple of 16, zeros past `rank`), so whole
+    // 8-element vectors up to lm_ld are valid.
+    const ActRef lr{a.lm, NQ_DTYPE_F32, lm_ld, lm_ld, nullptr, 0, a.tokens};
+    const uint32_t* tile = a.u_tiles + rt * a.nsc2 * 64;
+    v4f tot;
+    if (FUSED) {
+        // Touch the first window's words before waiting, so the U stream
+        // overlaps stage 1; the loop below then hits in cache.
+        if (sb < se) (void)__builtin_nontemporal_load(tile + sb * 64 + lane);
+        wait_ready(a, rt);
+        NQ_TRACE(1);
+        tot = wave_tile<MT, KW, NQ_DTYPE_F32, NQ_DTYPE_F32, true>(lr, tile, a.nsc2, sb, se, lds.act[wave], lane);
+    } else {
+        NQ_TRACE(1);
+        tot = wave_tile<MT, KW, NQ_DTYPE_F32, NQ_DTYPE_F32, false>(lr, tile, a.nsc2, sb, se, lds.act[wave], lane);
+    }
+    NQ_TRACE(2);
+    const float sum = reduce_waves(lds, tot);
+    if (store) {
+        float v = sum * sout;
         for (int64_t k = 0; k < a.salient_count; ++k) {
             float wv = nq::load_f32(a.salient_values, a.salient_dtype, o * a.salient_count + k);
             if (a.salient_scales) wv *= nq::load_f32(a.salient_scales, a.scale_dtype, k);
@@ -649,40 +714,48 @@ __device__ __forceinline__ void stage2_tile(const FusedArgs& a, Lds<MT, SCMAX>& 
     NQ_TRACE(3);
 }
 
-template <int MT, int SCMAX>
+// Linear of block b: the number of prefix entries first[1..count-1] <= b
+// (independent scalar loads, no dependent chain).
+__device__ __forceinline__ int member_of(const int64_t (&first)[kMaxBatch + 1], int count, int64_t b) {
+    int p = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxBatch; ++i) p += (i < count && b >= first[i]) ? 1 : 0;
+    return p;
+}
+
+// Kernel configurations: MT token rows, KW1 / KW2 superchunks per wave window
+// in stage 1 / stage 2, XD / SD the dtypes of x and s_in (kAny: runtime).
+template <int MT, int KW1, int KW2, int XD, int SD>
 __global__ __launch_bounds__(kBlock) void k_decode_fused(const FusedBatch batch) {
-    __shared__ Lds<MT, SCMAX> lds;
     const int64_t b = blockIdx.x;
     if (b < batch.first1[batch.count]) {
-        int p = 0;
-        while (p + 1 < batch.count && b >= batch.first1[p + 1]) ++p;
-        stage1_tile<MT, SCMAX, true>(batch.p[p], lds, b - batch.first1[p]);
+        __shared__ TileLds<MT, KW1> lds1;
+        const int p = member_of(batch.first1, batch.count, b);
+        stage1_tile<MT, KW1, XD, SD, true>(batch.p[p], lds1, b - batch.first1[p], b);
     } else {
-        int p = 0;
-        while (p + 1 < batch.count && b >= batch.first2[p + 1]) ++p;
-        stage2_tile<MT, SCMAX, true>(batch.p[p], lds, b - batch.first2[p]);
+        __shared__ TileLds<MT, KW2> lds2;
+        const int p = member_of(batch.first2, batch.count, b);
+        stage2_tile<MT, KW2, SD, true>(batch.p[p], lds2, b - batch.first2[p], b);
     }
 }
 
 // Split launch, kernel 1: the stage-1 tiles of every linear in the batch.
-template <int MT, int SCMAX>
+template <int MT, int KW, int XD, int SD>
 __global__ __launch_bounds__(kBlock) void k_decode_stage1(const FusedBatch batch) {
-    __shared__ Lds<MT, SCMAX> lds;
+    __shared__ TileLds<MT, KW> lds;
     const int64_t b = blockIdx.x;
-    int p = 0;
-    while (p + 1 < batch.count && b >= batch.first1[p + 1]) ++p;
-    stage1_tile<MT, SCMAX, false>(batch.p[p], lds, b - batch.first1[p]);
+    const int p = member_of(batch.first1, batch.count, b);
+    stage1_tile<MT, KW, XD, SD, false>(batch.p[p], lds, b - batch.first1[p], b);
 }
 
 // Split launch, kernel 2: the stage-2 tiles (block index offset by the
 // stage-1 count so first2[] is shared with the fused grid).
-template <int MT, int SCMAX>
+template <int MT, int KW, int SD>
 __global__ __launch_bounds__(kBlock) void k_decode_stage2(const FusedBatch batch) {
-    __shared__ Lds<MT, SCMAX> lds;
+    __shared__ TileLds<MT, KW> lds;
     const int64_t b = blockIdx.x + batch.first1[batch.count];
-    int p = 0;
-    while (p + 1 < batch.count && b >= batch.first2[p + 1]) ++p;
-    stage2_tile<MT, SCMAX, false>(batch.p[p], lds, b - batch.first2[p]);
+    const int p = member_of(batch.first2, batch.count, b);
+    stage2_tile<MT, KW, SD, false>(batch.p[p], lds, b - batch.first2[p], b);
 }
 
 struct TilesGeometry {
@@ -701,12 +774,8 @@ TilesGeometry geometry(int64_t in, int64_t out, int64_t rank) {
     return g;
 }
 
-int64_t scratch_lm_bytes(const TilesGeometry& g) {
-    return (kMaxTokens * g.rt1 * kTileRows * 4 + 255) & ~int64_t(255);
-}
-
 int64_t scratch_bytes(const TilesGeometry& g) {
-    return scratch_lm_bytes(g) + ((g.rt1 * kMaxTokens * 4 + 255) & ~int64_t(255));
+    return (kMaxTokens * g.rt1 * kTileRows * 4 + 255) & ~int64_t(255);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -717,6 +786,7 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
     g = geometry(d->in_features, d->out_features, d->rank);
     if (!d->tiles) return NQ_ERR_ARGUMENT;
     if (d->tiles_bytes < (kHeaderWords + g.v_words + g.u_words) * 4) return NQ_ERR_ARGUMENT;
+    if (!aligned16(scratch)) return NQ_ERR_ALIGNMENT;
     a = FusedArgs{};
     a.in = d->in_features;
     a.rank = d->rank;
@@ -745,40 +815,65 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
     a.bias_dtype = d->bias_dtype;
     a.y = y;
     a.y_dtype = y_dtype;
-    char* ws = static_cast<char*>(scratch);
-    a.lm = reinterpret_cast<float*>(ws);
-    a.wgmax = reinterpret_cast<float*>(ws + scratch_lm_bytes(g));
-    a.x_vec = (d->in_features % 8 == 0 && aligned16(x) && aligned16(d->scale_pre)) ? 1 : 0;
+    a.lm = static_cast<float*>(scratch);
     return NQ_OK;
 }
 
-template <int MT, int SCMAX>
+// Typed vector loads of x and s_in need rows of length % 8 == 0 and 16-byte
+// aligned bases; anything else takes the element-wise kAny configuration.
+bool typed_ok(const FusedArgs& a) {
+    return a.in % 8 == 0 && aligned16(a.x) && aligned16(a.s_in);
+}
+
+template <int MT, int KW1, int KW2, int XD, int SD>
 void enqueue(const FusedBatch& batch, bool fused, hipStream_t stream) {
     const int64_t n1 = batch.first1[batch.count];
     const int64_t n = batch.first2[batch.count];
     if (fused) {
-        hipLaunchKernelGGL((k_decode_fused<MT, SCMAX>), dim3(static_cast<unsigned>(n)), dim3(kBlock), 0, stream,
-                           batch);
+        hipLaunchKernelGGL((k_decode_fused<MT, KW1, KW2, XD, SD>), dim3(static_cast<unsigned>(n)), dim3(kBlock), 0,
+                           stream, batch);
     } else {
-        hipLaunchKernelGGL((k_decode_stage1<MT, SCMAX>), dim3(static_cast<unsigned>(n1)), dim3(kBlock), 0, stream,
-                           batch);
-        hipLaunchKernelGGL((k_decode_stage2<MT, SCMAX>), dim3(static_cast<unsigned>(n - n1)), dim3(kBlock), 0,
+        hipLaunchKernelGGL((k_decode_stage1<MT, KW1, XD, SD>), dim3(static_cast<unsigned>(n1)), dim3(kBlock), 0,
+                           stream, batch);
+        hipLaunchKernelGGL((k_decode_stage2<MT, KW2, SD>), dim3(static_cast<unsigned>(n - n1)), dim3(kBlock), 0,
                            stream, batch);
     }
 }
 
-int launch_batch(FusedBatch& batch, int64_t tokens, int64_t max_nsc, bool fused, hipStream_t stream) {
+// Stage-1 activation dtype configurations: typed bf16 / f16 / f32 x with fp16
+// scales (the packed-artifact convention), element-wise kAny otherwise.
+template <int MT, int KW1, int KW2>
+void enqueue_dtypes(const FusedBatch& batch, bool typed, bool fused, hipStream_t stream) {
+    const int xd = batch.p[0].x_dtype;
+    const int sd = batch.p[0].scale_dtype;
+    if (typed && sd == NQ_DTYPE_F16 && xd == NQ_DTYPE_BF16) {
+        enqueue<MT, KW1, KW2, NQ_DTYPE_BF16, NQ_DTYPE_F16>(batch, fused, stream);
+    } else if (typed && sd == NQ_DTYPE_F16 && xd == NQ_DTYPE_F16) {
+        enqueue<MT, KW1, KW2, NQ_DTYPE_F16, NQ_DTYPE_F16>(batch, fused, stream);
+    } else if (typed && sd == NQ_DTYPE_F16 && xd == NQ_DTYPE_F32) {
+        enqueue<MT, KW1, KW2, NQ_DTYPE_F32, NQ_DTYPE_F16>(batch, fused, stream);
+    } else {
+        enqueue<MT, KW1, KW2, kAny, kAny>(batch, fused, stream);
+    }
+}
+
+int launch_batch(FusedBatch& batch, int64_t tokens, int64_t max_nsc1, int64_t max_nsc2, bool typed, bool fused,
+                 hipStream_t stream) {
     const int64_t n = batch.first2[batch.count];
     if (n <= 0 || n > 0x7fffffff) return NQ_ERR_SHAPE;
-    if (tokens == 1 && max_nsc <= 32) {
-        // in, rank <= 4096: one 4096-column window per stage, small register file.
-        enqueue<1, 8>(batch, fused, stream);
-    } else if (tokens == 1) {
-        enqueue<1, 24>(batch, fused, stream);
+    if (tokens == 1) {
+        // One token: a wave's whole K range in one window when it fits
+        // (8 superchunks per wave covers K <= 4096, 24 covers K <= 12288).
+        const bool wide1 = max_nsc1 > 32;
+        const bool wide2 = max_nsc2 > 32;
+        if (!wide1 && !wide2) enqueue_dtypes<1, 8, 8>(batch, typed, fused, stream);
+        else if (wide1 && !wide2) enqueue_dtypes<1, 24, 8>(batch, typed, fused, stream);
+        else if (!wide1 && wide2) enqueue_dtypes<1, 8, 24>(batch, typed, fused, stream);
+        else enqueue_dtypes<1, 24, 24>(batch, typed, fused, stream);
     } else if (tokens <= 4) {
-        enqueue<4, 6>(batch, fused, stream);
+        enqueue_dtypes<4, 4, 4>(batch, typed, fused, stream);
     } else {
-        enqueue<16, 4>(batch, fused, stream);
+        enqueue_dtypes<16, 2, 2>(batch, typed, fused, stream);
     }
     return nq::launch_status();
 }
@@ -811,17 +906,20 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
     if (tokens < 1 || tokens > kMaxTokens) return NQ_ERR_SHAPE;
     FusedBatch batch{};
     batch.count = count;
-    int64_t max_nsc = 0;
+    int64_t max_nsc1 = 0, max_nsc2 = 0;
     int64_t stage1 = 0;
+    bool typed = true;
     for (int i = 0; i < count; ++i) {
         if (descs[i]->decode_launch != descs[0]->decode_launch) return NQ_ERR_ARGUMENT;
+        if (descs[i]->scale_dtype != descs[0]->scale_dtype) return NQ_ERR_DTYPE;
         TilesGeometry g{};
         const int st = describe(descs[i], xs[i], x_dtype, tokens, ys[i], y_dtype, scratch[i], batch.p[i], g);
         if (st != NQ_OK) return st;
+        typed = typed && typed_ok(batch.p[i]);
         batch.first1[i] = stage1;
         stage1 += g.rt1;
-        max_nsc = g.nsc1 > max_nsc ? g.nsc1 : max_nsc;
-        max_nsc = g.nsc2 > max_nsc ? g.nsc2 : max_nsc;
+        max_nsc1 = g.nsc1 > max_nsc1 ? g.nsc1 : max_nsc1;
+        max_nsc2 = g.nsc2 > max_nsc2 ? g.nsc2 : max_nsc2;
     }
     batch.first1[count] = stage1;
     int64_t stage2 = stage1;
@@ -830,7 +928,8 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
         stage2 += batch.p[i].n2;
     }
     batch.first2[count] = stage2;
-    return launch_batch(batch, tokens, max_nsc, descs[0]->decode_launch == NQ_DECODE_FUSED, stream);
+    return launch_batch(batch, tokens, max_nsc1, max_nsc2, typed, descs[0]->decode_launch == NQ_DECODE_FUSED,
+                        stream);
 }
 
 }  // namespace nq
@@ -859,8 +958,7 @@ extern "C" int nq_prepare_tiles(const nq_linear_desc* d, void* tiles, int64_t ti
     if (reinterpret_cast<uintptr_t>(tiles) % 256 != 0) return NQ_ERR_ALIGNMENT;
     auto s = static_cast<hipStream_t>(stream);
     uint32_t* base = static_cast<uint32_t*>(tiles);
-    hipLaunchKernelGGL(k_init_header, dim3(1), dim3(kBlock), 0, s, base, d->scale_pre, d->scale_dtype,
-                       d->in_features);
+    hipLaunchKernelGGL(k_init_header, dim3(1), dim3(kBlock), 0, s, base);
     auto grid_for = [](int64_t n) {
         const int64_t b = (n + kBlock - 1) / kBlock;
         return static_cast<unsigned>(b < 16384 ? (b > 0 ? b : 1) : 16384);
