@@ -27,6 +27,7 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_PROFILE = ROOT / "profiles" / "decode_qwen3_8b_m1_hbm_traffic.md"
 METRIC = "decode tok/s (Qwen3-8B-shape, ~1bpw); packed GEMV HBM GB/s vs peak"
 
 
@@ -168,6 +169,23 @@ def time_mode(backend, stack, mode: str, steps: int, warmup: int, use_graph: boo
         "bytes_per_call": step_bytes / len(calls),
         "achieved_gbs": step_bytes / len(calls) / (call_ms * 1e-3) / 1e9,
     }
+
+
+def measured_traffic(mode: str, tokens: int, layers: int):
+    """HBM bytes per call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (calibrated against a plain copy), when it was measured on this
+    exact workload; None otherwise. Counters cannot be read inside a timed run."""
+
+    import re
+
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_call = (\d+) \(grouping (\S+), tokens (\d+), layers (\d+)\)", text)
+    if not m or (m.group(2), int(m.group(3)), int(m.group(4))) != (mode, tokens, layers):
+        return None
+    return int(m.group(1))
 
 
 def algorithmic_bytes(shape, tokens: int) -> int:
@@ -353,7 +371,8 @@ def main(argv=None) -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(head_mode, args.tokens, args.layers),
+            "traffic_source": TRAFFIC_PROFILE.name,
             "kernel": (f"one decode call = k_decode_fused" if head_mode.endswith("-fused") else
                        "one decode call = k_decode_stage1 + k_decode_stage2") + f" (grouping '{head_mode}')",
             "bytes_per_call": round(head["bytes_per_call"]),
