@@ -71,9 +71,10 @@ constexpr int kAny = -1;  // dtype template tag: runtime dtype, element loads
 //   ready root: each slot completer adds 1; the root completer of launch k
 //     (old value == (k + 1) * used_slots - 1) writes k + 1 into every ready
 //     flag.
-//   arrive slots: stage-2 workgroup i adds 1 to slot i % kArriveSlots at its
-//     start, which yields its own launch index k the same way; it then waits
-//     until ready flag i % kReplicas reaches k + 1 (wrap-safe compare).
+//   arrive slots: each output tile i of a stage-2 workgroup adds 1 to slot
+//     i % kArriveSlots at the workgroup's start, which yields the launch index
+//     k the same way; the workgroup then waits until its ready flag (any of
+//     the kReplicas copies) reaches k + 1 (wrap-safe compare).
 constexpr int kLine = 64;  // words per line
 constexpr int kReadySlots = 16;
 constexpr int kArriveSlots = 32;
@@ -157,7 +158,8 @@ __global__ void k_init_header(uint32_t* header) {
 
 struct FusedArgs {
     int64_t in, rank, out;
-    int64_t n1, n2;          // stage-1 / stage-2 workgroups (= row tiles of V / U)
+    int64_t n1, n2;          // row tiles of V / U (stage-1 workgroups = n1)
+    int64_t g2;              // stage-2 workgroups (n2 tiles in groups of the launch's T)
     int64_t nsc1, nsc2;      // superchunks of in / rank
     const uint32_t* v_tiles;
     const uint32_t* u_tiles;
@@ -319,25 +321,28 @@ __device__ __forceinline__ float load_one(const void* __restrict__ p, int64_t i,
 
 // A window is KW superchunks (128 * KW columns) of MT token rows. Vector e =
 // lane + 64 * j (j < NV) covers token t = e / CV and columns 8 * (e % CV) of
-// the window. When 64 % CV == 0 the column (and so its column scale) is the
-// same for every j of a lane.
+// the window; vectors e >= MT * CV (a partial last j) are dead. When
+// 64 % CV == 0 the column (and so its column scale) is the same for every j
+// of a lane.
 template <int MT, int KW>
 struct Win {
-    static constexpr int CW = KW * kSuperCols;      // columns per window
-    static constexpr int CV = CW / 8;               // 8-column vectors per token row
-    static constexpr int NV = MT * CV / 64;         // vectors per lane
+    static constexpr int CW = KW * kSuperCols;          // columns per window
+    static constexpr int CV = CW / 8;                   // 8-column vectors per token row
+    static constexpr int NE = MT * CV;                  // vectors per window
+    static constexpr int NV = (NE + 63) / 64;           // vectors per lane
     static constexpr bool kSameCol = (CV <= 64) && (64 % CV == 0);
-    static constexpr int NS = kSameCol ? 1 : NV;    // column-scale vectors per lane
-    static constexpr int kStride = CW + 8;          // LDS row stride (halfs)
-    static_assert((MT * CV) % 64 == 0, "window must split evenly over a wave");
+    static constexpr int NS = kSameCol ? 1 : NV;        // column-scale vectors per lane
+    static constexpr int kStride = CW + 8;              // LDS row stride (halfs)
 };
 
-template <int MT, int KW, int XD, int SD>
+// Registers of one wave's window: the activation vectors and the sign words
+// of T tiles that share them.
+template <int MT, int KW, int XD, int SD, int T>
 struct WinRegs {
     Raw8<XD> x[Win<MT, KW>::NV];
     Raw8<SD> s[Win<MT, KW>::NS];
     bool live[Win<MT, KW>::NV];
-    uint32_t w[KW];
+    uint32_t w[T][KW];
 };
 
 // Where the activations of a window come from.
@@ -355,16 +360,16 @@ struct ActRef {
 // from clamped addresses (no branches, so the compiler can count outstanding
 // loads exactly) and record which vectors are live; dead vectors are zeroed
 // when unpacked. Columns past the wave's range are dead, so their MFMAs add 0.
-template <int MT, int KW, int XD, int SD>
-__device__ __forceinline__ void load_acts(WinRegs<MT, KW, XD, SD>& r, const ActRef& a, int64_t sc0, int64_t sc_end,
-                                          int lane) {
+template <int MT, int KW, int XD, int SD, int T>
+__device__ __forceinline__ void load_acts(WinRegs<MT, KW, XD, SD, T>& r, const ActRef& a, int64_t sc0,
+                                          int64_t sc_end, int lane) {
     using W = Win<MT, KW>;
 #pragma unroll
     for (int j = 0; j < W::NV; ++j) {
         const int e = lane + 64 * j;
         const int t = e / W::CV;
         const int64_t col = sc0 * kSuperCols + 8 * (e % W::CV);
-        r.live[j] = t < a.tokens && col < a.limit && sc0 + (8 * (e % W::CV)) / kSuperCols < sc_end;
+        r.live[j] = e < W::NE && t < a.tokens && col < a.limit && sc0 + (8 * (e % W::CV)) / kSuperCols < sc_end;
         if constexpr (XD == kAny) {
             if (r.live[j]) raw_load<XD>(r.x[j], a.p, t * a.ld, col, a.limit, a.dtype);
             else raw_zero<XD>(r.x[j]);
@@ -392,13 +397,16 @@ __device__ __forceinline__ void load_acts(WinRegs<MT, KW, XD, SD>& r, const ActR
 
 // Sign words of a window; superchunks past the tile's last load a valid word
 // (their activations are zero).
-template <int MT, int KW, int XD, int SD>
-__device__ __forceinline__ void load_words(WinRegs<MT, KW, XD, SD>& r, const uint32_t* __restrict__ tile,
+template <int MT, int KW, int XD, int SD, int T>
+__device__ __forceinline__ void load_words(WinRegs<MT, KW, XD, SD, T>& r, const uint32_t* const (&tiles)[T],
                                            int64_t sc0, int64_t nsc, int lane) {
 #pragma unroll
-    for (int i = 0; i < KW; ++i) {
-        const int64_t sc = sc0 + i < nsc ? sc0 + i : nsc - 1;
-        r.w[i] = __builtin_nontemporal_load(tile + sc * 64 + lane);
+    for (int tt = 0; tt < T; ++tt) {
+#pragma unroll
+        for (int i = 0; i < KW; ++i) {
+            const int64_t sc = sc0 + i < nsc ? sc0 + i : nsc - 1;
+            r.w[tt][i] = __builtin_nontemporal_load(tiles[tt] + sc * 64 + lane);
+        }
     }
 }
 
@@ -420,8 +428,8 @@ __device__ __forceinline__ float row16_max(float v) {
 // Scale the window into fp16 (per-token exact power of two from the window's
 // max |value|), write it to this wave's LDS rows act[t][c], and return the
 // per-token exponents (uniform; tokens >= MT unused).
-template <int MT, int KW, int XD, int SD>
-__device__ __forceinline__ void stage_window(const WinRegs<MT, KW, XD, SD>& r, bool has_colscale,
+template <int MT, int KW, int XD, int SD, int T>
+__device__ __forceinline__ void stage_window(const WinRegs<MT, KW, XD, SD, T>& r, bool has_colscale,
                                              _Float16* __restrict__ act, int lane, int (&expo)[MT]) {
     using W = Win<MT, KW>;
     // Two passes over the raw registers (max, then scale + pack) keep only one
@@ -456,8 +464,10 @@ __device__ __forceinline__ void stage_window(const WinRegs<MT, KW, XD, SD>& r, b
 #pragma unroll
         for (int row = 0; row < 4; ++row) {
             const int t = (16 * row + 64 * j) / W::CV;
-            const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 16 * row));
-            tmax[t] = fmaxf(tmax[t], rv);
+            if (t < MT) {  // compile time: rows of a dead tail hold zeros
+                const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rm), 16 * row));
+                tmax[t] = fmaxf(tmax[t], rv);
+            }
         }
     }
     float scale[MT];
@@ -472,7 +482,7 @@ __device__ __forceinline__ void stage_window(const WinRegs<MT, KW, XD, SD>& r, b
         // Token of this vector; uniform per j unless a token row spans less than a wave.
         float sc;
         if constexpr (W::CV >= 64) {
-            sc = scale[(64 * j) / W::CV];
+            sc = scale[(64 * j) / W::CV < MT ? (64 * j) / W::CV : MT - 1];
         } else {
             sc = scale[0];
 #pragma unroll
@@ -486,32 +496,42 @@ __device__ __forceinline__ void stage_window(const WinRegs<MT, KW, XD, SD>& r, b
         } pk;
 #pragma unroll
         for (int k = 0; k < 8; ++k) pk.h[k] = static_cast<_Float16>(v[k] * sc);
-        *reinterpret_cast<v4u*>(act + (e / W::CV) * W::kStride + 8 * (e % W::CV)) = pk.u;
+        if (W::NE % 64 == 0 || e < W::NE) *reinterpret_cast<v4u*>(act + (e / W::CV) * W::kStride + 8 * (e % W::CV)) = pk.u;
     }
 }
 
-// MFMAs of one window (KW superchunks). Every lane reads an A row: lanes of
-// token rows >= MT read row t % MT, which only feeds D rows that are never
-// used. One accumulator per 32-column chunk keeps the MFMA chains short; they
-// are summed in a fixed order.
-template <int MT, int KW, int XD, int SD>
-__device__ __forceinline__ v4f window_mfma(const WinRegs<MT, KW, XD, SD>& r, const _Float16* __restrict__ act,
-                                           int lane) {
+// MFMAs of one window (KW superchunks, of which the first nact are live) for
+// each of the T tiles. Every lane reads an A row: lanes of token rows >= MT
+// read row t % MT, which only feeds D rows that are never used. One accumulator per tile and 32-column chunk
+// keeps the MFMA chains short; they are summed in a fixed order.
+template <int MT, int KW, int XD, int SD, int T, bool SKIP>
+__device__ __forceinline__ void window_mfma(const WinRegs<MT, KW, XD, SD, T>& r, const _Float16* __restrict__ act,
+                                            int nact, int lane, v4f (&out)[T]) {
     using W = Win<MT, KW>;
     const int g = lane >> 4;
     const _Float16* row = act + ((lane & 15) % MT) * W::kStride + 8 * g;
-    v4f acc[4];
+    v4f acc[T][4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) acc[m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) acc[tt][m] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < KW; ++i) {
+        // Superchunks past the wave's range hold zero activations; SKIP
+        // branches over them (uniform), otherwise they add exact zeros.
+        if (!SKIP || i < nact) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const v8h a = *reinterpret_cast<const v8h*>(row + i * kSuperCols + 32 * m);
-            acc[m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, expand_signs(r.w[i], m), acc[m], 0, 0, 0);
+            for (int m = 0; m < 4; ++m) {
+                const v8h a = *reinterpret_cast<const v8h*>(row + i * kSuperCols + 32 * m);
+#pragma unroll
+                for (int tt = 0; tt < T; ++tt)
+                    acc[tt][m] =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(a, expand_signs(r.w[tt][i], m), acc[tt][m], 0, 0, 0);
+            }
         }
     }
-    return (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) out[tt] = (acc[tt][0] + acc[tt][1]) + (acc[tt][2] + acc[tt][3]);
 }
 
 // Order this wave's LDS writes before its own reads (waves never share rows).
@@ -540,38 +560,41 @@ __device__ __forceinline__ void add_scaled(v4f& tot, const v4f& acc, const int (
 }
 
 // Shared memory of one workgroup.
-template <int MT, int KW>
+template <int MT, int KW, int T>
 struct alignas(16) TileLds {
     _Float16 act[kWaves][MT * Win<MT, KW>::kStride];
-    float red[kWaves][kMaxTokens][kTileRows];
+    float red[T][kWaves][kMaxTokens][kTileRows];
 };
 
-// One wave's share of a 16-row tile: superchunks [s_begin, s_end) in windows
-// of KW. Returns the wave's fp32 partial D (tokens x 16 rows).
-template <int MT, int KW, int XD, int SD, bool WORDS_FIRST>
-__device__ __forceinline__ v4f wave_tile(const ActRef& act_ref, const uint32_t* __restrict__ tile, int64_t nsc,
-                                         int64_t s_begin, int64_t s_end, _Float16* __restrict__ act, int lane) {
-    v4f tot = {0.0f, 0.0f, 0.0f, 0.0f};
+// One wave's share of T 16-row tiles: superchunks [s_begin, s_end) in windows
+// of KW. Writes the wave's fp32 partial D (tokens x 16 rows) of each tile.
+template <int MT, int KW, int XD, int SD, int T, bool WORDS_FIRST, bool SKIP>
+__device__ __forceinline__ void wave_tile(const ActRef& act_ref, const uint32_t* const (&tiles)[T], int64_t nsc,
+                                          int64_t s_begin, int64_t s_end, _Float16* __restrict__ act, int lane,
+                                          v4f (&tot)[T]) {
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) tot[tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
     for (int64_t sc0 = s_begin; sc0 < s_end; sc0 += KW) {
-        WinRegs<MT, KW, XD, SD> r;
+        WinRegs<MT, KW, XD, SD, T> r;
         if (WORDS_FIRST) {
-            load_words(r, tile, sc0, nsc, lane);
+            load_words(r, tiles, sc0, nsc, lane);
             __builtin_amdgcn_sched_barrier(0);
             load_acts(r, act_ref, sc0, s_end, lane);
         } else {
             load_acts(r, act_ref, sc0, s_end, lane);
             __builtin_amdgcn_sched_barrier(0);
-            load_words(r, tile, sc0, nsc, lane);
+            load_words(r, tiles, sc0, nsc, lane);
         }
         __builtin_amdgcn_sched_barrier(0);  // every load is issued before any use
         int expo[MT];
         stage_window(r, act_ref.colscale != nullptr, act, lane, expo);
         wave_lds_sync();
-        const v4f acc = window_mfma(r, act, lane);
-        add_scaled<MT>(tot, acc, expo, lane);
+        v4f acc[T];
+        window_mfma<MT, KW, XD, SD, T, SKIP>(r, act, static_cast<int>(s_end - sc0 < KW ? s_end - sc0 : KW), lane, acc);
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) add_scaled<MT>(tot[tt], acc[tt], expo, lane);
         wave_lds_sync();  // the next window rewrites the rows this one read
     }
-    return tot;
 }
 
 // Contiguous superchunk range of wave `w` out of nsc.
@@ -581,22 +604,26 @@ __device__ __forceinline__ void wave_range(int64_t nsc, int w, int64_t& b, int64
     e = b + q < nsc ? b + q : nsc;
 }
 
-// Sum the four waves' partial tiles (fixed order: deterministic). Returns the
-// value for (t = tid / 16, n = tid % 16).
-template <int MT, int KW>
-__device__ __forceinline__ float reduce_waves(TileLds<MT, KW>& lds, v4f tot) {
+// Sum the four waves' partial tiles (fixed order: deterministic). Returns,
+// per tile, the value for (t = tid / 16, n = tid % 16).
+template <int MT, int KW, int T>
+__device__ __forceinline__ void reduce_waves(TileLds<MT, KW, T>& lds, const v4f (&tot)[T], float (&sum)[T]) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) lds.red[wave][4 * (lane >> 4) + i][lane & 15] = tot[i];
+    for (int tt = 0; tt < T; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds.red[tt][wave][4 * (lane >> 4) + i][lane & 15] = tot[tt][i];
     __syncthreads();
     const int t = threadIdx.x >> 4;
     const int n = threadIdx.x & 15;
-    return ((lds.red[0][t][n] + lds.red[1][t][n]) + lds.red[2][t][n]) + lds.red[3][t][n];
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt)
+        sum[tt] = ((lds.red[tt][0][t][n] + lds.red[tt][1][t][n]) + lds.red[tt][2][t][n]) + lds.red[tt][3][t][n];
 }
 
 template <int MT, int KW, int XD, int SD, bool FUSED>
-__device__ __forceinline__ void stage1_tile(const FusedArgs& a, TileLds<MT, KW>& lds, int64_t rt,
+__device__ __forceinline__ void stage1_tile(const FusedArgs& a, TileLds<MT, KW, 1>& lds, int64_t rt,
                                             [[maybe_unused]] int64_t gblock) {
     NQ_TRACE(0);
     const int lane = threadIdx.x & 63;
@@ -611,10 +638,13 @@ __device__ __forceinline__ void stage1_tile(const FusedArgs& a, TileLds<MT, KW>&
     int64_t sb, se;
     wave_range(a.nsc1, wave, sb, se);
     const ActRef xr{a.x, a.x_dtype, a.in, a.in, a.s_in, a.scale_dtype, a.tokens};
-    const v4f tot =
-        wave_tile<MT, KW, XD, SD, false>(xr, a.v_tiles + rt * a.nsc1 * 64, a.nsc1, sb, se, lds.act[wave], lane);
+    const uint32_t* const tiles[1] = {a.v_tiles + rt * a.nsc1 * 64};
+    v4f tot[1];
+    wave_tile<MT, KW, XD, SD, 1, false, FUSED>(xr, tiles, a.nsc1, sb, se, lds.act[wave], lane, tot);
     NQ_TRACE(1);
-    const float sum = reduce_waves(lds, tot);
+    float sums[1];
+    reduce_waves(lds, tot, sums);
+    const float sum = sums[0];
     NQ_TRACE(2);
     // Pad ranks [rank, 16 * n1) are written as zero: stage 2 reads whole rows
     // and their sign bits decode to +1.
@@ -649,12 +679,24 @@ __device__ __forceinline__ void stage1_tile(const FusedArgs& a, TileLds<MT, KW>&
 }
 
 // Fused launch: wait until every stage-1 workgroup of this launch has signalled.
-__device__ __forceinline__ void wait_ready(const FusedArgs& a, int64_t rt) {
+// Arrivals are counted per output tile (each of the group's tiles adds 1 to
+// slot tile % kArriveSlots), so the per-slot count of a launch depends only on
+// the layer, not on how many tiles a workgroup takes: launches of one layer
+// with different grouping keep consistent launch indices.
+template <int T>
+__device__ __forceinline__ void wait_ready(const FusedArgs& a, int64_t grp) {
     if (threadIdx.x == 0) {
-        const int slot = static_cast<int>(rt % kArriveSlots);
-        const uint64_t c = slot_count(slot, kArriveSlots, a.n2);
-        const uint32_t target = static_cast<uint32_t>(hdr_add(a.header, line_word(kArriveSlot0 + slot)) / c + 1);
-        const uint32_t* flag = a.header + line_word(kReplica0 + static_cast<int>(rt % kReplicas));
+        uint32_t target = 0;
+#pragma unroll
+        for (int tt = 0; tt < T; ++tt) {
+            const int64_t tile = grp * T + tt;
+            if (tile < a.n2) {
+                const int slot = static_cast<int>(tile % kArriveSlots);
+                const uint64_t v = hdr_add(a.header, line_word(kArriveSlot0 + slot));
+                if (tt == 0) target = static_cast<uint32_t>(v / slot_count(slot, kArriveSlots, a.n2) + 1);
+            }
+        }
+        const uint32_t* flag = a.header + line_word(kReplica0 + static_cast<int>(grp % kReplicas));
         uint32_t spins = 0;
         while (static_cast<int32_t>(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
             if (++spins > kSpinLimit) {
@@ -668,17 +710,26 @@ __device__ __forceinline__ void wait_ready(const FusedArgs& a, int64_t rt) {
     __syncthreads();
 }
 
-template <int MT, int KW, int SD, bool FUSED>
-__device__ __forceinline__ void stage2_tile(const FusedArgs& a, TileLds<MT, KW>& lds, int64_t rt,
+// Stage-2 workgroup `grp`: output tiles grp * T + tt (tt < T) share each lm window.
+template <int MT, int KW, int SD, int T, bool FUSED>
+__device__ __forceinline__ void stage2_tile(const FusedArgs& a, TileLds<MT, KW, T>& lds, int64_t grp,
                                             [[maybe_unused]] int64_t gblock) {
     NQ_TRACE(0);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int t = threadIdx.x >> 4;
     const int n = threadIdx.x & 15;
-    const int64_t o = rt * kTileRows + n;
-    const bool store = t < a.tokens && o < a.out;
-    const float sout = load_one<SD>(a.s_out, o < a.out ? o : a.out - 1, a.scale_dtype);
+    int64_t o[T];
+    float sout[T];
+    const uint32_t* tiles[T];
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) {
+        const int64_t rt = grp * T + tt;
+        o[tt] = rt * kTileRows + n;
+        sout[tt] = load_one<SD>(a.s_out, o[tt] < a.out ? o[tt] : a.out - 1, a.scale_dtype);
+        // A tile past the last one (partial group) reuses the last tile's words; it is never stored.
+        tiles[tt] = a.u_tiles + (rt < a.n2 ? rt : a.n2 - 1) * a.nsc2 * 64;
+    }
 
     int64_t sb, se;
     wave_range(a.nsc2, wave, sb, se);
@@ -686,30 +737,38 @@ __device__ __forceinline__ void stage2_tile(const FusedArgs& a, TileLds<MT, KW>&
     // lm rows have stride lm_ld (a multiple of 16, zeros past `rank`), so whole
     // 8-element vectors up to lm_ld are valid.
     const ActRef lr{a.lm, NQ_DTYPE_F32, lm_ld, lm_ld, nullptr, 0, a.tokens};
-    const uint32_t* tile = a.u_tiles + rt * a.nsc2 * 64;
-    v4f tot;
+    v4f tot[T];
     if (FUSED) {
         // Touch the first window's words before waiting, so the U stream
         // overlaps stage 1; the loop below then hits in cache.
-        if (sb < se) (void)__builtin_nontemporal_load(tile + sb * 64 + lane);
-        wait_ready(a, rt);
+        if (sb < se) {
+#pragma unroll
+            for (int tt = 0; tt < T; ++tt) (void)__builtin_nontemporal_load(tiles[tt] + sb * 64 + lane);
+        }
+        wait_ready<T>(a, grp);
         NQ_TRACE(1);
-        tot = wave_tile<MT, KW, NQ_DTYPE_F32, NQ_DTYPE_F32, true>(lr, tile, a.nsc2, sb, se, lds.act[wave], lane);
+        wave_tile<MT, KW, NQ_DTYPE_F32, NQ_DTYPE_F32, T, true, true>(lr, tiles, a.nsc2, sb, se, lds.act[wave], lane,
+                                                                     tot);
     } else {
         NQ_TRACE(1);
-        tot = wave_tile<MT, KW, NQ_DTYPE_F32, NQ_DTYPE_F32, false>(lr, tile, a.nsc2, sb, se, lds.act[wave], lane);
+        wave_tile<MT, KW, NQ_DTYPE_F32, NQ_DTYPE_F32, T, false, false>(lr, tiles, a.nsc2, sb, se, lds.act[wave], lane,
+                                                                       tot);
     }
     NQ_TRACE(2);
-    const float sum = reduce_waves(lds, tot);
-    if (store) {
-        float v = sum * sout;
-        for (int64_t k = 0; k < a.salient_count; ++k) {
-            float wv = nq::load_f32(a.salient_values, a.salient_dtype, o * a.salient_count + k);
-            if (a.salient_scales) wv *= nq::load_f32(a.salient_scales, a.scale_dtype, k);
-            v += wv * nq::load_f32(a.x, a.x_dtype, t * a.in + a.salient_indices[k]);
+    float sum[T];
+    reduce_waves(lds, tot, sum);
+#pragma unroll
+    for (int tt = 0; tt < T; ++tt) {
+        if (t < a.tokens && o[tt] < a.out) {
+            float v = sum[tt] * sout[tt];
+            for (int64_t k = 0; k < a.salient_count; ++k) {
+                float wv = nq::load_f32(a.salient_values, a.salient_dtype, o[tt] * a.salient_count + k);
+                if (a.salient_scales) wv *= nq::load_f32(a.salient_scales, a.scale_dtype, k);
+                v += wv * nq::load_f32(a.x, a.x_dtype, t * a.in + a.salient_indices[k]);
+            }
+            if (a.bias) v += nq::load_f32(a.bias, a.bias_dtype, o[tt]);
+            nq::store_f32_as(a.y, a.y_dtype, t * a.out + o[tt], v);
         }
-        if (a.bias) v += nq::load_f32(a.bias, a.bias_dtype, o);
-        nq::store_f32_as(a.y, a.y_dtype, t * a.out + o, v);
     }
     NQ_TRACE(3);
 }
@@ -724,25 +783,26 @@ __device__ __forceinline__ int member_of(const int64_t (&first)[kMaxBatch + 1], 
 }
 
 // Kernel configurations: MT token rows, KW1 / KW2 superchunks per wave window
-// in stage 1 / stage 2, XD / SD the dtypes of x and s_in (kAny: runtime).
-template <int MT, int KW1, int KW2, int XD, int SD>
+// in stage 1 / stage 2, XD / SD the dtypes of x and s_in (kAny: runtime), T2
+// the output tiles per stage-2 workgroup.
+template <int MT, int KW1, int KW2, int XD, int SD, int T2>
 __global__ __launch_bounds__(kBlock) void k_decode_fused(const FusedBatch batch) {
     const int64_t b = blockIdx.x;
     if (b < batch.first1[batch.count]) {
-        __shared__ TileLds<MT, KW1> lds1;
+        __shared__ TileLds<MT, KW1, 1> lds1;
         const int p = member_of(batch.first1, batch.count, b);
         stage1_tile<MT, KW1, XD, SD, true>(batch.p[p], lds1, b - batch.first1[p], b);
     } else {
-        __shared__ TileLds<MT, KW2> lds2;
+        __shared__ TileLds<MT, KW2, T2> lds2;
         const int p = member_of(batch.first2, batch.count, b);
-        stage2_tile<MT, KW2, SD, true>(batch.p[p], lds2, b - batch.first2[p], b);
+        stage2_tile<MT, KW2, SD, T2, true>(batch.p[p], lds2, b - batch.first2[p], b);
     }
 }
 
 // Split launch, kernel 1: the stage-1 tiles of every linear in the batch.
 template <int MT, int KW, int XD, int SD>
 __global__ __launch_bounds__(kBlock) void k_decode_stage1(const FusedBatch batch) {
-    __shared__ TileLds<MT, KW> lds;
+    __shared__ TileLds<MT, KW, 1> lds;
     const int64_t b = blockIdx.x;
     const int p = member_of(batch.first1, batch.count, b);
     stage1_tile<MT, KW, XD, SD, false>(batch.p[p], lds, b - batch.first1[p], b);
@@ -750,12 +810,12 @@ __global__ __launch_bounds__(kBlock) void k_decode_stage1(const FusedBatch batch
 
 // Split launch, kernel 2: the stage-2 tiles (block index offset by the
 // stage-1 count so first2[] is shared with the fused grid).
-template <int MT, int KW, int SD>
+template <int MT, int KW, int SD, int T>
 __global__ __launch_bounds__(kBlock) void k_decode_stage2(const FusedBatch batch) {
-    __shared__ TileLds<MT, KW> lds;
+    __shared__ TileLds<MT, KW, T> lds;
     const int64_t b = blockIdx.x + batch.first1[batch.count];
     const int p = member_of(batch.first2, batch.count, b);
-    stage2_tile<MT, KW, SD, false>(batch.p[p], lds, b - batch.first2[p], b);
+    stage2_tile<MT, KW, SD, T, false>(batch.p[p], lds, b - batch.first2[p], b);
 }
 
 struct TilesGeometry {
@@ -825,55 +885,115 @@ bool typed_ok(const FusedArgs& a) {
     return a.in % 8 == 0 && aligned16(a.x) && aligned16(a.s_in);
 }
 
-template <int MT, int KW1, int KW2, int XD, int SD>
-void enqueue(const FusedBatch& batch, bool fused, hipStream_t stream) {
-    const int64_t n1 = batch.first1[batch.count];
-    const int64_t n = batch.first2[batch.count];
-    if (fused) {
-        hipLaunchKernelGGL((k_decode_fused<MT, KW1, KW2, XD, SD>), dim3(static_cast<unsigned>(n)), dim3(kBlock), 0,
-                           stream, batch);
-    } else {
-        hipLaunchKernelGGL((k_decode_stage1<MT, KW1, XD, SD>), dim3(static_cast<unsigned>(n1)), dim3(kBlock), 0,
-                           stream, batch);
-        hipLaunchKernelGGL((k_decode_stage2<MT, KW2, SD>), dim3(static_cast<unsigned>(n - n1)), dim3(kBlock), 0,
-                           stream, batch);
-    }
-}
-
-// Stage-1 activation dtype configurations: typed bf16 / f16 / f32 x with fp16
-// scales (the packed-artifact convention), element-wise kAny otherwise.
-template <int MT, int KW1, int KW2>
-void enqueue_dtypes(const FusedBatch& batch, bool typed, bool fused, hipStream_t stream) {
+// Split launch: stage-1 configuration (KW1 superchunks per window, typed bf16 /
+// f16 / f32 x with fp16 scales, element-wise kAny otherwise).
+template <int MT, int KW1>
+void enqueue_stage1(const FusedBatch& batch, bool typed, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(batch.first1[batch.count]));
     const int xd = batch.p[0].x_dtype;
     const int sd = batch.p[0].scale_dtype;
     if (typed && sd == NQ_DTYPE_F16 && xd == NQ_DTYPE_BF16) {
-        enqueue<MT, KW1, KW2, NQ_DTYPE_BF16, NQ_DTYPE_F16>(batch, fused, stream);
+        hipLaunchKernelGGL((k_decode_stage1<MT, KW1, NQ_DTYPE_BF16, NQ_DTYPE_F16>), grid, dim3(kBlock), 0, stream,
+                           batch);
     } else if (typed && sd == NQ_DTYPE_F16 && xd == NQ_DTYPE_F16) {
-        enqueue<MT, KW1, KW2, NQ_DTYPE_F16, NQ_DTYPE_F16>(batch, fused, stream);
+        hipLaunchKernelGGL((k_decode_stage1<MT, KW1, NQ_DTYPE_F16, NQ_DTYPE_F16>), grid, dim3(kBlock), 0, stream,
+                           batch);
     } else if (typed && sd == NQ_DTYPE_F16 && xd == NQ_DTYPE_F32) {
-        enqueue<MT, KW1, KW2, NQ_DTYPE_F32, NQ_DTYPE_F16>(batch, fused, stream);
+        hipLaunchKernelGGL((k_decode_stage1<MT, KW1, NQ_DTYPE_F32, NQ_DTYPE_F16>), grid, dim3(kBlock), 0, stream,
+                           batch);
     } else {
-        enqueue<MT, KW1, KW2, kAny, kAny>(batch, fused, stream);
+        hipLaunchKernelGGL((k_decode_stage1<MT, KW1, kAny, kAny>), grid, dim3(kBlock), 0, stream, batch);
     }
 }
 
+template <int MT, int KW2, int T2>
+void enqueue_stage2(const FusedBatch& batch, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(batch.first2[batch.count] - batch.first1[batch.count]));
+    if (batch.p[0].scale_dtype == NQ_DTYPE_F16) {
+        hipLaunchKernelGGL((k_decode_stage2<MT, KW2, NQ_DTYPE_F16, T2>), grid, dim3(kBlock), 0, stream, batch);
+    } else {
+        hipLaunchKernelGGL((k_decode_stage2<MT, KW2, kAny, T2>), grid, dim3(kBlock), 0, stream, batch);
+    }
+}
+
+// Fused launch: element-wise activation loads and a window of 8 or 24
+// superchunks (dead superchunks skipped), so its few configurations cover
+// every shape; a single-window wave computes the same values for any window
+// size, so fused and split outputs are identical.
+template <int MT, int KW1, int KW2, int T2>
+void enqueue_fused(const FusedBatch& batch, hipStream_t stream) {
+    hipLaunchKernelGGL((k_decode_fused<MT, KW1, KW2, kAny, kAny, T2>),
+                       dim3(static_cast<unsigned>(batch.first2[batch.count])), dim3(kBlock), 0, stream, batch);
+}
+
+// Output tiles per stage-2 workgroup: two when the batch has enough tiles to
+// fill the GPU twice over (each lm window then feeds two tiles' MFMAs).
+constexpr int64_t kPairTilesFrom = 512;
+
+// Superchunks per wave of a K of nsc superchunks.
+int64_t per_wave(int64_t nsc) { return (nsc + kWaves - 1) / kWaves; }
+
 int launch_batch(FusedBatch& batch, int64_t tokens, int64_t max_nsc1, int64_t max_nsc2, bool typed, bool fused,
                  hipStream_t stream) {
+    int64_t tiles2 = 0;
+    for (int i = 0; i < batch.count; ++i) tiles2 += batch.p[i].n2;
+    const int t2 = (tokens == 1 && tiles2 >= kPairTilesFrom) ? 2 : 1;
+    int64_t stage2 = batch.first1[batch.count];
+    for (int i = 0; i < batch.count; ++i) {
+        batch.p[i].g2 = (batch.p[i].n2 + t2 - 1) / t2;
+        batch.first2[i] = stage2;
+        stage2 += batch.p[i].g2;
+    }
+    batch.first2[batch.count] = stage2;
     const int64_t n = batch.first2[batch.count];
     if (n <= 0 || n > 0x7fffffff) return NQ_ERR_SHAPE;
+    const int64_t q1 = per_wave(max_nsc1), q2 = per_wave(max_nsc2);
+    if (fused) {
+        if (tokens == 1) {
+            const bool w1 = q1 > 8, w2 = q2 > 8;
+            if (t2 == 2) {
+                if (!w1 && !w2) enqueue_fused<1, 8, 8, 2>(batch, stream);
+                else if (w1 && !w2) enqueue_fused<1, 24, 8, 2>(batch, stream);
+                else if (!w1 && w2) enqueue_fused<1, 8, 24, 2>(batch, stream);
+                else enqueue_fused<1, 24, 24, 2>(batch, stream);
+            } else {
+                if (!w1 && !w2) enqueue_fused<1, 8, 8, 1>(batch, stream);
+                else if (w1 && !w2) enqueue_fused<1, 24, 8, 1>(batch, stream);
+                else if (!w1 && w2) enqueue_fused<1, 8, 24, 1>(batch, stream);
+                else enqueue_fused<1, 24, 24, 1>(batch, stream);
+            }
+        } else if (tokens <= 4) {
+            enqueue_fused<4, 4, 4, 1>(batch, stream);
+        } else {
+            enqueue_fused<16, 2, 2, 1>(batch, stream);
+        }
+        return nq::launch_status();
+    }
     if (tokens == 1) {
-        // One token: a wave's whole K range in one window when it fits
-        // (8 superchunks per wave covers K <= 4096, 24 covers K <= 12288).
-        const bool wide1 = max_nsc1 > 32;
-        const bool wide2 = max_nsc2 > 32;
-        if (!wide1 && !wide2) enqueue_dtypes<1, 8, 8>(batch, typed, fused, stream);
-        else if (wide1 && !wide2) enqueue_dtypes<1, 24, 8>(batch, typed, fused, stream);
-        else if (!wide1 && wide2) enqueue_dtypes<1, 8, 24>(batch, typed, fused, stream);
-        else enqueue_dtypes<1, 24, 24>(batch, typed, fused, stream);
+        // One token: the window covers a wave's whole K range when it fits,
+        // sized to that range so no MFMA runs on dead superchunks.
+        if (q1 <= 4) enqueue_stage1<1, 4>(batch, typed, stream);
+        else if (q1 <= 8) enqueue_stage1<1, 8>(batch, typed, stream);
+        else enqueue_stage1<1, 24>(batch, typed, stream);
+        if (t2 == 2) {
+            if (q2 <= 2) enqueue_stage2<1, 2, 2>(batch, stream);
+            else if (q2 <= 4) enqueue_stage2<1, 4, 2>(batch, stream);
+            else if (q2 <= 6) enqueue_stage2<1, 6, 2>(batch, stream);
+            else if (q2 <= 8) enqueue_stage2<1, 8, 2>(batch, stream);
+            else enqueue_stage2<1, 24, 2>(batch, stream);
+        } else {
+            if (q2 <= 2) enqueue_stage2<1, 2, 1>(batch, stream);
+            else if (q2 <= 4) enqueue_stage2<1, 4, 1>(batch, stream);
+            else if (q2 <= 6) enqueue_stage2<1, 6, 1>(batch, stream);
+            else if (q2 <= 8) enqueue_stage2<1, 8, 1>(batch, stream);
+            else enqueue_stage2<1, 24, 1>(batch, stream);
+        }
     } else if (tokens <= 4) {
-        enqueue_dtypes<4, 4, 4>(batch, typed, fused, stream);
+        enqueue_stage1<4, 4>(batch, typed, stream);
+        enqueue_stage2<4, 4, 1>(batch, stream);
     } else {
-        enqueue_dtypes<16, 2, 2>(batch, typed, fused, stream);
+        enqueue_stage1<16, 2>(batch, typed, stream);
+        enqueue_stage2<16, 2, 1>(batch, stream);
     }
     return nq::launch_status();
 }
@@ -922,12 +1042,6 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
         max_nsc2 = g.nsc2 > max_nsc2 ? g.nsc2 : max_nsc2;
     }
     batch.first1[count] = stage1;
-    int64_t stage2 = stage1;
-    for (int i = 0; i < count; ++i) {
-        batch.first2[i] = stage2;
-        stage2 += batch.p[i].n2;
-    }
-    batch.first2[count] = stage2;
     return launch_batch(batch, tokens, max_nsc1, max_nsc2, typed, descs[0]->decode_launch == NQ_DECODE_FUSED,
                         stream);
 }

@@ -457,6 +457,26 @@ def test_split_and_fused_launches_are_bit_identical(tokens):
         assert torch.equal(a, b), shape.name
 
 
+def test_fused_launch_alternating_grouping_keeps_launch_index():
+    """The fused launch derives its launch index from monotonic per-tile arrival
+    counters; a layer used alone (one tile per stage-2 workgroup) and inside a
+    large batch (two tiles per workgroup), alternately, must stay exact."""
+
+    split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
+    shapes = syn.qwen3_8b_layer()
+    states = [syn.synthetic_packed_layer(shapes[0], seed=81), syn.synthetic_packed_layer(shapes[4], seed=82)]
+    xs = [syn.synthetic_activations(1, 4096, seed=s, device="cuda") for s in (1, 2)]
+    ref = [split.linear(x, split.prepare(st, "cuda")) for x, st in zip(xs, states)]
+    layers = [fused.prepare(st, "cuda") for st in states]
+    for rep in range(4):
+        _say("alternating grouping", rep)
+        alone = fused.linear(xs[0], layers[0])
+        pair = fused.linear_batch(xs, layers)
+        assert torch.equal(alone, ref[0]), rep
+        assert torch.equal(pair[0], ref[0]) and torch.equal(pair[1], ref[1]), rep
+    assert all(_sync_header_clean(layer) for layer in layers)
+
+
 def test_batch_rejects_mixed_launch_structures():
     state = syn.synthetic_packed_layer(syn.qwen3_8b_layer()[1], seed=3)
     split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
