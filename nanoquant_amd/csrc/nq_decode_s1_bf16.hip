@@ -1,0 +1,33 @@
+// Launcher of the split decode kernel for stage 1 with bf16 x and fp16 scales (instantiations of
+// k_decode_stage<1, kActBf16, ...>; the kernels are documented in
+// nq_decode_kernels.h). One translation unit per activation kind keeps the
+// library build parallel.
+#include "nq_decode_kernels.h"
+
+namespace nqdec {
+namespace {
+
+template <int TPB, int TB, int TW, int KC>
+int go(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
+    constexpr int kThreads = threads_for(TPB, KC);
+    if (64 * s.nw > kThreads) return NQ_ERR_LAUNCH;
+    hipLaunchKernelGGL((k_decode_stage<1, kActBf16, TPB, TB, TW, KC, kThreads>), dim3(s.grid), dim3(64 * s.nw),
+                       s.lds, stream, batch);
+    return nq::launch_status();
+}
+
+template <int TPB>
+int by_tiles(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
+    if (s.tw == 4) return s.kc == 2 ? go<TPB, 1, 4, 2>(batch, s, stream) : go<TPB, 1, 4, 1>(batch, s, stream);
+    return s.kc == 2 ? go<TPB, 1, 1, 2>(batch, s, stream) : go<TPB, 1, 1, 1>(batch, s, stream);
+}
+
+}  // namespace
+
+int enqueue_stage1_bf16(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
+    if (s.tpb == 1) return by_tiles<1>(batch, s, stream);
+    if (s.tb == 1) return by_tiles<4>(batch, s, stream);
+    return go<4, 4, 1, 1>(batch, s, stream);
+}
+
+}  // namespace nqdec

@@ -8,13 +8,19 @@
 //   GEMM 2:       y[t, o]    = s_out[o] * (lm16 · U±1ᵀ)[t, o] / 2^f_t
 //                              + Σ_k x[t, idx_k] W_sal[o, k] (* scale_k) + bias[o]
 //
-// The sign operand comes straight from the decode tile layout (16-row tiles x
-// 128-column superchunks, one word per lane per superchunk, bits in MFMA
-// B-operand order): a wave loads the words of its four 16-row tiles for one
-// superchunk (256 contiguous bytes each), expands them in registers to fp16
-// ±1 (one shift + one and_or per pair) and reuses every expanded operand for
-// its four 16-row M tiles. The activation tile (128 rows x 128 columns fp16)
-// is staged in LDS with a padded row stride and read as ds_read_b128.
+// The sign operand comes straight from the decode tile layout (16-row tiles;
+// in 128-column block kb = 4c + d a lane's word d of chunk c holds, at bit
+// 8b + m, column 128kb + 16m + 4g + b for lane group g). A wave loads the
+// words of its four 16-row tiles for one block and expands them in registers
+// to fp16 ±1: bits 8b + m and 8b + m + 16 (columns +b and +b + 2) become one
+// dword with one shift and one and_or. MFMA p (32 columns 32p..32p+31 of the
+// block) takes the dwords (b, m) = (0, 2p), (1, 2p), (0, 2p+1), (1, 2p+1), so
+// lane group g's eight B values are columns 32p + 4g + [0, 2, 1, 3] and
+// 32p + 16 + 4g + [0, 2, 1, 3]. k_prep_rows stores activation rows with
+// columns 1 and 2 of every group of four swapped, so the matching A operand is
+// two 8-byte LDS reads. Every expanded operand is reused for the wave's four
+// 16-row M tiles. The activation tile (128 rows x 128 columns fp16) is staged
+// in LDS with a padded row stride.
 //
 // Block tile 128 (tokens) x 128 (sign rows), 4 waves in a 2 x 2 grid, each
 // wave 64 x 64 = 4 x 4 MFMA tiles of 16 x 16 accumulated in fp32.
@@ -23,6 +29,7 @@
 namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kBlock = 256;
@@ -46,8 +53,12 @@ __device__ __forceinline__ float range_scale(float bound) {
     return exp2i(e);
 }
 
-// One workgroup per row: out16[t, c] = fp16(a[t, c] * s[c] * scale_t) for
-// c < cols, zero for cols <= c < cols_pad; scale_out[t] = scale_t.
+// Position of column c in a prepared row: columns 1 and 2 of every group of
+// four are swapped (the order the sign operand's fp16 pairs come in).
+__device__ __forceinline__ int64_t swizzle4(int64_t c) { return (c & ~int64_t(3)) | ((c & 1) << 1) | ((c >> 1) & 1); }
+
+// One workgroup per row: out16[t, swizzle4(c)] = fp16(a[t, c] * s[c] * scale_t)
+// for c < cols, zero for cols <= c < cols_pad; scale_out[t] = scale_t.
 __global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ act, int act_dtype, int64_t ld,
                                                       const void* __restrict__ colscale, int colscale_dtype,
                                                       int64_t cols, int64_t cols_pad,
@@ -70,31 +81,33 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ a
             v = nq::load_f32(act, act_dtype, t * ld + c);
             if (colscale) v *= nq::load_f32(colscale, colscale_dtype, c);
         }
-        out16[t * cols_pad + c] = static_cast<_Float16>(v * scale);
+        out16[t * cols_pad + swizzle4(c)] = static_cast<_Float16>(v * scale);
     }
     if (threadIdx.x == 0) scale_out[t] = scale;
 }
 
-__device__ __forceinline__ v8h expand_signs(uint32_t word, int m) {
+// B operand of MFMA p from one word: dwords (b, m) = (0, 2p), (1, 2p),
+// (0, 2p + 1), (1, 2p + 1), each bits 8b + m and 8b + m + 16 moved to the fp16
+// sign positions 15 and 31.
+__device__ __forceinline__ v8h expand_signs(uint32_t word, int p) {
     union {
         uint32_t u[4];
         v8h v;
     } r;
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        const int s = 4 * m + d;
-        r.u[d] = ((word << s) & 0x80008000u) | 0x3C003C00u;
-    }
+    r.u[0] = ((word << (15 - 2 * p)) & 0x80008000u) | 0x3C003C00u;
+    r.u[1] = ((word << (7 - 2 * p)) & 0x80008000u) | 0x3C003C00u;
+    r.u[2] = ((word << (14 - 2 * p)) & 0x80008000u) | 0x3C003C00u;
+    r.u[3] = ((word << (6 - 2 * p)) & 0x80008000u) | 0x3C003C00u;
     return r.v;
 }
 
 struct GemmArgs {
     const _Float16* a;        // [M, kpad] fp16 activations (row-scaled)
     int64_t m;                // tokens
-    int64_t kpad;             // nsc * 128
-    const uint32_t* tiles;    // sign tiles [rt][nsc][64]
+    int64_t kpad;             // nb * 128
+    const uint32_t* tiles;    // sign tiles [rt][nb * 64] (chunked, see above)
     int64_t n;                // sign rows (rank or out)
-    int64_t nsc;
+    int64_t nb;               // 128-column blocks
     const float* row_scale;   // [M]: divide accumulators by this
     const void* col_scale;    // [n] s_mid or s_out
     int col_scale_dtype;
@@ -139,12 +152,17 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
     // Plain locals (not the by-value kernel argument) so the loader stays in registers.
     const uint32_t* const tiles = g.tiles;
     const _Float16* const act = g.a;
-    const int64_t nsc = g.nsc, kpad = g.kpad, mrows = g.m;
+    const int64_t nsc = g.nb, kpad = g.kpad, mrows = g.m;
     auto load_step = [&](int64_t sc) {
+        // Block sc is word d of chunk c; the chunk holds dw words per lane.
+        const int64_t c = sc >> 2;
+        const int d = static_cast<int>(sc & 3);
+        const int64_t rem = nsc - 4 * c;
+        const int dw = static_cast<int>(rem < 4 ? rem : 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int64_t rt = rt0 + j;
-            next_words[j] = rt < rt_count ? tiles[(rt * nsc + sc) * 64 + lane] : 0u;
+            next_words[j] = rt < rt_count ? tiles[rt * nsc * 64 + c * 256 + lane * dw + d] : 0u;
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -174,7 +192,10 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 64 * wm + 16 * i + (lane & 15);
-                const v8h a = *reinterpret_cast<const v8h*>(&a_lds[r * kAStride + 32 * kc + 8 * (lane >> 4)]);
+                const _Float16* ap = &a_lds[r * kAStride + 32 * kc + 4 * (lane >> 4)];
+                const v4h lo = *reinterpret_cast<const v4h*>(ap);
+                const v4h hi = *reinterpret_cast<const v4h*>(ap + 16);
+                const v8h a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], acc[i][j], 0, 0, 0);
             }
@@ -215,6 +236,8 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
     }
 }
 
+// Tile counts and 128-column block counts of V [rank, in] and U [out, rank]
+// (the same geometry as the decode tiles).
 struct Geometry {
     int64_t rt1, nsc1, rt2, nsc2, v_words, u_words;
 };
@@ -286,7 +309,7 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     g1.kpad = geo.nsc1 * kBK;
     g1.tiles = base + header_words;
     g1.n = d->rank;
-    g1.nsc = geo.nsc1;
+    g1.nb = geo.nsc1;
     g1.row_scale = scale1;
     g1.col_scale = d->scale_mid;
     g1.col_scale_dtype = d->scale_dtype;
@@ -303,7 +326,7 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     g2.kpad = geo.nsc2 * kBK;
     g2.tiles = base + header_words + geo.v_words;
     g2.n = d->out_features;
-    g2.nsc = geo.nsc2;
+    g2.nb = geo.nsc2;
     g2.row_scale = scale2;
     g2.col_scale = d->scale_post;
     g2.col_scale_dtype = d->scale_dtype;

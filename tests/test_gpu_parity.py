@@ -1,8 +1,9 @@
 """HIP parity against the CPU oracle (run on an MI355X: ``pytest -m gpu``).
 
-Bar: bit-exact for unpacked signs; fp outputs within the reference tests'
-``rtol=2e-5, atol=2e-4`` on the small fixtures and within relative L2 2e-3 of
-the oracle's fp32 forward at the benchmark shapes; bit-exact replay.
+Bar: bit-exact for unpacked signs and the GPU tile layout; fp outputs within
+the reference tests' ``rtol=2e-5, atol=2e-4`` on the small fixtures (general
+fp32 path) and within relative L2 2e-3 of the oracle's fp32 forward for the
+tiled MFMA paths; bit-exact replay.
 """
 
 from __future__ import annotations
@@ -33,6 +34,8 @@ from nanoquant_amd.runtime import (
 )
 from nanoquant_amd.runtime import _native
 from oracle import nq_oracle as orc
+
+from tile_layout import build_tiles, geometry as tile_geometry
 
 pytestmark = [
     pytest.mark.gpu,
@@ -65,8 +68,9 @@ def _tiled(backend) -> bool:
 
 
 def _assert_parity(backend, actual, expected, case=None):
-    """fp32 path: the reference tests' rtol=2e-5/atol=2e-4. fp16-MFMA tiled
-    path: the north-star bar, relative L2 <= 2e-3 against the fp32 forward."""
+    """fp32 path: the reference tests' rtol=2e-5/atol=2e-4. Tiled MFMA paths
+    (int8 decode, fp16 prefill): the north-star bar, relative L2 <= 2e-3
+    against the fp32 forward."""
 
     if _tiled(backend):
         err = orc.relative_l2(actual, expected)
@@ -86,12 +90,35 @@ def _sync_header_clean(layer) -> bool:
     torch.cuda.synchronize()
     size = int(_native.load().nq_tiles_header_bytes())
     misc = tiles[:size].view(torch.int32).cpu()[-64:]
-    return int(misc[0]) == 0 and int(misc[1]) == 0x4E515432
+    return int(misc[0]) == 0 and int(misc[1]) == 0x4E515433
 
 
 def _run(backend, state, x):
     layer = backend.prepare(state, "cuda")
     return backend.linear(x.cuda(), layer), layer
+
+
+# --- tile layout ---------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("inp,out,rank", [(128, 16, 16), (819, 33, 100), (4096, 1024, 819), (1152, 6912, 768),
+                                         (12288, 40, 3072), (5, 3, 7)])
+def test_prepared_tiles_match_layout(inp, out, rank):
+    """nq_prepare_tiles writes V and U in the documented layout, word for word."""
+
+    _say("tiles", inp, out, rank)
+    shape = syn.LinearShape("t", inp, out, rank)
+    state = syn.synthetic_packed_layer(shape, seed=11)
+    layer = HipPackedBackend().prepare(state, "cuda")
+    torch.cuda.synchronize()
+    header = int(_native.load().nq_tiles_header_bytes()) // 4
+    words = layer.payload.tiles.view(torch.int32).cpu().numpy().view(np.uint32)
+    nt1, nb1, _ = tile_geometry(rank, inp)
+    nt2, nb2, _ = tile_geometry(out, rank)
+    v = words[header:header + nt1 * nb1 * 64]
+    u = words[header + nt1 * nb1 * 64:header + nt1 * nb1 * 64 + nt2 * nb2 * 64]
+    np.testing.assert_array_equal(v, build_tiles(state.right_words.numpy(), rank, inp))
+    np.testing.assert_array_equal(u, build_tiles(state.left_words.numpy(), out, rank))
 
 
 # --- unpack ------------------------------------------------------------------------
