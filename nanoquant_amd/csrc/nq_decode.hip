@@ -41,16 +41,34 @@ __global__ __launch_bounds__(256) void k_build_tiles(const uint32_t* __restrict_
     }
 }
 
-__global__ void k_init_header(uint32_t* header) {
+// Zero the header, write the magic and max|s_mid| (the stage-1 epilogue's
+// bound on the rank intermediate). One workgroup of 256 threads.
+__global__ __launch_bounds__(256) void k_init_header(uint32_t* header, const void* s_mid, int scale_dtype,
+                                                     int64_t rank) {
+    __shared__ float wmax[4];
     for (int i = threadIdx.x; i < kHeaderWords; i += blockDim.x) header[i] = 0;
+    float m = 0.0f;
+    for (int64_t r = threadIdx.x; r < rank; r += blockDim.x) m = fmaxf(m, fabsf(nq::load_f32(s_mid, scale_dtype, r)));
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
     __syncthreads();
-    if (threadIdx.x == 0) header[line_word(kMiscLine) + kMiscMagic] = kTilesMagic;
+    if (threadIdx.x == 0) {
+        header[line_word(kMiscLine) + kMiscMagic] = kTilesMagic;
+        header[line_word(kMiscLine) + kMiscMaxMid] =
+            __float_as_uint(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+    }
 }
 
 struct TilesGeometry {
     MatGeo g1, g2;
     int64_t v_words, u_words;
 };
+
+// Tail padding after the U tiles: a partial chunk's 16-byte word load reads up
+// to three words past its lane's own (see load_words).
+constexpr int64_t kTailBytes = 256;
+
+int64_t tiles_bytes_of(const TilesGeometry& g) { return (kHeaderWords + g.v_words + g.u_words) * 4 + kTailBytes; }
 
 TilesGeometry geometry(int64_t in, int64_t out, int64_t rank) {
     TilesGeometry g{};
@@ -61,10 +79,15 @@ TilesGeometry geometry(int64_t in, int64_t out, int64_t rank) {
     return g;
 }
 
-int64_t lm_ld_of(const TilesGeometry& g) { return g.g2.nb * kBlockCols; }
+// Decode workspace: [stage-2 operands (lmq)][per-token exponents (lme)].
+int64_t lmq_bytes_for(const MatGeo& g2, int64_t tokens) {
+    if (tokens == 1) return lmq_bytes<1, 1>(g2);
+    if (tokens <= 4) return lmq_bytes<4, 1>(g2);
+    return lmq_bytes<4, 4>(g2);
+}
 
 int64_t scratch_bytes(const TilesGeometry& g, int64_t tokens) {
-    return (tokens * lm_ld_of(g) * 4 + 255) & ~int64_t(255);
+    return ((lmq_bytes_for(g.g2, tokens) + 255) & ~int64_t(255)) + 256;
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -75,7 +98,7 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
              void* scratch, LinArgs& a, bool& vector_ok) {
     const TilesGeometry g = geometry(d->in_features, d->out_features, d->rank);
     if (!d->tiles) return NQ_ERR_ARGUMENT;
-    if (d->tiles_bytes < (kHeaderWords + g.v_words + g.u_words) * 4) return NQ_ERR_ARGUMENT;
+    if (d->tiles_bytes < tiles_bytes_of(g)) return NQ_ERR_ARGUMENT;
     if (!aligned(d->tiles, 16) || !aligned(scratch, 16)) return NQ_ERR_ALIGNMENT;
     a = LinArgs{};
     a.in = d->in_features;
@@ -108,8 +131,8 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
     a.bias_dtype = d->bias_dtype;
     a.y = y;
     a.y_dtype = y_dtype;
-    a.lm = static_cast<float*>(scratch);
-    a.lm_ld = lm_ld_of(g);
+    a.lmq = static_cast<uint8_t*>(scratch);
+    a.lme = reinterpret_cast<int*>(static_cast<char*>(scratch) + ((lmq_bytes_for(g.g2, tokens) + 255) & ~int64_t(255)));
     return NQ_OK;
 }
 
@@ -134,8 +157,12 @@ void pick_waves(int64_t nc, int tpb, int tb, int& nw, int& kc) {
     }
 }
 
-size_t lds_bytes(int tpb, int tb, int tw, int nw, int64_t nc) {
-    return static_cast<size_t>(nw) * (8 * 4 * tpb * 4 * 16) + static_cast<size_t>(nc) * tw * tb * 64 * 4;
+// Dynamic LDS of a stage: per-wave operand areas (stage 1 only), the partial
+// sums [nc][tw][tb][64] and the chunk maxima [nc][tpb * tb] (stage 1 only).
+size_t lds_bytes(int stage, int tpb, int tb, int tw, int nw, int64_t nc) {
+    const size_t red = static_cast<size_t>(nc) * tw * tb * 64 * 4;
+    if (stage == 2) return red;
+    return static_cast<size_t>(nw) * (8 * 4 * tpb * 4 * 16) + red + static_cast<size_t>(nc) * tpb * tb * 4;
 }
 
 // Tiles per workgroup: four when one tile per workgroup would need more waves
@@ -185,33 +212,31 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
     }
     batch.tw1 = s1.tw;
     batch.tw2 = fused ? 1 : s2.tw;
-    int64_t n1 = 0;
+    int64_t max1 = 0, max2 = 0;
     for (int i = 0; i < batch.count; ++i) {
-        batch.first1[i] = n1;
-        n1 += (batch.p[i].g1.nt + batch.tw1 - 1) / batch.tw1;
+        LinArgs& a = batch.p[i];
+        a.nw1 = s1.nw;
+        a.nw2 = fused ? s1.nw : s2.nw;
+        a.nwg1 = (a.g1.nt + batch.tw1 - 1) / batch.tw1;
+        a.nwg2 = (a.g2.nt + batch.tw2 - 1) / batch.tw2;
+        max1 = a.nwg1 > max1 ? a.nwg1 : max1;
+        max2 = a.nwg2 > max2 ? a.nwg2 : max2;
     }
-    batch.first1[batch.count] = n1;
-    int64_t n2 = n1;
-    for (int i = 0; i < batch.count; ++i) {
-        batch.first2[i] = n2;
-        n2 += (batch.p[i].g2.nt + batch.tw2 - 1) / batch.tw2;
-    }
-    batch.first2[batch.count] = n2;
-    if (n2 <= 0 || n2 > 0x7fffffff) return NQ_ERR_SHAPE;
+    if (max1 > 0x7fffffff || max2 > 0x7fffffff) return NQ_ERR_SHAPE;
+    const unsigned count = static_cast<unsigned>(batch.count);
 
     if (fused) {
-        const size_t l1 = lds_bytes(s1.tpb, s1.tb, 1, s1.nw, nc1), l2 = lds_bytes(s1.tpb, s1.tb, 1, s1.nw, nc2);
+        const size_t l1 = lds_bytes(1, s1.tpb, s1.tb, 1, s1.nw, nc1), l2 = lds_bytes(2, s1.tpb, s1.tb, 1, s1.nw, nc2);
         s1.lds = l1 > l2 ? l1 : l2;
-        s1.grid = static_cast<unsigned>(n2);
+        s1.grid = dim3(static_cast<unsigned>(max1 > max2 ? max1 : max2), 2 * count);
         return enqueue_fused(batch, s1, stream);
     }
-    s1.lds = lds_bytes(s1.tpb, s1.tb, s1.tw, s1.nw, nc1);
-    s1.grid = static_cast<unsigned>(n1);
+    s1.lds = lds_bytes(1, s1.tpb, s1.tb, s1.tw, s1.nw, nc1);
+    s1.grid = dim3(static_cast<unsigned>(max1), count);
     int st = enqueue_stage1(batch, s1, stream);
     if (st != NQ_OK) return st;
-    s2.ak = kActLm;
-    s2.lds = lds_bytes(s2.tpb, s2.tb, s2.tw, s2.nw, nc2);
-    s2.grid = static_cast<unsigned>(n2 - n1);
+    s2.lds = lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, nc2);
+    s2.grid = dim3(static_cast<unsigned>(max2), count);
     return enqueue_stage2(batch, s2, stream);
 }
 
@@ -265,20 +290,19 @@ extern "C" int64_t nq_tiles_header_bytes(void) { return static_cast<int64_t>(kHe
 
 extern "C" int64_t nq_tiles_bytes(int64_t in_features, int64_t out_features, int64_t rank) {
     if (in_features <= 0 || out_features <= 0 || rank <= 0) return -1;
-    const TilesGeometry g = geometry(in_features, out_features, rank);
-    return (kHeaderWords + g.v_words + g.u_words) * 4;
+    return tiles_bytes_of(geometry(in_features, out_features, rank));
 }
 
 extern "C" int nq_prepare_tiles(const nq_linear_desc* d, void* tiles, int64_t tiles_bytes, void* stream) {
-    if (!d || !tiles || !d->right_words || !d->left_words || !d->scale_pre) return NQ_ERR_ARGUMENT;
+    if (!d || !tiles || !d->right_words || !d->left_words || !d->scale_pre || !d->scale_mid) return NQ_ERR_ARGUMENT;
     if (d->in_features <= 0 || d->out_features <= 0 || d->rank <= 0) return NQ_ERR_SHAPE;
     if (!nq::is_float_dtype(d->scale_dtype)) return NQ_ERR_DTYPE;
     const TilesGeometry g = geometry(d->in_features, d->out_features, d->rank);
-    if (tiles_bytes < (kHeaderWords + g.v_words + g.u_words) * 4) return NQ_ERR_WORKSPACE;
+    if (tiles_bytes < tiles_bytes_of(g)) return NQ_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(tiles) % 256 != 0) return NQ_ERR_ALIGNMENT;
     auto s = static_cast<hipStream_t>(stream);
     uint32_t* base = static_cast<uint32_t*>(tiles);
-    hipLaunchKernelGGL(k_init_header, dim3(1), dim3(256), 0, s, base);
+    hipLaunchKernelGGL(k_init_header, dim3(1), dim3(256), 0, s, base, d->scale_mid, d->scale_dtype, d->rank);
     auto grid_for = [](int64_t n) {
         const int64_t b = (n + 255) / 256;
         return static_cast<unsigned>(b < 16384 ? (b > 0 ? b : 1) : 16384);

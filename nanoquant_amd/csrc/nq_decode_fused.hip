@@ -9,7 +9,7 @@ template <int TPB, int TB, int KC1, int KC2>
 int go(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     constexpr int kThreads = threads_for(TPB, KC1 > KC2 ? KC1 : KC2);
     if (64 * s.nw > kThreads) return NQ_ERR_LAUNCH;
-    hipLaunchKernelGGL((k_decode_fused<TPB, TB, KC1, KC2, kThreads>), dim3(s.grid), dim3(64 * s.nw), s.lds, stream,
+    hipLaunchKernelGGL((k_decode_fused<TPB, TB, KC1, KC2, kThreads>), s.grid, dim3(64 * s.nw), s.lds, stream,
                        batch);
     return nq::launch_status();
 }

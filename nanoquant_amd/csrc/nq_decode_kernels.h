@@ -5,7 +5,7 @@
 //   y[t, o]  = s_out[o] * Σ_r sgn(U[o, r]) * lm[t, r] + salient + bias    (stage 2)
 //
 // Both stages are the same contraction: rows R of a sign matrix [R, K] against
-// an activation a[t, k]. They run on v_mfma_i32_16x16x64_i8 with exact integer
+// an activation a[t, k], on v_mfma_i32_16x16x64_i8 with exact integer
 // arithmetic from the bits to the per-chunk fp32 partial.
 //
 // Weight layout ("tiles", built once by nq_prepare_tiles). A sign matrix
@@ -19,54 +19,60 @@
 //
 // Sign expansion is one v_and_b32 per four signs: word_d & (0x01010101 << m)
 // is four int8 values in {0, 2^m} (m = 7 gives {0, -128}), the B operand dword
-// d of MFMA m. The bits are used as b in {0, 1} with sgn = 1 - 2b, so
-//     Σ_k sgn_k a_k = Σ_k a_k - 2 Σ_k b_k a_k .
-// Activations (per chunk, per token) are rounded to x_q = rint(a * 2^E) with
-// the chunk's own exact power of two E (max |x_q| <= 2^15), then the value fed
-// to MFMA m is w = x_q * 2^(7-m) (w = -x_q for m = 7), written as three signed
-// int8 digits w = d0 + 256*d1 + 65536*d2 in A rows 4*t + {0, 1, 2}. Every
-// product is then 2^7 * b * x_q whatever m is, so the eight MFMAs of a chunk
-// accumulate into one int32 accumulator and
-//     Σ_k b_k x_q,k = (D0 + 256*D1 + 65536*D2) / 2^7    (D = digit rows of D)
-//     chunk partial = 2^-E * (Σ_k x_q,k - (D0 + 256*D1 + 65536*D2) / 64).
-// The only rounding before fp32 is x_q itself (|x_q| <= 2^15). Chunk partials
-// are summed in chunk order, so the result is the same for every launch shape
-// (waves per workgroup, tiles per workgroup, split or fused launch).
+// d of MFMA m; the bits are b in {0, 1} with sgn = 1 - 2b.
 //
-// Staging (per wave, per chunk, per block of up to 4 tokens): lane L loads
-// the 8 activations of (m, g, dp) = (L >> 3, (L >> 1) & 3, L & 1), namely the
-// runs 512c + 256dp + 16m + 4g + {0..3} and the same + 128, scales them, takes
-// the wave max and sum, and writes its 8 digit bytes per digit row into the
-// wave's LDS operand area A[m][row][g][16 bytes] with one 8-byte store; each
-// lane then reads its eight A operands (one 16-byte LDS read per MFMA).
+// Activation operands. An activation a is held as an integer x_q = rint(a*2^E)
+// with a power of two E shared by a chunk; MFMA m receives w = x_q * 2^(7-m)
+// (w = -x_q for m = 7) as signed int8 digits w = Σ_j 256^j d_j in A rows
+// 4*t + j. Every product with B is then 2^7 * b * x_q whatever m is, so the
+// eight MFMAs of a chunk share one int32 accumulator T (per digit row), and
+// eight more MFMAs against B = 0x01010101 << m give S = 2^7 * Σ x_q. Then
+//     Σ_k sgn_k x_q,k = (S - 2T) / 2^7,   combined over digit rows as
+//     Σ_j 256^j (S_j - 2 T_j)   (each S_j - 2 T_j exact in int32),
+//     chunk partial = 2^-E * 2^-7 * Σ_j 256^j (S_j - 2 T_j).
+// The only rounding before fp32 is x_q itself.
+//   Stage 1 stages x * s_in per (wave, chunk, block of up to 4 tokens): lane L
+//     takes the 8 columns of (m, g, dp) = (L >> 3, (L >> 1) & 3, L & 1), i.e.
+//     512c + 256dp + 16m + 4g + {0..3} and the same + 128, the wave max gives
+//     E (|x_q| <= 2^15, three digits), and each lane writes its 8 digit bytes
+//     per digit row into the wave's LDS area A[m][row][g][16 B]; each lane then
+//     reads its eight A operands (one 16-byte LDS read per MFMA).
+//   Stage 2 does no staging: stage 1's epilogue writes lm straight into the
+//     stage-2 operand layout in global memory (four digits, |x_q| <= 2^22)
+//     with one exponent per token from a bound every stage-1 workgroup
+//     computes identically, |lm| <= max|s_mid| * Σ_chunks 512 * max_chunk|x
+//     s_in|; stage 2 loads each A operand with one 16-byte load.
+// Chunk partials are summed in chunk order, so the result is the same for
+// every launch shape (waves or tiles per workgroup, split or fused launch).
 //
 // Workgroup: NW waves; wave w takes chunks w, w + NW, ... of TW consecutive
 // tiles, so one staged chunk feeds TW tiles. Per (chunk, tile) the wave stores
 // its fp32 partial in LDS; after one barrier each output sums its partials in
-// chunk order and the epilogue applies s_mid (stage 1, writes lm) or s_out +
-// salient + bias (stage 2).
+// chunk order and the epilogue applies s_mid (stage 1) or s_out + salient +
+// bias (stage 2). The grid is two-dimensional (blockIdx.y = batch member), so
+// a workgroup needs one round trip to its kernel arguments.
 //
 // Latency: every load of a pass (activations, then sign words; in the fused
 // stage 2 the words before the wait) is issued from straight-line code before
 // any of it is used: no branch surrounds a load (addresses are clamped, dead
 // chunks reload a valid chunk and skip only the arithmetic, the wave index is
 // made uniform with readfirstlane), so the compiler never waits on one load to
-// issue the next. The activation dtype pair is a template parameter
+// issue the next. The stage-1 activation dtype pair is a template parameter
 // (bf16 / f16 / f32 x with fp16 scales as vector loads); any other
 // combination, and unaligned buffers, take a generic variant whose element
 // loads are two unconditional 16-bit loads decoded by a uniform select.
 //
 // Launch structure (nq_linear_desc.decode_launch):
 //   split (default): kernel 1 runs the stage-1 tiles of every linear in the
-//     batch and stores lm; kernel 2 runs the stage-2 tiles. The kernel
+//     batch and writes the stage-2 operands; kernel 2 runs the stage-2 tiles. The kernel
 //     boundary is the grid-wide barrier.
-//   fused: one kernel whose first workgroups are the stage-1 tiles and the
-//     rest the stage-2 tiles. Stage-1 workgroups store lm at agent scope and
-//     then signal; stage-2 workgroups issue their U loads, wait for their
-//     linear's signal (bounded spin) and only then load lm. Workgroups are
-//     dispatched in index order, so every stage-1 workgroup is resident or
-//     finished before a stage-2 workgroup can take its slot, and stage-1
-//     workgroups never wait.
+//   fused: one kernel whose first grid rows are the stage-1 workgroups and
+//     the rest the stage-2 workgroups. Stage-1 workgroups store the operands
+//     at agent scope and then signal; stage-2 workgroups issue their U loads,
+//     wait for their linear's signal (bounded spin) and only then load the
+//     operands. Workgroups are dispatched in linear index order, so every
+//     stage-1 workgroup is resident or finished before a stage-2 workgroup
+//     can take its slot, and stage-1 workgroups never wait.
 // Measured on MI355X, a graph-launched kernel boundary (about 1.5 us) is
 // cheaper than any grid-wide handoff inside a kernel (3 us or more across the
 // eight XCDs), hence split is the default.
@@ -118,7 +124,7 @@ constexpr int kMiscLine = kReplica0 + kReplicas;
 constexpr int kHeaderLines = kMiscLine + 1;
 constexpr int kHeaderWords = kHeaderLines * kLine;
 // Words on the misc line.
-enum : int { kMiscError = 0, kMiscMagic = 1 };
+enum : int { kMiscError = 0, kMiscMagic = 1, kMiscMaxMid = 2 };
 
 __host__ __device__ constexpr int line_word(int line) { return line * kLine; }
 
@@ -152,6 +158,7 @@ __host__ __device__ inline int chunk_words(const MatGeo& g, int64_t c) {
 struct LinArgs {
     int64_t in, rank, out;
     MatGeo g1, g2;           // V [rank, in], U [out, rank]
+    int64_t nwg1, nwg2;      // workgroups of each stage (tiles / tiles per workgroup)
     const uint32_t* v_tiles;
     const uint32_t* u_tiles;
     uint32_t* header;
@@ -171,37 +178,104 @@ struct LinArgs {
     int bias_dtype;
     void* y;
     int y_dtype;
-    float* lm;               // [tokens][lm_ld]; entries past `rank` are never read
-    int64_t lm_ld;           // 128 * g2.nb
+    uint8_t* lmq;            // stage-2 A operands, see lmq_offset
+    int* lme;                // [tokens] exponent of lmq per token
+    int nw1, nw2;            // waves per workgroup of each stage (the fused launch: both equal)
 };
+static_assert(sizeof(LinArgs) % 16 == 0, "LinArgs is read as 16-byte vectors");
 
 struct Batch {
     int count;
-    int tw1, tw2;                    // tiles per workgroup of each stage
-    int64_t first1[kMaxBatch + 1];   // stage-1 workgroup prefix per linear
-    int64_t first2[kMaxBatch + 1];   // stage-2 workgroup prefix (after all stage-1)
+    int tw1, tw2;            // tiles per workgroup of each stage
+    int pad_;
     LinArgs p[kMaxBatch];
 };
 
-// Activation kinds (template parameter AK): how a stage reads a[t, k].
+// A member's arguments, copied field by field from the kernel-argument segment
+// with every field then used by an empty asm: all the scalar loads are issued
+// together and complete at one point, instead of lazily (one dependent round
+// trip per uniform branch that needs a field). The copies stay typed loads, so
+// the pointers are still known to be global.
+__device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
+    const LinArgs& s = batch.p[member];
+    LinArgs a;
+    a.in = s.in;
+    a.rank = s.rank;
+    a.out = s.out;
+    a.g1 = s.g1;
+    a.g2 = s.g2;
+    a.nwg1 = s.nwg1;
+    a.nwg2 = s.nwg2;
+    a.v_tiles = s.v_tiles;
+    a.u_tiles = s.u_tiles;
+    a.header = s.header;
+    a.x = s.x;
+    a.x_dtype = s.x_dtype;
+    a.tokens = s.tokens;
+    a.s_in = s.s_in;
+    a.s_mid = s.s_mid;
+    a.s_out = s.s_out;
+    a.scale_dtype = s.scale_dtype;
+    a.salient_count = s.salient_count;
+    a.salient_indices = s.salient_indices;
+    a.salient_values = s.salient_values;
+    a.salient_dtype = s.salient_dtype;
+    a.salient_scales = s.salient_scales;
+    a.bias = s.bias;
+    a.bias_dtype = s.bias_dtype;
+    a.y = s.y;
+    a.y_dtype = s.y_dtype;
+    a.lmq = s.lmq;
+    a.lme = s.lme;
+    a.nw1 = s.nw1;
+    a.nw2 = s.nw2;
+    // One statement, so every field is waited for at the same point; it
+    // redefines the integer fields, so no arithmetic on them can be hoisted
+    // above it (the pointers are only read, so they stay known-global).
+    asm volatile(""
+                 : "+s"(a.in), "+s"(a.rank), "+s"(a.out), "+s"(a.g1.nt), "+s"(a.g1.nb), "+s"(a.g1.nc),
+                   "+s"(a.g2.nt), "+s"(a.g2.nb), "+s"(a.g2.nc), "+s"(a.nwg1), "+s"(a.nwg2), "+s"(a.x_dtype),
+                   "+s"(a.tokens), "+s"(a.scale_dtype), "+s"(a.bias_dtype), "+s"(a.nw1), "+s"(a.nw2)
+                 : "s"(a.v_tiles), "s"(a.u_tiles), "s"(a.header), "s"(a.x), "s"(a.s_in), "s"(a.s_mid), "s"(a.s_out),
+                   "s"(a.bias), "s"(a.lmq), "s"(a.lme));
+    return a;
+}
+// Activation kinds (template parameter AK): how stage 1 reads a[t, k].
 enum : int {
-    kActBf16 = 0,     // stage 1: bf16 x, fp16 s_in, vector loads
-    kActF16 = 1,      // stage 1: fp16 x, fp16 s_in, vector loads
-    kActF32 = 2,      // stage 1: fp32 x, fp16 s_in, vector loads
-    kActGeneric = 3,  // stage 1: any float x and s_in, element loads
-    kActLm = 4,       // stage 2: fp32 lm, no column scale, vector loads
+    kActBf16 = 0,     // bf16 x, fp16 s_in, vector loads
+    kActF16 = 1,      // fp16 x, fp16 s_in, vector loads
+    kActF32 = 2,      // fp32 x, fp16 s_in, vector loads
+    kActGeneric = 3,  // any float x and s_in, element loads
 };
+
+// Rows of an A operand block: 4 digit rows for each of TPB tokens.
+template <int TPB>
+struct Ops {
+    static constexpr int kRows = 4 * TPB;
+    static constexpr int kBytes = 8 * kRows * 4 * 16;  // A[m][row][g][16 B]
+};
+
+// Byte offset of (chunk c, token block tb, MFMA m, row, lane group g) in the
+// stage-2 operand buffer; byte j of the 16 is column 512c + 128*(j/4) + 16m +
+// 4g + j%4.
+template <int TPB, int TB>
+__host__ __device__ inline int64_t lmq_offset(int64_t c, int tb, int m, int row, int g) {
+    return ((((c * TB + tb) * 8 + m) * Ops<TPB>::kRows + row) * 4 + g) * 16;
+}
+
+template <int TPB, int TB>
+__host__ __device__ inline int64_t lmq_bytes(const MatGeo& g2) { return g2.nc * TB * Ops<TPB>::kBytes; }
 
 // 2^e for an integer e in the fp32 normal range.
 __device__ __forceinline__ float exp2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
 
-// Exponent E with bound * 2^E < 2^15 (so |rint(a * 2^E)| <= 2^15 for |a| <=
-// bound); 0 when the bound is zero or not finite-positive.
-__device__ __forceinline__ int chunk_exponent(float bound) {
+// Exponent E with bound * 2^E < 2^(top + 1), clamped to [-113, 119] (so 2^-E-7
+// stays a normal fp32); 0 when the bound is zero or not finite-positive.
+__device__ __forceinline__ int range_exponent(float bound, int top) {
     if (!(bound > 0.0f)) return 0;
     int e = static_cast<int>((__float_as_uint(bound) >> 23) & 0xff) - 127;
-    e = 14 - (e < -126 ? -126 : e);
-    return e > 120 ? 120 : (e < -113 ? -113 : e);
+    e = top - (e < -126 ? -126 : e);
+    return e > 119 ? 119 : (e < -113 ? -113 : e);
 }
 
 template <int CTRL>
@@ -210,12 +284,7 @@ __device__ __forceinline__ float dpp_maxf(float x) {
     return fmaxf(x, __int_as_float(y));
 }
 
-template <int CTRL>
-__device__ __forceinline__ int dpp_addi(int x) {
-    return x + __builtin_amdgcn_update_dpp(0, x, CTRL, 0xf, 0xf, false);
-}
-
-// Max / sum over the whole wave (every lane gets the result, as a uniform value).
+// Max over the whole wave (every lane gets the result, as a uniform value).
 __device__ __forceinline__ float wave_max(float v) {
     v = dpp_maxf<0xB1>(v);   // quad_perm [1,0,3,2]
     v = dpp_maxf<0x4E>(v);   // quad_perm [2,3,0,1]
@@ -226,15 +295,6 @@ __device__ __forceinline__ float wave_max(float v) {
     const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
     const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
-}
-
-__device__ __forceinline__ int wave_sum(int v) {
-    v = dpp_addi<0xB1>(v);
-    v = dpp_addi<0x4E>(v);
-    v = dpp_addi<0x141>(v);
-    v = dpp_addi<0x140>(v);
-    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
-           __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
 }
 
 // --- branch-free element loads of a runtime float dtype ------------------------
@@ -266,7 +326,7 @@ __device__ __forceinline__ float elem_value(const RawElem& r, int dtype) {
     return dtype == NQ_DTYPE_F32 ? f32 : (dtype == NQ_DTYPE_BF16 ? bf16 : f16);
 }
 
-// --- activation runs: 4 consecutive columns -------------------------------------
+// --- stage-1 activation runs: 4 consecutive columns -----------------------------
 
 // Raw registers of one run for kind AK: fp16/bf16 pairs in two dwords, fp32 in
 // four, generic as four raw elements.
@@ -278,24 +338,23 @@ struct Run {
 };
 
 // Columns [k, k + 4) of row `row` of a buffer with leading dimension ld,
-// loaded from an address clamped to rows_valid rows and `clamp` columns
-// (vector kinds: k % 4 == 0, clamp % 4 == 0, clamp >= 4, ld % 4 == 0 and an
-// aligned base, checked by the host; generic: each element clamped to
-// cols_valid). Values past the valid range are zeroed when staged.
+// loaded from an address clamped to rows_valid rows and `cols` columns
+// (vector kinds: k % 4 == 0, cols % 4 == 0, cols >= 4, ld % 4 == 0 and an
+// aligned base, checked by the host; generic: each element clamped). Values
+// past the valid range are zeroed when staged.
 template <int AK, int DT>
 __device__ __forceinline__ Run<AK> load_run(const void* __restrict__ p, int rt_dtype, int64_t row,
-                                            int64_t rows_valid, int64_t ld, int64_t k, int64_t cols_valid,
-                                            int64_t clamp) {
+                                            int64_t rows_valid, int64_t ld, int64_t k, int64_t cols) {
     Run<AK> r;
     const int64_t rr = row < rows_valid ? row : rows_valid - 1;
     if constexpr (AK == kActGeneric) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int64_t kk = k + i < cols_valid ? k + i : cols_valid - 1;
+            const int64_t kk = k + i < cols ? k + i : cols - 1;
             r.e[i] = load_elem(p, rt_dtype, rr * ld + kk);
         }
     } else {
-        const int64_t kk = k < clamp ? k : clamp - 4;
+        const int64_t kk = k < cols ? k : cols - 4;
         if constexpr (DT == NQ_DTYPE_F32) {
             const v4u q = *reinterpret_cast<const v4u*>(static_cast<const float*>(p) + rr * ld + kk);
 #pragma unroll
@@ -338,124 +397,74 @@ __device__ __forceinline__ void run_values(const Run<AK>& r, int rt_dtype, float
     }
 }
 
-// Storage dtype of the activation and of the column scale for each kind.
 template <int AK>
 constexpr int act_dtype() {
     return AK == kActBf16 ? NQ_DTYPE_BF16 : (AK == kActF16 ? NQ_DTYPE_F16 : NQ_DTYPE_F32);
 }
 constexpr int kScaleDtype = NQ_DTYPE_F16;  // column scale of the vector kinds
 
-// What one stage reads and writes.
-struct StageView {
-    int64_t rows, cols;
-    MatGeo g;
-    const uint32_t* tiles;
-    const void* act;      // [tokens][act_ld]
-    int act_dtype;        // runtime dtype (generic kind)
-    int64_t act_ld;
-    int64_t act_clamp;    // vector loads stay below this column
-    const void* colscale; // s_in (stage 1) or null
-    int colscale_dtype;
-    const void* rowscale; // s_mid / s_out
-};
-
-template <int STAGE>
-__device__ __forceinline__ StageView stage_view(const LinArgs& a) {
-    StageView v;
-    if (STAGE == 1) {
-        v.rows = a.rank;
-        v.cols = a.in;
-        v.g = a.g1;
-        v.tiles = a.v_tiles;
-        v.act = a.x;
-        v.act_dtype = a.x_dtype;
-        v.act_ld = a.in;
-        v.act_clamp = a.in;
-        v.colscale = a.s_in;
-        v.colscale_dtype = a.scale_dtype;
-        v.rowscale = a.s_mid;
-    } else {
-        v.rows = a.out;
-        v.cols = a.rank;
-        v.g = a.g2;
-        v.tiles = a.u_tiles;
-        v.act = a.lm;
-        v.act_dtype = NQ_DTYPE_F32;
-        v.act_ld = a.lm_ld;
-        v.act_clamp = a.lm_ld;  // the last chunk's runs may reach past lm_ld: clamped, then masked
-        v.colscale = nullptr;
-        v.colscale_dtype = 0;
-        v.rowscale = a.s_out;
-    }
-    return v;
-}
-
-// Rows of the LDS operand area per token block: 4 digit rows per token.
-template <int TPB>
-struct Ops {
-    static constexpr int kRows = 4 * TPB;
-    static constexpr int kWaveBytes = 8 * kRows * 4 * 16;  // A[m][row][g][16 B]
-};
-
-// Registers one wave holds for one chunk: activation runs of every token and
-// the column-scale runs, plus the sign words of its TW tiles.
-template <int AK, int TOK, int TW>
-struct ChunkRegs {
-    Run<AK> x[TOK][2];
-    Run<AK> s[AK == kActLm ? 1 : 2];
-    v4u w[TW];
-};
-
 // Staging lane roles: lane L stages (m, g, dp) = (L >> 3, (L >> 1) & 3, L & 1),
-// i.e. columns k0 + {0..3} and k0 + 128 + {0..3} of the chunk.
+// i.e. columns k0 + {0..3} and k0 + 128 + {0..3} of chunk c.
 __device__ __forceinline__ int64_t stage_col0(int64_t c, int lane) {
     return kChunkCols * c + 2 * kBlockCols * (lane & 1) + 16 * (lane >> 3) + 4 * ((lane >> 1) & 3);
 }
 
-// Issue the activation loads of chunk c (tokens [0, TOK)).
+// Registers one stage-1 wave holds for one chunk: the activation runs of every
+// token, the s_in runs and the sign words of its TW tiles.
 template <int AK, int TOK, int TW>
-__device__ __forceinline__ void load_chunk_acts(ChunkRegs<AK, TOK, TW>& r, const StageView& v, int tokens,
-                                                int64_t c, int lane) {
+struct S1Regs {
+    Run<AK> x[TOK][2];
+    Run<AK> s[2];
+    v4u w[TW];
+};
+
+// Registers one stage-2 wave holds for one chunk: its A operands (8 per token
+// block) and the sign words of its TW tiles.
+template <int TB, int TW>
+struct S2Regs {
+    v4i a[TB][8];
+    v4u w[TW];
+};
+
+template <int AK, int TOK, int TW>
+__device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const LinArgs& a, int64_t c, int lane) {
     constexpr int DT = act_dtype<AK>();
     const int64_t k0 = stage_col0(c, lane);
 #pragma unroll
     for (int t = 0; t < TOK; ++t)
 #pragma unroll
         for (int run = 0; run < 2; ++run)
-            r.x[t][run] = load_run<AK, DT>(v.act, v.act_dtype, t, tokens, v.act_ld, k0 + kBlockCols * run, v.cols,
-                                           v.act_clamp);
-    if constexpr (AK != kActLm) {
+            r.x[t][run] = load_run<AK, DT>(a.x, a.x_dtype, t, a.tokens, a.in, k0 + kBlockCols * run, a.in);
 #pragma unroll
-        for (int run = 0; run < 2; ++run)
-            r.s[run] = load_run<AK, kScaleDtype>(v.colscale, v.colscale_dtype, 0, 1, 0, k0 + kBlockCols * run,
-                                                 v.cols, v.act_clamp);
+    for (int run = 0; run < 2; ++run)
+        r.s[run] = load_run<AK, kScaleDtype>(a.s_in, a.scale_dtype, 0, 1, 0, k0 + kBlockCols * run, a.in);
+}
+
+// Sign words of chunk c for tiles t0 .. t0 + TW - 1 (tiles past the last one
+// load the last tile; their results are never stored): one 16-byte load per
+// lane at word lane * dw. In a partial last chunk (dw < 4) the words past dw
+// belong to the next lane (or, for the last lane of the matrix, to the
+// buffer's tail padding) and the MFMA step masks them out.
+template <int TW>
+__device__ __forceinline__ void load_words(v4u (&w)[TW], const uint32_t* tiles, const MatGeo& g, int64_t t0,
+                                           int64_t c, int lane) {
+    const int dw = chunk_words(g, c);
+#pragma unroll
+    for (int tt = 0; tt < TW; ++tt) {
+        const int64_t tile = t0 + tt < g.nt ? t0 + tt : g.nt - 1;
+        const uint32_t* base = tiles + tile * g.nb * 64 + c * 256 + lane * dw;
+        w[tt] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(base));
     }
 }
 
-// Issue the sign-word loads of chunk c for tiles t0 .. t0 + TW - 1 (tiles past
-// the last one load the last tile; their results are never stored). A partial
-// last chunk (dw < 4 words per lane) loads its dw words and repeats the last
-// one; tile_partial masks the repeats out.
-template <int AK, int TOK, int TW>
-__device__ __forceinline__ void load_chunk_words(ChunkRegs<AK, TOK, TW>& r, const StageView& v, int64_t t0,
-                                                 int64_t c, int lane) {
-    const int dw = chunk_words(v.g, c);
+template <int TPB, int TB, int TW>
+__device__ __forceinline__ void load_s2_ops(S2Regs<TB, TW>& r, const LinArgs& a, int64_t c, int lane) {
+    const int row = TPB == 1 ? (lane & 3) : (lane & 15);
 #pragma unroll
-    for (int tt = 0; tt < TW; ++tt) {
-        const int64_t tile = t0 + tt < v.g.nt ? t0 + tt : v.g.nt - 1;
-        const uint32_t* base = v.tiles + tile * v.g.nb * 64 + c * 256;
-        if (dw == kChunkBlocks) {  // uniform
-            r.w[tt] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(base) + lane);
-        } else {
-            v4u w;
+    for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-            for (int d = 0; d < kChunkBlocks; ++d) {
-                const int dd = d < dw ? d : dw - 1;
-                w[d] = __builtin_nontemporal_load(base + lane * dw + dd);
-            }
-            r.w[tt] = w;
-        }
-    }
+        for (int m = 0; m < 8; ++m)
+            r.a[tb][m] = *reinterpret_cast<const v4i*>(a.lmq + lmq_offset<TPB, TB>(c, tb, m, row, lane >> 4));
 }
 
 // Order this wave's LDS writes before its own reads (waves never share areas).
@@ -465,74 +474,65 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-__device__ __forceinline__ int sext8(int v) { return (v << 24) >> 24; }
+// Low byte of each of four ints, packed.
+__device__ __forceinline__ uint32_t pack_bytes(int a, int b, int c, int d) {
+    return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
+           ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
+}
+
+// Signed base-256 digits of w: w = d0 + 256 d1 + 65536 d2 + ..., each digit in
+// [-128, 127]. The byte of d_j is the low byte of w_j with w_0 = w and
+// w_{j+1} = (w_j + 128) >> 8.
+__device__ __forceinline__ int next_digit_word(int w) { return (w + 128) >> 8; }
 
 // Stage tokens [t_base, t_base + TPB) of chunk c into this wave's operand area
-// and return each token's exponent E and integer sum S (uniform values).
+// (three digit rows per token) and return each token's exponent E and the
+// chunk max |a| (uniform values).
 template <int AK, int TOK, int TW, int TPB>
-__device__ __forceinline__ void stage_block(const ChunkRegs<AK, TOK, TW>& r, const StageView& v, int tokens,
-                                            int64_t c, int t_base, char* __restrict__ ops, int lane, int (&expo)[TPB],
-                                            int (&qsum)[TPB]) {
+__device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int64_t c, int t_base,
+                                            char* __restrict__ ops, int lane, int (&expo)[TPB], float (&cmax)[TPB]) {
     constexpr int DT = act_dtype<AK>();
     const int m = lane >> 3, grp = (lane >> 1) & 3, dp = lane & 1;
     const int64_t k0 = stage_col0(c, lane);
+    const int mult = m < 7 ? (1 << (7 - m)) : -1;  // w = x_q * mult
     float sc[2][4];
-    if constexpr (AK != kActLm) {
-        run_values<AK, kScaleDtype>(r.s[0], v.colscale_dtype, sc[0]);
-        run_values<AK, kScaleDtype>(r.s[1], v.colscale_dtype, sc[1]);
-    }
+    run_values<AK, kScaleDtype>(r.s[0], a.scale_dtype, sc[0]);
+    run_values<AK, kScaleDtype>(r.s[1], a.scale_dtype, sc[1]);
 #pragma unroll
     for (int u = 0; u < TPB; ++u) {
         const int t = t_base + u;
-        float a[2][4];
+        float v[2][4];
         float mx = 0.0f;
 #pragma unroll
         for (int run = 0; run < 2; ++run) {
-            run_values<AK, DT>(r.x[t][run], v.act_dtype, a[run]);
+            run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float val = a[run][i];
-                if constexpr (AK != kActLm) val *= sc[run][i];
-                const bool ok = t < tokens && k0 + kBlockCols * run + i < v.cols;
-                val = ok ? val : 0.0f;
-                a[run][i] = val;
-                mx = fmaxf(mx, fabsf(val));
+                const bool ok = t < a.tokens && k0 + kBlockCols * run + i < a.in;
+                v[run][i] = ok ? v[run][i] * sc[run][i] : 0.0f;
+                mx = fmaxf(mx, fabsf(v[run][i]));
             }
         }
-        const int e = chunk_exponent(wave_max(mx));
+        const float wmx = wave_max(mx);
+        const int e = range_exponent(wmx, 14);
         const float scale = exp2i(e);
-        int q[2][4];
-        int s = 0;
-#pragma unroll
-        for (int run = 0; run < 2; ++run)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                q[run][i] = static_cast<int>(__builtin_rintf(a[run][i] * scale));
-                s += q[run][i];
-            }
-        expo[u] = e;
-        qsum[u] = wave_sum(s);
-        // Digits of w = x_q * 2^(7 - m) (m < 7) or -x_q (m = 7); byte 4*run + i
-        // of each digit row is column k0 + 128*run + i.
         uint32_t dig[3][2];
 #pragma unroll
         for (int run = 0; run < 2; ++run) {
-            uint32_t b0 = 0, b1 = 0, b2 = 0;
+            int w0[4], w1[4], w2[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int w = m < 7 ? (q[run][i] << (7 - m)) : -q[run][i];
-                const int d0 = sext8(w);
-                const int w1 = (w - d0) >> 8;
-                const int d1 = sext8(w1);
-                const int d2 = (w1 - d1) >> 8;
-                b0 |= (static_cast<uint32_t>(d0) & 0xffu) << (8 * i);
-                b1 |= (static_cast<uint32_t>(d1) & 0xffu) << (8 * i);
-                b2 |= (static_cast<uint32_t>(d2) & 0xffu) << (8 * i);
+                const int q = static_cast<int>(__builtin_rintf(v[run][i] * scale));
+                w0[i] = q * mult;
+                w1[i] = next_digit_word(w0[i]);
+                w2[i] = next_digit_word(w1[i]);
             }
-            dig[0][run] = b0;
-            dig[1][run] = b1;
-            dig[2][run] = b2;
+            dig[0][run] = pack_bytes(w0[0], w0[1], w0[2], w0[3]);
+            dig[1][run] = pack_bytes(w1[0], w1[1], w1[2], w1[3]);
+            dig[2][run] = pack_bytes(w2[0], w2[1], w2[2], w2[3]);
         }
+        expo[u] = e;
+        cmax[u] = wmx;
 #pragma unroll
         for (int digit = 0; digit < 3; ++digit) {
             const int row = 4 * u + digit;
@@ -542,38 +542,41 @@ __device__ __forceinline__ void stage_block(const ChunkRegs<AK, TOK, TW>& r, con
     }
 }
 
-// The eight MFMAs of one (chunk, tile, token block) and the exact conversion to
-// the chunk's fp32 partial; words d >= dw (a partial chunk) count as zero.
-// Lane 16*t' + n returns token t' (of the block), row n.
-template <int TPB>
-__device__ __forceinline__ float tile_partial(const v4i (&A)[8], const v4u& w, int dw, int lane,
-                                              const int (&expo)[TPB], const int (&qsum)[TPB]) {
-    v4i acc = v4i{0, 0, 0, 0};
-    const uint32_t keep1 = dw > 1 ? ~0u : 0u, keep2 = dw > 2 ? ~0u : 0u, keep3 = dw > 3 ? ~0u : 0u;
+// S = 2^7 Σ x_q of one chunk and operand block: eight MFMAs against 0x01 << m.
+__device__ __forceinline__ v4i ones_mfma(const v4i (&A)[8]) {
+    v4i s0 = v4i{0, 0, 0, 0}, s1 = v4i{0, 0, 0, 0};
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-        const uint32_t mask = 0x01010101u << m;
-        const v4i b = v4i{static_cast<int>(w[0] & mask), static_cast<int>(w[1] & (mask & keep1)),
-                          static_cast<int>(w[2] & (mask & keep2)), static_cast<int>(w[3] & (mask & keep3))};
-        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], b, acc, 0, 0, 0);
+    for (int m = 0; m < 8; m += 2) {
+        const int o0 = static_cast<int>(0x01010101u << m), o1 = static_cast<int>(0x01010101u << (m + 1));
+        s0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], v4i{o0, o0, o0, o0}, s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m + 1], v4i{o1, o1, o1, o1}, s1, 0, 0, 0);
     }
-    int e = expo[0];
-    int s = qsum[0];
-    if (TPB > 1) {
-        const int tl = lane >> 4;
-#pragma unroll
-        for (int u = 1; u < TPB; ++u) {
-            e = tl == u ? expo[u] : e;
-            s = tl == u ? qsum[u] : s;
-        }
-    }
-    const float tsum = static_cast<float>(acc[0]) + 256.0f * static_cast<float>(acc[1]) +
-                       65536.0f * static_cast<float>(acc[2]);
-    return (static_cast<float>(s) - tsum * 0.015625f) * exp2i(-e);
+    return s0 + s1;
 }
 
-__device__ __forceinline__ void store_agent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The eight sign MFMAs of one (chunk, tile, operand block) and the exact
+// conversion to the chunk's fp32 partial; words d >= dw (a partial chunk)
+// count as zero. NDIG digit rows per token; lane 16*t' + n returns token t' of
+// the block, row n; e is that token's exponent.
+template <int NDIG>
+__device__ __forceinline__ float tile_partial(const v4i (&A)[8], const v4i& S, const v4u& w, int dw, int e) {
+    v4i t0 = v4i{0, 0, 0, 0}, t1 = v4i{0, 0, 0, 0};
+    const uint32_t keep1 = dw > 1 ? ~0u : 0u, keep2 = dw > 2 ? ~0u : 0u, keep3 = dw > 3 ? ~0u : 0u;
+#pragma unroll
+    for (int m = 0; m < 8; m += 2) {
+        const uint32_t k0 = 0x01010101u << m, k1 = 0x01010101u << (m + 1);
+        const v4i b0 = v4i{static_cast<int>(w[0] & k0), static_cast<int>(w[1] & (k0 & keep1)),
+                           static_cast<int>(w[2] & (k0 & keep2)), static_cast<int>(w[3] & (k0 & keep3))};
+        const v4i b1 = v4i{static_cast<int>(w[0] & k1), static_cast<int>(w[1] & (k1 & keep1)),
+                           static_cast<int>(w[2] & (k1 & keep2)), static_cast<int>(w[3] & (k1 & keep3))};
+        t0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], b0, t0, 0, 0, 0);
+        t1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m + 1], b1, t1, 0, 0, 0);
+    }
+    const v4i diff = S - 2 * (t0 + t1);
+    float v = static_cast<float>(diff[0]) + 256.0f * static_cast<float>(diff[1]) +
+              65536.0f * static_cast<float>(diff[2]);
+    if (NDIG == 4) v += 16777216.0f * static_cast<float>(diff[3]);
+    return v * exp2i(-e - 7);
 }
 
 __device__ __forceinline__ void hdr_store(uint32_t* header, int word, uint32_t v) {
@@ -592,7 +595,7 @@ __device__ __forceinline__ uint64_t slot_count(int slot, int slots, int64_t coun
 }
 
 // Fused launch, stage 1: thread 0 signals each of the workgroup's tiles once
-// the workgroup's lm stores are complete (the caller waits and barriers first).
+// the workgroup's operand stores are complete (the caller waits and barriers first).
 __device__ __forceinline__ void signal_ready(const LinArgs& a, int64_t t0, int tw) {
     if (threadIdx.x != 0) return;
     const int64_t n1 = a.g1.nt;
@@ -616,8 +619,8 @@ __device__ __forceinline__ void signal_ready(const LinArgs& a, int64_t t0, int t
 
 // Fused launch, stage 2: register the workgroup's tiles, then wait until every
 // stage-1 tile of this launch has signalled.
-__device__ __forceinline__ void wait_ready(const LinArgs& a, int64_t t0, int tw, int64_t wg) {
-    if (threadIdx.x == 0) {
+__device__ __forceinline__ void wait_ready(const LinArgs& a, int64_t t0, int tw, int64_t wg, bool dead) {
+    if (threadIdx.x == 0 && !dead) {
         const int64_t n2 = a.g2.nt;
         uint32_t target = 0;
         for (int tt = 0; tt < tw; ++tt) {
@@ -661,156 +664,276 @@ __device__ __forceinline__ PassChunks<KC> pass_chunks(int64_t base, int wave, in
     return p;
 }
 
-// One workgroup of one stage: tiles [t0, t0 + TW) of linear `a`. TPB tokens per
+// Output index idx of a workgroup: (tile tt, token t, row n).
+struct OutIdx {
+    int tt, t, n;
+};
+
+__device__ __forceinline__ OutIdx out_index(int idx, int tokens) {
+    OutIdx o;
+    o.tt = idx / (tokens * kTileRows);
+    o.t = (idx / kTileRows) % tokens;
+    o.n = idx & 15;
+    return o;
+}
+
+// Partial-sum slot of (chunk c, tile tt, token t, row n) in the LDS array red.
+template <int TPB, int TB, int TW>
+__device__ __forceinline__ int red_index(int64_t c, int tt, int t, int n) {
+    const int tb = TPB == 1 ? 0 : t / TPB;
+    const int rl = TPB == 1 ? n : 16 * (t % TPB) + n;
+    return static_cast<int>(((c * TW + tt) * TB + tb) * 64 + rl);
+}
+
+// Stage-1 epilogue store of one rank value: x_q = rint(v * 2^e) as four digits
+// of w = x_q * mult into the stage-2 operand buffer (agent scope when fused).
+template <int TPB, int TB, bool FUSED>
+__device__ __forceinline__ void store_lmq(uint8_t* lmq, int64_t r, int t, float v, int e) {
+    const int64_t c = r >> 9;
+    const int col = static_cast<int>(r & 511);
+    const int d = col >> 7, m = (col >> 4) & 7, g = (col >> 2) & 3, b = col & 3;
+    const int tb = TPB == 1 ? 0 : t / TPB, u = TPB == 1 ? 0 : t % TPB;
+    const int q = static_cast<int>(__builtin_rintf(v * exp2i(e)));
+    int w = q * (m < 7 ? (1 << (7 - m)) : -1);
+#pragma unroll
+    for (int digit = 0; digit < 4; ++digit) {
+        uint8_t* p = lmq + lmq_offset<TPB, TB>(c, tb, m, 4 * u + digit, g) + 4 * d + b;
+        const uint8_t byte = static_cast<uint8_t>(w & 0xff);
+        if (FUSED) __hip_atomic_store(p, byte, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else *p = byte;
+        w = next_digit_word(w);
+    }
+}
+
+// One stage-1 workgroup: tiles [t0, t0 + TW) of linear `a`. TPB tokens per
 // block and TB blocks cover the launch's tokens; KC chunks per wave per pass.
-template <int STAGE, int AK, int TPB, int TB, int TW, int KC, bool FUSED>
-__device__ __forceinline__ void stage_wg(const LinArgs& a, int64_t wg, char* __restrict__ lds) {
+template <int AK, int TPB, int TB, int TW, int KC, bool FUSED>
+__device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char* __restrict__ lds) {
     constexpr int TOK = TPB * TB;
-    const StageView v = stage_view<STAGE>(a);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int nw = static_cast<int>(blockDim.x >> 6);
+    const int nw = a.nw1;
     const int tokens = a.tokens;
+    // Workgroups past this member's count compute the last workgroup's tiles
+    // and store nothing.
+    const bool dead = wg_in >= a.nwg1;
+    const int64_t wg = dead ? a.nwg1 - 1 : wg_in;
     const int64_t t0 = wg * TW;
-    const int64_t nc = v.g.nc;
-    char* const ops = lds + wave * Ops<TPB>::kWaveBytes;
-    float* const red = reinterpret_cast<float*>(lds + nw * Ops<TPB>::kWaveBytes);
+    const MatGeo g = a.g1;
+    const int64_t nc = g.nc;
+    char* const ops = lds + wave * Ops<TPB>::kBytes;
+    float* const red = reinterpret_cast<float*>(lds + nw * Ops<TPB>::kBytes);
+    float* const cmx = red + nc * TW * TB * 64;  // [nc][TOK] chunk max |x s_in|
 
-    // Epilogue operands of this thread's first output (see the epilogue loop),
-    // issued first so their latency hides under the main loads.
+    // Epilogue operands issued first so their latency hides under the main loads.
     const int outs = TW * tokens * kTileRows;
-    const int first = threadIdx.x;
-    const int64_t first_tile = t0 + (first < outs ? first : 0) / (tokens * kTileRows);
-    const int64_t fr = first_tile * kTileRows + (first & 15);
-    const int64_t first_row = fr < v.rows ? fr : v.rows - 1;
-    const RawElem rs0 = load_elem(v.rowscale, a.scale_dtype, first_row);
-    RawElem bias0{0u, 0u};
-    if (STAGE == 2 && a.bias) bias0 = load_elem(a.bias, a.bias_dtype, first_row);
+    const OutIdx f = out_index(threadIdx.x < outs ? threadIdx.x : 0, tokens);
+    const int64_t fr = (t0 + f.tt) * kTileRows + f.n;
+    const RawElem rs0 = load_elem(a.s_mid, a.scale_dtype, fr < a.rank ? fr : a.rank - 1);
+    const float maxsm = __uint_as_float(a.header[line_word(kMiscLine) + kMiscMaxMid]);
 
     for (int64_t base = 0; base < nc; base += static_cast<int64_t>(nw) * KC) {
         const PassChunks<KC> pc = pass_chunks<KC>(base, wave, nw, nc);
-        ChunkRegs<AK, TOK, TW> r[KC];
-        if (FUSED && STAGE == 2) {
-            // The U words do not depend on stage 1: issue them, wait for the
-            // signal (first pass only), then load lm.
+        S1Regs<AK, TOK, TW> r[KC];
+        // Activations first, sign words second: the staging math waits only
+        // for the activations, the MFMAs for the words.
 #pragma unroll
-            for (int j = 0; j < KC; ++j) load_chunk_words(r[j], v, t0, pc.c[j], lane);
-            if (base == 0) wait_ready(a, t0, TW, wg);
+        for (int j = 0; j < KC; ++j) load_s1_acts(r[j], a, pc.c[j], lane);
 #pragma unroll
-            for (int j = 0; j < KC; ++j) load_chunk_acts(r[j], v, tokens, pc.c[j], lane);
-        } else {
-            // Activations first, sign words second: the staging math waits only
-            // for the activations, the MFMAs for the words.
-#pragma unroll
-            for (int j = 0; j < KC; ++j) load_chunk_acts(r[j], v, tokens, pc.c[j], lane);
-#pragma unroll
-            for (int j = 0; j < KC; ++j) load_chunk_words(r[j], v, t0, pc.c[j], lane);
-        }
+        for (int j = 0; j < KC; ++j) load_words(r[j].w, a.v_tiles, g, t0, pc.c[j], lane);
         __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
 #pragma unroll
         for (int j = 0; j < KC; ++j) {
             if (!pc.live[j]) continue;  // uniform
             const int64_t c = pc.c[j];
+            const int dw = chunk_words(g, c);
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb) {
                 if (tb * TPB >= tokens) break;
-                int expo[TPB], qsum[TPB];
-                stage_block<AK, TOK, TW, TPB>(r[j], v, tokens, c, tb * TPB, ops, lane, expo, qsum);
+                int expo[TPB];
+                float cm[TPB];
+                stage_block<AK, TOK, TW, TPB>(r[j], a, c, tb * TPB, ops, lane, expo, cm);
                 wave_lds_sync();
                 v4i A[8];
                 const int row = TPB == 1 ? (lane & 3) : (lane & 15);
 #pragma unroll
                 for (int m = 0; m < 8; ++m)
                     A[m] = *reinterpret_cast<const v4i*>(ops + ((m * Ops<TPB>::kRows + row) * 4 + (lane >> 4)) * 16);
-                const int dw = chunk_words(v.g, c);
+                const v4i S = ones_mfma(A);
+                int e = expo[0];
+#pragma unroll
+                for (int u = 1; u < TPB; ++u) e = (lane >> 4) == u ? expo[u] : e;
 #pragma unroll
                 for (int tt = 0; tt < TW; ++tt)
-                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<TPB>(A, r[j].w[tt], dw, lane, expo, qsum);
+                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<3>(A, S, r[j].w[tt], dw, e);
+                if (lane == 0) {
+#pragma unroll
+                    for (int u = 0; u < TPB; ++u) cmx[c * TOK + tb * TPB + u] = cm[u];
+                }
                 wave_lds_sync();  // the next block rewrites this wave's operand area
             }
         }
     }
     __syncthreads();
 
-    // Epilogue: output idx = (tt, t, n); partials summed in chunk order.
+    if (dead) return;  // uniform, after the workgroup's only barrier
+
+    // Epilogue: lm = s_mid * Σ_chunks partial, written as stage-2 operands with
+    // the per-token exponent of the bound max|s_mid| * Σ_c 512 * max_c.
     for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
-        const int tt = idx / (tokens * kTileRows);
-        const int t = (idx / kTileRows) % tokens;
-        const int n = idx & 15;
-        const int64_t row = (t0 + tt) * kTileRows + n;
-        if (t0 + tt >= v.g.nt || row >= v.rows) continue;
-        const int tb = TPB == 1 ? 0 : t / TPB;
-        const int rl = TPB == 1 ? n : 16 * (t % TPB) + n;
-        float sum = 0.0f;
-        for (int64_t c = 0; c < nc; ++c) sum += red[((c * TW + tt) * TB + tb) * 64 + rl];
-        const float rs = elem_value(idx == first ? rs0 : load_elem(v.rowscale, a.scale_dtype, row), a.scale_dtype);
-        if (STAGE == 1) {
-            const float val = sum * rs;
-            float* dst = a.lm + t * a.lm_ld + row;
-            if (FUSED) store_agent(dst, val);
-            else *dst = val;
-        } else {
-            float val = sum * rs;
-            for (int64_t k = 0; k < a.salient_count; ++k) {
-                float wv = nq::load_f32(a.salient_values, a.salient_dtype, row * a.salient_count + k);
-                if (a.salient_scales) wv *= nq::load_f32(a.salient_scales, a.scale_dtype, k);
-                val += wv * nq::load_f32(a.x, a.x_dtype, t * a.in + a.salient_indices[k]);
-            }
-            if (a.bias) val += elem_value(idx == first ? bias0 : load_elem(a.bias, a.bias_dtype, row), a.bias_dtype);
-            nq::store_f32_as(a.y, a.y_dtype, t * a.out + row, val);
+        const OutIdx o = out_index(idx, tokens);
+        const int64_t row = (t0 + o.tt) * kTileRows + o.n;
+        if (t0 + o.tt >= g.nt) continue;
+        float sum = 0.0f, bound = 0.0f;
+        for (int64_t c = 0; c < nc; ++c) {
+            sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
+            bound += cmx[c * TOK + o.t];
+        }
+        const int e = range_exponent(bound * (512.0f * maxsm), 21);
+        float v = 0.0f;
+        if (row < a.rank) v = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_mid, a.scale_dtype, row),
+                                               a.scale_dtype);
+        store_lmq<TPB, TB, FUSED>(a.lmq, row, o.t, v, e);
+        if (wg == 0 && o.tt == 0 && o.n == 0) {
+            if (FUSED) __hip_atomic_store(a.lme + o.t, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else a.lme[o.t] = e;
         }
     }
-    if (FUSED && STAGE == 1) {
-        // lm went out at agent scope; the wait makes it complete before the signal.
+    // The last workgroup zeroes the operand columns past its last tile up to
+    // the end of the last chunk (every stage-2 ones-MFMA reads them).
+    if (t0 + TW >= g.nt) {
+        const MatGeo g2 = a.g2;
+        const int64_t from = g.nt * kTileRows, to = g2.nc * kChunkCols;
+        const int64_t n = (to - from) * tokens;
+        for (int64_t i = threadIdx.x; i < n; i += blockDim.x) store_lmq<TPB, TB, FUSED>(a.lmq, from + i / tokens,
+                                                                                        static_cast<int>(i % tokens),
+                                                                                        0.0f, 0);
+    }
+    if (FUSED) {
+        // The operands went out at agent scope; the wait makes them complete
+        // before the signal.
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         signal_ready(a, t0, TW);
     }
 }
 
-// Linear of block b: the number of prefix entries first[1..count-1] <= b
-// (independent scalar loads, no dependent chain).
-__device__ __forceinline__ int member_of(const int64_t (&first)[kMaxBatch + 1], int count, int64_t b) {
-    int p = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxBatch; ++i) p += (i < count && b >= first[i]) ? 1 : 0;
-    return p;
-}
+// One stage-2 workgroup: output tiles [t0, t0 + TW) of linear `a`.
+template <int TPB, int TB, int TW, int KC, bool FUSED>
+__device__ __forceinline__ void stage2_wg(const LinArgs& a, int64_t wg_in, char* __restrict__ lds) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int nw = a.nw2;
+    const int tokens = a.tokens;
+    const bool dead = wg_in >= a.nwg2;  // computes the last workgroup's tiles, stores nothing
+    const int64_t wg = dead ? a.nwg2 - 1 : wg_in;
+    const int64_t t0 = wg * TW;
+    const MatGeo g = a.g2;
+    const int64_t nc = g.nc;
+    float* const red = reinterpret_cast<float*>(lds);
 
-// Split launch: one kernel per stage; block b of the stage-2 kernel is block
-// b + first1[count] of the combined numbering. THREADS is the launch bound:
-// 1024 for one token per block, 768 when a wave takes two chunks per pass
-// (168 VGPRs), 512 for four tokens per block (256 VGPRs).
-template <int STAGE, int AK, int TPB, int TB, int TW, int KC, int THREADS>
-__global__ __launch_bounds__(THREADS) void k_decode_stage(const Batch batch) {
-    extern __shared__ __attribute__((aligned(16))) char lds[];
-    if (STAGE == 1) {
-        const int64_t b = blockIdx.x;
-        const int p = member_of(batch.first1, batch.count, b);
-        stage_wg<1, AK, TPB, TB, TW, KC, false>(batch.p[p], b - batch.first1[p], lds);
-    } else {
-        const int64_t b = blockIdx.x + batch.first1[batch.count];
-        const int p = member_of(batch.first2, batch.count, b);
-        stage_wg<2, AK, TPB, TB, TW, KC, false>(batch.p[p], b - batch.first2[p], lds);
+    const int outs = TW * tokens * kTileRows;
+    const OutIdx f = out_index(threadIdx.x < outs ? threadIdx.x : 0, tokens);
+    const int64_t fr0 = (t0 + f.tt) * kTileRows + f.n;
+    const int64_t fr = fr0 < a.out ? fr0 : a.out - 1;
+    const RawElem rs0 = load_elem(a.s_out, a.scale_dtype, fr);
+    // No branch on the optional bias: without one, s_out is loaded instead and ignored.
+    const RawElem bias0 = load_elem(a.bias ? a.bias : a.s_out, a.bias ? a.bias_dtype : a.scale_dtype, fr);
+
+    for (int64_t base = 0; base < nc; base += static_cast<int64_t>(nw) * KC) {
+        const PassChunks<KC> pc = pass_chunks<KC>(base, wave, nw, nc);
+        S2Regs<TB, TW> r[KC];
+#pragma unroll
+        for (int j = 0; j < KC; ++j) load_words(r[j].w, a.u_tiles, g, t0, pc.c[j], lane);
+        // The U words do not depend on stage 1; the fused launch waits for its
+        // signal only now.
+        if (FUSED && base == 0) wait_ready(a, t0, TW, wg, dead);
+#pragma unroll
+        for (int j = 0; j < KC; ++j) load_s2_ops<TPB, TB, TW>(r[j], a, pc.c[j], lane);
+        int e[TB];
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+            const int t = tb * TPB + (TPB == 1 ? 0 : (lane >> 4));
+            e[tb] = a.lme[t < tokens ? t : tokens - 1];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            if (!pc.live[j]) continue;  // uniform
+            const int64_t c = pc.c[j];
+            const int dw = chunk_words(g, c);
+#pragma unroll
+            for (int tb = 0; tb < TB; ++tb) {
+                if (tb * TPB >= tokens) break;
+                const v4i S = ones_mfma(r[j].a[tb]);
+#pragma unroll
+                for (int tt = 0; tt < TW; ++tt)
+                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<4>(r[j].a[tb], S, r[j].w[tt], dw, e[tb]);
+            }
+        }
+    }
+    __syncthreads();
+    if (dead) return;  // uniform, after the workgroup's only barrier
+
+    for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
+        const OutIdx o = out_index(idx, tokens);
+        const int64_t row = (t0 + o.tt) * kTileRows + o.n;
+        if (t0 + o.tt >= g.nt || row >= a.out) continue;
+        float sum = 0.0f;
+        for (int64_t c = 0; c < nc; ++c) sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
+        float val = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_out, a.scale_dtype, row), a.scale_dtype);
+        for (int64_t k = 0; k < a.salient_count; ++k) {
+            float wv = nq::load_f32(a.salient_values, a.salient_dtype, row * a.salient_count + k);
+            if (a.salient_scales) wv *= nq::load_f32(a.salient_scales, a.scale_dtype, k);
+            val += wv * nq::load_f32(a.x, a.x_dtype, o.t * a.in + a.salient_indices[k]);
+        }
+        if (a.bias) val += elem_value(idx == threadIdx.x ? bias0 : load_elem(a.bias, a.bias_dtype, row), a.bias_dtype);
+        nq::store_f32_as(a.y, a.y_dtype, o.t * a.out + row, val);
     }
 }
 
-// Fused launch (one tile per workgroup, generic stage-1 loads): stage-1 blocks
-// first, then stage-2.
+// Split launch: one kernel per stage, grid (workgroups, members). THREADS is
+// the launch bound: 1024 for one token per block, 768 when a wave takes two
+// chunks per pass (168 VGPRs), 512 for four tokens per block (256 VGPRs).
+// Grid: (workgroups of the widest member, members). A workgroup reads its
+// member's arguments in one batch (load_args), and nothing branches on them
+// before the main loads are issued except the grid-padding exit (optional
+// operands load from a valid address and are selected later, partial chunks
+// use the same 16-byte word loads as full ones).
+template <int AK, int TPB, int TB, int TW, int KC, int THREADS>
+__global__ __launch_bounds__(THREADS) void k_decode_stage1(const Batch batch) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const LinArgs a = load_args(batch, blockIdx.y);
+    if (blockIdx.x >= a.nwg1) return;  // grid padding: the arguments are already loaded
+    stage1_wg<AK, TPB, TB, TW, KC, false>(a, blockIdx.x, lds);
+}
+
+template <int TPB, int TB, int TW, int KC, int THREADS>
+__global__ __launch_bounds__(THREADS) void k_decode_stage2(const Batch batch) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const LinArgs a = load_args(batch, blockIdx.y);
+    if (blockIdx.x >= a.nwg2) return;  // grid padding: the arguments are already loaded
+    stage2_wg<TPB, TB, TW, KC, false>(a, blockIdx.x, lds);
+}
+
+// Fused launch (one tile per workgroup, generic stage-1 loads): grid rows
+// [0, count) are stage 1, rows [count, 2 count) stage 2.
 template <int TPB, int TB, int KC1, int KC2, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_fused(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const int64_t b = blockIdx.x;
-    if (b < batch.first1[batch.count]) {
-        const int p = member_of(batch.first1, batch.count, b);
-        stage_wg<1, kActGeneric, TPB, TB, 1, KC1, true>(batch.p[p], b - batch.first1[p], lds);
+    const int y = static_cast<int>(blockIdx.y);
+    const int count = batch.count;
+    const LinArgs a = load_args(batch, y < count ? y : y - count);
+    if (y < count) {
+        if (blockIdx.x >= a.nwg1) return;
+        stage1_wg<kActGeneric, TPB, TB, 1, KC1, true>(a, blockIdx.x, lds);
     } else {
-        const int p = member_of(batch.first2, batch.count, b);
-        stage_wg<2, kActLm, TPB, TB, 1, KC2, true>(batch.p[p], b - batch.first2[p], lds);
+        if (blockIdx.x >= a.nwg2) return;
+        stage2_wg<TPB, TB, 1, KC2, true>(a, blockIdx.x, lds);
     }
 }
 
-// Launch bound of a configuration (see k_decode_stage).
+// Launch bound of a configuration (see k_decode_stage1).
 constexpr int threads_for(int tpb, int kc) { return tpb == 1 ? (kc == 1 ? 1024 : 768) : 512; }
 
 // Shape of one decode launch, chosen on the host (nq_decode.hip).
@@ -821,7 +944,7 @@ struct LaunchShape {
     int nw;          // waves per workgroup
     int kc, kc2;     // chunks per wave per pass (stage kernels: kc; fused: stage 1 kc, stage 2 kc2)
     size_t lds;      // dynamic LDS bytes
-    unsigned grid;   // workgroups
+    dim3 grid;
 };
 
 // Launchers, one translation unit each (they instantiate disjoint kernels).

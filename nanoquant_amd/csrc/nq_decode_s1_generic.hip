@@ -1,5 +1,5 @@
-// Launcher of the split decode kernel for stage 1 with any float x and scales (instantiations of
-// k_decode_stage<1, kActGeneric, ...>; the kernels are documented in
+// Launcher of the split decode stage-1 kernel for any float x and scales (instantiations of
+// k_decode_stage1<kActGeneric, ...>; the kernels are documented in
 // nq_decode_kernels.h). One translation unit per activation kind keeps the
 // library build parallel.
 #include "nq_decode_kernels.h"
@@ -11,8 +11,8 @@ template <int TPB, int TB, int TW, int KC>
 int go(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     constexpr int kThreads = threads_for(TPB, KC);
     if (64 * s.nw > kThreads) return NQ_ERR_LAUNCH;
-    hipLaunchKernelGGL((k_decode_stage<1, kActGeneric, TPB, TB, TW, KC, kThreads>), dim3(s.grid), dim3(64 * s.nw),
-                       s.lds, stream, batch);
+    hipLaunchKernelGGL((k_decode_stage1<kActGeneric, TPB, TB, TW, KC, kThreads>), s.grid, dim3(64 * s.nw), s.lds, stream,
+                       batch);
     return nq::launch_status();
 }
 

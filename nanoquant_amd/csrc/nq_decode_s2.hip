@@ -1,7 +1,5 @@
-// Launcher of the split decode kernel for stage 2 (fp32 rank intermediate) (instantiations of
-// k_decode_stage<2, kActLm, ...>; the kernels are documented in
-// nq_decode_kernels.h). One translation unit per activation kind keeps the
-// library build parallel.
+// Launcher of the split decode stage-2 kernel (instantiations of
+// k_decode_stage2; the kernels are documented in nq_decode_kernels.h).
 #include "nq_decode_kernels.h"
 
 namespace nqdec {
@@ -11,8 +9,7 @@ template <int TPB, int TB, int TW, int KC>
 int go(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     constexpr int kThreads = threads_for(TPB, KC);
     if (64 * s.nw > kThreads) return NQ_ERR_LAUNCH;
-    hipLaunchKernelGGL((k_decode_stage<2, kActLm, TPB, TB, TW, KC, kThreads>), dim3(s.grid), dim3(64 * s.nw),
-                       s.lds, stream, batch);
+    hipLaunchKernelGGL((k_decode_stage2<TPB, TB, TW, KC, kThreads>), s.grid, dim3(64 * s.nw), s.lds, stream, batch);
     return nq::launch_status();
 }
 
