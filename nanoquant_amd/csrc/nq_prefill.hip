@@ -24,6 +24,12 @@
 //
 // Block tile 128 (tokens) x 128 (sign rows), 4 waves in a 2 x 2 grid, each
 // wave 64 x 64 = 4 x 4 MFMA tiles of 16 x 16 accumulated in fp32.
+//
+// Split K: when a GEMM has too few (token, sign-row) tiles to fill the GPU,
+// grid dimension z splits the K blocks into ranges of at least four and each
+// workgroup writes its raw fp32 accumulators to partial[z][t][n]; then
+// k_reduce_splits, one thread per output element, sums them in z order
+// (deterministic) and applies the epilogue.
 #include "nq_prefill.h"
 
 namespace {
@@ -57,31 +63,92 @@ __device__ __forceinline__ float range_scale(float bound) {
 // four are swapped (the order the sign operand's fp16 pairs come in).
 __device__ __forceinline__ int64_t swizzle4(int64_t c) { return (c & ~int64_t(3)) | ((c & 1) << 1) | ((c >> 1) & 1); }
 
+// fp32 values of elements [c, c + 8) of a row (c % 8 == 0): one 16-byte (or
+// two, for fp32) vector load when `vec` (the host checked alignment and
+// cols % 8 == 0), bounds-checked element loads otherwise.
+__device__ __forceinline__ void load8(const void* __restrict__ p, int dtype, bool vec, int64_t base, int64_t c,
+                                      int64_t cols, float (&v)[8]) {
+    if (vec) {
+        if (dtype == NQ_DTYPE_F32) {
+            const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + base + c);
+            const float4 a = q[0], b = q[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {
+            const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + base + c);
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (dtype == NQ_DTYPE_BF16) {
+                    v[2 * i] = __uint_as_float(w[i] << 16);
+                    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+                } else {
+                    union {
+                        uint32_t u;
+                        _Float16 h[2];
+                    } h;
+                    h.u = w[i];
+                    v[2 * i] = static_cast<float>(h.h[0]);
+                    v[2 * i + 1] = static_cast<float>(h.h[1]);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = c + i < cols ? nq::load_f32(p, dtype, base + c + i) : 0.0f;
+    }
+}
+
 // One workgroup per row: out16[t, swizzle4(c)] = fp16(a[t, c] * s[c] * scale_t)
-// for c < cols, zero for cols <= c < cols_pad; scale_out[t] = scale_t.
+// for c < cols, zero for cols <= c < cols_pad; scale_out[t] = scale_t. Each
+// thread takes 8 consecutive columns per step (one 16-byte store of fp16).
 __global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ act, int act_dtype, int64_t ld,
                                                       const void* __restrict__ colscale, int colscale_dtype,
-                                                      int64_t cols, int64_t cols_pad,
+                                                      int64_t cols, int64_t cols_pad, int vec,
                                                       _Float16* __restrict__ out16, float* __restrict__ scale_out) {
     __shared__ float wmax[kBlock / 64];
     const int64_t t = blockIdx.x;
+    auto values = [&](int64_t c, float (&v)[8]) {
+        load8(act, act_dtype, vec != 0, t * ld, c, cols, v);
+        if (colscale) {
+            float s8[8];
+            load8(colscale, colscale_dtype, vec != 0, 0, c, cols, s8);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] *= s8[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = c + i < cols ? v[i] : 0.0f;
+    };
     float m = 0.0f;
-    for (int64_t c = threadIdx.x; c < cols; c += kBlock) {
-        float v = nq::load_f32(act, act_dtype, t * ld + c);
-        if (colscale) v *= nq::load_f32(colscale, colscale_dtype, c);
-        m = fmaxf(m, fabsf(v));
+    for (int64_t c = 8 * threadIdx.x; c < cols; c += 8 * kBlock) {
+        float v[8];
+        values(c, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
     }
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
     __syncthreads();
     const float scale = range_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
-    for (int64_t c = threadIdx.x; c < cols_pad; c += kBlock) {
-        float v = 0.0f;
-        if (c < cols) {
-            v = nq::load_f32(act, act_dtype, t * ld + c);
-            if (colscale) v *= nq::load_f32(colscale, colscale_dtype, c);
+    for (int64_t c = 8 * threadIdx.x; c < cols_pad; c += 8 * kBlock) {
+        float v[8];
+        if (c < cols) values(c, v);
+        else
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        union {
+            _Float16 h[8];
+            uint4 u;
+        } o;
+        // swizzle4 within each group of four: positions 1 and 2 exchanged.
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            o.h[4 * g + 0] = static_cast<_Float16>(v[4 * g + 0] * scale);
+            o.h[4 * g + 1] = static_cast<_Float16>(v[4 * g + 2] * scale);
+            o.h[4 * g + 2] = static_cast<_Float16>(v[4 * g + 1] * scale);
+            o.h[4 * g + 3] = static_cast<_Float16>(v[4 * g + 3] * scale);
         }
-        out16[t * cols_pad + swizzle4(c)] = static_cast<_Float16>(v * scale);
+        *reinterpret_cast<uint4*>(out16 + t * cols_pad + c) = o.u;
     }
     if (threadIdx.x == 0) scale_out[t] = scale;
 }
@@ -125,6 +192,8 @@ struct GemmArgs {
     int bias_dtype;
     void* out;                // [M, n]
     int out_dtype;
+    int64_t k_per_split;      // K blocks per grid-z slice
+    float* partial;           // [gridDim.z][M][n] raw accumulators, or null (direct epilogue)
 };
 
 __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
@@ -172,8 +241,10 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
                                     : make_uint4(0, 0, 0, 0);
         }
     };
-    load_step(0);
-    for (int64_t sc = 0; sc < nsc; ++sc) {
+    const int64_t k_begin = static_cast<int64_t>(blockIdx.z) * g.k_per_split;
+    const int64_t k_end = k_begin + g.k_per_split < nsc ? k_begin + g.k_per_split : nsc;
+    load_step(k_begin);
+    for (int64_t sc = k_begin; sc < k_end; ++sc) {
         __syncthreads();  // previous step's LDS reads are done
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -183,7 +254,7 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) words[j] = next_words[j];
         __syncthreads();
-        if (sc + 1 < nsc) load_step(sc + 1);
+        if (sc + 1 < k_end) load_step(sc + 1);
 #pragma unroll
         for (int kc = 0; kc < 4; ++kc) {
             v8h b[4];
@@ -218,12 +289,17 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
                 park[(16 * i + 4 * (lane >> 4) + q) * kParkStride + 16 * j + (lane & 15)] = acc[i][j][q];
     __syncthreads();
     const int64_t col = n0 + 64 * wn + lane;
+    const int64_t row0 = m0 + 64 * wm;
+    const int rows = static_cast<int>(g.m - row0 < 64 ? g.m - row0 : 64);
     if (col >= g.n) return;
+    if (g.partial) {
+        float* dst = g.partial + static_cast<int64_t>(blockIdx.z) * g.m * g.n;
+        for (int e = 0; e < rows; ++e) dst[(row0 + e) * g.n + col] = park[e * kParkStride + lane];
+        return;
+    }
     const float cs = nq::load_f32(g.col_scale, g.col_scale_dtype, col);
     const float bias = g.bias ? nq::load_f32(g.bias, g.bias_dtype, col) : 0.0f;
     const int64_t salient = g.salient_count;
-    const int64_t row0 = m0 + 64 * wm;
-    const int rows = static_cast<int>(g.m - row0 < 64 ? g.m - row0 : 64);
     for (int e = 0; e < rows; ++e) {
         const int64_t row = row0 + e;
         float v = park[e * kParkStride + lane] / g.row_scale[row] * cs + bias;
@@ -234,6 +310,32 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
         }
         nq::store_f32_as(g.out, g.out_dtype, row * g.n + col, v);
     }
+}
+
+// Split-K epilogue, one thread per output element (t, c):
+// out[t, c] = (Σ_z partial[z][t][c]) / row_scale[t] * col_scale[c] (+ bias
+// + salient columns for GEMM 2), the slices summed in z order.
+__global__ __launch_bounds__(kBlock) void k_reduce_splits(int splits, const GemmArgs g) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= g.m * g.n) return;
+    const int64_t t = i / g.n, c = i - t * g.n;
+    const int64_t plane = g.m * g.n;
+    float part[8];
+    float v = 0.0f;
+    for (int z0 = 0; z0 < splits; z0 += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part[j] = z0 + j < splits ? g.partial[(z0 + j) * plane + i] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v += part[j];
+    }
+    v = v / g.row_scale[t] * nq::load_f32(g.col_scale, g.col_scale_dtype, c);
+    if (g.bias) v += nq::load_f32(g.bias, g.bias_dtype, c);
+    for (int64_t k = 0; k < g.salient_count; ++k) {
+        float w = nq::load_f32(g.salient_values, g.salient_dtype, c * g.salient_count + k);
+        if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
+        v += w * nq::load_f32(g.x, g.x_dtype, t * g.in + g.salient_indices[k]);
+    }
+    nq::store_f32_as(g.out, g.out_dtype, i, v);
 }
 
 // Tile counts and 128-column block counts of V [rank, in] and U [out, rank]
@@ -255,19 +357,47 @@ Geometry geometry(const nq_linear_desc* d) {
 
 int64_t a256(int64_t n) { return (n + 255) & ~int64_t(255); }
 
+// Split of a GEMM with `tiles` (token, sign-row) tiles over K blocks: enough
+// slices to give the GPU about kTargetGroups workgroups, each slice at least
+// kMinSliceBlocks K blocks (the partials cost M x N x 4 bytes per slice).
+constexpr int64_t kTargetGroups = 512;
+constexpr int64_t kMinSliceBlocks = 4;
+
+struct Split {
+    int64_t slices, k_per_split;
+};
+
+Split split_for(int64_t tiles, int64_t k_blocks) {
+    int64_t want = (kTargetGroups + tiles - 1) / tiles;
+    const int64_t most = k_blocks / kMinSliceBlocks;
+    want = want > most ? most : want;
+    want = want < 1 ? 1 : want;
+    Split s;
+    s.k_per_split = (k_blocks + want - 1) / want;
+    s.slices = (k_blocks + s.k_per_split - 1) / s.k_per_split;
+    return s;
+}
+
 struct Scratch {
-    int64_t xs16, scale1, lm, lm16, scale2, total;
+    int64_t xs16, scale1, lm, lm16, scale2, partial, total;
+    Split s1, s2;
 };
 
 Scratch scratch_layout(const nq_linear_desc* d, int64_t tokens) {
     const Geometry g = geometry(d);
+    const int64_t mt = (tokens + kBM - 1) / kBM;
     Scratch s{};
+    s.s1 = split_for(mt * ((d->rank + kBN - 1) / kBN), g.nsc1);
+    s.s2 = split_for(mt * ((d->out_features + kBN - 1) / kBN), g.nsc2);
     s.xs16 = 0;
     s.scale1 = s.xs16 + a256(tokens * g.nsc1 * kBK * 2);
     s.lm = s.scale1 + a256(tokens * 4);
     s.lm16 = s.lm + a256(tokens * d->rank * 4);
     s.scale2 = s.lm16 + a256(tokens * g.nsc2 * kBK * 2);
-    s.total = s.scale2 + a256(tokens * 4);
+    s.partial = s.scale2 + a256(tokens * 4);
+    const int64_t p1 = s.s1.slices > 1 ? s.s1.slices * tokens * d->rank : 0;
+    const int64_t p2 = s.s2.slices > 1 ? s.s2.slices * tokens * d->out_features : 0;
+    s.total = s.partial + a256(4 * (p1 > p2 ? p1 : p2));
     return s;
 }
 
@@ -298,11 +428,16 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     auto* lm = reinterpret_cast<float*>(ws + sl.lm);
     auto* lm16 = reinterpret_cast<_Float16*>(ws + sl.lm16);
     auto* scale2 = reinterpret_cast<float*>(ws + sl.scale2);
+    auto* partial = reinterpret_cast<float*>(ws + sl.partial);
     const auto* base = static_cast<const uint32_t*>(d->tiles);
     const dim3 rows(static_cast<unsigned>(tokens));
+    auto aligned = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+    // Vector row loads: 8 elements per load, 16-byte aligned rows.
+    const int vec1_ok = (d->in_features % 8 == 0 && aligned(x, 16) && aligned(d->scale_pre, 16)) ? 1 : 0;
+    const int vec2 = (d->rank % 8 == 0 && aligned(lm, 16)) ? 1 : 0;
 
     hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, x, x_dtype, d->in_features, d->scale_pre,
-                       d->scale_dtype, d->in_features, geo.nsc1 * kBK, xs16, scale1);
+                       d->scale_dtype, d->in_features, geo.nsc1 * kBK, vec1_ok, xs16, scale1);
     GemmArgs g1{};
     g1.a = xs16;
     g1.m = tokens;
@@ -315,11 +450,18 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     g1.col_scale_dtype = d->scale_dtype;
     g1.out = lm;
     g1.out_dtype = NQ_DTYPE_F32;
-    const dim3 grid1(static_cast<unsigned>((d->rank + kBN - 1) / kBN), static_cast<unsigned>((tokens + kBM - 1) / kBM));
+    g1.k_per_split = sl.s1.k_per_split;
+    g1.partial = sl.s1.slices > 1 ? partial : nullptr;
+    const dim3 grid1(static_cast<unsigned>((d->rank + kBN - 1) / kBN), static_cast<unsigned>((tokens + kBM - 1) / kBM),
+                     static_cast<unsigned>(sl.s1.slices));
     hipLaunchKernelGGL(k_sign_gemm, grid1, dim3(kBlock), 0, stream, g1);
+    if (sl.s1.slices > 1) {
+        const dim3 grid(static_cast<unsigned>((tokens * d->rank + kBlock - 1) / kBlock));
+        hipLaunchKernelGGL(k_reduce_splits, grid, dim3(kBlock), 0, stream, static_cast<int>(sl.s1.slices), g1);
+    }
 
     hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, lm, NQ_DTYPE_F32, d->rank, nullptr, 0, d->rank,
-                       geo.nsc2 * kBK, lm16, scale2);
+                       geo.nsc2 * kBK, vec2, lm16, scale2);
     GemmArgs g2{};
     g2.a = lm16;
     g2.m = tokens;
@@ -343,9 +485,15 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     g2.bias_dtype = d->bias_dtype;
     g2.out = y;
     g2.out_dtype = y_dtype;
+    g2.k_per_split = sl.s2.k_per_split;
+    g2.partial = sl.s2.slices > 1 ? partial : nullptr;
     const dim3 grid2(static_cast<unsigned>((d->out_features + kBN - 1) / kBN),
-                     static_cast<unsigned>((tokens + kBM - 1) / kBM));
+                     static_cast<unsigned>((tokens + kBM - 1) / kBM), static_cast<unsigned>(sl.s2.slices));
     hipLaunchKernelGGL(k_sign_gemm, grid2, dim3(kBlock), 0, stream, g2);
+    if (sl.s2.slices > 1) {
+        const dim3 grid(static_cast<unsigned>((tokens * d->out_features + kBlock - 1) / kBlock));
+        hipLaunchKernelGGL(k_reduce_splits, grid, dim3(kBlock), 0, stream, static_cast<int>(sl.s2.slices), g2);
+    }
     return launch_status();
 }
 
