@@ -47,6 +47,9 @@ def parse_args(argv=None):
                    help="token counts of the Llama-3-8B prefill sweep ('' to skip)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 10 times (byte-counter calibration) and exit")
+    p.add_argument("--dominant-only", action="store_true",
+                   help="only launch the dominant call (gate/up batch) of every layer eagerly --steps times "
+                        "(per-dispatch counter collection) and exit")
     return p.parse_args(argv)
 
 
@@ -171,10 +174,46 @@ def time_mode(backend, stack, mode: str, steps: int, warmup: int, use_graph: boo
     }
 
 
-def measured_traffic(mode: str, tokens: int, layers: int):
-    """HBM bytes per call from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
-    summary (calibrated against a plain copy), when it was measured on this
-    exact workload; None otherwise. Counters cannot be read inside a timed run."""
+# The dominant decode call: the gate/up batch (two 4096 -> 12288 linears that
+# share x), the largest byte count of any call in a decode step.
+DOMINANT_GROUP = (4, 5)
+
+
+def time_dominant_call(backend, stack, steps: int, warmup: int) -> dict:
+    """Mean duration of the dominant call (gate/up batch, k_decode_stage1 +
+    k_decode_stage2) over the stack's distinct layers, captured in one HIP
+    graph and bracketed by events recorded on the stream the graph runs on."""
+
+    import torch
+
+    calls = [[entries[i] for i in DOMINANT_GROUP] for entries in stack]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run_step(backend, calls)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            run_step(backend, calls)
+        for _ in range(warmup):
+            graph.replay()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(side)
+        for _ in range(steps):
+            graph.replay()
+        stop.record(side)
+    stop.synchronize()
+    tokens = calls[0][0][2].shape[0]
+    call_us = start.elapsed_time(stop) * 1e3 / (steps * len(calls))
+    call_bytes = sum(algorithmic_bytes(m[0], tokens) for m in calls[0])
+    return {"mean_call_us": call_us, "bytes_per_call": call_bytes,
+            "achieved_gbs": call_bytes / (call_us * 1e-6) / 1e9, "calls": len(calls)}
+
+
+def measured_traffic(tokens: int, layers: int):
+    """HBM bytes per dominant call from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a plain copy), when it was measured
+    on this exact workload; None otherwise. Counters cannot be read inside a
+    timed run."""
 
     import re
 
@@ -182,8 +221,8 @@ def measured_traffic(mode: str, tokens: int, layers: int):
         text = TRAFFIC_PROFILE.read_text()
     except OSError:
         return None
-    m = re.search(r"traffic_bytes_per_call = (\d+) \(grouping (\S+), tokens (\d+), layers (\d+)\)", text)
-    if not m or (m.group(2), int(m.group(3)), int(m.group(4))) != (mode, tokens, layers):
+    m = re.search(r"traffic_bytes_per_call = (\d+) \(call gate/up, tokens (\d+), layers (\d+)\)", text)
+    if not m or (int(m.group(2)), int(m.group(3))) != (tokens, layers):
         return None
     return int(m.group(1))
 
@@ -331,6 +370,14 @@ def main(argv=None) -> int:
     print(f"[bench] building {args.layers}-layer stack, M={args.tokens}", file=sys.stderr, flush=True)
     backend, stack = build_stack(args.layers, args.tokens, device)
     torch.cuda.synchronize()
+    if args.dominant_only:
+        calls = [[entries[i] for i in DOMINANT_GROUP] for entries in stack]
+        for _ in range(args.steps):
+            run_step(backend, calls)
+        torch.cuda.synchronize()
+        print(json.dumps({"dominant_calls": args.steps * len(calls),
+                          "bytes_per_call": sum(algorithmic_bytes(m[0], args.tokens) for m in calls[0])}))
+        return 0
     modes = {}
     for mode in modes_wanted:
         print(f"[bench] mode {mode}: timing {args.steps} steps", file=sys.stderr, flush=True)
@@ -338,7 +385,9 @@ def main(argv=None) -> int:
     head_mode = modes_wanted[0]
     head = modes[head_mode]
     ms_per_step = head["ms_per_step"]
-    achieved = head["achieved_gbs"]
+    print("[bench] dominant call (gate/up batch) timing", file=sys.stderr, flush=True)
+    dom = time_dominant_call(backend, stack, args.steps, args.warmup)
+    achieved = dom["achieved_gbs"]
 
     result = {
         "metric": METRIC,
@@ -371,12 +420,13 @@ def main(argv=None) -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(head_mode, args.tokens, args.layers),
+            "traffic": measured_traffic(args.tokens, args.layers),
             "traffic_source": TRAFFIC_PROFILE.name,
-            "kernel": (f"one decode call = k_decode_fused" if head_mode.endswith("-fused") else
-                       "one decode call = k_decode_stage1 + k_decode_stage2") + f" (grouping '{head_mode}')",
-            "bytes_per_call": round(head["bytes_per_call"]),
-            "mean_call_us": round(head["mean_call_us"], 3),
+            "kernel": ("dominant decode call: gate/up batch (two 4096->12288 r3072 linears sharing x) = "
+                       "k_decode_stage1 + k_decode_stage2, graph of one call per layer"),
+            "bytes_per_call": round(dom["bytes_per_call"]),
+            "mean_call_us": round(dom["mean_call_us"], 3),
+            "step_achieved_gbs": round(head["achieved_gbs"], 1),
         },
         "calls_per_step": head["calls_per_step"],
         "kernels_per_step": head["kernels_per_step"],
