@@ -136,15 +136,18 @@ int nq_count_bad_padding(const int32_t* words, int64_t rows, int64_t cols,
                          int64_t row_stride_words, int32_t* bad_rows, void* stream);
 
 /* Bytes of the synchronisation header at the start of a tiles buffer. It holds
- * monotonic launch counters (never reset; graph replays are safe) and, on its
- * last 256-byte line, word 0 = sticky error flag (set if a decode launch ever
- * timed out waiting for its stage-1 results), word 1 = magic 0x4E515432,
- * word 2 = max|s_in| as fp32 bits. The header is per layer: launches that use
- * one prepared layer must not overlap in time (one stream, or ordered
- * streams). No reference counterpart. */
+ * the fused launch's monotonic counters (never reset; graph replays are safe)
+ * and, on its last 256-byte line, word 0 = sticky error flag (set if a fused
+ * decode launch ever timed out waiting for its stage-1 results), word 1 =
+ * magic 0x4E515433, word 2 = max|s_mid| as fp32 bits (bounds the stage-1
+ * results so the decode epilogue can pick their fixed-point exponent). The
+ * header is per layer: launches that use one prepared layer must not overlap
+ * in time (one stream, or ordered streams). No reference counterpart. */
 int64_t nq_tiles_header_bytes(void);
 
-/* Size in bytes of the GPU-private tiled weight layout for one linear. */
+/* Size in bytes of the GPU-private tiled weight layout for one linear:
+ * header, V tiles, U tiles and 256 bytes of tail padding (the decode kernels
+ * read whole 16-byte words per lane from clamped addresses). */
 int64_t nq_tiles_bytes(int64_t in_features, int64_t out_features, int64_t rank);
 
 /* Re-tile the canonical U and V words of `desc` into the GPU-private decode
