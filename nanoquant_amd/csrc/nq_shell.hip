@@ -1,0 +1,784 @@
+// Decoder-shell kernels for batch-1 autoregressive decode around the packed
+// linears on gfx950 (Qwen3 geometry): embedding gather, residual add +
+// RMSNorm, per-head q/k RMSNorm + rotate-half RoPE + KV-cache append,
+// split-sequence grouped-query attention, SiLU-gated product, bf16 output
+// projection with per-workgroup argmax partials, and greedy selection.
+//
+// All kernels read the token position from device memory, so one captured
+// decode step replays for every position. Every reduction runs in a fixed
+// order (wave butterflies, then waves in index order, then sequence blocks in
+// index order), so results are identical from run to run.
+#include <math.h>
+
+#include "nq_common.h"
+#include "../../include/nqamd_shell.h"
+
+namespace {
+
+using nq::f32_to_bf16_bits;
+
+constexpr int kWave = 64;
+constexpr int kSeqBlock = 64;           // cache rows per attention block
+constexpr int kRowThreads = 256;        // per-row kernels
+constexpr int kProjWaves = 4;           // output projection: waves per workgroup
+constexpr int kProjLoads = 32;          // 16-byte weight loads per lane in flight
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Elements [i, i + 8) of a typed buffer as fp32; i % 8 == 0 and the buffer is
+// 16-byte aligned (checked on the host).
+__device__ __forceinline__ void load8(const void* __restrict__ p, int dtype, int64_t i, float (&v)[8]) {
+    if (dtype == NQ_DTYPE_F32) {
+        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        const float4 a = q[0], b = q[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        return;
+    }
+    const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    if (dtype == NQ_DTYPE_BF16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = bf16_lo(w[j]);
+            v[2 * j + 1] = bf16_hi(w[j]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[j] & 0xffffu)));
+            v[2 * j + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[j] >> 16)));
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t pack2(int dtype, float a, float b) {
+    if (dtype == NQ_DTYPE_BF16) return f32_to_bf16_bits(a) | (static_cast<uint32_t>(f32_to_bf16_bits(b)) << 16);
+    const uint16_t ha = __builtin_bit_cast(uint16_t, static_cast<_Float16>(a));
+    const uint16_t hb = __builtin_bit_cast(uint16_t, static_cast<_Float16>(b));
+    return ha | (static_cast<uint32_t>(hb) << 16);
+}
+
+__device__ __forceinline__ void store8(void* __restrict__ p, int dtype, int64_t i, const float (&v)[8]) {
+    if (dtype == NQ_DTYPE_F32) {
+        float4* q = reinterpret_cast<float4*>(static_cast<float*>(p) + i);
+        q[0] = make_float4(v[0], v[1], v[2], v[3]);
+        q[1] = make_float4(v[4], v[5], v[6], v[7]);
+        return;
+    }
+    uint4 u;
+    u.x = pack2(dtype, v[0], v[1]);
+    u.y = pack2(dtype, v[2], v[3]);
+    u.z = pack2(dtype, v[4], v[5]);
+    u.w = pack2(dtype, v[6], v[7]);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = u;
+}
+
+// Sum over a 256-thread block: wave butterflies, then the four wave sums in
+// wave order (every thread gets the same value).
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+    __syncthreads();
+    const float total = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return total;
+}
+
+// ---------------------------------------------------------------------------
+// Embedding gather.
+
+__global__ __launch_bounds__(kRowThreads) void k_embedding(const int64_t* __restrict__ ids, const void* __restrict__ table,
+                                                           int dtype, int64_t vocab, int64_t hidden,
+                                                           const float* __restrict__ scale, float* __restrict__ out) {
+    const int64_t t = blockIdx.x;
+    const int64_t id = ids[t];
+    const bool ok = id >= 0 && id < vocab;
+    const float s = scale ? scale[0] : 1.0f;
+    for (int64_t i = threadIdx.x * 8; i < hidden; i += kRowThreads * 8) {
+        float v[8];
+        if (ok) {
+            load8(table, dtype, id * hidden + i, v);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __fmul_rn(v[j], s);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __builtin_nanf("");
+        }
+        store8(out, NQ_DTYPE_F32, t * hidden + i, v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Residual add + RMSNorm (one workgroup per token row).
+
+__global__ __launch_bounds__(kRowThreads) void k_add_rmsnorm(float* __restrict__ residual, const void* __restrict__ delta,
+                                                             int ddt, const void* __restrict__ weight, int wdt,
+                                                             float eps, int64_t hidden, void* __restrict__ out, int odt) {
+    __shared__ float red[kRowThreads / kWave];
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * hidden;
+    float ss = 0.0f;
+    for (int64_t i = threadIdx.x * 8; i < hidden; i += kRowThreads * 8) {
+        float v[8];
+        load8(residual, NQ_DTYPE_F32, row + i, v);
+        if (delta) {
+            float d[8];
+            load8(delta, ddt, row + i, d);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = __fadd_rn(v[j], d[j]);
+            store8(residual, NQ_DTYPE_F32, row + i, v);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+    }
+    const float total = block_sum256(ss, red);
+    const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
+    for (int64_t i = threadIdx.x * 8; i < hidden; i += kRowThreads * 8) {
+        float v[8], w[8];
+        load8(residual, NQ_DTYPE_F32, row + i, v);  // this thread's own values
+        load8(weight, wdt, i, w);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __fmul_rn(w[j], __fmul_rn(v[j], inv));
+        store8(out, odt, row + i, v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// q/k per-head RMSNorm + rotate-half RoPE + KV-cache append. One wave per
+// (token, head); grid.y = q_heads + kv_heads. Lane l holds elements
+// d = l + 64 j, so for head_dim >= 128 the rotate-half partner d +- D/2 is
+// element j +- E/2 of the same lane; for head_dim 64 it is lane l ^ 32.
+
+template <int D>
+__global__ __launch_bounds__(kWave) void k_qk_norm_rope_cache(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int q_heads,
+    int kv_heads, const void* __restrict__ q_norm, const void* __restrict__ k_norm, int ndt, float eps,
+    const float* __restrict__ cos_table, const float* __restrict__ sin_table, const int32_t* __restrict__ position,
+    int64_t max_positions, float* __restrict__ q_out, void* __restrict__ k_cache, void* __restrict__ v_cache, int cdt) {
+    constexpr int E = D / kWave;
+    constexpr int kHalf = D / 2;
+    const int64_t t = blockIdx.x;
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int64_t pos = static_cast<int64_t>(position[0]) + t;
+    if (pos < 0 || pos >= max_positions) return;
+    const bool is_q = h < q_heads;
+    const int g = is_q ? h : h - q_heads;
+    const float* src = is_q ? q + (t * q_heads + h) * D : k + (t * kv_heads + g) * D;
+    const void* nw = is_q ? q_norm : k_norm;
+    float x[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) x[j] = src[lane + kWave * j];
+    if (nw) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < E; ++j) ss = fmaf(x[j], x[j], ss);
+        ss = wave_sum(ss);
+        const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+        for (int j = 0; j < E; ++j) x[j] = __fmul_rn(nq::load_f32(nw, ndt, lane + kWave * j), __fmul_rn(x[j], inv));
+    }
+    const float* cr = cos_table + pos * kHalf;
+    const float* sr = sin_table + pos * kHalf;
+    float y[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int d = lane + kWave * j;
+        const bool first = d < kHalf;
+        float partner;
+        if constexpr (E == 1) {
+            partner = __shfl_xor(x[0], 32, kWave);
+        } else {
+            partner = first ? x[j + E / 2] : x[j - E / 2];
+        }
+        const int fi = first ? d : d - kHalf;
+        const float rot = first ? -partner : partner;
+        y[j] = __fadd_rn(__fmul_rn(x[j], cr[fi]), __fmul_rn(rot, sr[fi]));
+    }
+    if (is_q) {
+        float* dst = q_out + (t * q_heads + h) * D;
+#pragma unroll
+        for (int j = 0; j < E; ++j) dst[lane + kWave * j] = y[j];
+        return;
+    }
+    const int64_t crow = (static_cast<int64_t>(g) * max_positions + pos) * D;
+    const float* vs = v + (t * kv_heads + g) * D;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int d = lane + kWave * j;
+        nq::store_f32_as(k_cache, cdt, crow + d, y[j]);
+        nq::store_f32_as(v_cache, cdt, crow + d, vs[d]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention, pass 1: one workgroup per (kv head, block of QT queries,
+// 64-row cache block s); wave w serves q head kv_head * G + w. The K rows of
+// the block are copied to LDS as stored (16-byte copies, padded rows); lane j
+// scores cache row 64 s + j against the query (fp32, in LDS), the wave forms
+// its softmax partial (max m, sum l) and lane pairs of dimensions accumulate
+// P.V straight from the V rows (all waves of the workgroup read the same rows,
+// so they come from cache). The partial goes to the workspace.
+
+template <int CT>
+constexpr int cache_bytes() { return CT == NQ_DTYPE_F32 ? 4 : 2; }
+
+template <int D, int CT>
+constexpr int k_row_bytes() { return D * cache_bytes<CT>() + 16; }
+
+template <int D, int CT>
+constexpr size_t attention_lds(int waves) {
+    return static_cast<size_t>(kSeqBlock) * k_row_bytes<D, CT>() + static_cast<size_t>(waves) * (D + kSeqBlock) * 4;
+}
+
+template <int CT>
+__device__ __forceinline__ float cache_value(uint32_t bits16) {
+    if constexpr (CT == NQ_DTYPE_BF16) return __uint_as_float(bits16 << 16);
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+// Dot product of one staged K row with the query (both D long).
+template <int D, int CT>
+__device__ __forceinline__ float k_row_dot(const char* __restrict__ kr, const float* __restrict__ qw) {
+    float acc = 0.0f;
+    if constexpr (CT == NQ_DTYPE_F32) {
+#pragma unroll 8
+        for (int d = 0; d < D; d += 4) {
+            const float4 kk = *reinterpret_cast<const float4*>(kr + 4 * d);
+            const float4 qq = *reinterpret_cast<const float4*>(qw + d);
+            acc = fmaf(kk.x, qq.x, acc);
+            acc = fmaf(kk.y, qq.y, acc);
+            acc = fmaf(kk.z, qq.z, acc);
+            acc = fmaf(kk.w, qq.w, acc);
+        }
+    } else {
+#pragma unroll 4
+        for (int d = 0; d < D; d += 8) {
+            const uint4 u = *reinterpret_cast<const uint4*>(kr + 2 * d);
+            const float4 qa = *reinterpret_cast<const float4*>(qw + d);
+            const float4 qb = *reinterpret_cast<const float4*>(qw + d + 4);
+            acc = fmaf(cache_value<CT>(u.x & 0xffffu), qa.x, acc);
+            acc = fmaf(cache_value<CT>(u.x >> 16), qa.y, acc);
+            acc = fmaf(cache_value<CT>(u.y & 0xffffu), qa.z, acc);
+            acc = fmaf(cache_value<CT>(u.y >> 16), qa.w, acc);
+            acc = fmaf(cache_value<CT>(u.z & 0xffffu), qb.x, acc);
+            acc = fmaf(cache_value<CT>(u.z >> 16), qb.y, acc);
+            acc = fmaf(cache_value<CT>(u.w & 0xffffu), qb.z, acc);
+            acc = fmaf(cache_value<CT>(u.w >> 16), qb.w, acc);
+        }
+    }
+    return acc;
+}
+
+// E consecutive cache elements (E = D / 64, lane's dimensions) as fp32.
+template <int E, int CT>
+__device__ __forceinline__ void load_v(const char* __restrict__ p, float (&v)[E]) {
+    if constexpr (CT == NQ_DTYPE_F32) {
+#pragma unroll
+        for (int j = 0; j < E; ++j) v[j] = reinterpret_cast<const float*>(p)[j];
+    } else if constexpr (E == 1) {
+        v[0] = cache_value<CT>(*reinterpret_cast<const uint16_t*>(p));
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; j += 2) {
+            const uint32_t u = reinterpret_cast<const uint32_t*>(p)[j / 2];
+            v[j] = cache_value<CT>(u & 0xffffu);
+            v[j + 1] = cache_value<CT>(u >> 16);
+        }
+    }
+}
+
+__device__ __forceinline__ int64_t attn_part_index(int64_t t, int h, int s, int q_heads, int blocks) {
+    return (t * q_heads + h) * blocks + s;
+}
+
+template <int D, int CT>
+__global__ __launch_bounds__(1024) void k_attention_blocks(const float* __restrict__ q, const char* __restrict__ k_cache,
+                                                           const char* __restrict__ v_cache, int64_t tokens,
+                                                           int q_heads, int kv_heads, int qt,
+                                                           const int32_t* __restrict__ position, int64_t max_positions,
+                                                           float scaling, float* __restrict__ part_ml,
+                                                           float* __restrict__ part_acc) {
+    constexpr int E = D / kWave;
+    constexpr int EB = cache_bytes<CT>();
+    constexpr int RB = k_row_bytes<D, CT>();
+    constexpr int PIECES = D * EB / 16;  // 16-byte pieces per row
+    constexpr int U = 8;                 // V rows per unrolled step
+    extern __shared__ float lds_raw[];
+    char* klds = reinterpret_cast<char*>(lds_raw);
+    float* qv = reinterpret_cast<float*>(klds + kSeqBlock * RB);  // [waves][D]
+    float* pv = qv + (blockDim.x / kWave) * D;                     // [waves][64]
+
+    const int group = q_heads / kv_heads;
+    const int g = blockIdx.x % kv_heads;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x / kv_heads) * qt;
+    const int s = blockIdx.y;
+    const int blocks = gridDim.y;
+    const int64_t p0 = position[0];
+    const int64_t row0 = static_cast<int64_t>(s) * kSeqBlock;
+    const int64_t t_end = t0 + qt < tokens ? t0 + qt : tokens;
+    // Highest cache row any query of this workgroup may see.
+    int64_t last = p0 + t_end - 1;
+    if (last >= max_positions) last = max_positions - 1;
+    if (p0 < 0 || row0 > last) return;  // uniform: no query of this workgroup reaches row0
+    const int rows = static_cast<int>((last - row0 + 1) < kSeqBlock ? (last - row0 + 1) : kSeqBlock);
+
+    // Copy K rows [row0, row0 + rows) of kv head g to LDS as stored.
+    const int64_t head_row0 = static_cast<int64_t>(g) * max_positions + row0;
+    const char* kbase = k_cache + head_row0 * D * EB;
+    for (int i = threadIdx.x; i < rows * PIECES; i += blockDim.x) {
+        const int r = i / PIECES, c = i % PIECES;
+        *reinterpret_cast<uint4*>(klds + r * RB + 16 * c) =
+            *reinterpret_cast<const uint4*>(kbase + (static_cast<int64_t>(r) * D) * EB + 16 * c);
+    }
+    const int w = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int h = g * group + w;
+    float* qw = qv + w * D;
+    float* pw = pv + w * kSeqBlock;
+    const char* vlane = v_cache + (head_row0 * D + lane * E) * EB;
+    __syncthreads();
+
+    for (int64_t t = t0; t < t_end; ++t) {
+        const int64_t pt = p0 + t;
+        if (pt < row0 || pt >= max_positions) continue;  // uniform per workgroup
+        const float* qs = q + (t * q_heads + h) * D;
+#pragma unroll
+        for (int j = 0; j < E; ++j) qw[lane + kWave * j] = qs[lane + kWave * j];
+        __builtin_amdgcn_wave_barrier();
+        const int nvalid = static_cast<int>((pt - row0 + 1) < kSeqBlock ? (pt - row0 + 1) : kSeqBlock);
+        const bool valid = lane < nvalid;
+        // Lanes past the staged rows score row 0 (always staged) and are masked.
+        const float dot = k_row_dot<D, CT>(klds + (lane < rows ? lane : 0) * RB, qw);
+        const float score = valid ? dot * scaling : -INFINITY;
+        const float m = wave_max(score);
+        const float p = valid ? expf(score - m) : 0.0f;
+        const float l = wave_sum(p);
+        pw[lane] = p;
+        __builtin_amdgcn_wave_barrier();
+        float acc[E];
+#pragma unroll
+        for (int j = 0; j < E; ++j) acc[j] = 0.0f;
+        for (int r0 = 0; r0 < nvalid; r0 += U) {
+            float vv[U][E];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int r = r0 + u < nvalid ? r0 + u : nvalid - 1;  // p is 0 past nvalid
+                load_v<E, CT>(vlane + static_cast<int64_t>(r) * D * EB, vv[u]);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float pr = pw[(r0 + u) & (kSeqBlock - 1)];
+#pragma unroll
+                for (int j = 0; j < E; ++j) acc[j] = fmaf(pr, vv[u][j], acc[j]);
+            }
+        }
+        const int64_t pi = attn_part_index(t, h, s, q_heads, blocks);
+        if (lane == 0) {
+            part_ml[2 * pi] = m;
+            part_ml[2 * pi + 1] = l;
+        }
+        float* pa = part_acc + pi * D + lane * E;
+#pragma unroll
+        for (int j = 0; j < E; ++j) pa[j] = acc[j];
+        __builtin_amdgcn_wave_barrier();  // qw / pw are rewritten for the next query
+    }
+}
+
+// Attention, pass 2: merge the blocks of one (token, q head) in block order.
+template <int D>
+__global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__ part_ml, const float* __restrict__ part_acc,
+                                                       int q_heads, int blocks, const int32_t* __restrict__ position,
+                                                       int64_t max_positions, void* __restrict__ out, int odt) {
+    const int h = blockIdx.x;
+    const int64_t t = blockIdx.y;
+    const int d = threadIdx.x;
+    const int64_t pt = static_cast<int64_t>(position[0]) + t;
+    const int64_t o = (t * q_heads + h) * D + d;
+    if (pt < 0 || pt >= max_positions) {
+        nq::store_f32_as(out, odt, o, 0.0f);
+        return;
+    }
+    const int nb = static_cast<int>(pt / kSeqBlock) + 1;
+    const int64_t p0 = attn_part_index(t, h, 0, q_heads, blocks);
+    float mmax = -INFINITY;
+    for (int b = 0; b < nb; ++b) mmax = fmaxf(mmax, part_ml[2 * (p0 + b)]);
+    float lsum = 0.0f, acc = 0.0f;
+    for (int b = 0; b < nb; ++b) {
+        const float f = expf(part_ml[2 * (p0 + b)] - mmax);
+        lsum = fmaf(part_ml[2 * (p0 + b) + 1], f, lsum);
+        acc = fmaf(part_acc[(p0 + b) * D + d], f, acc);
+    }
+    nq::store_f32_as(out, odt, o, acc / lsum);
+}
+
+// ---------------------------------------------------------------------------
+// SiLU-gated product.
+
+__global__ __launch_bounds__(kRowThreads) void k_silu_mul(const float* __restrict__ gate, const float* __restrict__ up,
+                                                          int64_t n, void* __restrict__ out, int odt) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * kRowThreads + threadIdx.x) * 8;
+    if (i >= n) return;
+    float gv[8], uv[8];
+    load8(gate, NQ_DTYPE_F32, i, gv);
+    load8(up, NQ_DTYPE_F32, i, uv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) gv[j] = __fmul_rn(gv[j] / (1.0f + expf(-gv[j])), uv[j]);
+    store8(out, odt, i, gv);
+}
+
+// ---------------------------------------------------------------------------
+// Output projection: logits = W x for one token, W bf16 [vocab, hidden].
+// Wave w of workgroup b owns RW = kProjLoads / NCH consecutive rows; lane l
+// reads 8-element chunk k * 64 + l of each row for k < NCH, so all of a
+// wave's RW * NCH 16-byte loads are issued before the first is used. x is
+// staged in LDS as fp32. Each workgroup also writes its best (logit, index)
+// as one orderable 64-bit key.
+
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<uint64_t>(u) << 32) | static_cast<uint64_t>(0xffffffffu - idx);
+}
+
+template <int NCH>
+__global__ __launch_bounds__(kProjWaves * kWave) void k_output_projection(const void* __restrict__ x, int xdt,
+                                                                          const uint16_t* __restrict__ weight,
+                                                                          int64_t vocab, int64_t hidden,
+                                                                          float* __restrict__ logits,
+                                                                          uint64_t* __restrict__ partial) {
+    constexpr int RW = kProjLoads / NCH;
+    __shared__ float xs[NCH * kWave * 8];
+    __shared__ uint64_t best[kProjWaves];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = threadIdx.x / kWave;
+    const int64_t chunks = hidden / 8;
+    const int64_t row0 = (static_cast<int64_t>(blockIdx.x) * kProjWaves + w) * RW;
+
+    // Weight loads first (clamped rows and chunks; masked in the arithmetic).
+    uint4 wv[RW][NCH];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const int64_t row = row0 + r < vocab ? row0 + r : vocab - 1;
+#pragma unroll
+        for (int kk = 0; kk < NCH; ++kk) {
+            const int64_t c = kk * kWave + lane;
+            const int64_t cc = c < chunks ? c : chunks - 1;
+            wv[r][kk] = *reinterpret_cast<const uint4*>(weight + row * hidden + cc * 8);
+        }
+    }
+    for (int64_t i = threadIdx.x * 8; i < static_cast<int64_t>(NCH) * kWave * 8; i += kProjWaves * kWave * 8) {
+        float v[8];
+        if (i < hidden) {
+            load8(x, xdt, i, v);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+        }
+        float4* d = reinterpret_cast<float4*>(&xs[i]);
+        d[0] = make_float4(v[0], v[1], v[2], v[3]);
+        d[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    __syncthreads();
+
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < NCH; ++kk) {
+        const int64_t c = kk * kWave + lane;
+        const float4 xa = *reinterpret_cast<const float4*>(&xs[c * 8]);
+        const float4 xb = *reinterpret_cast<const float4*>(&xs[c * 8 + 4]);
+        const bool live = c < chunks;
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            const uint4 u = wv[r][kk];
+            float a = acc[r];
+            a = fmaf(bf16_lo(u.x), xa.x, a);
+            a = fmaf(bf16_hi(u.x), xa.y, a);
+            a = fmaf(bf16_lo(u.y), xa.z, a);
+            a = fmaf(bf16_hi(u.y), xa.w, a);
+            a = fmaf(bf16_lo(u.z), xb.x, a);
+            a = fmaf(bf16_hi(u.z), xb.y, a);
+            a = fmaf(bf16_lo(u.w), xb.z, a);
+            a = fmaf(bf16_hi(u.w), xb.w, a);
+            acc[r] = live ? a : acc[r];
+        }
+    }
+    uint64_t key = 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const float sum = wave_sum(acc[r]);
+        const int64_t row = row0 + r;
+        if (row < vocab) {
+            if (lane == r) logits[row] = sum;
+            const uint64_t kr = argmax_key(sum, static_cast<uint32_t>(row));
+            key = kr > key ? kr : key;
+        }
+    }
+    if (lane == 0) best[w] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = best[0];
+#pragma unroll
+        for (int i = 1; i < kProjWaves; ++i) b = best[i] > b ? best[i] : b;
+        partial[blockIdx.x] = b;
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_greedy_select(const uint64_t* __restrict__ partial, int64_t count,
+                                                        int64_t* __restrict__ token_out, int64_t* __restrict__ history,
+                                                        int64_t history_capacity, int32_t* __restrict__ step,
+                                                        int32_t* __restrict__ position) {
+    __shared__ uint64_t red[1024 / kWave];
+    uint64_t key = 0;
+    for (int64_t i = threadIdx.x; i < count; i += blockDim.x) key = partial[i] > key ? partial[i] : key;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t lo = __shfl_xor(static_cast<uint32_t>(key), o, kWave);
+        const uint32_t hi = __shfl_xor(static_cast<uint32_t>(key >> 32), o, kWave);
+        const uint64_t other = (static_cast<uint64_t>(hi) << 32) | lo;
+        key = other > key ? other : key;
+    }
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = key;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint64_t b = red[0];
+        for (int i = 1; i < static_cast<int>(blockDim.x / kWave); ++i) b = red[i] > b ? red[i] : b;
+        const int64_t token = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(b & 0xffffffffu));
+        token_out[0] = token;
+        if (history && step) {
+            const int32_t k = step[0];
+            if (k >= 0 && k < history_capacity) history[k] = token;
+            step[0] = k + 1;
+        }
+        if (position) position[0] += 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host helpers.
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool float_code(int d) { return nq::is_float_dtype(d); }
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+int proj_chunks_per_lane(int64_t hidden) {
+    for (int n : {1, 2, 4, 8, 16})
+        if (static_cast<int64_t>(n) * kWave * 8 >= hidden) return n;
+    return 0;
+}
+
+int64_t proj_workgroups(int64_t vocab, int64_t hidden) {
+    const int nch = proj_chunks_per_lane(hidden);
+    if (nch == 0) return -1;
+    const int64_t rows = static_cast<int64_t>(kProjWaves) * (kProjLoads / nch);
+    return (vocab + rows - 1) / rows;
+}
+
+int attention_blocks(int64_t max_positions) { return static_cast<int>((max_positions + kSeqBlock - 1) / kSeqBlock); }
+
+template <int D, int CT>
+int launch_attention(const float* q, const void* kc, const void* vc, int64_t tokens, int q_heads, int kv_heads,
+                     const int32_t* position, int64_t max_positions, float scaling, void* out, int odt, float* ml,
+                     float* acc, hipStream_t st) {
+    const int group = q_heads / kv_heads;
+    const int qt = tokens == 1 ? 1 : 16;
+    const int blocks = attention_blocks(max_positions);
+    const int64_t qblocks = (tokens + qt - 1) / qt;
+    const size_t lds = attention_lds<D, CT>(group);
+    if (lds > 64 * 1024) return NQ_ERR_UNSUPPORTED;
+    if (qblocks * kv_heads > 0x7fffffff) return NQ_ERR_SHAPE;
+    dim3 grid(static_cast<unsigned>(qblocks * kv_heads), static_cast<unsigned>(blocks));
+    hipLaunchKernelGGL((k_attention_blocks<D, CT>), grid, dim3(group * kWave), lds, st, q,
+                       static_cast<const char*>(kc), static_cast<const char*>(vc), tokens, q_heads, kv_heads, qt,
+                       position, max_positions, scaling, ml, acc);
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_attention_merge<D>, dim3(q_heads, static_cast<unsigned>(tokens)), dim3(D), 0, st, ml, acc,
+                       q_heads, blocks, position, max_positions, out, odt);
+    return nq::launch_status();
+}
+
+template <int D>
+int launch_attention_for(int cdt, const float* q, const void* kc, const void* vc, int64_t tokens, int q_heads,
+                         int kv_heads, const int32_t* position, int64_t max_positions, float scaling, void* out,
+                         int odt, float* ml, float* acc, hipStream_t st) {
+    switch (cdt) {
+        case NQ_DTYPE_F32:
+            return launch_attention<D, NQ_DTYPE_F32>(q, kc, vc, tokens, q_heads, kv_heads, position, max_positions,
+                                                     scaling, out, odt, ml, acc, st);
+        case NQ_DTYPE_F16:
+            return launch_attention<D, NQ_DTYPE_F16>(q, kc, vc, tokens, q_heads, kv_heads, position, max_positions,
+                                                     scaling, out, odt, ml, acc, st);
+        case NQ_DTYPE_BF16:
+            return launch_attention<D, NQ_DTYPE_BF16>(q, kc, vc, tokens, q_heads, kv_heads, position, max_positions,
+                                                      scaling, out, odt, ml, acc, st);
+        default:
+            return NQ_ERR_DTYPE;
+    }
+}
+
+}  // namespace
+
+extern "C" int nq_embedding(const int64_t* ids, int64_t tokens, const void* table, int32_t table_dtype, int64_t vocab,
+                            int64_t hidden, const float* scale, float* out, void* stream) {
+    if (!ids || !table || !out) return NQ_ERR_ARGUMENT;
+    if (!float_code(table_dtype)) return NQ_ERR_DTYPE;
+    if (tokens <= 0 || tokens > 0x7fffffff || vocab <= 0 || hidden <= 0 || hidden % 8) return NQ_ERR_SHAPE;
+    if (!aligned16(table) || !aligned16(out)) return NQ_ERR_ALIGNMENT;
+    hipLaunchKernelGGL(k_embedding, dim3(static_cast<unsigned>(tokens)), dim3(kRowThreads), 0, as_stream(stream), ids,
+                       table, table_dtype, vocab, hidden, scale, out);
+    return nq::launch_status();
+}
+
+extern "C" int nq_add_rmsnorm(float* residual, const void* delta, int32_t delta_dtype, const void* weight,
+                              int32_t weight_dtype, float eps, int64_t tokens, int64_t hidden, void* out,
+                              int32_t out_dtype, void* stream) {
+    if (!residual || !weight || !out) return NQ_ERR_ARGUMENT;
+    if ((delta && !float_code(delta_dtype)) || !float_code(weight_dtype) || !float_code(out_dtype)) return NQ_ERR_DTYPE;
+    if (tokens <= 0 || tokens > 0x7fffffff || hidden <= 0 || hidden % 8) return NQ_ERR_SHAPE;
+    if (!(eps >= 0.0f)) return NQ_ERR_ARGUMENT;
+    if (!aligned16(residual) || (delta && !aligned16(delta)) || !aligned16(weight) || !aligned16(out))
+        return NQ_ERR_ALIGNMENT;
+    hipLaunchKernelGGL(k_add_rmsnorm, dim3(static_cast<unsigned>(tokens)), dim3(kRowThreads), 0, as_stream(stream),
+                       residual, delta, delta_dtype, weight, weight_dtype, eps, hidden, out, out_dtype);
+    return nq::launch_status();
+}
+
+extern "C" int nq_qk_norm_rope_cache(const float* q, const float* k, const float* v, int64_t tokens, int32_t q_heads,
+                                     int32_t kv_heads, int32_t head_dim, const void* q_norm, const void* k_norm,
+                                     int32_t norm_dtype, float eps, const float* cos_table, const float* sin_table,
+                                     const int32_t* position, int64_t max_positions, float* q_out, void* k_cache,
+                                     void* v_cache, int32_t cache_dtype, void* stream) {
+    if (!q || !k || !v || !cos_table || !sin_table || !position || !q_out || !k_cache || !v_cache)
+        return NQ_ERR_ARGUMENT;
+    if (((q_norm || k_norm) && !float_code(norm_dtype)) || !float_code(cache_dtype)) return NQ_ERR_DTYPE;
+    if (tokens <= 0 || tokens > 0x7fffffff || q_heads <= 0 || kv_heads <= 0 || q_heads + kv_heads > 65535 ||
+        max_positions <= 0)
+        return NQ_ERR_SHAPE;
+    if (!(eps >= 0.0f)) return NQ_ERR_ARGUMENT;
+    dim3 grid(static_cast<unsigned>(tokens), static_cast<unsigned>(q_heads + kv_heads));
+    hipStream_t st = as_stream(stream);
+#define NQ_QKR(D)                                                                                                     \
+    hipLaunchKernelGGL(k_qk_norm_rope_cache<D>, grid, dim3(kWave), 0, st, q, k, v, q_heads, kv_heads, q_norm, k_norm, \
+                       norm_dtype, eps, cos_table, sin_table, position, max_positions, q_out, k_cache, v_cache,        \
+                       cache_dtype)
+    switch (head_dim) {
+        case 64: NQ_QKR(64); break;
+        case 128: NQ_QKR(128); break;
+        case 256: NQ_QKR(256); break;
+        default: return NQ_ERR_SHAPE;
+    }
+#undef NQ_QKR
+    return nq::launch_status();
+}
+
+extern "C" int64_t nq_attention_workspace_bytes(int64_t tokens, int32_t q_heads, int32_t head_dim,
+                                                int64_t max_positions) {
+    if (tokens <= 0 || q_heads <= 0 || head_dim <= 0 || max_positions <= 0) return -1;
+    const int64_t parts = tokens * q_heads * attention_blocks(max_positions);
+    return parts * (2 + head_dim) * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int nq_attention(const float* q, const void* k_cache, const void* v_cache, int32_t cache_dtype,
+                            int64_t tokens, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                            const int32_t* position, int64_t max_positions, float scaling, void* out, int32_t out_dtype,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!q || !k_cache || !v_cache || !position || !out || !workspace) return NQ_ERR_ARGUMENT;
+    if (!float_code(cache_dtype) || !float_code(out_dtype)) return NQ_ERR_DTYPE;
+    if (tokens <= 0 || tokens > 65535 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads ||
+        q_heads / kv_heads > 16 || max_positions <= 0 || attention_blocks(max_positions) > 65535)
+        return NQ_ERR_SHAPE;
+    if (!(scaling > 0.0f)) return NQ_ERR_ARGUMENT;
+    if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(workspace)) return NQ_ERR_ALIGNMENT;
+    const int64_t need = nq_attention_workspace_bytes(tokens, q_heads, head_dim, max_positions);
+    if (need < 0) return NQ_ERR_SHAPE;
+    if (workspace_bytes < need) return NQ_ERR_WORKSPACE;
+    const int64_t parts = tokens * q_heads * attention_blocks(max_positions);
+    float* ml = static_cast<float*>(workspace);
+    float* acc = ml + 2 * parts;
+    hipStream_t st = as_stream(stream);
+    switch (head_dim) {
+        case 64:
+            return launch_attention_for<64>(cache_dtype, q, k_cache, v_cache, tokens, q_heads, kv_heads, position,
+                                            max_positions, scaling, out, out_dtype, ml, acc, st);
+        case 128:
+            return launch_attention_for<128>(cache_dtype, q, k_cache, v_cache, tokens, q_heads, kv_heads, position,
+                                             max_positions, scaling, out, out_dtype, ml, acc, st);
+        case 256:
+            return launch_attention_for<256>(cache_dtype, q, k_cache, v_cache, tokens, q_heads, kv_heads, position,
+                                             max_positions, scaling, out, out_dtype, ml, acc, st);
+        default:
+            return NQ_ERR_SHAPE;
+    }
+}
+
+extern "C" int nq_silu_mul(const float* gate, const float* up, int64_t n, void* out, int32_t out_dtype, void* stream) {
+    if (!gate || !up || !out) return NQ_ERR_ARGUMENT;
+    if (!float_code(out_dtype)) return NQ_ERR_DTYPE;
+    if (n <= 0 || n % 8) return NQ_ERR_SHAPE;
+    if (!aligned16(gate) || !aligned16(up) || !aligned16(out)) return NQ_ERR_ALIGNMENT;
+    const int64_t groups = (n / 8 + kRowThreads - 1) / kRowThreads;
+    if (groups > 0x7fffffff) return NQ_ERR_SHAPE;
+    hipLaunchKernelGGL(k_silu_mul, dim3(static_cast<unsigned>(groups)), dim3(kRowThreads), 0, as_stream(stream), gate,
+                       up, n, out, out_dtype);
+    return nq::launch_status();
+}
+
+extern "C" int64_t nq_output_projection_workspace_bytes(int64_t vocab, int64_t hidden) {
+    if (vocab <= 0 || hidden <= 0 || hidden % 8) return -1;
+    const int64_t wgs = proj_workgroups(vocab, hidden);
+    return wgs < 0 ? -1 : wgs * static_cast<int64_t>(sizeof(uint64_t));
+}
+
+extern "C" int nq_output_projection(const void* x, int32_t x_dtype, const void* weight, int64_t vocab, int64_t hidden,
+                                    float* logits, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!x || !weight || !logits || !workspace) return NQ_ERR_ARGUMENT;
+    if (x_dtype != NQ_DTYPE_F32 && x_dtype != NQ_DTYPE_BF16) return NQ_ERR_DTYPE;
+    if (vocab <= 0 || vocab > 0x7fffffffLL || hidden <= 0 || hidden % 8 || hidden > 16 * kWave * 8)
+        return NQ_ERR_SHAPE;
+    if (!aligned16(x) || !aligned16(weight) || !aligned16(workspace)) return NQ_ERR_ALIGNMENT;
+    const int64_t need = nq_output_projection_workspace_bytes(vocab, hidden);
+    if (need < 0) return NQ_ERR_SHAPE;
+    if (workspace_bytes < need) return NQ_ERR_WORKSPACE;
+    const int64_t wgs = proj_workgroups(vocab, hidden);
+    hipStream_t st = as_stream(stream);
+    const uint16_t* w = static_cast<const uint16_t*>(weight);
+    uint64_t* part = static_cast<uint64_t*>(workspace);
+    const dim3 grid(static_cast<unsigned>(wgs)), block(kProjWaves * kWave);
+    switch (proj_chunks_per_lane(hidden)) {
+        case 1: hipLaunchKernelGGL(k_output_projection<1>, grid, block, 0, st, x, x_dtype, w, vocab, hidden, logits, part); break;
+        case 2: hipLaunchKernelGGL(k_output_projection<2>, grid, block, 0, st, x, x_dtype, w, vocab, hidden, logits, part); break;
+        case 4: hipLaunchKernelGGL(k_output_projection<4>, grid, block, 0, st, x, x_dtype, w, vocab, hidden, logits, part); break;
+        case 8: hipLaunchKernelGGL(k_output_projection<8>, grid, block, 0, st, x, x_dtype, w, vocab, hidden, logits, part); break;
+        case 16: hipLaunchKernelGGL(k_output_projection<16>, grid, block, 0, st, x, x_dtype, w, vocab, hidden, logits, part); break;
+        default: return NQ_ERR_SHAPE;
+    }
+    return nq::launch_status();
+}
+
+extern "C" int nq_greedy_select(const void* workspace, int64_t vocab, int64_t hidden, int64_t* token_out,
+                                int64_t* history, int64_t history_capacity, int32_t* step, int32_t* position,
+                                void* stream) {
+    if (!workspace || !token_out) return NQ_ERR_ARGUMENT;
+    if ((history != nullptr) != (step != nullptr) || history_capacity < 0) return NQ_ERR_ARGUMENT;
+    const int64_t wgs = vocab > 0 && vocab <= 0x7fffffffLL && hidden > 0 && hidden % 8 == 0 ? proj_workgroups(vocab, hidden) : -1;
+    if (wgs <= 0) return NQ_ERR_SHAPE;
+    hipLaunchKernelGGL(k_greedy_select, dim3(1), dim3(1024), 0, as_stream(stream),
+                       static_cast<const uint64_t*>(workspace), wgs, token_out, history, history_capacity, step,
+                       position);
+    return nq::launch_status();
+}

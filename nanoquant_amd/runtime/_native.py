@@ -35,7 +35,8 @@ DTYPE_CODES: dict[torch.dtype, int] = {
     torch.int32: 4,
 }
 
-# Every symbol include/nqamd.h declares; tests check the library exports them all.
+# Every symbol include/nqamd.h and include/nqamd_shell.h declare; tests check
+# the library exports them all.
 EXPORTED_SYMBOLS = (
     "nq_abi_version",
     "nq_status_string",
@@ -48,6 +49,15 @@ EXPORTED_SYMBOLS = (
     "nq_linear_workspace_bytes",
     "nq_linear",
     "nq_linear_batch",
+    "nq_embedding",
+    "nq_add_rmsnorm",
+    "nq_qk_norm_rope_cache",
+    "nq_attention_workspace_bytes",
+    "nq_attention",
+    "nq_silu_mul",
+    "nq_output_projection_workspace_bytes",
+    "nq_output_projection",
+    "nq_greedy_select",
 )
 
 
@@ -119,6 +129,7 @@ def library_available() -> bool:
 
 def _declare(lib: ctypes.CDLL) -> None:
     c_int, c_i64, vp = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+    i32, f32 = ctypes.c_int32, ctypes.c_float
     desc_p = ctypes.POINTER(LinearDesc)
     table = {
         "nq_abi_version": (c_int, []),
@@ -139,6 +150,20 @@ def _declare(lib: ctypes.CDLL) -> None:
             [ctypes.POINTER(desc_p), ctypes.c_int32, ctypes.POINTER(vp), ctypes.c_int32, c_i64,
              ctypes.POINTER(vp), ctypes.c_int32, ctypes.POINTER(vp), ctypes.POINTER(c_i64), vp],
         ),
+        "nq_embedding": (c_int, [vp, c_i64, vp, i32, c_i64, c_i64, vp, vp, vp]),
+        "nq_add_rmsnorm": (c_int, [vp, vp, i32, vp, i32, f32, c_i64, c_i64, vp, i32, vp]),
+        "nq_qk_norm_rope_cache": (
+            c_int,
+            [vp, vp, vp, c_i64, i32, i32, i32, vp, vp, i32, f32, vp, vp, vp, c_i64, vp, vp, vp, i32, vp],
+        ),
+        "nq_attention_workspace_bytes": (c_i64, [c_i64, i32, i32, c_i64]),
+        "nq_attention": (
+            c_int, [vp, vp, vp, i32, c_i64, i32, i32, i32, vp, c_i64, f32, vp, i32, vp, c_i64, vp],
+        ),
+        "nq_silu_mul": (c_int, [vp, vp, c_i64, vp, i32, vp]),
+        "nq_output_projection_workspace_bytes": (c_i64, [c_i64, c_i64]),
+        "nq_output_projection": (c_int, [vp, i32, vp, c_i64, c_i64, vp, vp, c_i64, vp]),
+        "nq_greedy_select": (c_int, [vp, c_i64, c_i64, vp, vp, c_i64, vp, vp, vp]),
     }
     for name, (restype, argtypes) in table.items():
         fn = getattr(lib, name)

@@ -1,0 +1,354 @@
+"""Batch-1 decoder shell (Qwen3 geometry) around the packed linears, on gfx950.
+
+The reference decodes a packed model by running the Transformers model shell
+with one ``PreparedLinear`` per projection and capturing the one-token step in
+a CUDA graph (``TransformersGenerationModel``,
+src/nanoquant/runtime/transformers_generation.py:37-260), driven by the
+generation engine's ``GenerationModel.forward_step`` protocol
+(src/nanoquant/runtime/generation.py:28-41). ``PackedDecoder`` is that model
+shell built from this library's kernels instead:
+
+* every projection is a packed linear on ``HipPackedBackend`` — Q/K/V and
+  gate/up run as one batched decode call each (tokens <= 16), the prompt runs
+  the MFMA prefill path;
+* embedding, residual add + RMSNorm, q/k RMSNorm + RoPE + KV append,
+  grouped-query attention, SiLU product, the bf16 output projection and
+  greedy selection are the HIP kernels of ``include/nqamd_shell.h``;
+* the KV cache is one device tensor per layer ``[kv_heads, max_positions,
+  head_dim]``, and the token position lives in device memory, so one HIP graph
+  of the whole one-token step (about 14 launches per layer) replays for every
+  position with no host synchronisation; ``generate_greedy`` keeps the chosen
+  tokens on the device and synchronises once at the end.
+
+``forward_step`` implements the reference's ``GenerationModel`` protocol for
+batch 1 (a prompt without padding), returning ``[1, 1, vocab]`` fp32 logits
+and itself as the cache handle.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from nanoquant_amd.runtime import shell_ops as ops
+from nanoquant_amd.runtime.backend import PreparedLayer
+from nanoquant_amd.runtime.hip_backend import HipPackedBackend
+from nanoquant_amd.runtime.packed import PackedLayerState
+
+ROLES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+class DecoderShellError(ValueError):
+    """A request the decoder shell does not support (batch > 1, padding, cache overflow)."""
+
+
+@dataclass(frozen=True)
+class DecoderShellConfig:
+    layers: int = 36
+    hidden: int = 4096
+    intermediate: int = 12288
+    q_heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    qk_norm: bool = True
+
+    @staticmethod
+    def qwen3_8b() -> "DecoderShellConfig":
+        return DecoderShellConfig()
+
+    def linear_dims(self) -> dict[str, tuple[int, int]]:
+        """(in, out) of each projection role."""
+
+        q, kv = self.q_heads * self.head_dim, self.kv_heads * self.head_dim
+        return {
+            "q_proj": (self.hidden, q),
+            "k_proj": (self.hidden, kv),
+            "v_proj": (self.hidden, kv),
+            "o_proj": (q, self.hidden),
+            "gate_proj": (self.hidden, self.intermediate),
+            "up_proj": (self.hidden, self.intermediate),
+            "down_proj": (self.intermediate, self.hidden),
+        }
+
+
+@dataclass
+class DecoderLayerWeights:
+    input_norm: torch.Tensor
+    post_norm: torch.Tensor
+    q_norm: torch.Tensor | None
+    k_norm: torch.Tensor | None
+    linears: dict[str, PackedLayerState]
+
+
+@dataclass
+class DecoderShellWeights:
+    embed: torch.Tensor  # [vocab, hidden] bf16
+    lm_head: torch.Tensor  # [vocab, hidden] bf16
+    final_norm: torch.Tensor  # [hidden]
+    layers: list[DecoderLayerWeights] = field(default_factory=list)
+
+
+def rope_tables(head_dim: int, theta: float, positions: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin ``[positions, head_dim / 2]`` fp32 of ``position * inv_freq`` with
+    ``inv_freq = 1 / theta^(arange(0, D, 2) / D)``, computed on the host in fp32
+    like the Transformers default rotary embedding."""
+
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+    freqs = torch.arange(positions, dtype=torch.float)[:, None] * inv[None, :]
+    return freqs.cos(), freqs.sin()
+
+
+@dataclass
+class _Buffers:
+    """Activations of one forward over `tokens` rows (fixed addresses for graphs)."""
+
+    tokens: int
+    residual: torch.Tensor
+    xn: torch.Tensor
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    q_rot: torch.Tensor
+    attn: torch.Tensor
+    o: torch.Tensor
+    gate: torch.Tensor
+    up: torch.Tensor
+    act: torch.Tensor
+    down: torch.Tensor
+    final: torch.Tensor
+    attn_ws: torch.Tensor
+
+
+class PackedDecoder:
+    """Batch-1 decoder over prepared packed linears; see the module docstring."""
+
+    def __init__(
+        self,
+        config: DecoderShellConfig,
+        weights: DecoderShellWeights,
+        *,
+        device: torch.device | str = "cuda",
+        max_positions: int = 640,
+        backend: HipPackedBackend | None = None,
+        activation_dtype: torch.dtype = torch.bfloat16,
+        cache_dtype: torch.dtype = torch.bfloat16,
+        history_capacity: int = 4096,
+    ) -> None:
+        self.config = c = config
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise DecoderShellError("the packed decoder shell runs on a HIP device")
+        if len(weights.layers) != c.layers:
+            raise DecoderShellError("weights do not match the configured layer count")
+        if c.q_heads % c.kv_heads or c.head_dim not in (64, 128, 256):
+            raise DecoderShellError("unsupported attention geometry")
+        if activation_dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise DecoderShellError("activation dtype must be BF16, F16 or F32")
+        self.max_positions = int(max_positions)
+        self.activation_dtype = activation_dtype
+        self.cache_dtype = cache_dtype
+        self.backend = backend or HipPackedBackend()
+        dev = self.device
+        self.embed = weights.embed.to(dev, torch.bfloat16).contiguous()
+        self.lm_head = weights.lm_head.to(dev, torch.bfloat16).contiguous()
+        self.final_norm = weights.final_norm.to(dev).contiguous()
+        self.layers: list[dict[str, PreparedLayer]] = []
+        self.norms: list[tuple[torch.Tensor, torch.Tensor, torch.Tensor | None, torch.Tensor | None]] = []
+        for layer in weights.layers:
+            self.layers.append({role: self.backend.prepare(layer.linears[role], dev) for role in ROLES})
+            qn = None if layer.q_norm is None or not c.qk_norm else layer.q_norm.to(dev).contiguous()
+            kn = None if layer.k_norm is None or not c.qk_norm else layer.k_norm.to(dev).contiguous()
+            self.norms.append((layer.input_norm.to(dev).contiguous(), layer.post_norm.to(dev).contiguous(), qn, kn))
+        cache_shape = (c.layers, c.kv_heads, self.max_positions, c.head_dim)
+        self.k_cache = torch.zeros(cache_shape, dtype=cache_dtype, device=dev)
+        self.v_cache = torch.zeros(cache_shape, dtype=cache_dtype, device=dev)
+        cos, sin = rope_tables(c.head_dim, c.rope_theta, self.max_positions)
+        self.cos, self.sin = cos.to(dev), sin.to(dev)
+        self.scaling = c.head_dim**-0.5
+        self.position = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.step = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.ids = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.history = torch.zeros(history_capacity, dtype=torch.int64, device=dev)
+        self.logits = torch.empty(c.vocab, dtype=torch.float32, device=dev)
+        self.proj_ws = torch.empty(ops.output_projection_workspace_bytes(c.vocab, c.hidden), dtype=torch.uint8, device=dev)
+        self._decode_bufs: _Buffers | None = None
+        self._graph: torch.cuda.CUDAGraph | None = None
+        self.host_position = 0
+
+    # -- buffers -----------------------------------------------------------------
+    def _buffers(self, tokens: int) -> _Buffers:
+        c, dev, act = self.config, self.device, self.activation_dtype
+        q_width, kv_width = c.q_heads * c.head_dim, c.kv_heads * c.head_dim
+
+        def f32(*shape):
+            return torch.empty(shape, dtype=torch.float32, device=dev)
+
+        def a(*shape):
+            return torch.empty(shape, dtype=act, device=dev)
+
+        return _Buffers(
+            tokens, f32(tokens, c.hidden), a(tokens, c.hidden), f32(tokens, q_width), f32(tokens, kv_width),
+            f32(tokens, kv_width), f32(tokens, c.q_heads, c.head_dim), a(tokens, q_width), f32(tokens, c.hidden),
+            f32(tokens, c.intermediate), f32(tokens, c.intermediate), a(tokens, c.intermediate),
+            f32(tokens, c.hidden), f32(tokens, c.hidden),
+            torch.empty(ops.attention_workspace_bytes(tokens, c.q_heads, c.head_dim, self.max_positions),
+                        dtype=torch.uint8, device=dev),
+        )
+
+    # -- one forward -----------------------------------------------------------------
+    def _linears(self, xs: list[torch.Tensor], layers: list[PreparedLayer], outs: list[torch.Tensor], tokens: int) -> None:
+        if tokens <= 16:
+            self.backend.linear_batch(xs, layers, outs=outs)
+        else:
+            for x, layer, out in zip(xs, layers, outs):
+                self.backend.linear_into(x, layer, out=out)
+
+    def _forward(self, ids: torch.Tensor, b: _Buffers) -> None:
+        """Embedding .. final norm for `b.tokens` rows at positions position[0] + t,
+        then the logits and argmax partials of the last row."""
+
+        c, t = self.config, b.tokens
+        ops.launch_embedding(ids, self.embed, out=b.residual)
+        for i, prepared in enumerate(self.layers):
+            in_norm, post_norm, qn, kn = self.norms[i]
+            ops.launch_add_rmsnorm(b.residual, in_norm, c.eps, delta=b.down if i else None, out=b.xn)
+            self._linears([b.xn] * 3, [prepared["q_proj"], prepared["k_proj"], prepared["v_proj"]], [b.q, b.k, b.v], t)
+            ops.launch_qk_norm_rope_cache(
+                b.q, b.k, b.v, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, q_norm=qn, k_norm=kn,
+                eps=c.eps, cos=self.cos, sin=self.sin, position=self.position, k_cache=self.k_cache[i],
+                v_cache=self.v_cache[i], q_out=b.q_rot,
+            )
+            ops.launch_attention(b.q_rot, self.k_cache[i], self.v_cache[i], position=self.position,
+                                 scaling=self.scaling, out=b.attn, workspace=b.attn_ws)
+            self._linears([b.attn], [prepared["o_proj"]], [b.o], t)
+            ops.launch_add_rmsnorm(b.residual, post_norm, c.eps, delta=b.o, out=b.xn)
+            self._linears([b.xn] * 2, [prepared["gate_proj"], prepared["up_proj"]], [b.gate, b.up], t)
+            ops.launch_silu_mul(b.gate, b.up, out=b.act)
+            self._linears([b.act], [prepared["down_proj"]], [b.down], t)
+        ops.launch_add_rmsnorm(b.residual, self.final_norm, c.eps, delta=b.down, out=b.final)
+        ops.launch_output_projection(b.final[t - 1], self.lm_head, logits=self.logits, workspace=self.proj_ws)
+
+    def _decode_body(self) -> None:
+        assert self._decode_bufs is not None
+        self._forward(self.ids, self._decode_bufs)
+        ops.launch_greedy_select(self.proj_ws, self.config.vocab, self.config.hidden, token_out=self.ids,
+                                 history=self.history, step=self.step, position=self.position)
+
+    def _decode_graph(self) -> torch.cuda.CUDAGraph:
+        """Capture the one-token step once. A warm-up run precedes the capture
+        (it allocates the packed calls' workspaces); it writes the cache row at
+        the current position, which the step that follows rewrites, and its
+        changes to the token, step and position counters are undone."""
+
+        if self._graph is None:
+            self._decode_bufs = self._decode_bufs or self._buffers(1)
+            saved = (self.position.clone(), self.step.clone(), self.ids.clone())
+            side = torch.cuda.Stream(self.device)
+            side.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(side):
+                self._decode_body()  # warm-up: allocates the packed-call workspaces
+            torch.cuda.current_stream(self.device).wait_stream(side)
+            self._restore(saved)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._decode_body()
+            self._restore(saved)
+            self._graph = graph
+        return self._graph
+
+    def _restore(self, saved: tuple[torch.Tensor, torch.Tensor, torch.Tensor]) -> None:
+        self.position.copy_(saved[0])
+        self.step.copy_(saved[1])
+        self.ids.copy_(saved[2])
+
+    # -- public API ------------------------------------------------------------------
+    def reset(self) -> None:
+        """Forget the sequence (the cache rows are overwritten as positions are reused)."""
+
+        self.position.zero_()
+        self.step.zero_()
+        self.host_position = 0
+
+    def prefill(self, prompt: torch.Tensor, *, start: int = 0) -> torch.Tensor:
+        """Run `prompt` (int64 ids) at positions start..; returns the last row's
+        logits (fp32 [vocab], the decoder's own buffer) and leaves the greedy
+        partials in the workspace."""
+
+        ids = prompt.reshape(-1).to(self.device, torch.int64).contiguous()
+        t = ids.numel()
+        if t < 1 or start + t > self.max_positions:
+            raise DecoderShellError("prompt does not fit the KV cache")
+        self.position.fill_(start)
+        self._forward(ids, self._buffers(t))
+        self.position.fill_(start + t)
+        self.host_position = start + t
+        return self.logits
+
+    def generate_greedy(self, prompt: torch.Tensor, max_new_tokens: int, *, use_graph: bool = True) -> torch.Tensor:
+        """Greedy continuation of one prompt: prefill, then `max_new_tokens - 1`
+        replays of the captured one-token step. Tokens stay on the device; the
+        only synchronisation is the caller's read of the result."""
+
+        if max_new_tokens < 1 or max_new_tokens > self.history.numel():
+            raise DecoderShellError("max_new_tokens outside the history capacity")
+        t = int(prompt.numel())
+        if t + max_new_tokens - 1 > self.max_positions:
+            raise DecoderShellError("prompt plus generated tokens exceed the KV cache")
+        graph = self._decode_graph() if use_graph else None
+        self.reset()
+        self.prefill(prompt)
+        ops.launch_greedy_select(self.proj_ws, self.config.vocab, self.config.hidden, token_out=self.ids,
+                                 history=self.history, step=self.step)
+        if not use_graph:
+            self._decode_bufs = self._decode_bufs or self._buffers(1)
+        for _ in range(max_new_tokens - 1):
+            if graph is not None:
+                graph.replay()
+            else:
+                self._decode_body()
+        self.host_position = t + max_new_tokens - 1
+        return self.history[:max_new_tokens].clone()
+
+    def forward_step(
+        self,
+        *,
+        input_ids: torch.Tensor,
+        attention_mask: torch.Tensor,
+        position_ids: torch.Tensor,
+        cache_position: torch.Tensor,
+        cache: object | None,
+        max_cache_length: int,
+        workload: str,
+        deterministic: bool,
+    ):
+        """``GenerationModel.forward_step`` (src/nanoquant/runtime/generation.py:28-41)
+        for batch 1: prefill rows run eagerly, a one-token decode step replays the
+        captured graph. Positions come from `cache_position` (device), so no
+        host synchronisation is needed."""
+
+        from nanoquant_amd.runtime.generation import GenerationStep
+
+        if input_ids.ndim != 2 or input_ids.shape[0] != 1:
+            raise DecoderShellError("the packed decoder shell serves batch 1")
+        if not deterministic:
+            raise DecoderShellError("the packed decoder shell is deterministic only")
+        if max_cache_length > self.max_positions:
+            raise DecoderShellError("max_cache_length exceeds the decoder's KV cache")
+        if attention_mask.ndim != 2 or attention_mask.shape[0] != 1:
+            raise DecoderShellError("attention mask must be [1, width] for the batch-1 shell")
+        t = input_ids.shape[1]
+        if cache is None:
+            self.reset()
+        self.position.copy_(cache_position.reshape(-1)[:1])
+        if workload == "decode" and t == 1:
+            self.ids.copy_(input_ids.reshape(1))
+            self._decode_graph().replay()
+        else:
+            if bool((~attention_mask.bool()).any()):
+                raise DecoderShellError("padded prompts are not supported by the batch-1 shell")
+            self._forward(input_ids.reshape(-1).contiguous(), self._buffers(t))
+        return GenerationStep(self.logits.clone().view(1, 1, -1), self)

@@ -203,3 +203,49 @@ def bits_per_weight(shape: LinearShape) -> float:
 
 def model_weight_bytes(shapes: list[LinearShape]) -> int:
     return int(math.fsum(s.weight_bytes for s in shapes))
+
+
+def synthetic_decoder(
+    config,
+    *,
+    seed: int = BASE_SEED + 5,
+    device: str | torch.device = "cpu",
+    bpw: float = 1.0,
+    random_norms: bool = False,
+):
+    """A random-init decoder of ``config`` (a ``DecoderShellConfig``): every
+    projection a packed linear at ``bpw`` (rank ``round(bpw*m*n/(m+n))``),
+    embeddings and untied ``lm_head`` bf16 ``N(0, 0.02)``, norm weights ones
+    (the Transformers initialisation) or, with ``random_norms``,
+    ``1 + 0.1 N(0, 1)`` so that tests see every weight applied."""
+
+    from nanoquant_amd.runtime.decoder_shell import ROLES, DecoderLayerWeights, DecoderShellWeights
+
+    device = torch.device(device)
+    g = torch.Generator(device=device).manual_seed(seed)
+    dims = config.linear_dims()
+
+    def dense(rows: int, cols: int) -> torch.Tensor:
+        return (0.02 * torch.randn(rows, cols, generator=g, device=device)).to(torch.bfloat16)
+
+    def norm(n: int) -> torch.Tensor:
+        if not random_norms:
+            return torch.ones(n, dtype=torch.float32, device=device)
+        return 1.0 + 0.1 * torch.randn(n, generator=g, device=device)
+
+    embed = dense(config.vocab, config.hidden)
+    lm_head = dense(config.vocab, config.hidden)
+    final_norm = norm(config.hidden)
+    layers = []
+    for layer in range(config.layers):
+        linears = {}
+        for r, role in enumerate(ROLES):
+            i, o = dims[role]
+            prefix = "self_attn" if r < 4 else "mlp"
+            shape = LinearShape(f"blocks.{layer}.{prefix}.{role}", i, o, rank_for(i, o, bpw))
+            linears[role] = synthetic_packed_layer(shape, seed=seed + 1000 * (layer + 1) + r, device=device)
+        layers.append(
+            DecoderLayerWeights(norm(config.hidden), norm(config.hidden), norm(config.head_dim),
+                                norm(config.head_dim), linears)
+        )
+    return DecoderShellWeights(embed, lm_head, final_norm, layers)

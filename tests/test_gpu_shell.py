@@ -1,0 +1,286 @@
+"""GPU parity of the decoder-shell kernels and of the end-to-end batch-1 decoder.
+
+Kernel tests compare each HIP kernel with the fp32 restatement in
+oracle/decoder_shell.py (itself pinned to transformers' Qwen3) or with plain
+torch fp32 on the same inputs. End-to-end tests run ``PackedDecoder`` against
+the oracle decoder on the same synthetic model, teacher-forced on the GPU's
+own greedy tokens:
+  * fp32 activations and KV cache: logits rel-L2 <= 2e-3 per step (the packed
+    linear's bar; the shell kernels themselves are fp32);
+  * bf16 activations and KV cache (the deployed configuration) against an
+    oracle that rounds at the same points: rel-L2 <= 2e-2;
+  * the greedy token is the argmax of the returned logits and agrees with the
+    oracle's unless the oracle's top-2 gap is within the tolerance;
+  * graph replay, eager steps and the generation engine give identical tokens.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from conftest import gpu_available
+from nanoquant_amd import synthetic as syn
+from nanoquant_amd.runtime import shell_ops as ops
+from nanoquant_amd.runtime.decoder_shell import DecoderShellConfig, PackedDecoder
+from oracle import decoder_shell as ods
+from oracle.nq_oracle import operands_from_state, relative_l2
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")]
+
+DEV = torch.device("cuda", 0)
+
+
+def _g(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+# --------------------------------------------------------------------------- kernels
+def test_embedding_gathers_rows_exactly():
+    table = (0.02 * torch.randn(1000, 256, generator=_g(1))).to(torch.bfloat16)
+    ids = torch.tensor([0, 999, 17, 17, 512])
+    out = ops.launch_embedding(ids.to(DEV), table.to(DEV))
+    assert torch.equal(out.cpu(), table[ids].float())
+    bad = ops.launch_embedding(torch.tensor([1000], device=DEV), table.to(DEV))
+    assert torch.isnan(bad).all()
+
+
+@pytest.mark.parametrize("rows,hidden,out_dtype", [(1, 4096, torch.bfloat16), (37, 1152, torch.float32)])
+def test_add_rmsnorm(rows, hidden, out_dtype):
+    g = _g(2)
+    residual = 50 * torch.randn(rows, hidden, generator=g)
+    delta = torch.randn(rows, hidden, generator=g)
+    weight = 1 + 0.1 * torch.randn(hidden, generator=g)
+    r = residual.to(DEV)
+    out = ops.launch_add_rmsnorm(r, weight.to(DEV), 1e-6, delta=delta.to(DEV), out_dtype=out_dtype)
+    expected_residual = residual + delta
+    assert torch.equal(r.cpu(), expected_residual)
+    expected = ods.rms_norm(expected_residual, weight, 1e-6)
+    tol = 1e-6 if out_dtype == torch.float32 else 4e-3
+    assert relative_l2(out.float().cpu(), expected) < tol
+    # without delta the residual is untouched
+    r2 = residual.to(DEV)
+    out2 = ops.launch_add_rmsnorm(r2, weight.to(DEV), 1e-6, out_dtype=torch.float32)
+    assert torch.equal(r2.cpu(), residual)
+    assert relative_l2(out2.cpu(), ods.rms_norm(residual, weight, 1e-6)) < 1e-6
+
+
+@pytest.mark.parametrize("head_dim,q_heads,kv_heads", [(128, 32, 8), (64, 4, 4), (256, 8, 2)])
+@pytest.mark.parametrize("cache_dtype", [torch.bfloat16, torch.float32])
+def test_qk_norm_rope_cache(head_dim, q_heads, kv_heads, cache_dtype):
+    g = _g(3)
+    tokens, max_pos, start = 5, 96, 61
+    q = 3 * torch.randn(tokens, q_heads * head_dim, generator=g)
+    k = 3 * torch.randn(tokens, kv_heads * head_dim, generator=g)
+    v = torch.randn(tokens, kv_heads * head_dim, generator=g)
+    qn = 1 + 0.1 * torch.randn(head_dim, generator=g)
+    kn = 1 + 0.1 * torch.randn(head_dim, generator=g)
+    cos, sin = ods.rope_tables(head_dim, 1e6, max_pos)
+    kc = torch.full((kv_heads, max_pos, head_dim), 7.0, dtype=cache_dtype, device=DEV)
+    vc = torch.full_like(kc, 7.0)
+    position = torch.tensor([start], dtype=torch.int32, device=DEV)
+    q_rot = ops.launch_qk_norm_rope_cache(
+        q.to(DEV), k.to(DEV), v.to(DEV), q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, q_norm=qn.to(DEV),
+        k_norm=kn.to(DEV), eps=1e-6, cos=cos.to(DEV), sin=sin.to(DEV), position=position, k_cache=kc, v_cache=vc,
+    )
+    c, s = cos[start:start + tokens], sin[start:start + tokens]
+    eq = ods.apply_rope(ods.rms_norm(q.view(tokens, q_heads, head_dim), qn, 1e-6), c, s)
+    ek = ods.apply_rope(ods.rms_norm(k.view(tokens, kv_heads, head_dim), kn, 1e-6), c, s)
+    assert relative_l2(q_rot.cpu(), eq) < 1e-6
+    got_k = kc[:, start:start + tokens].float().cpu().transpose(0, 1)
+    got_v = vc[:, start:start + tokens].float().cpu().transpose(0, 1)
+    tol = 1e-6 if cache_dtype == torch.float32 else 4e-3
+    assert relative_l2(got_k, ek) < tol
+    assert relative_l2(got_v, v.view(tokens, kv_heads, head_dim)) < tol
+    untouched = torch.ones(max_pos, dtype=torch.bool)
+    untouched[start:start + tokens] = False
+    assert (kc[:, untouched].float() == 7.0).all() and (vc[:, untouched].float() == 7.0).all()
+
+
+def reference_attention(q, kc, vc, start, scaling):
+    """fp32 causal GQA over cache rows [0, start + t] (q [T, Hq, D], caches [Hkv, L, D])."""
+
+    t, hq, d = q.shape
+    group = hq // kc.shape[0]
+    keys = kc.float().repeat_interleave(group, dim=0)
+    values = vc.float().repeat_interleave(group, dim=0)
+    length = start + t
+    scores = torch.einsum("thd,hld->htl", q, keys[:, :length]) * scaling
+    allowed = torch.arange(length)[None, :] <= (start + torch.arange(t))[:, None]
+    scores = scores.masked_fill(~allowed[None], float("-inf"))
+    return torch.einsum("htl,hld->thd", torch.softmax(scores, dim=-1), values[:, :length]).reshape(t, -1)
+
+
+@pytest.mark.parametrize(
+    "tokens,start,q_heads,kv_heads,head_dim,cache_dtype",
+    [
+        (1, 0, 32, 8, 128, torch.bfloat16),
+        (1, 63, 32, 8, 128, torch.bfloat16),
+        (1, 64, 32, 8, 128, torch.bfloat16),
+        (1, 639, 32, 8, 128, torch.bfloat16),
+        (1, 200, 4, 4, 64, torch.float32),
+        (1, 300, 16, 2, 256, torch.float16),
+        (37, 5, 32, 8, 128, torch.bfloat16),
+        (512, 0, 32, 8, 128, torch.bfloat16),
+        (100, 27, 8, 1, 64, torch.float32),
+    ],
+)
+def test_attention(tokens, start, q_heads, kv_heads, head_dim, cache_dtype):
+    g = _g(4)
+    max_pos = 640
+    kc = torch.randn(kv_heads, max_pos, head_dim, generator=g).to(cache_dtype)
+    vc = torch.randn(kv_heads, max_pos, head_dim, generator=g).to(cache_dtype)
+    q = 2 * torch.randn(tokens, q_heads, head_dim, generator=g)
+    scaling = head_dim**-0.5
+    position = torch.tensor([start], dtype=torch.int32, device=DEV)
+    out = ops.launch_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), position=position, scaling=scaling,
+                               out_dtype=torch.float32)
+    expected = reference_attention(q, kc, vc, start, scaling)
+    assert relative_l2(out.cpu(), expected) < 1e-5
+    again = ops.launch_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), position=position, scaling=scaling,
+                                 out_dtype=torch.float32)
+    assert torch.equal(out, again)
+
+
+def test_attention_single_row_returns_value():
+    kc = torch.randn(2, 64, 128).to(torch.bfloat16)
+    vc = torch.randn(2, 64, 128).to(torch.bfloat16)
+    q = torch.randn(1, 8, 128)
+    out = ops.launch_attention(q.to(DEV), kc.to(DEV), vc.to(DEV), position=torch.zeros(1, dtype=torch.int32, device=DEV),
+                               scaling=0.1, out_dtype=torch.float32)
+    expected = vc[:, 0].float().repeat_interleave(4, dim=0).reshape(1, -1)
+    assert torch.equal(out.cpu(), expected)
+
+
+def test_silu_mul():
+    g = _g(5)
+    gate = 4 * torch.randn(12288, generator=g)
+    up = torch.randn(12288, generator=g)
+    out = ops.launch_silu_mul(gate.to(DEV), up.to(DEV), out_dtype=torch.float32)
+    assert relative_l2(out.cpu(), torch.nn.functional.silu(gate) * up) < 1e-6
+
+
+@pytest.mark.parametrize("vocab,hidden,x_dtype", [(151936, 4096, torch.float32), (1000, 1152, torch.bfloat16),
+                                                 (77, 64, torch.float32), (5000, 8192, torch.float32)])
+def test_output_projection_and_greedy(vocab, hidden, x_dtype):
+    g = _g(6)
+    weight = (0.02 * torch.randn(vocab, hidden, generator=g)).to(torch.bfloat16).to(DEV)
+    x = torch.randn(hidden, generator=g).to(x_dtype)
+    logits, ws = ops.launch_output_projection(x.to(DEV), weight)
+    expected = weight.float() @ x.float().to(DEV)
+    assert relative_l2(logits, expected) < 1e-5
+    token = torch.zeros(1, dtype=torch.int64, device=DEV)
+    ops.launch_greedy_select(ws, vocab, hidden, token_out=token)
+    assert int(token) == int(torch.argmax(logits))
+
+
+def test_greedy_ties_take_the_lowest_index_and_advance_counters():
+    vocab, hidden = 3000, 64
+    weight = torch.zeros(vocab, hidden, dtype=torch.bfloat16)
+    weight[[2999, 1500, 1501], 0] = 1.0  # three equal maxima
+    x = torch.zeros(hidden)
+    x[0] = 2.0
+    logits, ws = ops.launch_output_projection(x.to(DEV), weight.to(DEV))
+    token = torch.zeros(1, dtype=torch.int64, device=DEV)
+    history = torch.full((2,), -1, dtype=torch.int64, device=DEV)
+    step = torch.zeros(1, dtype=torch.int32, device=DEV)
+    position = torch.tensor([9], dtype=torch.int32, device=DEV)
+    for _ in range(3):  # the third call is past the history capacity: not written
+        ops.launch_greedy_select(ws, vocab, hidden, token_out=token, history=history, step=step, position=position)
+    assert int(token) == 1500 == int(torch.argmax(logits))
+    assert history.tolist() == [1500, 1500]
+    assert int(step) == 3 and int(position) == 12
+
+
+# --------------------------------------------------------------------------- end to end
+SMALL = DecoderShellConfig(layers=3, hidden=256, intermediate=768, q_heads=4, kv_heads=2, head_dim=64, vocab=1000)
+QWEN_2L = DecoderShellConfig(layers=2, vocab=151936)
+
+
+def _oracle(config, weights, act, cache, max_positions):
+    geometry = ods.ShellGeometry(config.layers, config.hidden, config.intermediate, config.q_heads,
+                                 config.kv_heads, config.head_dim, config.vocab, config.eps, config.rope_theta)
+    ow = ods.ShellWeights(
+        weights.embed, weights.lm_head, weights.final_norm,
+        [ods.LayerWeights(l.input_norm, l.post_norm, l.q_norm, l.k_norm,
+                          {r: operands_from_state(s) for r, s in l.linears.items()}) for l in weights.layers],
+    )
+    return ods.OracleDecoder(geometry, ow, max_positions=max_positions, activation_dtype=act, cache_dtype=cache)
+
+
+def _teacher_forced(oracle, prompt, tokens):
+    oracle.reset()
+    rows = [oracle.forward(prompt, 0)[-1]]
+    position = prompt.numel()
+    for token in tokens[:-1]:
+        rows.append(oracle.forward(torch.tensor([token]), position)[-1])
+        position += 1
+    return rows
+
+
+def _gpu_steps(decoder, prompt, new_tokens):
+    """Greedy tokens and the logits each was chosen from, step by step (eager)."""
+
+    decoder.reset()
+    logits = [decoder.prefill(prompt.to(DEV)).clone()]
+    tokens = []
+    for i in range(new_tokens):
+        ops.launch_greedy_select(decoder.proj_ws, decoder.config.vocab, decoder.config.hidden,
+                                 token_out=decoder.ids, history=decoder.history, step=decoder.step)
+        tokens.append(int(decoder.ids))
+        if i + 1 == new_tokens:
+            break
+        decoder._decode_bufs = decoder._decode_bufs or decoder._buffers(1)
+        decoder._forward(decoder.ids, decoder._decode_bufs)
+        decoder.position += 1
+        logits.append(decoder.logits.clone())
+    return tokens, logits
+
+
+def _check_against_oracle(config, act, cache, tol, prompt_len, new_tokens, seed):
+    weights = syn.synthetic_decoder(config, seed=seed, random_norms=True)
+    max_positions = prompt_len + new_tokens + 3
+    decoder = PackedDecoder(config, weights, device=DEV, max_positions=max_positions, activation_dtype=act,
+                            cache_dtype=cache)
+    prompt = torch.randint(0, config.vocab, (prompt_len,), generator=_g(seed))
+    tokens, logits = _gpu_steps(decoder, prompt, new_tokens)
+    oracle = _oracle(config, weights, act, cache, max_positions)
+    expected = _teacher_forced(oracle, prompt, tokens)
+    for step, (got, exp, token) in enumerate(zip(logits, expected, tokens)):
+        err = relative_l2(got.cpu(), exp)
+        assert err <= tol, f"step {step}: rel_l2 {err:.3e} > {tol}"
+        assert token == int(torch.argmax(got))
+        top2 = torch.topk(exp, 2).values
+        if float(top2[0] - top2[1]) > 4 * tol * float(exp.abs().max()):
+            assert token == int(torch.argmax(exp)), f"step {step}: greedy token differs"
+    return decoder, prompt, tokens
+
+
+@pytest.mark.parametrize("act,cache,tol", [(torch.float32, torch.float32, 2e-3), (torch.bfloat16, torch.bfloat16, 2e-2)])
+def test_decoder_small_matches_oracle(act, cache, tol):
+    # prompt of 70 tokens: the MFMA prefill path and attention across two 64-row blocks
+    _check_against_oracle(SMALL, act, cache, tol, prompt_len=70, new_tokens=12, seed=syn.BASE_SEED + 61)
+
+
+@pytest.mark.parametrize("act,cache,tol", [(torch.float32, torch.float32, 2e-3), (torch.bfloat16, torch.bfloat16, 2e-2)])
+def test_decoder_qwen3_8b_geometry_matches_oracle(act, cache, tol):
+    # two layers of the Qwen3-8B geometry with its full vocabulary; prompt <= 16 uses the batched decode path
+    _check_against_oracle(QWEN_2L, act, cache, tol, prompt_len=12, new_tokens=5, seed=syn.BASE_SEED + 62)
+
+
+def test_graph_replay_matches_eager_and_engine():
+    from nanoquant_amd.runtime.generation import GenerationRequest, generate
+
+    weights = syn.synthetic_decoder(SMALL, seed=syn.BASE_SEED + 63)
+    decoder = PackedDecoder(SMALL, weights, device=DEV, max_positions=128)
+    prompt = torch.randint(0, SMALL.vocab, (40,), generator=_g(63))
+    eager_tokens, _ = _gpu_steps(decoder, prompt, 20)
+    graph_tokens = decoder.generate_greedy(prompt.to(DEV), 20).tolist()
+    graph_again = decoder.generate_greedy(prompt.to(DEV), 20).tolist()
+    no_graph = decoder.generate_greedy(prompt.to(DEV), 20, use_graph=False).tolist()
+    assert graph_tokens == eager_tokens == graph_again == no_graph
+    request = GenerationRequest(prompt[None].to(DEV), torch.ones(1, 40, dtype=torch.bool, device=DEV),
+                                max_new_tokens=20, eos_token_ids=(SMALL.vocab + 1,), pad_token_id=0)
+    result = generate(request, decoder)
+    assert result.token_ids[0].tolist() == graph_tokens
+    assert result.decode_forward_count == 19 and result.stop_reasons == ("max_new_tokens",)

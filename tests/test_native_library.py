@@ -1,4 +1,4 @@
-"""The C-ABI library loads and exports every entry point include/nqamd.h declares.
+"""The C-ABI library loads and exports every entry point include/*.h declares.
 No compute call is made here (no GPU needed)."""
 
 from __future__ import annotations
@@ -9,12 +9,15 @@ from pathlib import Path
 
 from nanoquant_amd.runtime import _native
 
-HEADER = Path(__file__).resolve().parent.parent / "include" / "nqamd.h"
+HEADERS = sorted((Path(__file__).resolve().parent.parent / "include").glob("*.h"))
 
 
 def _declared_functions() -> set[str]:
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return set(re.findall(r"\b(nq_[a-z0-9_]+)\s*\(", text))
+    names: set[str] = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(nq_[a-z0-9_]+)\s*\(", text))
+    return names
 
 
 def test_header_and_binding_agree():
