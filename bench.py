@@ -47,6 +47,9 @@ def parse_args(argv=None):
                    help="token counts of the Llama-3-8B prefill sweep ('' to skip)")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 10 times (byte-counter calibration) and exit")
+    p.add_argument("--e2e-tokens", type=int, default=128,
+                   help="greedy tokens of the end-to-end decoder run (0 to skip)")
+    p.add_argument("--e2e-prompt", type=int, default=512, help="prompt length of the end-to-end run")
     p.add_argument("--dominant-only", action="store_true",
                    help="only launch the dominant call (gate/up batch) of every layer eagerly --steps times "
                         "(per-dispatch counter collection) and exit")
@@ -328,6 +331,57 @@ def prefill_sweep(token_counts, steps: int, warmup: int) -> dict:
     }
 
 
+def e2e_decode(layers: int, prompt_len: int, new_tokens: int, repeats: int, packed_us_per_layer: float) -> dict:
+    """Greedy decode of a random-init Qwen3-8B-shaped model (36 layers, hidden
+    4096, intermediate 12288, GQA 32/8 x 128, vocab 151936; every projection
+    packed at ~1.0 bpw, bf16 N(0, 0.02) embeddings and untied lm_head, bf16
+    KV cache): a `prompt_len`-token prompt through the prefill path, then
+    `new_tokens` greedy tokens, each decode step one HIP-graph replay. Events
+    bracket prefill and decode; the best of `repeats` runs is reported."""
+
+    import torch
+
+    from nanoquant_amd import synthetic as syn
+    from nanoquant_amd.runtime.decoder_shell import DecoderShellConfig, PackedDecoder
+
+    device = torch.device("cuda", 0)
+    config = DecoderShellConfig(layers=layers)
+    weights = syn.synthetic_decoder(config, seed=syn.BASE_SEED + 5, device=device)
+    decoder = PackedDecoder(config, weights, device=device, max_positions=prompt_len + new_tokens)
+    del weights
+    g = torch.Generator().manual_seed(syn.BASE_SEED + 5)
+    prompt = torch.randint(0, config.vocab, (prompt_len,), generator=g).to(device)
+    decoder.generate_greedy(prompt, new_tokens)  # capture + warm-up
+    runs = []
+    tokens = None
+    for _ in range(repeats):
+        timing: dict = {}
+        out = decoder.generate_greedy(prompt, new_tokens, timings=timing)
+        if tokens is None:
+            tokens = out.tolist()
+        elif out.tolist() != tokens:
+            raise RuntimeError("end-to-end greedy decode is not deterministic across runs")
+        runs.append(timing)
+    best = min(runs, key=lambda r: r["decode_ms"])
+    decode_steps = new_tokens - 1
+    ms_per_token = best["decode_ms"] / decode_steps
+    kernels_per_layer = 12
+    return {
+        "workload": (f"qwen3-8b-shape random-init packed model, {layers} layers, vocab {config.vocab}, "
+                     f"prompt {prompt_len} ids, {new_tokens} greedy tokens, batch 1, bf16 activations/KV"),
+        "decode_tok_per_s": round(1000.0 / ms_per_token, 2),
+        "decode_ms_per_token": round(ms_per_token, 4),
+        "prefill_ms": round(best["prefill_ms"], 3),
+        "prefill_tok_per_s": round(prompt_len * 1000.0 / best["prefill_ms"], 1),
+        "total_tok_per_s": round(new_tokens * 1000.0 / (best["prefill_ms"] + best["decode_ms"]), 2),
+        "packed_linear_us_per_layer": round(packed_us_per_layer, 2),
+        "shell_us_per_token": round(ms_per_token * 1000.0 - packed_us_per_layer * layers, 1),
+        "kernels_per_token": layers * kernels_per_layer + 4,
+        "first_tokens": tokens[:8],
+        "repeats": repeats,
+    }
+
+
 def copy_calibration(mib: int) -> int:
     """A plain device-to-device copy of known size, for scaling HBM byte counters."""
 
@@ -450,6 +504,11 @@ def main(argv=None) -> int:
     if prefill_tokens:
         print(f"[bench] prefill sweep M={prefill_tokens}", file=sys.stderr, flush=True)
         result["prefill"] = prefill_sweep(prefill_tokens, max(args.steps // 2, 3), 2)
+    if args.e2e_tokens > 0:
+        print(f"[bench] end-to-end decode: prompt {args.e2e_prompt}, {args.e2e_tokens} tokens",
+              file=sys.stderr, flush=True)
+        packed_us = modes["grouped"]["ms_per_step"] * 1000.0 / args.layers if "grouped" in modes else float("nan")
+        result["e2e"] = e2e_decode(args.layers, args.e2e_prompt, args.e2e_tokens, 3, packed_us)
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.tokens, args.cpu_seconds, args.layers)

@@ -39,7 +39,7 @@ int nq_embedding(const int64_t* ids, int64_t tokens, const void* table, int32_t 
  *   residual[t, :] += delta[t, :]                      (skipped when delta is NULL)
  *   out[t, :] = weight * (residual[t, :] * rsqrt(mean(residual[t, :]^2) + eps))
  * residual fp32 (updated in place), delta F32/F16/BF16, weight F32/F16/BF16,
- * out F32/F16/BF16, hidden % 8 == 0. Replaces the residual adds of
+ * out F32/F16/BF16, hidden % 8 == 0 and hidden <= 16384. Replaces the residual adds of
  * Qwen3DecoderLayer.forward and Qwen3RMSNorm (the reference runs the
  * Transformers shell around its packed linears,
  * src/nanoquant/runtime/transformers_generation.py:84-114). */
@@ -79,6 +79,27 @@ int nq_attention(const float* q, const void* k_cache, const void* v_cache, int32
                  int64_t tokens, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
                  const int32_t* position, int64_t max_positions, float scaling, void* out,
                  int32_t out_dtype, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes of nq_decode_attention. */
+int64_t nq_decode_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                                            int32_t cache_dtype, int64_t max_positions);
+
+/* One decode token: nq_qk_norm_rope_cache followed by nq_attention with
+ * tokens == 1, as one kernel per layer when head_dim * cache element bytes
+ * <= 256 and q_heads / kv_heads is 1, 2, 4 or 8 (one workgroup per kv head
+ * and 1024-row cache range rotates its q heads, appends k/v at row
+ * position[0] when the range holds it, and attends over the range; ranges
+ * beyond the first are merged by a second kernel), otherwise as the two
+ * calls. q, k, v are the fp32 projection outputs [q_heads * head_dim],
+ * [kv_heads * head_dim] x2; out [q_heads * head_dim]. Replaces the pinned
+ * one-token rope / cache update / attention sequence of the reference
+ * (src/nanoquant/runtime/cuda_kernels.py:401-544,715-815). */
+int nq_decode_attention(const float* q, const float* k, const float* v, int32_t q_heads, int32_t kv_heads,
+                        int32_t head_dim, const void* q_norm, const void* k_norm, int32_t norm_dtype, float eps,
+                        const float* cos_table, const float* sin_table, const int32_t* position,
+                        int64_t max_positions, void* k_cache, void* v_cache, int32_t cache_dtype,
+                        float scaling, void* out, int32_t out_dtype, void* workspace,
+                        int64_t workspace_bytes, void* stream);
 
 /* out[i] = silu(gate[i]) * up[i], gate and up fp32, out F32/F16/BF16,
  * n % 8 == 0. Replaces the activation of Qwen3MLP.forward. */

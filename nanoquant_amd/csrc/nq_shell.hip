@@ -87,17 +87,6 @@ __device__ __forceinline__ void store8(void* __restrict__ p, int dtype, int64_t 
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = u;
 }
 
-// Sum over a 256-thread block: wave butterflies, then the four wave sums in
-// wave order (every thread gets the same value).
-__device__ __forceinline__ float block_sum256(float v, float* red) {
-    v = wave_sum(v);
-    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
-    __syncthreads();
-    const float total = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    return total;
-}
-
 // ---------------------------------------------------------------------------
 // Embedding gather.
 
@@ -123,36 +112,57 @@ __global__ __launch_bounds__(kRowThreads) void k_embedding(const int64_t* __rest
 }
 
 // ---------------------------------------------------------------------------
-// Residual add + RMSNorm (one workgroup per token row).
+// Residual add + RMSNorm, one workgroup of kNormThreads per token row. Thread
+// i holds elements [8 (i + kNormThreads j), +8) for j < NV in registers, so
+// residual, delta and weight are loaded in one round trip; the sum of squares
+// goes through wave butterflies and then the wave sums in wave order.
 
-__global__ __launch_bounds__(kRowThreads) void k_add_rmsnorm(float* __restrict__ residual, const void* __restrict__ delta,
-                                                             int ddt, const void* __restrict__ weight, int wdt,
-                                                             float eps, int64_t hidden, void* __restrict__ out, int odt) {
-    __shared__ float red[kRowThreads / kWave];
+constexpr int kNormThreads = 512;
+
+template <int NV>
+__global__ __launch_bounds__(kNormThreads) void k_add_rmsnorm(float* __restrict__ residual, const void* __restrict__ delta,
+                                                              int ddt, const void* __restrict__ weight, int wdt,
+                                                              float eps, int64_t hidden, void* __restrict__ out, int odt) {
+    __shared__ float red[kNormThreads / kWave];
     const int64_t row = static_cast<int64_t>(blockIdx.x) * hidden;
+    float v[NV][8], w[NV][8];
     float ss = 0.0f;
-    for (int64_t i = threadIdx.x * 8; i < hidden; i += kRowThreads * 8) {
-        float v[8];
-        load8(residual, NQ_DTYPE_F32, row + i, v);
-        if (delta) {
-            float d[8];
-            load8(delta, ddt, row + i, d);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) v[j] = __fadd_rn(v[j], d[j]);
-            store8(residual, NQ_DTYPE_F32, row + i, v);
+    for (int j = 0; j < NV; ++j) {
+        const int64_t i = (threadIdx.x + static_cast<int64_t>(kNormThreads) * j) * 8;
+        if (i < hidden) {
+            load8(residual, NQ_DTYPE_F32, row + i, v[j]);
+            load8(weight, wdt, i, w[j]);
+            if (delta) {
+                float d[8];
+                load8(delta, ddt, row + i, d);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[j][e] = __fadd_rn(v[j][e], d[e]);
+                store8(residual, NQ_DTYPE_F32, row + i, v[j]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[j][e] = w[j][e] = 0.0f;
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[j][e], v[j][e], ss);
     }
-    const float total = block_sum256(ss, red);
-    const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
-    for (int64_t i = threadIdx.x * 8; i < hidden; i += kRowThreads * 8) {
-        float v[8], w[8];
-        load8(residual, NQ_DTYPE_F32, row + i, v);  // this thread's own values
-        load8(weight, wdt, i, w);
+    ss = wave_sum(ss);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = ss;
+    __syncthreads();
+    float total = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = __fmul_rn(w[j], __fmul_rn(v[j], inv));
-        store8(out, odt, row + i, v);
+    for (int i = 0; i < kNormThreads / kWave; ++i) total += red[i];
+    const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int64_t i = (threadIdx.x + static_cast<int64_t>(kNormThreads) * j) * 8;
+        if (i < hidden) {
+            float o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = __fmul_rn(w[j][e], __fmul_rn(v[j][e], inv));
+            store8(out, odt, row + i, o);
+        }
     }
 }
 
@@ -162,23 +172,14 @@ __global__ __launch_bounds__(kRowThreads) void k_add_rmsnorm(float* __restrict__
 // d = l + 64 j, so for head_dim >= 128 the rotate-half partner d +- D/2 is
 // element j +- E/2 of the same lane; for head_dim 64 it is lane l ^ 32.
 
+// Lane's E = D / 64 elements d = lane + 64 j of one head vector: RMSNorm with
+// weight nw (when not NULL), then rotate-half RoPE with the table rows cr/sr.
 template <int D>
-__global__ __launch_bounds__(kWave) void k_qk_norm_rope_cache(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int q_heads,
-    int kv_heads, const void* __restrict__ q_norm, const void* __restrict__ k_norm, int ndt, float eps,
-    const float* __restrict__ cos_table, const float* __restrict__ sin_table, const int32_t* __restrict__ position,
-    int64_t max_positions, float* __restrict__ q_out, void* __restrict__ k_cache, void* __restrict__ v_cache, int cdt) {
+__device__ __forceinline__ void norm_rope(const float* __restrict__ src, const void* __restrict__ nw, int ndt, float eps,
+                                          const float* __restrict__ cr, const float* __restrict__ sr, int lane,
+                                          float (&y)[D / kWave]) {
     constexpr int E = D / kWave;
     constexpr int kHalf = D / 2;
-    const int64_t t = blockIdx.x;
-    const int h = blockIdx.y;
-    const int lane = threadIdx.x;
-    const int64_t pos = static_cast<int64_t>(position[0]) + t;
-    if (pos < 0 || pos >= max_positions) return;
-    const bool is_q = h < q_heads;
-    const int g = is_q ? h : h - q_heads;
-    const float* src = is_q ? q + (t * q_heads + h) * D : k + (t * kv_heads + g) * D;
-    const void* nw = is_q ? q_norm : k_norm;
     float x[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) x[j] = src[lane + kWave * j];
@@ -191,9 +192,6 @@ __global__ __launch_bounds__(kWave) void k_qk_norm_rope_cache(
 #pragma unroll
         for (int j = 0; j < E; ++j) x[j] = __fmul_rn(nq::load_f32(nw, ndt, lane + kWave * j), __fmul_rn(x[j], inv));
     }
-    const float* cr = cos_table + pos * kHalf;
-    const float* sr = sin_table + pos * kHalf;
-    float y[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) {
         const int d = lane + kWave * j;
@@ -208,6 +206,25 @@ __global__ __launch_bounds__(kWave) void k_qk_norm_rope_cache(
         const float rot = first ? -partner : partner;
         y[j] = __fadd_rn(__fmul_rn(x[j], cr[fi]), __fmul_rn(rot, sr[fi]));
     }
+}
+
+template <int D>
+__global__ __launch_bounds__(kWave) void k_qk_norm_rope_cache(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int q_heads,
+    int kv_heads, const void* __restrict__ q_norm, const void* __restrict__ k_norm, int ndt, float eps,
+    const float* __restrict__ cos_table, const float* __restrict__ sin_table, const int32_t* __restrict__ position,
+    int64_t max_positions, float* __restrict__ q_out, void* __restrict__ k_cache, void* __restrict__ v_cache, int cdt) {
+    constexpr int E = D / kWave;
+    const int64_t t = blockIdx.x;
+    const int h = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int64_t pos = static_cast<int64_t>(position[0]) + t;
+    if (pos < 0 || pos >= max_positions) return;
+    const bool is_q = h < q_heads;
+    const int g = is_q ? h : h - q_heads;
+    const float* src = is_q ? q + (t * q_heads + h) * D : k + (t * kv_heads + g) * D;
+    float y[E];
+    norm_rope<D>(src, is_q ? q_norm : k_norm, ndt, eps, cos_table + pos * (D / 2), sin_table + pos * (D / 2), lane, y);
     if (is_q) {
         float* dst = q_out + (t * q_heads + h) * D;
 #pragma unroll
@@ -398,11 +415,13 @@ __global__ __launch_bounds__(1024) void k_attention_blocks(const float* __restri
     }
 }
 
-// Attention, pass 2: merge the blocks of one (token, q head) in block order.
+// Attention, pass 2: merge the blocks (of block_rows cache rows each) of one
+// (token, q head) in block order.
 template <int D>
 __global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__ part_ml, const float* __restrict__ part_acc,
-                                                       int q_heads, int blocks, const int32_t* __restrict__ position,
-                                                       int64_t max_positions, void* __restrict__ out, int odt) {
+                                                       int q_heads, int blocks, int block_rows,
+                                                       const int32_t* __restrict__ position, int64_t max_positions,
+                                                       void* __restrict__ out, int odt) {
     const int h = blockIdx.x;
     const int64_t t = blockIdx.y;
     const int d = threadIdx.x;
@@ -412,7 +431,7 @@ __global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__
         nq::store_f32_as(out, odt, o, 0.0f);
         return;
     }
-    const int nb = static_cast<int>(pt / kSeqBlock) + 1;
+    const int nb = static_cast<int>(pt / block_rows) + 1;
     const int64_t p0 = attn_part_index(t, h, 0, q_heads, blocks);
     float mmax = -INFINITY;
     for (int b = 0; b < nb; ++b) mmax = fmaxf(mmax, part_ml[2 * (p0 + b)]);
@@ -423,6 +442,144 @@ __global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__
         acc = fmaf(part_acc[(p0 + b) * D + d], f, acc);
     }
     nq::store_f32_as(out, odt, o, acc / lsum);
+}
+
+// ---------------------------------------------------------------------------
+// One-token decode attention with the q/k RMSNorm + RoPE + KV append fused in
+// (pass 1; k_attention_merge is pass 2). Workgroup (kv head g, 64-row cache
+// block s), one wave per q head of the group:
+//   - every load is issued first: the block's K and V rows below the token's
+//     row p (coalesced 16-byte pieces), each wave's raw q head, and, in the
+//     block that holds p, the raw k and v of head g;
+//   - K and V rows go to LDS as stored; wave w normalises and rotates q head
+//     g * G + w into LDS; in p's block wave 0 rotates k and wave G - 1 (wave 0
+//     when G == 1) copies v into LDS row p - 64 s and into cache row p;
+//   - after one barrier lane j scores row 64 s + j (K row from LDS, q
+//     broadcast), the wave forms its softmax partial and lanes over
+//     dimensions accumulate P.V from LDS; the partial goes to the workspace.
+// Used when head_dim * element bytes <= 256 (the staged block fits LDS
+// twice) and G is 1, 2, 4 or 8.
+
+template <int D, int CT, int G>
+constexpr size_t decode_attention_lds() {
+    return static_cast<size_t>(kSeqBlock) * k_row_bytes<D, CT>() + static_cast<size_t>(kSeqBlock) * D * cache_bytes<CT>() +
+           static_cast<size_t>(G) * (D + kSeqBlock) * sizeof(float);
+}
+
+template <int D, int CT, int G>
+__global__ __launch_bounds__(G * kWave) void k_decode_attention(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int kv_heads,
+    const void* __restrict__ q_norm, const void* __restrict__ k_norm, int ndt, float eps,
+    const float* __restrict__ cos_table, const float* __restrict__ sin_table, const int32_t* __restrict__ position,
+    int64_t max_positions, char* __restrict__ k_cache, char* __restrict__ v_cache, float scaling,
+    float* __restrict__ part_ml, float* __restrict__ part_acc) {
+    constexpr int E = D / kWave;
+    constexpr int EB = cache_bytes<CT>();
+    constexpr int RB = k_row_bytes<D, CT>();   // padded K row in LDS
+    constexpr int VRB = D * EB;                // V row in LDS
+    constexpr int PIECES = D * EB / 16;        // 16-byte pieces per row
+    constexpr int PER_THREAD = kSeqBlock * PIECES / (G * kWave);
+    extern __shared__ float lds_raw[];
+    char* klds = reinterpret_cast<char*>(lds_raw);
+    char* vlds = klds + kSeqBlock * RB;
+    float* qs = reinterpret_cast<float*>(vlds + kSeqBlock * VRB);  // [G][D]
+    float* ps = qs + G * D;                                       // [G][64]
+
+    const int g = blockIdx.x;
+    const int s = blockIdx.y;
+    const int blocks = gridDim.y;
+    const int q_heads = kv_heads * G;
+    const int w = threadIdx.x / kWave;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t p = position[0];
+    const int64_t row0 = static_cast<int64_t>(s) * kSeqBlock;
+    if (p < 0 || p >= max_positions || row0 > p) return;  // uniform; the merge ignores such blocks
+    const bool owns_p = p < row0 + kSeqBlock;
+    const int rows = static_cast<int>(owns_p ? p - row0 + 1 : kSeqBlock);  // rows scored
+    const int cached = owns_p ? rows - 1 : rows;                              // rows read from the cache
+    const int64_t head_row0 = static_cast<int64_t>(g) * max_positions;
+
+    // Issue the loads.
+    uint4 kp[PER_THREAD], vp[PER_THREAD];
+    const char* kbase = k_cache + (head_row0 + row0) * VRB;
+    const char* vbase = v_cache + (head_row0 + row0) * VRB;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int idx = threadIdx.x + i * G * kWave;
+        const int r = idx / PIECES, c = idx % PIECES;
+        const int rr = r < cached ? r : 0;  // row 0 of the block is cached unless p == row0 (then unused)
+        kp[i] = *reinterpret_cast<const uint4*>(kbase + rr * VRB + 16 * c);
+        vp[i] = *reinterpret_cast<const uint4*>(vbase + rr * VRB + 16 * c);
+    }
+    const float* cr = cos_table + p * (D / 2);
+    const float* sr = sin_table + p * (D / 2);
+    float qy[E];
+    norm_rope<D>(q + static_cast<int64_t>(g * G + w) * D, q_norm, ndt, eps, cr, sr, lane, qy);
+    // Stage K and V rows below p.
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int idx = threadIdx.x + i * G * kWave;
+        const int r = idx / PIECES, c = idx % PIECES;
+        if (r < cached) {
+            *reinterpret_cast<uint4*>(klds + r * RB + 16 * c) = kp[i];
+            *reinterpret_cast<uint4*>(vlds + r * VRB + 16 * c) = vp[i];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < E; ++j) qs[w * D + lane + kWave * j] = qy[j];
+    if (owns_p) {
+        const int64_t crow = (head_row0 + p) * D;
+        const int r = rows - 1;
+        if (w == 0) {
+            float ky[E];
+            norm_rope<D>(k + static_cast<int64_t>(g) * D, k_norm, ndt, eps, cr, sr, lane, ky);
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                const int d = lane + kWave * j;
+                nq::store_f32_as(k_cache, CT, crow + d, ky[j]);
+                nq::store_f32_as(klds + r * RB, CT, d, ky[j]);
+            }
+        }
+        if (w == G - 1) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) {
+                const int d = lane + kWave * j;
+                const float vv = v[static_cast<int64_t>(g) * D + d];
+                nq::store_f32_as(v_cache, CT, crow + d, vv);
+                nq::store_f32_as(vlds + r * VRB, CT, d, vv);
+            }
+        }
+    }
+    __syncthreads();
+
+    // Scores, softmax partial, P.V for q head g * G + w.
+    const bool valid = lane < rows;
+    const float dot = k_row_dot<D, CT>(klds + (valid ? lane : 0) * RB, qs + w * D);
+    const float score = valid ? dot * scaling : -INFINITY;
+    const float m = wave_max(score);
+    const float pj = valid ? expf(score - m) : 0.0f;
+    const float l = wave_sum(pj);
+    float* pw = ps + w * kSeqBlock;
+    pw[lane] = pj;
+    __builtin_amdgcn_wave_barrier();
+    float acc[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = 0.0f;
+    for (int r = 0; r < rows; ++r) {
+        const float pr = pw[r];
+        float vv[E];
+        load_v<E, CT>(vlds + r * VRB + lane * E * EB, vv);
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[e] = fmaf(pr, vv[e], acc[e]);
+    }
+    const int h = g * G + w;
+    const int64_t pi = attn_part_index(0, h, s, q_heads, blocks);
+    if (lane == 0) {
+        part_ml[2 * pi] = m;
+        part_ml[2 * pi + 1] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) part_acc[pi * D + lane * E + e] = acc[e];
 }
 
 // ---------------------------------------------------------------------------
@@ -608,7 +765,7 @@ int launch_attention(const float* q, const void* kc, const void* vc, int64_t tok
                        position, max_positions, scaling, ml, acc);
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     hipLaunchKernelGGL(k_attention_merge<D>, dim3(q_heads, static_cast<unsigned>(tokens)), dim3(D), 0, st, ml, acc,
-                       q_heads, blocks, position, max_positions, out, odt);
+                       q_heads, blocks, kSeqBlock, position, max_positions, out, odt);
     return nq::launch_status();
 }
 
@@ -631,6 +788,48 @@ int launch_attention_for(int cdt, const float* q, const void* kc, const void* vc
     }
 }
 
+bool decode_fast_path(int head_dim, int cdt, int group) {
+    const int eb = cdt == NQ_DTYPE_F32 ? 4 : 2;
+    return head_dim * eb <= 256 && (group == 1 || group == 2 || group == 4 || group == 8);
+}
+
+int64_t round16(int64_t bytes) { return (bytes + 15) / 16 * 16; }
+
+template <int D, int CT, int G>
+int launch_decode_attention_g(const float* q, const float* k, const float* v, int kv_heads, const void* qn,
+                              const void* kn, int ndt, float eps, const float* cs, const float* sn,
+                              const int32_t* position, int64_t max_positions, void* kc, void* vc, float scaling,
+                              void* out, int odt, float* ml, float* acc, hipStream_t st) {
+    const int blocks = attention_blocks(max_positions);
+    const size_t lds = decode_attention_lds<D, CT, G>();
+    if (lds > 64 * 1024) return NQ_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((k_decode_attention<D, CT, G>), dim3(kv_heads, blocks), dim3(G * kWave), lds, st, q, k, v,
+                       kv_heads, qn, kn, ndt, eps, cs, sn, position, max_positions, static_cast<char*>(kc),
+                       static_cast<char*>(vc), scaling, ml, acc);
+    if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    hipLaunchKernelGGL(k_attention_merge<D>, dim3(kv_heads * G, 1), dim3(D), 0, st, ml, acc, kv_heads * G, blocks,
+                       kSeqBlock, position, max_positions, out, odt);
+    return nq::launch_status();
+}
+
+template <int D, int CT>
+int launch_decode_attention_ct(int group, const float* q, const float* k, const float* v, int kv_heads, const void* qn,
+                               const void* kn, int ndt, float eps, const float* cs, const float* sn,
+                               const int32_t* position, int64_t max_positions, void* kc, void* vc, float scaling,
+                               void* out, int odt, float* ml, float* acc, hipStream_t st) {
+#define NQ_DA(G)                                                                                                   \
+    return launch_decode_attention_g<D, CT, G>(q, k, v, kv_heads, qn, kn, ndt, eps, cs, sn, position, max_positions, \
+                                               kc, vc, scaling, out, odt, ml, acc, st)
+    switch (group) {
+        case 1: NQ_DA(1);
+        case 2: NQ_DA(2);
+        case 4: NQ_DA(4);
+        case 8: NQ_DA(8);
+        default: return NQ_ERR_UNSUPPORTED;
+    }
+#undef NQ_DA
+}
+
 }  // namespace
 
 extern "C" int nq_embedding(const int64_t* ids, int64_t tokens, const void* table, int32_t table_dtype, int64_t vocab,
@@ -649,12 +848,23 @@ extern "C" int nq_add_rmsnorm(float* residual, const void* delta, int32_t delta_
                               int32_t out_dtype, void* stream) {
     if (!residual || !weight || !out) return NQ_ERR_ARGUMENT;
     if ((delta && !float_code(delta_dtype)) || !float_code(weight_dtype) || !float_code(out_dtype)) return NQ_ERR_DTYPE;
-    if (tokens <= 0 || tokens > 0x7fffffff || hidden <= 0 || hidden % 8) return NQ_ERR_SHAPE;
+    if (tokens <= 0 || tokens > 0x7fffffff || hidden <= 0 || hidden % 8 || hidden > kNormThreads * 32)
+        return NQ_ERR_SHAPE;
     if (!(eps >= 0.0f)) return NQ_ERR_ARGUMENT;
     if (!aligned16(residual) || (delta && !aligned16(delta)) || !aligned16(weight) || !aligned16(out))
         return NQ_ERR_ALIGNMENT;
-    hipLaunchKernelGGL(k_add_rmsnorm, dim3(static_cast<unsigned>(tokens)), dim3(kRowThreads), 0, as_stream(stream),
-                       residual, delta, delta_dtype, weight, weight_dtype, eps, hidden, out, out_dtype);
+    const dim3 grid(static_cast<unsigned>(tokens)), block(kNormThreads);
+    hipStream_t st = as_stream(stream);
+    if (hidden <= kNormThreads * 8) {
+        hipLaunchKernelGGL(k_add_rmsnorm<1>, grid, block, 0, st, residual, delta, delta_dtype, weight, weight_dtype,
+                           eps, hidden, out, out_dtype);
+    } else if (hidden <= kNormThreads * 16) {
+        hipLaunchKernelGGL(k_add_rmsnorm<2>, grid, block, 0, st, residual, delta, delta_dtype, weight, weight_dtype,
+                           eps, hidden, out, out_dtype);
+    } else {
+        hipLaunchKernelGGL(k_add_rmsnorm<4>, grid, block, 0, st, residual, delta, delta_dtype, weight, weight_dtype,
+                           eps, hidden, out, out_dtype);
+    }
     return nq::launch_status();
 }
 
@@ -781,4 +991,62 @@ extern "C" int nq_greedy_select(const void* workspace, int64_t vocab, int64_t hi
                        static_cast<const uint64_t*>(workspace), wgs, token_out, history, history_capacity, step,
                        position);
     return nq::launch_status();
+}
+
+extern "C" int64_t nq_decode_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                                                       int32_t cache_dtype, int64_t max_positions) {
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || head_dim <= 0 || max_positions <= 0) return -1;
+    if (decode_fast_path(head_dim, cache_dtype, q_heads / kv_heads))
+        return nq_attention_workspace_bytes(1, q_heads, head_dim, max_positions);
+    const int64_t attn = nq_attention_workspace_bytes(1, q_heads, head_dim, max_positions);
+    return attn < 0 ? -1 : round16(static_cast<int64_t>(q_heads) * head_dim * 4) + attn;
+}
+
+extern "C" int nq_decode_attention(const float* q, const float* k, const float* v, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, const void* q_norm, const void* k_norm, int32_t norm_dtype,
+                                   float eps, const float* cos_table, const float* sin_table, const int32_t* position,
+                                   int64_t max_positions, void* k_cache, void* v_cache, int32_t cache_dtype,
+                                   float scaling, void* out, int32_t out_dtype, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+    if (!q || !k || !v || !cos_table || !sin_table || !position || !k_cache || !v_cache || !out || !workspace)
+        return NQ_ERR_ARGUMENT;
+    if (((q_norm || k_norm) && !float_code(norm_dtype)) || !float_code(cache_dtype) || !float_code(out_dtype))
+        return NQ_ERR_DTYPE;
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || max_positions <= 0 ||
+        attention_blocks(max_positions) > 65535)
+        return NQ_ERR_SHAPE;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return NQ_ERR_SHAPE;
+    if (!(eps >= 0.0f) || !(scaling > 0.0f)) return NQ_ERR_ARGUMENT;
+    if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(workspace)) return NQ_ERR_ALIGNMENT;
+    const int64_t need = nq_decode_attention_workspace_bytes(q_heads, kv_heads, head_dim, cache_dtype, max_positions);
+    if (need < 0) return NQ_ERR_SHAPE;
+    if (workspace_bytes < need) return NQ_ERR_WORKSPACE;
+    hipStream_t st = as_stream(stream);
+    const int group = q_heads / kv_heads;
+    if (!decode_fast_path(head_dim, cache_dtype, group)) {
+        // Unfused: rotate q into the workspace and append k/v, then attend.
+        float* q_rot = static_cast<float*>(workspace);
+        char* attn_ws = static_cast<char*>(workspace) + round16(static_cast<int64_t>(q_heads) * head_dim * 4);
+        int rc = nq_qk_norm_rope_cache(q, k, v, 1, q_heads, kv_heads, head_dim, q_norm, k_norm, norm_dtype, eps,
+                                       cos_table, sin_table, position, max_positions, q_rot, k_cache, v_cache,
+                                       cache_dtype, stream);
+        if (rc != NQ_OK) return rc;
+        return nq_attention(q_rot, k_cache, v_cache, cache_dtype, 1, q_heads, kv_heads, head_dim, position,
+                            max_positions, scaling, out, out_dtype, attn_ws,
+                            workspace_bytes - round16(static_cast<int64_t>(q_heads) * head_dim * 4), stream);
+    }
+    float* ml = static_cast<float*>(workspace);
+    float* acc = ml + 2 * static_cast<int64_t>(q_heads) * attention_blocks(max_positions);
+#define NQ_DAC(D, CT)                                                                                             \
+    return launch_decode_attention_ct<D, CT>(group, q, k, v, kv_heads, q_norm, k_norm, norm_dtype, eps, cos_table, \
+                                             sin_table, position, max_positions, k_cache, v_cache, scaling, out,   \
+                                             out_dtype, ml, acc, st)
+    if (head_dim == 64) {
+        if (cache_dtype == NQ_DTYPE_F32) NQ_DAC(64, NQ_DTYPE_F32);
+        if (cache_dtype == NQ_DTYPE_F16) NQ_DAC(64, NQ_DTYPE_F16);
+        NQ_DAC(64, NQ_DTYPE_BF16);
+    }
+    if (cache_dtype == NQ_DTYPE_F16) NQ_DAC(128, NQ_DTYPE_F16);
+    NQ_DAC(128, NQ_DTYPE_BF16);
+#undef NQ_DAC
 }

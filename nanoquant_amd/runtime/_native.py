@@ -54,6 +54,8 @@ EXPORTED_SYMBOLS = (
     "nq_qk_norm_rope_cache",
     "nq_attention_workspace_bytes",
     "nq_attention",
+    "nq_decode_attention_workspace_bytes",
+    "nq_decode_attention",
     "nq_silu_mul",
     "nq_output_projection_workspace_bytes",
     "nq_output_projection",
@@ -159,6 +161,12 @@ def _declare(lib: ctypes.CDLL) -> None:
         "nq_attention_workspace_bytes": (c_i64, [c_i64, i32, i32, c_i64]),
         "nq_attention": (
             c_int, [vp, vp, vp, i32, c_i64, i32, i32, i32, vp, c_i64, f32, vp, i32, vp, c_i64, vp],
+        ),
+        "nq_decode_attention_workspace_bytes": (c_i64, [i32, i32, i32, i32, c_i64]),
+        "nq_decode_attention": (
+            c_int,
+            [vp, vp, vp, i32, i32, i32, vp, vp, i32, f32, vp, vp, vp, c_i64, vp, vp, i32, f32, vp, i32, vp,
+             c_i64, vp],
         ),
         "nq_silu_mul": (c_int, [vp, vp, c_i64, vp, i32, vp]),
         "nq_output_projection_workspace_bytes": (c_i64, [c_i64, c_i64]),

@@ -12,11 +12,12 @@ shell built from this library's kernels instead:
   gate/up run as one batched decode call each (tokens <= 16), the prompt runs
   the MFMA prefill path;
 * embedding, residual add + RMSNorm, q/k RMSNorm + RoPE + KV append,
-  grouped-query attention, SiLU product, the bf16 output projection and
-  greedy selection are the HIP kernels of ``include/nqamd_shell.h``;
+  grouped-query attention (one fused kernel per layer for a decode token),
+  SiLU product, the bf16 output projection and greedy selection are the HIP
+  kernels of ``include/nqamd_shell.h``;
 * the KV cache is one device tensor per layer ``[kv_heads, max_positions,
   head_dim]``, and the token position lives in device memory, so one HIP graph
-  of the whole one-token step (about 14 launches per layer) replays for every
+  of the whole one-token step (12 launches per layer) replays for every
   position with no host synchronisation; ``generate_greedy`` keeps the chosen
   tokens on the device and synchronises once at the end.
 
@@ -195,8 +196,11 @@ class PackedDecoder:
             f32(tokens, kv_width), f32(tokens, c.q_heads, c.head_dim), a(tokens, q_width), f32(tokens, c.hidden),
             f32(tokens, c.intermediate), f32(tokens, c.intermediate), a(tokens, c.intermediate),
             f32(tokens, c.hidden), f32(tokens, c.hidden),
-            torch.empty(ops.attention_workspace_bytes(tokens, c.q_heads, c.head_dim, self.max_positions),
-                        dtype=torch.uint8, device=dev),
+            torch.empty(
+                ops.decode_attention_workspace_bytes(c.q_heads, c.kv_heads, c.head_dim, self.cache_dtype,
+                                                     self.max_positions)
+                if tokens == 1 else ops.attention_workspace_bytes(tokens, c.q_heads, c.head_dim, self.max_positions),
+                dtype=torch.uint8, device=dev),
         )
 
     # -- one forward -----------------------------------------------------------------
@@ -217,13 +221,21 @@ class PackedDecoder:
             in_norm, post_norm, qn, kn = self.norms[i]
             ops.launch_add_rmsnorm(b.residual, in_norm, c.eps, delta=b.down if i else None, out=b.xn)
             self._linears([b.xn] * 3, [prepared["q_proj"], prepared["k_proj"], prepared["v_proj"]], [b.q, b.k, b.v], t)
-            ops.launch_qk_norm_rope_cache(
-                b.q, b.k, b.v, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, q_norm=qn, k_norm=kn,
-                eps=c.eps, cos=self.cos, sin=self.sin, position=self.position, k_cache=self.k_cache[i],
-                v_cache=self.v_cache[i], q_out=b.q_rot,
-            )
-            ops.launch_attention(b.q_rot, self.k_cache[i], self.v_cache[i], position=self.position,
-                                 scaling=self.scaling, out=b.attn, workspace=b.attn_ws)
+            if t == 1:
+                ops.launch_decode_attention(
+                    b.q, b.k, b.v, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, q_norm=qn,
+                    k_norm=kn, eps=c.eps, cos=self.cos, sin=self.sin, position=self.position,
+                    k_cache=self.k_cache[i], v_cache=self.v_cache[i], scaling=self.scaling, out=b.attn,
+                    workspace=b.attn_ws,
+                )
+            else:
+                ops.launch_qk_norm_rope_cache(
+                    b.q, b.k, b.v, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, q_norm=qn,
+                    k_norm=kn, eps=c.eps, cos=self.cos, sin=self.sin, position=self.position,
+                    k_cache=self.k_cache[i], v_cache=self.v_cache[i], q_out=b.q_rot,
+                )
+                ops.launch_attention(b.q_rot, self.k_cache[i], self.v_cache[i], position=self.position,
+                                     scaling=self.scaling, out=b.attn, workspace=b.attn_ws)
             self._linears([b.attn], [prepared["o_proj"]], [b.o], t)
             ops.launch_add_rmsnorm(b.residual, post_norm, c.eps, delta=b.o, out=b.xn)
             self._linears([b.xn] * 2, [prepared["gate_proj"], prepared["up_proj"]], [b.gate, b.up], t)
@@ -288,10 +300,15 @@ class PackedDecoder:
         self.host_position = start + t
         return self.logits
 
-    def generate_greedy(self, prompt: torch.Tensor, max_new_tokens: int, *, use_graph: bool = True) -> torch.Tensor:
+    def generate_greedy(
+        self, prompt: torch.Tensor, max_new_tokens: int, *, use_graph: bool = True, timings: dict | None = None
+    ) -> torch.Tensor:
         """Greedy continuation of one prompt: prefill, then `max_new_tokens - 1`
         replays of the captured one-token step. Tokens stay on the device; the
-        only synchronisation is the caller's read of the result."""
+        only synchronisation is the caller's read of the result. With a
+        `timings` dict, device events bracket the prefill and the decode steps
+        and their milliseconds are stored under "prefill_ms" / "decode_ms"
+        (this synchronises once at the end)."""
 
         if max_new_tokens < 1 or max_new_tokens > self.history.numel():
             raise DecoderShellError("max_new_tokens outside the history capacity")
@@ -299,17 +316,27 @@ class PackedDecoder:
         if t + max_new_tokens - 1 > self.max_positions:
             raise DecoderShellError("prompt plus generated tokens exceed the KV cache")
         graph = self._decode_graph() if use_graph else None
+        if not use_graph:
+            self._decode_bufs = self._decode_bufs or self._buffers(1)
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(3)] if timings is not None else None
         self.reset()
+        if events:
+            events[0].record()
         self.prefill(prompt)
         ops.launch_greedy_select(self.proj_ws, self.config.vocab, self.config.hidden, token_out=self.ids,
                                  history=self.history, step=self.step)
-        if not use_graph:
-            self._decode_bufs = self._decode_bufs or self._buffers(1)
+        if events:
+            events[1].record()
         for _ in range(max_new_tokens - 1):
             if graph is not None:
                 graph.replay()
             else:
                 self._decode_body()
+        if events:
+            events[2].record()
+            events[2].synchronize()
+            timings["prefill_ms"] = events[0].elapsed_time(events[1])
+            timings["decode_ms"] = events[1].elapsed_time(events[2])
         self.host_position = t + max_new_tokens - 1
         return self.history[:max_new_tokens].clone()
 

@@ -142,6 +142,51 @@ def test_attention(tokens, start, q_heads, kv_heads, head_dim, cache_dtype):
     assert torch.equal(out, again)
 
 
+@pytest.mark.parametrize(
+    "q_heads,kv_heads,head_dim,cache_dtype,max_pos,p",
+    [
+        (32, 8, 128, torch.bfloat16, 640, 0),
+        (32, 8, 128, torch.bfloat16, 640, 577),
+        (32, 8, 128, torch.bfloat16, 640, 639),
+        (32, 8, 128, torch.bfloat16, 2500, 2300),  # three 1024-row ranges and the merge kernel
+        (16, 8, 128, torch.float16, 300, 130),
+        (8, 8, 64, torch.float32, 200, 150),
+        (64, 8, 128, torch.bfloat16, 1100, 1050),
+        (32, 8, 128, torch.float32, 640, 400),  # unfused fallback: K row > 256 bytes
+        (12, 4, 128, torch.bfloat16, 300, 200),  # unfused fallback: group of 3
+        (8, 2, 256, torch.bfloat16, 300, 77),  # unfused fallback: head_dim 256
+    ],
+)
+def test_decode_attention_fused(q_heads, kv_heads, head_dim, cache_dtype, max_pos, p):
+    g = _g(7)
+    q = 3 * torch.randn(q_heads * head_dim, generator=g)
+    k = 3 * torch.randn(kv_heads * head_dim, generator=g)
+    v = torch.randn(kv_heads * head_dim, generator=g)
+    qn = 1 + 0.1 * torch.randn(head_dim, generator=g)
+    kn = 1 + 0.1 * torch.randn(head_dim, generator=g)
+    cos, sin = ods.rope_tables(head_dim, 1e6, max_pos)
+    kc0 = torch.randn(kv_heads, max_pos, head_dim, generator=g).to(cache_dtype)
+    vc0 = torch.randn(kv_heads, max_pos, head_dim, generator=g).to(cache_dtype)
+    position = torch.tensor([p], dtype=torch.int32, device=DEV)
+    common = dict(q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, q_norm=qn.to(DEV), k_norm=kn.to(DEV),
+                  eps=1e-6, cos=cos.to(DEV), sin=sin.to(DEV), position=position)
+    kc, vc = kc0.to(DEV), vc0.to(DEV)
+    out = ops.launch_decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), k_cache=kc, v_cache=vc,
+                                      scaling=head_dim**-0.5, out_dtype=torch.float32, **common)
+    # the two-kernel sequence on a copy of the cache
+    kc2, vc2 = kc0.to(DEV), vc0.to(DEV)
+    q_rot = ops.launch_qk_norm_rope_cache(q.to(DEV), k.to(DEV), v.to(DEV), k_cache=kc2, v_cache=vc2, **common)
+    out2 = ops.launch_attention(q_rot.view(1, q_heads, head_dim), kc2, vc2, position=position,
+                                scaling=head_dim**-0.5, out_dtype=torch.float32)
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    expected = reference_attention(q_rot.view(1, q_heads, head_dim).cpu(), kc.cpu(), vc.cpu(), p, head_dim**-0.5)
+    assert relative_l2(out.view(1, -1).cpu(), expected) < 1e-5
+    assert relative_l2(out.view(1, -1), out2) < 1e-5
+    again = ops.launch_decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), k_cache=kc, v_cache=vc,
+                                        scaling=head_dim**-0.5, out_dtype=torch.float32, **common)
+    assert torch.equal(out, again)
+
+
 def test_attention_single_row_returns_value():
     kc = torch.randn(2, 64, 128).to(torch.bfloat16)
     vc = torch.randn(2, 64, 128).to(torch.bfloat16)
