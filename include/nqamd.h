@@ -145,6 +145,39 @@ int nq_count_bad_padding(const int32_t* words, int64_t rows, int64_t cols,
  * in time (one stream, or ordered streams). No reference counterpart. */
 int64_t nq_tiles_header_bytes(void);
 
+/* Prepare-time expansion of a mixed-V compact right factor
+ * (mixed-v-free-k10-pair9-v1) to canonical words out_words[rank, ceil(in/32)]:
+ * rows < free_rows copy free_words; every other word is one 19-bit record of
+ * the LSB-first payload (payload_words = ceil(records * 19 / 32)),
+ * codebook[index] with the two bits of its pair id flipped (ids enumerate
+ * bit pairs a < b < 32 in lexicographic order). *bad_records (device) is set
+ * to the count of ids past the 496 pairs. Replaces
+ * launch_decode_mixed_v_right_words
+ * (src/nanoquant/runtime/cuda_kernels.py:11-62,877-906). */
+int nq_decode_mixed_v_words(const int32_t* free_words, int64_t free_rows, const int32_t* payload,
+                            int64_t payload_words, const int32_t* codebook, int64_t rank,
+                            int64_t in_features, int32_t* out_words, int32_t* bad_records,
+                            void* stream);
+
+/* Prepare-time expansion of a product-codebook right factor
+ * (product-codebook-free-k16-v1): coded word = first_half[i & 255] |
+ * second_half[i >> 8] << 16 for the 16-bit index i of its record
+ * (payload_words = ceil(records / 2)). Device form of
+ * decode_product_codebook_right_words
+ * (src/nanoquant/runtime/product_codebook.py:102-128). */
+int nq_decode_product_codebook_words(const int32_t* free_words, int64_t free_rows,
+                                     const int32_t* payload, int64_t payload_words,
+                                     const int16_t* first_half, const int16_t* second_half,
+                                     int64_t rank, int64_t columns, int32_t* out_words,
+                                     void* stream);
+
+/* Packed sign-matrix transpose: out_words[cols, ceil(rows/32)] of the matrix
+ * words[rows, ceil(cols/32)] transposed (pad bits zero). Device form of the
+ * transposed-factorization conversion
+ * (src/nanoquant/runtime/product_codebook.py:232-250). */
+int nq_transpose_signs(const int32_t* words, int64_t rows, int64_t cols, int32_t* out_words,
+                       void* stream);
+
 /* Size in bytes of the GPU-private tiled weight layout for one linear:
  * header, V tiles, U tiles and 256 bytes of tail padding (the decode kernels
  * read whole 16-byte words per lane from clamped addresses). */

@@ -63,6 +63,31 @@ from nanoquant_amd.runtime.planning import (
     prepare_execution_workloads,
     prepare_plan,
 )
+from nanoquant_amd.runtime.decoder_shell import (
+    DecoderLayerWeights,
+    DecoderShellConfig,
+    DecoderShellError,
+    DecoderShellWeights,
+    PackedDecoder,
+)
+from nanoquant_amd.runtime.generation import (
+    GenerationError,
+    GenerationModel,
+    GenerationRequest,
+    GenerationResult,
+    GenerationStep,
+    SamplingConfig,
+    batch_prompts,
+    generate,
+)
+from nanoquant_amd.runtime.packed_artifact import (
+    OpenPackedArtifact,
+    PackedArtifactError,
+    PackedModelManifest,
+    RuntimeModelMetadata,
+    open_packed_artifact,
+    write_packed_artifact,
+)
 from nanoquant_amd.runtime.row_sidecar import OutputRowSidecar, RowSidecarLayerState
 from nanoquant_amd.runtime.torch_model import (
     PreparedLinear,

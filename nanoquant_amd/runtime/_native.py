@@ -49,6 +49,9 @@ EXPORTED_SYMBOLS = (
     "nq_linear_workspace_bytes",
     "nq_linear",
     "nq_linear_batch",
+    "nq_decode_mixed_v_words",
+    "nq_decode_product_codebook_words",
+    "nq_transpose_signs",
     "nq_embedding",
     "nq_add_rmsnorm",
     "nq_qk_norm_rope_cache",
@@ -152,6 +155,9 @@ def _declare(lib: ctypes.CDLL) -> None:
             [ctypes.POINTER(desc_p), ctypes.c_int32, ctypes.POINTER(vp), ctypes.c_int32, c_i64,
              ctypes.POINTER(vp), ctypes.c_int32, ctypes.POINTER(vp), ctypes.POINTER(c_i64), vp],
         ),
+        "nq_decode_mixed_v_words": (c_int, [vp, c_i64, vp, c_i64, vp, c_i64, c_i64, vp, vp, vp]),
+        "nq_decode_product_codebook_words": (c_int, [vp, c_i64, vp, c_i64, vp, vp, c_i64, c_i64, vp, vp]),
+        "nq_transpose_signs": (c_int, [vp, c_i64, c_i64, vp, vp]),
         "nq_embedding": (c_int, [vp, c_i64, vp, i32, c_i64, c_i64, vp, vp, vp]),
         "nq_add_rmsnorm": (c_int, [vp, vp, i32, vp, i32, f32, c_i64, c_i64, vp, i32, vp]),
         "nq_qk_norm_rope_cache": (

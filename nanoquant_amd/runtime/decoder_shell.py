@@ -93,6 +93,76 @@ class DecoderShellWeights:
     layers: list[DecoderLayerWeights] = field(default_factory=list)
 
 
+# Transformers names of the dense tensors of a Qwen3 checkpoint.
+QWEN3_DENSE_NAMES = {
+    "embed": "model.embed_tokens.weight",
+    "lm_head": "lm_head.weight",
+    "final_norm": "model.norm.weight",
+    "input_norm": "model.layers.{layer}.input_layernorm.weight",
+    "post_norm": "model.layers.{layer}.post_attention_layernorm.weight",
+    "q_norm": "model.layers.{layer}.self_attn.q_norm.weight",
+    "k_norm": "model.layers.{layer}.self_attn.k_norm.weight",
+}
+PACKED_LAYER_NAME = "blocks.{layer}.{module}.{role}"
+
+
+def load_decoder_weights(
+    artifact,
+    dense: dict[str, torch.Tensor],
+    config: DecoderShellConfig,
+    *,
+    device: torch.device | str = "cpu",
+    layer_name: str = PACKED_LAYER_NAME,
+    dense_names: dict[str, str] = QWEN3_DENSE_NAMES,
+) -> DecoderShellWeights:
+    """Decoder weights from a packed artifact (every projection, via
+    ``OpenPackedArtifact.load_layer``) and the checkpoint's dense tensors
+    (embeddings, norms, ``lm_head``; a missing ``lm_head`` means tied
+    embeddings). Packed layer names follow `layer_name` with ``module`` =
+    ``self_attn`` / ``mlp``."""
+
+    def get(key: str, **fmt) -> torch.Tensor:
+        name = dense_names[key].format(**fmt)
+        if name not in dense:
+            raise KeyError(f"dense tensor missing from the checkpoint: {name}")
+        return dense[name].to(device)
+
+    embed = get("embed")
+    lm_head = dense[dense_names["lm_head"]].to(device) if dense_names["lm_head"] in dense else embed
+    if tuple(embed.shape) != (config.vocab, config.hidden) or tuple(lm_head.shape) != (config.vocab, config.hidden):
+        raise DecoderShellError("embedding / lm_head shapes do not match the configuration")
+    dims = config.linear_dims()
+    layers = []
+    for layer in range(config.layers):
+        linears = {}
+        for i, role in enumerate(ROLES):
+            state = artifact.load_layer(layer_name.format(layer=layer, module="self_attn" if i < 4 else "mlp",
+                                                          role=role), device)
+            if (state.spec.in_features, state.spec.out_features) != dims[role]:
+                raise DecoderShellError(f"packed layer {state.spec.name} does not match the configuration")
+            linears[role] = state
+        qn = get("q_norm", layer=layer) if config.qk_norm else None
+        kn = get("k_norm", layer=layer) if config.qk_norm else None
+        layers.append(DecoderLayerWeights(get("input_norm", layer=layer), get("post_norm", layer=layer), qn, kn,
+                                          linears))
+    return DecoderShellWeights(embed, lm_head, get("final_norm"), layers)
+
+
+def dense_tensors(weights: DecoderShellWeights, dense_names: dict[str, str] = QWEN3_DENSE_NAMES) -> dict[str, torch.Tensor]:
+    """The dense tensors of `weights` under checkpoint names (inverse of the
+    dense part of ``load_decoder_weights``)."""
+
+    out = {dense_names["embed"]: weights.embed, dense_names["lm_head"]: weights.lm_head,
+           dense_names["final_norm"]: weights.final_norm}
+    for i, layer in enumerate(weights.layers):
+        out[dense_names["input_norm"].format(layer=i)] = layer.input_norm
+        out[dense_names["post_norm"].format(layer=i)] = layer.post_norm
+        if layer.q_norm is not None:
+            out[dense_names["q_norm"].format(layer=i)] = layer.q_norm
+            out[dense_names["k_norm"].format(layer=i)] = layer.k_norm
+    return out
+
+
 def rope_tables(head_dim: int, theta: float, positions: int) -> tuple[torch.Tensor, torch.Tensor]:
     """cos/sin ``[positions, head_dim / 2]`` fp32 of ``position * inv_freq`` with
     ``inv_freq = 1 / theta^(arange(0, D, 2) / D)``, computed on the host in fp32

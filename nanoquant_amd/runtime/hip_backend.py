@@ -17,6 +17,7 @@ from dataclasses import dataclass, field, replace
 import torch
 
 from nanoquant_amd.runtime import _native
+from nanoquant_amd.runtime.codecs import MixedVLayerState, ProductCodebookLayerState, device_packed_state
 from nanoquant_amd.runtime.backend import (
     BackendCapabilities,
     DeviceLike,
@@ -158,12 +159,13 @@ class HipPackedBackend:
         return result
 
     def prepare(self, state: RuntimeLayerState, device: DeviceLike) -> PreparedLayer:
-        if isinstance(state, RowSidecarLayerState):
-            packed, rows = state.base, state.rows
-        elif isinstance(state, PackedLayerState):
-            packed, rows = state, None
-        else:
-            raise TypeError("HIP packed backend requires PackedLayerState or RowSidecarLayerState")
+        """Copy a layer to the device once and build its tile layout. Compact
+        right factors (mixed-V, product codebook) are expanded on the device, as
+        the reference backend does for mixed-V (src/nanoquant/runtime/cuda_backend.py:199-241)."""
+
+        if not isinstance(state, (RowSidecarLayerState, PackedLayerState, MixedVLayerState, ProductCodebookLayerState)):
+            raise TypeError("HIP packed backend requires PackedLayerState, RowSidecarLayerState, MixedVLayerState "
+                            "or ProductCodebookLayerState")
         target = torch.device(device)
         if target.type != "cuda":
             raise ValueError("HIP packed backend preparation requires a CUDA (HIP) device")
@@ -171,6 +173,13 @@ class HipPackedBackend:
             raise RuntimeError("CUDA is not available in this runtime")
         if target.index is None:
             target = torch.device("cuda", torch.cuda.current_device())
+        if isinstance(state, RowSidecarLayerState):
+            packed, rows = state.base, state.rows
+        elif isinstance(state, PackedLayerState):
+            packed, rows = state, None
+        else:
+            with torch.cuda.device(target):
+                packed, rows = device_packed_state(state, target), None
         lib = _native.load()
         payload = _HipPackedPayload(
             target,
