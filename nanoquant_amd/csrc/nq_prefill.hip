@@ -1,5 +1,5 @@
 // Prefill path (tokens > 16) for the packed binary low-rank linear on gfx950:
-// two dense sign GEMMs on v_mfma_f32_16x16x32_f16.
+// two dense sign GEMMs on v_mfma_f32_32x32x16_f16.
 //
 //   k_prep_rows:  xs16[t, :] = fp16(x[t, :] * s_in * 2^e_t)       (exact power of
 //                 two per row from max |x * s_in|, so fp16 cannot overflow)
@@ -10,20 +10,22 @@
 //
 // The sign operand comes straight from the decode tile layout (16-row tiles;
 // in 128-column block kb = 4c + d a lane's word d of chunk c holds, at bit
-// 8b + m, column 128kb + 16m + 4g + b for lane group g). A wave loads the
-// words of its four 16-row tiles for one block and expands them in registers
-// to fp16 ±1: bits 8b + m and 8b + m + 16 (columns +b and +b + 2) become one
-// dword with one shift and one and_or. MFMA p (32 columns 32p..32p+31 of the
-// block) takes the dwords (b, m) = (0, 2p), (1, 2p), (0, 2p+1), (1, 2p+1), so
-// lane group g's eight B values are columns 32p + 4g + [0, 2, 1, 3] and
-// 32p + 16 + 4g + [0, 2, 1, 3]. k_prep_rows stores activation rows with
-// columns 1 and 2 of every group of four swapped, so the matching A operand is
-// two 8-byte LDS reads. Every expanded operand is reused for the wave's four
-// 16-row M tiles. The activation tile (128 rows x 128 columns fp16) is staged
-// in LDS with a padded row stride.
+// 8b + m, column 128kb + 16m + 4g + b for lane group g). A 32 x 32 x 16 MFMA
+// over 16-column slice m takes, in lane 32h + r, the 8 k slots of B column r
+// (sign row r of a 32-row pair of tiles) for columns 16m + 8h + [0, 8): the
+// words of lane groups 2h and 2h + 1 of row r hold exactly those columns, so
+// each lane loads two words per tile pair and 128-column block and expands
+// them in registers (one shift and one and_or per fp16 pair). k_prep_rows
+// stores activation rows with columns 1 and 2 of every group of four swapped,
+// which puts the A operand's 8 k slots in the same order: one 16-byte LDS
+// read per A fragment. Each expanded B fragment serves two A fragments and
+// each A fragment two B fragments.
 //
 // Block tile 128 (tokens) x 128 (sign rows), 4 waves in a 2 x 2 grid, each
-// wave 64 x 64 = 4 x 4 MFMA tiles of 16 x 16 accumulated in fp32.
+// wave 64 x 64 = 2 x 2 MFMA tiles of 32 x 32 accumulated in fp32. The
+// activation tile (128 x 128 fp16, padded rows) is double-buffered in LDS:
+// the loads of the next 128-column block are in flight during the current
+// block's MFMAs, and one barrier per block orders the buffer swap.
 //
 // Split K: when a GEMM has too few (token, sign-row) tiles to fill the GPU,
 // grid dimension z splits the K blocks into ranges of at least four and each
@@ -37,6 +39,7 @@ namespace {
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kBlock = 256;
 constexpr int kBM = 128;
@@ -47,7 +50,7 @@ constexpr int kTileRows = 16;
 constexpr int kParkStride = 65;          // floats per parked accumulator row
 constexpr int kALdsBytes = kBM * kAStride * 2;
 constexpr int kParkBytes = 4 * 64 * kParkStride * 4;
-constexpr int kLdsBytes = kALdsBytes > kParkBytes ? kALdsBytes : kParkBytes;
+constexpr int kLdsBytes = 2 * kALdsBytes > kParkBytes ? 2 * kALdsBytes : kParkBytes;  // double-buffered A
 
 __device__ __forceinline__ float exp2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
 
@@ -153,19 +156,31 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ a
     if (threadIdx.x == 0) scale_out[t] = scale;
 }
 
-// B operand of MFMA p from one word: dwords (b, m) = (0, 2p), (1, 2p),
-// (0, 2p + 1), (1, 2p + 1), each bits 8b + m and 8b + m + 16 moved to the fp16
-// sign positions 15 and 31.
-__device__ __forceinline__ v8h expand_signs(uint32_t word, int p) {
+// B operand of the 32 x 32 x 16 MFMA of 16-column slice m from the words of
+// lane groups 2h and 2h + 1 (w0, w1): at bit 8b + m they hold columns
+// 16m + 8h + b and 16m + 8h + 4 + b. The A rows are stored with columns 1 and
+// 2 of every group of four swapped, so the eight k slots of a lane are columns
+// 8h + {0, 2, 1, 3, 4, 6, 5, 7}: dword e pairs bits (m, m + 16) or
+// (m + 8, m + 24) of one word, which one shift moves to the fp16 sign
+// positions 15 and 31.
+__device__ __forceinline__ uint32_t sign_pair(uint32_t w, int shift, uint32_t mask, uint32_t one) {
+    // ((w << shift) & mask) | one as two instructions: the masks are kept in
+    // registers because a VOP3 instruction cannot take two literal constants.
+    uint32_t d;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(w << shift), "v"(mask), "v"(one));
+    return d;
+}
+
+__device__ __forceinline__ v8h expand_signs32(uint32_t w0, uint32_t w1, int m, uint32_t mask, uint32_t one) {
     union {
         uint32_t u[4];
         v8h v;
-    } r;
-    r.u[0] = ((word << (15 - 2 * p)) & 0x80008000u) | 0x3C003C00u;
-    r.u[1] = ((word << (7 - 2 * p)) & 0x80008000u) | 0x3C003C00u;
-    r.u[2] = ((word << (14 - 2 * p)) & 0x80008000u) | 0x3C003C00u;
-    r.u[3] = ((word << (6 - 2 * p)) & 0x80008000u) | 0x3C003C00u;
-    return r.v;
+    } x;
+    x.u[0] = sign_pair(w0, 15 - m, mask, one);
+    x.u[1] = sign_pair(w0, 7 - m, mask, one);
+    x.u[2] = sign_pair(w1, 15 - m, mask, one);
+    x.u[3] = sign_pair(w1, 7 - m, mask, one);
+    return x.v;
 }
 
 struct GemmArgs {
@@ -198,95 +213,116 @@ struct GemmArgs {
 
 __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
     __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
-    _Float16* const a_lds = reinterpret_cast<_Float16*>(lds);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave >> 1;  // wave row in the 2 x 2 grid
     const int wn = wave & 1;
+    const int h = lane >> 5;   // K half of the 32 x 32 x 16 operands
+    const int r = lane & 31;   // A row / B column within a 32-wide fragment
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kBN;
     const int64_t rt_count = (g.n + kTileRows - 1) / kTileRows;
-    const int64_t rt0 = n0 / kTileRows + 4 * wn;  // first 16-row tile of this wave
+    // B fragment jj covers sign rows n0 + 64 wn + 32 jj + [0, 32): lane r reads
+    // row r of tile (r >> 4) of that pair, from the words of lane groups 2h
+    // and 2h + 1, which hold columns 16m + 8h + [0, 8) of each 16-column slice.
+    const int64_t rt0 = n0 / kTileRows + 4 * wn + (r >> 4);
+    const int wl0 = 16 * (2 * h) + (r & 15), wl1 = wl0 + 16;
 
-    v4f acc[4][4];
+    v16f acc[2][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
 
-    // Software pipeline: the sign words and the activation tile of superchunk
-    // sc + 1 are loaded into registers while superchunk sc runs on the MFMAs.
-    uint32_t words[4], next_words[4];
+    uint32_t words[2][2], next_words[2][2];
     uint4 next_a[8];
-    // Plain locals (not the by-value kernel argument) so the loader stays in registers.
-    const uint32_t* const tiles = g.tiles;
-    const _Float16* const act = g.a;
-    const int64_t nsc = g.nb, kpad = g.kpad, mrows = g.m;
-    auto load_step = [&](int64_t sc) {
-        // Block sc is word d of chunk c; the chunk holds dw words per lane.
-        const int64_t c = sc >> 2;
-        const int d = static_cast<int>(sc & 3);
-        const int64_t rem = nsc - 4 * c;
-        const int dw = static_cast<int>(rem < 4 ? rem : 4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t rt = rt0 + j;
-            next_words[j] = rt < rt_count ? tiles[rt * nsc * 64 + c * 256 + lane * dw + d] : 0u;
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int v = threadIdx.x + i * kBlock;
-            const int64_t row = m0 + (v >> 4);
-            next_a[i] = row < mrows ? *reinterpret_cast<const uint4*>(act + row * kpad + sc * kBK + (v & 15) * 8)
-                                    : make_uint4(0, 0, 0, 0);
-        }
-    };
+    // Loads are unconditional: rows past M and sign tiles past N read a valid
+    // row / tile instead; they only feed accumulators whose outputs are never
+    // stored.
+    const int64_t nsc = g.nb, kpad = g.kpad;
+    const int a_row = threadIdx.x >> 4, a_col = (threadIdx.x & 15) * 8;
+    const int64_t a_last = g.m - 1 - m0;  // last valid row of this block
+    const _Float16* const a_base = g.a + m0 * kpad + a_col;
+    const int64_t rt_a = rt0 < rt_count ? rt0 : rt_count - 1;
+    const int64_t rt_b = rt0 + 2 < rt_count ? rt0 + 2 : rt_count - 1;
+    const uint32_t* const b0 = g.tiles + rt_a * nsc * 64;
+    const uint32_t* const b1 = g.tiles + rt_b * nsc * 64;
     const int64_t k_begin = static_cast<int64_t>(blockIdx.z) * g.k_per_split;
     const int64_t k_end = k_begin + g.k_per_split < nsc ? k_begin + g.k_per_split : nsc;
-    load_step(k_begin);
+#define NQ_LOAD_STEP(SC)                                                                            \
+    do {                                                                                            \
+        const int64_t c_ = (SC) >> 2;                                                               \
+        const int64_t rem_ = nsc - 4 * c_;                                                          \
+        const int dw_ = static_cast<int>(rem_ < 4 ? rem_ : 4);                                      \
+        const int64_t off_ = c_ * 256 + ((SC) & 3);                                                 \
+        next_words[0][0] = b0[off_ + wl0 * dw_];                                                    \
+        next_words[0][1] = b0[off_ + wl1 * dw_];                                                    \
+        next_words[1][0] = b1[off_ + wl0 * dw_];                                                    \
+        next_words[1][1] = b1[off_ + wl1 * dw_];                                                    \
+        _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) {                                          \
+            const int64_t r_ = a_row + 16 * i_ < a_last ? a_row + 16 * i_ : a_last;                 \
+            next_a[i_] = *reinterpret_cast<const uint4*>(a_base + r_ * kpad + (SC) * kBK);          \
+        }                                                                                           \
+    } while (0)
+#define NQ_STAGE_A(BUF)                                                                             \
+    do {                                                                                            \
+        _Float16* dst_ = reinterpret_cast<_Float16*>(lds) + (BUF) * (kBM * kAStride) + a_col;      \
+        _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_)                                            \
+            *reinterpret_cast<uint4*>(dst_ + (a_row + 16 * i_) * kAStride) = next_a[i_];            \
+    } while (0)
+    // Double-buffered activation tile: step s computes on buffer s & 1 while
+    // the loads of step s + 1 are in flight; they go to the other buffer after
+    // the compute, and one barrier per step orders both.
+    NQ_LOAD_STEP(k_begin);
+    NQ_STAGE_A(0);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) words[jj][0] = next_words[jj][0], words[jj][1] = next_words[jj][1];
+    __syncthreads();
+    int buf = 0;
+    uint32_t sign_mask = 0x80008000u, fp16_one = 0x3C003C00u;
+    asm volatile("" : "+v"(sign_mask), "+v"(fp16_one));  // keep them in VGPRs
     for (int64_t sc = k_begin; sc < k_end; ++sc) {
-        __syncthreads();  // previous step's LDS reads are done
+        // The last step prefetches its own block again (into the idle buffer)
+        // so that the prefetch registers are written on every path.
+        const int64_t next = sc + 1 < k_end ? sc + 1 : sc;
+        NQ_LOAD_STEP(next);
+        const _Float16* a_lds = reinterpret_cast<const _Float16*>(lds) + buf * (kBM * kAStride);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int v = threadIdx.x + i * kBlock;
-            *reinterpret_cast<uint4*>(&a_lds[(v >> 4) * kAStride + (v & 15) * 8]) = next_a[i];
-        }
+        for (int m = 0; m < 8; ++m) {
+            v8h b[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) words[j] = next_words[j];
-        __syncthreads();
-        if (sc + 1 < k_end) load_step(sc + 1);
+            for (int jj = 0; jj < 2; ++jj) b[jj] = expand_signs32(words[jj][0], words[jj][1], m, sign_mask, fp16_one);
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-            v8h b[4];
+            for (int ii = 0; ii < 2; ++ii) {
+                const v8h a = *reinterpret_cast<const v8h*>(&a_lds[(64 * wm + 32 * ii + r) * kAStride + 16 * m + 8 * h]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = expand_signs(words[j], kc);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 64 * wm + 16 * i + (lane & 15);
-                const _Float16* ap = &a_lds[r * kAStride + 32 * kc + 4 * (lane >> 4)];
-                const v4h lo = *reinterpret_cast<const v4h*>(ap);
-                const v4h hi = *reinterpret_cast<const v4h*>(ap + 16);
-                const v8h a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b[j], acc[i][j], 0, 0, 0);
+                for (int jj = 0; jj < 2; ++jj)
+                    acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[jj], acc[ii][jj], 0, 0, 0);
             }
         }
+        NQ_STAGE_A(buf ^ 1);
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) words[jj][0] = next_words[jj][0], words[jj][1] = next_words[jj][1];
+        __syncthreads();
+        buf ^= 1;
     }
+#undef NQ_LOAD_STEP
+#undef NQ_STAGE_A
+
 
     // Epilogue through LDS: each wave parks its 64 x 64 fp32 tile (lane holds
-    // D[4*(lane/16) + q][lane % 16] of each 16 x 16 MFMA tile), then walks it
-    // row by row with lane = column, so every output row segment is one
-    // coalesced 64-wide store and the salient sum joins before the single
-    // rounding to the output dtype.
-    __syncthreads();  // every wave is done reading the activation tile
+    // D[8 (q / 4) + 4 (lane / 32) + q % 4][lane % 32] of each 32 x 32 MFMA
+    // tile), then walks it row by row with lane = column, so every output row
+    // segment is one coalesced 64-wide store and the salient sum joins before
+    // the single rounding to the output dtype.
     float* park = reinterpret_cast<float*>(lds) + wave * (64 * kParkStride);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                park[(16 * i + 4 * (lane >> 4) + q) * kParkStride + 16 * j + (lane & 15)] = acc[i][j][q];
+            for (int q = 0; q < 16; ++q)
+                park[(32 * ii + 8 * (q >> 2) + 4 * h + (q & 3)) * kParkStride + 32 * jj + r] = acc[ii][jj][q];
     __syncthreads();
     const int64_t col = n0 + 64 * wn + lane;
     const int64_t row0 = m0 + 64 * wm;
@@ -302,7 +338,10 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
     const int64_t salient = g.salient_count;
     for (int e = 0; e < rows; ++e) {
         const int64_t row = row0 + e;
-        float v = park[e * kParkStride + lane] / g.row_scale[row] * cs + bias;
+        // row_scale is a normal power of two: its reciprocal (exponent field
+        // 254 - E) is exact, and so is multiplying by it.
+        const float inv = __uint_as_float((254u << 23) - (__float_as_uint(g.row_scale[row]) & 0x7f800000u));
+        float v = park[e * kParkStride + lane] * inv * cs + bias;
         for (int64_t k = 0; k < salient; ++k) {
             float w = nq::load_f32(g.salient_values, g.salient_dtype, col * salient + k);
             if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
