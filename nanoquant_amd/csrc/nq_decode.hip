@@ -157,11 +157,12 @@ void pick_waves(int64_t nc, int tpb, int tb, int& nw, int& kc) {
     }
 }
 
-// Dynamic LDS of a stage: per-wave operand areas (stage 1 only), the partial
-// sums [nc][tw][tb][64] and the chunk maxima [nc][tpb * tb] (stage 1 only).
-size_t lds_bytes(int stage, int tpb, int tb, int tw, int nw, int64_t nc) {
+// Dynamic LDS of a stage: per-wave operand areas (stage 1), the partial sums
+// [nc][tw][tb][64], the chunk maxima [nc][tpb * tb] (stage 1) and, for one
+// token, kc operand spread areas per wave (stage 2).
+size_t lds_bytes(int stage, int tpb, int tb, int tw, int nw, int kc, int64_t nc) {
     const size_t red = static_cast<size_t>(nc) * tw * tb * 64 * 4;
-    if (stage == 2) return red;
+    if (stage == 2) return red + (tpb == 1 ? static_cast<size_t>(nw) * kc * kS2SpreadBytes : 0);
     return static_cast<size_t>(nw) * (8 * 4 * tpb * 4 * 16) + red + static_cast<size_t>(nc) * tpb * tb * 4;
 }
 
@@ -226,16 +227,17 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
     const unsigned count = static_cast<unsigned>(batch.count);
 
     if (fused) {
-        const size_t l1 = lds_bytes(1, s1.tpb, s1.tb, 1, s1.nw, nc1), l2 = lds_bytes(2, s1.tpb, s1.tb, 1, s1.nw, nc2);
+        const size_t l1 = lds_bytes(1, s1.tpb, s1.tb, 1, s1.nw, s1.kc, nc1),
+                     l2 = lds_bytes(2, s1.tpb, s1.tb, 1, s1.nw, s1.kc2, nc2);
         s1.lds = l1 > l2 ? l1 : l2;
         s1.grid = dim3(static_cast<unsigned>(max1 > max2 ? max1 : max2), 2 * count);
         return enqueue_fused(batch, s1, stream);
     }
-    s1.lds = lds_bytes(1, s1.tpb, s1.tb, s1.tw, s1.nw, nc1);
+    s1.lds = lds_bytes(1, s1.tpb, s1.tb, s1.tw, s1.nw, s1.kc, nc1);
     s1.grid = dim3(static_cast<unsigned>(max1), count);
     int st = enqueue_stage1(batch, s1, stream);
     if (st != NQ_OK) return st;
-    s2.lds = lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, nc2);
+    s2.lds = lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, s2.kc, nc2);
     s2.grid = dim3(static_cast<unsigned>(max2), count);
     return enqueue_stage2(batch, s2, stream);
 }

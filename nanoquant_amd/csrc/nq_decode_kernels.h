@@ -457,21 +457,48 @@ __device__ __forceinline__ void load_words(v4u (&w)[TW], const uint32_t* tiles, 
     }
 }
 
-template <int TPB, int TB, int TW>
-__device__ __forceinline__ void load_s2_ops(S2Regs<TB, TW>& r, const LinArgs& a, int64_t c, int lane) {
-    const int row = TPB == 1 ? (lane & 3) : (lane & 15);
-#pragma unroll
-    for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-        for (int m = 0; m < 8; ++m)
-            r.a[tb][m] = *reinterpret_cast<const v4i*>(a.lmq + lmq_offset<TPB, TB>(c, tb, m, row, lane >> 4));
-}
-
 // Order this wave's LDS writes before its own reads (waves never share areas).
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
+}
+
+// Stage-2 A operands of chunk c. The eight operands of a one-token block
+// repeat four digit rows over the sixteen MFMA rows, so loading them directly
+// would fetch every byte four times: one token loads the chunk's 2 KB once
+// (two 16-byte loads per lane) and spread_s2_ops distributes it through the
+// wave's LDS area.
+constexpr int kS2SpreadBytes = 8 * 4 * 4 * 16;
+
+template <int TPB, int TB, int TW>
+__device__ __forceinline__ void load_s2_ops(S2Regs<TB, TW>& r, const LinArgs& a, int64_t c, int lane) {
+    if constexpr (TPB == 1) {
+        const uint8_t* src = a.lmq + lmq_offset<1, TB>(c, 0, 0, 0, 0);
+        r.a[0][0] = *reinterpret_cast<const v4i*>(src + 16 * lane);
+        r.a[0][1] = *reinterpret_cast<const v4i*>(src + kS2SpreadBytes / 2 + 16 * lane);
+    } else {
+        const int row = lane & 15;
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+                r.a[tb][m] = *reinterpret_cast<const v4i*>(a.lmq + lmq_offset<TPB, TB>(c, tb, m, row, lane >> 4));
+    }
+}
+
+// One token: the two loaded vectors through this wave's LDS area (kS2SpreadBytes)
+// into the eight A operands (MFMA m: digit row lane & 3, lane group lane >> 4).
+template <int TPB, int TB, int TW>
+__device__ __forceinline__ void spread_s2_ops(S2Regs<TB, TW>& r, char* __restrict__ area, int lane) {
+    if constexpr (TPB == 1) {
+        *reinterpret_cast<v4i*>(area + 16 * lane) = r.a[0][0];
+        *reinterpret_cast<v4i*>(area + kS2SpreadBytes / 2 + 16 * lane) = r.a[0][1];
+        wave_lds_sync();
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+            r.a[0][m] = *reinterpret_cast<const v4i*>(area + lmq_offset<1, 1>(0, 0, m, lane & 3, lane >> 4));
+    }
 }
 
 // Low byte of each of four ints, packed.
@@ -485,16 +512,37 @@ __device__ __forceinline__ uint32_t pack_bytes(int a, int b, int c, int d) {
 // w_{j+1} = (w_j + 128) >> 8.
 __device__ __forceinline__ int next_digit_word(int w) { return (w + 128) >> 8; }
 
+// Byte B of each of four words, packed (v_perm on the device).
+template <int B>
+__device__ __forceinline__ uint32_t bytes_at(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return ((a >> (8 * B)) & 0xffu) | (((b >> (8 * B)) & 0xffu) << 8) | (((c >> (8 * B)) & 0xffu) << 16) |
+           (((d >> (8 * B)) & 0xffu) << 24);
+}
+
 // Stage tokens [t_base, t_base + TPB) of chunk c into this wave's operand area
 // (three digit rows per token) and return each token's exponent E and the
 // chunk max |a| (uniform values).
+//
+// MFMA m receives w = rint(a * 2^(E + 7 - m)) (m = 7: w = -rint(a * 2^E)), so
+// every product with its B bytes {0, 2^m} (m = 7: {0, -128}) is b times a
+// multiple of 2^-(E+7) and the eight MFMAs of a chunk share one accumulator.
+// |a * 2^E| < 2^15 gives |w| <= 2^22: adding 1.5 * 2^23 in one fma rounds to
+// the nearest integer (ties to even) and leaves y = 0x4B400000 + w in the
+// bits, from which the three signed base-256 digits of w are bytes of
+// y (digit 0), y + 128 (digit 1) and y + 128 + 128 * 256 - 0x400000 (digit 2):
+// digit j is the low byte of w_j with w_0 = w, w_{j+1} = (w_j + 128) >> 8.
 template <int AK, int TOK, int TW, int TPB>
 __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int64_t c, int t_base,
                                             char* __restrict__ ops, int lane, int (&expo)[TPB], float (&cmax)[TPB]) {
     constexpr int DT = act_dtype<AK>();
     const int m = lane >> 3, grp = (lane >> 1) & 3, dp = lane & 1;
     const int64_t k0 = stage_col0(c, lane);
-    const int mult = m < 7 ? (1 << (7 - m)) : -1;  // w = x_q * mult
+    // Offset 128 * run + i of this lane's runs is inside the row when it is
+    // below lim (one 32-bit bound instead of a 64-bit compare per element).
+    const int64_t left = a.in - k0;
+    int lim = left > 2 * kBlockCols ? 2 * kBlockCols : (left < 0 ? 0 : static_cast<int>(left));
+    asm volatile("" : "+v"(lim));  // keeps the compares 32-bit
+    const bool full_chunk = (c + 1) * kChunkCols <= a.in;  // uniform
     float sc[2][4];
     run_values<AK, kScaleDtype>(r.s[0], a.scale_dtype, sc[0]);
     run_values<AK, kScaleDtype>(r.s[1], a.scale_dtype, sc[1]);
@@ -503,33 +551,45 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
         const int t = t_base + u;
         float v[2][4];
         float mx = 0.0f;
+        if (full_chunk && t < a.tokens) {  // uniform: every value is inside
 #pragma unroll
-        for (int run = 0; run < 2; ++run) {
-            run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
+            for (int run = 0; run < 2; ++run) {
+                run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bool ok = t < a.tokens && k0 + kBlockCols * run + i < a.in;
-                v[run][i] = ok ? v[run][i] * sc[run][i] : 0.0f;
-                mx = fmaxf(mx, fabsf(v[run][i]));
+                for (int i = 0; i < 4; ++i) {
+                    v[run][i] *= sc[run][i];
+                    mx = fmaxf(mx, fabsf(v[run][i]));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int run = 0; run < 2; ++run) {
+                run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const bool ok = t < a.tokens && kBlockCols * run + i < lim;
+                    v[run][i] = ok ? v[run][i] * sc[run][i] : 0.0f;
+                    mx = fmaxf(mx, fabsf(v[run][i]));
+                }
             }
         }
         const float wmx = wave_max(mx);
         const int e = range_exponent(wmx, 14);
-        const float scale = exp2i(e);
+        const float sm = m < 7 ? exp2i(e + 7 - m) : -exp2i(e);
         uint32_t dig[3][2];
 #pragma unroll
         for (int run = 0; run < 2; ++run) {
-            int w0[4], w1[4], w2[4];
+            uint32_t y0[4], y1[4], y2[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int q = static_cast<int>(__builtin_rintf(v[run][i] * scale));
-                w0[i] = q * mult;
-                w1[i] = next_digit_word(w0[i]);
-                w2[i] = next_digit_word(w1[i]);
+                const uint32_t y = __float_as_uint(__builtin_fmaf(v[run][i], sm, 12582912.0f));
+                y0[i] = y;
+                y1[i] = y + 128u;
+                y2[i] = y + (32896u - 0x400000u);
             }
-            dig[0][run] = pack_bytes(w0[0], w0[1], w0[2], w0[3]);
-            dig[1][run] = pack_bytes(w1[0], w1[1], w1[2], w1[3]);
-            dig[2][run] = pack_bytes(w2[0], w2[1], w2[2], w2[3]);
+            dig[0][run] = bytes_at<0>(y0[0], y0[1], y0[2], y0[3]);
+            dig[1][run] = bytes_at<1>(y1[0], y1[1], y1[2], y1[3]);
+            dig[2][run] = bytes_at<2>(y2[0], y2[1], y2[2], y2[3]);
         }
         expo[u] = e;
         cmax[u] = wmx;
@@ -732,7 +792,10 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
     const RawElem rs0 = load_elem(a.s_mid, a.scale_dtype, fr < a.rank ? fr : a.rank - 1);
     const float maxsm = __uint_as_float(a.header[line_word(kMiscLine) + kMiscMaxMid]);
 
-    for (int64_t base = 0; base < nc; base += static_cast<int64_t>(nw) * KC) {
+    // One pass: KC chunks per wave. The first pass is a separate copy ahead of
+    // the loop, so its loads are not held behind waits for registers a
+    // previous iteration could still be loading (here the epilogue operands).
+    const auto pass = [&](const int64_t base) __attribute__((always_inline)) {
         const PassChunks<KC> pc = pass_chunks<KC>(base, wave, nw, nc);
         S1Regs<AK, TOK, TW> r[KC];
         // Activations first, sign words second: the staging math waits only
@@ -754,6 +817,10 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
                 float cm[TPB];
                 stage_block<AK, TOK, TW, TPB>(r[j], a, c, tb * TPB, ops, lane, expo, cm);
                 wave_lds_sync();
+                // The staging waits only for the activations: the sign words
+                // are redefined here, so no use of them moves into it.
+#pragma unroll
+                for (int tt = 0; tt < TW; ++tt) asm volatile("" : "+v"(r[j].w[tt]));
                 v4i A[8];
                 const int row = TPB == 1 ? (lane & 3) : (lane & 15);
 #pragma unroll
@@ -773,7 +840,10 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
                 wave_lds_sync();  // the next block rewrites this wave's operand area
             }
         }
-    }
+    };
+    const int64_t step = static_cast<int64_t>(nw) * KC;
+    pass(0);
+    for (int64_t base = step; base < nc; base += step) pass(base);
     __syncthreads();
 
     if (dead) return;  // uniform, after the workgroup's only barrier
@@ -831,6 +901,8 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int64_t wg_in, char*
     const MatGeo g = a.g2;
     const int64_t nc = g.nc;
     float* const red = reinterpret_cast<float*>(lds);
+    // One token: this wave's operand spread areas (KC of them) after the partial sums.
+    char* const spread = lds + nc * TW * TB * 64 * 4 + wave * KC * kS2SpreadBytes;
 
     const int outs = TW * tokens * kTileRows;
     const OutIdx f = out_index(threadIdx.x < outs ? threadIdx.x : 0, tokens);
@@ -840,7 +912,8 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int64_t wg_in, char*
     // No branch on the optional bias: without one, s_out is loaded instead and ignored.
     const RawElem bias0 = load_elem(a.bias ? a.bias : a.s_out, a.bias ? a.bias_dtype : a.scale_dtype, fr);
 
-    for (int64_t base = 0; base < nc; base += static_cast<int64_t>(nw) * KC) {
+    // One pass; the first is peeled off the loop (see stage1_wg).
+    const auto pass = [&](const int64_t base) __attribute__((always_inline)) {
         const PassChunks<KC> pc = pass_chunks<KC>(base, wave, nw, nc);
         S2Regs<TB, TW> r[KC];
 #pragma unroll
@@ -862,6 +935,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int64_t wg_in, char*
             if (!pc.live[j]) continue;  // uniform
             const int64_t c = pc.c[j];
             const int dw = chunk_words(g, c);
+            spread_s2_ops<TPB, TB, TW>(r[j], spread + j * kS2SpreadBytes, lane);
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb) {
                 if (tb * TPB >= tokens) break;
@@ -871,7 +945,10 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int64_t wg_in, char*
                     red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<4>(r[j].a[tb], S, r[j].w[tt], dw, e[tb]);
             }
         }
-    }
+    };
+    const int64_t step = static_cast<int64_t>(nw) * KC;
+    pass(0);
+    for (int64_t base = step; base < nc; base += step) pass(base);
     __syncthreads();
     if (dead) return;  // uniform, after the workgroup's only barrier
 
