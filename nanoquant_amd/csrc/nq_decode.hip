@@ -112,10 +112,9 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
     a.u_tiles = base + kHeaderWords + g.v_words;
     a.x = x;
     a.x_dtype = x_dtype;
-    // Vector loads of x and s_in: rows of length % 4 == 0, fp16 scales and
-    // aligned bases (4 elements per load).
-    const uintptr_t xa = x_dtype == NQ_DTYPE_F32 ? 16 : 8;
-    if (!(d->in_features % 4 == 0 && d->scale_dtype == NQ_DTYPE_F16 && aligned(x, xa) && aligned(d->scale_pre, 8)))
+    // Vector loads of x and s_in: rows of length % 8 == 0, fp16 scales and
+    // 16-byte aligned bases (eight 16-bit or four fp32 elements per load).
+    if (!(d->in_features % 8 == 0 && d->scale_dtype == NQ_DTYPE_F16 && aligned(x, 16) && aligned(d->scale_pre, 16)))
         vector_ok = false;
     a.tokens = static_cast<int>(tokens);
     a.s_in = d->scale_pre;

@@ -21,27 +21,30 @@
 // is four int8 values in {0, 2^m} (m = 7 gives {0, -128}), the B operand dword
 // d of MFMA m; the bits are b in {0, 1} with sgn = 1 - 2b.
 //
-// Activation operands. An activation a is held as an integer x_q = rint(a*2^E)
-// with a power of two E shared by a chunk; MFMA m receives w = x_q * 2^(7-m)
-// (w = -x_q for m = 7) as signed int8 digits w = Σ_j 256^j d_j in A rows
-// 4*t + j. Every product with B is then 2^7 * b * x_q whatever m is, so the
-// eight MFMAs of a chunk share one int32 accumulator T (per digit row), and
-// eight more MFMAs against B = 0x01010101 << m give S = 2^7 * Σ x_q. Then
-//     Σ_k sgn_k x_q,k = (S - 2T) / 2^7,   combined over digit rows as
+// Activation operands. With a power of two E shared by a chunk, MFMA m
+// receives an integer w_m ~ a * 2^(E+7-m) (w_7 ~ -a * 2^E) as signed int8
+// digits w = Σ_j 256^j d_j in A rows 4*t + j. Every product with B is then b
+// times a multiple of 2^-(E+7) whatever m is, so the eight MFMAs of a chunk
+// share one int32 accumulator T (per digit row), and eight more MFMAs against
+// B = 0x01010101 << m give S, the same sum with every b = 1. Then
+//     Σ_k sgn_k a_k ~ (S - 2T) / 2^(E+7),   combined over digit rows as
 //     Σ_j 256^j (S_j - 2 T_j)   (each S_j - 2 T_j exact in int32),
 //     chunk partial = 2^-E * 2^-7 * Σ_j 256^j (S_j - 2 T_j).
-// The only rounding before fp32 is x_q itself.
+// The only rounding before fp32 is that of the w's.
 //   Stage 1 stages x * s_in per (wave, chunk, block of up to 4 tokens): lane L
-//     takes the 8 columns of (m, g, dp) = (L >> 3, (L >> 1) & 3, L & 1), i.e.
-//     512c + 256dp + 16m + 4g + {0..3} and the same + 128, the wave max gives
-//     E (|x_q| <= 2^15, three digits), and each lane writes its 8 digit bytes
-//     per digit row into the wave's LDS area A[m][row][g][16 B]; each lane then
-//     reads its eight A operands (one 16-byte LDS read per MFMA).
+//     takes the 8 consecutive columns 512c + 128d + 16m + 8h + {0..7} of
+//     (m, d, h) = (L >> 3, (L >> 1) & 3, L & 1) (one 16-byte load of x and one
+//     of s_in for 16-bit x), the wave max gives E (|a 2^E| < 2^15, so
+//     w_m = rint(a 2^(E+7-m)) has three digits), and each lane writes its
+//     digit bytes into the wave's LDS area A[m][row][g][16 B] (g = 2h, 2h + 1,
+//     byte 4d + b); each lane then reads its eight A operands (one 16-byte LDS
+//     read per MFMA).
 //   Stage 2 does no staging: stage 1's epilogue writes lm straight into the
-//     stage-2 operand layout in global memory (four digits, |x_q| <= 2^22)
-//     with one exponent per token from a bound every stage-1 workgroup
-//     computes identically, |lm| <= max|s_mid| * Σ_chunks 512 * max_chunk|x
-//     s_in|; stage 2 loads each A operand with one 16-byte load.
+//     stage-2 operand layout in global memory as x_q = rint(lm 2^E) times
+//     2^(7-m) (four digits, |x_q| <= 2^22) with one exponent per token from a
+//     bound every stage-1 workgroup computes identically, |lm| <= max|s_mid| *
+//     Σ_chunks 512 * max_chunk|x s_in|; stage 2 loads a chunk's operands (one
+//     token: 2 KB, spread through LDS; more tokens: one 16-byte load each).
 // Chunk partials are summed in chunk order, so the result is the same for
 // every launch shape (waves or tiles per workgroup, split or fused launch).
 //
@@ -314,6 +317,19 @@ __device__ __forceinline__ RawElem load_elem(const void* __restrict__ p, int dty
     return r;
 }
 
+// A word at a uniform address, read through the scalar data cache (s_load).
+__device__ __forceinline__ uint32_t scalar_load(const uint32_t* p) {
+    typedef const __attribute__((address_space(4))) uint32_t* ConstWord;
+    return *(ConstWord)(p);
+}
+
+// Element i of a 16-bit buffer in the RawElem form (both halves the same).
+__device__ __forceinline__ RawElem load_half(const void* __restrict__ p, int64_t i) {
+    RawElem r;
+    r.lo = r.hi = static_cast<const uint16_t*>(p)[i];
+    return r;
+}
+
 __device__ __forceinline__ float elem_value(const RawElem& r, int dtype) {
     union {
         uint16_t u;
@@ -403,10 +419,11 @@ constexpr int act_dtype() {
 }
 constexpr int kScaleDtype = NQ_DTYPE_F16;  // column scale of the vector kinds
 
-// Staging lane roles: lane L stages (m, g, dp) = (L >> 3, (L >> 1) & 3, L & 1),
-// i.e. columns k0 + {0..3} and k0 + 128 + {0..3} of chunk c.
+// Staging lane roles: lane L stages (m, d, h) = (L >> 3, (L >> 1) & 3, L & 1),
+// the eight consecutive columns k0 + {0..7}, k0 = 512c + 128d + 16m + 8h: run 0
+// is lane group g = 2h, run 1 is g = 2h + 1 (byte 4d + b of each group's 16).
 __device__ __forceinline__ int64_t stage_col0(int64_t c, int lane) {
-    return kChunkCols * c + 2 * kBlockCols * (lane & 1) + 16 * (lane >> 3) + 4 * ((lane >> 1) & 3);
+    return kChunkCols * c + kBlockCols * ((lane >> 1) & 3) + 16 * (lane >> 3) + 8 * (lane & 1);
 }
 
 // Registers one stage-1 wave holds for one chunk: the activation runs of every
@@ -426,18 +443,33 @@ struct S2Regs {
     v4u w[TW];
 };
 
+// The two runs of a lane's eight columns: one 16-byte load for 16-bit kinds
+// (vector kinds need in % 8 == 0 and 16-byte aligned rows, checked by the
+// host), a load per run otherwise.
+template <int AK, int DT>
+__device__ __forceinline__ void load_runs(Run<AK> (&r)[2], const void* __restrict__ p, int rt_dtype, int64_t row,
+                                          int64_t rows_valid, int64_t ld, int64_t k, int64_t cols) {
+    if constexpr (AK != kActGeneric && DT != NQ_DTYPE_F32) {
+        const int64_t rr = row < rows_valid ? row : rows_valid - 1;
+        const int64_t kk = k < cols ? k : cols - 8;
+        const v4u q = *reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(p) + rr * ld + kk);
+        r[0].u[0] = q.x;
+        r[0].u[1] = q.y;
+        r[1].u[0] = q.z;
+        r[1].u[1] = q.w;
+    } else {
+        r[0] = load_run<AK, DT>(p, rt_dtype, row, rows_valid, ld, k, cols);
+        r[1] = load_run<AK, DT>(p, rt_dtype, row, rows_valid, ld, k + 4, cols);
+    }
+}
+
 template <int AK, int TOK, int TW>
 __device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const LinArgs& a, int64_t c, int lane) {
     constexpr int DT = act_dtype<AK>();
     const int64_t k0 = stage_col0(c, lane);
 #pragma unroll
-    for (int t = 0; t < TOK; ++t)
-#pragma unroll
-        for (int run = 0; run < 2; ++run)
-            r.x[t][run] = load_run<AK, DT>(a.x, a.x_dtype, t, a.tokens, a.in, k0 + kBlockCols * run, a.in);
-#pragma unroll
-    for (int run = 0; run < 2; ++run)
-        r.s[run] = load_run<AK, kScaleDtype>(a.s_in, a.scale_dtype, 0, 1, 0, k0 + kBlockCols * run, a.in);
+    for (int t = 0; t < TOK; ++t) load_runs<AK, DT>(r.x[t], a.x, a.x_dtype, t, a.tokens, a.in, k0, a.in);
+    load_runs<AK, kScaleDtype>(r.s, a.s_in, a.scale_dtype, 0, 1, 0, k0, a.in);
 }
 
 // Sign words of chunk c for tiles t0 .. t0 + TW - 1 (tiles past the last one
@@ -535,12 +567,12 @@ template <int AK, int TOK, int TW, int TPB>
 __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int64_t c, int t_base,
                                             char* __restrict__ ops, int lane, int (&expo)[TPB], float (&cmax)[TPB]) {
     constexpr int DT = act_dtype<AK>();
-    const int m = lane >> 3, grp = (lane >> 1) & 3, dp = lane & 1;
+    const int m = lane >> 3, d = (lane >> 1) & 3, h = lane & 1;
     const int64_t k0 = stage_col0(c, lane);
-    // Offset 128 * run + i of this lane's runs is inside the row when it is
-    // below lim (one 32-bit bound instead of a 64-bit compare per element).
+    // Column k0 + 4 * run + i is inside the row when 4 * run + i is below lim
+    // (one 32-bit bound instead of a 64-bit compare per element).
     const int64_t left = a.in - k0;
-    int lim = left > 2 * kBlockCols ? 2 * kBlockCols : (left < 0 ? 0 : static_cast<int>(left));
+    int lim = left > 8 ? 8 : (left < 0 ? 0 : static_cast<int>(left));
     asm volatile("" : "+v"(lim));  // keeps the compares 32-bit
     const bool full_chunk = (c + 1) * kChunkCols <= a.in;  // uniform
     float sc[2][4];
@@ -567,7 +599,7 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
                 run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const bool ok = t < a.tokens && kBlockCols * run + i < lim;
+                    const bool ok = t < a.tokens && 4 * run + i < lim;
                     v[run][i] = ok ? v[run][i] * sc[run][i] : 0.0f;
                     mx = fmaxf(mx, fabsf(v[run][i]));
                 }
@@ -596,8 +628,10 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
 #pragma unroll
         for (int digit = 0; digit < 3; ++digit) {
             const int row = 4 * u + digit;
-            *reinterpret_cast<v2u*>(ops + ((m * Ops<TPB>::kRows + row) * 4 + grp) * 16 + 8 * dp) =
-                v2u{dig[digit][0], dig[digit][1]};
+#pragma unroll
+            for (int run = 0; run < 2; ++run)
+                *reinterpret_cast<uint32_t*>(ops + ((m * Ops<TPB>::kRows + row) * 4 + 2 * h + run) * 16 + 4 * d) =
+                    dig[digit][run];
         }
     }
 }
@@ -789,8 +823,11 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
     const int outs = TW * tokens * kTileRows;
     const OutIdx f = out_index(threadIdx.x < outs ? threadIdx.x : 0, tokens);
     const int64_t fr = (t0 + f.tt) * kTileRows + f.n;
-    const RawElem rs0 = load_elem(a.s_mid, a.scale_dtype, fr < a.rank ? fr : a.rank - 1);
-    const float maxsm = __uint_as_float(a.header[line_word(kMiscLine) + kMiscMaxMid]);
+    // Vector kinds have fp16 scales: one 16-bit load (the generic kind loads both halves).
+    const RawElem rs0 = AK == kActGeneric ? load_elem(a.s_mid, a.scale_dtype, fr < a.rank ? fr : a.rank - 1)
+                                          : load_half(a.s_mid, fr < a.rank ? fr : a.rank - 1);
+    // A uniform address: a scalar load.
+    const float maxsm = __uint_as_float(scalar_load(a.header + line_word(kMiscLine) + kMiscMaxMid));
 
     // One pass: KC chunks per wave. The first pass is a separate copy ahead of
     // the loop, so its loads are not held behind waits for registers a
