@@ -92,6 +92,14 @@ int64_t scratch_bytes(const TilesGeometry& g, int64_t tokens) {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// The kernels index with 32-bit offsets: every word, operand byte and element
+// offset of a launch stays below 2^31 (sign words up to 8 GiB per factor).
+bool offsets_fit(const TilesGeometry& g, int64_t in, int64_t out, int64_t tokens, int64_t salient) {
+    constexpr int64_t kMax = int64_t(1) << 31;
+    return g.v_words < kMax && g.u_words < kMax && scratch_bytes(g, tokens) < kMax && tokens * in < kMax &&
+           tokens * out < kMax && out * (salient > 0 ? salient : 1) < kMax;
+}
+
 // Fill one linear of a batch; NQ_OK or an error status. `vector_ok` is cleared
 // when this member's x or s_in cannot take the vector-load kinds.
 int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y, int y_dtype,
@@ -99,6 +107,7 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
     const TilesGeometry g = geometry(d->in_features, d->out_features, d->rank);
     if (!d->tiles) return NQ_ERR_ARGUMENT;
     if (d->tiles_bytes < tiles_bytes_of(g)) return NQ_ERR_ARGUMENT;
+    if (!offsets_fit(g, d->in_features, d->out_features, tokens, d->salient_count)) return NQ_ERR_SHAPE;
     if (!aligned(d->tiles, 16) || !aligned(scratch, 16)) return NQ_ERR_ALIGNMENT;
     a = LinArgs{};
     a.in = d->in_features;
@@ -165,16 +174,27 @@ size_t lds_bytes(int stage, int tpb, int tb, int tw, int nw, int kc, int64_t nc)
     return static_cast<size_t>(nw) * (8 * 4 * tpb * 4 * 16) + red + static_cast<size_t>(nc) * tpb * tb * 4;
 }
 
-// Tiles per workgroup: four when one tile per workgroup would need more waves
-// than the GPU holds at once (about three per SIMD at these register counts),
-// so the stage runs in a single round; one otherwise, for blocks of several
-// token groups (registers) and for the fused launch (its stage-2 wait is per
-// workgroup).
-constexpr int64_t kResidentWaves = 3 * 4 * 256;
+// Tiles per workgroup (measured on MI355X over the Qwen3-8B decode calls).
+// A wave's fixed work (arguments, addresses, the chunk's ones-MFMAs and, in
+// stage 1, the staging) is shared by its TW tiles, against fewer waves to
+// hide latency:
+//   stage 1: two tiles when one chunk per wave and one tile per workgroup
+//     would launch more than 1536 waves (the staging is then the larger
+//     cost), else one;
+//   stage 2: the fewest tiles that keep the stage within three waves per SIMD
+//     (3072 waves), at most four.
+// Blocks of several token groups (registers) and the fused launch (its
+// stage-2 wait is per workgroup) take one.
+constexpr int64_t kStage1Waves = 1536;
+constexpr int64_t kStage2Waves = 3 * 4 * 256;
 
-int pick_tiles(int64_t tiles, int nw, int tb, bool fused) {
+int pick_tiles(int stage, int64_t tiles, int nw, int kc, int tb, bool fused) {
     if (fused || tb > 1) return 1;
-    return tiles * nw > kResidentWaves ? 4 : 1;
+    const int64_t waves = tiles * nw;
+    if (stage == 1) return kc == 1 && waves > kStage1Waves ? 2 : 1;
+    for (int tw = 1; tw < 4; ++tw)
+        if (waves <= kStage2Waves * tw) return tw;
+    return 4;
 }
 
 int enqueue_stage1(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
@@ -207,8 +227,8 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
     } else {
         pick_waves(nc1, s1.tpb, s1.tb, s1.nw, s1.kc);
         pick_waves(nc2, s2.tpb, s2.tb, s2.nw, s2.kc);
-        s1.tw = pick_tiles(tiles1, s1.nw, s1.tb, false);
-        s2.tw = pick_tiles(tiles2, s2.nw, s2.tb, false);
+        s1.tw = pick_tiles(1, tiles1, s1.nw, s1.kc, s1.tb, false);
+        s2.tw = pick_tiles(2, tiles2, s2.nw, s2.kc, s2.tb, false);
     }
     batch.tw1 = s1.tw;
     batch.tw2 = fused ? 1 : s2.tw;

@@ -154,6 +154,13 @@ __host__ __device__ inline int chunk_words(const MatGeo& g, int64_t c) {
     return static_cast<int>(r < kChunkBlocks ? r : kChunkBlocks);
 }
 
+// Kernel-side indices are 32-bit: the host rejects a launch whose word,
+// operand or element offsets could reach 2^31 (check_offsets in nq_decode.hip).
+__device__ __forceinline__ int chunk_words32(int nb, int c) {
+    const int r = nb - kChunkBlocks * c;
+    return r < kChunkBlocks ? r : kChunkBlocks;
+}
+
 // ---------------------------------------------------------------------------
 // Decode kernels.
 // ---------------------------------------------------------------------------
@@ -262,7 +269,7 @@ struct Ops {
 // stage-2 operand buffer; byte j of the 16 is column 512c + 128*(j/4) + 16m +
 // 4g + j%4.
 template <int TPB, int TB>
-__host__ __device__ inline int64_t lmq_offset(int64_t c, int tb, int m, int row, int g) {
+__host__ __device__ inline int lmq_offset(int c, int tb, int m, int row, int g) {
     return ((((c * TB + tb) * 8 + m) * Ops<TPB>::kRows + row) * 4 + g) * 16;
 }
 
@@ -359,18 +366,18 @@ struct Run {
 // aligned base, checked by the host; generic: each element clamped). Values
 // past the valid range are zeroed when staged.
 template <int AK, int DT>
-__device__ __forceinline__ Run<AK> load_run(const void* __restrict__ p, int rt_dtype, int64_t row,
-                                            int64_t rows_valid, int64_t ld, int64_t k, int64_t cols) {
+__device__ __forceinline__ Run<AK> load_run(const void* __restrict__ p, int rt_dtype, int row, int rows_valid,
+                                            int ld, int k, int cols) {
     Run<AK> r;
-    const int64_t rr = row < rows_valid ? row : rows_valid - 1;
+    const int rr = row < rows_valid ? row : rows_valid - 1;
     if constexpr (AK == kActGeneric) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int64_t kk = k + i < cols ? k + i : cols - 1;
+            const int kk = k + i < cols ? k + i : cols - 1;
             r.e[i] = load_elem(p, rt_dtype, rr * ld + kk);
         }
     } else {
-        const int64_t kk = k < cols ? k : cols - 4;
+        const int kk = k < cols ? k : cols - 4;
         if constexpr (DT == NQ_DTYPE_F32) {
             const v4u q = *reinterpret_cast<const v4u*>(static_cast<const float*>(p) + rr * ld + kk);
 #pragma unroll
@@ -422,7 +429,7 @@ constexpr int kScaleDtype = NQ_DTYPE_F16;  // column scale of the vector kinds
 // Staging lane roles: lane L stages (m, d, h) = (L >> 3, (L >> 1) & 3, L & 1),
 // the eight consecutive columns k0 + {0..7}, k0 = 512c + 128d + 16m + 8h: run 0
 // is lane group g = 2h, run 1 is g = 2h + 1 (byte 4d + b of each group's 16).
-__device__ __forceinline__ int64_t stage_col0(int64_t c, int lane) {
+__device__ __forceinline__ int stage_col0(int c, int lane) {
     return kChunkCols * c + kBlockCols * ((lane >> 1) & 3) + 16 * (lane >> 3) + 8 * (lane & 1);
 }
 
@@ -447,11 +454,11 @@ struct S2Regs {
 // (vector kinds need in % 8 == 0 and 16-byte aligned rows, checked by the
 // host), a load per run otherwise.
 template <int AK, int DT>
-__device__ __forceinline__ void load_runs(Run<AK> (&r)[2], const void* __restrict__ p, int rt_dtype, int64_t row,
-                                          int64_t rows_valid, int64_t ld, int64_t k, int64_t cols) {
+__device__ __forceinline__ void load_runs(Run<AK> (&r)[2], const void* __restrict__ p, int rt_dtype, int row,
+                                          int rows_valid, int ld, int k, int cols) {
     if constexpr (AK != kActGeneric && DT != NQ_DTYPE_F32) {
-        const int64_t rr = row < rows_valid ? row : rows_valid - 1;
-        const int64_t kk = k < cols ? k : cols - 8;
+        const int rr = row < rows_valid ? row : rows_valid - 1;
+        const int kk = k < cols ? k : cols - 8;
         const v4u q = *reinterpret_cast<const v4u*>(static_cast<const uint16_t*>(p) + rr * ld + kk);
         r[0].u[0] = q.x;
         r[0].u[1] = q.y;
@@ -464,12 +471,13 @@ __device__ __forceinline__ void load_runs(Run<AK> (&r)[2], const void* __restric
 }
 
 template <int AK, int TOK, int TW>
-__device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const LinArgs& a, int64_t c, int lane) {
+__device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const LinArgs& a, int c, int lane) {
     constexpr int DT = act_dtype<AK>();
-    const int64_t k0 = stage_col0(c, lane);
+    const int k0 = stage_col0(c, lane);
+    const int in = static_cast<int>(a.in);
 #pragma unroll
-    for (int t = 0; t < TOK; ++t) load_runs<AK, DT>(r.x[t], a.x, a.x_dtype, t, a.tokens, a.in, k0, a.in);
-    load_runs<AK, kScaleDtype>(r.s, a.s_in, a.scale_dtype, 0, 1, 0, k0, a.in);
+    for (int t = 0; t < TOK; ++t) load_runs<AK, DT>(r.x[t], a.x, a.x_dtype, t, a.tokens, in, k0, in);
+    load_runs<AK, kScaleDtype>(r.s, a.s_in, a.scale_dtype, 0, 1, 0, k0, in);
 }
 
 // Sign words of chunk c for tiles t0 .. t0 + TW - 1 (tiles past the last one
@@ -478,13 +486,13 @@ __device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const LinAr
 // belong to the next lane (or, for the last lane of the matrix, to the
 // buffer's tail padding) and the MFMA step masks them out.
 template <int TW>
-__device__ __forceinline__ void load_words(v4u (&w)[TW], const uint32_t* tiles, const MatGeo& g, int64_t t0,
-                                           int64_t c, int lane) {
-    const int dw = chunk_words(g, c);
+__device__ __forceinline__ void load_words(v4u (&w)[TW], const uint32_t* tiles, int nt, int nb, int t0, int c,
+                                           int lane) {
+    const int dw = chunk_words32(nb, c);
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
-        const int64_t tile = t0 + tt < g.nt ? t0 + tt : g.nt - 1;
-        const uint32_t* base = tiles + tile * g.nb * 64 + c * 256 + lane * dw;
+        const int tile = t0 + tt < nt ? t0 + tt : nt - 1;
+        const uint32_t* base = tiles + (tile * nb * 64 + c * 256 + lane * dw);
         w[tt] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(base));
     }
 }
@@ -504,7 +512,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 constexpr int kS2SpreadBytes = 8 * 4 * 4 * 16;
 
 template <int TPB, int TB, int TW>
-__device__ __forceinline__ void load_s2_ops(S2Regs<TB, TW>& r, const LinArgs& a, int64_t c, int lane) {
+__device__ __forceinline__ void load_s2_ops(S2Regs<TB, TW>& r, const LinArgs& a, int c, int lane) {
     if constexpr (TPB == 1) {
         const uint8_t* src = a.lmq + lmq_offset<1, TB>(c, 0, 0, 0, 0);
         r.a[0][0] = *reinterpret_cast<const v4i*>(src + 16 * lane);
@@ -564,17 +572,16 @@ __device__ __forceinline__ uint32_t bytes_at(uint32_t a, uint32_t b, uint32_t c,
 // y (digit 0), y + 128 (digit 1) and y + 128 + 128 * 256 - 0x400000 (digit 2):
 // digit j is the low byte of w_j with w_0 = w, w_{j+1} = (w_j + 128) >> 8.
 template <int AK, int TOK, int TW, int TPB>
-__device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int64_t c, int t_base,
+__device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int c, int t_base,
                                             char* __restrict__ ops, int lane, int (&expo)[TPB], float (&cmax)[TPB]) {
     constexpr int DT = act_dtype<AK>();
     const int m = lane >> 3, d = (lane >> 1) & 3, h = lane & 1;
-    const int64_t k0 = stage_col0(c, lane);
-    // Column k0 + 4 * run + i is inside the row when 4 * run + i is below lim
-    // (one 32-bit bound instead of a 64-bit compare per element).
-    const int64_t left = a.in - k0;
-    int lim = left > 8 ? 8 : (left < 0 ? 0 : static_cast<int>(left));
-    asm volatile("" : "+v"(lim));  // keeps the compares 32-bit
-    const bool full_chunk = (c + 1) * kChunkCols <= a.in;  // uniform
+    const int k0 = stage_col0(c, lane);
+    const int in = static_cast<int>(a.in);
+    // Column k0 + 4 * run + i is inside the row when 4 * run + i is below lim.
+    const int left = in - k0;
+    const int lim = left > 8 ? 8 : (left < 0 ? 0 : left);
+    const bool full_chunk = (c + 1) * kChunkCols <= in;  // uniform
     float sc[2][4];
     run_values<AK, kScaleDtype>(r.s[0], a.scale_dtype, sc[0]);
     run_values<AK, kScaleDtype>(r.s[1], a.scale_dtype, sc[1]);
@@ -742,16 +749,16 @@ __device__ __forceinline__ void wait_ready(const LinArgs& a, int64_t t0, int tw,
 // loads chunk nc - 1 and skips its arithmetic.
 template <int KC>
 struct PassChunks {
-    int64_t c[KC];
+    int c[KC];
     bool live[KC];
 };
 
 template <int KC>
-__device__ __forceinline__ PassChunks<KC> pass_chunks(int64_t base, int wave, int nw, int64_t nc) {
+__device__ __forceinline__ PassChunks<KC> pass_chunks(int base, int wave, int nw, int nc) {
     PassChunks<KC> p;
 #pragma unroll
     for (int j = 0; j < KC; ++j) {
-        const int64_t c = base + wave + static_cast<int64_t>(j) * nw;
+        const int c = base + wave + j * nw;
         p.live[j] = c < nc;
         p.c[j] = c < nc ? c : nc - 1;
     }
@@ -763,28 +770,30 @@ struct OutIdx {
     int tt, t, n;
 };
 
+// One token per block (TPB = 1) means one token per launch: no division.
+template <int TPB>
 __device__ __forceinline__ OutIdx out_index(int idx, int tokens) {
     OutIdx o;
-    o.tt = idx / (tokens * kTileRows);
-    o.t = (idx / kTileRows) % tokens;
+    o.tt = TPB == 1 ? idx >> 4 : idx / (tokens * kTileRows);
+    o.t = TPB == 1 ? 0 : (idx / kTileRows) % tokens;
     o.n = idx & 15;
     return o;
 }
 
 // Partial-sum slot of (chunk c, tile tt, token t, row n) in the LDS array red.
 template <int TPB, int TB, int TW>
-__device__ __forceinline__ int red_index(int64_t c, int tt, int t, int n) {
+__device__ __forceinline__ int red_index(int c, int tt, int t, int n) {
     const int tb = TPB == 1 ? 0 : t / TPB;
     const int rl = TPB == 1 ? n : 16 * (t % TPB) + n;
-    return static_cast<int>(((c * TW + tt) * TB + tb) * 64 + rl);
+    return ((c * TW + tt) * TB + tb) * 64 + rl;
 }
 
 // Stage-1 epilogue store of one rank value: x_q = rint(v * 2^e) as four digits
 // of w = x_q * mult into the stage-2 operand buffer (agent scope when fused).
 template <int TPB, int TB, bool FUSED>
-__device__ __forceinline__ void store_lmq(uint8_t* lmq, int64_t r, int t, float v, int e) {
-    const int64_t c = r >> 9;
-    const int col = static_cast<int>(r & 511);
+__device__ __forceinline__ void store_lmq(uint8_t* lmq, int r, int t, float v, int e) {
+    const int c = r >> 9;
+    const int col = r & 511;
     const int d = col >> 7, m = (col >> 4) & 7, g = (col >> 2) & 3, b = col & 3;
     const int tb = TPB == 1 ? 0 : t / TPB, u = TPB == 1 ? 0 : t % TPB;
     const int q = static_cast<int>(__builtin_rintf(v * exp2i(e)));
@@ -802,7 +811,7 @@ __device__ __forceinline__ void store_lmq(uint8_t* lmq, int64_t r, int t, float 
 // One stage-1 workgroup: tiles [t0, t0 + TW) of linear `a`. TPB tokens per
 // block and TB blocks cover the launch's tokens; KC chunks per wave per pass.
 template <int AK, int TPB, int TB, int TW, int KC, bool FUSED>
-__device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char* __restrict__ lds) {
+__device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __restrict__ lds) {
     constexpr int TOK = TPB * TB;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -810,29 +819,27 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
     const int tokens = a.tokens;
     // Workgroups past this member's count compute the last workgroup's tiles
     // and store nothing.
-    const bool dead = wg_in >= a.nwg1;
-    const int64_t wg = dead ? a.nwg1 - 1 : wg_in;
-    const int64_t t0 = wg * TW;
-    const MatGeo g = a.g1;
-    const int64_t nc = g.nc;
+    const int nwg = static_cast<int>(a.nwg1);
+    const bool dead = wg_in >= nwg;
+    const int wg = dead ? nwg - 1 : wg_in;
+    const int t0 = wg * TW;
+    const int nt = static_cast<int>(a.g1.nt), nb = static_cast<int>(a.g1.nb), nc = static_cast<int>(a.g1.nc);
+    const int rank = static_cast<int>(a.rank);
     char* const ops = lds + wave * Ops<TPB>::kBytes;
     float* const red = reinterpret_cast<float*>(lds + nw * Ops<TPB>::kBytes);
     float* const cmx = red + nc * TW * TB * 64;  // [nc][TOK] chunk max |x s_in|
 
-    // Epilogue operands issued first so their latency hides under the main loads.
     const int outs = TW * tokens * kTileRows;
-    const OutIdx f = out_index(threadIdx.x < outs ? threadIdx.x : 0, tokens);
-    const int64_t fr = (t0 + f.tt) * kTileRows + f.n;
-    // Vector kinds have fp16 scales: one 16-bit load (the generic kind loads both halves).
-    const RawElem rs0 = AK == kActGeneric ? load_elem(a.s_mid, a.scale_dtype, fr < a.rank ? fr : a.rank - 1)
-                                          : load_half(a.s_mid, fr < a.rank ? fr : a.rank - 1);
-    // A uniform address: a scalar load.
-    const float maxsm = __uint_as_float(scalar_load(a.header + line_word(kMiscLine) + kMiscMaxMid));
+    const OutIdx f = out_index<TPB>(threadIdx.x < outs ? threadIdx.x : 0, tokens);
+    const int fr = (t0 + f.tt) * kTileRows + f.n;
+    RawElem rs0;
+    float maxsm;
 
     // One pass: KC chunks per wave. The first pass is a separate copy ahead of
-    // the loop, so its loads are not held behind waits for registers a
-    // previous iteration could still be loading (here the epilogue operands).
-    const auto pass = [&](const int64_t base) __attribute__((always_inline)) {
+    // the loop (so its loads are not held behind waits for registers a
+    // previous iteration could still be loading) and issues the epilogue
+    // operands right after its own loads.
+    const auto pass = [&](const int base, const bool first) __attribute__((always_inline)) {
         const PassChunks<KC> pc = pass_chunks<KC>(base, wave, nw, nc);
         S1Regs<AK, TOK, TW> r[KC];
         // Activations first, sign words second: the staging math waits only
@@ -840,13 +847,20 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
 #pragma unroll
         for (int j = 0; j < KC; ++j) load_s1_acts(r[j], a, pc.c[j], lane);
 #pragma unroll
-        for (int j = 0; j < KC; ++j) load_words(r[j].w, a.v_tiles, g, t0, pc.c[j], lane);
+        for (int j = 0; j < KC; ++j) load_words(r[j].w, a.v_tiles, nt, nb, t0, pc.c[j], lane);
+        if (first) {
+            // Vector kinds have fp16 scales: one 16-bit load (the generic kind
+            // loads both halves); the bound sits at a uniform address.
+            const int frc = fr < rank ? fr : rank - 1;
+            rs0 = AK == kActGeneric ? load_elem(a.s_mid, a.scale_dtype, frc) : load_half(a.s_mid, frc);
+            maxsm = __uint_as_float(scalar_load(a.header + line_word(kMiscLine) + kMiscMaxMid));
+        }
         __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
 #pragma unroll
         for (int j = 0; j < KC; ++j) {
             if (!pc.live[j]) continue;  // uniform
-            const int64_t c = pc.c[j];
-            const int dw = chunk_words(g, c);
+            const int c = pc.c[j];
+            const int dw = chunk_words32(nb, c);
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb) {
                 if (tb * TPB >= tokens) break;
@@ -878,9 +892,9 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
             }
         }
     };
-    const int64_t step = static_cast<int64_t>(nw) * KC;
-    pass(0);
-    for (int64_t base = step; base < nc; base += step) pass(base);
+    const int step = nw * KC;
+    pass(0, true);
+    for (int base = step; base < nc; base += step) pass(base, false);
     __syncthreads();
 
     if (dead) return;  // uniform, after the workgroup's only barrier
@@ -888,18 +902,18 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
     // Epilogue: lm = s_mid * Σ_chunks partial, written as stage-2 operands with
     // the per-token exponent of the bound max|s_mid| * Σ_c 512 * max_c.
     for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
-        const OutIdx o = out_index(idx, tokens);
-        const int64_t row = (t0 + o.tt) * kTileRows + o.n;
-        if (t0 + o.tt >= g.nt) continue;
+        const OutIdx o = out_index<TPB>(idx, tokens);
+        const int row = (t0 + o.tt) * kTileRows + o.n;
+        if (t0 + o.tt >= nt) continue;
         float sum = 0.0f, bound = 0.0f;
-        for (int64_t c = 0; c < nc; ++c) {
+        for (int c = 0; c < nc; ++c) {
             sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
             bound += cmx[c * TOK + o.t];
         }
         const int e = range_exponent(bound * (512.0f * maxsm), 21);
         float v = 0.0f;
-        if (row < a.rank) v = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_mid, a.scale_dtype, row),
-                                               a.scale_dtype);
+        if (row < rank) v = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_mid, a.scale_dtype, row),
+                                             a.scale_dtype);
         store_lmq<TPB, TB, FUSED>(a.lmq, row, o.t, v, e);
         if (wg == 0 && o.tt == 0 && o.n == 0) {
             if (FUSED) __hip_atomic_store(a.lme + o.t, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -908,13 +922,11 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
     }
     // The last workgroup zeroes the operand columns past its last tile up to
     // the end of the last chunk (every stage-2 ones-MFMA reads them).
-    if (t0 + TW >= g.nt) {
-        const MatGeo g2 = a.g2;
-        const int64_t from = g.nt * kTileRows, to = g2.nc * kChunkCols;
-        const int64_t n = (to - from) * tokens;
-        for (int64_t i = threadIdx.x; i < n; i += blockDim.x) store_lmq<TPB, TB, FUSED>(a.lmq, from + i / tokens,
-                                                                                        static_cast<int>(i % tokens),
-                                                                                        0.0f, 0);
+    if (t0 + TW >= nt) {
+        const int from = nt * kTileRows, to = static_cast<int>(a.g2.nc) * kChunkCols;
+        const int n = (to - from) * tokens;
+        for (int i = threadIdx.x; i < n; i += blockDim.x)
+            store_lmq<TPB, TB, FUSED>(a.lmq, from + i / tokens, i % tokens, 0.0f, 0);
     }
     if (FUSED) {
         // The operands went out at agent scope; the wait makes them complete
@@ -927,37 +939,37 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int64_t wg_in, char*
 
 // One stage-2 workgroup: output tiles [t0, t0 + TW) of linear `a`.
 template <int TPB, int TB, int TW, int KC, bool FUSED>
-__device__ __forceinline__ void stage2_wg(const LinArgs& a, int64_t wg_in, char* __restrict__ lds) {
+__device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __restrict__ lds) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nw = a.nw2;
     const int tokens = a.tokens;
-    const bool dead = wg_in >= a.nwg2;  // computes the last workgroup's tiles, stores nothing
-    const int64_t wg = dead ? a.nwg2 - 1 : wg_in;
-    const int64_t t0 = wg * TW;
-    const MatGeo g = a.g2;
-    const int64_t nc = g.nc;
+    const int nwg = static_cast<int>(a.nwg2);
+    const bool dead = wg_in >= nwg;  // computes the last workgroup's tiles, stores nothing
+    const int wg = dead ? nwg - 1 : wg_in;
+    const int t0 = wg * TW;
+    const int nt = static_cast<int>(a.g2.nt), nb = static_cast<int>(a.g2.nb), nc = static_cast<int>(a.g2.nc);
+    const int out = static_cast<int>(a.out), in = static_cast<int>(a.in);
     float* const red = reinterpret_cast<float*>(lds);
     // One token: this wave's operand spread areas (KC of them) after the partial sums.
     char* const spread = lds + nc * TW * TB * 64 * 4 + wave * KC * kS2SpreadBytes;
 
     const int outs = TW * tokens * kTileRows;
-    const OutIdx f = out_index(threadIdx.x < outs ? threadIdx.x : 0, tokens);
-    const int64_t fr0 = (t0 + f.tt) * kTileRows + f.n;
-    const int64_t fr = fr0 < a.out ? fr0 : a.out - 1;
-    const RawElem rs0 = load_elem(a.s_out, a.scale_dtype, fr);
-    // No branch on the optional bias: without one, s_out is loaded instead and ignored.
-    const RawElem bias0 = load_elem(a.bias ? a.bias : a.s_out, a.bias ? a.bias_dtype : a.scale_dtype, fr);
+    const OutIdx f = out_index<TPB>(threadIdx.x < outs ? threadIdx.x : 0, tokens);
+    const int fr0 = (t0 + f.tt) * kTileRows + f.n;
+    const int fr = fr0 < out ? fr0 : out - 1;
+    RawElem rs0, bias0;
 
-    // One pass; the first is peeled off the loop (see stage1_wg).
-    const auto pass = [&](const int64_t base) __attribute__((always_inline)) {
+    // One pass; the first is peeled off the loop and issues the epilogue
+    // operands after its own loads (see stage1_wg).
+    const auto pass = [&](const int base, const bool first) __attribute__((always_inline)) {
         const PassChunks<KC> pc = pass_chunks<KC>(base, wave, nw, nc);
         S2Regs<TB, TW> r[KC];
 #pragma unroll
-        for (int j = 0; j < KC; ++j) load_words(r[j].w, a.u_tiles, g, t0, pc.c[j], lane);
+        for (int j = 0; j < KC; ++j) load_words(r[j].w, a.u_tiles, nt, nb, t0, pc.c[j], lane);
         // The U words do not depend on stage 1; the fused launch waits for its
         // signal only now.
-        if (FUSED && base == 0) wait_ready(a, t0, TW, wg, dead);
+        if (FUSED && first) wait_ready(a, t0, TW, wg, dead);
 #pragma unroll
         for (int j = 0; j < KC; ++j) load_s2_ops<TPB, TB, TW>(r[j], a, pc.c[j], lane);
         int e[TB];
@@ -966,12 +978,17 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int64_t wg_in, char*
             const int t = tb * TPB + (TPB == 1 ? 0 : (lane >> 4));
             e[tb] = a.lme[t < tokens ? t : tokens - 1];
         }
+        if (first) {
+            rs0 = load_elem(a.s_out, a.scale_dtype, fr);
+            // No branch on the optional bias: without one, s_out is loaded instead and ignored.
+            bias0 = load_elem(a.bias ? a.bias : a.s_out, a.bias ? a.bias_dtype : a.scale_dtype, fr);
+        }
         __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
 #pragma unroll
         for (int j = 0; j < KC; ++j) {
             if (!pc.live[j]) continue;  // uniform
-            const int64_t c = pc.c[j];
-            const int dw = chunk_words(g, c);
+            const int c = pc.c[j];
+            const int dw = chunk_words32(nb, c);
             spread_s2_ops<TPB, TB, TW>(r[j], spread + j * kS2SpreadBytes, lane);
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb) {
@@ -983,26 +1000,27 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int64_t wg_in, char*
             }
         }
     };
-    const int64_t step = static_cast<int64_t>(nw) * KC;
-    pass(0);
-    for (int64_t base = step; base < nc; base += step) pass(base);
+    const int step = nw * KC;
+    pass(0, true);
+    for (int base = step; base < nc; base += step) pass(base, false);
     __syncthreads();
     if (dead) return;  // uniform, after the workgroup's only barrier
 
     for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
-        const OutIdx o = out_index(idx, tokens);
-        const int64_t row = (t0 + o.tt) * kTileRows + o.n;
-        if (t0 + o.tt >= g.nt || row >= a.out) continue;
+        const OutIdx o = out_index<TPB>(idx, tokens);
+        const int row = (t0 + o.tt) * kTileRows + o.n;
+        if (t0 + o.tt >= nt || row >= out) continue;
         float sum = 0.0f;
-        for (int64_t c = 0; c < nc; ++c) sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
+        for (int c = 0; c < nc; ++c) sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
         float val = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_out, a.scale_dtype, row), a.scale_dtype);
-        for (int64_t k = 0; k < a.salient_count; ++k) {
-            float wv = nq::load_f32(a.salient_values, a.salient_dtype, row * a.salient_count + k);
+        const int ks = static_cast<int>(a.salient_count);
+        for (int k = 0; k < ks; ++k) {
+            float wv = nq::load_f32(a.salient_values, a.salient_dtype, row * ks + k);
             if (a.salient_scales) wv *= nq::load_f32(a.salient_scales, a.scale_dtype, k);
-            val += wv * nq::load_f32(a.x, a.x_dtype, o.t * a.in + a.salient_indices[k]);
+            val += wv * nq::load_f32(a.x, a.x_dtype, o.t * in + a.salient_indices[k]);
         }
         if (a.bias) val += elem_value(idx == threadIdx.x ? bias0 : load_elem(a.bias, a.bias_dtype, row), a.bias_dtype);
-        nq::store_f32_as(a.y, a.y_dtype, o.t * a.out + row, val);
+        nq::store_f32_as(a.y, a.y_dtype, o.t * out + row, val);
     }
 }
 

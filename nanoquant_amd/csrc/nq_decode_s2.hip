@@ -17,6 +17,7 @@ template <int TPB>
 int by_tiles(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     if (s.tw == 4) return s.kc == 2 ? go<TPB, 1, 4, 2>(batch, s, stream) : go<TPB, 1, 4, 1>(batch, s, stream);
     if (s.tw == 2) return s.kc == 2 ? go<TPB, 1, 2, 2>(batch, s, stream) : go<TPB, 1, 2, 1>(batch, s, stream);
+    if (s.tw == 3) return s.kc == 2 ? go<TPB, 1, 3, 2>(batch, s, stream) : go<TPB, 1, 3, 1>(batch, s, stream);
     return s.kc == 2 ? go<TPB, 1, 1, 2>(batch, s, stream) : go<TPB, 1, 1, 1>(batch, s, stream);
 }
 
