@@ -492,7 +492,7 @@ __device__ __forceinline__ void load_words(v4u (&w)[TW], const uint32_t* tiles, 
 #pragma unroll
     for (int tt = 0; tt < TW; ++tt) {
         const int tile = t0 + tt < nt ? t0 + tt : nt - 1;
-        const uint32_t* base = tiles + (tile * nb * 64 + c * 256 + lane * dw);
+        const uint32_t* base = tiles + (tile * nb * 64 + c * 256 + static_cast<int>(__umul24(lane, dw)));
         w[tt] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(base));
     }
 }
@@ -660,16 +660,19 @@ __device__ __forceinline__ v4i ones_mfma(const v4i (&A)[8]) {
 // count as zero. NDIG digit rows per token; lane 16*t' + n returns token t' of
 // the block, row n; e is that token's exponent.
 template <int NDIG>
-__device__ __forceinline__ float tile_partial(const v4i (&A)[8], const v4i& S, const v4u& w, int dw, int e) {
+__device__ __forceinline__ float tile_partial(const v4i (&A)[8], const v4i& S, v4u w, int dw, int e) {
+    // A partial last chunk: words past dw belong to other lanes (uniform masks).
+    w[1] &= dw > 1 ? ~0u : 0u;
+    w[2] &= dw > 2 ? ~0u : 0u;
+    w[3] &= dw > 3 ? ~0u : 0u;
     v4i t0 = v4i{0, 0, 0, 0}, t1 = v4i{0, 0, 0, 0};
-    const uint32_t keep1 = dw > 1 ? ~0u : 0u, keep2 = dw > 2 ? ~0u : 0u, keep3 = dw > 3 ? ~0u : 0u;
 #pragma unroll
     for (int m = 0; m < 8; m += 2) {
         const uint32_t k0 = 0x01010101u << m, k1 = 0x01010101u << (m + 1);
-        const v4i b0 = v4i{static_cast<int>(w[0] & k0), static_cast<int>(w[1] & (k0 & keep1)),
-                           static_cast<int>(w[2] & (k0 & keep2)), static_cast<int>(w[3] & (k0 & keep3))};
-        const v4i b1 = v4i{static_cast<int>(w[0] & k1), static_cast<int>(w[1] & (k1 & keep1)),
-                           static_cast<int>(w[2] & (k1 & keep2)), static_cast<int>(w[3] & (k1 & keep3))};
+        const v4i b0 = v4i{static_cast<int>(w[0] & k0), static_cast<int>(w[1] & k0), static_cast<int>(w[2] & k0),
+                           static_cast<int>(w[3] & k0)};
+        const v4i b1 = v4i{static_cast<int>(w[0] & k1), static_cast<int>(w[1] & k1), static_cast<int>(w[2] & k1),
+                           static_cast<int>(w[3] & k1)};
         t0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m], b0, t0, 0, 0, 0);
         t1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[m + 1], b1, t1, 0, 0, 0);
     }

@@ -18,6 +18,7 @@ namespace {
 using nq::f32_to_bf16_bits;
 
 constexpr int kWave = 64;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSeqBlock = 64;           // cache rows per attention block
 constexpr int kRowThreads = 256;        // per-row kernels
 constexpr int kProjWaves = 4;           // output projection: waves per workgroup
@@ -26,16 +27,33 @@ constexpr int kProjLoads = 32;          // 16-byte weight loads per lane in flig
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Wave reductions with DPP row operations and four lane reads (no LDS round
+// trips); every lane gets the result, combined in a fixed order.
+// Lane value CTRL-permuted within rows; `identity` where a source lane is off.
+template <int CTRL>
+__device__ __forceinline__ float dpp_src(float x, float identity) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(identity), __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float row_lane(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    v += dpp_src<0xB1>(v, 0.0f);   // quad_perm [1,0,3,2]
+    v += dpp_src<0x4E>(v, 0.0f);   // quad_perm [2,3,0,1]
+    v += dpp_src<0x141>(v, 0.0f);  // row_half_mirror
+    v += dpp_src<0x140>(v, 0.0f);  // row_mirror
+    return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    v = fmaxf(v, dpp_src<0xB1>(v, -INFINITY));
+    v = fmaxf(v, dpp_src<0x4E>(v, -INFINITY));
+    v = fmaxf(v, dpp_src<0x141>(v, -INFINITY));
+    v = fmaxf(v, dpp_src<0x140>(v, -INFINITY));
+    return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
 }
 
 // Elements [i, i + 8) of a typed buffer as fp32; i % 8 == 0 and the buffer is
@@ -153,7 +171,7 @@ __global__ __launch_bounds__(kNormThreads) void k_add_rmsnorm(float* __restrict_
     float total = 0.0f;
 #pragma unroll
     for (int i = 0; i < kNormThreads / kWave; ++i) total += red[i];
-    const float inv = 1.0f / sqrtf(total / static_cast<float>(hidden) + eps);
+    const float inv = 1.0f / sqrtf(__fadd_rn(total / static_cast<float>(hidden), eps));  // no fma contraction
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int64_t i = (threadIdx.x + static_cast<int64_t>(kNormThreads) * j) * 8;
@@ -172,25 +190,71 @@ __global__ __launch_bounds__(kNormThreads) void k_add_rmsnorm(float* __restrict_
 // d = l + 64 j, so for head_dim >= 128 the rotate-half partner d +- D/2 is
 // element j +- E/2 of the same lane; for head_dim 64 it is lane l ^ 32.
 
-// Lane's E = D / 64 elements d = lane + 64 j of one head vector: RMSNorm with
-// weight nw (when not NULL), then rotate-half RoPE with the table rows cr/sr.
+// Element i of an F32 / F16 / BF16 buffer from two unconditional 16-bit loads
+// (the halves of an fp32, or the same half twice): no branch surrounds the
+// load, so a wave issues all of them before waiting on any.
+struct RawHalves {
+    uint32_t lo, hi;
+};
+
+__device__ __forceinline__ RawHalves load_raw(const void* __restrict__ p, int dtype, int64_t i) {
+    const uint16_t* h = static_cast<const uint16_t*>(p);
+    const bool wide = dtype == NQ_DTYPE_F32;
+    RawHalves r;
+    r.lo = h[wide ? 2 * i : i];
+    r.hi = h[wide ? 2 * i + 1 : i];
+    return r;
+}
+
+__device__ __forceinline__ float raw_value(const RawHalves& r, int dtype) {
+    const float f32 = __uint_as_float((r.hi << 16) | (r.lo & 0xffffu));
+    const float bf16 = __uint_as_float(r.lo << 16);
+    const float f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.lo)));
+    return dtype == NQ_DTYPE_F32 ? f32 : (dtype == NQ_DTYPE_BF16 ? bf16 : f16);
+}
+
+// The operands of norm_rope_regs for one lane: the head vector's elements
+// d = lane + 64 j and the norm weights (loaded from the head vector itself,
+// and ignored, when there is no weight).
 template <int D>
-__device__ __forceinline__ void norm_rope(const float* __restrict__ src, const void* __restrict__ nw, int ndt, float eps,
-                                          const float* __restrict__ cr, const float* __restrict__ sr, int lane,
-                                          float (&y)[D / kWave]) {
+struct NormRopeIn {
+    float x[D / kWave];
+    RawHalves w[D / kWave];
+};
+
+template <int D>
+__device__ __forceinline__ void load_norm_rope_in(NormRopeIn<D>& in, const float* __restrict__ src,
+                                                  const void* __restrict__ nw, int ndt, int lane) {
+    const void* wp = nw ? nw : static_cast<const void*>(src);
+    const int wdt = nw ? ndt : NQ_DTYPE_F32;
+#pragma unroll
+    for (int j = 0; j < D / kWave; ++j) {
+        in.x[j] = src[lane + kWave * j];
+        in.w[j] = load_raw(wp, wdt, lane + kWave * j);
+    }
+}
+
+// norm_rope on loaded operands: cs / sn are the lane's RoPE table entries
+// (index d mod D/2 of the position's row).
+template <int D>
+__device__ __forceinline__ void norm_rope_regs(const NormRopeIn<D>& in, bool has_w, int ndt, float eps,
+                                               const float (&cs)[D / kWave], const float (&sn)[D / kWave], int lane,
+                                               float (&y)[D / kWave]) {
     constexpr int E = D / kWave;
     constexpr int kHalf = D / 2;
     float x[E];
 #pragma unroll
-    for (int j = 0; j < E; ++j) x[j] = src[lane + kWave * j];
-    if (nw) {
-        float ss = 0.0f;
+    for (int j = 0; j < E; ++j) x[j] = in.x[j];
+    // Branch-free (a branch here would sink the weight loads into it).
+    float ss = 0.0f;
 #pragma unroll
-        for (int j = 0; j < E; ++j) ss = fmaf(x[j], x[j], ss);
-        ss = wave_sum(ss);
-        const float inv = 1.0f / sqrtf(ss / static_cast<float>(D) + eps);
+    for (int j = 0; j < E; ++j) ss = fmaf(x[j], x[j], ss);
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(__fadd_rn(ss / static_cast<float>(D), eps));  // no fma contraction
 #pragma unroll
-        for (int j = 0; j < E; ++j) x[j] = __fmul_rn(nq::load_f32(nw, ndt, lane + kWave * j), __fmul_rn(x[j], inv));
+    for (int j = 0; j < E; ++j) {
+        const float normed = __fmul_rn(raw_value(in.w[j], ndt), __fmul_rn(x[j], inv));
+        x[j] = has_w ? normed : x[j];
     }
 #pragma unroll
     for (int j = 0; j < E; ++j) {
@@ -202,10 +266,30 @@ __device__ __forceinline__ void norm_rope(const float* __restrict__ src, const v
         } else {
             partner = first ? x[j + E / 2] : x[j - E / 2];
         }
-        const int fi = first ? d : d - kHalf;
         const float rot = first ? -partner : partner;
-        y[j] = __fadd_rn(__fmul_rn(x[j], cr[fi]), __fmul_rn(rot, sr[fi]));
+        y[j] = __fadd_rn(__fmul_rn(x[j], cs[j]), __fmul_rn(rot, sn[j]));
     }
+}
+
+// Lane's E = D / 64 elements d = lane + 64 j of one head vector: RMSNorm with
+// weight nw (when not NULL), then rotate-half RoPE with the table rows cr/sr
+// (the same arithmetic as the fused decode attention, norm_rope_regs).
+template <int D>
+__device__ __forceinline__ void norm_rope(const float* __restrict__ src, const void* __restrict__ nw, int ndt, float eps,
+                                          const float* __restrict__ cr, const float* __restrict__ sr, int lane,
+                                          float (&y)[D / kWave]) {
+    constexpr int E = D / kWave;
+    NormRopeIn<D> in;
+    load_norm_rope_in<D>(in, src, nw, ndt, lane);
+    float cs[E], sn[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int d = lane + kWave * j;
+        const int fi = d < D / 2 ? d : d - D / 2;
+        cs[j] = cr[fi];
+        sn[j] = sr[fi];
+    }
+    norm_rope_regs<D>(in, nw != nullptr, ndt, eps, cs, sn, lane, y);
 }
 
 template <int D>
@@ -317,6 +401,8 @@ __device__ __forceinline__ void load_v(const char* __restrict__ p, float (&v)[E]
         }
     }
 }
+
+constexpr int kMergeRound = 16;  // partial blocks merged per round of loads
 
 __device__ __forceinline__ int64_t attn_part_index(int64_t t, int h, int s, int q_heads, int blocks) {
     return (t * q_heads + h) * blocks + s;
@@ -433,13 +519,32 @@ __global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__
     }
     const int nb = static_cast<int>(pt / block_rows) + 1;
     const int64_t p0 = attn_part_index(t, h, 0, q_heads, blocks);
-    float mmax = -INFINITY;
-    for (int b = 0; b < nb; ++b) mmax = fmaxf(mmax, part_ml[2 * (p0 + b)]);
-    float lsum = 0.0f, acc = 0.0f;
-    for (int b = 0; b < nb; ++b) {
-        const float f = expf(part_ml[2 * (p0 + b)] - mmax);
-        lsum = fmaf(part_ml[2 * (p0 + b) + 1], f, lsum);
-        acc = fmaf(part_acc[(p0 + b) * D + d], f, acc);
+    // Rounds of kMergeRound blocks: every load of a round is issued before any
+    // use (addresses clamped to the last block, extra blocks weighted 0), and
+    // rounds combine with a running max.
+    float mrun = -INFINITY, lsum = 0.0f, acc = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += kMergeRound) {
+        float mb[kMergeRound], lb[kMergeRound], ab[kMergeRound];
+#pragma unroll
+        for (int i = 0; i < kMergeRound; ++i) {
+            const int64_t pb = p0 + (b0 + i < nb ? b0 + i : nb - 1);
+            mb[i] = part_ml[2 * pb];
+            lb[i] = part_ml[2 * pb + 1];
+            ab[i] = part_acc[pb * D + d];
+        }
+        float mnew = mrun;
+#pragma unroll
+        for (int i = 0; i < kMergeRound; ++i) mnew = fmaxf(mnew, mb[i]);
+        const float keep = expf(mrun - mnew);  // 0 in the first round
+        lsum *= keep;
+        acc *= keep;
+#pragma unroll
+        for (int i = 0; i < kMergeRound; ++i) {
+            const float f = b0 + i < nb ? expf(mb[i] - mnew) : 0.0f;
+            lsum = fmaf(lb[i], f, lsum);
+            acc = fmaf(ab[i], f, acc);
+        }
+        mrun = mnew;
     }
     nq::store_f32_as(out, odt, o, acc / lsum);
 }
@@ -462,8 +567,8 @@ __global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__
 
 template <int D, int CT, int G>
 constexpr size_t decode_attention_lds() {
-    return static_cast<size_t>(kSeqBlock) * k_row_bytes<D, CT>() + static_cast<size_t>(kSeqBlock) * D * cache_bytes<CT>() +
-           static_cast<size_t>(G) * (D + kSeqBlock) * sizeof(float);
+    return static_cast<size_t>(kSeqBlock + 1) * k_row_bytes<D, CT>() +
+           static_cast<size_t>(kSeqBlock + 1) * D * cache_bytes<CT>() + static_cast<size_t>(G) * (D + kSeqBlock) * sizeof(float);
 }
 
 template <int D, int CT, int G>
@@ -480,10 +585,10 @@ __global__ __launch_bounds__(G * kWave) void k_decode_attention(
     constexpr int PIECES = D * EB / 16;        // 16-byte pieces per row
     constexpr int PER_THREAD = kSeqBlock * PIECES / (G * kWave);
     extern __shared__ float lds_raw[];
-    char* klds = reinterpret_cast<char*>(lds_raw);
-    char* vlds = klds + kSeqBlock * RB;
-    float* qs = reinterpret_cast<float*>(vlds + kSeqBlock * VRB);  // [G][D]
-    float* ps = qs + G * D;                                       // [G][64]
+    char* klds = reinterpret_cast<char*>(lds_raw);   // kSeqBlock rows + one scratch row
+    char* vlds = klds + (kSeqBlock + 1) * RB;
+    float* qs = reinterpret_cast<float*>(vlds + (kSeqBlock + 1) * VRB);  // [G][D]
+    float* ps = qs + G * D;                                             // [G][64]
 
     const int g = blockIdx.x;
     const int s = blockIdx.y;
@@ -491,63 +596,88 @@ __global__ __launch_bounds__(G * kWave) void k_decode_attention(
     const int q_heads = kv_heads * G;
     const int w = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t p = position[0];
+
+    // Loads that do not need the position go first: this wave's q head and
+    // the k and v of head g, with their norm weights (no branch on the dtype).
+    NormRopeIn<D> qin, kin;
+    load_norm_rope_in<D>(qin, q + static_cast<int64_t>(g * G + w) * D, q_norm, ndt, lane);
+    load_norm_rope_in<D>(kin, k + static_cast<int64_t>(g) * D, k_norm, ndt, lane);
+    float vraw[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) vraw[j] = v[static_cast<int64_t>(g) * D + lane + kWave * j];
+
+    // No early exit (it would sink the loads above below the wait for the
+    // position): a block past the position runs the arithmetic of a one-row
+    // block at row0 and stores nothing; the merge ignores it.
+    const int64_t pos = position[0];
     const int64_t row0 = static_cast<int64_t>(s) * kSeqBlock;
-    if (p < 0 || p >= max_positions || row0 > p) return;  // uniform; the merge ignores such blocks
-    const bool owns_p = p < row0 + kSeqBlock;
-    const int rows = static_cast<int>(owns_p ? p - row0 + 1 : kSeqBlock);  // rows scored
-    const int cached = owns_p ? rows - 1 : rows;                              // rows read from the cache
+    const bool live = pos >= 0 && pos < max_positions && row0 <= pos;  // uniform
+    const int64_t p = live ? pos : row0;
+    const bool owns_p = live && p < row0 + kSeqBlock;
+    const int rows = live ? static_cast<int>(owns_p ? p - row0 + 1 : kSeqBlock) : 1;  // rows scored
+    const int cached = live ? (owns_p ? rows - 1 : rows) : 0;                         // rows read from the cache
     const int64_t head_row0 = static_cast<int64_t>(g) * max_positions;
 
-    // Issue the loads.
-    uint4 kp[PER_THREAD], vp[PER_THREAD];
+    // The block's cached K and V rows and the position's RoPE entries, all
+    // issued before any is used (rows past `cached` reload row 0 and go to
+    // the scratch row).
+    u32x4 kp[PER_THREAD], vp[PER_THREAD];
     const char* kbase = k_cache + (head_row0 + row0) * VRB;
     const char* vbase = v_cache + (head_row0 + row0) * VRB;
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
         const int idx = threadIdx.x + i * G * kWave;
         const int r = idx / PIECES, c = idx % PIECES;
-        const int rr = r < cached ? r : 0;  // row 0 of the block is cached unless p == row0 (then unused)
-        kp[i] = *reinterpret_cast<const uint4*>(kbase + rr * VRB + 16 * c);
-        vp[i] = *reinterpret_cast<const uint4*>(vbase + rr * VRB + 16 * c);
+        const int rr = r < cached ? r : 0;  // row 0 of the block is in range (row0 <= p)
+        kp[i] = *reinterpret_cast<const u32x4*>(kbase + rr * VRB + 16 * c);
+        vp[i] = *reinterpret_cast<const u32x4*>(vbase + rr * VRB + 16 * c);
     }
-    const float* cr = cos_table + p * (D / 2);
-    const float* sr = sin_table + p * (D / 2);
+    float cs[E], sn[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int d = lane + kWave * j;
+        const int fi = d < D / 2 ? d : d - D / 2;
+        cs[j] = cos_table[p * (D / 2) + fi];
+        sn[j] = sin_table[p * (D / 2) + fi];
+    }
+    // Pin the block loads here: all of them are issued before the first wait.
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) asm volatile("" : "+v"(kp[i]), "+v"(vp[i]));
     float qy[E];
-    norm_rope<D>(q + static_cast<int64_t>(g * G + w) * D, q_norm, ndt, eps, cr, sr, lane, qy);
-    // Stage K and V rows below p.
+    norm_rope_regs<D>(qin, q_norm != nullptr, ndt, eps, cs, sn, lane, qy);
+    // Stage K and V rows below p (the others to the scratch row).
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
         const int idx = threadIdx.x + i * G * kWave;
         const int r = idx / PIECES, c = idx % PIECES;
-        if (r < cached) {
-            *reinterpret_cast<uint4*>(klds + r * RB + 16 * c) = kp[i];
-            *reinterpret_cast<uint4*>(vlds + r * VRB + 16 * c) = vp[i];
-        }
+        const int lr = r < cached ? r : kSeqBlock;
+        *reinterpret_cast<u32x4*>(klds + lr * RB + 16 * c) = kp[i];
+        *reinterpret_cast<u32x4*>(vlds + lr * VRB + 16 * c) = vp[i];
     }
 #pragma unroll
     for (int j = 0; j < E; ++j) qs[w * D + lane + kWave * j] = qy[j];
+    // Row p's k and v: every wave forms them (identical values) and writes
+    // them to LDS row rows - 1 when this block holds p, else to the scratch
+    // row (no branch, so their loads stay ahead of the position wait); wave 0
+    // appends k and wave G - 1 appends v to the cache.
+    float ky[E];
+    norm_rope_regs<D>(kin, k_norm != nullptr, ndt, eps, cs, sn, lane, ky);
+    const int nr = owns_p ? rows - 1 : kSeqBlock;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int d = lane + kWave * j;
+        nq::store_f32_as(klds + nr * RB, CT, d, ky[j]);
+        nq::store_f32_as(vlds + nr * VRB, CT, d, vraw[j]);
+    }
     if (owns_p) {
         const int64_t crow = (head_row0 + p) * D;
-        const int r = rows - 1;
         if (w == 0) {
-            float ky[E];
-            norm_rope<D>(k + static_cast<int64_t>(g) * D, k_norm, ndt, eps, cr, sr, lane, ky);
 #pragma unroll
-            for (int j = 0; j < E; ++j) {
-                const int d = lane + kWave * j;
-                nq::store_f32_as(k_cache, CT, crow + d, ky[j]);
-                nq::store_f32_as(klds + r * RB, CT, d, ky[j]);
-            }
+            for (int j = 0; j < E; ++j) nq::store_f32_as(k_cache, CT, crow + lane + kWave * j, ky[j]);
         }
         if (w == G - 1) {
 #pragma unroll
-            for (int j = 0; j < E; ++j) {
-                const int d = lane + kWave * j;
-                const float vv = v[static_cast<int64_t>(g) * D + d];
-                nq::store_f32_as(v_cache, CT, crow + d, vv);
-                nq::store_f32_as(vlds + r * VRB, CT, d, vv);
-            }
+            for (int j = 0; j < E; ++j) nq::store_f32_as(v_cache, CT, crow + lane + kWave * j, vraw[j]);
         }
     }
     __syncthreads();
@@ -572,6 +702,7 @@ __global__ __launch_bounds__(G * kWave) void k_decode_attention(
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[e] = fmaf(pr, vv[e], acc[e]);
     }
+    if (!live) return;
     const int h = g * G + w;
     const int64_t pi = attn_part_index(0, h, s, q_heads, blocks);
     if (lane == 0) {
