@@ -365,7 +365,10 @@ def e2e_decode(layers: int, prompt_len: int, new_tokens: int, repeats: int, pack
     best = min(runs, key=lambda r: r["decode_ms"])
     decode_steps = new_tokens - 1
     ms_per_token = best["decode_ms"] / decode_steps
-    kernels_per_layer = 12
+    # per layer: unfused RMSNorm, QKV (2), attention (2), O (2), RMSNorm, gate/up (2), SiLU product,
+    # down (2); fused: the two norms and the SiLU product run inside the packed calls (layer 0 keeps
+    # its input norm). Plus embedding, final norm, lm_head and greedy select.
+    kernels = layers * 10 + 5 if decoder.fuse_decode else layers * 12 + 4
     return {
         "workload": (f"qwen3-8b-shape random-init packed model, {layers} layers, vocab {config.vocab}, "
                      f"prompt {prompt_len} ids, {new_tokens} greedy tokens, batch 1, bf16 activations/KV"),
@@ -376,7 +379,8 @@ def e2e_decode(layers: int, prompt_len: int, new_tokens: int, repeats: int, pack
         "total_tok_per_s": round(new_tokens * 1000.0 / (best["prefill_ms"] + best["decode_ms"]), 2),
         "packed_linear_us_per_layer": round(packed_us_per_layer, 2),
         "shell_us_per_token": round(ms_per_token * 1000.0 - packed_us_per_layer * layers, 1),
-        "kernels_per_token": layers * kernels_per_layer + 4,
+        "kernels_per_token": kernels,
+        "fused_decode": decoder.fuse_decode,
         "first_tokens": tokens[:8],
         "repeats": repeats,
     }

@@ -214,6 +214,48 @@ int nq_linear_batch(const nq_linear_desc* const* descs, int32_t count, const voi
                     int32_t x_dtype, int64_t tokens, void* const* ys, int32_t y_dtype,
                     void* const* workspaces, const int64_t* workspace_bytes, void* stream);
 
+/* Input forms of a fused one-token decode call (nq_linear_batch_fused). */
+typedef enum nq_input_kind {
+    NQ_INPUT_PLAIN = 0,     /* x as in nq_linear_batch                                */
+    NQ_INPUT_RMSNORM = 1,   /* x is an fp32 residual h [in]; member i sees RMSNorm(h) * w
+                               through col_scales[i] = w * s_in (fp32 [in], replacing
+                               its s_in) and 1 / RMS(h) from norm_slots               */
+    NQ_INPUT_SILU_GATE = 2  /* x is the fp32 gate g [in], ups[i] the fp32 up u [in];
+                               member i sees silu(g) * u                              */
+} nq_input_kind;
+
+/* Decoder fusions around the packed linears of one decode token. */
+typedef struct nq_decode_fusion {
+    int32_t input_kind;              /* nq_input_kind                                   */
+    float eps;                       /* RMSNORM: epsilon of the norm                    */
+    const float* const* col_scales;  /* RMSNORM: [count] fp32 [in] column scales        */
+    const float* norm_slots;         /* RMSNORM: sums of h^2 per 16-row tile of h, as
+                                        written by a residual epilogue (out_slots)     */
+    int64_t norm_slot_count;         /* RMSNORM: ceil(in / 16), a multiple of 4, <= 1024 */
+    const void* const* ups;          /* SILU_GATE: [count] fp32 [in]                     */
+    float* const* residuals;         /* NULL, or [count]: member i adds its output to
+                                        residuals[i] (fp32 [out]) instead of writing y  */
+    float* const* out_slots;         /* with residuals: [count] fp32 [ceil(out / 16)]
+                                        sums of the new residual's squares per tile     */
+} nq_decode_fusion;
+
+/* One launch pair for `count` (1..8) packed linears of ONE token with the
+ * decoder's neighbouring element-wise work fused in: the input RMSNorm (the
+ * factor 1 / RMS(h) is applied to the rank intermediate, the weight is folded
+ * into the column scale) or the SiLU-gated product, and the residual add of
+ * the output with the per-tile sums of squares the next RMSNorm input needs.
+ * x is fp32 for the RMSNORM and SILU_GATE inputs; scales fp16; ys[i] may be
+ * NULL with residuals; no patch or row sidecar, and no salient columns with a
+ * non-plain input. Workspaces as for nq_linear_batch with tokens = 1.
+ * No reference counterpart: the reference decoder runs the norms,
+ * act_fn(gate) * up and the residual adds as separate torch operations around
+ * its packed linears (src/nanoquant/runtime/torch_model.py:493-505 MLP,
+ * :625-660 decoder layer; CudaPackedBackend.linear,
+ * src/nanoquant/runtime/cuda_backend.py:243-278). */
+int nq_linear_batch_fused(const nq_linear_desc* const* descs, int32_t count, const void* const* xs,
+                          int32_t x_dtype, void* const* ys, int32_t y_dtype, void* const* workspaces,
+                          const int64_t* workspace_bytes, const nq_decode_fusion* fusion, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -19,8 +19,9 @@ int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t t
                   int y_dtype, void* scratch, hipStream_t stream);
 
 // One launch for `count` (1..8) linears sharing the token count and dtypes.
+// `fusion` (NULL for none) adds the decoder fusions of nq_linear_batch_fused.
 int launch_decode_batch(const nq_linear_desc* const* descs, int count, const void* const* xs, int x_dtype,
                         int64_t tokens, void* const* ys, int y_dtype, void* const* scratch,
-                        hipStream_t stream);
+                        hipStream_t stream, const nq_decode_fusion* fusion = nullptr);
 
 }  // namespace nq

@@ -202,8 +202,40 @@ int enqueue_stage1(const Batch& batch, const LaunchShape& s, hipStream_t stream)
         case kActBf16: return enqueue_stage1_bf16(batch, s, stream);
         case kActF16: return enqueue_stage1_f16(batch, s, stream);
         case kActF32: return enqueue_stage1_f32(batch, s, stream);
+        case kActNormF32:
+        case kActGatedF32: return enqueue_stage1_fused(batch, s, stream);
         default: return enqueue_stage1_generic(batch, s, stream);
     }
+}
+
+// Fill member i's fusion fields; NQ_OK or an error status.
+int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, LinArgs& a) {
+    const int64_t in = d->in_features;
+    if (f.input_kind == NQ_INPUT_RMSNORM) {
+        if (!f.col_scales || !f.col_scales[i] || !f.norm_slots) return NQ_ERR_ARGUMENT;
+        if (f.norm_slot_count != (in + kTileRows - 1) / kTileRows || f.norm_slot_count % 4 != 0 ||
+            f.norm_slot_count > 256 * kSlotVecs)
+            return NQ_ERR_SHAPE;
+        if (!aligned(f.col_scales[i], 16) || !aligned(f.norm_slots, 16)) return NQ_ERR_ALIGNMENT;
+        if (!(f.eps > 0.0f)) return NQ_ERR_ARGUMENT;
+        a.col_scale = f.col_scales[i];
+        a.slots_in = f.norm_slots;
+        a.nslots = static_cast<int>(f.norm_slot_count);
+        a.eps = f.eps;
+    } else if (f.input_kind == NQ_INPUT_SILU_GATE) {
+        if (!f.ups || !f.ups[i]) return NQ_ERR_ARGUMENT;
+        if (!aligned(f.ups[i], 16)) return NQ_ERR_ALIGNMENT;
+        a.x2 = f.ups[i];
+    } else if (f.input_kind != NQ_INPUT_PLAIN) {
+        return NQ_ERR_ARGUMENT;
+    }
+    if (f.input_kind != NQ_INPUT_PLAIN && d->salient_count > 0) return NQ_ERR_UNSUPPORTED;
+    if (f.residuals) {
+        if (!f.residuals[i] || !f.out_slots || !f.out_slots[i]) return NQ_ERR_ARGUMENT;
+        a.residual = f.residuals[i];
+        a.slots_out = f.out_slots[i];
+    }
+    return NQ_OK;
 }
 
 int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t stream) {
@@ -286,7 +318,7 @@ int launch_decode(const nq_linear_desc* d, const void* x, int x_dtype, int64_t t
 
 int launch_decode_batch(const nq_linear_desc* const* descs, int count, const void* const* xs, int x_dtype,
                         int64_t tokens, void* const* ys, int y_dtype, void* const* scratch,
-                        hipStream_t stream) {
+                        hipStream_t stream, const nq_decode_fusion* fusion) {
     if (count < 1 || count > kMaxBatch) return NQ_ERR_SHAPE;
     if (tokens < 1 || tokens > kMaxTokens) return NQ_ERR_SHAPE;
     Batch batch{};
@@ -295,12 +327,26 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
     for (int i = 0; i < count; ++i) {
         if (descs[i]->decode_launch != descs[0]->decode_launch) return NQ_ERR_ARGUMENT;
         if (descs[i]->scale_dtype != descs[0]->scale_dtype) return NQ_ERR_DTYPE;
-        const int st = describe(descs[i], xs[i], x_dtype, tokens, ys[i], y_dtype, scratch[i], batch.p[i], vector_ok);
+        int st = describe(descs[i], xs[i], x_dtype, tokens, ys[i], y_dtype, scratch[i], batch.p[i], vector_ok);
         if (st != NQ_OK) return st;
+        if (fusion) {
+            st = describe_fusion(*fusion, i, descs[i], batch.p[i]);
+            if (st != NQ_OK) return st;
+        }
     }
     int ak = kActGeneric;
     if (vector_ok) {
         ak = x_dtype == NQ_DTYPE_BF16 ? kActBf16 : (x_dtype == NQ_DTYPE_F16 ? kActF16 : kActF32);
+    }
+    if (fusion) {
+        // The fused forms have vector kernels only: one token, the split launch,
+        // fp32 x and fp16 scales with the vector-load shape.
+        if (tokens != 1 || descs[0]->decode_launch != NQ_DECODE_SPLIT) return NQ_ERR_UNSUPPORTED;
+        if (fusion->input_kind != NQ_INPUT_PLAIN) {
+            if (x_dtype != NQ_DTYPE_F32) return NQ_ERR_DTYPE;
+            if (!vector_ok) return NQ_ERR_ALIGNMENT;
+            ak = fusion->input_kind == NQ_INPUT_RMSNORM ? kActNormF32 : kActGatedF32;
+        }
     }
     return launch_batch(batch, tokens, ak, descs[0]->decode_launch == NQ_DECODE_FUSED, stream);
 }

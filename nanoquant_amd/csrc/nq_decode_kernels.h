@@ -88,6 +88,7 @@ namespace nqdec {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kTileRows = 16;
 constexpr int kBlockCols = 128;   // one word per lane
@@ -191,6 +192,14 @@ struct LinArgs {
     uint8_t* lmq;            // stage-2 A operands, see lmq_offset
     int* lme;                // [tokens] exponent of lmq per token
     int nw1, nw2;            // waves per workgroup of each stage (the fused launch: both equal)
+    // Decoder fusions (nq_linear_batch_fused, one token; null / zero otherwise).
+    const void* x2;          // gated input: up [in] (fp32); x is the gate
+    const float* col_scale;  // normed input: fp32 column scale replacing s_in
+    const float* slots_in;   // normed input: sums of squares of x per 16-row tile of its producer
+    float* residual;         // stage 2: residual[o] += y (y is not written)
+    float* slots_out;        // stage 2: sum of residual^2 per 16-row output tile
+    int nslots;              // entries of slots_in
+    float eps;               // normed input: RMSNorm epsilon
 };
 static_assert(sizeof(LinArgs) % 16 == 0, "LinArgs is read as 16-byte vectors");
 
@@ -239,6 +248,13 @@ __device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
     a.lme = s.lme;
     a.nw1 = s.nw1;
     a.nw2 = s.nw2;
+    a.x2 = s.x2;
+    a.col_scale = s.col_scale;
+    a.slots_in = s.slots_in;
+    a.residual = s.residual;
+    a.slots_out = s.slots_out;
+    a.nslots = s.nslots;
+    a.eps = s.eps;
     // One statement, so every field is waited for at the same point; it
     // redefines the integer fields, so no arithmetic on them can be hoisted
     // above it (the pointers are only read, so they stay known-global).
@@ -252,11 +268,17 @@ __device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
 }
 // Activation kinds (template parameter AK): how stage 1 reads a[t, k].
 enum : int {
-    kActBf16 = 0,     // bf16 x, fp16 s_in, vector loads
-    kActF16 = 1,      // fp16 x, fp16 s_in, vector loads
-    kActF32 = 2,      // fp32 x, fp16 s_in, vector loads
-    kActGeneric = 3,  // any float x and s_in, element loads
+    kActBf16 = 0,      // bf16 x, fp16 s_in, vector loads
+    kActF16 = 1,       // fp16 x, fp16 s_in, vector loads
+    kActF32 = 2,       // fp32 x, fp16 s_in, vector loads
+    kActGeneric = 3,   // any float x and s_in, element loads
+    kActNormF32 = 4,   // fp32 x (a residual), fp32 col_scale (norm weight * s_in), RMS factor from slots_in
+    kActGatedF32 = 5,  // silu(x) * x2 from fp32 gate x and up x2, fp16 s_in
 };
+
+// Column-scale dtype of a vector kind.
+template <int AK>
+constexpr int col_scale_dtype() { return AK == kActNormF32 ? NQ_DTYPE_F32 : NQ_DTYPE_F16; }
 
 // Rows of an A operand block: 4 digit rows for each of TPB tokens.
 template <int TPB>
@@ -305,6 +327,31 @@ __device__ __forceinline__ float wave_max(float v) {
     const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
     const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_addf(float x) {
+    const int y = __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false);
+    return x + __int_as_float(y);
+}
+
+// Sum over each row of 16 lanes (every lane of the row gets it); the whole
+// wave must be active.
+__device__ __forceinline__ float row16_sum(float v) {
+    v = dpp_addf<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_addf<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_addf<0x141>(v);  // row_half_mirror
+    return dpp_addf<0x140>(v);  // row_mirror
+}
+
+// Sum over the whole wave (a uniform value); the whole wave must be active.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (a + b) + (c + d);
 }
 
 // --- branch-free element loads of a runtime float dtype ------------------------
@@ -424,7 +471,6 @@ template <int AK>
 constexpr int act_dtype() {
     return AK == kActBf16 ? NQ_DTYPE_BF16 : (AK == kActF16 ? NQ_DTYPE_F16 : NQ_DTYPE_F32);
 }
-constexpr int kScaleDtype = NQ_DTYPE_F16;  // column scale of the vector kinds
 
 // Staging lane roles: lane L stages (m, d, h) = (L >> 3, (L >> 1) & 3, L & 1),
 // the eight consecutive columns k0 + {0..7}, k0 = 512c + 128d + 16m + 8h: run 0
@@ -438,6 +484,7 @@ __device__ __forceinline__ int stage_col0(int c, int lane) {
 template <int AK, int TOK, int TW>
 struct S1Regs {
     Run<AK> x[TOK][2];
+    Run<AK> x2[AK == kActGatedF32 ? TOK : 1][2];  // gated kind: up
     Run<AK> s[2];
     v4u w[TW];
 };
@@ -477,7 +524,12 @@ __device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const LinAr
     const int in = static_cast<int>(a.in);
 #pragma unroll
     for (int t = 0; t < TOK; ++t) load_runs<AK, DT>(r.x[t], a.x, a.x_dtype, t, a.tokens, in, k0, in);
-    load_runs<AK, kScaleDtype>(r.s, a.s_in, a.scale_dtype, 0, 1, 0, k0, in);
+    if constexpr (AK == kActGatedF32) {
+#pragma unroll
+        for (int t = 0; t < TOK; ++t) load_runs<AK, DT>(r.x2[t], a.x2, a.x_dtype, t, a.tokens, in, k0, in);
+    }
+    load_runs<AK, col_scale_dtype<AK>()>(r.s, AK == kActNormF32 ? static_cast<const void*>(a.col_scale) : a.s_in,
+                                         a.scale_dtype, 0, 1, 0, k0, in);
 }
 
 // Sign words of chunk c for tiles t0 .. t0 + TW - 1 (tiles past the last one
@@ -559,6 +611,37 @@ __device__ __forceinline__ uint32_t bytes_at(uint32_t a, uint32_t b, uint32_t c,
            (((d >> (8 * B)) & 0xffu) << 24);
 }
 
+// Normed kind: lane l's share of the producer's tile sums, vectors i * 64 + l
+// (zero past nslots; nslots % 4 == 0 and nslots <= 256 * kSlotVecs, checked
+// by the host).
+constexpr int kSlotVecs = 4;
+
+__device__ __forceinline__ void load_slots(v4f (&sl)[kSlotVecs], const float* __restrict__ slots, int nslots,
+                                           int lane) {
+    const int nv = nslots >> 2;
+#pragma unroll
+    for (int i = 0; i < kSlotVecs; ++i) {
+        sl[i] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (i * 64 < nv) {  // uniform
+            const int vi = i * 64 + lane;
+            const v4f q = *reinterpret_cast<const v4f*>(slots + 4 * (vi < nv ? vi : nv - 1));
+            sl[i] = vi < nv ? q : sl[i];
+        }
+    }
+}
+
+// Gated kind: v = silu(v) * up (the arithmetic of the separate SiLU-product
+// kernel); other kinds leave v unchanged.
+template <int AK, int TOK, int TW>
+__device__ __forceinline__ void gate_values(const S1Regs<AK, TOK, TW>& r, int t, int run, float (&v)[4]) {
+    if constexpr (AK == kActGatedF32) {
+        float up[4];
+        run_values<AK, NQ_DTYPE_F32>(r.x2[t][run], NQ_DTYPE_F32, up);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(v[i] / (1.0f + expf(-v[i])), up[i]);
+    }
+}
+
 // Stage tokens [t_base, t_base + TPB) of chunk c into this wave's operand area
 // (three digit rows per token) and return each token's exponent E and the
 // chunk max |a| (uniform values).
@@ -583,8 +666,8 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
     const int lim = left > 8 ? 8 : (left < 0 ? 0 : left);
     const bool full_chunk = (c + 1) * kChunkCols <= in;  // uniform
     float sc[2][4];
-    run_values<AK, kScaleDtype>(r.s[0], a.scale_dtype, sc[0]);
-    run_values<AK, kScaleDtype>(r.s[1], a.scale_dtype, sc[1]);
+    run_values<AK, col_scale_dtype<AK>()>(r.s[0], a.scale_dtype, sc[0]);
+    run_values<AK, col_scale_dtype<AK>()>(r.s[1], a.scale_dtype, sc[1]);
 #pragma unroll
     for (int u = 0; u < TPB; ++u) {
         const int t = t_base + u;
@@ -594,6 +677,7 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
 #pragma unroll
             for (int run = 0; run < 2; ++run) {
                 run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
+                gate_values<AK, TOK, TW>(r, t, run, v[run]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     v[run][i] *= sc[run][i];
@@ -604,6 +688,7 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
 #pragma unroll
             for (int run = 0; run < 2; ++run) {
                 run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
+                gate_values<AK, TOK, TW>(r, t, run, v[run]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const bool ok = t < a.tokens && 4 * run + i < lim;
@@ -837,6 +922,10 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
     const int fr = (t0 + f.tt) * kTileRows + f.n;
     RawElem rs0;
     float maxsm;
+    // Normed kind: the producer's per-tile sums of squares of x (up to
+    // kSlotVecs * 256 of them), loaded ahead of the first pass's loads.
+    v4f slots[kSlotVecs];
+    float rs = 1.0f;  // 1 / RMS(x)
 
     // One pass: KC chunks per wave. The first pass is a separate copy ahead of
     // the loop (so its loads are not held behind waits for registers a
@@ -845,12 +934,28 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
     const auto pass = [&](const int base, const bool first) __attribute__((always_inline)) {
         const PassChunks<KC> pc = pass_chunks<KC>(base, wave, nw, nc);
         S1Regs<AK, TOK, TW> r[KC];
+        if constexpr (AK == kActNormF32) {
+            if (first) load_slots(slots, a.slots_in, a.nslots, lane);
+        }
         // Activations first, sign words second: the staging math waits only
         // for the activations, the MFMAs for the words.
 #pragma unroll
         for (int j = 0; j < KC; ++j) load_s1_acts(r[j], a, pc.c[j], lane);
 #pragma unroll
         for (int j = 0; j < KC; ++j) load_words(r[j].w, a.v_tiles, nt, nb, t0, pc.c[j], lane);
+        if constexpr (AK == kActNormF32) {
+            if (first) {
+                // Issued before the activations, so waiting for them here costs
+                // nothing the staging would not wait for anyway.
+#pragma unroll
+                for (int i = 0; i < kSlotVecs; ++i) asm volatile("" : "+v"(slots[i]));
+                float part = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kSlotVecs; ++i) part += (slots[i].x + slots[i].y) + (slots[i].z + slots[i].w);
+                const float total = wave_sum(part);
+                rs = 1.0f / sqrtf(__fadd_rn(total / static_cast<float>(a.in), a.eps));  // no fma contraction
+            }
+        }
         if (first) {
             // Vector kinds have fp16 scales: one 16-bit load (the generic kind
             // loads both halves); the bound sits at a uniform address.
@@ -913,10 +1018,10 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
             sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
             bound += cmx[c * TOK + o.t];
         }
-        const int e = range_exponent(bound * (512.0f * maxsm), 21);
+        const int e = range_exponent(bound * rs * (512.0f * maxsm), 21);
         float v = 0.0f;
         if (row < rank) v = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_mid, a.scale_dtype, row),
-                                             a.scale_dtype);
+                                             a.scale_dtype) * rs;
         store_lmq<TPB, TB, FUSED>(a.lmq, row, o.t, v, e);
         if (wg == 0 && o.tt == 0 && o.n == 0) {
             if (FUSED) __hip_atomic_store(a.lme + o.t, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1009,10 +1114,8 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     __syncthreads();
     if (dead) return;  // uniform, after the workgroup's only barrier
 
-    for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
-        const OutIdx o = out_index<TPB>(idx, tokens);
-        const int row = (t0 + o.tt) * kTileRows + o.n;
-        if (t0 + o.tt >= nt || row >= out) continue;
+    // Output value of index idx (row < out and its tile < nt).
+    const auto value = [&](const int idx, const OutIdx& o, const int row) __attribute__((always_inline)) {
         float sum = 0.0f;
         for (int c = 0; c < nc; ++c) sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
         float val = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_out, a.scale_dtype, row), a.scale_dtype);
@@ -1023,7 +1126,33 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
             val += wv * nq::load_f32(a.x, a.x_dtype, o.t * in + a.salient_indices[k]);
         }
         if (a.bias) val += elem_value(idx == threadIdx.x ? bias0 : load_elem(a.bias, a.bias_dtype, row), a.bias_dtype);
-        nq::store_f32_as(a.y, a.y_dtype, o.t * out + row, val);
+        return val;
+    };
+    if (TPB == 1 && a.residual) {
+        // Residual epilogue (one token, outs <= 64: wave 0, lanes 16 tt + n):
+        // residual[row] += value, and lane 16 tt writes the tile's sum of the
+        // new residual's squares (added in a fixed order).
+        if (threadIdx.x < 64) {
+            const int idx = threadIdx.x;
+            const OutIdx o = out_index<TPB>(idx, tokens);
+            const int row = (t0 + o.tt) * kTileRows + o.n;
+            const bool ok = idx < outs && t0 + o.tt < nt && row < out;
+            float sq = 0.0f;
+            if (ok) {
+                const float h = a.residual[row] + value(idx, o, row);
+                a.residual[row] = h;
+                sq = h * h;
+            }
+            sq = row16_sum(sq);
+            if (o.n == 0 && idx < outs && t0 + o.tt < nt) a.slots_out[t0 + o.tt] = sq;
+        }
+        return;
+    }
+    for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
+        const OutIdx o = out_index<TPB>(idx, tokens);
+        const int row = (t0 + o.tt) * kTileRows + o.n;
+        if (t0 + o.tt >= nt || row >= out) continue;
+        nq::store_f32_as(a.y, a.y_dtype, o.t * out + row, value(idx, o, row));
     }
 }
 
@@ -1087,6 +1216,7 @@ int enqueue_stage1_bf16(const Batch& batch, const LaunchShape& s, hipStream_t st
 int enqueue_stage1_f16(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_stage1_f32(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_stage1_generic(const Batch& batch, const LaunchShape& s, hipStream_t stream);
+int enqueue_stage1_fused(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_stage2(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_fused(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 

@@ -434,3 +434,31 @@ extern "C" int nq_linear_batch(const nq_linear_desc* const* descs, int32_t count
     }
     return NQ_OK;
 }
+
+extern "C" int nq_linear_batch_fused(const nq_linear_desc* const* descs, int32_t count, const void* const* xs,
+                                     int32_t x_dtype, void* const* ys, int32_t y_dtype, void* const* workspaces,
+                                     const int64_t* workspace_bytes, const nq_decode_fusion* fusion, void* stream) {
+    if (!descs || !xs || !ys || !workspaces || !workspace_bytes || !fusion) return NQ_ERR_ARGUMENT;
+    if (count < 1 || count > 8) return NQ_ERR_SHAPE;
+    if (!nq::is_float_dtype(x_dtype) || !nq::is_float_dtype(y_dtype)) return NQ_ERR_DTYPE;
+    if (fusion->input_kind != NQ_INPUT_PLAIN && x_dtype != NQ_DTYPE_F32) return NQ_ERR_DTYPE;
+    constexpr int64_t tokens = 1;
+    void* scratch[8];
+    for (int i = 0; i < count; ++i) {
+        const nq_linear_desc* d = descs[i];
+        int st = validate(d);
+        if (st != NQ_OK) return st;
+        if (!d->tiles || !xs[i]) return NQ_ERR_ARGUMENT;
+        if (!fusion->residuals && !ys[i]) return NQ_ERR_ARGUMENT;
+        if (d->patch_rank > 0 || d->row_count > 0) return NQ_ERR_UNSUPPORTED;  // they add to y afterwards
+        if (d->scale_dtype != NQ_DTYPE_F16) return NQ_ERR_DTYPE;
+        for (int j = 0; j < i; ++j) {
+            if (descs[j]->tiles == d->tiles) return NQ_ERR_ARGUMENT;  // one sync header per launch
+        }
+        const WorkspaceLayout wl = workspace_layout(d, tokens);
+        if (!workspaces[i] || workspace_bytes[i] < wl.total) return NQ_ERR_WORKSPACE;
+        scratch[i] = static_cast<char*>(workspaces[i]) + wl.decode_offset;
+    }
+    return nq::launch_decode_batch(descs, count, xs, x_dtype, tokens, ys, y_dtype, scratch,
+                                   static_cast<hipStream_t>(stream), fusion);
+}

@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "nq_linear_workspace_bytes",
     "nq_linear",
     "nq_linear_batch",
+    "nq_linear_batch_fused",
     "nq_decode_mixed_v_words",
     "nq_decode_product_codebook_words",
     "nq_transpose_signs",
@@ -125,6 +126,25 @@ class LinearDesc(ctypes.Structure):
     ]
 
 
+# nq_input_kind
+INPUT_PLAIN, INPUT_RMSNORM, INPUT_SILU_GATE = 0, 1, 2
+
+
+class DecodeFusion(ctypes.Structure):
+    """nq_decode_fusion (include/nqamd.h)."""
+
+    _fields_ = [
+        ("input_kind", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("col_scales", ctypes.POINTER(ctypes.c_void_p)),
+        ("norm_slots", ctypes.c_void_p),
+        ("norm_slot_count", ctypes.c_int64),
+        ("ups", ctypes.POINTER(ctypes.c_void_p)),
+        ("residuals", ctypes.POINTER(ctypes.c_void_p)),
+        ("out_slots", ctypes.POINTER(ctypes.c_void_p)),
+    ]
+
+
 _LIB: ctypes.CDLL | None = None
 
 
@@ -154,6 +174,11 @@ def _declare(lib: ctypes.CDLL) -> None:
             c_int,
             [ctypes.POINTER(desc_p), ctypes.c_int32, ctypes.POINTER(vp), ctypes.c_int32, c_i64,
              ctypes.POINTER(vp), ctypes.c_int32, ctypes.POINTER(vp), ctypes.POINTER(c_i64), vp],
+        ),
+        "nq_linear_batch_fused": (
+            c_int,
+            [ctypes.POINTER(desc_p), ctypes.c_int32, ctypes.POINTER(vp), ctypes.c_int32, ctypes.POINTER(vp),
+             ctypes.c_int32, ctypes.POINTER(vp), ctypes.POINTER(c_i64), ctypes.POINTER(DecodeFusion), vp],
         ),
         "nq_decode_mixed_v_words": (c_int, [vp, c_i64, vp, c_i64, vp, c_i64, c_i64, vp, vp, vp]),
         "nq_decode_product_codebook_words": (c_int, [vp, c_i64, vp, c_i64, vp, vp, c_i64, c_i64, vp, vp]),

@@ -192,6 +192,8 @@ class _Buffers:
     down: torch.Tensor
     final: torch.Tensor
     attn_ws: torch.Tensor
+    o_slots: torch.Tensor      # fused decode: sums of residual^2 per 16 rows after the o-projection
+    down_slots: torch.Tensor   # ... and after the down-projection
 
 
 class PackedDecoder:
@@ -208,6 +210,7 @@ class PackedDecoder:
         activation_dtype: torch.dtype = torch.bfloat16,
         cache_dtype: torch.dtype = torch.bfloat16,
         history_capacity: int = 4096,
+        fuse_decode: bool = True,
     ) -> None:
         self.config = c = config
         self.device = torch.device(device)
@@ -234,6 +237,17 @@ class PackedDecoder:
             qn = None if layer.q_norm is None or not c.qk_norm else layer.q_norm.to(dev).contiguous()
             kn = None if layer.k_norm is None or not c.qk_norm else layer.k_norm.to(dev).contiguous()
             self.norms.append((layer.input_norm.to(dev).contiguous(), layer.post_norm.to(dev).contiguous(), qn, kn))
+        # One-token steps fold the RMSNorms, the SiLU product and the residual
+        # adds into the packed calls (nq_linear_batch_fused) when every layer
+        # allows it: fp16 scales, no sidecars, hidden a multiple of 64 up to 16384.
+        self.fuse_decode = bool(fuse_decode) and self._fusable(weights)
+        self.col_scales: list[tuple[torch.Tensor, ...]] = []
+        if self.fuse_decode:
+            for prepared, (in_norm, post_norm, _qn, _kn) in zip(self.layers, self.norms):
+                self.col_scales.append(tuple(
+                    self.backend.norm_column_scale(prepared[role], norm)
+                    for role, norm in (("q_proj", in_norm), ("k_proj", in_norm), ("v_proj", in_norm),
+                                       ("gate_proj", post_norm), ("up_proj", post_norm))))
         cache_shape = (c.layers, c.kv_heads, self.max_positions, c.head_dim)
         self.k_cache = torch.zeros(cache_shape, dtype=cache_dtype, device=dev)
         self.v_cache = torch.zeros(cache_shape, dtype=cache_dtype, device=dev)
@@ -249,6 +263,20 @@ class PackedDecoder:
         self._decode_bufs: _Buffers | None = None
         self._graph: torch.cuda.CUDAGraph | None = None
         self.host_position = 0
+
+    def _fusable(self, weights: DecoderShellWeights) -> bool:
+        c = self.config
+        if c.hidden % 64 or c.hidden > 16384:
+            return False
+        for layer in weights.layers:
+            for state in layer.linears.values():
+                if state.scale_pre.dtype != torch.float16 or state.scale_mid.dtype != torch.float16 \
+                        or state.scale_post.dtype != torch.float16:
+                    return False
+                if state.outlier_indices is not None or state.patch_left is not None \
+                        or getattr(state, "row_indices", None) is not None:
+                    return False
+        return True
 
     # -- buffers -----------------------------------------------------------------
     def _buffers(self, tokens: int) -> _Buffers:
@@ -271,6 +299,7 @@ class PackedDecoder:
                                                      self.max_positions)
                 if tokens == 1 else ops.attention_workspace_bytes(tokens, c.q_heads, c.head_dim, self.max_positions),
                 dtype=torch.uint8, device=dev),
+            f32(-(-c.hidden // 16)), f32(-(-c.hidden // 16)),
         )
 
     # -- one forward -----------------------------------------------------------------
@@ -286,11 +315,19 @@ class PackedDecoder:
         then the logits and argmax partials of the last row."""
 
         c, t = self.config, b.tokens
+        fused = t == 1 and self.fuse_decode
         ops.launch_embedding(ids, self.embed, out=b.residual)
         for i, prepared in enumerate(self.layers):
             in_norm, post_norm, qn, kn = self.norms[i]
-            ops.launch_add_rmsnorm(b.residual, in_norm, c.eps, delta=b.down if i else None, out=b.xn)
-            self._linears([b.xn] * 3, [prepared["q_proj"], prepared["k_proj"], prepared["v_proj"]], [b.q, b.k, b.v], t)
+            qkv = [prepared["q_proj"], prepared["k_proj"], prepared["v_proj"]]
+            if fused and i > 0:
+                # residual already holds the previous down-projection (its epilogue)
+                self.backend.linear_batch_fused([b.residual[0]] * 3, qkv, input_kind="rmsnorm", eps=c.eps,
+                                                col_scales=list(self.col_scales[i][:3]), norm_slots=b.down_slots,
+                                                outs=[b.q[0], b.k[0], b.v[0]])
+            else:
+                ops.launch_add_rmsnorm(b.residual, in_norm, c.eps, delta=b.down if i else None, out=b.xn)
+                self._linears([b.xn] * 3, qkv, [b.q, b.k, b.v], t)
             if t == 1:
                 ops.launch_decode_attention(
                     b.q, b.k, b.v, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, q_norm=qn,
@@ -306,12 +343,22 @@ class PackedDecoder:
                 )
                 ops.launch_attention(b.q_rot, self.k_cache[i], self.v_cache[i], position=self.position,
                                      scaling=self.scaling, out=b.attn, workspace=b.attn_ws)
+            if fused:
+                self.backend.linear_batch_fused([b.attn.view(-1)], [prepared["o_proj"]], residuals=[b.residual[0]],
+                                                out_slots=[b.o_slots])
+                self.backend.linear_batch_fused([b.residual[0]] * 2, [prepared["gate_proj"], prepared["up_proj"]],
+                                                input_kind="rmsnorm", eps=c.eps,
+                                                col_scales=list(self.col_scales[i][3:]), norm_slots=b.o_slots,
+                                                outs=[b.gate[0], b.up[0]])
+                self.backend.linear_batch_fused([b.gate[0]], [prepared["down_proj"]], input_kind="silu_gate",
+                                                ups=[b.up[0]], residuals=[b.residual[0]], out_slots=[b.down_slots])
+                continue
             self._linears([b.attn], [prepared["o_proj"]], [b.o], t)
             ops.launch_add_rmsnorm(b.residual, post_norm, c.eps, delta=b.o, out=b.xn)
             self._linears([b.xn] * 2, [prepared["gate_proj"], prepared["up_proj"]], [b.gate, b.up], t)
             ops.launch_silu_mul(b.gate, b.up, out=b.act)
             self._linears([b.act], [prepared["down_proj"]], [b.down], t)
-        ops.launch_add_rmsnorm(b.residual, self.final_norm, c.eps, delta=b.down, out=b.final)
+        ops.launch_add_rmsnorm(b.residual, self.final_norm, c.eps, delta=None if fused else b.down, out=b.final)
         ops.launch_output_projection(b.final[t - 1], self.lm_head, logits=self.logits, workspace=self.proj_ws)
 
     def _decode_body(self) -> None:

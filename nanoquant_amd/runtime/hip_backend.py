@@ -302,6 +302,143 @@ class HipPackedBackend:
         _native.check("nq_linear_batch", status)
         return list(outs)
 
+    def norm_column_scale(self, layer: PreparedLayer, norm_weight: torch.Tensor) -> torch.Tensor:
+        """fp32 column scale norm_weight * s_in of a prepared layer: the
+        RMSNorm weight folded into the linear for ``linear_batch_fused``."""
+
+        payload = self._payload(layer)
+        weight = norm_weight.to(device=payload.device, dtype=torch.float32).reshape(-1)
+        if weight.numel() != layer.spec.in_features:
+            raise ValueError("norm weight width differs from the layer's input features")
+        return (weight * payload.scale_pre.to(torch.float32)).contiguous()
+
+    def linear_batch_fused(
+        self,
+        values: list[torch.Tensor] | tuple[torch.Tensor, ...],
+        layers: list[PreparedLayer] | tuple[PreparedLayer, ...],
+        *,
+        input_kind: str = "plain",
+        eps: float = 1e-6,
+        col_scales: list[torch.Tensor] | None = None,
+        norm_slots: torch.Tensor | None = None,
+        ups: list[torch.Tensor] | None = None,
+        residuals: list[torch.Tensor] | None = None,
+        out_slots: list[torch.Tensor] | None = None,
+        outs: list[torch.Tensor] | None = None,
+        output_dtype: torch.dtype = torch.float32,
+    ) -> list[torch.Tensor] | None:
+        """One decode token through 1-8 prepared layers with the decoder's
+        neighbouring element-wise work fused in (nq_linear_batch_fused):
+
+        * ``input_kind="rmsnorm"``: each value is the fp32 residual h; member i
+          sees RMSNorm(h) * w through ``col_scales[i]`` (``norm_column_scale``)
+          and the per-16-row-tile sums of h^2 in ``norm_slots``;
+        * ``input_kind="silu_gate"``: each value is the fp32 gate, ``ups[i]`` the
+          fp32 up; member i sees silu(gate) * up;
+        * ``residuals`` / ``out_slots``: member i adds its output to
+          ``residuals[i]`` (fp32) and writes the tile sums of the new residual's
+          squares to ``out_slots[i]`` instead of producing an output tensor.
+
+        No reference counterpart: the reference runs these element-wise steps as
+        separate torch operations (src/nanoquant/runtime/torch_model.py:493-505,
+        625-660)."""
+
+        kinds = {"plain": _native.INPUT_PLAIN, "rmsnorm": _native.INPUT_RMSNORM,
+                 "silu_gate": _native.INPUT_SILU_GATE}
+        if input_kind not in kinds:
+            raise ValueError(f"unknown fused input kind {input_kind!r}")
+        n = len(layers)
+        if len(values) != n or not 1 <= n <= 8:
+            raise ValueError("HIP fused batch needs 1-8 layers with one input each")
+        if len({id(layer) for layer in layers}) != n:
+            raise ValueError("HIP fused batch members must be distinct prepared layers")
+        payloads = [self._payload(layer) for layer in layers]
+        if any(p.tiles is None for p in payloads):
+            raise ValueError("HIP fused batch requires layers prepared with tiled decode")
+        device = payloads[0].device
+        for value, layer in zip(values, layers):
+            _check_value(value, layer.spec, device)
+            if value.numel() != layer.spec.in_features:
+                raise ValueError("HIP fused batch runs exactly one token")
+        if input_kind != "plain" and any(v.dtype != torch.float32 for v in values):
+            raise ValueError("HIP fused rmsnorm / silu_gate inputs are fp32")
+        if len({v.dtype for v in values}) != 1:
+            raise ValueError("HIP fused batch members must share the input dtype")
+
+        def vec(t: torch.Tensor | None, length: int, what: str) -> torch.Tensor:
+            if (t is None or t.device != device or t.dtype != torch.float32 or not t.is_contiguous()
+                    or t.numel() != length):
+                raise ValueError(f"HIP fused {what} must be a contiguous fp32 device vector of {length}")
+            return t
+
+        def ptrs(items: list[torch.Tensor] | None):
+            return None if items is None else (ctypes.c_void_p * n)(*[t.data_ptr() for t in items])
+
+        fusion = _native.DecodeFusion()
+        fusion.input_kind = kinds[input_kind]
+        fusion.eps = float(eps)
+        keep: list = []
+        if input_kind == "rmsnorm":
+            if col_scales is None or len(col_scales) != n:
+                raise ValueError("rmsnorm input needs one column scale per member")
+            for t, layer in zip(col_scales, layers):
+                vec(t, layer.spec.in_features, "column scale")
+            in_features = {layer.spec.in_features for layer in layers}
+            if len(in_features) != 1:
+                raise ValueError("rmsnorm members share one residual width")
+            slots = -(-in_features.pop() // 16)
+            vec(norm_slots, slots, "norm slots")
+            arr = ptrs(col_scales)
+            keep.append(arr)
+            fusion.col_scales = ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p))
+            fusion.norm_slots = norm_slots.data_ptr()
+            fusion.norm_slot_count = slots
+        elif input_kind == "silu_gate":
+            if ups is None or len(ups) != n:
+                raise ValueError("silu_gate input needs one up tensor per member")
+            for t, layer in zip(ups, layers):
+                vec(t.reshape(-1) if t is not None else None, layer.spec.in_features, "up")
+            arr = ptrs(ups)
+            keep.append(arr)
+            fusion.ups = ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p))
+        if residuals is not None:
+            if out_slots is None or len(residuals) != n or len(out_slots) != n:
+                raise ValueError("residual epilogue needs one residual and one slot vector per member")
+            for r, sl, layer in zip(residuals, out_slots, layers):
+                vec(r.reshape(-1), layer.spec.out_features, "residual")
+                vec(sl, -(-layer.spec.out_features // 16), "output slots")
+            ra, sa = ptrs(residuals), ptrs(out_slots)
+            keep += [ra, sa]
+            fusion.residuals = ctypes.cast(ra, ctypes.POINTER(ctypes.c_void_p))
+            fusion.out_slots = ctypes.cast(sa, ctypes.POINTER(ctypes.c_void_p))
+            outs = None
+        else:
+            if output_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                raise ValueError(f"HIP packed output dtype is unsupported: {output_dtype}")
+            if outs is None:
+                outs = [torch.empty((*v.shape[:-1], layer.spec.out_features), dtype=output_dtype, device=device)
+                        for v, layer in zip(values, layers)]
+            for out, value, layer in zip(outs, values, layers):
+                if (tuple(out.shape) != (*value.shape[:-1], layer.spec.out_features) or out.dtype != output_dtype
+                        or not out.is_contiguous()):
+                    raise ValueError("HIP packed output tensor shape, dtype or layout differs")
+        lib = _native.load()
+        sizes = [int(lib.nq_linear_workspace_bytes(ctypes.byref(p.desc), 1)) for p in payloads]
+        if min(sizes) < 0:
+            raise ValueError("HIP packed layer descriptor was rejected")
+        workspaces = [torch.empty(max(b, 1), dtype=torch.uint8, device=device) for b in sizes]
+        desc_ptrs = (ctypes.POINTER(_native.LinearDesc) * n)(*[ctypes.pointer(p.desc) for p in payloads])
+        x_ptrs = (ctypes.c_void_p * n)(*[v.data_ptr() for v in values])
+        y_ptrs = (ctypes.c_void_p * n)(*[(o.data_ptr() if outs is not None else 0) for o in (outs or values)])
+        w_ptrs = (ctypes.c_void_p * n)(*[w.data_ptr() for w in workspaces])
+        w_sizes = (ctypes.c_int64 * n)(*sizes)
+        status = lib.nq_linear_batch_fused(
+            desc_ptrs, n, x_ptrs, _native.dtype_code(values[0].dtype), y_ptrs, _native.dtype_code(output_dtype),
+            w_ptrs, w_sizes, ctypes.byref(fusion), _native.current_stream_handle(device),
+        )
+        _native.check("nq_linear_batch_fused", status)
+        return None if outs is None else list(outs)
+
     def linear_into(
         self,
         value: torch.Tensor,

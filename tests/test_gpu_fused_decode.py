@@ -1,0 +1,155 @@
+"""Fused one-token decode calls (nq_linear_batch_fused) against the oracle's
+fp32 forward of the same element-wise chain: the RMSNorm-folded residual
+input, the SiLU-gated input and the residual epilogue with its per-tile sums
+of squares; and the fused decoder against the unfused one."""
+
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+from nanoquant_amd import synthetic as syn
+from nanoquant_amd.runtime import DecoderShellConfig, HipPackedBackend, PackedDecoder
+from nanoquant_amd.runtime._native import NativeCallError
+from oracle import nq_oracle as orc
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a HIP device"),
+]
+
+REL_L2 = 2e-3  # against the fp32 reference forward
+EPS = 1e-6
+
+
+def _say(*parts) -> None:
+    print("[case]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def _tile_sums(h: torch.Tensor) -> torch.Tensor:
+    """Sums of squares per 16 rows (fp64), the layout the residual epilogue writes."""
+
+    h = h.double().reshape(-1)
+    h = torch.nn.functional.pad(h, (0, (-h.numel()) % 16))
+    return h.view(-1, 16).pow(2).sum(1)
+
+
+def _rmsnorm(h: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    h = h.double()
+    return (h / torch.sqrt(h.pow(2).mean() + EPS) * w.double()).float()
+
+
+def _layers(backend, shapes, seed):
+    states = [syn.synthetic_packed_layer(s, seed=seed + i) for i, s in enumerate(shapes)]
+    return states, [backend.prepare(st, "cuda") for st in states]
+
+
+@pytest.mark.parametrize("roles", [(0, 1, 2), (4, 5)])
+def test_rmsnorm_input_matches_oracle(roles):
+    backend = HipPackedBackend()
+    shapes = [syn.qwen3_8b_layer()[r] for r in roles]
+    _say("rmsnorm input", [s.name for s in shapes])
+    states, layers = _layers(backend, shapes, syn.BASE_SEED + 300)
+    g = torch.Generator().manual_seed(5)
+    h = 3 * torch.randn(4096, generator=g)
+    w = 1 + 0.1 * torch.randn(4096, generator=g)
+    slots = _tile_sums(h).float().cuda()
+    cols = [backend.norm_column_scale(layer, w.cuda()) for layer in layers]
+    kwargs = dict(input_kind="rmsnorm", eps=EPS, col_scales=cols, norm_slots=slots)
+    outs = backend.linear_batch_fused([h.cuda()] * len(layers), layers, **kwargs)
+    again = backend.linear_batch_fused([h.cuda()] * len(layers), layers, **kwargs)
+    xn = _rmsnorm(h, w)
+    unfused = backend.linear_batch([xn.cuda()] * len(layers), layers)
+    for state, y, y2, yu in zip(states, outs, again, unfused):
+        expected = orc.packed_forward(orc.operands_from_state(state), xn[None])[0]
+        err = orc.relative_l2(y, expected)
+        assert err <= REL_L2, (state.spec.name, err)
+        assert orc.relative_l2(y, yu) <= 2e-4, state.spec.name  # same arithmetic up to rounding
+        assert torch.equal(y, y2)
+        print(f"  {state.spec.name} rel_l2={err:.2e}", flush=True)
+
+
+def test_silu_gate_input_matches_oracle():
+    backend = HipPackedBackend()
+    shape = syn.qwen3_8b_layer()[6]
+    _say("silu gate input", shape.name)
+    (state,), (layer,) = _layers(backend, [shape], syn.BASE_SEED + 310)
+    g = torch.Generator().manual_seed(6)
+    gate = 2 * torch.randn(12288, generator=g)
+    up = torch.randn(12288, generator=g)
+    (y,) = backend.linear_batch_fused([gate.cuda()], [layer], input_kind="silu_gate", ups=[up.cuda()])
+    act = (gate.double() * torch.sigmoid(gate.double()) * up.double()).float()
+    expected = orc.packed_forward(orc.operands_from_state(state), act[None])[0]
+    err = orc.relative_l2(y, expected)
+    assert err <= REL_L2, err
+    print(f"  rel_l2={err:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("role", [3, 6])
+def test_residual_epilogue_adds_and_writes_tile_sums(role):
+    backend = HipPackedBackend()
+    shape = syn.qwen3_8b_layer()[role]
+    _say("residual epilogue", shape.name)
+    (state,), (layer,) = _layers(backend, [shape], syn.BASE_SEED + 320)
+    x = syn.synthetic_activations(1, shape.in_features, seed=7)[0]
+    r0 = 4 * torch.randn(shape.out_features, generator=torch.Generator().manual_seed(8))
+    r = r0.cuda()
+    slots = torch.full((-(-shape.out_features // 16),), -1.0, device="cuda")
+    kind = "plain" if role == 3 else "silu_gate"
+    ups = None if role == 3 else [torch.ones(shape.in_features, device="cuda")]
+    value = x.cuda() if role == 3 else x.float().cuda()
+    ret = backend.linear_batch_fused([value], [layer], input_kind=kind, ups=ups, residuals=[r], out_slots=[slots])
+    assert ret is None
+    act = x.float() if role == 3 else (x.double() * torch.sigmoid(x.double())).float()
+    expected = orc.packed_forward(orc.operands_from_state(state), act[None])[0]
+    err = orc.relative_l2((r.cpu() - r0), expected)
+    assert err <= REL_L2, err
+    assert torch.allclose(slots.cpu().double(), _tile_sums(r.cpu()), rtol=1e-5, atol=1e-3)
+
+
+def test_fused_calls_reject_what_they_do_not_cover():
+    backend = HipPackedBackend()
+    shape = syn.qwen3_8b_layer()[0]
+    state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 330, salient=4)
+    layer = backend.prepare(state, "cuda")
+    h = torch.randn(4096, device="cuda")
+    col = backend.norm_column_scale(layer, torch.ones(4096, device="cuda"))
+    slots = _tile_sums(h).float().cuda()
+    with pytest.raises(NativeCallError):  # salient columns read the raw input
+        backend.linear_batch_fused([h], [layer], input_kind="rmsnorm", col_scales=[col], norm_slots=slots)
+    with pytest.raises(ValueError):  # one token only
+        backend.linear_batch_fused([torch.randn(2, 4096, device="cuda")], [layer])
+
+
+SMALL = DecoderShellConfig(layers=3, hidden=256, intermediate=768, q_heads=4, kv_heads=2, head_dim=64, vocab=1000)
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+def test_fused_decoder_matches_unfused(act):
+    weights = syn.synthetic_decoder(SMALL, seed=syn.BASE_SEED + 340, random_norms=True)
+    prompt = torch.randint(0, SMALL.vocab, (20,), generator=torch.Generator().manual_seed(9)).cuda()
+    runs = {}
+    for fuse in (True, False):
+        decoder = PackedDecoder(SMALL, weights, device="cuda", max_positions=64, activation_dtype=act,
+                                cache_dtype=torch.float32, fuse_decode=fuse)
+        assert decoder.fuse_decode == fuse
+        logits = []
+        tokens = decoder.generate_greedy(prompt, 8, use_graph=False)
+        runs[fuse] = tokens.tolist()
+        decoder.reset()
+        decoder.prefill(prompt)
+        bufs = decoder._decode_bufs or decoder._buffers(1)
+        decoder._decode_bufs = bufs
+        for token in runs[fuse][:4]:
+            decoder.ids.fill_(token)
+            decoder._forward(decoder.ids, bufs)
+            decoder.position += 1
+            logits.append(decoder.logits.clone())
+        runs[(fuse, "logits")] = logits
+    tol = 2e-3 if act == torch.float32 else 2e-2
+    for a, b in zip(runs[(True, "logits")], runs[(False, "logits")]):
+        assert orc.relative_l2(a, b) <= tol
+    assert runs[True][:3] == runs[False][:3]
