@@ -630,15 +630,17 @@ __device__ __forceinline__ void load_slots(v4f (&sl)[kSlotVecs], const float* __
     }
 }
 
-// Gated kind: v = silu(v) * up (the arithmetic of the separate SiLU-product
-// kernel); other kinds leave v unchanged.
+// Gated kind: v = silu(v) * up = v * up / (1 + e^-v), with the hardware
+// exponential and reciprocal (a few ulp; the staging then rounds to 15 bits
+// per chunk); other kinds leave v unchanged.
 template <int AK, int TOK, int TW>
 __device__ __forceinline__ void gate_values(const S1Regs<AK, TOK, TW>& r, int t, int run, float (&v)[4]) {
     if constexpr (AK == kActGatedF32) {
         float up[4];
         run_values<AK, NQ_DTYPE_F32>(r.x2[t][run], NQ_DTYPE_F32, up);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(v[i] / (1.0f + expf(-v[i])), up[i]);
+        for (int i = 0; i < 4; ++i)
+            v[i] = v[i] * up[i] * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v[i] * -1.4426950408889634f));
     }
 }
 

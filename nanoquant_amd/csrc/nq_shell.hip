@@ -354,16 +354,18 @@ __device__ __forceinline__ float cache_value(uint32_t bits16) {
 // Dot product of one staged K row with the query (both D long).
 template <int D, int CT>
 __device__ __forceinline__ float k_row_dot(const char* __restrict__ kr, const float* __restrict__ qw) {
-    float acc = 0.0f;
+    // Four accumulators (dimensions d mod 4), combined at the end: four short
+    // dependency chains instead of one of length D.
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
     if constexpr (CT == NQ_DTYPE_F32) {
 #pragma unroll 8
         for (int d = 0; d < D; d += 4) {
             const float4 kk = *reinterpret_cast<const float4*>(kr + 4 * d);
             const float4 qq = *reinterpret_cast<const float4*>(qw + d);
-            acc = fmaf(kk.x, qq.x, acc);
-            acc = fmaf(kk.y, qq.y, acc);
-            acc = fmaf(kk.z, qq.z, acc);
-            acc = fmaf(kk.w, qq.w, acc);
+            a0 = fmaf(kk.x, qq.x, a0);
+            a1 = fmaf(kk.y, qq.y, a1);
+            a2 = fmaf(kk.z, qq.z, a2);
+            a3 = fmaf(kk.w, qq.w, a3);
         }
     } else {
 #pragma unroll 4
@@ -371,17 +373,17 @@ __device__ __forceinline__ float k_row_dot(const char* __restrict__ kr, const fl
             const uint4 u = *reinterpret_cast<const uint4*>(kr + 2 * d);
             const float4 qa = *reinterpret_cast<const float4*>(qw + d);
             const float4 qb = *reinterpret_cast<const float4*>(qw + d + 4);
-            acc = fmaf(cache_value<CT>(u.x & 0xffffu), qa.x, acc);
-            acc = fmaf(cache_value<CT>(u.x >> 16), qa.y, acc);
-            acc = fmaf(cache_value<CT>(u.y & 0xffffu), qa.z, acc);
-            acc = fmaf(cache_value<CT>(u.y >> 16), qa.w, acc);
-            acc = fmaf(cache_value<CT>(u.z & 0xffffu), qb.x, acc);
-            acc = fmaf(cache_value<CT>(u.z >> 16), qb.y, acc);
-            acc = fmaf(cache_value<CT>(u.w & 0xffffu), qb.z, acc);
-            acc = fmaf(cache_value<CT>(u.w >> 16), qb.w, acc);
+            a0 = fmaf(cache_value<CT>(u.x & 0xffffu), qa.x, a0);
+            a1 = fmaf(cache_value<CT>(u.x >> 16), qa.y, a1);
+            a2 = fmaf(cache_value<CT>(u.y & 0xffffu), qa.z, a2);
+            a3 = fmaf(cache_value<CT>(u.y >> 16), qa.w, a3);
+            a0 = fmaf(cache_value<CT>(u.z & 0xffffu), qb.x, a0);
+            a1 = fmaf(cache_value<CT>(u.z >> 16), qb.y, a1);
+            a2 = fmaf(cache_value<CT>(u.w & 0xffffu), qb.z, a2);
+            a3 = fmaf(cache_value<CT>(u.w >> 16), qb.w, a3);
         }
     }
-    return acc;
+    return (a0 + a1) + (a2 + a3);
 }
 
 // E consecutive cache elements (E = D / 64, lane's dimensions) as fp32.
@@ -511,41 +513,46 @@ __global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__
     const int h = blockIdx.x;
     const int64_t t = blockIdx.y;
     const int d = threadIdx.x;
-    const int64_t pt = static_cast<int64_t>(position[0]) + t;
     const int64_t o = (t * q_heads + h) * D + d;
-    if (pt < 0 || pt >= max_positions) {
-        nq::store_f32_as(out, odt, o, 0.0f);
-        return;
-    }
-    const int nb = static_cast<int>(pt / block_rows) + 1;
     const int64_t p0 = attn_part_index(t, h, 0, q_heads, blocks);
     // Rounds of kMergeRound blocks: every load of a round is issued before any
-    // use (addresses clamped to the last block, extra blocks weighted 0), and
-    // rounds combine with a running max.
-    float mrun = -INFINITY, lsum = 0.0f, acc = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += kMergeRound) {
-        float mb[kMergeRound], lb[kMergeRound], ab[kMergeRound];
+    // use, the first round before the position is read (block indices clamped
+    // to the grid's blocks; blocks past the position weigh 0), and rounds
+    // combine with a running max.
+    float mb[kMergeRound], lb[kMergeRound], ab[kMergeRound];
+    const auto load_round = [&](const int b0, const int last) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < kMergeRound; ++i) {
-            const int64_t pb = p0 + (b0 + i < nb ? b0 + i : nb - 1);
+            const int64_t pb = p0 + (b0 + i < last ? b0 + i : last);
             mb[i] = part_ml[2 * pb];
             lb[i] = part_ml[2 * pb + 1];
             ab[i] = part_acc[pb * D + d];
         }
+    };
+    load_round(0, blocks - 1);
+    const int64_t pt = static_cast<int64_t>(position[0]) + t;
+    const bool in_range = pt >= 0 && pt < max_positions;  // uniform
+    const int nb = in_range ? static_cast<int>(pt / block_rows) + 1 : 1;
+    float mrun = -INFINITY, lsum = 0.0f, acc = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += kMergeRound) {
+        if (b0 > 0) load_round(b0, nb - 1);
         float mnew = mrun;
 #pragma unroll
-        for (int i = 0; i < kMergeRound; ++i) mnew = fmaxf(mnew, mb[i]);
+        for (int i = 0; i < kMergeRound; ++i) mnew = b0 + i < nb ? fmaxf(mnew, mb[i]) : mnew;
         const float keep = expf(mrun - mnew);  // 0 in the first round
         lsum *= keep;
         acc *= keep;
 #pragma unroll
         for (int i = 0; i < kMergeRound; ++i) {
-            const float f = b0 + i < nb ? expf(mb[i] - mnew) : 0.0f;
-            lsum = fmaf(lb[i], f, lsum);
-            acc = fmaf(ab[i], f, acc);
+            if (b0 + i < nb) {  // a select: slots past the position may hold anything
+                const float f = expf(mb[i] - mnew);
+                lsum = fmaf(lb[i], f, lsum);
+                acc = fmaf(ab[i], f, acc);
+            }
         }
         mrun = mnew;
     }
+    if (!in_range) acc = 0.0f, lsum = 1.0f;
     nq::store_f32_as(out, odt, o, acc / lsum);
 }
 
@@ -692,16 +699,30 @@ __global__ __launch_bounds__(G * kWave) void k_decode_attention(
     float* pw = ps + w * kSeqBlock;
     pw[lane] = pj;
     __builtin_amdgcn_wave_barrier();
+    // P.V over the scored rows in groups of four, one accumulator per row of
+    // the group (four short dependency chains), combined at the end; rows past
+    // `rows` read row 0 with weight 0.
+    float acc4[4][E];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc4[u][e] = 0.0f;
+    for (int r0 = 0; r0 < rows; r0 += 4) {
+        float pr[4], vv[4][E];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = r0 + u < rows ? r0 + u : 0;
+            pr[u] = r0 + u < rows ? pw[r] : 0.0f;
+            load_v<E, CT>(vlds + r * VRB + lane * E * EB, vv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < E; ++e) acc4[u][e] = fmaf(pr[u], vv[u][e], acc4[u][e]);
+    }
     float acc[E];
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] = 0.0f;
-    for (int r = 0; r < rows; ++r) {
-        const float pr = pw[r];
-        float vv[E];
-        load_v<E, CT>(vlds + r * VRB + lane * E * EB, vv);
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[e] = fmaf(pr, vv[e], acc[e]);
-    }
+    for (int e = 0; e < E; ++e) acc[e] = (acc4[0][e] + acc4[1][e]) + (acc4[2][e] + acc4[3][e]);
     if (!live) return;
     const int h = g * G + w;
     const int64_t pi = attn_part_index(0, h, s, q_heads, blocks);
