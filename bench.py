@@ -281,10 +281,10 @@ FP16_DENSE_PEAK_TFLOPS = 2500.0
 
 
 def prefill_sweep(token_counts, steps: int, warmup: int) -> dict:
-    """Config: the seven Llama-3-8B linears (~0.8 bpw) at each token count, each
-    linear launched eagerly on the current stream; events bracket `steps`
-    repetitions of the whole layer. TFLOP/s counts the two sign GEMMs
-    (2*M*(in*r + r*out)) against the fp16 dense MFMA peak."""
+    """Config: the seven Llama-3-8B linears (~0.8 bpw) at each token count, one
+    layer pass (every linear once) captured in a HIP graph so host launch costs
+    stay out of the timing; events bracket `steps` replays. TFLOP/s counts the
+    two sign GEMMs (2*M*(in*r + r*out)) against the fp16 dense MFMA peak."""
 
     import torch
 
@@ -306,15 +306,21 @@ def prefill_sweep(token_counts, steps: int, warmup: int) -> dict:
             for s, layer, out in zip(shapes, layers, outs):
                 backend.linear_into(xs[s.in_features], layer, out=out)
 
-        for _ in range(warmup):
-            layer_pass()
-        torch.cuda.synchronize()
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(steps):
-            layer_pass()
-        stop.record()
-        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            layer_pass()  # allocates the calls' workspaces outside the capture
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                layer_pass()
+            for _ in range(warmup):
+                graph.replay()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(side)
+            for _ in range(steps):
+                graph.replay()
+            stop.record(side)
+        stop.synchronize()
         ms = start.elapsed_time(stop) / steps
         flops = sum(2 * tokens * (s.in_features * s.rank + s.rank * s.out_features) for s in shapes)
         tflops = flops / (ms * 1e-3) / 1e12
