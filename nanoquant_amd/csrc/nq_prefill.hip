@@ -326,28 +326,82 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
     __syncthreads();
     const int64_t col = n0 + 64 * wn + lane;
     const int64_t row0 = m0 + 64 * wm;
-    const int rows = static_cast<int>(g.m - row0 < 64 ? g.m - row0 : 64);
-    if (col >= g.n) return;
+    const int rows = __builtin_amdgcn_readfirstlane(static_cast<int>(g.m - row0 < 64 ? g.m - row0 : 64));
+    if (rows <= 0) return;  // the whole wave is past the last token
+    const bool col_ok = col < g.n;
     if (g.partial) {
+        if (!col_ok) return;
         float* dst = g.partial + static_cast<int64_t>(blockIdx.z) * g.m * g.n;
         for (int e = 0; e < rows; ++e) dst[(row0 + e) * g.n + col] = park[e * kParkStride + lane];
         return;
     }
-    const float cs = nq::load_f32(g.col_scale, g.col_scale_dtype, col);
-    const float bias = g.bias ? nq::load_f32(g.bias, g.bias_dtype, col) : 0.0f;
+    // Every lane stays active up to the stores: lane e holds values of row
+    // row0 + e that other lanes read with readlane. 1 / row_scale is exact
+    // (row_scale is a normal power of two; exponent field 254 - E), so the
+    // row loop multiplies by it and waits on no memory.
+    const int64_t col_c = col_ok ? col : g.n - 1;
+    const int lane_row = lane < rows ? lane : rows - 1;
+    const float inv_lane =
+        __uint_as_float((254u << 23) - (__float_as_uint(g.row_scale[row0 + lane_row]) & 0x7f800000u));
+    const float cs = nq::load_f32(g.col_scale, g.col_scale_dtype, col_c);
+    const float bias = g.bias ? nq::load_f32(g.bias, g.bias_dtype, col_c) : 0.0f;
+    auto inv_of = [&](int e) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_lane), e)); };
     const int64_t salient = g.salient_count;
-    for (int e = 0; e < rows; ++e) {
-        const int64_t row = row0 + e;
-        // row_scale is a normal power of two: its reciprocal (exponent field
-        // 254 - E) is exact, and so is multiplying by it.
-        const float inv = __uint_as_float((254u << 23) - (__float_as_uint(g.row_scale[row]) & 0x7f800000u));
-        float v = park[e * kParkStride + lane] * inv * cs + bias;
-        for (int64_t k = 0; k < salient; ++k) {
-            float w = nq::load_f32(g.salient_values, g.salient_dtype, col * salient + k);
+    float v[64];
+#pragma unroll
+    for (int e = 0; e < 64; ++e) v[e] = park[e * kParkStride + lane] * inv_of(e) * cs + bias;
+    // Salient columns (none for most layers): v[e] for the wave's 64 rows
+    // stays in registers while the columns are added in index order, eight at
+    // a time. Lane e loads x[row0 + e, idx_k] and the row loop takes it with
+    // readlane, so a batch of eight columns costs one round of loads.
+    for (int64_t k0 = 0; k0 < salient; k0 += 8) {
+        float xk[8], wk[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t k = k0 + j < salient ? k0 + j : salient - 1;
+            const int64_t idx = g.salient_indices[k];
+            xk[j] = nq::load_f32(g.x, g.x_dtype, (row0 + lane_row) * g.in + idx);
+            float w = nq::load_f32(g.salient_values, g.salient_dtype, col_c * salient + k);
             if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
-            v += w * nq::load_f32(g.x, g.x_dtype, row * g.in + g.salient_indices[k]);
+            wk[j] = k0 + j < salient ? w : 0.0f;
         }
-        nq::store_f32_as(g.out, g.out_dtype, row * g.n + col, v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (k0 + j < salient) {
+#pragma unroll
+                for (int e = 0; e < 64; ++e)
+                    v[e] += wk[j] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xk[j]), e));
+            }
+        }
+    }
+    if (!col_ok) return;
+    // One switch on the output dtype, then 64 predicated stores with
+    // constant register indices.
+    const int64_t out0 = row0 * g.n + col;
+    switch (g.out_dtype) {
+        case NQ_DTYPE_F32: {
+            float* o = static_cast<float*>(g.out) + out0;
+#pragma unroll
+            for (int e = 0; e < 64; ++e)
+                if (e < rows) o[e * g.n] = v[e];
+            break;
+        }
+        case NQ_DTYPE_F16: {
+            _Float16* o = static_cast<_Float16*>(g.out) + out0;
+#pragma unroll
+            for (int e = 0; e < 64; ++e)
+                if (e < rows) o[e * g.n] = static_cast<_Float16>(v[e]);
+            break;
+        }
+        case NQ_DTYPE_BF16: {
+            uint16_t* o = static_cast<uint16_t*>(g.out) + out0;
+#pragma unroll
+            for (int e = 0; e < 64; ++e)
+                if (e < rows) o[e * g.n] = nq::f32_to_bf16_bits(v[e]);
+            break;
+        }
+        default:
+            break;
     }
 }
 
