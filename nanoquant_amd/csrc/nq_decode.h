@@ -8,6 +8,9 @@ namespace nq {
 // Words of the sync header in front of the V tiles in a tiles buffer.
 int64_t tiles_header_words();
 
+// Word index, within that header, of max|s_mid| (fp32 bits, written by nq_prepare_tiles).
+int64_t tiles_max_mid_word();
+
 // Extra workspace bytes the tiled decode path needs for `tokens` slots.
 int64_t decode_scratch_bytes(const nq_linear_desc* d, int64_t tokens);
 

@@ -302,6 +302,8 @@ namespace nq {
 
 int64_t tiles_header_words() { return kHeaderWords; }
 
+int64_t tiles_max_mid_word() { return line_word(kMiscLine) + kMiscMaxMid; }
+
 int64_t decode_scratch_bytes(const nq_linear_desc* d, int64_t tokens) {
     if (!d->tiles) return 0;
     return scratch_bytes(geometry(d->in_features, d->out_features, d->rank), tokens);

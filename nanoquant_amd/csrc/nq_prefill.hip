@@ -2,11 +2,16 @@
 // two dense sign GEMMs on v_mfma_f32_32x32x16_f16.
 //
 //   k_prep_rows:  xs16[t, :] = fp16(x[t, :] * s_in * 2^e_t)       (exact power of
-//                 two per row from max |x * s_in|, so fp16 cannot overflow)
-//   GEMM 1:       lm[t, r]   = s_mid[r] * (xs16 · V±1ᵀ)[t, r] / 2^e_t   (fp32)
-//   k_prep_rows:  lm16[t, :] = fp16(lm[t, :] * 2^f_t)
+//                 two per row from max |x * s_in|, so fp16 cannot overflow),
+//                 and 2^f_t from the bound |lm[t, r]| <= max|s_mid| * Σ_i |x s_in|
+//   GEMM 1:       lm16[t, r] = fp16(2^f_t * s_mid[r] * (xs16 · V±1ᵀ)[t, r] / 2^e_t)
 //   GEMM 2:       y[t, o]    = s_out[o] * (lm16 · U±1ᵀ)[t, o] / 2^f_t
 //                              + Σ_k x[t, idx_k] W_sal[o, k] (* scale_k) + bias[o]
+//
+// The bound puts every lm16 value at or below 2^14, inside the fp16 range,
+// and values far below the bound keep fp16's relative precision down to
+// 2^-14 (they lie within a few binades of it for any real row), so the
+// rank intermediate never takes a pass of its own.
 //
 // The sign operand comes straight from the decode tile layout (16-row tiles;
 // in 128-column block kb = 4c + d a lane's word d of chunk c holds, at bit
@@ -105,11 +110,17 @@ __device__ __forceinline__ void load8(const void* __restrict__ p, int dtype, boo
 // One workgroup per row: out16[t, swizzle4(c)] = fp16(a[t, c] * s[c] * scale_t)
 // for c < cols, zero for cols <= c < cols_pad; scale_out[t] = scale_t. Each
 // thread takes 8 consecutive columns per step (one 16-byte store of fp16).
+// With `max_mid_bits` (fp32 bits of max|s_mid|) it also writes
+// bound_scale_out[t], the power of two that puts max|s_mid| * Σ_c |a s| at
+// or below 2^14: the scale of the row's rank intermediate.
 __global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ act, int act_dtype, int64_t ld,
                                                       const void* __restrict__ colscale, int colscale_dtype,
                                                       int64_t cols, int64_t cols_pad, int vec,
-                                                      _Float16* __restrict__ out16, float* __restrict__ scale_out) {
+                                                      _Float16* __restrict__ out16, float* __restrict__ scale_out,
+                                                      const uint32_t* __restrict__ max_mid_bits,
+                                                      float* __restrict__ bound_scale_out) {
     __shared__ float wmax[kBlock / 64];
+    __shared__ float wsum[kBlock / 64];
     const int64_t t = blockIdx.x;
     auto values = [&](int64_t c, float (&v)[8]) {
         load8(act, act_dtype, vec != 0, t * ld, c, cols, v);
@@ -122,17 +133,19 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ a
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = c + i < cols ? v[i] : 0.0f;
     };
-    float m = 0.0f;
+    float m = 0.0f, l1 = 0.0f;
     for (int64_t c = 8 * threadIdx.x; c < cols; c += 8 * kBlock) {
         float v[8];
         values(c, v);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i]));
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, fabsf(v[i])), l1 += fabsf(v[i]);
     }
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off)), l1 += __shfl_xor(l1, off);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m, wsum[threadIdx.x >> 6] = l1;
     __syncthreads();
     const float scale = range_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+    if (max_mid_bits && threadIdx.x == 0)
+        bound_scale_out[t] = range_scale(__uint_as_float(*max_mid_bits) * ((wsum[0] + wsum[1]) + (wsum[2] + wsum[3])));
     for (int64_t c = 8 * threadIdx.x; c < cols_pad; c += 8 * kBlock) {
         float v[8];
         if (c < cols) values(c, v);
@@ -205,8 +218,11 @@ struct GemmArgs {
     int scale_dtype;
     const void* bias;
     int bias_dtype;
-    void* out;                // [M, n]
+    void* out;                // [M, n], or fp16 [M, out_ld] with out_scale
     int out_dtype;
+    const float* out_scale;   // [M] or null: write fp16(v * out_scale[t]) at column
+                              // swizzle4(c) of an out_ld-wide row, zero for n <= c < out_ld
+    int64_t out_ld;
     int64_t k_per_split;      // K blocks per grid-z slice
     float* partial;           // [gridDim.z][M][n] raw accumulators, or null (direct epilogue)
 };
@@ -374,6 +390,18 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
             }
         }
     }
+    if (g.out_scale) {
+        // The rank intermediate for GEMM 2: fp16, row-scaled, swizzled, with
+        // the padding columns up to out_ld written as zeros.
+        const float os_lane = g.out_scale[row0 + lane_row];
+        _Float16* o = static_cast<_Float16*>(g.out) + row0 * g.out_ld + swizzle4(col);
+#pragma unroll
+        for (int e = 0; e < 64; ++e) {
+            const float os = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(os_lane), e));
+            if (e < rows) o[e * g.out_ld] = col_ok ? static_cast<_Float16>(v[e] * os) : static_cast<_Float16>(0.0f);
+        }
+        return;
+    }
     if (!col_ok) return;
     // One switch on the output dtype, then 64 predicated stores with
     // constant register indices.
@@ -407,17 +435,25 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
 
 // Split-K epilogue, one thread per output element (t, c):
 // out[t, c] = (Σ_z partial[z][t][c]) / row_scale[t] * col_scale[c] (+ bias
-// + salient columns for GEMM 2), the slices summed in z order.
+// + salient columns for GEMM 2), the slices summed in z order. With
+// out_scale the threads cover [M, out_ld] and write the fp16 rank
+// intermediate as the direct epilogue does (zeros past column n).
 __global__ __launch_bounds__(kBlock) void k_reduce_splits(int splits, const GemmArgs g) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (i >= g.m * g.n) return;
-    const int64_t t = i / g.n, c = i - t * g.n;
+    const int64_t width = g.out_scale ? g.out_ld : g.n;
+    if (i >= g.m * width) return;
+    const int64_t t = i / width, c = i - t * width;
     const int64_t plane = g.m * g.n;
+    if (g.out_scale && c >= g.n) {
+        static_cast<_Float16*>(g.out)[t * g.out_ld + swizzle4(c)] = static_cast<_Float16>(0.0f);
+        return;
+    }
+    const int64_t pi = t * g.n + c;
     float part[8];
     float v = 0.0f;
     for (int z0 = 0; z0 < splits; z0 += 8) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) part[j] = z0 + j < splits ? g.partial[(z0 + j) * plane + i] : 0.0f;
+        for (int j = 0; j < 8; ++j) part[j] = z0 + j < splits ? g.partial[(z0 + j) * plane + pi] : 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) v += part[j];
     }
@@ -428,7 +464,10 @@ __global__ __launch_bounds__(kBlock) void k_reduce_splits(int splits, const Gemm
         if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
         v += w * nq::load_f32(g.x, g.x_dtype, t * g.in + g.salient_indices[k]);
     }
-    nq::store_f32_as(g.out, g.out_dtype, i, v);
+    if (g.out_scale)
+        static_cast<_Float16*>(g.out)[t * g.out_ld + swizzle4(c)] = static_cast<_Float16>(v * g.out_scale[t]);
+    else
+        nq::store_f32_as(g.out, g.out_dtype, pi, v);
 }
 
 // Tile counts and 128-column block counts of V [rank, in] and U [out, rank]
@@ -472,7 +511,7 @@ Split split_for(int64_t tiles, int64_t k_blocks) {
 }
 
 struct Scratch {
-    int64_t xs16, scale1, lm, lm16, scale2, partial, total;
+    int64_t xs16, scale1, lm16, scale2, partial, total;
     Split s1, s2;
 };
 
@@ -484,8 +523,7 @@ Scratch scratch_layout(const nq_linear_desc* d, int64_t tokens) {
     s.s2 = split_for(mt * ((d->out_features + kBN - 1) / kBN), g.nsc2);
     s.xs16 = 0;
     s.scale1 = s.xs16 + a256(tokens * g.nsc1 * kBK * 2);
-    s.lm = s.scale1 + a256(tokens * 4);
-    s.lm16 = s.lm + a256(tokens * d->rank * 4);
+    s.lm16 = s.scale1 + a256(tokens * 4);
     s.scale2 = s.lm16 + a256(tokens * g.nsc2 * kBK * 2);
     s.partial = s.scale2 + a256(tokens * 4);
     const int64_t p1 = s.s1.slices > 1 ? s.s1.slices * tokens * d->rank : 0;
@@ -518,7 +556,6 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     char* ws = static_cast<char*>(scratch);
     auto* xs16 = reinterpret_cast<_Float16*>(ws + sl.xs16);
     auto* scale1 = reinterpret_cast<float*>(ws + sl.scale1);
-    auto* lm = reinterpret_cast<float*>(ws + sl.lm);
     auto* lm16 = reinterpret_cast<_Float16*>(ws + sl.lm16);
     auto* scale2 = reinterpret_cast<float*>(ws + sl.scale2);
     auto* partial = reinterpret_cast<float*>(ws + sl.partial);
@@ -527,10 +564,10 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     auto aligned = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
     // Vector row loads: 8 elements per load, 16-byte aligned rows.
     const int vec1_ok = (d->in_features % 8 == 0 && aligned(x, 16) && aligned(d->scale_pre, 16)) ? 1 : 0;
-    const int vec2 = (d->rank % 8 == 0 && aligned(lm, 16)) ? 1 : 0;
 
     hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, x, x_dtype, d->in_features, d->scale_pre,
-                       d->scale_dtype, d->in_features, geo.nsc1 * kBK, vec1_ok, xs16, scale1);
+                       d->scale_dtype, d->in_features, geo.nsc1 * kBK, vec1_ok, xs16, scale1,
+                       base + tiles_max_mid_word(), scale2);
     GemmArgs g1{};
     g1.a = xs16;
     g1.m = tokens;
@@ -541,20 +578,20 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     g1.row_scale = scale1;
     g1.col_scale = d->scale_mid;
     g1.col_scale_dtype = d->scale_dtype;
-    g1.out = lm;
-    g1.out_dtype = NQ_DTYPE_F32;
+    g1.out = lm16;
+    g1.out_dtype = NQ_DTYPE_F16;
+    g1.out_scale = scale2;
+    g1.out_ld = geo.nsc2 * kBK;  // GEMM 1's column blocks cover exactly this width
     g1.k_per_split = sl.s1.k_per_split;
     g1.partial = sl.s1.slices > 1 ? partial : nullptr;
     const dim3 grid1(static_cast<unsigned>((d->rank + kBN - 1) / kBN), static_cast<unsigned>((tokens + kBM - 1) / kBM),
                      static_cast<unsigned>(sl.s1.slices));
     hipLaunchKernelGGL(k_sign_gemm, grid1, dim3(kBlock), 0, stream, g1);
     if (sl.s1.slices > 1) {
-        const dim3 grid(static_cast<unsigned>((tokens * d->rank + kBlock - 1) / kBlock));
+        const dim3 grid(static_cast<unsigned>((tokens * g1.out_ld + kBlock - 1) / kBlock));
         hipLaunchKernelGGL(k_reduce_splits, grid, dim3(kBlock), 0, stream, static_cast<int>(sl.s1.slices), g1);
     }
 
-    hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, lm, NQ_DTYPE_F32, d->rank, nullptr, 0, d->rank,
-                       geo.nsc2 * kBK, vec2, lm16, scale2);
     GemmArgs g2{};
     g2.a = lm16;
     g2.m = tokens;
