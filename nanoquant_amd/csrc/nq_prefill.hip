@@ -489,25 +489,38 @@ Geometry geometry(const nq_linear_desc* d) {
 
 int64_t a256(int64_t n) { return (n + 255) & ~int64_t(255); }
 
-// Split of a GEMM with `tiles` (token, sign-row) tiles over K blocks: enough
-// slices to give the GPU about kTargetGroups workgroups, each slice at least
-// kMinSliceBlocks K blocks (the partials cost M x N x 4 bytes per slice).
-constexpr int64_t kTargetGroups = 512;
-constexpr int64_t kMinSliceBlocks = 4;
+// Split of a GEMM with `tiles` (token, sign-row) tiles over K blocks, from a
+// latency model of the K loop (fitted to kernel traces on MI355X): a K step
+// costs about one memory round trip, kStepNs, while the GPU holds every
+// workgroup at once (kResident: two per CU, bound by LDS); workgroups beyond
+// that run in further rounds; a split adds the reduce launch and the
+// partials' write and read (M x N x 4 bytes per slice, mostly served by the
+// last-level cache). Slices hold at least kMinSliceBlocks K blocks.
+constexpr int64_t kResident = 512;
+constexpr int64_t kMinSliceBlocks = 2;
+constexpr double kStepNs = 2000.0;
+constexpr double kReduceNs = 3000.0;
+constexpr double kPartialBytesPerNs = 8000.0;
 
 struct Split {
     int64_t slices, k_per_split;
 };
 
-Split split_for(int64_t tiles, int64_t k_blocks) {
-    int64_t want = (kTargetGroups + tiles - 1) / tiles;
-    const int64_t most = k_blocks / kMinSliceBlocks;
-    want = want > most ? most : want;
-    want = want < 1 ? 1 : want;
-    Split s;
-    s.k_per_split = (k_blocks + want - 1) / want;
-    s.slices = (k_blocks + s.k_per_split - 1) / s.k_per_split;
-    return s;
+Split split_for(int64_t tiles, int64_t k_blocks, int64_t tokens, int64_t n) {
+    Split best{1, k_blocks};
+    double best_ns = -1.0;
+    const int64_t most = k_blocks / kMinSliceBlocks > 1 ? k_blocks / kMinSliceBlocks : 1;
+    for (int64_t want = 1; want <= most; ++want) {
+        Split s;
+        s.k_per_split = (k_blocks + want - 1) / want;
+        s.slices = (k_blocks + s.k_per_split - 1) / s.k_per_split;
+        const int64_t rounds = (tiles * s.slices + kResident - 1) / kResident;
+        double ns = static_cast<double>(rounds * (s.k_per_split + 1)) * kStepNs;
+        if (s.slices > 1)
+            ns += kReduceNs + 2.0 * static_cast<double>(s.slices * tokens * n * 4) / kPartialBytesPerNs;
+        if (best_ns < 0.0 || ns < best_ns) best = s, best_ns = ns;
+    }
+    return best;
 }
 
 struct Scratch {
@@ -519,8 +532,8 @@ Scratch scratch_layout(const nq_linear_desc* d, int64_t tokens) {
     const Geometry g = geometry(d);
     const int64_t mt = (tokens + kBM - 1) / kBM;
     Scratch s{};
-    s.s1 = split_for(mt * ((d->rank + kBN - 1) / kBN), g.nsc1);
-    s.s2 = split_for(mt * ((d->out_features + kBN - 1) / kBN), g.nsc2);
+    s.s1 = split_for(mt * ((d->rank + kBN - 1) / kBN), g.nsc1, tokens, d->rank);
+    s.s2 = split_for(mt * ((d->out_features + kBN - 1) / kBN), g.nsc2, tokens, d->out_features);
     s.xs16 = 0;
     s.scale1 = s.xs16 + a256(tokens * g.nsc1 * kBK * 2);
     s.lm16 = s.scale1 + a256(tokens * 4);
