@@ -35,6 +35,10 @@ def _g(seed: int) -> torch.Generator:
     return torch.Generator().manual_seed(seed)
 
 
+def _say(*parts) -> None:
+    print("[case]", *parts, flush=True)
+
+
 # --------------------------------------------------------------------------- kernels
 def test_embedding_gathers_rows_exactly():
     table = (0.02 * torch.randn(1000, 256, generator=_g(1))).to(torch.bfloat16)
@@ -148,7 +152,7 @@ def test_attention(tokens, start, q_heads, kv_heads, head_dim, cache_dtype):
         (32, 8, 128, torch.bfloat16, 640, 0),
         (32, 8, 128, torch.bfloat16, 640, 577),
         (32, 8, 128, torch.bfloat16, 640, 639),
-        (32, 8, 128, torch.bfloat16, 2500, 2300),  # three 1024-row ranges and the merge kernel
+        (32, 8, 128, torch.bfloat16, 2500, 2300),  # 36 blocks: three merge rounds
         (16, 8, 128, torch.float16, 300, 130),
         (8, 8, 64, torch.float32, 200, 150),
         (64, 8, 128, torch.bfloat16, 1100, 1050),
@@ -185,6 +189,40 @@ def test_decode_attention_fused(q_heads, kv_heads, head_dim, cache_dtype, max_po
     again = ops.launch_decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), k_cache=kc, v_cache=vc,
                                         scaling=head_dim**-0.5, out_dtype=torch.float32, **common)
     assert torch.equal(out, again)
+
+
+def test_decode_attention_workspace_reuse():
+    """One workspace over a run of positions (block edges, a position past
+    the cache, a short context after a long one): partials a call leaves in
+    the workspace never leak into the next, so each call matches the
+    two-kernel sequence on a copy of the cache."""
+    q_heads, kv_heads, head_dim, max_pos = 32, 8, 128, 640
+    g = _g(11)
+    qn = (1 + 0.1 * torch.randn(head_dim, generator=g)).to(DEV)
+    kn = (1 + 0.1 * torch.randn(head_dim, generator=g)).to(DEV)
+    cos, sin = ods.rope_tables(head_dim, 1e6, max_pos)
+    kc = torch.randn(kv_heads, max_pos, head_dim, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(kv_heads, max_pos, head_dim, generator=g).to(torch.bfloat16).to(DEV)
+    need = ops.decode_attention_workspace_bytes(q_heads, kv_heads, head_dim, torch.bfloat16, max_pos)
+    ws = torch.full((need,), 0x7F, dtype=torch.uint8, device=DEV)  # stale bytes, not zeros
+    for p in (0, 63, 64, 130, 639, 640, 5, 577):
+        _say("decode attention workspace reuse", p)
+        q = (3 * torch.randn(q_heads * head_dim, generator=g)).to(DEV)
+        k = (3 * torch.randn(kv_heads * head_dim, generator=g)).to(DEV)
+        v = torch.randn(kv_heads * head_dim, generator=g).to(DEV)
+        position = torch.tensor([p], dtype=torch.int32, device=DEV)
+        common = dict(q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, q_norm=qn, k_norm=kn, eps=1e-6,
+                      cos=cos.to(DEV), sin=sin.to(DEV), position=position)
+        kc2, vc2 = kc.clone(), vc.clone()
+        out = ops.launch_decode_attention(q, k, v, k_cache=kc, v_cache=vc, scaling=head_dim**-0.5,
+                                          out_dtype=torch.float32, workspace=ws, **common)
+        q_rot = ops.launch_qk_norm_rope_cache(q, k, v, k_cache=kc2, v_cache=vc2, **common)
+        out2 = ops.launch_attention(q_rot.view(1, q_heads, head_dim), kc2, vc2, position=position,
+                                    scaling=head_dim**-0.5, out_dtype=torch.float32)
+        assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+        if p >= max_pos:
+            assert torch.count_nonzero(out) == 0
+        assert relative_l2(out.view(1, -1), out2) < 1e-5
 
 
 def test_attention_single_row_returns_value():
