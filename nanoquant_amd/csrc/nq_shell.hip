@@ -190,26 +190,28 @@ __global__ __launch_bounds__(kNormThreads) void k_add_rmsnorm(float* __restrict_
 // d = l + 64 j, so for head_dim >= 128 the rotate-half partner d +- D/2 is
 // element j +- E/2 of the same lane; for head_dim 64 it is lane l ^ 32.
 
-// Element i of an F32 / F16 / BF16 buffer from two unconditional 16-bit loads
-// (the halves of an fp32, or the same half twice): no branch surrounds the
-// load, so a wave issues all of them before waiting on any.
+// Element i of an F32 / F16 / BF16 buffer from one unconditional 32-bit load
+// (the fp32 itself, or the word holding the 16-bit element; the buffer is
+// 4-byte aligned and holds an even number of 16-bit elements): no branch
+// surrounds the load and nothing is derived from it before use, so a wave
+// issues all of them before waiting on any.
 struct RawHalves {
-    uint32_t lo, hi;
+    uint32_t word, shift;
 };
 
 __device__ __forceinline__ RawHalves load_raw(const void* __restrict__ p, int dtype, int64_t i) {
-    const uint16_t* h = static_cast<const uint16_t*>(p);
     const bool wide = dtype == NQ_DTYPE_F32;
     RawHalves r;
-    r.lo = h[wide ? 2 * i : i];
-    r.hi = h[wide ? 2 * i + 1 : i];
+    r.word = static_cast<const uint32_t*>(p)[wide ? i : i >> 1];
+    r.shift = wide ? 0u : static_cast<uint32_t>(i & 1) << 4;
     return r;
 }
 
 __device__ __forceinline__ float raw_value(const RawHalves& r, int dtype) {
-    const float f32 = __uint_as_float((r.hi << 16) | (r.lo & 0xffffu));
-    const float bf16 = __uint_as_float(r.lo << 16);
-    const float f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.lo)));
+    const uint32_t half = r.word >> r.shift;
+    const float f32 = __uint_as_float(r.word);
+    const float bf16 = __uint_as_float(half << 16);
+    const float f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(half)));
     return dtype == NQ_DTYPE_F32 ? f32 : (dtype == NQ_DTYPE_BF16 ? bf16 : f16);
 }
 
@@ -613,32 +615,38 @@ __global__ __launch_bounds__(G * kWave) void k_decode_attention(
 #pragma unroll
     for (int j = 0; j < E; ++j) vraw[j] = v[static_cast<int64_t>(g) * D + lane + kWave * j];
 
-    // No early exit (it would sink the loads above below the wait for the
-    // position): a block past the position runs the arithmetic of a one-row
-    // block at row0 and stores nothing; the merge ignores it.
-    const int64_t pos = position[0];
+    // The block's K and V rows, loaded whatever the position (rows past the
+    // cache's end reload its last row); rows at or past `cached` go to the
+    // scratch row. The position and its RoPE entries follow the barrier;
+    // nothing is used before all are issued.
     const int64_t row0 = static_cast<int64_t>(s) * kSeqBlock;
-    const bool live = pos >= 0 && pos < max_positions && row0 <= pos;  // uniform
-    const int64_t p = live ? pos : row0;
-    const bool owns_p = live && p < row0 + kSeqBlock;
-    const int rows = live ? static_cast<int>(owns_p ? p - row0 + 1 : kSeqBlock) : 1;  // rows scored
-    const int cached = live ? (owns_p ? rows - 1 : rows) : 0;                         // rows read from the cache
     const int64_t head_row0 = static_cast<int64_t>(g) * max_positions;
-
-    // The block's cached K and V rows and the position's RoPE entries, all
-    // issued before any is used (rows past `cached` reload row 0 and go to
-    // the scratch row).
     u32x4 kp[PER_THREAD], vp[PER_THREAD];
+    const int last_row = static_cast<int>(max_positions - 1 - row0);  // >= 0: the block starts in the cache
     const char* kbase = k_cache + (head_row0 + row0) * VRB;
     const char* vbase = v_cache + (head_row0 + row0) * VRB;
 #pragma unroll
     for (int i = 0; i < PER_THREAD; ++i) {
         const int idx = threadIdx.x + i * G * kWave;
         const int r = idx / PIECES, c = idx % PIECES;
-        const int rr = r < cached ? r : 0;  // row 0 of the block is in range (row0 <= p)
+        const int rr = r < last_row ? r : last_row;
         kp[i] = *reinterpret_cast<const u32x4*>(kbase + rr * VRB + 16 * c);
         vp[i] = *reinterpret_cast<const u32x4*>(vbase + rr * VRB + 16 * c);
     }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // No early exit (it would sink the loads above below the wait for the
+    // position): a block past the position runs the arithmetic of a one-row
+    // block at row0 and stores nothing; the merge ignores it. The position is
+    // read after the scheduling barrier, so every load above is issued before
+    // its (scalar) wait.
+    const int64_t pos = position[0];
+    const bool live = pos >= 0 && pos < max_positions && row0 <= pos;  // uniform
+    const int64_t p = live ? pos : row0;
+    const bool owns_p = live && p < row0 + kSeqBlock;
+    const int rows = live ? static_cast<int>(owns_p ? p - row0 + 1 : kSeqBlock) : 1;  // rows scored
+    const int cached = live ? (owns_p ? rows - 1 : rows) : 0;                         // rows read from the cache
+
     float cs[E], sn[E];
 #pragma unroll
     for (int j = 0; j < E; ++j) {
