@@ -42,7 +42,7 @@ pytestmark = [
     pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a HIP device"),
 ]
 
-REL_L2 = 2e-3  # north-star tolerance against the fp32 reference forward
+REL_L2 = 2e-3  # tolerance of the tiled MFMA paths against the fp32 reference forward
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_fixtures.json").read_text())
 _FLOATS = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -69,8 +69,8 @@ def _tiled(backend) -> bool:
 
 def _assert_parity(backend, actual, expected, case=None):
     """fp32 path: the reference tests' rtol=2e-5/atol=2e-4. Tiled MFMA paths
-    (int8 decode, fp16 prefill): the north-star bar, relative L2 <= 2e-3
-    against the fp32 forward."""
+    (int8 decode, fp16 prefill): relative L2 <= 2e-3 against the fp32
+    forward."""
 
     if _tiled(backend):
         err = orc.relative_l2(actual, expected)
