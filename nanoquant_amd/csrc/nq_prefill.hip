@@ -227,16 +227,23 @@ struct GemmArgs {
     float* partial;           // [gridDim.z][M][n] raw accumulators, or null (direct epilogue)
 };
 
-__global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
+// WM = 2: the four waves form a 2 x 2 grid of 64 x 64 tiles (block tile
+// 128 x 128). WM = 1: they sit side by side, each 128 x 64 (block tile
+// 128 x 256): every expanded sign fragment then serves four A fragments
+// instead of two, for GEMMs with enough blocks to fill the GPU at that size.
+template <int WM>
+__global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmArgs g) {
+    constexpr int II = 4 / WM;            // 32-row A fragments per wave
+    constexpr int BN = 64 * (4 / WM);     // sign rows per block
     __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 1;  // wave row in the 2 x 2 grid
-    const int wn = wave & 1;
+    const int wm = WM == 2 ? wave >> 1 : 0;  // wave row
+    const int wn = WM == 2 ? wave & 1 : wave;  // wave column
     const int h = lane >> 5;   // K half of the 32 x 32 x 16 operands
     const int r = lane & 31;   // A row / B column within a 32-wide fragment
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kBN;
+    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
     const int64_t rt_count = (g.n + kTileRows - 1) / kTileRows;
     // B fragment jj covers sign rows n0 + 64 wn + 32 jj + [0, 32): lane r reads
     // row r of tile (r >> 4) of that pair, from the words of lane groups 2h
@@ -244,9 +251,9 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
     const int64_t rt0 = n0 / kTileRows + 4 * wn + (r >> 4);
     const int wl0 = 16 * (2 * h) + (r & 15), wl1 = wl0 + 16;
 
-    v16f acc[2][2];
+    v16f acc[II][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < II; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
 
@@ -309,7 +316,7 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) b[jj] = expand_signs32(words[jj][0], words[jj][1], m, sign_mask, fp16_one);
 #pragma unroll
-            for (int ii = 0; ii < 2; ++ii) {
+            for (int ii = 0; ii < II; ++ii) {
                 const v8h a = *reinterpret_cast<const v8h*>(&a_lds[(64 * wm + 32 * ii + r) * kAStride + 16 * m + 8 * h]);
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj)
@@ -332,104 +339,115 @@ __global__ __launch_bounds__(kBlock) void k_sign_gemm(const GemmArgs g) {
     // segment is one coalesced 64-wide store and the salient sum joins before
     // the single rounding to the output dtype.
     float* park = reinterpret_cast<float*>(lds) + wave * (64 * kParkStride);
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int q = 0; q < 16; ++q)
-                park[(32 * ii + 8 * (q >> 2) + 4 * h + (q & 3)) * kParkStride + 32 * jj + r] = acc[ii][jj][q];
-    __syncthreads();
-    const int64_t col = n0 + 64 * wn + lane;
-    const int64_t row0 = m0 + 64 * wm;
-    const int rows = __builtin_amdgcn_readfirstlane(static_cast<int>(g.m - row0 < 64 ? g.m - row0 : 64));
-    if (rows <= 0) return;  // the whole wave is past the last token
-    const bool col_ok = col < g.n;
-    if (g.partial) {
-        if (!col_ok) return;
-        float* dst = g.partial + static_cast<int64_t>(blockIdx.z) * g.m * g.n;
-        for (int e = 0; e < rows; ++e) dst[(row0 + e) * g.n + col] = park[e * kParkStride + lane];
-        return;
-    }
-    // Every lane stays active up to the stores: lane e holds values of row
-    // row0 + e that other lanes read with readlane. 1 / row_scale is exact
-    // (row_scale is a normal power of two; exponent field 254 - E), so the
-    // row loop multiplies by it and waits on no memory.
-    const int64_t col_c = col_ok ? col : g.n - 1;
-    const int lane_row = lane < rows ? lane : rows - 1;
-    const float inv_lane =
-        __uint_as_float((254u << 23) - (__float_as_uint(g.row_scale[row0 + lane_row]) & 0x7f800000u));
-    const float cs = nq::load_f32(g.col_scale, g.col_scale_dtype, col_c);
-    const float bias = g.bias ? nq::load_f32(g.bias, g.bias_dtype, col_c) : 0.0f;
-    auto inv_of = [&](int e) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_lane), e)); };
-    const int64_t salient = g.salient_count;
-    float v[64];
-#pragma unroll
-    for (int e = 0; e < 64; ++e) v[e] = park[e * kParkStride + lane] * inv_of(e) * cs + bias;
-    // Salient columns (none for most layers): v[e] for the wave's 64 rows
-    // stays in registers while the columns are added in index order, eight at
-    // a time. Lane e loads x[row0 + e, idx_k] and the row loop takes it with
-    // readlane, so a batch of eight columns costs one round of loads.
-    for (int64_t k0 = 0; k0 < salient; k0 += 8) {
-        float xk[8], wk[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int64_t k = k0 + j < salient ? k0 + j : salient - 1;
-            const int64_t idx = g.salient_indices[k];
-            xk[j] = nq::load_f32(g.x, g.x_dtype, (row0 + lane_row) * g.in + idx);
-            float w = nq::load_f32(g.salient_values, g.salient_dtype, col_c * salient + k);
-            if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
-            wk[j] = k0 + j < salient ? w : 0.0f;
+    // One 64-row half of the wave's tile (rows row0 + [0, 64)); `return`
+    // leaves only this lambda.
+    const auto emit = [&](const int64_t row0) __attribute__((always_inline)) {
+        const int64_t col = n0 + 64 * wn + lane;
+        const int rows = __builtin_amdgcn_readfirstlane(static_cast<int>(g.m - row0 < 64 ? g.m - row0 : 64));
+        if (rows <= 0) return;  // the whole wave is past the last token
+        const bool col_ok = col < g.n;
+        if (g.partial) {
+            if (!col_ok) return;
+            float* dst = g.partial + static_cast<int64_t>(blockIdx.z) * g.m * g.n;
+            for (int e = 0; e < rows; ++e) dst[(row0 + e) * g.n + col] = park[e * kParkStride + lane];
+            return;
         }
+        // Every lane stays active up to the stores: lane e holds values of row
+        // row0 + e that other lanes read with readlane. 1 / row_scale is exact
+        // (row_scale is a normal power of two; exponent field 254 - E), so the
+        // row loop multiplies by it and waits on no memory.
+        const int64_t col_c = col_ok ? col : g.n - 1;
+        const int lane_row = lane < rows ? lane : rows - 1;
+        const float inv_lane =
+            __uint_as_float((254u << 23) - (__float_as_uint(g.row_scale[row0 + lane_row]) & 0x7f800000u));
+        const float cs = nq::load_f32(g.col_scale, g.col_scale_dtype, col_c);
+        const float bias = g.bias ? nq::load_f32(g.bias, g.bias_dtype, col_c) : 0.0f;
+        auto inv_of = [&](int e) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv_lane), e)); };
+        const int64_t salient = g.salient_count;
+        float v[64];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (k0 + j < salient) {
+        for (int e = 0; e < 64; ++e) v[e] = park[e * kParkStride + lane] * inv_of(e) * cs + bias;
+        // Salient columns (none for most layers): v[e] for the wave's 64 rows
+        // stays in registers while the columns are added in index order, eight at
+        // a time. Lane e loads x[row0 + e, idx_k] and the row loop takes it with
+        // readlane, so a batch of eight columns costs one round of loads.
+        for (int64_t k0 = 0; k0 < salient; k0 += 8) {
+            float xk[8], wk[8];
 #pragma unroll
-                for (int e = 0; e < 64; ++e)
-                    v[e] += wk[j] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xk[j]), e));
+            for (int j = 0; j < 8; ++j) {
+                const int64_t k = k0 + j < salient ? k0 + j : salient - 1;
+                const int64_t idx = g.salient_indices[k];
+                xk[j] = nq::load_f32(g.x, g.x_dtype, (row0 + lane_row) * g.in + idx);
+                float w = nq::load_f32(g.salient_values, g.salient_dtype, col_c * salient + k);
+                if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
+                wk[j] = k0 + j < salient ? w : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                if (k0 + j < salient) {
+#pragma unroll
+                    for (int e = 0; e < 64; ++e)
+                        v[e] += wk[j] * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(xk[j]), e));
+                }
             }
         }
-    }
-    if (g.out_scale) {
-        // The rank intermediate for GEMM 2: fp16, row-scaled, swizzled, with
-        // the padding columns up to out_ld written as zeros.
-        const float os_lane = g.out_scale[row0 + lane_row];
-        _Float16* o = static_cast<_Float16*>(g.out) + row0 * g.out_ld + swizzle4(col);
+        if (g.out_scale) {
+            // The rank intermediate for GEMM 2: fp16, row-scaled, swizzled, with
+            // the padding columns up to out_ld written as zeros (a 256-wide
+            // block can reach past out_ld: those lanes store nothing).
+            const float os_lane = g.out_scale[row0 + lane_row];
+            const bool in_row = col < g.out_ld;
+            _Float16* o = static_cast<_Float16*>(g.out) + row0 * g.out_ld + swizzle4(in_row ? col : 0);
 #pragma unroll
-        for (int e = 0; e < 64; ++e) {
-            const float os = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(os_lane), e));
-            if (e < rows) o[e * g.out_ld] = col_ok ? static_cast<_Float16>(v[e] * os) : static_cast<_Float16>(0.0f);
+            for (int e = 0; e < 64; ++e) {
+                const float os = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(os_lane), e));
+                if (e < rows && in_row)
+                    o[e * g.out_ld] = col_ok ? static_cast<_Float16>(v[e] * os) : static_cast<_Float16>(0.0f);
+            }
+            return;
         }
-        return;
-    }
-    if (!col_ok) return;
-    // One switch on the output dtype, then 64 predicated stores with
-    // constant register indices.
-    const int64_t out0 = row0 * g.n + col;
-    switch (g.out_dtype) {
-        case NQ_DTYPE_F32: {
-            float* o = static_cast<float*>(g.out) + out0;
+        if (!col_ok) return;
+        // One switch on the output dtype, then 64 predicated stores with
+        // constant register indices.
+        const int64_t out0 = row0 * g.n + col;
+        switch (g.out_dtype) {
+            case NQ_DTYPE_F32: {
+                float* o = static_cast<float*>(g.out) + out0;
 #pragma unroll
-            for (int e = 0; e < 64; ++e)
-                if (e < rows) o[e * g.n] = v[e];
-            break;
-        }
-        case NQ_DTYPE_F16: {
-            _Float16* o = static_cast<_Float16*>(g.out) + out0;
+                for (int e = 0; e < 64; ++e)
+                    if (e < rows) o[e * g.n] = v[e];
+                break;
+            }
+            case NQ_DTYPE_F16: {
+                _Float16* o = static_cast<_Float16*>(g.out) + out0;
 #pragma unroll
-            for (int e = 0; e < 64; ++e)
-                if (e < rows) o[e * g.n] = static_cast<_Float16>(v[e]);
-            break;
-        }
-        case NQ_DTYPE_BF16: {
-            uint16_t* o = static_cast<uint16_t*>(g.out) + out0;
+                for (int e = 0; e < 64; ++e)
+                    if (e < rows) o[e * g.n] = static_cast<_Float16>(v[e]);
+                break;
+            }
+            case NQ_DTYPE_BF16: {
+                uint16_t* o = static_cast<uint16_t*>(g.out) + out0;
 #pragma unroll
-            for (int e = 0; e < 64; ++e)
-                if (e < rows) o[e * g.n] = nq::f32_to_bf16_bits(v[e]);
-            break;
+                for (int e = 0; e < 64; ++e)
+                    if (e < rows) o[e * g.n] = nq::f32_to_bf16_bits(v[e]);
+                break;
+            }
+            default:
+                break;
         }
-        default:
-            break;
+    };
+#pragma unroll
+    for (int hf = 0; hf < II / 2; ++hf) {
+        if (hf > 0) __syncthreads();  // the previous half is read out of the park area
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    park[(32 * ii + 8 * (q >> 2) + 4 * h + (q & 3)) * kParkStride + 32 * jj + r] = acc[2 * hf + ii][jj][q];
+        __syncthreads();
+        emit(m0 + 64 * wm + 64 * hf);
     }
 }
 
@@ -523,6 +541,30 @@ Split split_for(int64_t tiles, int64_t k_blocks, int64_t tokens, int64_t n) {
     return best;
 }
 
+// The 128 x 256 block tile (k_sign_gemm<1>) for a GEMM that is not split
+// and still has at least kResident blocks at that size; 128 x 128 otherwise.
+bool wide_blocks(int64_t tokens, int64_t n, const Split& sp) {
+    const int64_t mt = (tokens + kBM - 1) / kBM;
+    return sp.slices == 1 && mt * ((n + 2 * kBN - 1) / (2 * kBN)) >= kResident;
+}
+
+// Launch one sign GEMM and, when K is split, its reduction over
+// `reduce_cols` output columns (n, or out_ld for the fp16 rank intermediate).
+void launch_gemm(const GemmArgs& g, const Split& sp, int64_t tokens, int64_t reduce_cols, hipStream_t stream) {
+    const bool wide = wide_blocks(tokens, g.n, sp);
+    const int64_t bn = wide ? 2 * kBN : kBN;
+    const dim3 grid(static_cast<unsigned>((g.n + bn - 1) / bn), static_cast<unsigned>((tokens + kBM - 1) / kBM),
+                    static_cast<unsigned>(sp.slices));
+    if (wide)
+        hipLaunchKernelGGL(k_sign_gemm<1>, grid, dim3(kBlock), 0, stream, g);
+    else
+        hipLaunchKernelGGL(k_sign_gemm<2>, grid, dim3(kBlock), 0, stream, g);
+    if (sp.slices > 1) {
+        const dim3 rgrid(static_cast<unsigned>((tokens * reduce_cols + kBlock - 1) / kBlock));
+        hipLaunchKernelGGL(k_reduce_splits, rgrid, dim3(kBlock), 0, stream, static_cast<int>(sp.slices), g);
+    }
+}
+
 struct Scratch {
     int64_t xs16, scale1, lm16, scale2, partial, total;
     Split s1, s2;
@@ -597,13 +639,7 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     g1.out_ld = geo.nsc2 * kBK;  // GEMM 1's column blocks cover exactly this width
     g1.k_per_split = sl.s1.k_per_split;
     g1.partial = sl.s1.slices > 1 ? partial : nullptr;
-    const dim3 grid1(static_cast<unsigned>((d->rank + kBN - 1) / kBN), static_cast<unsigned>((tokens + kBM - 1) / kBM),
-                     static_cast<unsigned>(sl.s1.slices));
-    hipLaunchKernelGGL(k_sign_gemm, grid1, dim3(kBlock), 0, stream, g1);
-    if (sl.s1.slices > 1) {
-        const dim3 grid(static_cast<unsigned>((tokens * g1.out_ld + kBlock - 1) / kBlock));
-        hipLaunchKernelGGL(k_reduce_splits, grid, dim3(kBlock), 0, stream, static_cast<int>(sl.s1.slices), g1);
-    }
+    launch_gemm(g1, sl.s1, tokens, g1.out_ld, stream);
 
     GemmArgs g2{};
     g2.a = lm16;
@@ -630,13 +666,7 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     g2.out_dtype = y_dtype;
     g2.k_per_split = sl.s2.k_per_split;
     g2.partial = sl.s2.slices > 1 ? partial : nullptr;
-    const dim3 grid2(static_cast<unsigned>((d->out_features + kBN - 1) / kBN),
-                     static_cast<unsigned>((tokens + kBM - 1) / kBM), static_cast<unsigned>(sl.s2.slices));
-    hipLaunchKernelGGL(k_sign_gemm, grid2, dim3(kBlock), 0, stream, g2);
-    if (sl.s2.slices > 1) {
-        const dim3 grid(static_cast<unsigned>((tokens * d->out_features + kBlock - 1) / kBlock));
-        hipLaunchKernelGGL(k_reduce_splits, grid, dim3(kBlock), 0, stream, static_cast<int>(sl.s2.slices), g2);
-    }
+    launch_gemm(g2, sl.s2, tokens, d->out_features, stream);
     return launch_status();
 }
 

@@ -344,6 +344,21 @@ def test_prefill_ragged_geometries(tokens, geometry):
     _check_shape(backend, state, tokens, seed=tokens)
 
 
+@pytest.mark.parametrize("geometry", [(1024, 64, 8200, 2), (512, 9000, 300, 0)])
+def test_prefill_wide_blocks(geometry):
+    """GEMMs large enough for the 128 x 256 block tile at M = 2048: a rank of
+    8200 puts it on the first GEMM (whose last block reaches past the padded
+    fp16 intermediate), an output of 9000 rows on the second (a partial last
+    block and partial tile)."""
+
+    in_f, out_f, rank, k = geometry
+    backend = HipPackedBackend()
+    _say("prefill wide", geometry)
+    shape = syn.LinearShape("blocks.0.mlp.gate_proj", in_f, out_f, rank)
+    state = syn.synthetic_packed_layer(shape, seed=sum(geometry), salient=k, bias=True)
+    _check_shape(backend, state, 2048, seed=7)
+
+
 @pytest.mark.parametrize("x_dtype", _FLOATS)
 def test_prefill_input_dtypes_and_patch(x_dtype):
     logical = _matrix_state(torch.bfloat16, torch.float16, torch.float16, True)
