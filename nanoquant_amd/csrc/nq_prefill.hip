@@ -169,6 +169,97 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ a
     if (threadIdx.x == 0) scale_out[t] = scale;
 }
 
+// Elements [i, i + 8) of a buffer of dtype DT as fp32: one 16-byte load
+// (two for fp32), no branch.
+template <int DT>
+__device__ __forceinline__ void load8_as(const void* __restrict__ p, int64_t i, float (&v)[8]) {
+    if constexpr (DT == NQ_DTYPE_F32) {
+        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+        const float4 a = q[0], b = q[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p) + i);
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (DT == NQ_DTYPE_BF16) {
+                v[2 * j] = __uint_as_float(w[j] << 16);
+                v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+            } else {
+                v[2 * j] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[j])));
+                v[2 * j + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w[j] >> 16)));
+            }
+        }
+    }
+}
+
+// k_prep_rows for rows of at most NCH * 8 * kBlock padded columns whose
+// activations and column scales allow 16-byte loads (cols % 8 == 0, aligned):
+// each thread keeps its NCH chunks of eight columns in registers, so the row
+// is read once, and every load is issued before the first use. Same
+// arithmetic and summation order as k_prep_rows, so both give identical
+// results. NCH = 2 (rows up to 4096 columns) keeps the registers low enough
+// for eight workgroups per CU.
+constexpr int kPrepChunksMax = 8;
+
+template <int ADT, int SDT, int NCH>
+__global__ __launch_bounds__(kBlock) void k_prep_rows_vec(const void* __restrict__ act, int64_t ld,
+                                                          const void* __restrict__ colscale, int64_t cols,
+                                                          int64_t cols_pad, _Float16* __restrict__ out16,
+                                                          float* __restrict__ scale_out,
+                                                          const uint32_t* __restrict__ max_mid_bits,
+                                                          float* __restrict__ bound_scale_out) {
+    __shared__ float wmax[kBlock / 64];
+    __shared__ float wsum[kBlock / 64];
+    const int64_t t = blockIdx.x;
+    float v[NCH][8];
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        const int64_t c = 8 * threadIdx.x + 8 * kBlock * k;
+        const int64_t cc = c < cols ? c : 0;  // chunks past the row reload its first
+        float s8[8];
+        load8_as<ADT>(act, t * ld + cc, v[k]);
+        load8_as<SDT>(colscale, cc, s8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[k][i] *= s8[i];
+    }
+    float m = 0.0f, l1 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        const bool live = 8 * threadIdx.x + 8 * kBlock * k < cols;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[k][i] = live ? v[k][i] : 0.0f;
+            if (live) m = fmaxf(m, fabsf(v[k][i])), l1 += fabsf(v[k][i]);
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off)), l1 += __shfl_xor(l1, off);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m, wsum[threadIdx.x >> 6] = l1;
+    __syncthreads();
+    const float scale = range_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+    if (max_mid_bits && threadIdx.x == 0)
+        bound_scale_out[t] = range_scale(__uint_as_float(*max_mid_bits) * ((wsum[0] + wsum[1]) + (wsum[2] + wsum[3])));
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        const int64_t c = 8 * threadIdx.x + 8 * kBlock * k;
+        if (c >= cols_pad) continue;
+        union {
+            _Float16 h[8];
+            uint4 u;
+        } o;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            o.h[4 * g + 0] = static_cast<_Float16>(v[k][4 * g + 0] * scale);
+            o.h[4 * g + 1] = static_cast<_Float16>(v[k][4 * g + 2] * scale);
+            o.h[4 * g + 2] = static_cast<_Float16>(v[k][4 * g + 1] * scale);
+            o.h[4 * g + 3] = static_cast<_Float16>(v[k][4 * g + 3] * scale);
+        }
+        *reinterpret_cast<uint4*>(out16 + t * cols_pad + c) = o.u;
+    }
+    if (threadIdx.x == 0) scale_out[t] = scale;
+}
+
 // B operand of the 32 x 32 x 16 MFMA of 16-column slice m from the words of
 // lane groups 2h and 2h + 1 (w0, w1): at bit 8b + m they hold columns
 // 16m + 8h + b and 16m + 8h + 4 + b. The A rows are stored with columns 1 and
@@ -620,9 +711,31 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
     // Vector row loads: 8 elements per load, 16-byte aligned rows.
     const int vec1_ok = (d->in_features % 8 == 0 && aligned(x, 16) && aligned(d->scale_pre, 16)) ? 1 : 0;
 
-    hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, x, x_dtype, d->in_features, d->scale_pre,
-                       d->scale_dtype, d->in_features, geo.nsc1 * kBK, vec1_ok, xs16, scale1,
-                       base + tiles_max_mid_word(), scale2);
+    const int64_t cols_pad1 = geo.nsc1 * kBK;
+    const uint32_t* max_mid = base + tiles_max_mid_word();
+    bool prepped = false;
+    if (vec1_ok && cols_pad1 <= int64_t(kPrepChunksMax) * 8 * kBlock) {
+        const bool short_rows = cols_pad1 <= 2 * 8 * kBlock;
+#define NQ_PREP(ADT, SDT)                                                                                      \
+    if (x_dtype == ADT && d->scale_dtype == SDT) {                                                             \
+        if (short_rows)                                                                                        \
+            hipLaunchKernelGGL((k_prep_rows_vec<ADT, SDT, 2>), rows, dim3(kBlock), 0, stream, x,                \
+                               d->in_features, d->scale_pre, d->in_features, cols_pad1, xs16, scale1, max_mid,  \
+                               scale2);                                                                        \
+        else                                                                                                   \
+            hipLaunchKernelGGL((k_prep_rows_vec<ADT, SDT, kPrepChunksMax>), rows, dim3(kBlock), 0, stream, x,   \
+                               d->in_features, d->scale_pre, d->in_features, cols_pad1, xs16, scale1, max_mid,  \
+                               scale2);                                                                        \
+        prepped = true;                                                                                        \
+    }
+#define NQ_PREP_S(ADT) NQ_PREP(ADT, NQ_DTYPE_F16) NQ_PREP(ADT, NQ_DTYPE_BF16) NQ_PREP(ADT, NQ_DTYPE_F32)
+        NQ_PREP_S(NQ_DTYPE_BF16) NQ_PREP_S(NQ_DTYPE_F16) NQ_PREP_S(NQ_DTYPE_F32)
+#undef NQ_PREP_S
+#undef NQ_PREP
+    }
+    if (!prepped)
+        hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, x, x_dtype, d->in_features, d->scale_pre,
+                           d->scale_dtype, d->in_features, cols_pad1, vec1_ok, xs16, scale1, max_mid, scale2);
     GemmArgs g1{};
     g1.a = xs16;
     g1.m = tokens;
