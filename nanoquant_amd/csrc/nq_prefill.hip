@@ -542,22 +542,75 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmArgs g) {
     }
 }
 
-// Split-K epilogue, one thread per output element (t, c):
-// out[t, c] = (Σ_z partial[z][t][c]) / row_scale[t] * col_scale[c] (+ bias
-// + salient columns for GEMM 2), the slices summed in z order. With
-// out_scale the threads cover [M, out_ld] and write the fp16 rank
+// Element i of an F32 / F16 / BF16 buffer from two unconditional 16-bit
+// loads (the halves of an fp32, or the same half twice), decoded by a
+// uniform select: no branch surrounds the loads, so they issue together.
+struct Raw2 {
+    uint32_t lo, hi;
+};
+
+__device__ __forceinline__ Raw2 load_raw2(const void* __restrict__ p, int dtype, int64_t i) {
+    const uint16_t* h = static_cast<const uint16_t*>(p);
+    const bool wide = dtype == NQ_DTYPE_F32;
+    return Raw2{h[wide ? 2 * i : i], h[wide ? 2 * i + 1 : i]};
+}
+
+__device__ __forceinline__ float raw2_value(const Raw2& r, int dtype) {
+    const float f32 = __uint_as_float((r.hi << 16) | (r.lo & 0xffffu));
+    const float bf16 = __uint_as_float(r.lo << 16);
+    const float f16 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.lo)));
+    return dtype == NQ_DTYPE_F32 ? f32 : (dtype == NQ_DTYPE_BF16 ? bf16 : f16);
+}
+
+// Split-K epilogue, one thread per output element (t, c), grid (column
+// blocks, token rows; t = blockIdx.y + kRowsPerGridZ * blockIdx.z): out[t, c] =
+// (Σ_z partial[z][t][c]) / row_scale[t] * col_scale[c] (+ bias + salient
+// columns for GEMM 2), the slices summed in z order. The column's scale and
+// bias and the first eight partials are loaded before any is used. With
+// out_scale the threads cover out_ld columns and write the fp16 rank
 // intermediate as the direct epilogue does (zeros past column n).
-__global__ __launch_bounds__(kBlock) void k_reduce_splits(int splits, const GemmArgs g) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+constexpr int64_t kRowsPerGridZ = 65535;
+
+__global__ __launch_bounds__(kBlock) void k_reduce_splits(int splits, const GemmArgs ga) {
+    // Every argument the kernel reads is loaded in one batch: the empty asm
+    // needs them all at one point, instead of one round trip per branch.
+    GemmArgs g;
+    g.m = ga.m;
+    g.n = ga.n;
+    g.out_ld = ga.out_ld;
+    g.out_scale = ga.out_scale;
+    g.out = ga.out;
+    g.out_dtype = ga.out_dtype;
+    g.partial = ga.partial;
+    g.row_scale = ga.row_scale;
+    g.col_scale = ga.col_scale;
+    g.col_scale_dtype = ga.col_scale_dtype;
+    g.bias = ga.bias;
+    g.bias_dtype = ga.bias_dtype;
+    g.salient_count = ga.salient_count;
+    asm volatile("" ::"s"(g.m), "s"(g.n), "s"(g.out_ld), "s"(g.out_scale), "s"(g.out), "s"(g.out_dtype),
+                 "s"(g.partial), "s"(g.row_scale), "s"(g.col_scale), "s"(g.col_scale_dtype), "s"(g.bias),
+                 "s"(g.bias_dtype), "s"(g.salient_count), "s"(splits));
+    g.salient_values = ga.salient_values;
+    g.salient_dtype = ga.salient_dtype;
+    g.salient_scales = ga.salient_scales;
+    g.scale_dtype = ga.scale_dtype;
+    g.salient_indices = ga.salient_indices;
+    g.x = ga.x;
+    g.x_dtype = ga.x_dtype;
+    g.in = ga.in;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int64_t t = static_cast<int64_t>(blockIdx.z) * kRowsPerGridZ + blockIdx.y;
     const int64_t width = g.out_scale ? g.out_ld : g.n;
-    if (i >= g.m * width) return;
-    const int64_t t = i / width, c = i - t * width;
-    const int64_t plane = g.m * g.n;
-    if (g.out_scale && c >= g.n) {
+    if (c >= width || t >= g.m) return;
+    if (c >= g.n) {  // only with out_scale: a padding column of the rank intermediate
         static_cast<_Float16*>(g.out)[t * g.out_ld + swizzle4(c)] = static_cast<_Float16>(0.0f);
         return;
     }
+    const int64_t plane = g.m * g.n;
     const int64_t pi = t * g.n + c;
+    const Raw2 cs_raw = load_raw2(g.col_scale, g.col_scale_dtype, c);
+    const Raw2 bias_raw = load_raw2(g.bias ? g.bias : g.col_scale, g.bias ? g.bias_dtype : g.col_scale_dtype, c);
     float part[8];
     float v = 0.0f;
     for (int z0 = 0; z0 < splits; z0 += 8) {
@@ -566,8 +619,8 @@ __global__ __launch_bounds__(kBlock) void k_reduce_splits(int splits, const Gemm
 #pragma unroll
         for (int j = 0; j < 8; ++j) v += part[j];
     }
-    v = v / g.row_scale[t] * nq::load_f32(g.col_scale, g.col_scale_dtype, c);
-    if (g.bias) v += nq::load_f32(g.bias, g.bias_dtype, c);
+    v = v / g.row_scale[t] * raw2_value(cs_raw, g.col_scale_dtype);
+    if (g.bias) v += raw2_value(bias_raw, g.bias_dtype);
     for (int64_t k = 0; k < g.salient_count; ++k) {
         float w = nq::load_f32(g.salient_values, g.salient_dtype, c * g.salient_count + k);
         if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
@@ -651,7 +704,9 @@ void launch_gemm(const GemmArgs& g, const Split& sp, int64_t tokens, int64_t red
     else
         hipLaunchKernelGGL(k_sign_gemm<2>, grid, dim3(kBlock), 0, stream, g);
     if (sp.slices > 1) {
-        const dim3 rgrid(static_cast<unsigned>((tokens * reduce_cols + kBlock - 1) / kBlock));
+        const dim3 rgrid(static_cast<unsigned>((reduce_cols + kBlock - 1) / kBlock),
+                         static_cast<unsigned>(tokens < kRowsPerGridZ ? tokens : kRowsPerGridZ),
+                         static_cast<unsigned>((tokens + kRowsPerGridZ - 1) / kRowsPerGridZ));
         hipLaunchKernelGGL(k_reduce_splits, rgrid, dim3(kBlock), 0, stream, static_cast<int>(sp.slices), g);
     }
 }
