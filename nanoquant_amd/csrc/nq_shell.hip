@@ -191,10 +191,11 @@ __global__ __launch_bounds__(kNormThreads) void k_add_rmsnorm(float* __restrict_
 // element j +- E/2 of the same lane; for head_dim 64 it is lane l ^ 32.
 
 // Element i of an F32 / F16 / BF16 buffer from one unconditional 32-bit load
-// (the fp32 itself, or the word holding the 16-bit element; the buffer is
-// 4-byte aligned and holds an even number of 16-bit elements): no branch
-// surrounds the load and nothing is derived from it before use, so a wave
-// issues all of them before waiting on any.
+// (the fp32 itself, or the pair of 16-bit elements 2 (i / 2) and 2 (i / 2) + 1,
+// counted from the buffer's start: the callers' buffers hold head_dim
+// elements, an even count): no branch surrounds the load and nothing is
+// derived from it before use, so a wave issues all of them before waiting on
+// any.
 struct RawHalves {
     uint32_t word, shift;
 };
