@@ -343,9 +343,16 @@ constexpr int cache_bytes() { return CT == NQ_DTYPE_F32 ? 4 : 2; }
 template <int D, int CT>
 constexpr int k_row_bytes() { return D * cache_bytes<CT>() + 16; }
 
+// k_attention_blocks stages the block's V rows in LDS too when a row is at
+// most 256 bytes (the K and V blocks then fit 64 KB with the per-wave rows).
+template <int D, int CT>
+constexpr bool attention_stages_v() { return D * cache_bytes<CT>() <= 256; }
+
 template <int D, int CT>
 constexpr size_t attention_lds(int waves) {
-    return static_cast<size_t>(kSeqBlock) * k_row_bytes<D, CT>() + static_cast<size_t>(waves) * (D + kSeqBlock) * 4;
+    return static_cast<size_t>(kSeqBlock) * k_row_bytes<D, CT>() +
+           (attention_stages_v<D, CT>() ? static_cast<size_t>(kSeqBlock) * D * cache_bytes<CT>() : 0) +
+           static_cast<size_t>(waves) * (D + kSeqBlock) * 4;
 }
 
 template <int CT>
@@ -425,10 +432,13 @@ __global__ __launch_bounds__(1024) void k_attention_blocks(const float* __restri
     constexpr int RB = k_row_bytes<D, CT>();
     constexpr int PIECES = D * EB / 16;  // 16-byte pieces per row
     constexpr int U = 8;                 // V rows per unrolled step
+    constexpr bool SV = attention_stages_v<D, CT>();
+    constexpr int VRB = D * EB;          // V row in LDS
     extern __shared__ float lds_raw[];
     char* klds = reinterpret_cast<char*>(lds_raw);
-    float* qv = reinterpret_cast<float*>(klds + kSeqBlock * RB);  // [waves][D]
-    float* pv = qv + (blockDim.x / kWave) * D;                     // [waves][64]
+    char* vlds = klds + kSeqBlock * RB;                                         // [64][D] when SV
+    float* qv = reinterpret_cast<float*>(vlds + (SV ? kSeqBlock * VRB : 0));  // [waves][D]
+    float* pv = qv + (blockDim.x / kWave) * D;                                  // [waves][64]
 
     const int group = q_heads / kv_heads;
     const int g = blockIdx.x % kv_heads;
@@ -444,20 +454,26 @@ __global__ __launch_bounds__(1024) void k_attention_blocks(const float* __restri
     if (p0 < 0 || row0 > last) return;  // uniform: no query of this workgroup reaches row0
     const int rows = static_cast<int>((last - row0 + 1) < kSeqBlock ? (last - row0 + 1) : kSeqBlock);
 
-    // Copy K rows [row0, row0 + rows) of kv head g to LDS as stored.
+    // Copy K rows [row0, row0 + rows) of kv head g to LDS as stored, and the
+    // V rows too when they fit (every query of the workgroup reads them).
     const int64_t head_row0 = static_cast<int64_t>(g) * max_positions + row0;
     const char* kbase = k_cache + head_row0 * D * EB;
+    const char* vbase = v_cache + head_row0 * D * EB;
     for (int i = threadIdx.x; i < rows * PIECES; i += blockDim.x) {
         const int r = i / PIECES, c = i % PIECES;
-        *reinterpret_cast<uint4*>(klds + r * RB + 16 * c) =
-            *reinterpret_cast<const uint4*>(kbase + (static_cast<int64_t>(r) * D) * EB + 16 * c);
+        const uint4 kq = *reinterpret_cast<const uint4*>(kbase + (static_cast<int64_t>(r) * D) * EB + 16 * c);
+        if constexpr (SV) {
+            const uint4 vq = *reinterpret_cast<const uint4*>(vbase + (static_cast<int64_t>(r) * D) * EB + 16 * c);
+            *reinterpret_cast<uint4*>(vlds + r * VRB + 16 * c) = vq;
+        }
+        *reinterpret_cast<uint4*>(klds + r * RB + 16 * c) = kq;
     }
     const int w = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
     const int h = g * group + w;
     float* qw = qv + w * D;
     float* pw = pv + w * kSeqBlock;
-    const char* vlane = v_cache + (head_row0 * D + lane * E) * EB;
+    const char* vlane = SV ? vlds + lane * E * EB : v_cache + (head_row0 * D + lane * E) * EB;
     __syncthreads();
 
     for (int64_t t = t0; t < t_end; ++t) {
