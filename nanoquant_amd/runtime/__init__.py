@@ -1,6 +1,6 @@
-"""Runtime surface for the packed linear: backend contract, layout, planner,
-module binding, the HIP backend and benchmark statistics (mirrors the names of
-the reference's ``nanoquant.runtime`` for this path)."""
+"""Runtime surface for the packed linear: backend contract, layout, backend
+selection, module binding and the HIP backend (the contract and layout keep the
+names of the reference's ``nanoquant.runtime`` for this path)."""
 
 from nanoquant_amd.runtime.backend import (
     BackendCapabilities,
@@ -12,13 +12,6 @@ from nanoquant_amd.runtime.backend import (
     SupportResult,
     WorkloadSpec,
     evaluate_capabilities,
-)
-from nanoquant_amd.runtime.benchmark import (
-    BenchmarkDistribution,
-    benchmark_wall,
-    profile_ratio_samples,
-    sum_aligned_profile_samples,
-    summarize_benchmark,
 )
 from nanoquant_amd.runtime.constants import RUNTIME_ARTIFACT_SCHEMA_VERSION, PackedLayout
 from nanoquant_amd.runtime.hip_backend import (
@@ -49,36 +42,20 @@ from nanoquant_amd.runtime.packed import (
     supports_vector_word_loads,
     unpack_sign_matrix,
 )
-from nanoquant_amd.runtime.planning import (
-    BackendPlan,
-    BackendPlanningError,
-    BackendRejection,
-    ExecutionPlans,
-    LayerDispatch,
-    PreparedBackendPlan,
-    PreparedDispatch,
-    PreparedExecutionPlans,
-    plan_backends,
-    plan_execution_workloads,
-    prepare_execution_workloads,
-    prepare_plan,
+from nanoquant_amd.runtime.dispatch import (
+    Choice,
+    PreparedModel,
+    Rejection,
+    SelectionError,
+    choose_backends,
 )
 from nanoquant_amd.runtime.decoder_shell import (
+    DecodeStep,
     DecoderLayerWeights,
     DecoderShellConfig,
     DecoderShellError,
     DecoderShellWeights,
     PackedDecoder,
-)
-from nanoquant_amd.runtime.generation import (
-    GenerationError,
-    GenerationModel,
-    GenerationRequest,
-    GenerationResult,
-    GenerationStep,
-    SamplingConfig,
-    batch_prompts,
-    generate,
 )
 from nanoquant_amd.runtime.packed_artifact import (
     OpenPackedArtifact,

@@ -29,6 +29,7 @@ and itself as the cache handle.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
+from typing import NamedTuple
 
 import torch
 
@@ -38,6 +39,14 @@ from nanoquant_amd.runtime.hip_backend import HipPackedBackend
 from nanoquant_amd.runtime.packed import PackedLayerState
 
 ROLES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+class DecodeStep(NamedTuple):
+    """Result of ``PackedDecoder.forward_step``: logits ``[1, 1, vocab]`` and the
+    cache handle (the decoder itself, which owns its KV cache)."""
+
+    logits: torch.Tensor
+    cache: object | None
 
 
 class DecoderShellError(ValueError):
@@ -470,11 +479,11 @@ class PackedDecoder:
         deterministic: bool,
     ):
         """``GenerationModel.forward_step`` (src/nanoquant/runtime/generation.py:28-41)
-        for batch 1: prefill rows run eagerly, a one-token decode step replays the
-        captured graph. Positions come from `cache_position` (device), so no
-        host synchronisation is needed."""
-
-        from nanoquant_amd.runtime.generation import GenerationStep
+        for batch 1, so the reference's generation engine can drive this shell:
+        prefill rows run eagerly, a one-token decode step replays the captured
+        graph. Positions come from `cache_position` (device), so no host
+        synchronisation is needed. Returns a ``DecodeStep`` (the engine reads
+        its ``logits`` and ``cache``)."""
 
         if input_ids.ndim != 2 or input_ids.shape[0] != 1:
             raise DecoderShellError("the packed decoder shell serves batch 1")
@@ -495,4 +504,4 @@ class PackedDecoder:
             if bool((~attention_mask.bool()).any()):
                 raise DecoderShellError("padded prompts are not supported by the batch-1 shell")
             self._forward(input_ids.reshape(-1).contiguous(), self._buffers(t))
-        return GenerationStep(self.logits.clone().view(1, 1, -1), self)
+        return DecodeStep(self.logits.clone().view(1, 1, -1), self)

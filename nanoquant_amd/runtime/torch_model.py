@@ -1,8 +1,8 @@
 """Module-level API: ``PreparedLinear`` replaces ``nn.Linear`` in a model shell.
 
 Mirrors the reference's module binding (src/nanoquant/runtime/torch_model.py:18-90,
-684-783): a ``ContextVar`` selects the prefill or decode plan for a whole
-forward, the module dispatches through ``PreparedBackendPlan.linear_at`` and by
+684-783): a ``ContextVar`` selects the prefill or decode workload for a whole
+forward, the module runs its layer through ``PreparedModel.linear`` and by
 default casts the backend's fp32 output back to the input dtype.
 """
 
@@ -18,7 +18,7 @@ import torch
 from torch import nn
 
 from nanoquant_amd.runtime.backend import WorkloadKind
-from nanoquant_amd.runtime.planning import PreparedExecutionPlans
+from nanoquant_amd.runtime.dispatch import PreparedModel
 
 _ACTIVE_WORKLOAD: ContextVar[WorkloadKind | None] = ContextVar(
     "nanoquant_amd_active_workload", default=None
@@ -44,7 +44,7 @@ class PreparedLinear(nn.Module):
 
     def __init__(
         self,
-        plans: PreparedExecutionPlans,
+        model: PreparedModel,
         layer_index: int,
         *,
         output_dtype: Literal["input", "backend"] = "input",
@@ -52,15 +52,12 @@ class PreparedLinear(nn.Module):
         super().__init__()
         if output_dtype not in ("input", "backend"):
             raise ValueError(f"unsupported prepared linear output dtype policy: {output_dtype}")
-        prefill_spec = plans.prefill.dispatches[layer_index].layer.spec
-        decode_spec = plans.decode.dispatches[layer_index].layer.spec
-        if prefill_spec != decode_spec:
-            raise ValueError(f"paired prepared layer specifications differ: {prefill_spec.name}")
-        self._plans = plans
+        spec = model.spec(layer_index)
+        self._model = model
         self._layer_index = layer_index
         self._output_dtype = output_dtype
-        self.in_features = prefill_spec.in_features
-        self.out_features = prefill_spec.out_features
+        self.in_features = spec.in_features
+        self.out_features = spec.out_features
 
     def forward(self, value: torch.Tensor) -> torch.Tensor:
         kind = _ACTIVE_WORKLOAD.get()
@@ -68,8 +65,7 @@ class PreparedLinear(nn.Module):
             raise RuntimeError(
                 "NanoQuant prepared linear executed outside an execution_workload context"
             )
-        plan = self._plans.decode if kind == "decode" else self._plans.prefill
-        output = plan.linear_at(self._layer_index, value)
+        output = self._model.linear(kind, self._layer_index, value)
         if self._output_dtype == "input":
             return output.to(dtype=value.dtype)
         return output
@@ -125,7 +121,7 @@ def _resolve_linear(model: nn.Module, path: str, layer_name: str) -> tuple[nn.Mo
 
 def bind_prepared_linears(
     model: nn.Module,
-    plans: PreparedExecutionPlans,
+    prepared: PreparedModel,
     module_paths: Mapping[str, str],
     *,
     output_dtype: Literal["input", "backend"] = "input",
@@ -133,7 +129,7 @@ def bind_prepared_linears(
     """Replace exactly the planned ``nn.Linear`` inventory; validate everything
     before mutating the model (src/nanoquant/runtime/torch_model.py:684-768)."""
 
-    names = tuple(d.plan.layer_name for d in plans.prefill.dispatches)
+    names = prepared.names
     if set(module_paths) != set(names):
         raise ValueError(
             "runtime model module mapping differs from the plan: "
@@ -147,12 +143,12 @@ def bind_prepared_linears(
     swaps: list[tuple[nn.Module, str, nn.Module]] = []
     owners: list[tuple[nn.Module, str, PreparedLinear]] = []
     for index, (name, path) in enumerate(zip(names, paths, strict=True)):
-        spec = plans.prefill.dispatches[index].layer.spec
+        spec = prepared.spec(index)
         if not spec.members:
             parent, attribute, existing = _resolve_linear(model, path, name)
             if (existing.in_features, existing.out_features) != (spec.in_features, spec.out_features):
                 raise ValueError(f"runtime model linear dimensions differ for {name}: {path}")
-            swaps.append((parent, attribute, PreparedLinear(plans, index, output_dtype=output_dtype)))
+            swaps.append((parent, attribute, PreparedLinear(prepared, index, output_dtype=output_dtype)))
             continue
         block_path, marker, relative = path.partition(".self_attn.")
         if not (marker and block_path and relative):
@@ -161,7 +157,7 @@ def bind_prepared_linears(
             block = model.get_submodule(block_path)
         except (AttributeError, KeyError) as error:
             raise ValueError(f"runtime projection group block is unavailable for {name}: {path}") from error
-        owner = PreparedLinear(plans, index, output_dtype=output_dtype)
+        owner = PreparedLinear(prepared, index, output_dtype=output_dtype)
         for member in spec.members:
             member_path = transformers_decoder_module_paths((member.name,))[member.name]
             parent, attribute, existing = _resolve_linear(model, member_path, name)

@@ -23,13 +23,12 @@ from nanoquant_amd.runtime import (
     HipPackedBackend,
     LogicalLayerState,
     PreparedLinear,
+    PreparedModel,
     QuantizedLinearSpec,
     WorkloadSpec,
     execution_workload,
     pack_logical_layer,
     pack_sign_matrix,
-    plan_execution_workloads,
-    prepare_execution_workloads,
     unpack_sign_matrix_device,
 )
 from nanoquant_amd.runtime import _native
@@ -404,22 +403,21 @@ def test_llama3_8b_prefill_sweep(tokens):
 # --- integration ---------------------------------------------------------------------
 
 
-def test_planner_and_module_on_gpu(backend):
+def test_selection_and_module_on_gpu(backend):
     logical = _matrix_state(torch.float32, torch.bfloat16, torch.bfloat16, True)
     packed = pack_logical_layer(logical)
-    plans = plan_execution_workloads(
-        (packed.spec,),
+    prepared = PreparedModel(
+        {packed.spec.name: packed},
         prefill=WorkloadSpec("prefill", "cuda", "bfloat16", 1, 4, deterministic=True),
         decode=WorkloadSpec("decode", "cuda", "bfloat16", 1, 1, deterministic=True),
-        prefill_backends=(backend,), decode_backends=(backend,), strict=True,
+        backends=(backend,), device="cuda",
     )
-    prepared = prepare_execution_workloads(plans, {packed.spec.name: packed}, (backend,), "cuda")
-    assert prepared.prefill.dispatches[0].layer is prepared.decode.dispatches[0].layer
+    assert prepared.prepared("prefill", 0) is prepared.prepared("decode", 0)
     prefill = torch.linspace(-1, 1, 140, dtype=torch.bfloat16).reshape(1, 4, 35).cuda()
     decode = prefill[:, -1, :].contiguous()
     fwd = orc.CpuPackedForward(orc.operands_from_state(packed))
-    _assert_parity(backend, prepared.prefill.linear_at(0, prefill), fwd(prefill.cpu()))
-    _assert_parity(backend, prepared.decode.linear_at(0, decode), fwd(decode.cpu()))
+    _assert_parity(backend, prepared.linear("prefill", 0, prefill), fwd(prefill.cpu()))
+    _assert_parity(backend, prepared.linear("decode", 0, decode), fwd(decode.cpu()))
     module = PreparedLinear(prepared, 0)
     with execution_workload("decode"):
         out = module(decode)

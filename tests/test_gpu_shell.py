@@ -11,7 +11,7 @@ own greedy tokens:
     oracle that rounds at the same points: rel-L2 <= 2e-2;
   * the greedy token is the argmax of the returned logits and agrees with the
     oracle's unless the oracle's top-2 gap is within the tolerance;
-  * graph replay, eager steps and the generation engine give identical tokens.
+  * graph replay, eager steps and the ``forward_step`` protocol give identical tokens.
 """
 
 from __future__ import annotations
@@ -351,9 +351,7 @@ def test_decoder_qwen3_8b_geometry_matches_oracle(act, cache, tol):
     _check_against_oracle(QWEN_2L, act, cache, tol, prompt_len=12, new_tokens=5, seed=syn.BASE_SEED + 62)
 
 
-def test_graph_replay_matches_eager_and_engine():
-    from nanoquant_amd.runtime.generation import GenerationRequest, generate
-
+def test_graph_replay_matches_eager_and_forward_step():
     weights = syn.synthetic_decoder(SMALL, seed=syn.BASE_SEED + 63)
     decoder = PackedDecoder(SMALL, weights, device=DEV, max_positions=128)
     prompt = torch.randint(0, SMALL.vocab, (40,), generator=_g(63))
@@ -362,8 +360,20 @@ def test_graph_replay_matches_eager_and_engine():
     graph_again = decoder.generate_greedy(prompt.to(DEV), 20).tolist()
     no_graph = decoder.generate_greedy(prompt.to(DEV), 20, use_graph=False).tolist()
     assert graph_tokens == eager_tokens == graph_again == no_graph
-    request = GenerationRequest(prompt[None].to(DEV), torch.ones(1, 40, dtype=torch.bool, device=DEV),
-                                max_new_tokens=20, eos_token_ids=(SMALL.vocab + 1,), pad_token_id=0)
-    result = generate(request, decoder)
-    assert result.token_ids[0].tolist() == graph_tokens
-    assert result.decode_forward_count == 19 and result.stop_reasons == ("max_new_tokens",)
+    # The reference engine's calls (src/nanoquant/runtime/generation.py:314-404):
+    # one prefill step over the prompt, then one-token decode steps that pass
+    # the returned cache back, greedy argmax of the last logits row.
+    ids = prompt[None].to(DEV)
+    step = decoder.forward_step(
+        input_ids=ids, attention_mask=torch.ones_like(ids, dtype=torch.bool),
+        position_ids=torch.arange(40, device=DEV)[None], cache_position=torch.arange(40, device=DEV), cache=None, max_cache_length=128,
+        workload="prefill", deterministic=True)
+    tokens = [int(step.logits[0, -1].argmax())]
+    for pos in range(40, 59):
+        ids = torch.tensor([[tokens[-1]]], device=DEV)
+        step = decoder.forward_step(
+            input_ids=ids, attention_mask=torch.ones(1, pos + 1, dtype=torch.bool, device=DEV),
+            position_ids=torch.tensor([[pos]], device=DEV), cache_position=torch.tensor([pos], device=DEV), cache=step.cache, max_cache_length=128,
+            workload="decode", deterministic=True)
+        tokens.append(int(step.logits[0, -1].argmax()))
+    assert tokens == graph_tokens

@@ -1,7 +1,7 @@
 """Host-side runtime API: layout helpers, layer-state invariants, capability
-codes, planner behaviour and the module binding. Mirrors the reference's
-tests/unit/test_runtime_{packed,backend,execution_plans}.py behaviour with
-fake backends; no GPU needed."""
+codes, backend selection and the module binding, with fake backends; no GPU
+needed. The layout and state cases follow the reference's
+tests/unit/test_runtime_{packed,backend}.py."""
 
 from __future__ import annotations
 
@@ -18,15 +18,15 @@ from nanoquant_amd.runtime import (
     PACKED_REFERENCE_COMMIT,
     PACKED_REFERENCE_CUDA_SHA256,
     BackendCapabilities,
-    BackendPlanningError,
-    ExecutionPlans,
     HipPackedBackend,
     LogicalLayerState,
     PackedLayerState,
     PackedLayoutMetadata,
     PreparedLayer,
     PreparedLinear,
+    PreparedModel,
     QuantizedLinearSpec,
+    SelectionError,
     SupportResult,
     WorkloadSpec,
     bind_prepared_linears,
@@ -35,12 +35,8 @@ from nanoquant_amd.runtime import (
     pack_logical_layer,
     pack_sign_matrix,
     packed_row_stride_bytes,
+    choose_backends,
     packed_word_count,
-    plan_backends,
-    plan_execution_workloads,
-    prepare_execution_workloads,
-    prepare_plan,
-    summarize_benchmark,
     supports_vector_word_loads,
     unpack_sign_matrix,
 )
@@ -253,59 +249,60 @@ def _state(name):
                              torch.ones(4), torch.ones(2), torch.ones(3))
 
 
-def test_planner_fallback_strict_and_named_rejections():
+def test_selection_fallback_strict_and_named_rejections():
     states = {n: _state(n) for n in ("blocks.0.proj", "blocks.1.proj")}
     rejecting = _KindBackend("rejecting", ("prefill", "decode"), reject_code="NQ-INF-RANK-ALIGNMENT")
     fallback = _KindBackend("fallback", ("prefill", "decode"))
     work = WorkloadSpec("decode", "cpu", "float32", 1, 1, deterministic=True)
-    plan = plan_backends(tuple(s.spec for s in states.values()), work, (rejecting, fallback), strict=False)
-    assert plan.fallback_count == 2
-    assert [d.rejected_backends[0].support.code for d in plan.layers] == ["NQ-INF-RANK-ALIGNMENT"] * 2
-    prepared = prepare_plan(plan, states, (rejecting, fallback), "cpu")
-    assert prepared[0].linear(torch.ones(1, 4)).shape == (1, 3)
-    with pytest.raises(BackendPlanningError, match="strict runtime plan rejected fallback.*NQ-INF-RANK-ALIGNMENT"):
-        plan_backends((_spec(),), work, (rejecting, fallback), strict=True)
-    with pytest.raises(ValueError, match="missing=.*blocks.0.proj"):
-        prepare_plan(plan, {}, (fallback,), "cpu")
+    choices = choose_backends([s.spec for s in states.values()], work, (rejecting, fallback), strict=False)
+    assert [c.fallback for c in choices] == [True, True]
+    assert [c.rejections[0].code for c in choices] == ["NQ-INF-RANK-ALIGNMENT"] * 2
+    assert [c.backend for c in choices] == [fallback, fallback]
+    with pytest.raises(SelectionError, match="strict selection refuses the fallback.*NQ-INF-RANK-ALIGNMENT"):
+        choose_backends((_spec(),), work, (rejecting, fallback), strict=True)
+    with pytest.raises(SelectionError, match="no backend accepts the decode workload.*NQ-INF-RANK-ALIGNMENT"):
+        choose_backends((_spec(),), work, (rejecting,), strict=False)
+    with pytest.raises(ValueError, match="unique"):
+        choose_backends((_spec(), _spec()), work, (fallback,), strict=False)
 
 
-def test_execution_plans_share_payloads_and_fix_decode_geometry():
+def _model(states, backend, *, batch=2, prefill_tokens=3, device="cpu"):
+    return PreparedModel(
+        states,
+        prefill=WorkloadSpec("prefill", "cpu", "float32", batch, prefill_tokens, deterministic=True),
+        decode=WorkloadSpec("decode", "cpu", "float32", batch, 1, deterministic=True),
+        backends=(backend,), device=device,
+    )
+
+
+def test_prepared_model_shares_payloads_and_fixes_decode_geometry():
     states = {n: _state(n) for n in ("blocks.0.proj", "blocks.1.proj")}
     backend = _KindBackend("both", ("prefill", "decode"))
-    plans = plan_execution_workloads(
-        tuple(s.spec for s in states.values()),
-        prefill=WorkloadSpec("prefill", "cpu", "float32", 2, 3, deterministic=True),
-        decode=WorkloadSpec("decode", "cpu", "float32", 2, 1, deterministic=True),
-        prefill_backends=(backend,), decode_backends=(backend,), strict=True,
-    )
-    prepared = prepare_execution_workloads(plans, states, (backend,), "cpu")
+    model = _model(states, backend)
     assert backend.prepare_count == 2
-    assert all(p.layer is d.layer for p, d in zip(prepared.prefill.dispatches, prepared.decode.dispatches))
-    assert prepared.prefill.linear_at(0, torch.ones(2, 1, 4)).shape == (2, 1, 3)
-    with pytest.raises(ValueError, match="prefill input has 8 token slots, expected at most 6"):
-        prepared.prefill.linear_at(0, torch.ones(2, 4, 4))
-    with pytest.raises(ValueError, match="decode input has 6 token slots, expected exactly 2"):
-        prepared.decode.linear_at(0, torch.ones(2, 3, 4))
-    with pytest.raises(ValueError, match="prefill input dtype differs"):
-        prepared.prefill.linear_at(0, torch.ones(2, 3, 4, dtype=torch.float16))
-    with pytest.raises(IndexError, match="outside the inventory"):
-        prepared.decode.linear_at(2, torch.ones(2, 4))
-    with pytest.raises(ValueError, match="decode plans require exactly one token"):
-        ExecutionPlans(plans.prefill, replace(plans.decode, workload=WorkloadSpec("decode", "cpu", "float32", 1, 2)))
-    with pytest.raises(ValueError, match="preparation device 'cuda' differs"):
-        prepare_execution_workloads(plans, states, (backend,), "cuda")
+    assert all(model.prepared("prefill", i) is model.prepared("decode", i) for i in range(2))
+    assert model.linear("prefill", 0, torch.ones(2, 1, 4)).shape == (2, 1, 3)
+    with pytest.raises(ValueError, match="prefill input holds 8 token slots; at most 6 fit"):
+        model.linear("prefill", 0, torch.ones(2, 4, 4))
+    with pytest.raises(ValueError, match="decode input holds 6 token slots; it must hold 2"):
+        model.linear("decode", 0, torch.ones(2, 3, 4))
+    with pytest.raises(ValueError, match="prefill input dtype"):
+        model.linear("prefill", 0, torch.ones(2, 3, 4, dtype=torch.float16))
+    with pytest.raises(IndexError, match="not in the inventory"):
+        model.linear("decode", 2, torch.ones(2, 4))
+    with pytest.raises(ValueError, match="decode workload runs one token"):
+        PreparedModel(states, prefill=WorkloadSpec("prefill", "cpu", "float32", 1, 4),
+                      decode=WorkloadSpec("decode", "cpu", "float32", 1, 2), backends=(backend,), device="cpu")
+    with pytest.raises(ValueError, match="is not the preparation device 'cuda'"):
+        _model(states, backend, device="cuda")
+    with pytest.raises(ValueError, match="stored under the name"):
+        _model({"blocks.9.proj": states["blocks.0.proj"]}, backend)
 
 
 def test_prepared_linear_binding_and_context():
     states = {"blocks.0.mlp.up": _state("blocks.0.mlp.up")}
     backend = _KindBackend("both", ("prefill", "decode"))
-    plans = plan_execution_workloads(
-        (states["blocks.0.mlp.up"].spec,),
-        prefill=WorkloadSpec("prefill", "cpu", "float32", 1, 4),
-        decode=WorkloadSpec("decode", "cpu", "float32", 1, 1),
-        prefill_backends=(backend,), decode_backends=(backend,), strict=True,
-    )
-    prepared = prepare_execution_workloads(plans, states, (backend,), "cpu")
+    prepared = _model(states, backend, batch=1, prefill_tokens=4)
     model = nn.Module()
     model.mlp = nn.Module()
     model.mlp.up = nn.Linear(4, 3)
@@ -315,12 +312,3 @@ def test_prepared_linear_binding_and_context():
         model.mlp.up(torch.ones(1, 4))
     with execution_workload("decode"):
         assert model.mlp.up(torch.ones(1, 4)).shape == (1, 3)
-
-
-def test_benchmark_summary_percentiles():
-    dist = summarize_benchmark([0.4, 0.1, 0.2, 0.3], unit_name="tokens", units_per_sample=2)
-    assert dist.samples_seconds == (0.4, 0.1, 0.2, 0.3)
-    assert dist.latency_seconds["p50"] == pytest.approx(0.25)
-    assert dist.throughput_per_second["max"] == pytest.approx(20.0)
-    with pytest.raises(ValueError):
-        summarize_benchmark([0.0], unit_name="t", units_per_sample=1)
