@@ -138,9 +138,12 @@ int nq_count_bad_padding(const int32_t* words, int64_t rows, int64_t cols,
 /* Bytes of the synchronisation header at the start of a tiles buffer. It holds
  * the fused launch's monotonic counters (never reset; graph replays are safe)
  * and, on its last 256-byte line, word 0 = sticky error flag (set if a fused
- * decode launch ever timed out waiting for its stage-1 results), word 1 =
- * magic 0x4E515433, word 2 = max|s_mid| as fp32 bits (bounds the stage-1
- * results so the decode epilogue can pick their fixed-point exponent). The
+ * decode launch ever timed out waiting for its stage-1 results; the outputs of
+ * the workgroups that timed out are NaN), word 1 = magic 0x4E515433, word 2 =
+ * max|s_mid| as fp32 bits (bounds the stage-1 results so the decode epilogue
+ * can pick their fixed-point exponent), word 3 = the fused launch's spin
+ * limit (polls of the stage-1 signal before giving up; 2^22 from
+ * nq_prepare_tiles, a caller may lower it). The
  * header is per layer: launches that use one prepared layer must not overlap
  * in time (one stream, or ordered streams). No reference counterpart. */
 int64_t nq_tiles_header_bytes(void);

@@ -41,8 +41,9 @@ __global__ __launch_bounds__(256) void k_build_tiles(const uint32_t* __restrict_
     }
 }
 
-// Zero the header, write the magic and max|s_mid| (the stage-1 epilogue's
-// bound on the rank intermediate). One workgroup of 256 threads.
+// Zero the header, write the magic, the fused launch's spin limit and
+// max|s_mid| (the stage-1 epilogue's bound on the rank intermediate). One
+// workgroup of 256 threads.
 __global__ __launch_bounds__(256) void k_init_header(uint32_t* header, const void* s_mid, int scale_dtype,
                                                      int64_t rank) {
     __shared__ float wmax[4];
@@ -54,6 +55,7 @@ __global__ __launch_bounds__(256) void k_init_header(uint32_t* header, const voi
     __syncthreads();
     if (threadIdx.x == 0) {
         header[line_word(kMiscLine) + kMiscMagic] = kTilesMagic;
+        header[line_word(kMiscLine) + kMiscSpin] = kSpinLimit;
         header[line_word(kMiscLine) + kMiscMaxMid] =
             __float_as_uint(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
     }

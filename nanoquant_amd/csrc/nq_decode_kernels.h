@@ -127,8 +127,9 @@ constexpr int kReplica0 = kArriveSlot0 + kArriveSlots;
 constexpr int kMiscLine = kReplica0 + kReplicas;
 constexpr int kHeaderLines = kMiscLine + 1;
 constexpr int kHeaderWords = kHeaderLines * kLine;
-// Words on the misc line.
-enum : int { kMiscError = 0, kMiscMagic = 1, kMiscMaxMid = 2 };
+// Words on the misc line. kMiscSpin is the fused launch's spin limit
+// (kSpinLimit from prepare; a host may lower it, e.g. to exercise the timeout).
+enum : int { kMiscError = 0, kMiscMagic = 1, kMiscMaxMid = 2, kMiscSpin = 3 };
 
 __host__ __device__ constexpr int line_word(int line) { return line * kLine; }
 
@@ -644,6 +645,16 @@ __device__ __forceinline__ void gate_values(const S1Regs<AK, TOK, TW>& r, int t,
     }
 }
 
+// Bits that are set in the fma word of a non-finite staged value and clear in
+// every finite one (finite words have the top byte 0x4B, see stage_block).
+constexpr uint32_t kNonFiniteBits = 0x34000000u;
+
+// Exponent a stage-1 epilogue writes for a token whose activations hold a
+// NaN or an infinity: stage 2 then stores NaN for every output of that token,
+// as the reference's fp32 forward yields (a non-finite activation reaches
+// every rank value with both signs; reference.py:208-217).
+constexpr int kPoisonExp = 0x7fffffff;
+
 // Stage tokens [t_base, t_base + TPB) of chunk c into this wave's operand area
 // (three digit rows per token) and return each token's exponent E and the
 // chunk max |a| (uniform values).
@@ -703,12 +714,14 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
         const int e = range_exponent(wmx, 14);
         const float sm = m < 7 ? exp2i(e + 7 - m) : -exp2i(e);
         uint32_t dig[3][2];
+        uint32_t seen = 0;  // OR of the fma words: flags a non-finite staged value
 #pragma unroll
         for (int run = 0; run < 2; ++run) {
             uint32_t y0[4], y1[4], y2[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t y = __float_as_uint(__builtin_fmaf(v[run][i], sm, 12582912.0f));
+                seen |= y;
                 y0[i] = y;
                 y1[i] = y + 128u;
                 y2[i] = y + (32896u - 0x400000u);
@@ -718,7 +731,11 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
             dig[2][run] = bytes_at<2>(y2[0], y2[1], y2[2], y2[3]);
         }
         expo[u] = e;
-        cmax[u] = wmx;
+        // A finite value gives |w| <= 2^22, so its word lies in [2^23, 2^24]
+        // (top byte 0x4B); NaN and +-Inf give exponent bits 0xFF, which set
+        // bits the finite words never have. The chunk max then becomes +Inf,
+        // which makes the token's bound non-finite in the epilogue.
+        cmax[u] = __builtin_amdgcn_ballot_w64((seen & kNonFiniteBits) != 0) != 0 ? __builtin_inff() : wmx;
 #pragma unroll
         for (int digit = 0; digit < 3; ++digit) {
             const int row = 4 * u + digit;
@@ -745,9 +762,9 @@ __device__ __forceinline__ v4i ones_mfma(const v4i (&A)[8]) {
 // The eight sign MFMAs of one (chunk, tile, operand block) and the exact
 // conversion to the chunk's fp32 partial; words d >= dw (a partial chunk)
 // count as zero. NDIG digit rows per token; lane 16*t' + n returns token t' of
-// the block, row n; e is that token's exponent.
+// the block, row n; scale is 2^(-e-7) for that token's exponent e.
 template <int NDIG>
-__device__ __forceinline__ float tile_partial(const v4i (&A)[8], const v4i& S, v4u w, int dw, int e) {
+__device__ __forceinline__ float tile_partial(const v4i (&A)[8], const v4i& S, v4u w, int dw, float scale) {
     // A partial last chunk: words past dw belong to other lanes (uniform masks).
     w[1] &= dw > 1 ? ~0u : 0u;
     w[2] &= dw > 2 ? ~0u : 0u;
@@ -767,7 +784,7 @@ __device__ __forceinline__ float tile_partial(const v4i (&A)[8], const v4i& S, v
     float v = static_cast<float>(diff[0]) + 256.0f * static_cast<float>(diff[1]) +
               65536.0f * static_cast<float>(diff[2]);
     if (NDIG == 4) v += 16777216.0f * static_cast<float>(diff[3]);
-    return v * exp2i(-e - 7);
+    return v * scale;
 }
 
 __device__ __forceinline__ void hdr_store(uint32_t* header, int word, uint32_t v) {
@@ -809,8 +826,13 @@ __device__ __forceinline__ void signal_ready(const LinArgs& a, int64_t t0, int t
 }
 
 // Fused launch, stage 2: register the workgroup's tiles, then wait until every
-// stage-1 tile of this launch has signalled.
-__device__ __forceinline__ void wait_ready(const LinArgs& a, int64_t t0, int tw, int64_t wg, bool dead) {
+// stage-1 tile of this launch has signalled. Returns true (in every thread)
+// when the bounded wait gave up: the stage-1 operands may then be stale, so
+// the caller stores NaN for the workgroup's outputs, and the sticky error
+// flag in the header records the event for the host.
+__device__ __forceinline__ bool wait_ready(const LinArgs& a, int64_t t0, int tw, int64_t wg, bool dead) {
+    __shared__ int gave_up;
+    if (threadIdx.x == 0) gave_up = 0;
     if (threadIdx.x == 0 && !dead) {
         const int64_t n2 = a.g2.nt;
         uint32_t target = 0;
@@ -822,10 +844,12 @@ __device__ __forceinline__ void wait_ready(const LinArgs& a, int64_t t0, int tw,
             if (tt == 0) target = static_cast<uint32_t>(v / slot_count(slot, kArriveSlots, n2) + 1);
         }
         const uint32_t* flag = a.header + line_word(kReplica0 + static_cast<int>(wg % kReplicas));
+        const uint32_t limit = a.header[line_word(kMiscLine) + kMiscSpin];
         uint32_t spins = 0;
         while (static_cast<int32_t>(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-            if (++spins > kSpinLimit) {
+            if (++spins > limit) {
                 hdr_store(a.header, line_word(kMiscLine) + kMiscError, 1u);
+                gave_up = 1;
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
@@ -833,6 +857,7 @@ __device__ __forceinline__ void wait_ready(const LinArgs& a, int64_t t0, int tw,
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
+    return gave_up != 0;
 }
 
 // Chunks of one pass: chunk c_j = base + wave + j * nw; a dead chunk (past nc)
@@ -991,9 +1016,10 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
                 int e = expo[0];
 #pragma unroll
                 for (int u = 1; u < TPB; ++u) e = (lane >> 4) == u ? expo[u] : e;
+                const float sc = exp2i(-e - 7);
 #pragma unroll
                 for (int tt = 0; tt < TW; ++tt)
-                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<3>(A, S, r[j].w[tt], dw, e);
+                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<3>(A, S, r[j].w[tt], dw, sc);
                 if (lane == 0) {
 #pragma unroll
                     for (int u = 0; u < TPB; ++u) cmx[c * TOK + tb * TPB + u] = cm[u];
@@ -1020,14 +1046,18 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
             sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
             bound += cmx[c * TOK + o.t];
         }
-        const int e = range_exponent(bound * rs * (512.0f * maxsm), 21);
+        // Every workgroup sums the same chunk maxima in the same order, so all
+        // agree on the exponent and on a poisoned (non-finite) token.
+        const bool poison = !(bound <= 3.402823466e38f);
+        const int e = poison ? 0 : range_exponent(bound * rs * (512.0f * maxsm), 21);
         float v = 0.0f;
-        if (row < rank) v = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_mid, a.scale_dtype, row),
-                                             a.scale_dtype) * rs;
+        if (row < rank && !poison)
+            v = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_mid, a.scale_dtype, row), a.scale_dtype) * rs;
         store_lmq<TPB, TB, FUSED>(a.lmq, row, o.t, v, e);
         if (wg == 0 && o.tt == 0 && o.n == 0) {
-            if (FUSED) __hip_atomic_store(a.lme + o.t, e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else a.lme[o.t] = e;
+            const int le = poison ? kPoisonExp : e;
+            if (FUSED) __hip_atomic_store(a.lme + o.t, le, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            else a.lme[o.t] = le;
         }
     }
     // The last workgroup zeroes the operand columns past its last tile up to
@@ -1069,6 +1099,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     const int fr0 = (t0 + f.tt) * kTileRows + f.n;
     const int fr = fr0 < out ? fr0 : out - 1;
     RawElem rs0, bias0;
+    bool stale = false;  // fused launch: the wait for stage 1 gave up
 
     // One pass; the first is peeled off the loop and issues the epilogue
     // operands after its own loads (see stage1_wg).
@@ -1079,7 +1110,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
         for (int j = 0; j < KC; ++j) load_words(r[j].w, a.u_tiles, nt, nb, t0, pc.c[j], lane);
         // The U words do not depend on stage 1; the fused launch waits for its
         // signal only now.
-        if (FUSED && first) wait_ready(a, t0, TW, wg, dead);
+        if (FUSED && first) stale = wait_ready(a, t0, TW, wg, dead);
 #pragma unroll
         for (int j = 0; j < KC; ++j) load_s2_ops<TPB, TB, TW>(r[j], a, pc.c[j], lane);
         int e[TB];
@@ -1104,9 +1135,11 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
             for (int tb = 0; tb < TB; ++tb) {
                 if (tb * TPB >= tokens) break;
                 const v4i S = ones_mfma(r[j].a[tb]);
+                // A poisoned token (non-finite activations) yields NaN partials.
+                const float sc = e[tb] == kPoisonExp ? __builtin_nanf("") : exp2i(-e[tb] - 7);
 #pragma unroll
                 for (int tt = 0; tt < TW; ++tt)
-                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<4>(r[j].a[tb], S, r[j].w[tt], dw, e[tb]);
+                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<4>(r[j].a[tb], S, r[j].w[tt], dw, sc);
             }
         }
     };
@@ -1128,7 +1161,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
             val += wv * nq::load_f32(a.x, a.x_dtype, o.t * in + a.salient_indices[k]);
         }
         if (a.bias) val += elem_value(idx == threadIdx.x ? bias0 : load_elem(a.bias, a.bias_dtype, row), a.bias_dtype);
-        return val;
+        return stale ? __builtin_nanf("") : val;
     };
     if (TPB == 1 && a.residual) {
         // Residual epilogue (one token, outs <= 64: wave 0, lanes 16 tt + n):

@@ -67,6 +67,15 @@ __device__ __forceinline__ float range_scale(float bound) {
     return exp2i(e);
 }
 
+// Scale of a prepared row from its max |a s| and its sum of |a s|. The sum
+// is NaN or +Inf exactly when the row holds a NaN or an infinity (fmaxf
+// drops NaN, a sum does not); such a row is scaled by NaN, so every output of
+// the token is NaN, as the reference's fp32 forward yields (a non-finite
+// activation reaches every rank value with both signs; reference.py:208-217).
+__device__ __forceinline__ float prep_scale(float max_abs, float sum_abs) {
+    return sum_abs <= 3.402823466e38f ? range_scale(max_abs) : __builtin_nanf("");
+}
+
 // Position of column c in a prepared row: columns 1 and 2 of every group of
 // four are swapped (the order the sign operand's fp16 pairs come in).
 __device__ __forceinline__ int64_t swizzle4(int64_t c) { return (c & ~int64_t(3)) | ((c & 1) << 1) | ((c >> 1) & 1); }
@@ -143,9 +152,9 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ a
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off)), l1 += __shfl_xor(l1, off);
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m, wsum[threadIdx.x >> 6] = l1;
     __syncthreads();
-    const float scale = range_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
-    if (max_mid_bits && threadIdx.x == 0)
-        bound_scale_out[t] = range_scale(__uint_as_float(*max_mid_bits) * ((wsum[0] + wsum[1]) + (wsum[2] + wsum[3])));
+    const float l1t = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    const float scale = prep_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])), l1t);
+    if (max_mid_bits && threadIdx.x == 0) bound_scale_out[t] = range_scale(__uint_as_float(*max_mid_bits) * l1t);
     for (int64_t c = 8 * threadIdx.x; c < cols_pad; c += 8 * kBlock) {
         float v[8];
         if (c < cols) values(c, v);
@@ -237,9 +246,9 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows_vec(const void* __restrict
     for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off)), l1 += __shfl_xor(l1, off);
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m, wsum[threadIdx.x >> 6] = l1;
     __syncthreads();
-    const float scale = range_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
-    if (max_mid_bits && threadIdx.x == 0)
-        bound_scale_out[t] = range_scale(__uint_as_float(*max_mid_bits) * ((wsum[0] + wsum[1]) + (wsum[2] + wsum[3])));
+    const float l1t = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    const float scale = prep_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])), l1t);
+    if (max_mid_bits && threadIdx.x == 0) bound_scale_out[t] = range_scale(__uint_as_float(*max_mid_bits) * l1t);
 #pragma unroll
     for (int k = 0; k < NCH; ++k) {
         const int64_t c = 8 * threadIdx.x + 8 * kBlock * k;

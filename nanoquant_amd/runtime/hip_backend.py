@@ -232,6 +232,20 @@ class HipPackedBackend:
         desc.decode_launch = _DECODE_LAUNCH[decode_launch]
         return PreparedLayer(layer.backend_name, layer.backend_version, layer.spec, replace(payload, desc=desc))
 
+    def fused_launch_timed_out(self, layer: PreparedLayer) -> bool:
+        """True when a fused decode launch of this layer ever gave up waiting for
+        its stage-1 results (the sticky flag in the tiles header). Such a launch
+        stored NaN for the outputs of the workgroups that gave up, so a caller
+        that cannot check every call still sees the failure. Reads the flag
+        after synchronising the device: a diagnostic, not for the token loop."""
+
+        payload = self._payload(layer)
+        if payload.tiles is None:
+            return False
+        torch.cuda.synchronize(payload.device)
+        misc = int(_native.load().nq_tiles_header_bytes()) // 4 - 64
+        return int(payload.tiles.view(torch.int32)[misc].item()) != 0
+
     def _payload(self, layer: PreparedLayer) -> _HipPackedPayload:
         if (layer.backend_name, layer.backend_version) != (self.name, self.version):
             raise ValueError("prepared runtime layer belongs to a different backend")

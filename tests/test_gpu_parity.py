@@ -517,6 +517,100 @@ def test_fused_launch_alternating_grouping_keeps_launch_index():
     assert all(_sync_header_clean(layer) for layer in layers)
 
 
+def test_fused_wait_timeout_poisons_outputs_and_sets_flag():
+    """Forced from the host, with every kernel still exiting normally: the
+    header's spin limit is lowered to 16 polls and every stage-2 arrival
+    counter is advanced by three launches, so no stage-2 workgroup's target
+    launch is ever signalled. Each one gives up after 16 polls, stores NaN for
+    its outputs and sets the sticky flag."""
+
+    fused = HipPackedBackend(decode_launch="fused")
+    shape = syn.qwen3_8b_layer()[1]  # k_proj 4096 -> 1024 r819: 64 stage-2 tiles
+    state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 90)
+    layer = fused.prepare(state, "cuda")
+    x = syn.synthetic_activations(1, shape.in_features, seed=90, device="cuda")
+    good = fused.linear(x, layer)
+    assert not fused.fused_launch_timed_out(layer)
+    assert orc.relative_l2(good, orc.packed_forward(orc.operands_from_state(state), x.cpu())) <= REL_L2
+    # Header lines (256 bytes each; nq_decode_kernels.h): 16 ready slots, the
+    # ready root, 32 arrive slots (64-bit counters at the start of lines
+    # 17-48), 64 flag replicas, then the misc line (word 3: spin limit).
+    header = layer.payload.tiles[: int(_native.load().nq_tiles_header_bytes())]
+    lines = header.numel() // 256
+    assert lines == 16 + 1 + 32 + 64 + 1
+    counters, words = header.view(torch.int64), header.view(torch.int32)
+    tiles2 = -(-shape.out_features // 16)
+    for slot in range(32):
+        participants = tiles2 // 32 + (1 if slot < tiles2 % 32 else 0)
+        counters[(17 + slot) * 32] += 3 * participants
+    words[(lines - 1) * 64 + 3] = 16
+    _say("fused timeout forced", shape.name)
+    bad = fused.linear(x, layer)
+    torch.cuda.synchronize()
+    assert torch.isnan(bad).all()
+    assert fused.fused_launch_timed_out(layer)
+
+
+_PLANTS = (float("nan"), float("inf"), float("-inf"))
+
+
+def _nonfinite_inputs(tokens: int, width: int, seed: int, first: int = 0) -> torch.Tensor:
+    """bf16 activations with NaN, +Inf and -Inf planted at random columns of
+    token rows 0, 1, 2 (one token: only row 0, with _PLANTS[first]); with
+    more than eight tokens also row 5 (three infinities) and the last row."""
+
+    x = syn.synthetic_activations(tokens, width, seed=seed)
+    g = torch.Generator().manual_seed(seed)
+    rows = [0] if tokens == 1 else [r for r in (0, 1, 2) if r < tokens - 1]
+    for j, t in enumerate(rows):
+        x[t, int(torch.randint(0, width, (1,), generator=g))] = _PLANTS[(first + j) % 3]
+    if tokens > 8:
+        x[5, torch.randint(0, width, (3,), generator=g)] = float("inf")
+        x[tokens - 1, int(torch.randint(0, width, (1,), generator=g))] = float("nan")
+    return x
+
+
+@pytest.mark.parametrize("shape_index,tokens,first", [(1, 1, 0), (1, 1, 1), (6, 1, 2), (0, 4, 0), (4, 16, 0)])
+def test_nonfinite_activations_poison_their_tokens_decode(backend, shape_index, tokens, first):
+    """A NaN or an infinity in a token's activations makes every output of that
+    token non-finite (reference.py:208-235 in fp32); the other tokens keep
+    their values. Qwen3-8B layer shapes, decode token counts."""
+
+    shape = syn.qwen3_8b_layer()[shape_index]
+    _say("nonfinite decode", shape.name, tokens, _PLANTS[first])
+    state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 95 + shape_index, salient=4, bias=True)
+    x = _nonfinite_inputs(tokens, shape.in_features, seed=95 + tokens, first=first)
+    _check_nonfinite(backend, state, x)
+
+
+@pytest.mark.parametrize("shape_index,tokens", [(1, 64), (4, 129)])
+def test_nonfinite_activations_poison_their_tokens_prefill(backend, shape_index, tokens):
+    """Same contract on the prefill path (Llama-3-8B shapes, MFMA GEMMs)."""
+
+    shape = syn.llama3_8b_layer()[shape_index]
+    _say("nonfinite prefill", shape.name, tokens)
+    state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 96 + shape_index, salient=4)
+    x = _nonfinite_inputs(tokens, shape.in_features, seed=96 + tokens)
+    _check_nonfinite(backend, state, x)
+
+
+def _check_nonfinite(backend, state, x):
+    expected = orc.packed_forward(orc.operands_from_state(state), x)
+    layer = backend.prepare(state, "cuda")
+    actual = backend.linear(x.cuda(), layer).cpu()
+    bad_rows = ~torch.isfinite(x.float()).all(dim=1)
+    assert bad_rows.any() and (x.shape[0] == 1 or not bad_rows.all())
+    assert torch.equal(torch.isfinite(actual), torch.isfinite(expected))
+    assert not torch.isfinite(actual[bad_rows]).any()
+    if (~bad_rows).any():
+        # Full layer shapes: the relative-L2 bar on every path (outputs are
+        # sums of thousands of terms, so the small fixtures' elementwise
+        # atol does not apply).
+        err = orc.relative_l2(actual[~bad_rows], expected[~bad_rows])
+        print(f"  finite rows rel_l2={err:.2e}", flush=True)
+        assert err <= REL_L2, err
+
+
 def test_batch_rejects_mixed_launch_structures():
     state = syn.synthetic_packed_layer(syn.qwen3_8b_layer()[1], seed=3)
     split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
