@@ -49,8 +49,13 @@ typedef enum nq_status {
     NQ_ERR_WORKSPACE = -5,   /* workspace smaller than nq_linear_workspace_bytes */
     NQ_ERR_LAUNCH = -6,      /* hipLaunchKernel / hipGetLastError failure    */
     NQ_ERR_DEVICE = -7,      /* no HIP device or wrong architecture          */
-    NQ_ERR_UNSUPPORTED = -8  /* valid request this build does not implement  */
+    NQ_ERR_UNSUPPORTED = -8, /* valid request this build does not implement  */
+    NQ_ERR_SCRATCH = -9      /* nq_linear_static: the call needs more than
+                                NQ_STATIC_SCRATCH_BYTES of workspace         */
 } nq_status;
+
+/* Size of the per-device static scratch array of nq_linear_static (4 MiB). */
+#define NQ_STATIC_SCRATCH_BYTES (4 << 20)
 
 /* Launch structure of the tiled decode path (tokens <= 16).
  *   NQ_DECODE_SPLIT: two kernels per call (stage 1 writes the rank-r
@@ -204,6 +209,18 @@ int64_t nq_linear_workspace_bytes(const nq_linear_desc* desc, int64_t tokens);
 int nq_linear(const nq_linear_desc* desc, const void* x, int32_t x_dtype,
               int64_t tokens, void* y, int32_t y_dtype, void* workspace,
               int64_t workspace_bytes, void* stream);
+
+/* nq_linear without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation). No reference counterpart. The workspace is a
+ * file-scope device array of NQ_STATIC_SCRATCH_BYTES per GPU, held until the
+ * process ends; calls whose nq_linear_workspace_bytes exceeds it return
+ * NQ_ERR_SCRATCH (decode token counts fit any Qwen3/Llama-sized layer;
+ * larger prefill calls need nq_linear). Allocates nothing itself. All calls
+ * on one GPU share the array: calls that overlap in time on one GPU race and
+ * must not be issued (one stream, or streams ordered by the caller). */
+int nq_linear_static(const nq_linear_desc* desc, const void* x, int32_t x_dtype,
+                     int64_t tokens, void* y, int32_t y_dtype, void* stream);
 
 /* One launch for `count` (1..8) packed linears with the same token count
  * (1..16) and dtypes: y_i = linear_i(x_i). Inputs may alias (Q/K/V or gate/up

@@ -23,6 +23,8 @@ NQ_ERR_WORKSPACE = -5
 NQ_ERR_LAUNCH = -6
 NQ_ERR_DEVICE = -7
 NQ_ERR_UNSUPPORTED = -8
+NQ_ERR_SCRATCH = -9
+NQ_STATIC_SCRATCH_BYTES = 4 << 20
 
 NQ_DECODE_SPLIT = 0
 NQ_DECODE_FUSED = 1
@@ -48,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "nq_prepare_tiles",
     "nq_linear_workspace_bytes",
     "nq_linear",
+    "nq_linear_static",
     "nq_linear_batch",
     "nq_linear_batch_fused",
     "nq_decode_mixed_v_words",
@@ -170,6 +173,7 @@ def _declare(lib: ctypes.CDLL) -> None:
             c_int,
             [desc_p, vp, ctypes.c_int32, c_i64, vp, ctypes.c_int32, vp, c_i64, vp],
         ),
+        "nq_linear_static": (c_int, [desc_p, vp, ctypes.c_int32, c_i64, vp, ctypes.c_int32, vp]),
         "nq_linear_batch": (
             c_int,
             [ctypes.POINTER(desc_p), ctypes.c_int32, ctypes.POINTER(vp), ctypes.c_int32, c_i64,
