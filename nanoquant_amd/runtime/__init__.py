@@ -18,6 +18,9 @@ from nanoquant_amd.runtime.hip_backend import (
     HIP_PACKED_BACKEND_NAME,
     HIP_PACKED_BACKEND_VERSION,
     HipPackedBackend,
+    HipProjectionGroup,
+    grouped_hip_projection,
+    prepare_hip_projection_group,
     unpack_sign_matrix_device,
 )
 from nanoquant_amd.runtime.logical import (

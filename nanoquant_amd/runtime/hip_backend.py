@@ -496,6 +496,65 @@ class HipPackedBackend:
         return out
 
 
+@dataclass(frozen=True, slots=True)
+class HipProjectionGroup:
+    """Prepared layers that read the same input (Q/K/V, gate/up), run as one
+    decode launch pair. Holds the layers themselves: no device copies."""
+
+    device: torch.device
+    layers: tuple[PreparedLayer, ...]
+    ranks: tuple[int, ...]
+    output_features: tuple[int, ...]
+
+
+def prepare_hip_projection_group(layers: tuple[PreparedLayer, ...]) -> HipProjectionGroup | None:
+    """Group prepared HIP layers that share one input, or None when they cannot
+    share a launch: fewer than 2 or more than 8 layers, a layer that is not a
+    tiled HIP layer, repeated layers, or different devices or input widths.
+
+    Same name, argument and None-for-incompatible contract as the reference's
+    prepare_cuda_projection_group (src/nanoquant/runtime/cuda_backend.py:65-120),
+    without its restrictions (ranks and output widths that are multiples of 8,
+    salient columns required, no bias or salient scales): the launch takes any
+    rank, such as Qwen3 k/v's 819, and every sidecar."""
+
+    layers = tuple(layers)
+    if not 2 <= len(layers) <= 8 or len({id(layer) for layer in layers}) != len(layers):
+        return None
+    keys = {(layer.backend_name, layer.backend_version) for layer in layers}
+    if keys != {(HIP_PACKED_BACKEND_NAME, HIP_PACKED_BACKEND_VERSION)}:
+        return None
+    payloads = [layer.payload for layer in layers]
+    if not all(isinstance(p, _HipPackedPayload) and p.tiles is not None for p in payloads):
+        return None
+    if len({p.device for p in payloads}) != 1 or len({layer.spec.in_features for layer in layers}) != 1:
+        return None
+    if len({p.desc.decode_launch for p in payloads}) != 1:
+        return None
+    return HipProjectionGroup(
+        payloads[0].device,
+        layers,
+        tuple(layer.spec.rank for layer in layers),
+        tuple(layer.spec.out_features for layer in layers),
+    )
+
+
+def grouped_hip_projection(value: torch.Tensor, group: HipProjectionGroup) -> tuple[torch.Tensor, ...]:
+    """Every layer of `group` applied to `value` ([..., in], f16/bf16/f32): fp32
+    outputs ``[..., out_i]`` in group order, as grouped_cuda_projection returns
+    (src/nanoquant/runtime/cuda_backend.py:123-144). Token counts 1-16 run as
+    one decode launch pair for the whole group (nq_linear_batch); larger
+    counts run each layer's prefill call."""
+
+    if value.device != group.device:
+        raise ValueError("grouped HIP projection input uses a different device")
+    backend = HipPackedBackend()
+    tokens = value.numel() // max(value.shape[-1], 1) if value.ndim else 0
+    if 1 <= tokens <= 16:
+        return tuple(backend.linear_batch([value] * len(group.layers), list(group.layers)))
+    return tuple(backend.linear(value, layer) for layer in group.layers)
+
+
 def _check_value(value: torch.Tensor, spec: QuantizedLinearSpec, device: torch.device) -> None:
     if value.device != device:
         raise ValueError("HIP packed input and prepared layer must use the same device")

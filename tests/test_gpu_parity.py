@@ -27,7 +27,9 @@ from nanoquant_amd.runtime import (
     QuantizedLinearSpec,
     WorkloadSpec,
     execution_workload,
+    grouped_hip_projection,
     pack_logical_layer,
+    prepare_hip_projection_group,
     pack_sign_matrix,
     unpack_sign_matrix_device,
 )
@@ -609,6 +611,69 @@ def _check_nonfinite(backend, state, x):
         err = orc.relative_l2(actual[~bad_rows], expected[~bad_rows])
         print(f"  finite rows rel_l2={err:.2e}", flush=True)
         assert err <= REL_L2, err
+
+
+def _group_member(index: int, rank: int, out_features: int) -> LogicalLayerState:
+    """A 64-input member with two bf16 salient columns (1 and 7, s_in zero
+    there), the geometry of the reference's grouped-projection test
+    (tests/unit/test_runtime_cuda_backend.py:152-195, ranks 32/40/48, outputs
+    24/16/32)."""
+
+    g = torch.Generator().manual_seed(700 + index)
+    spec = QuantizedLinearSpec(f"blocks.0.self_attn.group_{index}", "nanoquant-v1", 64, out_features, rank,
+                               "float32", "bfloat16", outlier_count=2, outlier_value_dtype="bfloat16")
+    signs = lambda r, c: torch.where(torch.rand(r, c, generator=g) < 0.5, -1.0, 1.0)  # noqa: E731
+    left, right = signs(out_features, rank), signs(rank, 64)
+    pre = torch.randn(64, generator=g).bfloat16()
+    idx = torch.tensor([1, 7], dtype=torch.int32)
+    pre[idx.long()] = 0
+    return LogicalLayerState(spec, left, right, pre, torch.randn(rank, generator=g).bfloat16(),
+                             torch.randn(out_features, generator=g).bfloat16(), outlier_indices=idx,
+                             outlier_values=torch.randn(out_features, 2, generator=g).bfloat16())
+
+
+@pytest.mark.parametrize("group_count", [2, 3])
+def test_grouped_projection_entry_points(group_count):
+    """prepare_hip_projection_group / grouped_hip_projection: within the
+    rel-L2 bar of the oracle, and bit-identical to the same layers run one by
+    one and through linear_batch (one launch pair for the group)."""
+
+    backend = HipPackedBackend()
+    states = [pack_logical_layer(_group_member(i, r, o)) for i, (r, o) in enumerate([(32, 24), (40, 16), (48, 32)])]
+    layers = tuple(backend.prepare(st, "cuda") for st in states[:group_count])
+    group = prepare_hip_projection_group(layers)
+    assert group is not None and group.ranks == tuple(st.spec.rank for st in states[:group_count])
+    value = torch.randn(1, 1, 64, generator=torch.Generator().manual_seed(99)).cuda()
+    actual = grouped_hip_projection(value, group)
+    assert len(actual) == group_count
+    batch = backend.linear_batch([value] * group_count, list(layers))
+    for out, layer, state, whole in zip(actual, layers, states, batch):
+        assert out.shape == (1, 1, state.spec.out_features) and out.dtype == torch.float32
+        assert torch.equal(out, backend.linear(value, layer))
+        assert torch.equal(out, whole)
+        err = orc.relative_l2(out, orc.packed_forward(orc.operands_from_state(state), value.cpu()))
+        assert err <= REL_L2, err
+    assert prepare_hip_projection_group(layers[:1]) is None
+    assert prepare_hip_projection_group((layers[0], layers[0])) is None
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 64])
+def test_grouped_projection_qwen3_qkv_and_gate_up(tokens):
+    """Qwen3-8B Q/K/V (ranks 2048/819/819, which the reference's grouped path
+    rejects) and gate/up through the grouped entry points; 64 tokens run each
+    member's prefill call."""
+
+    backend = HipPackedBackend()
+    shapes = syn.qwen3_8b_layer()
+    for members in ((0, 1, 2), (4, 5)):
+        states = [syn.synthetic_packed_layer(shapes[i], seed=syn.BASE_SEED + 120 + i) for i in members]
+        group = prepare_hip_projection_group(tuple(backend.prepare(st, "cuda") for st in states))
+        assert group is not None
+        x = syn.synthetic_activations(tokens, 4096, seed=120 + tokens)
+        _say("grouped qwen", members, tokens)
+        for out, state in zip(grouped_hip_projection(x.cuda(), group), states):
+            err = orc.relative_l2(out, orc.packed_forward(orc.operands_from_state(state), x))
+            assert err <= REL_L2, (state.spec.name, err)
 
 
 def test_batch_rejects_mixed_launch_structures():

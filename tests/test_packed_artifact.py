@@ -197,3 +197,88 @@ def test_loaded_layer_runs_on_hip_backend(tmp_path: Path):
         x = syn.synthetic_activations(4, state.spec.in_features, seed=3)
         y = backend.linear(x.to(device), layer)
         assert orc.relative_l2(y, orc.packed_forward(orc.operands_from_state(state), x)) <= 2e-3
+
+
+# --- an artifact written by the reference's own writer --------------------------------
+#
+# tests/golden/reference_artifact/ was written by the reference's
+# write_packed_artifact and pack_logical_layer (tests/golden/make_artifact_fixture.py)
+# from the dense layers of tests/golden/artifact_recipe.py.
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+REFERENCE_ARTIFACT = GOLDEN / "reference_artifact"
+
+
+def _recipe_states():
+    import sys
+
+    sys.path.insert(0, str(GOLDEN))
+    from artifact_recipe import LAYERS, dense_layer
+
+    states = []
+    for i in range(len(LAYERS)):
+        kwargs = dense_layer(i)
+        spec = QuantizedLinearSpec(**kwargs.pop("spec_args"))
+        states.append(pack_logical_layer(LogicalLayerState(spec, **kwargs)))
+    return states
+
+
+_ROLES = ("left_words", "right_words", "scale_pre", "scale_mid", "scale_post", "bias", "outlier_indices",
+          "outlier_values", "outlier_scales", "patch_left", "patch_right")
+
+
+def test_reference_written_artifact_opens_and_loads_exactly():
+    """The loader accepts the reference writer's manifest and shards (strict
+    field check, sizes, SHA-256, tensor headers) and each loaded layer equals
+    this package's packing of the same dense layer: words bit for bit,
+    scales and sidecars value for value, same spec."""
+
+    artifact = open_packed_artifact(REFERENCE_ARTIFACT)
+    manifest = json.loads((REFERENCE_ARTIFACT / "nanoquant-packed-model.json").read_text())
+    assert manifest["layer_count"] == 3 and len(manifest["blocks"]) == 2
+    for expected in _recipe_states():
+        loaded = artifact.load_layer(expected.spec.name)
+        assert loaded.spec == expected.spec
+        for role in _ROLES:
+            a, b = getattr(loaded, role), getattr(expected, role)
+            assert (a is None) == (b is None), role
+            if a is not None:
+                assert a.dtype == b.dtype and torch.equal(a, b), (expected.spec.name, role)
+
+
+def test_reference_written_artifact_rejects_a_flipped_shard_byte(tmp_path: Path):
+    import shutil
+
+    copy = tmp_path / "artifact"
+    shutil.copytree(REFERENCE_ARTIFACT, copy)
+    shard = copy / "weights" / "block-00001.safetensors"
+    data = bytearray(shard.read_bytes())
+    data[-1] ^= 1
+    shard.write_bytes(bytes(data))
+    with pytest.raises(PackedArtifactError, match="hash"):
+        open_packed_artifact(copy)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not gpu_available(), reason="needs a HIP device")
+@pytest.mark.parametrize("tokens", [1, 5, 40])
+def test_reference_written_artifact_runs_on_hip_backend(tokens):
+    """Every layer of the reference-written artifact, loaded to the device and
+    run on the HIP backend (decode and prefill token counts), against the oracle."""
+
+    from nanoquant_amd.runtime import HipPackedBackend
+    from oracle import nq_oracle as orc
+
+    artifact = open_packed_artifact(REFERENCE_ARTIFACT)
+    device = torch.device("cuda", 0)
+    for backend in (HipPackedBackend(), HipPackedBackend(tiled_decode=False)):
+        for i, name in enumerate(layer.spec.name for block in artifact.manifest.blocks for layer in block.layers):
+            state = artifact.load_layer(name, device)
+            layer = backend.prepare(state, device)
+            g = torch.Generator().manual_seed(tokens * 10 + i)
+            x = torch.randn(tokens, state.spec.in_features, generator=g).to(torch.bfloat16)
+            y = backend.linear(x.to(device), layer)
+            expected = orc.packed_forward(orc.operands_from_state(artifact.load_layer(name)), x)
+            err = orc.relative_l2(y, expected)
+            print(f"  {name} M={tokens} tiled={backend._tiled_decode} rel_l2={err:.2e}", flush=True)
+            assert err <= 2e-3, (name, tokens, err)

@@ -37,6 +37,7 @@ from nanoquant_amd.runtime import (
     packed_row_stride_bytes,
     choose_backends,
     packed_word_count,
+    prepare_hip_projection_group,
     supports_vector_word_loads,
     unpack_sign_matrix,
 )
@@ -312,3 +313,13 @@ def test_prepared_linear_binding_and_context():
         model.mlp.up(torch.ones(1, 4))
     with execution_workload("decode"):
         assert model.mlp.up(torch.ones(1, 4)).shape == (1, 3)
+
+
+def test_projection_group_declines_layers_it_cannot_launch_together():
+    """prepare_hip_projection_group answers None (the reference's contract for
+    an incompatible group) for foreign payloads and wrong member counts."""
+
+    foreign = [PreparedLayer("torch-packed-reference", "1", _spec(f"blocks.0.p{i}"), object()) for i in range(3)]
+    assert prepare_hip_projection_group(tuple(foreign)) is None
+    assert prepare_hip_projection_group(tuple(foreign[:1])) is None
+    assert prepare_hip_projection_group(tuple(foreign * 3)) is None
