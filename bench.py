@@ -1,15 +1,30 @@
 #!/usr/bin/env python
-"""Decode throughput of a Qwen3-8B-shaped packed-linear stack on one MI355X.
+"""Decode throughput of a Qwen3-8B-shaped packed model on one MI355X, with
+every configuration of the workload measured beside it.
 
-Workload (one "step" = one decode token through every packed linear of the
-model): 36 decoder layers x 7 packed binary low-rank linears at ~1.0 bpw
-(q/o 4096->4096 r2048, k/v 4096->1024 r819, gate/up 4096->12288 r3072,
-down 12288->4096 r3072), 874.9 MB of distinct packed weights (well above the
-256 MB Infinity Cache), synthetic Bernoulli(0.5) signs, fp16 lognormal scales,
-bf16 N(0,1) activations resident in HBM, fp32 outputs (the backend boundary).
-The step is captured once in a HIP graph and replayed.
+Headline (``value``): median greedy-decode tok/s of a random-init
+Qwen3-8B-shaped model (36 layers, hidden 4096, intermediate 12288, GQA 32/8
+x 128, vocab 151936; all 252 projections packed binary low-rank at ~1.0 bpw,
+bf16 N(0, 0.02) embeddings / untied lm_head / KV cache), 512-id prompt, 128
+greedy tokens, batch 1, each decode step one HIP-graph replay.
 
-Prints one JSON line (metric/value/unit, ms_per_step, roofline, cpu_baseline).
+Beside it, each with p10/p50/p90 over at least 10 repetitions:
+  config1  Gemma-3-1B gate 1152->6912 r768, one token;
+  config2  the seven Qwen3-8B linears per call and per layer at 1, 4 and 16
+           tokens, the 36-layer decode stack in several launch groupings, and
+           the dominant call (gate/up batch) that ``roofline`` reports;
+  config3  the Llama-3-8B prefill sweep (64 to 2048 tokens, MFMA GEMMs);
+  config4  Gemma-3-4B down 10240->2560 r1536 with a 26-entry int8 sidecar in
+           column and row form at 1 and 8 tokens;
+  copy     the measured streaming ceiling of plain device copies and reads.
+Per-call figures rotate over replicas of the layer's weights (at least
+512 MB, twice the 256 MB Infinity Cache) so the bytes come from HBM.
+
+CPU baselines (the oracle's restatement of the reference's CPU torch path:
+unpack once to fp32 +-1, two fp32 F.linear) run on the host cores for each
+configuration; ``cpu_baseline`` is the config-5 one.
+
+Prints ONE JSON line.
 """
 
 from __future__ import annotations
@@ -20,6 +35,7 @@ import os
 import platform
 import sys
 import time
+from dataclasses import replace
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -27,33 +43,38 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+FP16_DENSE_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+REPLICA_BYTES = 512 << 20  # distinct weight bytes a per-call measurement rotates over
 TRAFFIC_PROFILE = ROOT / "profiles" / "decode_qwen3_8b_m1_hbm_traffic.md"
 METRIC = "decode tok/s (Qwen3-8B-shape, ~1bpw); packed GEMV HBM GB/s vs peak"
+# Published reference figure (RTX 4000 Ada Laptop, Triton two-stage kernel,
+# Gemma-3-1B gate 1152->6912, one token, median): evidence/m6/README.md:299.
+REFERENCE_GEMMA_GATE_DECODE_MS = 0.141
 
 
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--steps", type=int, default=10, help="timed repetitions of every figure (>= 10 for percentiles)")
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--layers", type=int, default=36)
-    p.add_argument("--tokens", type=int, default=1, help="decode token slots per step (1-16)")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
-    p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-graph", action="store_true", help="time eager launches instead of a graph")
     p.add_argument("--modes", default="grouped,grouped-fused,single,layer",
-                   help="comma-separated decode launch groupings to time (first one is the headline)")
-    p.add_argument("--prefill-tokens", default="64,256,512,2048",
-                   help="token counts of the Llama-3-8B prefill sweep ('' to skip)")
+                   help="launch groupings of the 36-layer decode stack")
+    p.add_argument("--prefill-tokens", default="64,256,512,2048", help="config-3 token counts ('' to skip)")
+    p.add_argument("--e2e-tokens", type=int, default=128, help="greedy tokens of the config-5 run (0 to skip)")
+    p.add_argument("--e2e-prompt", type=int, default=512)
+    p.add_argument("--skip", default="", help="comma-separated sections to skip: config1..config5,copy,cpu")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 10 times (byte-counter calibration) and exit")
-    p.add_argument("--e2e-tokens", type=int, default=128,
-                   help="greedy tokens of the end-to-end decoder run (0 to skip)")
-    p.add_argument("--e2e-prompt", type=int, default=512, help="prompt length of the end-to-end run")
     p.add_argument("--dominant-only", action="store_true",
                    help="only launch the dominant call (gate/up batch) of every layer eagerly --steps times "
                         "(per-dispatch counter collection) and exit")
     return p.parse_args(argv)
+
+
+def _say(*parts) -> None:
+    print("[bench]", *parts, file=sys.stderr, flush=True)
 
 
 def _cpu_model() -> str:
@@ -66,6 +87,193 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def pct(samples) -> dict:
+    """p10 / p50 / p90 (linear interpolation between order statistics) and the
+    count of a list of samples."""
+
+    xs = sorted(float(s) for s in samples)
+    if not xs:
+        raise ValueError("no samples")
+
+    def q(f: float) -> float:
+        pos = f * (len(xs) - 1)
+        lo = int(pos)
+        hi = min(lo + 1, len(xs) - 1)
+        return xs[lo] + (xs[hi] - xs[lo]) * (pos - lo)
+
+    return {"p10": q(0.1), "p50": q(0.5), "p90": q(0.9), "n": len(xs)}
+
+
+def _scaled(d: dict, f, digits: int = 3) -> dict:
+    """A percentile dict mapped through a monotonic function f (order kept when
+    f is decreasing: p10 of a rate is f of p90 of a time)."""
+
+    vals = [f(d["p10"]), f(d["p50"]), f(d["p90"])]
+    vals.sort()
+    return {"p10": round(vals[0], digits), "p50": round(vals[1], digits), "p90": round(vals[2], digits)}
+
+
+# --- algorithmic units ---------------------------------------------------------------
+
+
+def algorithmic_bytes(shape, tokens: int, ybytes: int = 4, sidecar: int = 0) -> int:
+    """Sign words + fp16 scales + bf16 x + y (+ sidecar); the rank intermediate is excluded."""
+
+    return shape.weight_bytes + sidecar + 2 * tokens * shape.in_features + ybytes * tokens * shape.out_features
+
+
+def _sidecar_bytes(state) -> int:
+    """Column form: out*k int8 + 4k indices + 2k scales; row form: k*in + 4k + 2k."""
+
+    from nanoquant_amd.runtime import RowSidecarLayerState
+
+    if isinstance(state, RowSidecarLayerState):
+        k = int(state.rows.indices.numel())
+        return k * state.spec.in_features + 6 * k
+    k = state.spec.outlier_count
+    return k * state.spec.out_features + 6 * k if k else 0
+
+
+# --- timing helpers ------------------------------------------------------------------
+
+
+def graph_reps(run, reps: int, warmup: int) -> list[float]:
+    """Capture `run` once in a HIP graph on a side stream, replay it `warmup`
+    times, then time `reps` replays one by one with events recorded on that
+    stream. Returns ms per replay."""
+
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()  # allocations (workspaces) happen outside the capture
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            run()
+        for _ in range(warmup):
+            graph.replay()
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        marks[0].record(side)
+        for i in range(reps):
+            graph.replay()
+            marks[i + 1].record(side)
+    marks[-1].synchronize()
+    return [marks[i].elapsed_time(marks[i + 1]) for i in range(reps)]
+
+
+def replicas(backend, layer, count: int, *, sidecars: bool = False):
+    """`count` prepared layers with the same values but distinct device copies
+    of the tile layout (and, with `sidecars`, of the salient / row sidecar
+    values), so a graph that rotates over them streams count x the weight
+    bytes. The canonical words and scales stay shared (the decode and prefill
+    kernels read the tiles)."""
+
+    import torch
+
+    from nanoquant_amd.runtime import PreparedLayer
+    from nanoquant_amd.runtime import _native
+
+    out = [layer]
+    p = layer.payload
+    torch.cuda.synchronize()
+    for _ in range(count - 1):
+        tiles = p.tiles.clone()
+        desc = _native.LinearDesc.from_buffer_copy(p.desc)
+        desc.tiles = tiles.data_ptr()
+        extra = {}
+        if sidecars and p.outlier_values is not None:
+            extra["outlier_values"] = p.outlier_values.clone()
+            desc.salient_values = extra["outlier_values"].data_ptr()
+        if sidecars and p.row_values is not None:
+            extra["row_values"] = p.row_values.clone()
+            desc.row_values = extra["row_values"].data_ptr()
+        out.append(PreparedLayer(layer.backend_name, layer.backend_version, layer.spec,
+                                 replace(p, tiles=tiles, desc=desc, **extra)))
+    return out
+
+
+def replica_count(weight_bytes: int) -> int:
+    return max(2, -(-REPLICA_BYTES // weight_bytes))
+
+
+def per_call(backend, layers, x, out, reps: int, warmup: int) -> list[float]:
+    """ms per call of a graph that runs each replica once on (x, out)."""
+
+    def run():
+        for layer in layers:
+            backend.linear_into(x, layer, out=out)
+
+    return [t / len(layers) for t in graph_reps(run, reps, warmup)]
+
+
+def call_figures(shape, tokens: int, call_ms: list[float], sidecar: int = 0) -> dict:
+    """Per-call figure: time percentiles, algorithmic bytes, GB/s and the
+    fraction of the HBM peak (at the median)."""
+
+    d = pct(call_ms)
+    b = algorithmic_bytes(shape, tokens, sidecar=sidecar)
+    return {
+        "us": _scaled(d, lambda ms: ms * 1e3),
+        "bytes": b,
+        "gbs": _scaled(d, lambda ms: b / (ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(b / (d["p50"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "reps": d["n"],
+    }
+
+
+# --- copy ceiling ----------------------------------------------------------------------
+
+
+SINK_SLOTS = 8192  # workgroups of one nq_read_stream launch, at most
+
+
+def copy_ceiling(reps: int, warmup: int) -> dict:
+    """Measured streaming ceilings: device-to-device copies (torch copy_, read
+    + write bytes) and reads with the decode kernels' load pattern
+    (nq_read_stream), at the dominant decode call's size, at the Infinity
+    Cache size and at 1 GiB, rotated over distinct buffers so at least 512 MB
+    stream per replay (the small sizes)."""
+
+    import torch
+
+    from nanoquant_amd.runtime import _native
+
+    res = {}
+    for label, size in (("12.8MB", 12_775_424), ("256MiB", 256 << 20), ("1GiB", 1 << 30)):
+        count = max(1, -(-REPLICA_BYTES // size)) if size < MALL_BYTES else 2
+        n = size // 4
+        srcs = [torch.ones(n, dtype=torch.float32, device="cuda") for _ in range(count)]
+        dsts = [torch.empty_like(s) for s in srcs]
+        sink = torch.zeros(count, SINK_SLOTS, dtype=torch.int32, device="cuda")
+        lib = _native.load()
+
+        def copies():
+            for s, d in zip(srcs, dsts):
+                d.copy_(s)
+
+        def reads():
+            stream = torch.cuda.current_stream().cuda_stream
+            for i, s in enumerate(srcs):
+                _native.check("nq_read_stream", lib.nq_read_stream(s.data_ptr(), size, sink[i].data_ptr(),
+                                                                   SINK_SLOTS, stream))
+
+        c = pct([t / count for t in graph_reps(copies, reps, warmup)])
+        r = pct([t / count for t in graph_reps(reads, reps, warmup)])
+        res[label] = {
+            "copy_gbs": _scaled(c, lambda ms: 2 * size / (ms * 1e-3) / 1e9, 1),
+            "read_gbs": _scaled(r, lambda ms: size / (ms * 1e-3) / 1e9, 1),
+            "copy_us": _scaled(c, lambda ms: ms * 1e3),
+            "read_us": _scaled(r, lambda ms: ms * 1e3),
+        }
+        del srcs, dsts
+        torch.cuda.empty_cache()
+    return {"workload": "torch copy_ (read+write bytes) and nq_read_stream (read bytes) over distinct buffers, "
+                        "one HIP graph per size", "points": res}
+
+
+# --- config 2: the Qwen3-8B stack ----------------------------------------------------------
+
 # Launch grouping per decoder layer (indices into the seven projections):
 #   grouped: decode dependency order - Q/K/V share x, O, gate/up share x, down;
 #   single:  one launch per linear;
@@ -77,16 +285,15 @@ GROUPINGS = {
     "single": ((0,), (1,), (2,), (3,), (4,), (5,), (6,)),
     "layer": ((0, 1, 2, 3, 4, 5, 6),),
 }
+INPUT_KEY = {"q_proj": "attn", "k_proj": "attn", "v_proj": "attn", "o_proj": "o",
+             "gate_proj": "mlp", "up_proj": "mlp", "down_proj": "down"}
+# The dominant decode call: the gate/up batch (two 4096 -> 12288 linears that
+# share x), the largest byte count of any call in a decode step.
+DOMINANT_GROUP = (4, 5)
 
 
-def _grouping(mode: str):
-    return GROUPINGS[mode.removesuffix("-fused")]
-
-
-def build_stack(layers: int, tokens: int, device):
-    """Prepared layers plus resident inputs/outputs for every linear of a step."""
-
-    import torch
+def build_layers(layers: int, device):
+    """Prepared layers of a `layers`-deep Qwen3-8B stack: [layer][7] of (shape, prepared)."""
 
     from nanoquant_amd import synthetic as syn
     from nanoquant_amd.runtime import HipPackedBackend
@@ -94,122 +301,452 @@ def build_stack(layers: int, tokens: int, device):
     backend = HipPackedBackend()
     stack = []
     for layer in range(layers):
-        shapes = syn.qwen3_8b_layer(layer)
-        inputs = {}
-        entries = []
-        for i, shape in enumerate(shapes):
+        row = []
+        for i, shape in enumerate(syn.qwen3_8b_layer(layer)):
             state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 1000 * layer + i, device=device)
-            prepared = backend.prepare(state, device)
-            role = shape.name.split(".")[-1]
-            key = {"q_proj": "attn", "k_proj": "attn", "v_proj": "attn", "o_proj": "o",
-                   "gate_proj": "mlp", "up_proj": "mlp", "down_proj": "down"}[role]
-            if key not in inputs:
-                inputs[key] = syn.synthetic_activations(
-                    tokens, shape.in_features, seed=layer * 10 + i, device=device)
-            out = torch.empty(tokens, shape.out_features, dtype=torch.float32, device=device)
-            entries.append((shape, prepared, inputs[key], out))
-        stack.append(entries)
+            row.append((shape, backend.prepare(state, device)))
+        stack.append(row)
     return backend, stack
 
 
-def step_calls(stack, mode: str, backend=None):
-    """The calls of one step: a list of member lists."""
+def stack_io(stack, tokens: int, device):
+    """Resident inputs (shared as in a decoder: Q/K/V and gate/up read one x)
+    and fp32 outputs for every linear of the stack: [layer][7] of
+    (shape, prepared, x, out)."""
 
-    calls = [[entries[i] for i in group] for entries in stack for group in _grouping(mode)]
+    import torch
+
+    from nanoquant_amd import synthetic as syn
+
+    entries = []
+    for layer, row in enumerate(stack):
+        inputs, items = {}, []
+        for i, (shape, prepared) in enumerate(row):
+            key = INPUT_KEY[shape.name.split(".")[-1]]
+            if key not in inputs:
+                inputs[key] = syn.synthetic_activations(tokens, shape.in_features, seed=layer * 10 + i, device=device)
+            out = torch.empty(tokens, shape.out_features, dtype=torch.float32, device=device)
+            items.append((shape, prepared, inputs[key], out))
+        entries.append(items)
+    return entries
+
+
+def step_calls(entries, mode: str, backend):
+    calls = [[row[i] for i in group] for row in entries for group in GROUPINGS[mode.removesuffix("-fused")]]
     if mode.endswith("-fused"):
-        calls = [[(shape, backend.with_decode_launch(prepared, "fused"), x, out)
-                  for shape, prepared, x, out in members] for members in calls]
+        calls = [[(shape, backend.with_decode_launch(prepared, "fused"), x, out) for shape, prepared, x, out in members]
+                 for members in calls]
     return calls
 
 
-def run_step(backend, calls):
+def run_calls(backend, calls):
     for members in calls:
         if len(members) == 1:
             _shape, prepared, x, out = members[0]
             backend.linear_into(x, prepared, out=out)
         else:
-            backend.linear_batch([m[2] for m in members], [m[1] for m in members],
-                                 outs=[m[3] for m in members])
+            backend.linear_batch([m[2] for m in members], [m[1] for m in members], outs=[m[3] for m in members])
 
 
-def time_mode(backend, stack, mode: str, steps: int, warmup: int, use_graph: bool) -> dict:
-    """Capture one step of `mode` in a HIP graph, replay `warmup` + `steps` times;
-    events bracket the timed region."""
-
-    import torch
-
-    calls = step_calls(stack, mode, backend)
-    replay = lambda: run_step(backend, calls)  # noqa: E731
-    if use_graph:
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            run_step(backend, calls)
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            run_step(backend, calls)
-        replay = graph.replay
-    for _ in range(warmup):
-        replay()
-    torch.cuda.synchronize()
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    wall0 = time.perf_counter()
-    start.record()
-    for _ in range(steps):
-        replay()
-    stop.record()
-    torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - wall0) * 1e3
-    ms_per_step = max(start.elapsed_time(stop), wall_ms) / steps
+def time_stack(backend, entries, mode: str, reps: int, warmup: int) -> dict:
+    calls = step_calls(entries, mode, backend)
     tokens = calls[0][0][2].shape[0]
+    step = pct(graph_reps(lambda: run_calls(backend, calls), reps, warmup))
     step_bytes = sum(algorithmic_bytes(m[0], tokens) for members in calls for m in members)
-    call_ms = ms_per_step / len(calls)
+    kernels = len(calls) * (1 if mode.endswith("-fused") else 2)
+    ms = step["p50"]
     return {
-        "ms_per_step": ms_per_step,
+        "ms_per_step": _scaled(step, lambda v: v, 4),
+        "tok_per_s": _scaled(step, lambda v: tokens * 1000.0 / v, 2),
         "calls_per_step": len(calls),
-        "kernels_per_step": len(calls) * (1 if mode.endswith("-fused") else 2),
+        "kernels_per_step": kernels,
         "step_bytes": step_bytes,
-        "mean_call_us": call_ms * 1e3,
-        "bytes_per_call": step_bytes / len(calls),
-        "achieved_gbs": step_bytes / len(calls) / (call_ms * 1e-3) / 1e9,
+        "mean_call_us": round(ms * 1e3 / len(calls), 3),
+        "achieved_gbs": round(step_bytes / (ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "reps": step["n"],
     }
 
 
-# The dominant decode call: the gate/up batch (two 4096 -> 12288 linears that
-# share x), the largest byte count of any call in a decode step.
-DOMINANT_GROUP = (4, 5)
+def time_dominant(backend, entries, reps: int, warmup: int) -> dict:
+    """The dominant call (gate/up batch = k_decode_stage1 + k_decode_stage2) of
+    every layer, captured in one graph; events on the graph's stream."""
+
+    calls = [[row[i] for i in DOMINANT_GROUP] for row in entries]
+    tokens = calls[0][0][2].shape[0]
+    per = pct([t / len(calls) for t in graph_reps(lambda: run_calls(backend, calls), reps, warmup)])
+    b = sum(algorithmic_bytes(m[0], tokens) for m in calls[0])
+    return {"call": per, "bytes_per_call": b, "calls": len(calls),
+            "achieved_gbs": b / (per["p50"] * 1e-3) / 1e9}
 
 
-def time_dominant_call(backend, stack, steps: int, warmup: int) -> dict:
-    """Mean duration of the dominant call (gate/up batch, k_decode_stage1 +
-    k_decode_stage2) over the stack's distinct layers, captured in one HIP
-    graph and bracketed by events recorded on the stream the graph runs on."""
+def config2(args, device) -> tuple[dict, dict, object, list]:
+    import torch
+
+    _say(f"config2: building the {args.layers}-layer stack")
+    backend, stack = build_layers(args.layers, device)
+    torch.cuda.synchronize()
+    result = {"workload": ("qwen3-8b-shape packed linears (q/o r2048, k/v r819, gate/up/down r3072), "
+                           f"{args.layers}-layer stack, 874.9 MB of distinct weights"),
+              "per_layer": {}, "per_linear": {}, "stack_m1": {}}
+    io = {m: stack_io(stack, m, device) for m in (1, 4, 16)}
+    for m in (1, 4, 16):
+        _say(f"config2: per layer M={m}")
+        fig = time_stack(backend, io[m], "grouped", args.steps, args.warmup)
+        result["per_layer"][str(m)] = {
+            "us": {k: round(v * 1e3 / args.layers, 2) for k, v in fig["ms_per_step"].items()},
+            "bytes": round(fig["step_bytes"] / args.layers),
+            "gbs": fig["achieved_gbs"],
+            "frac_of_hbm_peak": fig["frac_of_hbm_peak"],
+            "reps": fig["reps"],
+        }
+        if m == 1:
+            result["stack_m1"]["grouped"] = fig
+    for mode in [x for x in args.modes.split(",") if x and x != "grouped"]:
+        _say(f"config2: stack mode {mode}")
+        result["stack_m1"][mode] = time_stack(backend, io[1], mode, args.steps, args.warmup)
+    _say("config2: dominant call")
+    dom = time_dominant(backend, io[1], args.steps, args.warmup)
+    for i, (shape, layer) in enumerate(stack[0]):
+        count = replica_count(shape.weight_bytes)
+        reps_layers = replicas(backend, layer, count)
+        fig = {}
+        for m in (1, 4, 16):
+            _say(f"config2: per linear {shape.name} M={m} ({count} replicas)")
+            x = io[m][0][i][2]
+            out = torch.empty(m, shape.out_features, dtype=torch.float32, device=device)
+            fig[str(m)] = call_figures(shape, m, per_call(backend, reps_layers, x, out, args.steps, args.warmup))
+        result["per_linear"][shape.name.split(".")[-1]] = {"shape": [shape.in_features, shape.out_features,
+                                                                     shape.rank], "replicas": count, "M": fig}
+        del reps_layers
+    return result, dom, backend, io[1]
+
+
+# --- config 1 and 4 ---------------------------------------------------------------------
+
+
+def config1(args, device) -> dict:
+    import torch
+
+    from nanoquant_amd import synthetic as syn
+    from nanoquant_amd.runtime import HipPackedBackend
+
+    shape = syn.gemma3_1b_gate()
+    backend = HipPackedBackend()
+    layer = backend.prepare(syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 0, device=device), device)
+    count = replica_count(shape.weight_bytes)
+    layers = replicas(backend, layer, count)
+    x = syn.synthetic_activations(1, shape.in_features, seed=1, device=device)
+    out = torch.empty(1, shape.out_features, dtype=torch.float32, device=device)
+    _say(f"config1: gemma gate ({count} replicas)")
+    fig = call_figures(shape, 1, per_call(backend, layers, x, out, args.steps, args.warmup))
+    return {
+        "workload": "gemma-3-1b gate 1152->6912 r768, M=1, packed decode call (nq_linear, two kernels)",
+        "replicas": count,
+        "M": {"1": fig},
+        "reference_published_ms": REFERENCE_GEMMA_GATE_DECODE_MS,
+        "reference_published_hw": "RTX 4000 Ada Laptop, Triton two-stage kernel, median (evidence/m6/README.md:299)",
+        "speedup_vs_published": round(REFERENCE_GEMMA_GATE_DECODE_MS * 1e3 / fig["us"]["p50"], 2),
+    }
+
+
+def config4_states(device):
+    from nanoquant_amd import synthetic as syn
+
+    shape = syn.gemma3_4b_down()
+    column = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 3, salient=26, device=device)
+    plain = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 3, device=device)
+    rows = syn.synthetic_row_sidecar(plain, 26, seed=syn.BASE_SEED + 4)
+    return shape, {"column": column, "row": rows}
+
+
+def config4(args, device) -> dict:
+    import torch
+
+    from nanoquant_amd import synthetic as syn
+    from nanoquant_amd.runtime import HipPackedBackend
+
+    backend = HipPackedBackend()
+    shape, states = config4_states(device)
+    res = {"workload": ("gemma-3-4b down 10240->2560 r1536 with 26 int8 sidecar entries "
+                        "(column form: salient input columns, s_in zero there; row form: dense int8 output rows)"),
+           "forms": {}}
+    for form, state in states.items():
+        side = _sidecar_bytes(state)
+        layer = backend.prepare(state, device)
+        count = replica_count(shape.weight_bytes + side)
+        layers = replicas(backend, layer, count, sidecars=True)
+        figs = {}
+        for m in (1, 8):
+            _say(f"config4: {form} form M={m} ({count} replicas)")
+            x = syn.synthetic_activations(m, shape.in_features, seed=m, device=device)
+            out = torch.empty(m, shape.out_features, dtype=torch.float32, device=device)
+            figs[str(m)] = call_figures(shape, m, per_call(backend, layers, x, out, args.steps, args.warmup),
+                                        sidecar=side)
+        res["forms"][form] = {"sidecar_bytes": side, "replicas": count, "M": figs}
+        del layers
+    return res
+
+
+# --- config 3 ---------------------------------------------------------------------------
+
+
+def config3(args, device) -> dict:
+    """The seven Llama-3-8B linears (~0.8 bpw) at each token count, one layer
+    pass captured in a HIP graph; TFLOP/s counts the two sign GEMMs
+    (2*M*(in*r + r*out)) against the fp16 dense MFMA peak."""
 
     import torch
 
-    calls = [[entries[i] for i in DOMINANT_GROUP] for entries in stack]
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        run_step(backend, calls)
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=side):
-            run_step(backend, calls)
-        for _ in range(warmup):
-            graph.replay()
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(side)
-        for _ in range(steps):
-            graph.replay()
-        stop.record(side)
-    stop.synchronize()
-    tokens = calls[0][0][2].shape[0]
-    call_us = start.elapsed_time(stop) * 1e3 / (steps * len(calls))
-    call_bytes = sum(algorithmic_bytes(m[0], tokens) for m in calls[0])
-    return {"mean_call_us": call_us, "bytes_per_call": call_bytes,
-            "achieved_gbs": call_bytes / (call_us * 1e-6) / 1e9, "calls": len(calls)}
+    from nanoquant_amd import synthetic as syn
+    from nanoquant_amd.runtime import HipPackedBackend
+
+    backend = HipPackedBackend()
+    shapes = syn.llama3_8b_layer()
+    layers = [backend.prepare(syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 500 + i, device=device), device)
+              for i, s in enumerate(shapes)]
+    sweep = {}
+    for tokens in [int(t) for t in args.prefill_tokens.split(",") if t]:
+        _say(f"config3: prefill M={tokens}")
+        xs = {s.in_features: syn.synthetic_activations(tokens, s.in_features, seed=tokens, device=device)
+              for s in shapes}
+        outs = [torch.empty(tokens, s.out_features, dtype=torch.float32, device=device) for s in shapes]
+
+        def layer_pass():
+            for s, layer, out in zip(shapes, layers, outs):
+                backend.linear_into(xs[s.in_features], layer, out=out)
+
+        d = pct(graph_reps(layer_pass, args.steps, 2))
+        flops = sum(2 * tokens * (s.in_features * s.rank + s.rank * s.out_features) for s in shapes)
+        sweep[str(tokens)] = {
+            "ms_per_layer": _scaled(d, lambda v: v, 4),
+            "tok_per_s": round(tokens * 1000.0 / d["p50"], 1),
+            "tflops": _scaled(d, lambda ms: flops / (ms * 1e-3) / 1e12, 2),
+            "frac_of_fp16_peak": round(flops / (d["p50"] * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS, 4),
+            "reps": d["n"],
+        }
+        del xs, outs
+    return {"workload": "llama-3-8b-shape packed linears (q/o r1638, k/v r655, gate/up/down r2549), one layer",
+            "peak_tflops": FP16_DENSE_PEAK_TFLOPS, "points": sweep}
+
+
+# --- config 5 ---------------------------------------------------------------------------
+
+
+def config5(args, device, packed_us_per_layer: float | None) -> dict:
+    import torch
+
+    from nanoquant_amd import synthetic as syn
+    from nanoquant_amd.runtime.decoder_shell import DecoderShellConfig, PackedDecoder
+
+    config = DecoderShellConfig(layers=args.layers)
+    _say("config5: building the decoder")
+    weights = syn.synthetic_decoder(config, seed=syn.BASE_SEED + 5, device=device)
+    decoder = PackedDecoder(config, weights, device=device, max_positions=args.e2e_prompt + args.e2e_tokens)
+    del weights
+    g = torch.Generator().manual_seed(syn.BASE_SEED + 5)
+    prompt = torch.randint(0, config.vocab, (args.e2e_prompt,), generator=g).to(device)
+    decoder.generate_greedy(prompt, args.e2e_tokens)  # capture + warm-up
+    decode_ms, prefill_ms, tokens = [], [], None
+    for rep in range(max(args.steps, 10)):
+        timing: dict = {}
+        out = decoder.generate_greedy(prompt, args.e2e_tokens, timings=timing)
+        if tokens is None:
+            tokens = out.tolist()
+        elif out.tolist() != tokens:
+            raise RuntimeError("end-to-end greedy decode is not deterministic across runs")
+        decode_ms.append(timing["decode_ms"] / (args.e2e_tokens - 1))
+        prefill_ms.append(timing["prefill_ms"])
+    d, pf = pct(decode_ms), pct(prefill_ms)
+    kernels = args.layers * 10 + 5 if decoder.fuse_decode else args.layers * 12 + 4
+    res = {
+        "workload": (f"qwen3-8b-shape random-init packed model, {args.layers} layers, vocab {config.vocab}, "
+                     f"prompt {args.e2e_prompt} ids, {args.e2e_tokens} greedy tokens, batch 1, "
+                     "bf16 activations/KV, one HIP-graph replay per decode token"),
+        "decode_tok_per_s": _scaled(d, lambda ms: 1000.0 / ms, 2),
+        "decode_ms_per_token": _scaled(d, lambda v: v, 4),
+        "prefill_ms": _scaled(pf, lambda v: v, 3),
+        "prefill_tok_per_s": round(args.e2e_prompt * 1000.0 / pf["p50"], 1),
+        "total_tok_per_s": round(args.e2e_tokens * 1000.0 / (pf["p50"] + d["p50"] * (args.e2e_tokens - 1)), 2),
+        "kernels_per_token": kernels,
+        "fused_decode": decoder.fuse_decode,
+        "first_tokens": tokens[:8],
+        "reps": d["n"],
+    }
+    bytes_per_token = 874_863_792 + 1_244_659_712 + 147_456 * (args.e2e_prompt + args.e2e_tokens // 2)
+    res["bytes_per_token"] = bytes_per_token
+    res["frac_of_hbm_peak"] = round(bytes_per_token / (d["p50"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    if packed_us_per_layer is not None:
+        res["packed_linear_us_per_layer"] = round(packed_us_per_layer, 2)
+        res["shell_us_per_token"] = round(d["p50"] * 1e3 - packed_us_per_layer * args.layers, 1)
+    del decoder
+    torch.cuda.empty_cache()
+    return res
+
+
+# --- CPU baselines ----------------------------------------------------------------------
+
+
+def cpu_threads() -> int:
+    """Host threads for the CPU baselines: the job's CPU share (OMP_NUM_THREADS
+    when set, as on the GPU host), at most os.cpu_count()."""
+
+    total = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS") or total)
+    return max(1, min(total, share))
+
+
+def _cpu_time(fn, reps: int, warmup: int) -> dict:
+    for _ in range(warmup):
+        fn()
+    samples = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    return pct(samples)
+
+
+def _cpu_meta(threads: int) -> dict:
+    import torch
+
+    return {"cores": threads, "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+            "cpu": _cpu_model(), "kind": "port"}
+
+
+def cpu_baselines(args, reps: int, warmup: int) -> dict:
+    """The oracle's restatement of the reference's CPU torch path
+    (PackedReferenceBackend, reference.py:184-235: unpack once to fp32 +-1,
+    two fp32 F.linear, sidecars, x cast to fp32) on the same seeded inputs."""
+
+    import torch
+
+    from nanoquant_amd import synthetic as syn
+    from oracle import nq_oracle as orc
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    res = {"threads": threads, "os_cpu_count": os.cpu_count(), "cpu": _cpu_model()}
+
+    def fwd(state):
+        return orc.CpuPackedForward(orc.operands_from_state(state))
+
+    def linear_ms(state, tokens, seed):
+        f = fwd(state)
+        x = syn.synthetic_activations(tokens, state.spec.in_features, seed=seed)
+        return _cpu_time(lambda: f(x), reps, warmup)
+
+    _say("cpu: config1")
+    g1 = syn.gemma3_1b_gate()
+    d = linear_ms(syn.synthetic_packed_layer(g1, seed=syn.BASE_SEED + 0), 1, 1)
+    res["config1"] = {"ms": _scaled(d, lambda v: v, 4), "tok_per_s": round(1000.0 / d["p50"], 2)}
+
+    _say("cpu: config2 layer")
+    shapes = syn.qwen3_8b_layer(0)
+    fwds = [fwd(syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + i)) for i, s in enumerate(shapes)]
+    res["config2"] = {}
+    for m in (1, 16):
+        xs = [syn.synthetic_activations(m, s.in_features, seed=i) for i, s in enumerate(shapes)]
+        d = _cpu_time(lambda: [f(x) for f, x in zip(fwds, xs)], reps, warmup)
+        res["config2"][str(m)] = {"ms_per_layer": _scaled(d, lambda v: v, 3),
+                                  "stack_tok_per_s": round(m * 1000.0 / (d["p50"] * args.layers), 3)}
+    del fwds
+
+    _say("cpu: config3 layer")
+    shapes3 = syn.llama3_8b_layer()
+    fwds = [fwd(syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 500 + i)) for i, s in enumerate(shapes3)]
+    res["config3"] = {}
+    for m in (64, 512):
+        xs = [syn.synthetic_activations(m, s.in_features, seed=m) for s in shapes3]
+        d = _cpu_time(lambda: [f(x) for f, x in zip(fwds, xs)], max(3, reps // 2), 1)
+        flops = sum(2 * m * (s.in_features * s.rank + s.rank * s.out_features) for s in shapes3)
+        res["config3"][str(m)] = {"ms_per_layer": _scaled(d, lambda v: v, 2),
+                                  "tflops": round(flops / (d["p50"] * 1e-3) / 1e12, 4)}
+    del fwds
+
+    _say("cpu: config4")
+    _shape4, states4 = config4_states("cpu")
+    res["config4"] = {}
+    for form, state in states4.items():
+        f = fwd(state)  # the row form is folded in as the reference's float patch
+        res["config4"][form] = {}
+        for m in (1, 8):
+            x = syn.synthetic_activations(m, state.spec.in_features, seed=m)
+            d = _cpu_time(lambda: f(x), reps, warmup)
+            res["config4"][form][str(m)] = {"ms": _scaled(d, lambda v: v, 4)}
+
+    _say("cpu: config5 (2 real-geometry layers)")
+    res["config5"] = cpu_e2e(args, reps=8, warmup=1)
+    return res
+
+
+def cpu_e2e(args, reps: int, warmup: int) -> dict:
+    """The oracle decoder (fp32 CPU restatement of the Qwen3 shell around
+    CpuPackedForward linears) on TWO layers of the Qwen3-8B geometry with the
+    full 151936-row vocabulary: a 16-id prompt, then `reps` greedy decode
+    tokens timed one by one. The 36-layer per-token time is estimated as the
+    final norm + lm_head time plus 18 x the two layers' share."""
+
+    import torch
+
+    from nanoquant_amd import synthetic as syn
+    from nanoquant_amd.runtime.decoder_shell import DecoderShellConfig
+    from oracle import decoder_shell as ods
+    from oracle import nq_oracle as orc
+
+    config = DecoderShellConfig(layers=2)
+    device = "cuda" if torch.cuda.is_available() else "cpu"
+    w = syn.synthetic_decoder(config, seed=syn.BASE_SEED + 5, device=device)
+    geometry = ods.ShellGeometry(config.layers, config.hidden, config.intermediate, config.q_heads,
+                                 config.kv_heads, config.head_dim, config.vocab, config.eps, config.rope_theta)
+    ow = ods.ShellWeights(
+        w.embed.cpu(), w.lm_head.cpu().float(), w.final_norm.cpu(),  # lm_head converted once, like the factors
+        [ods.LayerWeights(l.input_norm.cpu(), l.post_norm.cpu(), l.q_norm.cpu(), l.k_norm.cpu(),
+                          {r: orc.operands_from_state(s) for r, s in l.linears.items()}) for l in w.layers],
+    )
+    del w
+    decoder = ods.OracleDecoder(geometry, ow, max_positions=64)
+    prompt = torch.randint(0, config.vocab, (16,), generator=torch.Generator().manual_seed(5))
+    token = int(torch.argmax(decoder.forward(prompt, 0)[-1]))
+    samples, position = [], 16
+    for i in range(warmup + reps):
+        t0 = time.perf_counter()
+        token = int(torch.argmax(decoder.forward(torch.tensor([token]), position)[-1]))
+        if i >= warmup:
+            samples.append((time.perf_counter() - t0) * 1e3)
+        position += 1
+    h = torch.randn(1, config.hidden)
+    head = _cpu_time(lambda: ods.rms_norm(h, ow.final_norm, config.eps) @ ow.lm_head.T, 5, 1)
+    two = pct(samples)
+    per_layer = (two["p50"] - head["p50"]) / 2
+    est_ms = head["p50"] + per_layer * args.layers
+    return {
+        "two_layer_ms_per_token": _scaled(two, lambda v: v, 2),
+        "lm_head_ms": round(head["p50"], 2),
+        "ms_per_layer": round(per_layer, 2),
+        "estimated_36_layer_ms_per_token": round(est_ms, 1),
+        "estimated_tok_per_s": round(1000.0 / est_ms, 4),
+        "sample": (f"oracle decoder, 2 of {args.layers} Qwen3-8B-geometry layers + full vocab lm_head, 16-id prompt, "
+                   f"{reps} greedy decode tokens timed (p50), {args.layers}-layer time = lm_head + "
+                   f"{args.layers} x per-layer"),
+    }
+
+
+# --- misc entry modes -------------------------------------------------------------------
+
+
+def copy_calibration(mib: int) -> int:
+    """A plain device-to-device copy of known size, for scaling HBM byte counters."""
+
+    import torch
+
+    src = torch.ones(mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": src.numel() * 4, "written": dst.numel() * 4}))
+    return 0
 
 
 def measured_traffic(tokens: int, layers: int):
@@ -230,179 +767,17 @@ def measured_traffic(tokens: int, layers: int):
     return int(m.group(1))
 
 
-def algorithmic_bytes(shape, tokens: int) -> int:
-    """Sign words + fp16 scales + bf16 x + fp32 y (the rank-r latent is excluded)."""
-
-    return shape.weight_bytes + 2 * tokens * shape.in_features + 4 * tokens * shape.out_features
-
-
-def cpu_baseline(tokens: int, budget_s: float, layers: int) -> dict:
-    """The oracle's restatement of the reference CPU torch path (unpack once, two
-    fp32 F.linear per linear) on the 7 linears of one layer, scaled to the stack."""
-
+def dominant_only(args, device) -> int:
     import torch
 
-    from nanoquant_amd import synthetic as syn
-    from oracle import nq_oracle as orc
-
-    forwards, inputs = [], []
-    for i, shape in enumerate(syn.qwen3_8b_layer(0)):
-        state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + i)
-        forwards.append(orc.CpuPackedForward(orc.operands_from_state(state)))
-        inputs.append(syn.synthetic_activations(tokens, shape.in_features, seed=i))
-
-    def one_layer():
-        for fwd, x in zip(forwards, inputs):
-            fwd(x)
-
-    one_layer()
-    samples = []
-    begin = time.perf_counter()
-    while (time.perf_counter() - begin < budget_s and len(samples) < 200) or len(samples) < 3:
-        t0 = time.perf_counter()
-        one_layer()
-        samples.append(time.perf_counter() - t0)
-    samples.sort()
-    median = samples[len(samples) // 2]
-    return {
-        "value": round(tokens / (median * layers), 4),
-        "unit": "tok/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": (
-            f"oracle torch fp32 forward (unpack once, 2x F.linear) over the 7 Qwen3-8B linears "
-            f"of one layer at M={tokens}, {len(samples)} timed reps (median "
-            f"{median * 1e3:.1f} ms/layer), scaled x{layers} layers; cpu={_cpu_model()}"
-        ),
-    }
-
-
-FP16_DENSE_PEAK_TFLOPS = 2500.0
-
-
-def prefill_sweep(token_counts, steps: int, warmup: int) -> dict:
-    """Config: the seven Llama-3-8B linears (~0.8 bpw) at each token count, one
-    layer pass (every linear once) captured in a HIP graph so host launch costs
-    stay out of the timing; events bracket `steps` replays. TFLOP/s counts the
-    two sign GEMMs (2*M*(in*r + r*out)) against the fp16 dense MFMA peak."""
-
-    import torch
-
-    from nanoquant_amd import synthetic as syn
-    from nanoquant_amd.runtime import HipPackedBackend
-
-    device = torch.device("cuda", 0)
-    backend = HipPackedBackend()
-    shapes = syn.llama3_8b_layer()
-    layers = [backend.prepare(syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 500 + i, device=device), device)
-              for i, s in enumerate(shapes)]
-    sweep = {}
-    for tokens in token_counts:
-        xs = {s.in_features: syn.synthetic_activations(tokens, s.in_features, seed=tokens, device=device)
-              for s in shapes}
-        outs = [torch.empty(tokens, s.out_features, dtype=torch.float32, device=device) for s in shapes]
-
-        def layer_pass():
-            for s, layer, out in zip(shapes, layers, outs):
-                backend.linear_into(xs[s.in_features], layer, out=out)
-
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            layer_pass()  # allocates the calls' workspaces outside the capture
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=side):
-                layer_pass()
-            for _ in range(warmup):
-                graph.replay()
-            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record(side)
-            for _ in range(steps):
-                graph.replay()
-            stop.record(side)
-        stop.synchronize()
-        ms = start.elapsed_time(stop) / steps
-        flops = sum(2 * tokens * (s.in_features * s.rank + s.rank * s.out_features) for s in shapes)
-        tflops = flops / (ms * 1e-3) / 1e12
-        sweep[str(tokens)] = {
-            "ms_per_layer": round(ms, 4),
-            "tok_per_s": round(tokens * 1000.0 / ms, 1),
-            "tflops": round(tflops, 2),
-            "frac_of_fp16_peak": round(tflops / FP16_DENSE_PEAK_TFLOPS, 4),
-        }
-    return {
-        "workload": "llama-3-8b-shape packed linears (q/o r1638, k/v r655, gate/up/down r2549), one layer",
-        "peak_tflops": FP16_DENSE_PEAK_TFLOPS,
-        "points": sweep,
-    }
-
-
-def e2e_decode(layers: int, prompt_len: int, new_tokens: int, repeats: int, packed_us_per_layer: float) -> dict:
-    """Greedy decode of a random-init Qwen3-8B-shaped model (36 layers, hidden
-    4096, intermediate 12288, GQA 32/8 x 128, vocab 151936; every projection
-    packed at ~1.0 bpw, bf16 N(0, 0.02) embeddings and untied lm_head, bf16
-    KV cache): a `prompt_len`-token prompt through the prefill path, then
-    `new_tokens` greedy tokens, each decode step one HIP-graph replay. Events
-    bracket prefill and decode; the best of `repeats` runs is reported."""
-
-    import torch
-
-    from nanoquant_amd import synthetic as syn
-    from nanoquant_amd.runtime.decoder_shell import DecoderShellConfig, PackedDecoder
-
-    device = torch.device("cuda", 0)
-    config = DecoderShellConfig(layers=layers)
-    weights = syn.synthetic_decoder(config, seed=syn.BASE_SEED + 5, device=device)
-    decoder = PackedDecoder(config, weights, device=device, max_positions=prompt_len + new_tokens)
-    del weights
-    g = torch.Generator().manual_seed(syn.BASE_SEED + 5)
-    prompt = torch.randint(0, config.vocab, (prompt_len,), generator=g).to(device)
-    decoder.generate_greedy(prompt, new_tokens)  # capture + warm-up
-    runs = []
-    tokens = None
-    for _ in range(repeats):
-        timing: dict = {}
-        out = decoder.generate_greedy(prompt, new_tokens, timings=timing)
-        if tokens is None:
-            tokens = out.tolist()
-        elif out.tolist() != tokens:
-            raise RuntimeError("end-to-end greedy decode is not deterministic across runs")
-        runs.append(timing)
-    best = min(runs, key=lambda r: r["decode_ms"])
-    decode_steps = new_tokens - 1
-    ms_per_token = best["decode_ms"] / decode_steps
-    # per layer: unfused RMSNorm, QKV (2), attention (2), O (2), RMSNorm, gate/up (2), SiLU product,
-    # down (2); fused: the two norms and the SiLU product run inside the packed calls (layer 0 keeps
-    # its input norm). Plus embedding, final norm, lm_head and greedy select.
-    kernels = layers * 10 + 5 if decoder.fuse_decode else layers * 12 + 4
-    return {
-        "workload": (f"qwen3-8b-shape random-init packed model, {layers} layers, vocab {config.vocab}, "
-                     f"prompt {prompt_len} ids, {new_tokens} greedy tokens, batch 1, bf16 activations/KV"),
-        "decode_tok_per_s": round(1000.0 / ms_per_token, 2),
-        "decode_ms_per_token": round(ms_per_token, 4),
-        "prefill_ms": round(best["prefill_ms"], 3),
-        "prefill_tok_per_s": round(prompt_len * 1000.0 / best["prefill_ms"], 1),
-        "total_tok_per_s": round(new_tokens * 1000.0 / (best["prefill_ms"] + best["decode_ms"]), 2),
-        "packed_linear_us_per_layer": round(packed_us_per_layer, 2),
-        "shell_us_per_token": round(ms_per_token * 1000.0 - packed_us_per_layer * layers, 1),
-        "kernels_per_token": kernels,
-        "fused_decode": decoder.fuse_decode,
-        "first_tokens": tokens[:8],
-        "repeats": repeats,
-    }
-
-
-def copy_calibration(mib: int) -> int:
-    """A plain device-to-device copy of known size, for scaling HBM byte counters."""
-
-    import torch
-
-    src = torch.ones(mib * (1 << 20) // 4, dtype=torch.float32, device="cuda")
-    dst = torch.empty_like(src)
-    for _ in range(10):
-        dst.copy_(src)
+    backend, stack = build_layers(args.layers, device)
+    entries = stack_io(stack, 1, device)
+    calls = [[row[i] for i in DOMINANT_GROUP] for row in entries]
+    for _ in range(args.steps):
+        run_calls(backend, calls)
     torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes_read": src.numel() * 4, "written": dst.numel() * 4}))
+    print(json.dumps({"dominant_calls": args.steps * len(calls),
+                      "bytes_per_call": sum(algorithmic_bytes(m[0], 1) for m in calls[0])}))
     return 0
 
 
@@ -416,46 +791,55 @@ def main(argv=None) -> int:
             file=sys.stderr,
         )
         return 2
-    if not 1 <= args.tokens <= 16:
-        print("--tokens must be in 1..16 (decode path)", file=sys.stderr)
+    if args.steps < 1:
+        print("--steps must be positive", file=sys.stderr)
         return 2
-
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
-    modes_wanted = [m for m in args.modes.split(",") if m]
-    if not modes_wanted or any(m.removesuffix("-fused") not in GROUPINGS for m in modes_wanted):
-        print(f"--modes must name some of {sorted(GROUPINGS)} (optionally with -fused)", file=sys.stderr)
-        return 2
+    skip = {s for s in args.skip.split(",") if s}
 
     import torch
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
-    print(f"[bench] building {args.layers}-layer stack, M={args.tokens}", file=sys.stderr, flush=True)
-    backend, stack = build_stack(args.layers, args.tokens, device)
-    torch.cuda.synchronize()
     if args.dominant_only:
-        calls = [[entries[i] for i in DOMINANT_GROUP] for entries in stack]
-        for _ in range(args.steps):
-            run_step(backend, calls)
-        torch.cuda.synchronize()
-        print(json.dumps({"dominant_calls": args.steps * len(calls),
-                          "bytes_per_call": sum(algorithmic_bytes(m[0], args.tokens) for m in calls[0])}))
-        return 0
-    modes = {}
-    for mode in modes_wanted:
-        print(f"[bench] mode {mode}: timing {args.steps} steps", file=sys.stderr, flush=True)
-        modes[mode] = time_mode(backend, stack, mode, args.steps, args.warmup, not args.no_graph)
-    head_mode = modes_wanted[0]
-    head = modes[head_mode]
-    ms_per_step = head["ms_per_step"]
-    print("[bench] dominant call (gate/up batch) timing", file=sys.stderr, flush=True)
-    dom = time_dominant_call(backend, stack, args.steps, args.warmup)
-    achieved = dom["achieved_gbs"]
+        return dominant_only(args, device)
+    wall0 = time.perf_counter()
+    result: dict = {}
+    c2, dom, backend, _ = (None, None, None, None)
+    if "config2" not in skip:
+        c2, dom, backend, _ = config2(args, device)
+        torch.cuda.empty_cache()
+    c1 = config1(args, device) if "config1" not in skip else None
+    c4 = config4(args, device) if "config4" not in skip else None
+    torch.cuda.empty_cache()
+    c3 = config3(args, device) if "config3" not in skip and args.prefill_tokens else None
+    packed_us = None
+    if c2 is not None:
+        packed_us = c2["stack_m1"]["grouped"]["ms_per_step"]["p50"] * 1e3 / args.layers
+    del backend
+    torch.cuda.empty_cache()
+    c5 = config5(args, device, packed_us) if "config5" not in skip and args.e2e_tokens > 1 else None
+    copy = copy_ceiling(args.steps, args.warmup) if "copy" not in skip else None
+    cpu = None
+    if "cpu" not in skip:
+        cpu = cpu_baselines(args, reps=args.steps, warmup=args.warmup)
 
-    result = {
+    # Headline: the config-5 median decode rate (the stack's grouped rate when
+    # config 5 is skipped).
+    if c5 is not None:
+        value = c5["decode_tok_per_s"]["p50"]
+        ms_per_step = c5["decode_ms_per_token"]["p50"]
+        workload = c5["workload"]
+        unit_note = "median decode tok/s of the end-to-end model"
+    else:
+        head = c2["stack_m1"]["grouped"]
+        value, ms_per_step = head["tok_per_s"]["p50"], head["ms_per_step"]["p50"]
+        workload = c2["workload"] + ", launch grouping 'grouped'"
+        unit_note = "median decode tok/s of the packed-linear stack (config 5 skipped)"
+    result.update({
         "metric": METRIC,
-        "value": round(args.tokens * 1000.0 / ms_per_step, 3),
+        "value": round(value, 3),
         "unit": "tok/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -464,64 +848,44 @@ def main(argv=None) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16-in/fp32-acc (1-bit signs)",
-        "data": "synthetic (Bernoulli(0.5) signs, fp16 lognormal(0,0.25) scales, bf16 N(0,1) x)",
-        "config": {
-            "workload": (
-                f"qwen3-8b-shape packed-linear decode stack: {args.layers} layers x 7 linears "
-                f"(q/o r2048, k/v r819, gate/up/down r3072), M={args.tokens}, one HIP-graph step, "
-                f"launch grouping '{head_mode}'"
-            ),
-            "global_batch": args.tokens,
-            "layers": args.layers,
-            "linears_per_step": 7 * args.layers,
-            "weight_bytes_per_step": sum(e[0].weight_bytes for entries in stack for e in entries),
-            "parallelism": "single-gpu",
-        },
-        "roofline": {
+        "dtype": "bf16-in/fp32-acc (1-bit signs, int8-digit MFMA decode, fp16 MFMA prefill)",
+        "data": ("synthetic: Bernoulli(0.5) signs, fp16 lognormal(0,0.25) scales, bf16 N(0,1) activations, "
+                 "random-init bf16 N(0,0.02) embeddings/lm_head"),
+        "config": {"workload": workload, "value_is": unit_note, "global_batch": 1, "layers": args.layers,
+                   "parallelism": "single-gpu"},
+    })
+    if dom is not None:
+        achieved = dom["achieved_gbs"]
+        result["roofline"] = {
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(args.tokens, args.layers),
+            "traffic": measured_traffic(1, args.layers),
             "traffic_source": TRAFFIC_PROFILE.name,
             "kernel": ("dominant decode call: gate/up batch (two 4096->12288 r3072 linears sharing x) = "
                        "k_decode_stage1 + k_decode_stage2, graph of one call per layer"),
-            "bytes_per_call": round(dom["bytes_per_call"]),
-            "mean_call_us": round(dom["mean_call_us"], 3),
-            "step_achieved_gbs": round(head["achieved_gbs"], 1),
-        },
-        "calls_per_step": head["calls_per_step"],
-        "kernels_per_step": head["kernels_per_step"],
-        "modes": {
-            name: {
-                "calls_per_step": m["calls_per_step"],
-                "kernels_per_step": m["kernels_per_step"],
-                "ms_per_step": round(m["ms_per_step"], 4),
-                "tok_per_s": round(args.tokens * 1000.0 / m["ms_per_step"], 2),
-                "mean_call_us": round(m["mean_call_us"], 3),
-                "bytes_per_call": round(m["bytes_per_call"]),
-                "achieved_gbs": round(m["achieved_gbs"], 1),
-                "frac_of_hbm_peak": round(m["achieved_gbs"] / HBM_PEAK_GBS, 4),
-            }
-            for name, m in modes.items()
-        },
-        "prefill": None,
-        "cpu_baseline": None,
-    }
-    prefill_tokens = [int(t) for t in args.prefill_tokens.split(",") if t]
-    if prefill_tokens:
-        print(f"[bench] prefill sweep M={prefill_tokens}", file=sys.stderr, flush=True)
-        result["prefill"] = prefill_sweep(prefill_tokens, max(args.steps // 2, 3), 2)
-    if args.e2e_tokens > 0:
-        print(f"[bench] end-to-end decode: prompt {args.e2e_prompt}, {args.e2e_tokens} tokens",
-              file=sys.stderr, flush=True)
-        packed_us = modes["grouped"]["ms_per_step"] * 1000.0 / args.layers if "grouped" in modes else float("nan")
-        result["e2e"] = e2e_decode(args.layers, args.e2e_prompt, args.e2e_tokens, 3, packed_us)
-    if not args.no_cpu_baseline:
-        print("[bench] CPU baseline", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(args.tokens, args.cpu_seconds, args.layers)
+            "bytes_per_call": dom["bytes_per_call"],
+            "call_us": _scaled(dom["call"], lambda ms: ms * 1e3),
+        }
+        if copy is not None:
+            ceiling = copy["points"]["12.8MB"]["read_gbs"]["p50"]
+            result["roofline"]["measured_read_ceiling_gbs_at_call_size"] = ceiling
+            result["roofline"]["frac_of_measured_ceiling"] = round(achieved / ceiling, 4)
+    if cpu is not None:
+        c5cpu = cpu["config5"]
+        result["cpu_baseline"] = {
+            "value": c5cpu["estimated_tok_per_s"],
+            "unit": "tok/s",
+            "cores": cpu["threads"],
+            "kind": "port",
+            "sample": c5cpu["sample"] + f"; host {cpu['cpu']}, os.cpu_count() {cpu['os_cpu_count']}",
+        }
+    result["configs"] = {"config1": c1, "config2": c2, "config3": c3, "config4": c4, "config5": c5}
+    result["copy_ceiling"] = copy
+    result["cpu_baselines"] = cpu
+    result["bench_wall_s"] = round(time.perf_counter() - wall0, 1)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -222,6 +222,13 @@ int nq_linear(const nq_linear_desc* desc, const void* x, int32_t x_dtype,
 int nq_linear_static(const nq_linear_desc* desc, const void* x, int32_t x_dtype,
                      int64_t tokens, void* y, int32_t y_dtype, void* stream);
 
+/* Read `bytes` (a multiple of 16, 16-byte aligned) of device memory with the
+ * decode kernels' load pattern and write, for each of min(sink_count,
+ * ceil(bytes / 16384)) workgroups, the XOR of the 32-bit words it read to
+ * sink[workgroup]. No reference counterpart: a measurement aid, the HBM read
+ * ceiling the decode path is compared with. */
+int nq_read_stream(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_count, void* stream);
+
 /* One launch for `count` (1..8) packed linears with the same token count
  * (1..16) and dtypes: y_i = linear_i(x_i). Inputs may alias (Q/K/V or gate/up
  * share x); every descriptor must carry tiles and no two may share them.

@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "nq_linear_workspace_bytes",
     "nq_linear",
     "nq_linear_static",
+    "nq_read_stream",
     "nq_linear_batch",
     "nq_linear_batch_fused",
     "nq_decode_mixed_v_words",
@@ -174,6 +175,7 @@ def _declare(lib: ctypes.CDLL) -> None:
             [desc_p, vp, ctypes.c_int32, c_i64, vp, ctypes.c_int32, vp, c_i64, vp],
         ),
         "nq_linear_static": (c_int, [desc_p, vp, ctypes.c_int32, c_i64, vp, ctypes.c_int32, vp]),
+        "nq_read_stream": (c_int, [vp, c_i64, vp, c_i64, vp]),
         "nq_linear_batch": (
             c_int,
             [ctypes.POINTER(desc_p), ctypes.c_int32, ctypes.POINTER(vp), ctypes.c_int32, c_i64,

@@ -692,3 +692,20 @@ def test_batch_rejects_duplicate_members():
     x = syn.synthetic_activations(1, 4096, seed=1, device="cuda")
     with pytest.raises(ValueError, match="distinct"):
         backend.linear_batch([x, x], [layer, layer])
+
+
+def test_read_stream_probe_reads_every_word():
+    """nq_read_stream (the bench's HBM read ceiling) touches every word: the
+    XOR of its per-workgroup sinks equals the XOR of the buffer."""
+
+    g = torch.Generator().manual_seed(17)
+    data = torch.randint(-(2**31), 2**31, (3_000_004,), generator=g, dtype=torch.int64).to(torch.int32)
+    sink = torch.zeros(4096, dtype=torch.int32, device="cuda")
+    lib = _native.load()
+    dev = data.cuda()
+    status = lib.nq_read_stream(dev.data_ptr(), dev.numel() * 4, sink.data_ptr(), sink.numel(),
+                                _native.current_stream_handle(dev.device))
+    assert status == _native.NQ_OK
+    expected = np.bitwise_xor.reduce(data.numpy().view(np.uint32))
+    assert np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)) == expected
+    assert lib.nq_read_stream(dev.data_ptr(), 20, sink.data_ptr(), 1, None) == _native.NQ_ERR_ALIGNMENT
