@@ -832,11 +832,13 @@ def main(argv=None) -> int:
         ms_per_step = c5["decode_ms_per_token"]["p50"]
         workload = c5["workload"]
         unit_note = "median decode tok/s of the end-to-end model"
-    else:
+    elif c2 is not None:
         head = c2["stack_m1"]["grouped"]
         value, ms_per_step = head["tok_per_s"]["p50"], head["ms_per_step"]["p50"]
         workload = c2["workload"] + ", launch grouping 'grouped'"
         unit_note = "median decode tok/s of the packed-linear stack (config 5 skipped)"
+    else:
+        value, ms_per_step, workload, unit_note = 0.0, 0.0, "partial run", "configs 2 and 5 skipped: no headline"
     result.update({
         "metric": METRIC,
         "value": round(value, 3),

@@ -169,10 +169,12 @@ void pick_waves(int64_t nc, int tpb, int tb, int& nw, int& kc) {
 
 // Dynamic LDS of a stage: per-wave operand areas (stage 1), the partial sums
 // [nc][tw][tb][64], the chunk maxima [nc][tpb * tb] (stage 1) and, for one
-// token, kc operand spread areas per wave (stage 2).
-size_t lds_bytes(int stage, int tpb, int tb, int tw, int nw, int kc, int64_t nc) {
+// token, kc operand spread areas per wave (stage 2), then the staged salient
+// operands of the member with the most salient columns (stage 2).
+size_t lds_bytes(int stage, int tpb, int tb, int tw, int nw, int kc, int64_t nc, int64_t ks = 0, int tokens = 1) {
     const size_t red = static_cast<size_t>(nc) * tw * tb * 64 * 4;
-    if (stage == 2) return red + (tpb == 1 ? static_cast<size_t>(nw) * kc * kS2SpreadBytes : 0);
+    if (stage == 2)
+        return red + (tpb == 1 ? static_cast<size_t>(nw) * kc * kS2SpreadBytes : 0) + sal_lds_bytes(ks, tw, tokens);
     return static_cast<size_t>(nw) * (8 * 4 * tpb * 4 * 16) + red + static_cast<size_t>(nc) * tpb * tb * 4;
 }
 
@@ -241,8 +243,9 @@ int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, L
 }
 
 int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t stream) {
-    int64_t tiles1 = 0, tiles2 = 0, nc1 = 0, nc2 = 0;
+    int64_t tiles1 = 0, tiles2 = 0, nc1 = 0, nc2 = 0, ks = 0;
     for (int i = 0; i < batch.count; ++i) {
+        ks = batch.p[i].salient_count <= kSalMax && batch.p[i].salient_count > ks ? batch.p[i].salient_count : ks;
         tiles1 += batch.p[i].g1.nt;
         tiles2 += batch.p[i].g2.nt;
         nc1 = batch.p[i].g1.nc > nc1 ? batch.p[i].g1.nc : nc1;
@@ -281,7 +284,7 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
 
     if (fused) {
         const size_t l1 = lds_bytes(1, s1.tpb, s1.tb, 1, s1.nw, s1.kc, nc1),
-                     l2 = lds_bytes(2, s1.tpb, s1.tb, 1, s1.nw, s1.kc2, nc2);
+                     l2 = lds_bytes(2, s1.tpb, s1.tb, 1, s1.nw, s1.kc2, nc2, ks, static_cast<int>(tokens));
         s1.lds = l1 > l2 ? l1 : l2;
         s1.grid = dim3(static_cast<unsigned>(max1 > max2 ? max1 : max2), 2 * count);
         return enqueue_fused(batch, s1, stream);
@@ -290,7 +293,7 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
     s1.grid = dim3(static_cast<unsigned>(max1), count);
     int st = enqueue_stage1(batch, s1, stream);
     if (st != NQ_OK) return st;
-    s2.lds = lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, s2.kc, nc2);
+    s2.lds = lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, s2.kc, nc2, ks, static_cast<int>(tokens));
     s2.grid = dim3(static_cast<unsigned>(max2), count);
     return enqueue_stage2(batch, s2, stream);
 }

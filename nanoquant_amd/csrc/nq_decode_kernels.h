@@ -1077,6 +1077,35 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
     }
 }
 
+// Salient columns in the stage-2 epilogue. Up to kSalMax columns, the
+// workgroup's rows of W_sal (16 TW rows x k) and the gathered x[t, idx_k] *
+// scale_k of every token are loaded in the first pass, with the other
+// epilogue operands, and parked in LDS after the partial sums; each output
+// then adds Σ_k W_sal[row, k] * xs[t, k] from LDS. More columns take a loop of
+// element loads. Each thread loads at most kSalLoads weights in the first pass.
+constexpr int kSalMax = 96;
+constexpr int kSalLoads = 4;
+
+// LDS bytes of the staged salient operands (0 when the loop is used).
+__host__ __device__ constexpr int sal_lds_bytes(int64_t ks, int tw, int tokens) {
+    return ks > 0 && ks <= kSalMax ? static_cast<int>((16 * tw + tokens) * ks * 4) : 0;
+}
+
+// Raw bits of element i of an F32 / F16 / BF16 / I8 buffer (one load of the
+// element's size) and their value.
+__device__ __forceinline__ uint32_t load_bits(const void* __restrict__ p, int dtype, int i) {
+    if (dtype == NQ_DTYPE_F32) return static_cast<const uint32_t*>(p)[i];
+    if (dtype == NQ_DTYPE_I8) return static_cast<const uint8_t*>(p)[i];
+    return static_cast<const uint16_t*>(p)[i];
+}
+
+__device__ __forceinline__ float bits_value(uint32_t b, int dtype) {
+    if (dtype == NQ_DTYPE_F32) return __uint_as_float(b);
+    if (dtype == NQ_DTYPE_I8) return static_cast<float>(static_cast<int8_t>(b & 0xffu));
+    if (dtype == NQ_DTYPE_BF16) return __uint_as_float(b << 16);
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
+}
+
 // One stage-2 workgroup: output tiles [t0, t0 + TW) of linear `a`.
 template <int TPB, int TB, int TW, int KC, bool FUSED>
 __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __restrict__ lds) {
@@ -1093,6 +1122,12 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     float* const red = reinterpret_cast<float*>(lds);
     // One token: this wave's operand spread areas (KC of them) after the partial sums.
     char* const spread = lds + nc * TW * TB * 64 * 4 + wave * KC * kS2SpreadBytes;
+    // Staged salient operands after the spread areas: W rows [16 TW][ks], then xs [tokens][ks].
+    const int ks = static_cast<int>(a.salient_count);
+    const bool sal_lds = ks > 0 && ks <= kSalMax;  // uniform
+    float* const salw = reinterpret_cast<float*>(lds + nc * TW * TB * 64 * 4 +
+                                                 (TPB == 1 ? nw * KC * kS2SpreadBytes : 0));
+    float* const salx = salw + 16 * TW * ks;
 
     const int outs = TW * tokens * kTileRows;
     const OutIdx f = out_index<TPB>(threadIdx.x < outs ? threadIdx.x : 0, tokens);
@@ -1100,6 +1135,13 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     const int fr = fr0 < out ? fr0 : out - 1;
     RawElem rs0, bias0;
     bool stale = false;  // fused launch: the wait for stage 1 gave up
+    // First-pass salient loads: weights i = threadIdx.x + n * blockDim.x of the
+    // workgroup's block, and for threadIdx.x < tokens * ks one gathered x and scale.
+    uint32_t wbits[kSalLoads];
+    RawElem sx, ssc;
+    const int wtotal = 16 * TW * ks;           // weights parked per workgroup
+    const int wlimit = out * ks - 1;           // last weight element of the buffer
+    const int wbase = t0 * kTileRows * ks;     // first weight element of the workgroup
 
     // One pass; the first is peeled off the loop and issues the epilogue
     // operands after its own loads (see stage1_wg).
@@ -1123,6 +1165,17 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
             rs0 = load_elem(a.s_out, a.scale_dtype, fr);
             // No branch on the optional bias: without one, s_out is loaded instead and ignored.
             bias0 = load_elem(a.bias ? a.bias : a.s_out, a.bias ? a.bias_dtype : a.scale_dtype, fr);
+            if (sal_lds) {  // uniform
+#pragma unroll
+                for (int n = 0; n < kSalLoads; ++n) {
+                    const int i = wbase + static_cast<int>(threadIdx.x) + n * static_cast<int>(blockDim.x);
+                    wbits[n] = load_bits(a.salient_values, a.salient_dtype, i < wlimit ? i : wlimit);
+                }
+                const int j = static_cast<int>(threadIdx.x) < tokens * ks ? static_cast<int>(threadIdx.x) : 0;
+                const int t = j / ks, k = j - (j / ks) * ks;
+                sx = load_elem(a.x, a.x_dtype, t * in + a.salient_indices[k]);
+                ssc = load_elem(a.salient_scales ? a.salient_scales : a.s_in, a.scale_dtype, k);  // s_in: ks <= in
+            }
         }
         __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
 #pragma unroll
@@ -1146,6 +1199,26 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     const int step = nw * KC;
     pass(0, true);
     for (int base = step; base < nc; base += step) pass(base, false);
+    if (sal_lds) {  // uniform: park the salient operands beside the partial sums
+#pragma unroll
+        for (int n = 0; n < kSalLoads; ++n) {
+            const int i = static_cast<int>(threadIdx.x) + n * static_cast<int>(blockDim.x);
+            if (i < wtotal) salw[i] = bits_value(wbits[n], a.salient_dtype);
+        }
+        for (int i = static_cast<int>(threadIdx.x) + kSalLoads * static_cast<int>(blockDim.x); i < wtotal;
+             i += static_cast<int>(blockDim.x))  // blocks wider than the first-pass loads
+            salw[i] = bits_value(load_bits(a.salient_values, a.salient_dtype, wbase + i < wlimit ? wbase + i : wlimit),
+                                 a.salient_dtype);
+        const auto gathered = [&](const RawElem& xv, const RawElem& sv) __attribute__((always_inline)) {
+            return elem_value(xv, a.x_dtype) * (a.salient_scales ? elem_value(sv, a.scale_dtype) : 1.0f);
+        };
+        if (static_cast<int>(threadIdx.x) < tokens * ks) salx[threadIdx.x] = gathered(sx, ssc);
+        for (int j = static_cast<int>(threadIdx.x + blockDim.x); j < tokens * ks; j += static_cast<int>(blockDim.x)) {
+            const int t = j / ks, k = j - t * ks;  // more gathered values than threads
+            salx[j] = gathered(load_elem(a.x, a.x_dtype, t * in + a.salient_indices[k]),
+                               load_elem(a.salient_scales ? a.salient_scales : a.s_in, a.scale_dtype, k));
+        }
+    }
     __syncthreads();
     if (dead) return;  // uniform, after the workgroup's only barrier
 
@@ -1154,11 +1227,16 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
         float sum = 0.0f;
         for (int c = 0; c < nc; ++c) sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
         float val = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_out, a.scale_dtype, row), a.scale_dtype);
-        const int ks = static_cast<int>(a.salient_count);
-        for (int k = 0; k < ks; ++k) {
-            float wv = nq::load_f32(a.salient_values, a.salient_dtype, row * ks + k);
-            if (a.salient_scales) wv *= nq::load_f32(a.salient_scales, a.scale_dtype, k);
-            val += wv * nq::load_f32(a.x, a.x_dtype, o.t * in + a.salient_indices[k]);
+        if (sal_lds) {
+            const float* w = salw + (row - t0 * kTileRows) * ks;
+            const float* xs = salx + o.t * ks;
+            for (int k = 0; k < ks; ++k) val += w[k] * xs[k];
+        } else {
+            for (int k = 0; k < ks; ++k) {
+                float wv = nq::load_f32(a.salient_values, a.salient_dtype, row * ks + k);
+                if (a.salient_scales) wv *= nq::load_f32(a.salient_scales, a.scale_dtype, k);
+                val += wv * nq::load_f32(a.x, a.x_dtype, o.t * in + a.salient_indices[k]);
+            }
         }
         if (a.bias) val += elem_value(idx == threadIdx.x ? bias0 : load_elem(a.bias, a.bias_dtype, row), a.bias_dtype);
         return stale ? __builtin_nanf("") : val;

@@ -203,6 +203,135 @@ __global__ __launch_bounds__(kBlock) void k_dense_rows(const DenseRowsArgs args)
     *cell = args.accumulate ? *cell + v : v;
 }
 
+// Output-row sidecar, vector form: out[t, dst[r]] += scale[r] * Σ_k Q[r, k] * x[t, k]
+// for int8 rows Q [rows, K] with K % 16 == 0 and 16-byte aligned Q and x rows.
+// One workgroup per (row, token group); each thread takes 16 consecutive
+// columns per step (one 16-byte load of Q, one or more of x per token), all
+// loads of a step issued before use; the four waves' sums are added in wave
+// order, so the result does not depend on timing.
+constexpr int kRowSteps = 4;  // 16-byte Q loads in flight per thread
+
+template <int MT, int XDT>
+__global__ __launch_bounds__(kBlock) void k_row_sidecar(const int8_t* __restrict__ q, int64_t cols,
+                                                         const void* __restrict__ x, int64_t tokens,
+                                                         const void* __restrict__ scale, int scale_dtype,
+                                                         const int32_t* __restrict__ dst, float* __restrict__ out,
+                                                         int64_t out_ld) {
+    __shared__ float part[kBlock / 64][MT];
+    const int64_t row = blockIdx.x;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.y) * MT;
+    const int64_t vecs = cols / 16;
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = 0.0f;
+    for (int64_t v0 = threadIdx.x; v0 < vecs; v0 += kBlock * kRowSteps) {
+        int4 qv[kRowSteps];
+#pragma unroll
+        for (int s = 0; s < kRowSteps; ++s) {
+            const int64_t v = v0 + s * kBlock;
+            qv[s] = reinterpret_cast<const int4*>(q + row * cols)[v < vecs ? v : vecs - 1];
+        }
+#pragma unroll
+        for (int s = 0; s < kRowSteps; ++s) {
+            const int64_t v = v0 + s * kBlock;
+            if (v >= vecs) break;
+            float w[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t d = static_cast<uint32_t>(reinterpret_cast<const int*>(&qv[s])[i]);
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w[4 * i + b] = static_cast<float>(static_cast<int8_t>(d >> (8 * b)));
+            }
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int64_t tt = t0 + t < tokens ? t0 + t : tokens - 1;
+                float xv[16];
+                if constexpr (XDT == NQ_DTYPE_F32) {
+                    const float4* xp = reinterpret_cast<const float4*>(static_cast<const float*>(x) + tt * cols) + 4 * v;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float4 f = xp[i];
+                        xv[4 * i] = f.x; xv[4 * i + 1] = f.y; xv[4 * i + 2] = f.z; xv[4 * i + 3] = f.w;
+                    }
+                } else {
+                    const uint4* xp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + tt * cols) + 2 * v;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const uint4 h = xp[i];
+                        const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            if constexpr (XDT == NQ_DTYPE_BF16) {
+                                xv[8 * i + 2 * j] = __uint_as_float(hw[j] << 16);
+                                xv[8 * i + 2 * j + 1] = __uint_as_float(hw[j] & 0xffff0000u);
+                            } else {
+                                xv[8 * i + 2 * j] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hw[j])));
+                                xv[8 * i + 2 * j + 1] =
+                                    static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hw[j] >> 16)));
+                            }
+                        }
+                    }
+                }
+                float sum = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) sum += w[i] * xv[i];
+                acc[t] += sum;
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+        for (int off = 32; off >= 1; off >>= 1) acc[t] += __shfl_xor(acc[t], off);
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) part[threadIdx.x >> 6][t] = acc[t];
+    }
+    __syncthreads();
+    if (threadIdx.x < MT && t0 + threadIdx.x < tokens) {
+        const int t = threadIdx.x;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kBlock / 64; ++w) v += part[w][t];
+        v *= nq::load_f32(scale, scale_dtype, row);
+        float* cell = out + (t0 + t) * out_ld + dst[row];
+        *cell += v;
+    }
+}
+
+template <int XDT>
+int launch_row_sidecar_x(int mt, dim3 grid, hipStream_t s, const int8_t* q, int64_t cols, const void* x,
+                         int64_t tokens, const void* scale, int scale_dtype, const int32_t* dst, float* out,
+                         int64_t out_ld) {
+    switch (mt) {
+        case 1: hipLaunchKernelGGL((k_row_sidecar<1, XDT>), grid, dim3(kBlock), 0, s, q, cols, x, tokens, scale, scale_dtype, dst, out, out_ld); break;
+        case 2: hipLaunchKernelGGL((k_row_sidecar<2, XDT>), grid, dim3(kBlock), 0, s, q, cols, x, tokens, scale, scale_dtype, dst, out, out_ld); break;
+        case 4: hipLaunchKernelGGL((k_row_sidecar<4, XDT>), grid, dim3(kBlock), 0, s, q, cols, x, tokens, scale, scale_dtype, dst, out, out_ld); break;
+        default: hipLaunchKernelGGL((k_row_sidecar<8, XDT>), grid, dim3(kBlock), 0, s, q, cols, x, tokens, scale, scale_dtype, dst, out, out_ld); break;
+    }
+    return nq::launch_status();
+}
+
+// The vector row-sidecar kernel when the shapes allow it, else -1.
+int launch_row_sidecar(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, float* y, hipStream_t s) {
+    const int64_t cols = d->in_features;
+    const bool ok = cols % 16 == 0 && (reinterpret_cast<uintptr_t>(d->row_values) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(x) & 15) == 0 && nq::is_float_dtype(x_dtype);
+    if (!ok) return -1;
+    const int mt = tokens <= 1 ? 1 : (tokens <= 2 ? 2 : (tokens <= 4 ? 4 : 8));
+    const dim3 grid(static_cast<unsigned>(d->row_count), static_cast<unsigned>((tokens + mt - 1) / mt));
+    switch (x_dtype) {
+        case NQ_DTYPE_F32:
+            return launch_row_sidecar_x<NQ_DTYPE_F32>(mt, grid, s, d->row_values, cols, x, tokens, d->row_scales,
+                                                      d->scale_dtype, d->row_indices, y, d->out_features);
+        case NQ_DTYPE_F16:
+            return launch_row_sidecar_x<NQ_DTYPE_F16>(mt, grid, s, d->row_values, cols, x, tokens, d->row_scales,
+                                                      d->scale_dtype, d->row_indices, y, d->out_features);
+        default:
+            return launch_row_sidecar_x<NQ_DTYPE_BF16>(mt, grid, s, d->row_values, cols, x, tokens, d->row_scales,
+                                                       d->scale_dtype, d->row_indices, y, d->out_features);
+    }
+}
+
 int tokens_tile(int64_t tokens) {
     if (tokens <= 1) return 1;
     if (tokens <= 2) return 2;
@@ -313,6 +442,8 @@ int apply_extras(const nq_linear_desc* d, const void* x, int x_dtype, int64_t to
         if (st != NQ_OK) return st;
     }
     if (d->row_count > 0) {
+        st = launch_row_sidecar(d, x, x_dtype, tokens, static_cast<float*>(y), s);
+        if (st >= 0) return st;
         DenseRowsArgs r{};
         r.w = d->row_values;
         r.w_dtype = NQ_DTYPE_I8;
