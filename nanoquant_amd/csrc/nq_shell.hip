@@ -48,6 +48,21 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (row_lane(v, 0) + row_lane(v, 16)) + (row_lane(v, 32) + row_lane(v, 48));
 }
 
+// Max / sum over each row of 16 lanes (every lane of the row gets it).
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_src<0xB1>(v, -INFINITY));
+    v = fmaxf(v, dpp_src<0x4E>(v, -INFINITY));
+    v = fmaxf(v, dpp_src<0x141>(v, -INFINITY));
+    return fmaxf(v, dpp_src<0x140>(v, -INFINITY));
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_src<0xB1>(v, 0.0f);
+    v += dpp_src<0x4E>(v, 0.0f);
+    v += dpp_src<0x141>(v, 0.0f);
+    return v + dpp_src<0x140>(v, 0.0f);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp_src<0xB1>(v, -INFINITY));
     v = fmaxf(v, dpp_src<0x4E>(v, -INFINITY));
@@ -576,6 +591,256 @@ __global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__
 }
 
 // ---------------------------------------------------------------------------
+// One-token decode attention on MFMA (head_dim 128, four q heads per kv head,
+// 16-bit cache): the same workgroup grid, loads, staging, RoPE / KV append and
+// partial output as k_decode_attention below, with the two products on
+// v_mfma_f32_16x16x32 (bf16 or f16, the cache's type). The query and the
+// softmax weights are fp32; each is split into three 16-bit parts (the
+// rounding of the value, of its remainder and of the remainder's remainder),
+// which occupy A rows 4h, 4h + 1, 4h + 2 for q head h of the group (row
+// 4h + 3 is zero), so the products carry about 24 bits of the fp32 operand
+// and K / V (stored 16-bit) are exact. Output rows 4h .. 4h + 3 then sit in
+// the four accumulator registers of lane group h.
+//   Scores: wave w takes cache rows 16w + n (B columns n; B = K rows from LDS,
+//   eight dimensions per lane per step), four steps of 32 dimensions.
+//   P.V: wave w takes dimensions 32w + 16u + n (u = 0, 1), two steps of 32
+//   cache rows; A = the weights from LDS, B = V rows from LDS.
+// The softmax max and sum cross the four waves through LDS; rows past the
+// token's position weigh zero (their LDS rows are zero-filled, so 0 * V stays
+// 0). Results differ from k_decode_attention only by rounding.
+constexpr int kMfmaHeads = 4;
+
+template <int CT>
+struct Mfma16 {
+    typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+};
+template <>
+struct Mfma16<NQ_DTYPE_F16> {
+    typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+};
+
+typedef float v4f_t __attribute__((ext_vector_type(4)));
+
+template <int CT>
+__device__ __forceinline__ v4f_t mfma16(const typename Mfma16<CT>::v8& a, const typename Mfma16<CT>::v8& b,
+                                        const v4f_t& c) {
+    if constexpr (CT == NQ_DTYPE_BF16) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// The 16-bit rounding (nearest-even) of x, and a 16-bit value as fp32.
+template <int CT>
+__device__ __forceinline__ uint16_t to16(float x) {
+    if constexpr (CT == NQ_DTYPE_BF16) return f32_to_bf16_bits(x);
+    else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+template <int CT>
+__device__ __forceinline__ float from16(uint16_t h) {
+    if constexpr (CT == NQ_DTYPE_BF16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
+    else return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// The three 16-bit parts of x: the rounding of x, of its remainder and of the
+// remainder's remainder (each subtraction is exact in fp32).
+template <int CT>
+__device__ __forceinline__ void split3(float x, uint16_t (&h)[3]) {
+    h[0] = to16<CT>(x);
+    const float r1 = x - from16<CT>(h[0]);
+    h[1] = to16<CT>(r1);
+    h[2] = to16<CT>(r1 - from16<CT>(h[1]));
+}
+
+template <int CT>
+constexpr size_t decode_attention_mfma_lds() {
+    // K and V blocks (plus a scratch row each), the 16-bit parts of q [4][4][128]
+    // and of P [4][4][64], maxima and sums [2][4][4].
+    return static_cast<size_t>(kSeqBlock + 1) * k_row_bytes<128, CT>() * 2 + kMfmaHeads * 4 * 128 * 2 +
+           kMfmaHeads * 4 * kSeqBlock * 2 + 2 * kMfmaHeads * kMfmaHeads * 4;
+}
+
+template <int CT>
+__global__ __launch_bounds__(kMfmaHeads * kWave) void k_decode_attention_mfma(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int kv_heads,
+    const void* __restrict__ q_norm, const void* __restrict__ k_norm, int ndt, float eps,
+    const float* __restrict__ cos_table, const float* __restrict__ sin_table, const int32_t* __restrict__ position,
+    int64_t max_positions, char* __restrict__ k_cache, char* __restrict__ v_cache, float scaling,
+    float* __restrict__ part_ml, float* __restrict__ part_acc) {
+    constexpr int D = 128;
+    constexpr int G = kMfmaHeads;
+    constexpr int E = D / kWave;
+    constexpr int RB = k_row_bytes<D, CT>();  // padded row in LDS (K and V alike)
+    constexpr int VRB = D * 2;                // row in the cache
+    constexpr int PIECES = VRB / 16;
+    constexpr int PER_THREAD = kSeqBlock * PIECES / (G * kWave);
+    typedef typename Mfma16<CT>::v8 v8;
+    extern __shared__ float lds_raw[];
+    char* klds = reinterpret_cast<char*>(lds_raw);
+    char* vlds = klds + (kSeqBlock + 1) * RB;
+    uint16_t* qs = reinterpret_cast<uint16_t*>(vlds + (kSeqBlock + 1) * RB);  // [G][4 parts][D]
+    uint16_t* ps = qs + G * 4 * D;                                             // [G][4 parts][64]
+    float* mx = reinterpret_cast<float*>(ps + G * 4 * kSeqBlock);             // [G][4 waves]
+    float* ls = mx + G * G;                                                    // [G][4 waves]
+
+    const int g = blockIdx.x;
+    const int s = blockIdx.y;
+    const int blocks = gridDim.y;
+    const int q_heads = kv_heads * G;
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int lane = threadIdx.x & (kWave - 1);
+
+    NormRopeIn<D> qin, kin;
+    load_norm_rope_in<D>(qin, q + static_cast<int64_t>(g * G + w) * D, q_norm, ndt, lane);
+    load_norm_rope_in<D>(kin, k + static_cast<int64_t>(g) * D, k_norm, ndt, lane);
+    float vraw[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) vraw[j] = v[static_cast<int64_t>(g) * D + lane + kWave * j];
+
+    const int64_t row0 = static_cast<int64_t>(s) * kSeqBlock;
+    const int64_t head_row0 = static_cast<int64_t>(g) * max_positions;
+    u32x4 kp[PER_THREAD], vp[PER_THREAD];
+    const int last_row = static_cast<int>(max_positions - 1 - row0);
+    const char* kbase = k_cache + (head_row0 + row0) * VRB;
+    const char* vbase = v_cache + (head_row0 + row0) * VRB;
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int idx = threadIdx.x + i * G * kWave;
+        const int r = idx / PIECES, c = idx % PIECES;
+        const int rr = r < last_row ? r : last_row;
+        kp[i] = *reinterpret_cast<const u32x4*>(kbase + rr * VRB + 16 * c);
+        vp[i] = *reinterpret_cast<const u32x4*>(vbase + rr * VRB + 16 * c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int64_t pos = position[0];
+    const bool live = pos >= 0 && pos < max_positions && row0 <= pos;  // uniform
+    const int64_t p = live ? pos : row0;
+    const bool owns_p = live && p < row0 + kSeqBlock;
+    const int rows = live ? static_cast<int>(owns_p ? p - row0 + 1 : kSeqBlock) : 1;
+    const int cached = live ? (owns_p ? rows - 1 : rows) : 0;
+
+    float cs[E], sn[E];
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int d = lane + kWave * j;
+        const int fi = d < D / 2 ? d : d - D / 2;
+        cs[j] = cos_table[p * (D / 2) + fi];
+        sn[j] = sin_table[p * (D / 2) + fi];
+    }
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) asm volatile("" : "+v"(kp[i]), "+v"(vp[i]));
+    float qy[E];
+    norm_rope_regs<D>(qin, q_norm != nullptr, ndt, eps, cs, sn, lane, qy);
+    // Cached rows go to their LDS rows; rows past the token's row are zero
+    // (their weights are zero, and 0 * V must stay 0); the token's own row is
+    // written below, so its staging piece goes to the scratch row.
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int idx = threadIdx.x + i * G * kWave;
+        const int r = idx / PIECES, c = idx % PIECES;
+        const bool keep = r < cached;
+        const int lr = keep || r >= rows ? r : kSeqBlock;
+        const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(klds + lr * RB + 16 * c) = keep ? kp[i] : zero;
+        *reinterpret_cast<u32x4*>(vlds + lr * RB + 16 * c) = keep ? vp[i] : zero;
+    }
+#pragma unroll
+    for (int j = 0; j < E; ++j) {  // wave w: the parts of q head w (part 3 zero)
+        uint16_t h[3];
+        split3<CT>(qy[j], h);
+        const int d = lane + kWave * j;
+#pragma unroll
+        for (int part = 0; part < 3; ++part) qs[(w * 4 + part) * D + d] = h[part];
+        qs[(w * 4 + 3) * D + d] = 0;
+    }
+    float ky[E];
+    norm_rope_regs<D>(kin, k_norm != nullptr, ndt, eps, cs, sn, lane, ky);
+    const int nr = owns_p ? rows - 1 : kSeqBlock;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const int d = lane + kWave * j;
+        nq::store_f32_as(klds + nr * RB, CT, d, ky[j]);
+        nq::store_f32_as(vlds + nr * RB, CT, d, vraw[j]);
+    }
+    if (owns_p) {
+        const int64_t crow = (head_row0 + p) * D;
+        if (w == 0) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) nq::store_f32_as(k_cache, CT, crow + lane + kWave * j, ky[j]);
+        }
+        if (w == G - 1) {
+#pragma unroll
+            for (int j = 0; j < E; ++j) nq::store_f32_as(v_cache, CT, crow + lane + kWave * j, vraw[j]);
+        }
+    }
+    __syncthreads();
+
+    // Lane (kg, n): column n of the B operands, q head kg of the A rows
+    // (row 4 kg + part, part = n & 3) and of the accumulator rows 4 kg + j.
+    const int n = lane & 15, kg = lane >> 4;
+    const int arow = lane & 15;  // A row: head arow / 4, part arow % 4 (parts are stored in that order)
+    // Scores of cache rows 16w + n.
+    v4f_t sc = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < D / 32; ++st) {
+        const int d0 = 32 * st + 8 * kg;
+        const v8 a = *reinterpret_cast<const v8*>(qs + arow * D + d0);
+        const v8 b = *reinterpret_cast<const v8*>(klds + (16 * w + n) * RB + 2 * d0);
+        sc = mfma16<CT>(a, b, sc);
+    }
+    const int r = 16 * w + n;
+    const bool valid = r < rows;
+    const float score = valid ? ((sc[0] + sc[1]) + (sc[2] + sc[3])) * scaling : -INFINITY;  // head kg
+    const float mw = row16_max(score);
+    if (n == 0) mx[kg * G + w] = mw;
+    __syncthreads();
+    float M = mx[kg * G];
+#pragma unroll
+    for (int i = 1; i < G; ++i) M = fmaxf(M, mx[kg * G + i]);
+    const float pr = valid ? expf(score - M) : 0.0f;
+    const float lw = row16_sum(pr);
+    {
+        uint16_t h[3];
+        split3<CT>(pr, h);
+#pragma unroll
+        for (int part = 0; part < 3; ++part) ps[(kg * 4 + part) * kSeqBlock + r] = h[part];
+        ps[(kg * 4 + 3) * kSeqBlock + r] = 0;
+    }
+    if (n == 0) ls[kg * G + w] = lw;
+    __syncthreads();
+
+    // P.V for dimensions 32w + 16u + n.
+    v4f_t o[2] = {v4f_t{0.0f, 0.0f, 0.0f, 0.0f}, v4f_t{0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+    for (int t = 0; t < kSeqBlock / 32; ++t) {
+        const int r0 = 32 * t + 8 * kg;
+        const v8 a = *reinterpret_cast<const v8*>(ps + arow * kSeqBlock + r0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            union {
+                uint16_t h[8];
+                v8 v;
+            } b;
+            const int d = 32 * w + 16 * u + n;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) b.h[i] = *reinterpret_cast<const uint16_t*>(vlds + (r0 + i) * RB + 2 * d);
+            o[u] = mfma16<CT>(a, b.v, o[u]);
+        }
+    }
+    if (!live) return;
+    const int64_t pi = attn_part_index(0, g * G + kg, s, q_heads, blocks);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) part_acc[pi * D + 32 * w + 16 * u + n] = (o[u][0] + o[u][1]) + (o[u][2] + o[u][3]);
+    if (w == 0 && n == 0) {
+        float l = 0.0f;
+#pragma unroll
+        for (int i = 0; i < G; ++i) l += ls[kg * G + i];
+        part_ml[2 * pi] = M;
+        part_ml[2 * pi + 1] = l;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // One-token decode attention with the q/k RMSNorm + RoPE + KV append fused in
 // (pass 1; k_attention_merge is pass 2). Workgroup (kv head g, 64-row cache
 // block s), one wave per q head of the group:
@@ -978,11 +1243,17 @@ int launch_decode_attention_g(const float* q, const float* k, const float* v, in
                               const int32_t* position, int64_t max_positions, void* kc, void* vc, float scaling,
                               void* out, int odt, float* ml, float* acc, hipStream_t st) {
     const int blocks = attention_blocks(max_positions);
-    const size_t lds = decode_attention_lds<D, CT, G>();
-    if (lds > 64 * 1024) return NQ_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL((k_decode_attention<D, CT, G>), dim3(kv_heads, blocks), dim3(G * kWave), lds, st, q, k, v,
-                       kv_heads, qn, kn, ndt, eps, cs, sn, position, max_positions, static_cast<char*>(kc),
-                       static_cast<char*>(vc), scaling, ml, acc);
+    if constexpr (D == 128 && G == kMfmaHeads && CT != NQ_DTYPE_F32) {
+        hipLaunchKernelGGL((k_decode_attention_mfma<CT>), dim3(kv_heads, blocks), dim3(G * kWave),
+                           decode_attention_mfma_lds<CT>(), st, q, k, v, kv_heads, qn, kn, ndt, eps, cs, sn, position,
+                           max_positions, static_cast<char*>(kc), static_cast<char*>(vc), scaling, ml, acc);
+    } else {
+        const size_t lds = decode_attention_lds<D, CT, G>();
+        if (lds > 64 * 1024) return NQ_ERR_UNSUPPORTED;
+        hipLaunchKernelGGL((k_decode_attention<D, CT, G>), dim3(kv_heads, blocks), dim3(G * kWave), lds, st, q, k, v,
+                           kv_heads, qn, kn, ndt, eps, cs, sn, position, max_positions, static_cast<char*>(kc),
+                           static_cast<char*>(vc), scaling, ml, acc);
+    }
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     hipLaunchKernelGGL(k_attention_merge<D>, dim3(kv_heads * G, 1), dim3(D), 0, st, ml, acc, kv_heads * G, blocks,
                        kSeqBlock, position, max_positions, out, odt);
