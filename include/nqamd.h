@@ -251,6 +251,15 @@ typedef enum nq_input_kind {
                                member i sees silu(g) * u                              */
 } nq_input_kind;
 
+/* Output forms of a fused one-token decode call (nq_linear_batch_fused). */
+typedef enum nq_output_kind {
+    NQ_OUTPUT_PLAIN = 0,        /* each member writes its y (or adds it to its residual) */
+    NQ_OUTPUT_SILU_PRODUCT = 1  /* exactly two members of equal out and rank, no salient
+                                   columns, bias, patch, row sidecar or residuals: ys[0]
+                                   receives silu(y_0) * y_1 in y_dtype (ys[1] unused);
+                                   the SiLU-gated MLP input of the next projection */
+} nq_output_kind;
+
 /* Decoder fusions around the packed linears of one decode token. */
 typedef struct nq_decode_fusion {
     int32_t input_kind;              /* nq_input_kind                                   */
@@ -264,6 +273,7 @@ typedef struct nq_decode_fusion {
                                         residuals[i] (fp32 [out]) instead of writing y  */
     float* const* out_slots;         /* with residuals: [count] fp32 [ceil(out / 16)]
                                         sums of the new residual's squares per tile     */
+    int32_t output_kind;             /* nq_output_kind                                  */
 } nq_decode_fusion;
 
 /* One launch pair for `count` (1..8) packed linears of ONE token with the

@@ -242,7 +242,7 @@ int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, L
     return NQ_OK;
 }
 
-int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t stream) {
+int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t stream, bool pair = false) {
     int64_t tiles1 = 0, tiles2 = 0, nc1 = 0, nc2 = 0, ks = 0;
     for (int i = 0; i < batch.count; ++i) {
         ks = batch.p[i].salient_count <= kSalMax && batch.p[i].salient_count > ks ? batch.p[i].salient_count : ks;
@@ -294,6 +294,12 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
     int st = enqueue_stage1(batch, s1, stream);
     if (st != NQ_OK) return st;
     s2.lds = lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, s2.kc, nc2, ks, static_cast<int>(tokens));
+    if (pair) {
+        // Both members' partial sums in one workgroup: a second partial-sum area.
+        s2.lds += static_cast<size_t>(nc2) * s2.tw * s2.tb * 64 * 4;
+        s2.grid = dim3(static_cast<unsigned>(max2), 1);
+        return enqueue_stage2_pair(batch, s2, stream);
+    }
     s2.grid = dim3(static_cast<unsigned>(max2), count);
     return enqueue_stage2(batch, s2, stream);
 }
@@ -345,17 +351,28 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
     if (vector_ok) {
         ak = x_dtype == NQ_DTYPE_BF16 ? kActBf16 : (x_dtype == NQ_DTYPE_F16 ? kActF16 : kActF32);
     }
+    bool pair = false;
     if (fusion) {
         // The fused forms have vector kernels only: one token, the split launch,
         // fp32 x and fp16 scales with the vector-load shape.
         if (tokens != 1 || descs[0]->decode_launch != NQ_DECODE_SPLIT) return NQ_ERR_UNSUPPORTED;
+        if (fusion->output_kind == NQ_OUTPUT_SILU_PRODUCT) {
+            const nq_linear_desc* a = descs[0];
+            const nq_linear_desc* b = count == 2 ? descs[1] : nullptr;
+            if (!b || fusion->residuals || a->out_features != b->out_features || a->rank != b->rank) return NQ_ERR_SHAPE;
+            for (const nq_linear_desc* d : {a, b})
+                if (d->salient_count > 0 || d->bias || d->patch_rank > 0 || d->row_count > 0) return NQ_ERR_UNSUPPORTED;
+            pair = true;
+        } else if (fusion->output_kind != NQ_OUTPUT_PLAIN) {
+            return NQ_ERR_ARGUMENT;
+        }
         if (fusion->input_kind != NQ_INPUT_PLAIN) {
             if (x_dtype != NQ_DTYPE_F32) return NQ_ERR_DTYPE;
             if (!vector_ok) return NQ_ERR_ALIGNMENT;
             ak = fusion->input_kind == NQ_INPUT_RMSNORM ? kActNormF32 : kActGatedF32;
         }
     }
-    return launch_batch(batch, tokens, ak, descs[0]->decode_launch == NQ_DECODE_FUSED, stream);
+    return launch_batch(batch, tokens, ak, descs[0]->decode_launch == NQ_DECODE_FUSED, stream, pair);
 }
 
 }  // namespace nq

@@ -1106,9 +1106,13 @@ __device__ __forceinline__ float bits_value(uint32_t b, int dtype) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b)));
 }
 
-// One stage-2 workgroup: output tiles [t0, t0 + TW) of linear `a`.
-template <int TPB, int TB, int TW, int KC, bool FUSED>
-__device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __restrict__ lds) {
+// One stage-2 workgroup: output tiles [t0, t0 + TW) of linear `a`. PAIR: the
+// same tiles of `a` (gate) and `b` (up, same geometry, no sidecars or bias),
+// one token, and the output silu(y_a) * y_b stored to a.y (the decoder's
+// SiLU-gated MLP product), so the down projection reads one plain input.
+template <int TPB, int TB, int TW, int KC, bool FUSED, bool PAIR = false>
+__device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __restrict__ lds,
+                                          const LinArgs* pair = nullptr) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nw = a.nw2;
@@ -1120,20 +1124,22 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     const int nt = static_cast<int>(a.g2.nt), nb = static_cast<int>(a.g2.nb), nc = static_cast<int>(a.g2.nc);
     const int out = static_cast<int>(a.out), in = static_cast<int>(a.in);
     float* const red = reinterpret_cast<float*>(lds);
+    // PAIR: the second member's partial sums follow the first's.
+    float* const red_b = red + nc * TW * TB * 64;
+    char* const after_red = lds + (PAIR ? 2 : 1) * nc * TW * TB * 64 * 4;
     // One token: this wave's operand spread areas (KC of them) after the partial sums.
-    char* const spread = lds + nc * TW * TB * 64 * 4 + wave * KC * kS2SpreadBytes;
+    char* const spread = after_red + wave * KC * kS2SpreadBytes;
     // Staged salient operands after the spread areas: W rows [16 TW][ks], then xs [tokens][ks].
     const int ks = static_cast<int>(a.salient_count);
     const bool sal_lds = ks > 0 && ks <= kSalMax;  // uniform
-    float* const salw = reinterpret_cast<float*>(lds + nc * TW * TB * 64 * 4 +
-                                                 (TPB == 1 ? nw * KC * kS2SpreadBytes : 0));
+    float* const salw = reinterpret_cast<float*>(after_red + (TPB == 1 ? nw * KC * kS2SpreadBytes : 0));
     float* const salx = salw + 16 * TW * ks;
 
     const int outs = TW * tokens * kTileRows;
     const OutIdx f = out_index<TPB>(threadIdx.x < outs ? threadIdx.x : 0, tokens);
     const int fr0 = (t0 + f.tt) * kTileRows + f.n;
     const int fr = fr0 < out ? fr0 : out - 1;
-    RawElem rs0, bias0;
+    RawElem rs0, bias0, rs1;
     bool stale = false;  // fused launch: the wait for stage 1 gave up
     // First-pass salient loads: weights i = threadIdx.x + n * blockDim.x of the
     // workgroup's block, and for threadIdx.x < tokens * ks one gathered x and scale.
@@ -1145,23 +1151,30 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
 
     // One pass; the first is peeled off the loop and issues the epilogue
     // operands after its own loads (see stage1_wg).
-    const auto pass = [&](const int base, const bool first) __attribute__((always_inline)) {
-        const PassChunks<KC> pc = pass_chunks<KC>(base, wave, nw, nc);
+    // A pass is split into its loads and its arithmetic so that a paired
+    // workgroup issues both members' loads before either waits.
+    struct PassRegs {
+        PassChunks<KC> pc;
         S2Regs<TB, TW> r[KC];
+        int e[TB];
+    };
+    const auto load_pass = [&](const LinArgs& m, PassRegs& ps, const int base, const bool first)
+                               __attribute__((always_inline)) {
+        ps.pc = pass_chunks<KC>(base, wave, nw, nc);
 #pragma unroll
-        for (int j = 0; j < KC; ++j) load_words(r[j].w, a.u_tiles, nt, nb, t0, pc.c[j], lane);
+        for (int j = 0; j < KC; ++j) load_words(ps.r[j].w, m.u_tiles, nt, nb, t0, ps.pc.c[j], lane);
         // The U words do not depend on stage 1; the fused launch waits for its
         // signal only now.
-        if (FUSED && first) stale = wait_ready(a, t0, TW, wg, dead);
+        if (FUSED && first) stale = wait_ready(m, t0, TW, wg, dead);
 #pragma unroll
-        for (int j = 0; j < KC; ++j) load_s2_ops<TPB, TB, TW>(r[j], a, pc.c[j], lane);
-        int e[TB];
+        for (int j = 0; j < KC; ++j) load_s2_ops<TPB, TB, TW>(ps.r[j], m, ps.pc.c[j], lane);
 #pragma unroll
         for (int tb = 0; tb < TB; ++tb) {
             const int t = tb * TPB + (TPB == 1 ? 0 : (lane >> 4));
-            e[tb] = a.lme[t < tokens ? t : tokens - 1];
+            ps.e[tb] = m.lme[t < tokens ? t : tokens - 1];
         }
-        if (first) {
+        if (PAIR && first && &m != &a) rs1 = load_elem(m.s_out, m.scale_dtype, fr);
+        if (first && &m == &a) {
             rs0 = load_elem(a.s_out, a.scale_dtype, fr);
             // No branch on the optional bias: without one, s_out is loaded instead and ignored.
             bias0 = load_elem(a.bias ? a.bias : a.s_out, a.bias ? a.bias_dtype : a.scale_dtype, fr);
@@ -1177,28 +1190,56 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
                 ssc = load_elem(a.salient_scales ? a.salient_scales : a.s_in, a.scale_dtype, k);  // s_in: ks <= in
             }
         }
-        __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
+    };
+    const auto compute_pass = [&](PassRegs& ps, float* const redm) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < KC; ++j) {
-            if (!pc.live[j]) continue;  // uniform
-            const int c = pc.c[j];
+            if (!ps.pc.live[j]) continue;  // uniform
+            const int c = ps.pc.c[j];
             const int dw = chunk_words32(nb, c);
-            spread_s2_ops<TPB, TB, TW>(r[j], spread + j * kS2SpreadBytes, lane);
+            spread_s2_ops<TPB, TB, TW>(ps.r[j], spread + j * kS2SpreadBytes, lane);
 #pragma unroll
             for (int tb = 0; tb < TB; ++tb) {
                 if (tb * TPB >= tokens) break;
-                const v4i S = ones_mfma(r[j].a[tb]);
+                const v4i S = ones_mfma(ps.r[j].a[tb]);
                 // A poisoned token (non-finite activations) yields NaN partials.
-                const float sc = e[tb] == kPoisonExp ? __builtin_nanf("") : exp2i(-e[tb] - 7);
+                const float sc = ps.e[tb] == kPoisonExp ? __builtin_nanf("") : exp2i(-ps.e[tb] - 7);
 #pragma unroll
                 for (int tt = 0; tt < TW; ++tt)
-                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<4>(r[j].a[tb], S, r[j].w[tt], dw, sc);
+                    redm[((c * TW + tt) * TB + tb) * 64 + lane] =
+                        tile_partial<4>(ps.r[j].a[tb], S, ps.r[j].w[tt], dw, sc);
             }
         }
     };
     const int step = nw * KC;
-    pass(0, true);
-    for (int base = step; base < nc; base += step) pass(base, false);
+    {
+        PassRegs pa;
+        load_pass(a, pa, 0, true);
+        if constexpr (PAIR) {
+            PassRegs pb;
+            load_pass(*pair, pb, 0, true);
+            __builtin_amdgcn_sched_barrier(0);  // both members' loads are issued before any use
+            compute_pass(pa, red);
+            compute_pass(pb, red_b);
+        } else {
+            __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
+            compute_pass(pa, red);
+        }
+    }
+    for (int base = step; base < nc; base += step) {
+        PassRegs ps;
+        load_pass(a, ps, base, false);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_pass(ps, red);
+    }
+    if constexpr (PAIR) {
+        for (int base = step; base < nc; base += step) {
+            PassRegs ps;
+            load_pass(*pair, ps, base, false);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_pass(ps, red_b);
+        }
+    }
     if (sal_lds) {  // uniform: park the salient operands beside the partial sums
 #pragma unroll
         for (int n = 0; n < kSalLoads; ++n) {
@@ -1241,6 +1282,25 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
         if (a.bias) val += elem_value(idx == threadIdx.x ? bias0 : load_elem(a.bias, a.bias_dtype, row), a.bias_dtype);
         return stale ? __builtin_nanf("") : val;
     };
+    if constexpr (PAIR) {
+        // One token: outputs idx = 16 tt + n; silu(gate) * up in a.y's dtype.
+        for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
+            const OutIdx o = out_index<TPB>(idx, tokens);
+            const int row = (t0 + o.tt) * kTileRows + o.n;
+            if (t0 + o.tt >= nt || row >= out) continue;
+            float sg = 0.0f, su = 0.0f;
+            for (int c = 0; c < nc; ++c) {
+                sg += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
+                su += red_b[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
+            }
+            const bool own = idx == static_cast<int>(threadIdx.x);
+            const float g = sg * elem_value(own ? rs0 : load_elem(a.s_out, a.scale_dtype, row), a.scale_dtype);
+            const float u = su * elem_value(own ? rs1 : load_elem(pair->s_out, pair->scale_dtype, row),
+                                            pair->scale_dtype);
+            nq::store_f32_as(a.y, a.y_dtype, row, g / (1.0f + expf(-g)) * u);
+        }
+        return;
+    }
     if (TPB == 1 && a.residual) {
         // Residual epilogue (one token, outs <= 64: wave 0, lanes 16 tt + n):
         // residual[row] += value, and lane 16 tt writes the tile's sum of the
@@ -1293,6 +1353,16 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage2(const Batch batch) {
     stage2_wg<TPB, TB, TW, KC, false>(a, blockIdx.x, lds);
 }
 
+// Paired stage 2 (one token): members 0 and 1 of the batch, one grid row.
+template <int TW, int KC, int THREADS>
+__global__ __launch_bounds__(THREADS) void k_decode_stage2_pair(const Batch batch) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const LinArgs a = load_args(batch, 0);
+    const LinArgs b = load_args(batch, 1);
+    if (blockIdx.x >= a.nwg2) return;
+    stage2_wg<1, 1, TW, KC, false, true>(a, blockIdx.x, lds, &b);
+}
+
 // Fused launch (one tile per workgroup, generic stage-1 loads): grid rows
 // [0, count) are stage 1, rows [count, 2 count) stage 2.
 template <int TPB, int TB, int KC1, int KC2, int THREADS>
@@ -1331,6 +1401,7 @@ int enqueue_stage1_f32(const Batch& batch, const LaunchShape& s, hipStream_t str
 int enqueue_stage1_generic(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_stage1_fused(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_stage2(const Batch& batch, const LaunchShape& s, hipStream_t stream);
+int enqueue_stage2_pair(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_fused(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 
 }  // namespace nqdec

@@ -21,7 +21,22 @@ int by_tiles(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     return s.kc == 2 ? go<TPB, 1, 1, 2>(batch, s, stream) : go<TPB, 1, 1, 1>(batch, s, stream);
 }
 
+template <int TW, int KC>
+int go_pair(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
+    constexpr int kThreads = threads_for(1, KC);
+    if (64 * s.nw > kThreads) return NQ_ERR_LAUNCH;
+    hipLaunchKernelGGL((k_decode_stage2_pair<TW, KC, kThreads>), s.grid, dim3(64 * s.nw), s.lds, stream, batch);
+    return nq::launch_status();
+}
+
 }  // namespace
+
+int enqueue_stage2_pair(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
+    if (s.tw == 4) return s.kc == 2 ? go_pair<4, 2>(batch, s, stream) : go_pair<4, 1>(batch, s, stream);
+    if (s.tw == 3) return s.kc == 2 ? go_pair<3, 2>(batch, s, stream) : go_pair<3, 1>(batch, s, stream);
+    if (s.tw == 2) return s.kc == 2 ? go_pair<2, 2>(batch, s, stream) : go_pair<2, 1>(batch, s, stream);
+    return s.kc == 2 ? go_pair<1, 2>(batch, s, stream) : go_pair<1, 1>(batch, s, stream);
+}
 
 int enqueue_stage2(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     if (s.tpb == 1) return by_tiles<1>(batch, s, stream);

@@ -580,7 +580,8 @@ extern "C" int nq_linear_batch_fused(const nq_linear_desc* const* descs, int32_t
         int st = validate(d);
         if (st != NQ_OK) return st;
         if (!d->tiles || !xs[i]) return NQ_ERR_ARGUMENT;
-        if (!fusion->residuals && !ys[i]) return NQ_ERR_ARGUMENT;
+        const bool silu_second = fusion->output_kind == NQ_OUTPUT_SILU_PRODUCT && i == 1;  // writes nothing
+        if (!fusion->residuals && !ys[i] && !silu_second) return NQ_ERR_ARGUMENT;
         if (d->patch_rank > 0 || d->row_count > 0) return NQ_ERR_UNSUPPORTED;  // they add to y afterwards
         if (d->scale_dtype != NQ_DTYPE_F16) return NQ_ERR_DTYPE;
         for (int j = 0; j < i; ++j) {

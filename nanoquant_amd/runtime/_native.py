@@ -132,6 +132,8 @@ class LinearDesc(ctypes.Structure):
 
 # nq_input_kind
 INPUT_PLAIN, INPUT_RMSNORM, INPUT_SILU_GATE = 0, 1, 2
+# nq_output_kind
+OUTPUT_PLAIN, OUTPUT_SILU_PRODUCT = 0, 1
 
 
 class DecodeFusion(ctypes.Structure):
@@ -146,6 +148,7 @@ class DecodeFusion(ctypes.Structure):
         ("ups", ctypes.POINTER(ctypes.c_void_p)),
         ("residuals", ctypes.POINTER(ctypes.c_void_p)),
         ("out_slots", ctypes.POINTER(ctypes.c_void_p)),
+        ("output_kind", ctypes.c_int32),
     ]
 
 

@@ -355,12 +355,15 @@ class PackedDecoder:
             if fused:
                 self.backend.linear_batch_fused([b.attn.view(-1)], [prepared["o_proj"]], residuals=[b.residual[0]],
                                                 out_slots=[b.o_slots])
+                # gate and up in one workgroup per output tile: the epilogue writes
+                # silu(gate) * up in the activation dtype, the down projection's input
                 self.backend.linear_batch_fused([b.residual[0]] * 2, [prepared["gate_proj"], prepared["up_proj"]],
                                                 input_kind="rmsnorm", eps=c.eps,
                                                 col_scales=list(self.col_scales[i][3:]), norm_slots=b.o_slots,
-                                                outs=[b.gate[0], b.up[0]])
-                self.backend.linear_batch_fused([b.gate[0]], [prepared["down_proj"]], input_kind="silu_gate",
-                                                ups=[b.up[0]], residuals=[b.residual[0]], out_slots=[b.down_slots])
+                                                output_kind="silu_product", outs=[b.act[0]],
+                                                output_dtype=self.activation_dtype)
+                self.backend.linear_batch_fused([b.act[0]], [prepared["down_proj"]], residuals=[b.residual[0]],
+                                                out_slots=[b.down_slots])
                 continue
             self._linears([b.attn], [prepared["o_proj"]], [b.o], t)
             ops.launch_add_rmsnorm(b.residual, post_norm, c.eps, delta=b.o, out=b.xn)

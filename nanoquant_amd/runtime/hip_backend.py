@@ -340,6 +340,7 @@ class HipPackedBackend:
         out_slots: list[torch.Tensor] | None = None,
         outs: list[torch.Tensor] | None = None,
         output_dtype: torch.dtype = torch.float32,
+        output_kind: str = "plain",
     ) -> list[torch.Tensor] | None:
         """One decode token through 1-8 prepared layers with the decoder's
         neighbouring element-wise work fused in (nq_linear_batch_fused):
@@ -351,7 +352,11 @@ class HipPackedBackend:
           fp32 up; member i sees silu(gate) * up;
         * ``residuals`` / ``out_slots``: member i adds its output to
           ``residuals[i]`` (fp32) and writes the tile sums of the new residual's
-          squares to ``out_slots[i]`` instead of producing an output tensor.
+          squares to ``out_slots[i]`` instead of producing an output tensor;
+        * ``output_kind="silu_product"``: two members of equal geometry (gate
+          and up) produce ONE output, ``silu(y_0) * y_1`` in ``output_dtype``
+          (returned as a one-element list), which a following projection reads
+          as a plain input.
 
         No reference counterpart: the reference runs these element-wise steps as
         separate torch operations (src/nanoquant/runtime/torch_model.py:493-505,
@@ -361,9 +366,14 @@ class HipPackedBackend:
                  "silu_gate": _native.INPUT_SILU_GATE}
         if input_kind not in kinds:
             raise ValueError(f"unknown fused input kind {input_kind!r}")
+        out_kinds = {"plain": _native.OUTPUT_PLAIN, "silu_product": _native.OUTPUT_SILU_PRODUCT}
+        if output_kind not in out_kinds:
+            raise ValueError(f"unknown fused output kind {output_kind!r}")
         n = len(layers)
         if len(values) != n or not 1 <= n <= 8:
             raise ValueError("HIP fused batch needs 1-8 layers with one input each")
+        if output_kind == "silu_product" and n != 2:
+            raise ValueError("silu_product takes two members of the same output width")
         if len({id(layer) for layer in layers}) != n:
             raise ValueError("HIP fused batch members must be distinct prepared layers")
         payloads = [self._payload(layer) for layer in layers]
@@ -390,6 +400,7 @@ class HipPackedBackend:
 
         fusion = _native.DecodeFusion()
         fusion.input_kind = kinds[input_kind]
+        fusion.output_kind = out_kinds[output_kind]
         fusion.eps = float(eps)
         keep: list = []
         if input_kind == "rmsnorm":
@@ -426,6 +437,17 @@ class HipPackedBackend:
             fusion.residuals = ctypes.cast(ra, ctypes.POINTER(ctypes.c_void_p))
             fusion.out_slots = ctypes.cast(sa, ctypes.POINTER(ctypes.c_void_p))
             outs = None
+        elif output_kind == "silu_product":
+            if n != 2 or layers[0].spec.out_features != layers[1].spec.out_features:
+                raise ValueError("silu_product takes two members of the same output width")
+            if output_dtype not in (torch.float32, torch.bfloat16, torch.float16):
+                raise ValueError(f"HIP packed output dtype is unsupported: {output_dtype}")
+            width = layers[0].spec.out_features
+            if outs is None:
+                outs = [torch.empty(width, dtype=output_dtype, device=device)]
+            if (len(outs) != 1 or outs[0].numel() != width or outs[0].dtype != output_dtype
+                    or not outs[0].is_contiguous() or outs[0].device != device):
+                raise ValueError("silu_product writes one contiguous output of the members' width")
         else:
             if output_dtype not in (torch.float32, torch.bfloat16, torch.float16):
                 raise ValueError(f"HIP packed output dtype is unsupported: {output_dtype}")
@@ -443,7 +465,10 @@ class HipPackedBackend:
         workspaces = [torch.empty(max(b, 1), dtype=torch.uint8, device=device) for b in sizes]
         desc_ptrs = (ctypes.POINTER(_native.LinearDesc) * n)(*[ctypes.pointer(p.desc) for p in payloads])
         x_ptrs = (ctypes.c_void_p * n)(*[v.data_ptr() for v in values])
-        y_ptrs = (ctypes.c_void_p * n)(*[(o.data_ptr() if outs is not None else 0) for o in (outs or values)])
+        if output_kind == "silu_product":
+            y_ptrs = (ctypes.c_void_p * n)(outs[0].data_ptr(), 0)
+        else:
+            y_ptrs = (ctypes.c_void_p * n)(*[(o.data_ptr() if outs is not None else 0) for o in (outs or values)])
         w_ptrs = (ctypes.c_void_p * n)(*[w.data_ptr() for w in workspaces])
         w_sizes = (ctypes.c_int64 * n)(*sizes)
         status = lib.nq_linear_batch_fused(

@@ -88,6 +88,45 @@ def test_silu_gate_input_matches_oracle():
     print(f"  rel_l2={err:.2e}", flush=True)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("input_kind", ["rmsnorm", "plain"])
+def test_silu_product_output_matches_oracle(input_kind, out_dtype):
+    """gate/up in one workgroup per output tile, the epilogue storing
+    silu(gate) * up: against the oracle's fp32 gate and up, and equal to the
+    two outputs of the same fused call computed separately."""
+
+    backend = HipPackedBackend()
+    shapes = [syn.qwen3_8b_layer()[r] for r in (4, 5)]
+    _say("silu product", input_kind, out_dtype)
+    states, layers = _layers(backend, shapes, syn.BASE_SEED + 330)
+    g = torch.Generator().manual_seed(9)
+    h = 3 * torch.randn(4096, generator=g)
+    w = 1 + 0.1 * torch.randn(4096, generator=g)
+    if input_kind == "rmsnorm":
+        kwargs = dict(input_kind="rmsnorm", eps=EPS, col_scales=[backend.norm_column_scale(lay, w.cuda())
+                                                                 for lay in layers],
+                      norm_slots=_tile_sums(h).float().cuda())
+        value, xn = h.cuda(), _rmsnorm(h, w)
+    else:
+        kwargs = {}
+        value = syn.synthetic_activations(1, 4096, seed=9, device="cuda")[0]
+        xn = value.float().cpu()
+    (prod,) = backend.linear_batch_fused([value] * 2, layers, output_kind="silu_product", output_dtype=out_dtype,
+                                         **kwargs)
+    gate, up = backend.linear_batch_fused([value] * 2, layers, **kwargs)
+    assert prod.dtype == out_dtype and prod.shape == (12288,)
+    separate = torch.nn.functional.silu(gate.double()) * up.double()
+    ref = [orc.packed_forward(orc.operands_from_state(st), xn[None])[0].double() for st in states]
+    expected = (torch.nn.functional.silu(ref[0]) * ref[1]).float()
+    tol = REL_L2 if out_dtype == torch.float32 else 5e-3  # bf16 rounding of the product: 2^-9
+    err = orc.relative_l2(prod.float(), expected)
+    assert err <= tol, err
+    assert orc.relative_l2(prod.float(), separate.float()) <= (1e-5 if out_dtype == torch.float32 else 5e-3)
+    print(f"  rel_l2={err:.2e}", flush=True)
+    with pytest.raises(ValueError, match="two members"):
+        backend.linear_batch_fused([value], layers[:1], output_kind="silu_product", **kwargs)
+
+
 @pytest.mark.parametrize("role", [3, 6])
 def test_residual_epilogue_adds_and_writes_tile_sums(role):
     backend = HipPackedBackend()
