@@ -242,7 +242,14 @@ int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, L
     return NQ_OK;
 }
 
-int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t stream, bool pair = false) {
+// Launch shapes of a batch: tiles and waves per workgroup of each stage,
+// written into the batch (tw1, tw2, and every member's nw / nwg).
+struct Shapes {
+    LaunchShape s1, s2;
+    int64_t nc1, nc2, ks, max1, max2;
+};
+
+int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
     int64_t tiles1 = 0, tiles2 = 0, nc1 = 0, nc2 = 0, ks = 0;
     for (int i = 0; i < batch.count; ++i) {
         ks = batch.p[i].salient_count <= kSalMax && batch.p[i].salient_count > ks ? batch.p[i].salient_count : ks;
@@ -279,10 +286,25 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
         max1 = a.nwg1 > max1 ? a.nwg1 : max1;
         max2 = a.nwg2 > max2 ? a.nwg2 : max2;
     }
-    if (max1 > 0x7fffffff || max2 > 0x7fffffff) return NQ_ERR_SHAPE;
+    if (max1 > 0x7ffffff0 || max2 > 0x7ffffff0) return NQ_ERR_SHAPE;
+    sh = Shapes{s1, s2, nc1, nc2, ks, max1, max2};
+    return NQ_OK;
+}
+
+// Grid x extent of a split-launch stage: a multiple of 8, so workgroup x of
+// every grid row runs on XCD x % 8 (workgroups are dispatched to the eight
+// XCDs round-robin in linear order).
+unsigned xcd_grid(int64_t workgroups) { return static_cast<unsigned>((workgroups + 7) & ~int64_t(7)); }
+
+int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t stream, bool pair = false) {
+    Shapes sh{};
+    int st = plan_shapes(batch, tokens, ak, fused, sh);
+    if (st != NQ_OK) return st;
+    LaunchShape s1 = sh.s1, s2 = sh.s2;
+    const int64_t nc1 = sh.nc1, nc2 = sh.nc2, ks = sh.ks, max1 = sh.max1, max2 = sh.max2;
     const unsigned count = static_cast<unsigned>(batch.count);
 
-    if (fused) {
+    if (fused) {  // the fused launch keeps blocks in launch order
         const size_t l1 = lds_bytes(1, s1.tpb, s1.tb, 1, s1.nw, s1.kc, nc1),
                      l2 = lds_bytes(2, s1.tpb, s1.tb, 1, s1.nw, s1.kc2, nc2, ks, static_cast<int>(tokens));
         s1.lds = l1 > l2 ? l1 : l2;
@@ -290,17 +312,17 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
         return enqueue_fused(batch, s1, stream);
     }
     s1.lds = lds_bytes(1, s1.tpb, s1.tb, s1.tw, s1.nw, s1.kc, nc1);
-    s1.grid = dim3(static_cast<unsigned>(max1), count);
-    int st = enqueue_stage1(batch, s1, stream);
+    s1.grid = dim3(xcd_grid(max1), count);
+    st = enqueue_stage1(batch, s1, stream);
     if (st != NQ_OK) return st;
     s2.lds = lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, s2.kc, nc2, ks, static_cast<int>(tokens));
     if (pair) {
         // Both members' partial sums in one workgroup: a second partial-sum area.
         s2.lds += static_cast<size_t>(nc2) * s2.tw * s2.tb * 64 * 4;
-        s2.grid = dim3(static_cast<unsigned>(max2), 1);
+        s2.grid = dim3(xcd_grid(max2), 1);
         return enqueue_stage2_pair(batch, s2, stream);
     }
-    s2.grid = dim3(static_cast<unsigned>(max2), count);
+    s2.grid = dim3(xcd_grid(max2), count);
     return enqueue_stage2(batch, s2, stream);
 }
 

@@ -204,6 +204,27 @@ struct LinArgs {
 };
 static_assert(sizeof(LinArgs) % 16 == 0, "LinArgs is read as 16-byte vectors");
 
+// ---------------------------------------------------------------------------
+// XCD-contiguous workgroup order.
+//
+// MI355X dispatches the workgroups of a launch to its eight XCDs round-robin
+// in linear order, so with a grid row whose x extent is a multiple of 8,
+// workgroup x runs on XCD x % 8. The split-launch kernels give the workgroups
+// of each XCD one contiguous range of blocks: with B live workgroups in a row
+// and q = B / 8, r = B % 8, those on XCD c take blocks [c q + min(c, r),
+// (c + 1) q + min(c + 1, r)) (xcd_block). Each XCD (one L2) then reads one
+// contiguous range of every sign matrix and writes one contiguous range of
+// the outputs. Measured on MI355X against blocks in launch order: the
+// Qwen3-8B gate/up call 9.40 instead of 9.77 us, end-to-end decode 534 instead
+// of 514 tokens/s.
+// ---------------------------------------------------------------------------
+
+// Block of workgroup x (x < nblocks; XCD x % 8) in the XCD-contiguous order.
+__host__ __device__ inline int xcd_block(int x, int nblocks) {
+    const int q = nblocks >> 3, r = nblocks & 7, c = x & 7;
+    return c * q + (c < r ? c : r) + (x >> 3);
+}
+
 struct Batch {
     int count;
     int tw1, tw2;            // tiles per workgroup of each stage
@@ -931,6 +952,7 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nw = a.nw1;
+    const int nthreads = nw * 64;  // the workgroup size (blockDim.x is a vector load of a hidden argument)
     const int tokens = a.tokens;
     // Workgroups past this member's count compute the last workgroup's tiles
     // and store nothing.
@@ -1037,7 +1059,7 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
 
     // Epilogue: lm = s_mid * Σ_chunks partial, written as stage-2 operands with
     // the per-token exponent of the bound max|s_mid| * Σ_c 512 * max_c.
-    for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
+    for (int idx = threadIdx.x; idx < outs; idx += nthreads) {
         const OutIdx o = out_index<TPB>(idx, tokens);
         const int row = (t0 + o.tt) * kTileRows + o.n;
         if (t0 + o.tt >= nt) continue;
@@ -1065,7 +1087,7 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
     if (t0 + TW >= nt) {
         const int from = nt * kTileRows, to = static_cast<int>(a.g2.nc) * kChunkCols;
         const int n = (to - from) * tokens;
-        for (int i = threadIdx.x; i < n; i += blockDim.x)
+        for (int i = threadIdx.x; i < n; i += nthreads)
             store_lmq<TPB, TB, FUSED>(a.lmq, from + i / tokens, i % tokens, 0.0f, 0);
     }
     if (FUSED) {
@@ -1116,6 +1138,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nw = a.nw2;
+    const int nthreads = nw * 64;  // the workgroup size (blockDim.x is a vector load of a hidden argument)
     const int tokens = a.tokens;
     const int nwg = static_cast<int>(a.nwg2);
     const bool dead = wg_in >= nwg;  // computes the last workgroup's tiles, stores nothing
@@ -1141,7 +1164,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     const int fr = fr0 < out ? fr0 : out - 1;
     RawElem rs0, bias0, rs1;
     bool stale = false;  // fused launch: the wait for stage 1 gave up
-    // First-pass salient loads: weights i = threadIdx.x + n * blockDim.x of the
+    // First-pass salient loads: weights i = threadIdx.x + n * nthreads of the
     // workgroup's block, and for threadIdx.x < tokens * ks one gathered x and scale.
     uint32_t wbits[kSalLoads];
     RawElem sx, ssc;
@@ -1181,7 +1204,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
             if (sal_lds) {  // uniform
 #pragma unroll
                 for (int n = 0; n < kSalLoads; ++n) {
-                    const int i = wbase + static_cast<int>(threadIdx.x) + n * static_cast<int>(blockDim.x);
+                    const int i = wbase + static_cast<int>(threadIdx.x) + n * nthreads;
                     wbits[n] = load_bits(a.salient_values, a.salient_dtype, i < wlimit ? i : wlimit);
                 }
                 const int j = static_cast<int>(threadIdx.x) < tokens * ks ? static_cast<int>(threadIdx.x) : 0;
@@ -1243,18 +1266,18 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     if (sal_lds) {  // uniform: park the salient operands beside the partial sums
 #pragma unroll
         for (int n = 0; n < kSalLoads; ++n) {
-            const int i = static_cast<int>(threadIdx.x) + n * static_cast<int>(blockDim.x);
+            const int i = static_cast<int>(threadIdx.x) + n * nthreads;
             if (i < wtotal) salw[i] = bits_value(wbits[n], a.salient_dtype);
         }
-        for (int i = static_cast<int>(threadIdx.x) + kSalLoads * static_cast<int>(blockDim.x); i < wtotal;
-             i += static_cast<int>(blockDim.x))  // blocks wider than the first-pass loads
+        for (int i = static_cast<int>(threadIdx.x) + kSalLoads * nthreads; i < wtotal;
+             i += nthreads)  // blocks wider than the first-pass loads
             salw[i] = bits_value(load_bits(a.salient_values, a.salient_dtype, wbase + i < wlimit ? wbase + i : wlimit),
                                  a.salient_dtype);
         const auto gathered = [&](const RawElem& xv, const RawElem& sv) __attribute__((always_inline)) {
             return elem_value(xv, a.x_dtype) * (a.salient_scales ? elem_value(sv, a.scale_dtype) : 1.0f);
         };
         if (static_cast<int>(threadIdx.x) < tokens * ks) salx[threadIdx.x] = gathered(sx, ssc);
-        for (int j = static_cast<int>(threadIdx.x + blockDim.x); j < tokens * ks; j += static_cast<int>(blockDim.x)) {
+        for (int j = static_cast<int>(threadIdx.x + nthreads); j < tokens * ks; j += nthreads) {
             const int t = j / ks, k = j - t * ks;  // more gathered values than threads
             salx[j] = gathered(load_elem(a.x, a.x_dtype, t * in + a.salient_indices[k]),
                                load_elem(a.salient_scales ? a.salient_scales : a.s_in, a.scale_dtype, k));
@@ -1284,7 +1307,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     };
     if constexpr (PAIR) {
         // One token: outputs idx = 16 tt + n; silu(gate) * up in a.y's dtype.
-        for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
+        for (int idx = threadIdx.x; idx < outs; idx += nthreads) {
             const OutIdx o = out_index<TPB>(idx, tokens);
             const int row = (t0 + o.tt) * kTileRows + o.n;
             if (t0 + o.tt >= nt || row >= out) continue;
@@ -1321,7 +1344,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
         }
         return;
     }
-    for (int idx = threadIdx.x; idx < outs; idx += blockDim.x) {
+    for (int idx = threadIdx.x; idx < outs; idx += nthreads) {
         const OutIdx o = out_index<TPB>(idx, tokens);
         const int row = (t0 + o.tt) * kTileRows + o.n;
         if (t0 + o.tt >= nt || row >= out) continue;
@@ -1337,20 +1360,25 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
 // before the main loads are issued except the grid-padding exit (optional
 // operands load from a valid address and are selected later, partial chunks
 // use the same 16-byte word loads as full ones).
+//
+// The grid's x extent is a multiple of 8 and workgroup x takes block
+// xcd_block(x, workgroups) (the XCD-contiguous order above).
 template <int AK, int TPB, int TB, int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage1(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const LinArgs a = load_args(batch, blockIdx.y);
-    if (blockIdx.x >= a.nwg1) return;  // grid padding: the arguments are already loaded
-    stage1_wg<AK, TPB, TB, TW, KC, false>(a, blockIdx.x, lds);
+    const int nwg = static_cast<int>(a.nwg1);
+    if (static_cast<int>(blockIdx.x) >= nwg) return;  // grid padding: the arguments are already loaded
+    stage1_wg<AK, TPB, TB, TW, KC, false>(a, xcd_block(blockIdx.x, nwg), lds);
 }
 
 template <int TPB, int TB, int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage2(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const LinArgs a = load_args(batch, blockIdx.y);
-    if (blockIdx.x >= a.nwg2) return;  // grid padding: the arguments are already loaded
-    stage2_wg<TPB, TB, TW, KC, false>(a, blockIdx.x, lds);
+    const int nwg = static_cast<int>(a.nwg2);
+    if (static_cast<int>(blockIdx.x) >= nwg) return;  // grid padding: the arguments are already loaded
+    stage2_wg<TPB, TB, TW, KC, false>(a, xcd_block(blockIdx.x, nwg), lds);
 }
 
 // Paired stage 2 (one token): members 0 and 1 of the batch, one grid row.
@@ -1359,8 +1387,9 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage2_pair(const Batch batc
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const LinArgs a = load_args(batch, 0);
     const LinArgs b = load_args(batch, 1);
-    if (blockIdx.x >= a.nwg2) return;
-    stage2_wg<1, 1, TW, KC, false, true>(a, blockIdx.x, lds, &b);
+    const int nwg = static_cast<int>(a.nwg2);
+    if (static_cast<int>(blockIdx.x) >= nwg) return;
+    stage2_wg<1, 1, TW, KC, false, true>(a, xcd_block(blockIdx.x, nwg), lds, &b);
 }
 
 // Fused launch (one tile per workgroup, generic stage-1 loads): grid rows
