@@ -59,7 +59,7 @@ def parse_args(argv=None):
     p.add_argument("--steps", type=int, default=10, help="timed repetitions of every figure (>= 10 for percentiles)")
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--layers", type=int, default=36)
-    p.add_argument("--modes", default="grouped,grouped-fused,single,layer",
+    p.add_argument("--modes", default="grouped,grouped-fused,single,layer,layer-streams",
                    help="launch groupings of the 36-layer decode stack")
     p.add_argument("--prefill-tokens", default="64,256,512,2048", help="config-3 token counts ('' to skip)")
     p.add_argument("--e2e-tokens", type=int, default=128, help="greedy tokens of the config-5 run (0 to skip)")
@@ -348,10 +348,39 @@ def run_calls(backend, calls):
             backend.linear_batch([m[2] for m in members], [m[1] for m in members], outs=[m[3] for m in members])
 
 
+STREAMS = 4  # "-streams" modes: independent calls spread round-robin over this many streams
+
+
+def run_calls_streams(backend, calls, streams):
+    """The calls spread round-robin over `streams`, forked from and joined to
+    the current stream (the calls are independent: distinct inputs and
+    outputs), so one stream's launch gaps can overlap another's kernels."""
+
+    import torch
+
+    main = torch.cuda.current_stream()
+    for s in streams:
+        s.wait_stream(main)
+    for i, members in enumerate(calls):
+        with torch.cuda.stream(streams[i % len(streams)]):
+            run_calls(backend, [members])
+    for s in streams:
+        main.wait_stream(s)
+
+
 def time_stack(backend, entries, mode: str, reps: int, warmup: int) -> dict:
+    import torch
+
+    streams = None
+    if mode.endswith("-streams"):
+        streams = [torch.cuda.Stream() for _ in range(STREAMS)]
+        mode = mode.removesuffix("-streams")
     calls = step_calls(entries, mode, backend)
     tokens = calls[0][0][2].shape[0]
-    step = pct(graph_reps(lambda: run_calls(backend, calls), reps, warmup))
+    if streams is None:
+        step = pct(graph_reps(lambda: run_calls(backend, calls), reps, warmup))
+    else:
+        step = pct(graph_reps(lambda: run_calls_streams(backend, calls, streams), reps, warmup))
     step_bytes = sum(algorithmic_bytes(m[0], tokens) for members in calls for m in members)
     kernels = len(calls) * (1 if mode.endswith("-fused") else 2)
     ms = step["p50"]

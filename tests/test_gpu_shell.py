@@ -225,6 +225,39 @@ def test_decode_attention_workspace_reuse():
         assert relative_l2(out.view(1, -1), out2) < 1e-5
 
 
+@pytest.mark.parametrize("kv_heads", [2, 12])
+def test_decode_attention_mfma_other_head_counts(kv_heads):
+    """The MFMA decode attention (head_dim 128, four q heads per kv head, bf16
+    cache) with kv head counts that are not eight: within 1e-5 of the separate
+    rotate/append and attention calls, the same cache rows, and identical on a
+    repeat."""
+    q_heads, head_dim, max_pos = 4 * kv_heads, 128, 300
+    g = _g(12 + kv_heads)
+    cos, sin = ods.rope_tables(head_dim, 1e6, max_pos)
+    for p in (0, 64, 299):
+        _say("decode attention mfma head counts", kv_heads, p)
+        kc = torch.randn(kv_heads, max_pos, head_dim, generator=g).to(torch.bfloat16).to(DEV)
+        vc = torch.randn(kv_heads, max_pos, head_dim, generator=g).to(torch.bfloat16).to(DEV)
+        q = (3 * torch.randn(q_heads * head_dim, generator=g)).to(DEV)
+        k = (3 * torch.randn(kv_heads * head_dim, generator=g)).to(DEV)
+        v = torch.randn(kv_heads * head_dim, generator=g).to(DEV)
+        position = torch.tensor([p], dtype=torch.int32, device=DEV)
+        common = dict(q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, q_norm=None, k_norm=None, eps=1e-6,
+                      cos=cos.to(DEV), sin=sin.to(DEV), position=position)
+        kc2, vc2 = kc.clone(), vc.clone()
+        kc3, vc3 = kc.clone(), vc.clone()
+        out = ops.launch_decode_attention(q, k, v, k_cache=kc, v_cache=vc, scaling=head_dim**-0.5,
+                                          out_dtype=torch.float32, **common)
+        again = ops.launch_decode_attention(q, k, v, k_cache=kc3, v_cache=vc3, scaling=head_dim**-0.5,
+                                            out_dtype=torch.float32, **common)
+        q_rot = ops.launch_qk_norm_rope_cache(q, k, v, k_cache=kc2, v_cache=vc2, **common)
+        out2 = ops.launch_attention(q_rot.view(1, q_heads, head_dim), kc2, vc2, position=position,
+                                    scaling=head_dim**-0.5, out_dtype=torch.float32)
+        assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+        assert torch.equal(out, again)
+        assert relative_l2(out.view(1, -1), out2) < 1e-5
+
+
 def test_attention_single_row_returns_value():
     kc = torch.randn(2, 64, 128).to(torch.bfloat16)
     vc = torch.randn(2, 64, 128).to(torch.bfloat16)
