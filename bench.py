@@ -522,8 +522,11 @@ def config4(args, device) -> dict:
 
 def config3(args, device) -> dict:
     """The seven Llama-3-8B linears (~0.8 bpw) at each token count, one layer
-    pass captured in a HIP graph; TFLOP/s counts the two sign GEMMs
-    (2*M*(in*r + r*out)) against the fp16 dense MFMA peak."""
+    pass captured in a HIP graph: q/k/v and gate/up as one batched call each
+    (one launch per kernel phase for the group), o and down alone; the same
+    pass with every linear called on its own is reported beside it. TFLOP/s
+    counts the two sign GEMMs (2*M*(in*r + r*out)) against the fp16 dense
+    MFMA peak."""
 
     import torch
 
@@ -541,17 +544,26 @@ def config3(args, device) -> dict:
               for s in shapes}
         outs = [torch.empty(tokens, s.out_features, dtype=torch.float32, device=device) for s in shapes]
 
+        groups = ([0, 1, 2], [3], [4, 5], [6])  # q/k/v, o, gate/up, down
+
         def layer_pass():
+            for g in groups:
+                backend.linear_batch([xs[shapes[i].in_features] for i in g], [layers[i] for i in g],
+                                     outs=[outs[i] for i in g])
+
+        def layer_pass_single():
             for s, layer, out in zip(shapes, layers, outs):
                 backend.linear_into(xs[s.in_features], layer, out=out)
 
         d = pct(graph_reps(layer_pass, args.steps, 2))
+        d_single = pct(graph_reps(layer_pass_single, args.steps, 2))
         flops = sum(2 * tokens * (s.in_features * s.rank + s.rank * s.out_features) for s in shapes)
         sweep[str(tokens)] = {
             "ms_per_layer": _scaled(d, lambda v: v, 4),
             "tok_per_s": round(tokens * 1000.0 / d["p50"], 1),
             "tflops": _scaled(d, lambda ms: flops / (ms * 1e-3) / 1e12, 2),
             "frac_of_fp16_peak": round(flops / (d["p50"] * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS, 4),
+            "ms_per_layer_unbatched": round(d_single["p50"], 4),
             "reps": d["n"],
         }
         del xs, outs

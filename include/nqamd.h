@@ -229,9 +229,12 @@ int nq_linear_static(const nq_linear_desc* desc, const void* x, int32_t x_dtype,
  * ceiling the decode path is compared with. */
 int nq_read_stream(const void* src, int64_t bytes, uint32_t* sink, int64_t sink_count, void* stream);
 
-/* One launch for `count` (1..8) packed linears with the same token count
- * (1..16) and dtypes: y_i = linear_i(x_i). Inputs may alias (Q/K/V or gate/up
- * share x); every descriptor must carry tiles and no two may share them.
+/* One launch per kernel phase for `count` (1..8) packed linears with the same
+ * token count and dtypes: y_i = linear_i(x_i). Up to 16 tokens the members
+ * share the decode kernels' launches (no two descriptors may then share
+ * tiles); above 16, the prefill row pass, both sign GEMMs and their split-K
+ * reductions each take one launch for all members. Inputs may alias (Q/K/V
+ * or gate/up share x); every descriptor must carry tiles.
  * workspaces[i] holds nq_linear_workspace_bytes(descs[i], tokens) bytes.
  * Replaces launch_grouped_packed_linears / grouped_cuda_projection
  * (src/nanoquant/runtime/cuda_kernels.py:301-374,

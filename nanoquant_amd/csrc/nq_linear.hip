@@ -538,8 +538,9 @@ extern "C" int nq_linear_batch(const nq_linear_desc* const* descs, int32_t count
                                void* const* workspaces, const int64_t* workspace_bytes, void* stream) {
     if (!descs || !xs || !ys || !workspaces || !workspace_bytes) return NQ_ERR_ARGUMENT;
     if (count < 1 || count > 8) return NQ_ERR_SHAPE;
-    if (tokens < 1 || tokens > 16) return NQ_ERR_SHAPE;
+    if (tokens < 1) return NQ_ERR_SHAPE;
     if (!nq::is_float_dtype(x_dtype) || !nq::is_float_dtype(y_dtype)) return NQ_ERR_DTYPE;
+    const bool decode = tokens <= 16;
     void* scratch[8];
     for (int i = 0; i < count; ++i) {
         const nq_linear_desc* d = descs[i];
@@ -547,15 +548,20 @@ extern "C" int nq_linear_batch(const nq_linear_desc* const* descs, int32_t count
         if (st != NQ_OK) return st;
         if (!d->tiles || !xs[i] || !ys[i]) return NQ_ERR_ARGUMENT;
         if (y_dtype != NQ_DTYPE_F32 && (d->patch_rank > 0 || d->row_count > 0)) return NQ_ERR_UNSUPPORTED;
-        for (int j = 0; j < i; ++j) {
-            if (descs[j]->tiles == d->tiles) return NQ_ERR_ARGUMENT;  // one sync header per launch
+        if (decode) {
+            for (int j = 0; j < i; ++j) {
+                if (descs[j]->tiles == d->tiles) return NQ_ERR_ARGUMENT;  // one sync header per launch
+            }
+        } else if (!nq::prefill_path_applies(d, tokens)) {
+            return NQ_ERR_SHAPE;
         }
         const WorkspaceLayout wl = workspace_layout(d, tokens);
         if (!workspaces[i] || workspace_bytes[i] < wl.total) return NQ_ERR_WORKSPACE;
         scratch[i] = static_cast<char*>(workspaces[i]) + wl.decode_offset;
     }
     auto s = static_cast<hipStream_t>(stream);
-    int st = nq::launch_decode_batch(descs, count, xs, x_dtype, tokens, ys, y_dtype, scratch, s);
+    int st = decode ? nq::launch_decode_batch(descs, count, xs, x_dtype, tokens, ys, y_dtype, scratch, s)
+                    : nq::launch_prefill_batch(descs, count, xs, x_dtype, tokens, ys, y_dtype, scratch, s);
     if (st != NQ_OK) return st;
     for (int i = 0; i < count; ++i) {
         const WorkspaceLayout wl = workspace_layout(descs[i], tokens);

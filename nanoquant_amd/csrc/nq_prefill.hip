@@ -52,6 +52,7 @@ constexpr int kBN = 128;
 constexpr int kBK = 128;                 // one superchunk per K step
 constexpr int kAStride = kBK + 8;        // halfs; rows land in different banks
 constexpr int kTileRows = 16;
+constexpr int kPrefillBatch = 8;         // members of one batched call
 constexpr int kParkStride = 65;          // floats per parked accumulator row
 constexpr int kALdsBytes = kBM * kAStride * 2;
 constexpr int kParkBytes = 4 * 64 * kParkStride * 4;
@@ -116,18 +117,42 @@ __device__ __forceinline__ void load8(const void* __restrict__ p, int dtype, boo
     }
 }
 
+// Row pass of one member of a batched call (grid y = member, x = token).
+struct PrepArgs {
+    const void* act;                 // [tokens, ld] activations
+    int64_t ld;
+    const void* colscale;            // [cols] s_in, or null
+    int colscale_dtype;
+    int vec;                         // 16-byte loads allowed (generic kernel)
+    int64_t cols, cols_pad;
+    _Float16* out16;                 // [tokens, cols_pad]
+    float* scale_out;                // [tokens]
+    const uint32_t* max_mid_bits;    // fp32 bits of max|s_mid|, or null
+    float* bound_scale_out;          // [tokens]
+};
+
+struct PrepBatch {
+    PrepArgs p[kPrefillBatch];
+};
+
 // One workgroup per row: out16[t, swizzle4(c)] = fp16(a[t, c] * s[c] * scale_t)
 // for c < cols, zero for cols <= c < cols_pad; scale_out[t] = scale_t. Each
 // thread takes 8 consecutive columns per step (one 16-byte store of fp16).
 // With `max_mid_bits` (fp32 bits of max|s_mid|) it also writes
 // bound_scale_out[t], the power of two that puts max|s_mid| * Σ_c |a s| at
 // or below 2^14: the scale of the row's rank intermediate.
-__global__ __launch_bounds__(kBlock) void k_prep_rows(const void* __restrict__ act, int act_dtype, int64_t ld,
-                                                      const void* __restrict__ colscale, int colscale_dtype,
-                                                      int64_t cols, int64_t cols_pad, int vec,
-                                                      _Float16* __restrict__ out16, float* __restrict__ scale_out,
-                                                      const uint32_t* __restrict__ max_mid_bits,
-                                                      float* __restrict__ bound_scale_out) {
+__global__ __launch_bounds__(kBlock) void k_prep_rows(const PrepBatch batch, int act_dtype) {
+    const PrepArgs& pa = batch.p[blockIdx.y];
+    const void* __restrict__ act = pa.act;
+    const int64_t ld = pa.ld;
+    const void* __restrict__ colscale = pa.colscale;
+    const int colscale_dtype = pa.colscale_dtype;
+    const int64_t cols = pa.cols, cols_pad = pa.cols_pad;
+    const int vec = pa.vec;
+    _Float16* __restrict__ out16 = pa.out16;
+    float* __restrict__ scale_out = pa.scale_out;
+    const uint32_t* __restrict__ max_mid_bits = pa.max_mid_bits;
+    float* __restrict__ bound_scale_out = pa.bound_scale_out;
     __shared__ float wmax[kBlock / 64];
     __shared__ float wsum[kBlock / 64];
     const int64_t t = blockIdx.x;
@@ -213,12 +238,16 @@ __device__ __forceinline__ void load8_as(const void* __restrict__ p, int64_t i, 
 constexpr int kPrepChunksMax = 8;
 
 template <int ADT, int SDT, int NCH>
-__global__ __launch_bounds__(kBlock) void k_prep_rows_vec(const void* __restrict__ act, int64_t ld,
-                                                          const void* __restrict__ colscale, int64_t cols,
-                                                          int64_t cols_pad, _Float16* __restrict__ out16,
-                                                          float* __restrict__ scale_out,
-                                                          const uint32_t* __restrict__ max_mid_bits,
-                                                          float* __restrict__ bound_scale_out) {
+__global__ __launch_bounds__(kBlock) void k_prep_rows_vec(const PrepBatch batch) {
+    const PrepArgs& pa = batch.p[blockIdx.y];
+    const void* __restrict__ act = pa.act;
+    const int64_t ld = pa.ld;
+    const void* __restrict__ colscale = pa.colscale;
+    const int64_t cols = pa.cols, cols_pad = pa.cols_pad;
+    _Float16* __restrict__ out16 = pa.out16;
+    float* __restrict__ scale_out = pa.scale_out;
+    const uint32_t* __restrict__ max_mid_bits = pa.max_mid_bits;
+    float* __restrict__ bound_scale_out = pa.bound_scale_out;
     __shared__ float wmax[kBlock / 64];
     __shared__ float wsum[kBlock / 64];
     const int64_t t = blockIdx.x;
@@ -323,18 +352,45 @@ struct GemmArgs {
     const float* out_scale;   // [M] or null: write fp16(v * out_scale[t]) at column
                               // swizzle4(c) of an out_ld-wide row, zero for n <= c < out_ld
     int64_t out_ld;
-    int64_t k_per_split;      // K blocks per grid-z slice
-    float* partial;           // [gridDim.z][M][n] raw accumulators, or null (direct epilogue)
+    int64_t k_per_split;      // K blocks per K slice
+    int64_t splits;           // K slices (1: no split)
+    int64_t col_blocks;       // column blocks at the launch's block width
+    float* partial;           // [splits][M][n] raw accumulators, or null (direct epilogue)
 };
+
+// Up to kPrefillBatch GEMMs of one phase (the members of a batched call share
+// the token count) in one launch. Grid x concatenates the members' ranges:
+// member i owns [begin[i], begin[i + 1]) (k_sign_gemm: col_blocks * splits
+// workgroups, slice-major; k_reduce_splits: its column blocks, none for a
+// member without a split); begin[i] = INT32_MAX past the last member.
+struct GemmBatch {
+    int32_t begin[kPrefillBatch];
+    GemmArgs p[kPrefillBatch];
+};
+
+// The member whose range holds grid-x index x: the last one beginning at or
+// before it (a member with an empty range shares its begin with the next).
+__device__ __forceinline__ int batch_member(const GemmBatch& b, int x) {
+    int m = 0;
+#pragma unroll
+    for (int i = 1; i < kPrefillBatch; ++i) m = x >= b.begin[i] ? i : m;
+    return m;
+}
 
 // WM = 2: the four waves form a 2 x 2 grid of 64 x 64 tiles (block tile
 // 128 x 128). WM = 1: they sit side by side, each 128 x 64 (block tile
 // 128 x 256): every expanded sign fragment then serves four A fragments
 // instead of two, for GEMMs with enough blocks to fill the GPU at that size.
 template <int WM>
-__global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmArgs g) {
+__global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) {
     constexpr int II = 4 / WM;            // 32-row A fragments per wave
     constexpr int BN = 64 * (4 / WM);     // sign rows per block
+    const int member = batch_member(batch, static_cast<int>(blockIdx.x));
+    const GemmArgs& g = batch.p[member];
+    const int local = static_cast<int>(blockIdx.x) - batch.begin[member];
+    const int col_blocks = static_cast<int>(g.col_blocks);
+    const int slice = local / col_blocks;
+    const int col_block = local - slice * col_blocks;
     __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -343,7 +399,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmArgs g) {
     const int h = lane >> 5;   // K half of the 32 x 32 x 16 operands
     const int r = lane & 31;   // A row / B column within a 32-wide fragment
     const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
+    const int64_t n0 = static_cast<int64_t>(col_block) * BN;
     const int64_t rt_count = (g.n + kTileRows - 1) / kTileRows;
     // B fragment jj covers sign rows n0 + 64 wn + 32 jj + [0, 32): lane r reads
     // row r of tile (r >> 4) of that pair, from the words of lane groups 2h
@@ -370,7 +426,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmArgs g) {
     const int64_t rt_b = rt0 + 2 < rt_count ? rt0 + 2 : rt_count - 1;
     const uint32_t* const b0 = g.tiles + rt_a * nsc * 64;
     const uint32_t* const b1 = g.tiles + rt_b * nsc * 64;
-    const int64_t k_begin = static_cast<int64_t>(blockIdx.z) * g.k_per_split;
+    const int64_t k_begin = static_cast<int64_t>(slice) * g.k_per_split;
     const int64_t k_end = k_begin + g.k_per_split < nsc ? k_begin + g.k_per_split : nsc;
 #define NQ_LOAD_STEP(SC)                                                                            \
     do {                                                                                            \
@@ -448,7 +504,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmArgs g) {
         const bool col_ok = col < g.n;
         if (g.partial) {
             if (!col_ok) return;
-            float* dst = g.partial + static_cast<int64_t>(blockIdx.z) * g.m * g.n;
+            float* dst = g.partial + static_cast<int64_t>(slice) * g.m * g.n;
             for (int e = 0; e < rows; ++e) dst[(row0 + e) * g.n + col] = park[e * kParkStride + lane];
             return;
         }
@@ -536,18 +592,27 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmArgs g) {
                 break;
         }
     };
+    // Park fragments ii0 and ii0 + 1 (a 64-row half), then emit it. Written
+    // out per half rather than as a loop: the accumulators must keep constant
+    // register indices, and the compiler does not always unroll a loop around
+    // two copies of emit.
+    const auto park_half = [&](const v16f (&a0)[2], const v16f (&a1)[2]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int hf = 0; hf < II / 2; ++hf) {
-        if (hf > 0) __syncthreads();  // the previous half is read out of the park area
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    park[(32 * ii + 8 * (q >> 2) + 4 * h + (q & 3)) * kParkStride + 32 * jj + r] = acc[2 * hf + ii][jj][q];
+            for (int q = 0; q < 16; ++q) {
+                park[(8 * (q >> 2) + 4 * h + (q & 3)) * kParkStride + 32 * jj + r] = a0[jj][q];
+                park[(32 + 8 * (q >> 2) + 4 * h + (q & 3)) * kParkStride + 32 * jj + r] = a1[jj][q];
+            }
+    };
+    park_half(acc[0], acc[1]);
+    __syncthreads();
+    emit(m0 + 64 * wm);
+    if constexpr (II == 4) {
+        __syncthreads();  // the first half is read out of the park area
+        park_half(acc[2], acc[3]);
         __syncthreads();
-        emit(m0 + 64 * wm + 64 * hf);
+        emit(m0 + 64 * wm + 64);
     }
 }
 
@@ -571,8 +636,8 @@ __device__ __forceinline__ float raw2_value(const Raw2& r, int dtype) {
     return dtype == NQ_DTYPE_F32 ? f32 : (dtype == NQ_DTYPE_BF16 ? bf16 : f16);
 }
 
-// Split-K epilogue, one thread per output element (t, c), grid (column
-// blocks, token rows; t = blockIdx.y + kRowsPerGridZ * blockIdx.z): out[t, c] =
+// Split-K epilogue, one thread per output element (t, c), grid (the members'
+// column blocks, token rows; t = blockIdx.y + kRowsPerGridZ * blockIdx.z): out[t, c] =
 // (Σ_z partial[z][t][c]) / row_scale[t] * col_scale[c] (+ bias + salient
 // columns for GEMM 2), the slices summed in z order. The column's scale and
 // bias and the first eight partials are loaded before any is used. With
@@ -580,7 +645,10 @@ __device__ __forceinline__ float raw2_value(const Raw2& r, int dtype) {
 // intermediate as the direct epilogue does (zeros past column n).
 constexpr int64_t kRowsPerGridZ = 65535;
 
-__global__ __launch_bounds__(kBlock) void k_reduce_splits(int splits, const GemmArgs ga) {
+__global__ __launch_bounds__(kBlock) void k_reduce_splits(const GemmBatch batch) {
+    const int member = batch_member(batch, static_cast<int>(blockIdx.x));
+    const GemmArgs& ga = batch.p[member];
+    const int splits = static_cast<int>(ga.splits);
     // Every argument the kernel reads is loaded in one batch: the empty asm
     // needs them all at one point, instead of one round trip per branch.
     GemmArgs g;
@@ -608,10 +676,10 @@ __global__ __launch_bounds__(kBlock) void k_reduce_splits(int splits, const Gemm
     g.x = ga.x;
     g.x_dtype = ga.x_dtype;
     g.in = ga.in;
-    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    const int64_t c = static_cast<int64_t>(static_cast<int>(blockIdx.x) - batch.begin[member]) * kBlock + threadIdx.x;
     const int64_t t = static_cast<int64_t>(blockIdx.z) * kRowsPerGridZ + blockIdx.y;
     const int64_t width = g.out_scale ? g.out_ld : g.n;
-    if (c >= width || t >= g.m) return;
+    if (splits <= 1 || c >= width || t >= g.m) return;  // members without a split have no partials
     if (c >= g.n) {  // only with out_scale: a padding column of the rank intermediate
         static_cast<_Float16*>(g.out)[t * g.out_ld + swizzle4(c)] = static_cast<_Float16>(0.0f);
         return;
@@ -694,34 +762,95 @@ Split split_for(int64_t tiles, int64_t k_blocks, int64_t tokens, int64_t n) {
     return best;
 }
 
-// The 128 x 256 block tile (k_sign_gemm<1>) for a GEMM that is not split
-// and still has at least kResident blocks at that size; 128 x 128 otherwise.
-bool wide_blocks(int64_t tokens, int64_t n, const Split& sp) {
-    const int64_t mt = (tokens + kBM - 1) / kBM;
-    return sp.slices == 1 && mt * ((n + 2 * kBN - 1) / (2 * kBN)) >= kResident;
+// Splits of the members of one batched GEMM launch: each member's slices
+// come from one bound kmax on K blocks per workgroup, chosen by the same
+// latency model over the whole launch (its workgroups share the GPU), and
+// stay within what the member's partial buffer holds (cap[i] elements) and
+// kMinSliceBlocks. A batch of one takes split_for's choice, which the
+// member's workspace is sized for.
+void batch_splits(int count, const int64_t* tiles, const int64_t* k_blocks, const int64_t* n, const int64_t* cap,
+                  const Split* solo, int64_t tokens, Split* out) {
+    if (count == 1) {
+        out[0] = solo[0];
+        return;
+    }
+    int64_t kb_max = 1;
+    for (int i = 0; i < count; ++i) kb_max = k_blocks[i] > kb_max ? k_blocks[i] : kb_max;
+    double best_ns = -1.0;
+    for (int64_t kmax = kb_max; kmax >= 1; --kmax) {
+        Split cand[kPrefillBatch];
+        int64_t wgs = 0, steps = 0, partial_elems = 0;
+        for (int i = 0; i < count; ++i) {
+            const int64_t most_k = k_blocks[i] / kMinSliceBlocks > 1 ? k_blocks[i] / kMinSliceBlocks : 1;
+            const int64_t most_cap = cap[i] / (tokens * n[i]) > 1 ? cap[i] / (tokens * n[i]) : 1;
+            int64_t sl = (k_blocks[i] + kmax - 1) / kmax;
+            sl = sl < most_k ? sl : most_k;
+            sl = sl < most_cap ? sl : most_cap;
+            cand[i].k_per_split = (k_blocks[i] + sl - 1) / sl;
+            cand[i].slices = (k_blocks[i] + cand[i].k_per_split - 1) / cand[i].k_per_split;
+            wgs += tiles[i] * cand[i].slices;
+            steps = cand[i].k_per_split > steps ? cand[i].k_per_split : steps;
+            if (cand[i].slices > 1) partial_elems += cand[i].slices * tokens * n[i];
+        }
+        const int64_t rounds = (wgs + kResident - 1) / kResident;
+        double ns = static_cast<double>(rounds * (steps + 1)) * kStepNs;
+        if (partial_elems > 0) ns += kReduceNs + 2.0 * static_cast<double>(partial_elems * 4) / kPartialBytesPerNs;
+        if (best_ns < 0.0 || ns < best_ns) {
+            best_ns = ns;
+            for (int i = 0; i < count; ++i) out[i] = cand[i];
+        }
+    }
 }
 
-// Launch one sign GEMM and, when K is split, its reduction over
-// `reduce_cols` output columns (n, or out_ld for the fp16 rank intermediate).
-void launch_gemm(const GemmArgs& g, const Split& sp, int64_t tokens, int64_t reduce_cols, hipStream_t stream) {
-    const bool wide = wide_blocks(tokens, g.n, sp);
+// One launch of a phase's GEMMs (p[i].splits, k_per_split and partial set)
+// and, when any member's K is split, one launch of the reductions. The
+// 128 x 256 block tile (k_sign_gemm<1>) is used when no member is split and
+// the launch still has at least kResident blocks at that size; 128 x 128
+// otherwise.
+void launch_phase(GemmArgs* p, int count, int64_t tokens, hipStream_t stream) {
+    const int64_t mt = (tokens + kBM - 1) / kBM;
+    bool wide = true;
+    int64_t wide_blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        wide = wide && p[i].splits == 1;
+        wide_blocks += mt * ((p[i].n + 2 * kBN - 1) / (2 * kBN));
+    }
+    wide = wide && wide_blocks >= kResident;
     const int64_t bn = wide ? 2 * kBN : kBN;
-    const dim3 grid(static_cast<unsigned>((g.n + bn - 1) / bn), static_cast<unsigned>((tokens + kBM - 1) / kBM),
-                    static_cast<unsigned>(sp.slices));
+    GemmBatch gb;
+    GemmBatch rb;
+    int64_t x = 0, rx = 0;
+    for (int i = 0; i < kPrefillBatch; ++i) {
+        if (i >= count) {
+            gb.begin[i] = rb.begin[i] = INT32_MAX;
+            gb.p[i] = rb.p[i] = GemmArgs{};
+            continue;
+        }
+        p[i].col_blocks = (p[i].n + bn - 1) / bn;
+        gb.begin[i] = static_cast<int32_t>(x);
+        rb.begin[i] = static_cast<int32_t>(rx);
+        gb.p[i] = rb.p[i] = p[i];
+        x += p[i].col_blocks * p[i].splits;
+        if (p[i].splits > 1) {
+            const int64_t width = p[i].out_scale ? p[i].out_ld : p[i].n;
+            rx += (width + kBlock - 1) / kBlock;
+        }
+    }
+    const dim3 grid(static_cast<unsigned>(x), static_cast<unsigned>(mt));
     if (wide)
-        hipLaunchKernelGGL(k_sign_gemm<1>, grid, dim3(kBlock), 0, stream, g);
+        hipLaunchKernelGGL(k_sign_gemm<1>, grid, dim3(kBlock), 0, stream, gb);
     else
-        hipLaunchKernelGGL(k_sign_gemm<2>, grid, dim3(kBlock), 0, stream, g);
-    if (sp.slices > 1) {
-        const dim3 rgrid(static_cast<unsigned>((reduce_cols + kBlock - 1) / kBlock),
-                         static_cast<unsigned>(tokens < kRowsPerGridZ ? tokens : kRowsPerGridZ),
+        hipLaunchKernelGGL(k_sign_gemm<2>, grid, dim3(kBlock), 0, stream, gb);
+    if (rx > 0) {
+        const dim3 rgrid(static_cast<unsigned>(rx), static_cast<unsigned>(tokens < kRowsPerGridZ ? tokens : kRowsPerGridZ),
                          static_cast<unsigned>((tokens + kRowsPerGridZ - 1) / kRowsPerGridZ));
-        hipLaunchKernelGGL(k_reduce_splits, rgrid, dim3(kBlock), 0, stream, static_cast<int>(sp.slices), g);
+        hipLaunchKernelGGL(k_reduce_splits, rgrid, dim3(kBlock), 0, stream, rb);
     }
 }
 
 struct Scratch {
     int64_t xs16, scale1, lm16, scale2, partial, total;
+    int64_t partial_elems;  // fp32 elements of the partial buffer
     Split s1, s2;
 };
 
@@ -738,7 +867,8 @@ Scratch scratch_layout(const nq_linear_desc* d, int64_t tokens) {
     s.partial = s.scale2 + a256(tokens * 4);
     const int64_t p1 = s.s1.slices > 1 ? s.s1.slices * tokens * d->rank : 0;
     const int64_t p2 = s.s2.slices > 1 ? s.s2.slices * tokens * d->out_features : 0;
-    s.total = s.partial + a256(4 * (p1 > p2 ? p1 : p2));
+    s.partial_elems = p1 > p2 ? p1 : p2;
+    s.total = s.partial + a256(4 * s.partial_elems);
     return s;
 }
 
@@ -755,41 +885,53 @@ bool prefill_path_applies(const nq_linear_desc* d, int64_t tokens) {
     return d->tiles != nullptr && tokens > 16 && tokens <= 65535 * int64_t(kBM);
 }
 
-int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y, int y_dtype,
-                   void* scratch, hipStream_t stream) {
-    const Geometry geo = geometry(d);
+int launch_prefill_batch(const nq_linear_desc* const* descs, int count, const void* const* xs, int x_dtype,
+                         int64_t tokens, void* const* ys, int y_dtype, void* const* scratch, hipStream_t stream) {
+    if (count < 1 || count > kPrefillBatch) return NQ_ERR_SHAPE;
     const int64_t header_words = tiles_header_words();
-    if (d->tiles_bytes < (header_words + geo.v_words + geo.u_words) * 4) return NQ_ERR_ARGUMENT;
-    // The GEMMs read the fp16 staging buffers with 16-byte vector loads.
-    if ((reinterpret_cast<uintptr_t>(scratch) & 15) != 0) return NQ_ERR_ALIGNMENT;
-    const Scratch sl = scratch_layout(d, tokens);
-    char* ws = static_cast<char*>(scratch);
-    auto* xs16 = reinterpret_cast<_Float16*>(ws + sl.xs16);
-    auto* scale1 = reinterpret_cast<float*>(ws + sl.scale1);
-    auto* lm16 = reinterpret_cast<_Float16*>(ws + sl.lm16);
-    auto* scale2 = reinterpret_cast<float*>(ws + sl.scale2);
-    auto* partial = reinterpret_cast<float*>(ws + sl.partial);
-    const auto* base = static_cast<const uint32_t*>(d->tiles);
-    const dim3 rows(static_cast<unsigned>(tokens));
     auto aligned = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
-    // Vector row loads: 8 elements per load, 16-byte aligned rows.
-    const int vec1_ok = (d->in_features % 8 == 0 && aligned(x, 16) && aligned(d->scale_pre, 16)) ? 1 : 0;
+    Geometry geo[kPrefillBatch];
+    Scratch sl[kPrefillBatch];
+    PrepBatch pb{};
+    bool all_vec = true;
+    int64_t pad_max = 0;
+    for (int i = 0; i < count; ++i) {
+        const nq_linear_desc* d = descs[i];
+        geo[i] = geometry(d);
+        if (d->tiles_bytes < (header_words + geo[i].v_words + geo[i].u_words) * 4) return NQ_ERR_ARGUMENT;
+        // The GEMMs read the fp16 staging buffers with 16-byte vector loads.
+        if (!aligned(scratch[i], 16)) return NQ_ERR_ALIGNMENT;
+        sl[i] = scratch_layout(d, tokens);
+        char* ws = static_cast<char*>(scratch[i]);
+        PrepArgs& pa = pb.p[i];
+        pa.act = xs[i];
+        pa.ld = d->in_features;
+        pa.colscale = d->scale_pre;
+        pa.colscale_dtype = d->scale_dtype;
+        // Vector row loads: 8 elements per load, 16-byte aligned rows.
+        pa.vec = (d->in_features % 8 == 0 && aligned(xs[i], 16) && aligned(d->scale_pre, 16)) ? 1 : 0;
+        pa.cols = d->in_features;
+        pa.cols_pad = geo[i].nsc1 * kBK;
+        pa.out16 = reinterpret_cast<_Float16*>(ws + sl[i].xs16);
+        pa.scale_out = reinterpret_cast<float*>(ws + sl[i].scale1);
+        pa.max_mid_bits = static_cast<const uint32_t*>(d->tiles) + tiles_max_mid_word();
+        pa.bound_scale_out = reinterpret_cast<float*>(ws + sl[i].scale2);
+        all_vec = all_vec && pa.vec && d->scale_dtype == descs[0]->scale_dtype;
+        pad_max = pa.cols_pad > pad_max ? pa.cols_pad : pad_max;
+    }
 
-    const int64_t cols_pad1 = geo.nsc1 * kBK;
-    const uint32_t* max_mid = base + tiles_max_mid_word();
+    // Row passes: one launch, grid (tokens, members).
+    const dim3 rows(static_cast<unsigned>(tokens), static_cast<unsigned>(count));
     bool prepped = false;
-    if (vec1_ok && cols_pad1 <= int64_t(kPrepChunksMax) * 8 * kBlock) {
-        const bool short_rows = cols_pad1 <= 2 * 8 * kBlock;
+    if (all_vec && pad_max <= int64_t(kPrepChunksMax) * 8 * kBlock) {
+        const bool short_rows = pad_max <= 2 * 8 * kBlock;
+        const int sdt = descs[0]->scale_dtype;
 #define NQ_PREP(ADT, SDT)                                                                                      \
-    if (x_dtype == ADT && d->scale_dtype == SDT) {                                                             \
+    if (x_dtype == ADT && sdt == SDT) {                                                                        \
         if (short_rows)                                                                                        \
-            hipLaunchKernelGGL((k_prep_rows_vec<ADT, SDT, 2>), rows, dim3(kBlock), 0, stream, x,                \
-                               d->in_features, d->scale_pre, d->in_features, cols_pad1, xs16, scale1, max_mid,  \
-                               scale2);                                                                        \
+            hipLaunchKernelGGL((k_prep_rows_vec<ADT, SDT, 2>), rows, dim3(kBlock), 0, stream, pb);              \
         else                                                                                                   \
-            hipLaunchKernelGGL((k_prep_rows_vec<ADT, SDT, kPrepChunksMax>), rows, dim3(kBlock), 0, stream, x,   \
-                               d->in_features, d->scale_pre, d->in_features, cols_pad1, xs16, scale1, max_mid,  \
-                               scale2);                                                                        \
+            hipLaunchKernelGGL((k_prep_rows_vec<ADT, SDT, kPrepChunksMax>), rows, dim3(kBlock), 0, stream, pb); \
         prepped = true;                                                                                        \
     }
 #define NQ_PREP_S(ADT) NQ_PREP(ADT, NQ_DTYPE_F16) NQ_PREP(ADT, NQ_DTYPE_BF16) NQ_PREP(ADT, NQ_DTYPE_F32)
@@ -797,54 +939,92 @@ int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t 
 #undef NQ_PREP_S
 #undef NQ_PREP
     }
-    if (!prepped)
-        hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, x, x_dtype, d->in_features, d->scale_pre,
-                           d->scale_dtype, d->in_features, cols_pad1, vec1_ok, xs16, scale1, max_mid, scale2);
-    GemmArgs g1{};
-    g1.a = xs16;
-    g1.m = tokens;
-    g1.kpad = geo.nsc1 * kBK;
-    g1.tiles = base + header_words;
-    g1.n = d->rank;
-    g1.nb = geo.nsc1;
-    g1.row_scale = scale1;
-    g1.col_scale = d->scale_mid;
-    g1.col_scale_dtype = d->scale_dtype;
-    g1.out = lm16;
-    g1.out_dtype = NQ_DTYPE_F16;
-    g1.out_scale = scale2;
-    g1.out_ld = geo.nsc2 * kBK;  // GEMM 1's column blocks cover exactly this width
-    g1.k_per_split = sl.s1.k_per_split;
-    g1.partial = sl.s1.slices > 1 ? partial : nullptr;
-    launch_gemm(g1, sl.s1, tokens, g1.out_ld, stream);
+    if (!prepped) hipLaunchKernelGGL(k_prep_rows, rows, dim3(kBlock), 0, stream, pb, x_dtype);
 
-    GemmArgs g2{};
-    g2.a = lm16;
-    g2.m = tokens;
-    g2.kpad = geo.nsc2 * kBK;
-    g2.tiles = base + header_words + geo.v_words;
-    g2.n = d->out_features;
-    g2.nb = geo.nsc2;
-    g2.row_scale = scale2;
-    g2.col_scale = d->scale_post;
-    g2.col_scale_dtype = d->scale_dtype;
-    g2.x = x;
-    g2.x_dtype = x_dtype;
-    g2.in = d->in_features;
-    g2.salient_count = d->salient_count;
-    g2.salient_indices = d->salient_indices;
-    g2.salient_values = d->salient_values;
-    g2.salient_dtype = d->salient_dtype;
-    g2.salient_scales = d->salient_scales;
-    g2.scale_dtype = d->scale_dtype;
-    g2.bias = d->bias;
-    g2.bias_dtype = d->bias_dtype;
-    g2.out = y;
-    g2.out_dtype = y_dtype;
-    g2.k_per_split = sl.s2.k_per_split;
-    g2.partial = sl.s2.slices > 1 ? partial : nullptr;
-    launch_gemm(g2, sl.s2, tokens, d->out_features, stream);
+    const int64_t mt = (tokens + kBM - 1) / kBM;
+    int64_t tiles[kPrefillBatch], kb[kPrefillBatch], n[kPrefillBatch], cap[kPrefillBatch];
+    Split solo[kPrefillBatch], sp[kPrefillBatch];
+    GemmArgs g[kPrefillBatch];
+
+    // GEMM 1: lm16 = fp16 rank intermediate, scaled per row by scale2.
+    for (int i = 0; i < count; ++i) {
+        tiles[i] = mt * ((descs[i]->rank + kBN - 1) / kBN);
+        kb[i] = geo[i].nsc1;
+        n[i] = descs[i]->rank;
+        cap[i] = sl[i].partial_elems;
+        solo[i] = sl[i].s1;
+    }
+    batch_splits(count, tiles, kb, n, cap, solo, tokens, sp);
+    for (int i = 0; i < count; ++i) {
+        const nq_linear_desc* d = descs[i];
+        char* ws = static_cast<char*>(scratch[i]);
+        GemmArgs& a = g[i];
+        a = GemmArgs{};
+        a.a = pb.p[i].out16;
+        a.m = tokens;
+        a.kpad = geo[i].nsc1 * kBK;
+        a.tiles = static_cast<const uint32_t*>(d->tiles) + header_words;
+        a.n = d->rank;
+        a.nb = geo[i].nsc1;
+        a.row_scale = pb.p[i].scale_out;
+        a.col_scale = d->scale_mid;
+        a.col_scale_dtype = d->scale_dtype;
+        a.out = ws + sl[i].lm16;
+        a.out_dtype = NQ_DTYPE_F16;
+        a.out_scale = pb.p[i].bound_scale_out;
+        a.out_ld = geo[i].nsc2 * kBK;  // GEMM 1's column blocks cover exactly this width
+        a.k_per_split = sp[i].k_per_split;
+        a.splits = sp[i].slices;
+        a.partial = sp[i].slices > 1 ? reinterpret_cast<float*>(ws + sl[i].partial) : nullptr;
+    }
+    launch_phase(g, count, tokens, stream);
+
+    // GEMM 2: y = s_out * (lm16 · U±1ᵀ) / scale2 + salient columns + bias.
+    for (int i = 0; i < count; ++i) {
+        tiles[i] = mt * ((descs[i]->out_features + kBN - 1) / kBN);
+        kb[i] = geo[i].nsc2;
+        n[i] = descs[i]->out_features;
+        solo[i] = sl[i].s2;
+    }
+    batch_splits(count, tiles, kb, n, cap, solo, tokens, sp);
+    for (int i = 0; i < count; ++i) {
+        const nq_linear_desc* d = descs[i];
+        char* ws = static_cast<char*>(scratch[i]);
+        GemmArgs& a = g[i];
+        a = GemmArgs{};
+        a.a = reinterpret_cast<const _Float16*>(ws + sl[i].lm16);
+        a.m = tokens;
+        a.kpad = geo[i].nsc2 * kBK;
+        a.tiles = static_cast<const uint32_t*>(d->tiles) + header_words + geo[i].v_words;
+        a.n = d->out_features;
+        a.nb = geo[i].nsc2;
+        a.row_scale = pb.p[i].bound_scale_out;
+        a.col_scale = d->scale_post;
+        a.col_scale_dtype = d->scale_dtype;
+        a.x = xs[i];
+        a.x_dtype = x_dtype;
+        a.in = d->in_features;
+        a.salient_count = d->salient_count;
+        a.salient_indices = d->salient_indices;
+        a.salient_values = d->salient_values;
+        a.salient_dtype = d->salient_dtype;
+        a.salient_scales = d->salient_scales;
+        a.scale_dtype = d->scale_dtype;
+        a.bias = d->bias;
+        a.bias_dtype = d->bias_dtype;
+        a.out = ys[i];
+        a.out_dtype = y_dtype;
+        a.k_per_split = sp[i].k_per_split;
+        a.splits = sp[i].slices;
+        a.partial = sp[i].slices > 1 ? reinterpret_cast<float*>(ws + sl[i].partial) : nullptr;
+    }
+    launch_phase(g, count, tokens, stream);
     return launch_status();
+}
+
+int launch_prefill(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y, int y_dtype,
+                   void* scratch, hipStream_t stream) {
+    return launch_prefill_batch(&d, 1, &x, x_dtype, tokens, &y, y_dtype, &scratch, stream);
 }
 
 }  // namespace nq

@@ -9,8 +9,8 @@ generation engine's ``GenerationModel.forward_step`` protocol
 shell built from this library's kernels instead:
 
 * every projection is a packed linear on ``HipPackedBackend`` — Q/K/V and
-  gate/up run as one batched decode call each (tokens <= 16), the prompt runs
-  the MFMA prefill path;
+  gate/up run as one batched call each: the decode stages for up to 16
+  tokens, the MFMA prefill phases for a longer prompt;
 * embedding, residual add + RMSNorm, q/k RMSNorm + RoPE + KV append,
   grouped-query attention (one fused kernel per layer for a decode token),
   SiLU product, the bf16 output projection and greedy selection are the HIP
@@ -313,11 +313,7 @@ class PackedDecoder:
 
     # -- one forward -----------------------------------------------------------------
     def _linears(self, xs: list[torch.Tensor], layers: list[PreparedLayer], outs: list[torch.Tensor], tokens: int) -> None:
-        if tokens <= 16:
-            self.backend.linear_batch(xs, layers, outs=outs)
-        else:
-            for x, layer, out in zip(xs, layers, outs):
-                self.backend.linear_into(x, layer, out=out)
+        self.backend.linear_batch(xs, layers, outs=outs)
 
     def _forward(self, ids: torch.Tensor, b: _Buffers) -> None:
         """Embedding .. final norm for `b.tokens` rows at positions position[0] + t,

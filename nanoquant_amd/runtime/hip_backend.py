@@ -264,7 +264,9 @@ class HipPackedBackend:
         output_dtype: torch.dtype = torch.float32,
         outs: list[torch.Tensor] | None = None,
     ) -> list[torch.Tensor]:
-        """Run up to 8 prepared layers in ONE decode launch (1-16 token slots).
+        """Run up to 8 prepared layers with one launch per kernel phase: the
+        decode kernels for 1-16 token slots, the prefill row pass, sign GEMMs
+        and reductions above that.
 
         Generalises the reference's grouped Q/K/V and gate/up projection
         (src/nanoquant/runtime/cuda_backend.py:65-144): members may have distinct
@@ -282,8 +284,6 @@ class HipPackedBackend:
         if len(tokens) != 1 or len(dtypes) != 1:
             raise ValueError("HIP packed batch members must share token count and input dtype")
         (count,) = tokens
-        if not 1 <= count <= 16:
-            raise ValueError("HIP packed batch supports 1-16 token slots")
         for value, layer, payload in zip(values, layers, payloads):
             _check_value(value, layer.spec, payload.device)
         if output_dtype not in (torch.float32, torch.bfloat16, torch.float16):
@@ -567,17 +567,14 @@ def prepare_hip_projection_group(layers: tuple[PreparedLayer, ...]) -> HipProjec
 def grouped_hip_projection(value: torch.Tensor, group: HipProjectionGroup) -> tuple[torch.Tensor, ...]:
     """Every layer of `group` applied to `value` ([..., in], f16/bf16/f32): fp32
     outputs ``[..., out_i]`` in group order, as grouped_cuda_projection returns
-    (src/nanoquant/runtime/cuda_backend.py:123-144). Token counts 1-16 run as
-    one decode launch pair for the whole group (nq_linear_batch); larger
-    counts run each layer's prefill call."""
+    (src/nanoquant/runtime/cuda_backend.py:123-144). The whole group shares
+    one launch per kernel phase (nq_linear_batch): the decode stages for 1-16
+    tokens, the prefill phases above that."""
 
     if value.device != group.device:
         raise ValueError("grouped HIP projection input uses a different device")
     backend = HipPackedBackend()
-    tokens = value.numel() // max(value.shape[-1], 1) if value.ndim else 0
-    if 1 <= tokens <= 16:
-        return tuple(backend.linear_batch([value] * len(group.layers), list(group.layers)))
-    return tuple(backend.linear(value, layer) for layer in group.layers)
+    return tuple(backend.linear_batch([value] * len(group.layers), list(group.layers)))
 
 
 def _check_value(value: torch.Tensor, spec: QuantizedLinearSpec, device: torch.device) -> None:

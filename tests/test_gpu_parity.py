@@ -676,6 +676,90 @@ def test_grouped_projection_qwen3_qkv_and_gate_up(tokens):
             assert err <= REL_L2, (state.spec.name, err)
 
 
+@pytest.mark.parametrize("tokens", [17, 64, 300])
+def test_prefill_batches_match_oracle(tokens):
+    """Above 16 tokens a batch runs each prefill phase (row passes, both sign
+    GEMMs, their split-K reductions) as one launch for all members, with K
+    splits chosen for the whole launch. Q/K/V of Llama-3-8B on a shared x and
+    all seven linears on four inputs (salient columns on o, bias on down),
+    each member against the oracle and against its single-linear call; a
+    batch of one is that call, bit for bit."""
+
+    backend = HipPackedBackend()
+    shapes = syn.llama3_8b_layer()
+    states = [syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 90 + i, salient=5 if i == 3 else 0, bias=i == 6)
+              for i, s in enumerate(shapes)]
+    layers = [backend.prepare(st, "cuda") for st in states]
+    xa, xo, xm = (syn.synthetic_activations(tokens, 4096, seed=s, device="cuda") for s in (1, 2, 3))
+    xd = syn.synthetic_activations(tokens, 14336, seed=4, device="cuda")
+    inputs = [xa, xa, xa, xo, xm, xm, xd]
+    _say("prefill qkv batch", tokens)
+    qkv = backend.linear_batch(inputs[:3], layers[:3])
+    _say("prefill layer batch", tokens)
+    whole = backend.linear_batch(inputs, layers)
+    again = backend.linear_batch(inputs, layers)
+    for i, (state, x) in enumerate(zip(states, inputs)):
+        expected = orc.packed_forward(orc.operands_from_state(state), x.cpu())
+        single = backend.linear(x, layers[i])
+        for name, y in (("layer", whole[i]), ("qkv", qkv[i] if i < 3 else None)):
+            if y is None:
+                continue
+            err = orc.relative_l2(y, expected)
+            assert err <= REL_L2, (state.spec.name, name, tokens, err)
+            assert orc.relative_l2(y, single) <= 1e-4, (state.spec.name, name, tokens)
+        assert torch.equal(whole[i], again[i])
+        (one,) = backend.linear_batch([x], [layers[i]])
+        assert torch.equal(one, single), state.spec.name
+    print(f"  M={tokens}: 7 members within {REL_L2} of the oracle", flush=True)
+
+
+@pytest.mark.parametrize("tokens", [40, 129])
+def test_prefill_batch_ragged_members(tokens):
+    """Members of unlike geometry in one prefill batch: word tails, partial
+    tiles, an input width that is not a multiple of 8 (the generic row pass for
+    the whole batch), salient columns and bias, members whose K is split beside
+    members whose K is not (empty reduction ranges), bf16 outputs."""
+
+    backend = HipPackedBackend()
+    geometries = [(35, 17, 33, 3), (200, 130, 129, 5), (1152, 864, 768, 0), (640, 257, 96, 31),
+                  (4096, 1024, 655, 0)]
+    states = [syn.synthetic_packed_layer(syn.LinearShape(f"blocks.0.m{i}", g[0], g[1], g[2]), seed=tokens + 7 * i,
+                                         salient=g[3], bias=True) for i, g in enumerate(geometries)]
+    layers = [backend.prepare(st, "cuda") for st in states]
+    xs = [syn.synthetic_activations(tokens, g[0], seed=tokens + i, device="cuda") for i, g in enumerate(geometries)]
+    _say("prefill ragged batch", tokens)
+    ys = backend.linear_batch(xs, layers)
+    outs = [torch.empty(tokens, g[1], dtype=torch.bfloat16, device="cuda") for g in geometries]
+    backend.linear_batch(xs, layers, output_dtype=torch.bfloat16, outs=outs)
+    for state, x, y, out in zip(states, xs, ys, outs):
+        err = orc.relative_l2(y, orc.packed_forward(orc.operands_from_state(state), x.cpu()))
+        assert err <= REL_L2, (state.spec.name, tokens, err)
+        torch.testing.assert_close(out, y.to(torch.bfloat16), rtol=0, atol=0)
+    # The vector row pass where every member allows it (widths divisible by 8).
+    _say("prefill vector-row batch", tokens)
+    ys = backend.linear_batch(xs[2:], layers[2:])
+    for state, x, y in zip(states[2:], xs[2:], ys):
+        err = orc.relative_l2(y, orc.packed_forward(orc.operands_from_state(state), x.cpu()))
+        assert err <= REL_L2, (state.spec.name, tokens, err)
+
+
+def test_prefill_batch_wide_blocks_at_2048():
+    """Gate/up of Llama-3-8B at M = 2048: the batch takes the 128 x 256 block
+    tile for its second GEMM (no member split) and matches the oracle."""
+
+    backend = HipPackedBackend()
+    shapes = syn.llama3_8b_layer()[4:6]
+    states = [syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 95 + i) for i, s in enumerate(shapes)]
+    layers = [backend.prepare(st, "cuda") for st in states]
+    x = syn.synthetic_activations(2048, 4096, seed=9, device="cuda")
+    _say("prefill gate/up batch", 2048)
+    ys = backend.linear_batch([x, x], layers)
+    for state, y, layer in zip(states, ys, layers):
+        err = orc.relative_l2(y, orc.packed_forward(orc.operands_from_state(state), x.cpu()))
+        assert err <= REL_L2, (state.spec.name, err)
+        assert orc.relative_l2(y, backend.linear(x, layer)) <= 1e-4
+
+
 def test_batch_rejects_mixed_launch_structures():
     state = syn.synthetic_packed_layer(syn.qwen3_8b_layer()[1], seed=3)
     split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
