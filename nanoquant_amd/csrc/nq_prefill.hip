@@ -27,16 +27,21 @@
 // each A fragment two B fragments.
 //
 // Block tile 128 (tokens) x 128 (sign rows), 4 waves in a 2 x 2 grid, each
-// wave 64 x 64 = 2 x 2 MFMA tiles of 32 x 32 accumulated in fp32. The
-// activation tile (128 x 128 fp16, padded rows) is double-buffered in LDS:
-// the loads of the next 128-column block are in flight during the current
-// block's MFMAs, and one barrier per block orders the buffer swap.
+// wave 64 x 64 = 2 x 2 MFMA tiles of 32 x 32 accumulated in fp32 (or 128 x
+// 256, waves side by side, for large GEMMs). The activation tile (128 x 128
+// fp16, 16-byte chunks XOR-swizzled by row) is double-buffered in LDS and
+// moved there by global_load_lds_dwordx4, so the next 128-column block is in
+// flight during the current block's MFMAs without holding registers; one
+// barrier per block orders the buffer swap. Within a block the eight
+// 16-column slices are software-pipelined: slice m's MFMAs issue while slice
+// m + 1's A fragments are read and its signs expanded.
 //
 // Split K: when a GEMM has too few (token, sign-row) tiles to fill the GPU,
-// grid dimension z splits the K blocks into ranges of at least four and each
-// workgroup writes its raw fp32 accumulators to partial[z][t][n]; then
-// k_reduce_splits, one thread per output element, sums them in z order
-// (deterministic) and applies the epilogue.
+// its K blocks are split into slices of at least two, each workgroup writes
+// its raw fp32 accumulators to partial[slice][t][n], and k_reduce_splits, one
+// thread per output element, sums them in slice order (deterministic) and
+// applies the epilogue. A batched call runs up to eight GEMMs of one phase in
+// one launch, their (column block, slice) ranges concatenated along grid x.
 #include "nq_prefill.h"
 
 namespace {
@@ -50,11 +55,14 @@ constexpr int kBlock = 256;
 constexpr int kBM = 128;
 constexpr int kBN = 128;
 constexpr int kBK = 128;                 // one superchunk per K step
-constexpr int kAStride = kBK + 8;        // halfs; rows land in different banks
 constexpr int kTileRows = 16;
 constexpr int kPrefillBatch = 8;         // members of one batched call
+// s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15): wait for this wave's vector
+// memory operations only (gfx9 encoding), as a builtin the compiler's own
+// wait tracking takes into account.
+constexpr int kWaitVmcnt0 = 0x0F70;
 constexpr int kParkStride = 65;          // floats per parked accumulator row
-constexpr int kALdsBytes = kBM * kAStride * 2;
+constexpr int kALdsBytes = kBM * kBK * 2;  // one activation tile, rows of 256 bytes
 constexpr int kParkBytes = 4 * 64 * kParkStride * 4;
 constexpr int kLdsBytes = 2 * kALdsBytes > kParkBytes ? 2 * kALdsBytes : kParkBytes;  // double-buffered A
 
@@ -308,9 +316,7 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows_vec(const PrepBatch batch)
 __device__ __forceinline__ uint32_t sign_pair(uint32_t w, int shift, uint32_t mask, uint32_t one) {
     // ((w << shift) & mask) | one as two instructions: the masks are kept in
     // registers because a VOP3 instruction cannot take two literal constants.
-    uint32_t d;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(w << shift), "v"(mask), "v"(one));
-    return d;
+    return ((w << shift) & mask) | one;
 }
 
 __device__ __forceinline__ v8h expand_signs32(uint32_t w0, uint32_t w1, int m, uint32_t mask, uint32_t one) {
@@ -393,7 +399,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
     const int col_block = local - slice * col_blocks;
     __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int wm = WM == 2 ? wave >> 1 : 0;  // wave row
     const int wn = WM == 2 ? wave & 1 : wave;  // wave column
     const int h = lane >> 5;   // K half of the 32 x 32 x 16 operands
@@ -414,79 +420,137 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
         for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
 
     uint32_t words[2][2], next_words[2][2];
-    uint4 next_a[8];
-    // Loads are unconditional: rows past M and sign tiles past N read a valid
-    // row / tile instead; they only feed accumulators whose outputs are never
-    // stored.
+    // Activation tile: 128 rows of 128 fp16 (256 bytes) per buffer, moved
+    // from global memory straight into LDS (global_load_lds_dwordx4: lane l
+    // of an instruction writes 16 bytes at the wave's LDS address + 16 l), so
+    // the next K step's tile costs no registers while it is in flight. Wave w's
+    // instruction j fills LDS rows 4 (8 w + j) + [0, 4); lane l writes chunk
+    // position p = l & 15 of row r, which holds the row's 16-byte column chunk
+    // p ^ (r & 15): the A-fragment reads (32 rows at one chunk per
+    // instruction) then fall on distinct banks. Rows past M read the last
+    // valid row; an instruction whose four rows are all past M is skipped
+    // (those rows only feed accumulators whose outputs are never stored).
+    // Loads are unconditional otherwise: sign tiles past N read a valid tile.
     const int64_t nsc = g.nb, kpad = g.kpad;
-    const int a_row = threadIdx.x >> 4, a_col = (threadIdx.x & 15) * 8;
-    const int64_t a_last = g.m - 1 - m0;  // last valid row of this block
-    const _Float16* const a_base = g.a + m0 * kpad + a_col;
+    const int64_t a_rows = g.m - m0;  // valid rows of this block (>= 1)
+    // Byte offsets from the block's first row (below 2^31: 128 rows of a
+    // padded K that the host limits), added to a wave-uniform base.
+    const char* const a_blk = reinterpret_cast<const char*>(g.a + m0 * kpad);
+    uint32_t a_src[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int row = 4 * (8 * wave + j) + (lane >> 4);
+        const int chunk = (lane & 15) ^ (row & 15);
+        const int64_t rr = row < a_rows ? row : a_rows - 1;
+        a_src[j] = static_cast<uint32_t>((rr * kpad + 8 * chunk) * 2);
+    }
     const int64_t rt_a = rt0 < rt_count ? rt0 : rt_count - 1;
     const int64_t rt_b = rt0 + 2 < rt_count ? rt0 + 2 : rt_count - 1;
     const uint32_t* const b0 = g.tiles + rt_a * nsc * 64;
     const uint32_t* const b1 = g.tiles + rt_b * nsc * 64;
     const int64_t k_begin = static_cast<int64_t>(slice) * g.k_per_split;
     const int64_t k_end = k_begin + g.k_per_split < nsc ? k_begin + g.k_per_split : nsc;
-#define NQ_LOAD_STEP(SC)                                                                            \
-    do {                                                                                            \
-        const int64_t c_ = (SC) >> 2;                                                               \
-        const int64_t rem_ = nsc - 4 * c_;                                                          \
-        const int dw_ = static_cast<int>(rem_ < 4 ? rem_ : 4);                                      \
-        const int64_t off_ = c_ * 256 + ((SC) & 3);                                                 \
-        next_words[0][0] = b0[off_ + wl0 * dw_];                                                    \
-        next_words[0][1] = b0[off_ + wl1 * dw_];                                                    \
-        next_words[1][0] = b1[off_ + wl0 * dw_];                                                    \
-        next_words[1][1] = b1[off_ + wl1 * dw_];                                                    \
-        _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_) {                                          \
-            const int64_t r_ = a_row + 16 * i_ < a_last ? a_row + 16 * i_ : a_last;                 \
-            next_a[i_] = *reinterpret_cast<const uint4*>(a_base + r_ * kpad + (SC) * kBK);          \
-        }                                                                                           \
-    } while (0)
-#define NQ_STAGE_A(BUF)                                                                             \
-    do {                                                                                            \
-        _Float16* dst_ = reinterpret_cast<_Float16*>(lds) + (BUF) * (kBM * kAStride) + a_col;      \
-        _Pragma("unroll") for (int i_ = 0; i_ < 8; ++i_)                                            \
-            *reinterpret_cast<uint4*>(dst_ + (a_row + 16 * i_) * kAStride) = next_a[i_];            \
-    } while (0)
-    // Double-buffered activation tile: step s computes on buffer s & 1 while
-    // the loads of step s + 1 are in flight; they go to the other buffer after
-    // the compute, and one barrier per step orders both.
-    NQ_LOAD_STEP(k_begin);
-    NQ_STAGE_A(0);
+    // The transfer is issued as inline asm with its LDS address in M0: the
+    // compiler then does not track it, so the A-fragment reads of the current
+    // buffer wait only on themselves (lgkmcnt(4)) instead of lgkmcnt(0) while
+    // the next tile is in flight. Completion is this kernel's own business: a
+    // transfer only targets the buffer no wave reads in that step, and every
+    // step ends with vmcnt(0) and a barrier before that buffer is read.
+    typedef __attribute__((address_space(3))) void lds_void_t;
+    const auto load_a = [&](int64_t sc, int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (4 * (8 * wave + j) >= a_rows) continue;  // wave-uniform
+            lds_void_t* dst = (lds_void_t*)(lds + buf * kALdsBytes + (8 * wave + j) * 1024);
+            const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
+            const char* src = a_blk + sc * (2 * kBK) + a_src[j];
+            // s_nop: one wait state between the M0 write and the LDS transfer.
+            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
+        }
+    };
+    const auto load_words = [&](int64_t sc) __attribute__((always_inline)) {
+        const int64_t c_ = sc >> 2;
+        const int64_t rem_ = nsc - 4 * c_;
+        const int dw_ = static_cast<int>(rem_ < 4 ? rem_ : 4);
+        const int64_t off_ = c_ * 256 + (sc & 3);
+        next_words[0][0] = b0[off_ + wl0 * dw_];
+        next_words[0][1] = b0[off_ + wl1 * dw_];
+        next_words[1][0] = b1[off_ + wl0 * dw_];
+        next_words[1][1] = b1[off_ + wl1 * dw_];
+    };
+    // Byte offset, within a buffer, of the A fragment of 16-column slice m
+    // for fragment row 0 (fragment ii adds 32 rows = 8192 bytes).
+    int a_off[8];
+#pragma unroll
+    for (int m = 0; m < 8; ++m) a_off[m] = (64 * wm + r) * 256 + 16 * ((2 * m + h) ^ (r & 15));
+    // Step s computes on buffer s & 1 while the tile of step s + 1 moves into
+    // the other; a wait for this wave's transfers and one barrier per step
+    // make every wave's part of the next tile visible before it is read.
+    load_a(k_begin, 0);
+    load_words(k_begin);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
 #pragma unroll
     for (int jj = 0; jj < 2; ++jj) words[jj][0] = next_words[jj][0], words[jj][1] = next_words[jj][1];
-    __syncthreads();
     int buf = 0;
     uint32_t sign_mask = 0x80008000u, fp16_one = 0x3C003C00u;
     asm volatile("" : "+v"(sign_mask), "+v"(fp16_one));  // keep them in VGPRs
     for (int64_t sc = k_begin; sc < k_end; ++sc) {
-        // The last step prefetches its own block again (into the idle buffer)
-        // so that the prefetch registers are written on every path.
-        const int64_t next = sc + 1 < k_end ? sc + 1 : sc;
-        NQ_LOAD_STEP(next);
-        const _Float16* a_lds = reinterpret_cast<const _Float16*>(lds) + buf * (kBM * kAStride);
+        const bool more = sc + 1 < k_end;
+        if (more) load_a(sc + 1, buf ^ 1);
+        load_words(more ? sc + 1 : sc);
+        // The sign words of the next step are issued here, ahead of the
+        // MFMAs; left to itself the scheduler sinks them to the step's end,
+        // where the wait before the barrier would take their whole latency.
+        __builtin_amdgcn_sched_barrier(0);
+        const char* a_lds = lds + buf * kALdsBytes;
+        // Software pipeline over the eight 16-column slices: slice m's MFMAs
+        // issue while slice m + 1's A fragments are read from LDS and its
+        // sign fragments expanded, so no MFMA waits on a read issued just
+        // before it. Each slice is one scheduling region (sched_barrier) laid
+        // out as the reads, then MFMAs alternating with the expansion.
+        v8h a_cur[II], b_cur[2];
+#pragma unroll
+        for (int ii = 0; ii < II; ++ii) a_cur[ii] = *reinterpret_cast<const v8h*>(a_lds + a_off[0] + 8192 * ii);
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) b_cur[jj] = expand_signs32(words[jj][0], words[jj][1], 0, sign_mask, fp16_one);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
-            v8h b[2];
+            __builtin_amdgcn_sched_barrier(0);
+            v8h a_nxt[II], b_nxt[2];
+            if (m < 7) {
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) b[jj] = expand_signs32(words[jj][0], words[jj][1], m, sign_mask, fp16_one);
-#pragma unroll
-            for (int ii = 0; ii < II; ++ii) {
-                const v8h a = *reinterpret_cast<const v8h*>(&a_lds[(64 * wm + 32 * ii + r) * kAStride + 16 * m + 8 * h]);
+                for (int ii = 0; ii < II; ++ii)
+                    a_nxt[ii] = *reinterpret_cast<const v8h*>(a_lds + a_off[m + 1] + 8192 * ii);
 #pragma unroll
                 for (int jj = 0; jj < 2; ++jj)
-                    acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[jj], acc[ii][jj], 0, 0, 0);
+                    b_nxt[jj] = expand_signs32(words[jj][0], words[jj][1], m + 1, sign_mask, fp16_one);
+            }
+#pragma unroll
+            for (int ii = 0; ii < II; ++ii)
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj)
+                    acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[ii], b_cur[jj], acc[ii][jj], 0, 0, 0);
+            if (m < 7) {
+                __builtin_amdgcn_sched_group_barrier(0x100, II, 0);  // LDS reads of slice m + 1
+#pragma unroll
+                for (int q = 0; q < 2 * II; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA of slice m
+                    __builtin_amdgcn_sched_group_barrier(0x002, 16 / (2 * II), 0);  // expansion of m + 1
+                }
+#pragma unroll
+                for (int ii = 0; ii < II; ++ii) a_cur[ii] = a_nxt[ii];
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) b_cur[jj] = b_nxt[jj];
             }
         }
-        NQ_STAGE_A(buf ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) words[jj][0] = next_words[jj][0], words[jj][1] = next_words[jj][1];
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
         buf ^= 1;
     }
-#undef NQ_LOAD_STEP
-#undef NQ_STAGE_A
 
 
     // Epilogue through LDS: each wave parks its 64 x 64 fp32 tile (lane holds
@@ -729,15 +793,16 @@ Geometry geometry(const nq_linear_desc* d) {
 int64_t a256(int64_t n) { return (n + 255) & ~int64_t(255); }
 
 // Split of a GEMM with `tiles` (token, sign-row) tiles over K blocks, from a
-// latency model of the K loop (fitted to kernel traces on MI355X): a K step
-// costs about one memory round trip, kStepNs, while the GPU holds every
+// latency model of the K loop (fitted to layer timings on MI355X): a K step
+// costs kStepNs (the next step's tile is in flight during the current one,
+// so a step is about one compute pass, not a memory round trip), while the GPU holds every
 // workgroup at once (kResident: two per CU, bound by LDS); workgroups beyond
 // that run in further rounds; a split adds the reduce launch and the
 // partials' write and read (M x N x 4 bytes per slice, mostly served by the
 // last-level cache). Slices hold at least kMinSliceBlocks K blocks.
 constexpr int64_t kResident = 512;
 constexpr int64_t kMinSliceBlocks = 2;
-constexpr double kStepNs = 2000.0;
+constexpr double kStepNs = 1000.0;
 constexpr double kReduceNs = 3000.0;
 constexpr double kPartialBytesPerNs = 8000.0;
 
