@@ -61,10 +61,6 @@ constexpr int kPrefillBatch = 8;         // members of one batched call
 // memory operations only (gfx9 encoding), as a builtin the compiler's own
 // wait tracking takes into account.
 constexpr int kWaitVmcnt0 = 0x0F70;
-constexpr int kParkStride = 65;          // floats per parked accumulator row
-constexpr int kALdsBytes = kBM * kBK * 2;  // one activation tile, rows of 256 bytes
-constexpr int kParkBytes = 4 * 64 * kParkStride * 4;
-constexpr int kLdsBytes = 2 * kALdsBytes > kParkBytes ? 2 * kALdsBytes : kParkBytes;  // double-buffered A
 
 __device__ __forceinline__ float exp2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
 
@@ -383,48 +379,57 @@ __device__ __forceinline__ int batch_member(const GemmBatch& b, int x) {
     return m;
 }
 
-// WM = 2: the four waves form a 2 x 2 grid of 64 x 64 tiles (block tile
-// 128 x 128). WM = 1: they sit side by side, each 128 x 64 (block tile
-// 128 x 256): every expanded sign fragment then serves four A fragments
-// instead of two, for GEMMs with enough blocks to fill the GPU at that size.
-template <int WM>
-__global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) {
-    constexpr int II = 4 / WM;            // 32-row A fragments per wave
-    constexpr int BN = 64 * (4 / WM);     // sign rows per block
+// Block shapes, as (WR wave rows, II 32-row A fragments and JJ 32-column B
+// fragments per wave): (2, 2, 2): the four waves form a 2 x 2 grid of 64 x 64
+// tiles (block tile 128 x 128). (1, 4, 2): they sit side by side, each
+// 128 x 64 (block tile 128 x 256): every expanded sign fragment then serves
+// four A fragments instead of two, for GEMMs with enough blocks to fill the
+// GPU at that size. (1, 2, 1): side by side, each 64 x 32 (block tile
+// 64 x 128), for at most 64 tokens: no MFMA or A read is spent on rows past
+// the last token.
+template <int WR, int II, int JJ>
+__global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const GemmBatch batch) {
+    constexpr int BM = WR * 32 * II;      // token rows per block
+    constexpr int BN = (4 / WR) * 32 * JJ;  // sign rows per block
+    constexpr int NJ = BM / 16;           // 1-KB LDS transfers per wave per K step
+    constexpr int kABytes = BM * kBK * 2;   // one activation tile, rows of 256 bytes
+    constexpr int kParkStride = 32 * JJ + 1;  // floats per parked accumulator row
+    constexpr int kParkBytes = 4 * 64 * kParkStride * 4;
+    constexpr int kLds = 2 * kABytes > kParkBytes ? 2 * kABytes : kParkBytes;  // double-buffered A
     const int member = batch_member(batch, static_cast<int>(blockIdx.x));
     const GemmArgs& g = batch.p[member];
     const int local = static_cast<int>(blockIdx.x) - batch.begin[member];
     const int col_blocks = static_cast<int>(g.col_blocks);
     const int slice = local / col_blocks;
     const int col_block = local - slice * col_blocks;
-    __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+    __shared__ __attribute__((aligned(16))) char lds[kLds];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-    const int wm = WM == 2 ? wave >> 1 : 0;  // wave row
-    const int wn = WM == 2 ? wave & 1 : wave;  // wave column
+    const int wm = WR == 2 ? wave >> 1 : 0;  // wave row
+    const int wn = WR == 2 ? wave & 1 : wave;  // wave column
     const int h = lane >> 5;   // K half of the 32 x 32 x 16 operands
     const int r = lane & 31;   // A row / B column within a 32-wide fragment
-    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kBM;
+    const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
     const int64_t n0 = static_cast<int64_t>(col_block) * BN;
     const int64_t rt_count = (g.n + kTileRows - 1) / kTileRows;
-    // B fragment jj covers sign rows n0 + 64 wn + 32 jj + [0, 32): lane r reads
-    // row r of tile (r >> 4) of that pair, from the words of lane groups 2h
-    // and 2h + 1, which hold columns 16m + 8h + [0, 8) of each 16-column slice.
-    const int64_t rt0 = n0 / kTileRows + 4 * wn + (r >> 4);
+    // B fragment jj covers sign rows n0 + 32 JJ wn + 32 jj + [0, 32): lane r
+    // reads row r of tile (r >> 4) of that pair, from the words of lane groups
+    // 2h and 2h + 1, which hold columns 16m + 8h + [0, 8) of each 16-column slice.
+    const int64_t rt0 = n0 / kTileRows + 2 * JJ * wn + (r >> 4);
     const int wl0 = 16 * (2 * h) + (r & 15), wl1 = wl0 + 16;
 
-    v16f acc[II][2];
+    v16f acc[II][JJ];
 #pragma unroll
     for (int i = 0; i < II; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = v16f{};
+        for (int j = 0; j < JJ; ++j) acc[i][j] = v16f{};
 
-    uint32_t words[2][2], next_words[2][2];
-    // Activation tile: 128 rows of 128 fp16 (256 bytes) per buffer, moved
+    uint32_t words[JJ][2], next_words[JJ][2];
+    // Activation tile: BM rows of 128 fp16 (256 bytes) per buffer, moved
     // from global memory straight into LDS (global_load_lds_dwordx4: lane l
     // of an instruction writes 16 bytes at the wave's LDS address + 16 l), so
     // the next K step's tile costs no registers while it is in flight. Wave w's
-    // instruction j fills LDS rows 4 (8 w + j) + [0, 4); lane l writes chunk
+    // instruction j fills LDS rows 4 (NJ w + j) + [0, 4); lane l writes chunk
     // position p = l & 15 of row r, which holds the row's 16-byte column chunk
     // p ^ (r & 15): the A-fragment reads (32 rows at one chunk per
     // instruction) then fall on distinct banks. Rows past M read the last
@@ -433,21 +438,23 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
     // Loads are unconditional otherwise: sign tiles past N read a valid tile.
     const int64_t nsc = g.nb, kpad = g.kpad;
     const int64_t a_rows = g.m - m0;  // valid rows of this block (>= 1)
-    // Byte offsets from the block's first row (below 2^31: 128 rows of a
-    // padded K that the host limits), added to a wave-uniform base.
+    // Byte offsets from the block's first row (below 2^31: at most 128 rows
+    // of a padded K that the host limits), added to a wave-uniform base.
     const char* const a_blk = reinterpret_cast<const char*>(g.a + m0 * kpad);
-    uint32_t a_src[8];
+    uint32_t a_src[NJ];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int row = 4 * (8 * wave + j) + (lane >> 4);
+    for (int j = 0; j < NJ; ++j) {
+        const int row = 4 * (NJ * wave + j) + (lane >> 4);
         const int chunk = (lane & 15) ^ (row & 15);
         const int64_t rr = row < a_rows ? row : a_rows - 1;
         a_src[j] = static_cast<uint32_t>((rr * kpad + 8 * chunk) * 2);
     }
-    const int64_t rt_a = rt0 < rt_count ? rt0 : rt_count - 1;
-    const int64_t rt_b = rt0 + 2 < rt_count ? rt0 + 2 : rt_count - 1;
-    const uint32_t* const b0 = g.tiles + rt_a * nsc * 64;
-    const uint32_t* const b1 = g.tiles + rt_b * nsc * 64;
+    const uint32_t* bt[JJ];
+#pragma unroll
+    for (int jj = 0; jj < JJ; ++jj) {
+        const int64_t rt = rt0 + 2 * jj < rt_count ? rt0 + 2 * jj : rt_count - 1;
+        bt[jj] = g.tiles + rt * nsc * 64;
+    }
     const int64_t k_begin = static_cast<int64_t>(slice) * g.k_per_split;
     const int64_t k_end = k_begin + g.k_per_split < nsc ? k_begin + g.k_per_split : nsc;
     // The transfer is issued as inline asm with its LDS address in M0: the
@@ -459,9 +466,9 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
     typedef __attribute__((address_space(3))) void lds_void_t;
     const auto load_a = [&](int64_t sc, int buf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            if (4 * (8 * wave + j) >= a_rows) continue;  // wave-uniform
-            lds_void_t* dst = (lds_void_t*)(lds + buf * kALdsBytes + (8 * wave + j) * 1024);
+        for (int j = 0; j < NJ; ++j) {
+            if (4 * (NJ * wave + j) >= a_rows) continue;  // wave-uniform
+            lds_void_t* dst = (lds_void_t*)(lds + buf * kABytes + (NJ * wave + j) * 1024);
             const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
             const char* src = a_blk + sc * (2 * kBK) + a_src[j];
             // s_nop: one wait state between the M0 write and the LDS transfer.
@@ -473,16 +480,17 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
         const int64_t rem_ = nsc - 4 * c_;
         const int dw_ = static_cast<int>(rem_ < 4 ? rem_ : 4);
         const int64_t off_ = c_ * 256 + (sc & 3);
-        next_words[0][0] = b0[off_ + wl0 * dw_];
-        next_words[0][1] = b0[off_ + wl1 * dw_];
-        next_words[1][0] = b1[off_ + wl0 * dw_];
-        next_words[1][1] = b1[off_ + wl1 * dw_];
+#pragma unroll
+        for (int jj = 0; jj < JJ; ++jj) {
+            next_words[jj][0] = bt[jj][off_ + wl0 * dw_];
+            next_words[jj][1] = bt[jj][off_ + wl1 * dw_];
+        }
     };
     // Byte offset, within a buffer, of the A fragment of 16-column slice m
     // for fragment row 0 (fragment ii adds 32 rows = 8192 bytes).
     int a_off[8];
 #pragma unroll
-    for (int m = 0; m < 8; ++m) a_off[m] = (64 * wm + r) * 256 + 16 * ((2 * m + h) ^ (r & 15));
+    for (int m = 0; m < 8; ++m) a_off[m] = (32 * II * wm + r) * 256 + 16 * ((2 * m + h) ^ (r & 15));
     // Step s computes on buffer s & 1 while the tile of step s + 1 moves into
     // the other; a wait for this wave's transfers and one barrier per step
     // make every wave's part of the next tile visible before it is read.
@@ -491,7 +499,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) words[jj][0] = next_words[jj][0], words[jj][1] = next_words[jj][1];
+    for (int jj = 0; jj < JJ; ++jj) words[jj][0] = next_words[jj][0], words[jj][1] = next_words[jj][1];
     int buf = 0;
     uint32_t sign_mask = 0x80008000u, fp16_one = 0x3C003C00u;
     asm volatile("" : "+v"(sign_mask), "+v"(fp16_one));  // keep them in VGPRs
@@ -503,50 +511,50 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
         // MFMAs; left to itself the scheduler sinks them to the step's end,
         // where the wait before the barrier would take their whole latency.
         __builtin_amdgcn_sched_barrier(0);
-        const char* a_lds = lds + buf * kALdsBytes;
+        const char* a_lds = lds + buf * kABytes;
         // Software pipeline over the eight 16-column slices: slice m's MFMAs
         // issue while slice m + 1's A fragments are read from LDS and its
         // sign fragments expanded, so no MFMA waits on a read issued just
         // before it. Each slice is one scheduling region (sched_barrier) laid
         // out as the reads, then MFMAs alternating with the expansion.
-        v8h a_cur[II], b_cur[2];
+        v8h a_cur[II], b_cur[JJ];
 #pragma unroll
         for (int ii = 0; ii < II; ++ii) a_cur[ii] = *reinterpret_cast<const v8h*>(a_lds + a_off[0] + 8192 * ii);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) b_cur[jj] = expand_signs32(words[jj][0], words[jj][1], 0, sign_mask, fp16_one);
+        for (int jj = 0; jj < JJ; ++jj) b_cur[jj] = expand_signs32(words[jj][0], words[jj][1], 0, sign_mask, fp16_one);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             __builtin_amdgcn_sched_barrier(0);
-            v8h a_nxt[II], b_nxt[2];
+            v8h a_nxt[II], b_nxt[JJ];
             if (m < 7) {
 #pragma unroll
                 for (int ii = 0; ii < II; ++ii)
                     a_nxt[ii] = *reinterpret_cast<const v8h*>(a_lds + a_off[m + 1] + 8192 * ii);
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj)
+                for (int jj = 0; jj < JJ; ++jj)
                     b_nxt[jj] = expand_signs32(words[jj][0], words[jj][1], m + 1, sign_mask, fp16_one);
             }
 #pragma unroll
             for (int ii = 0; ii < II; ++ii)
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj)
+                for (int jj = 0; jj < JJ; ++jj)
                     acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[ii], b_cur[jj], acc[ii][jj], 0, 0, 0);
             if (m < 7) {
                 __builtin_amdgcn_sched_group_barrier(0x100, II, 0);  // LDS reads of slice m + 1
 #pragma unroll
-                for (int q = 0; q < 2 * II; ++q) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA of slice m
-                    __builtin_amdgcn_sched_group_barrier(0x002, 16 / (2 * II), 0);  // expansion of m + 1
+                for (int q = 0; q < II * JJ; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA of slice m
+                    __builtin_amdgcn_sched_group_barrier(0x002, 8 / II, 0);  // expansion of m + 1
                 }
 #pragma unroll
                 for (int ii = 0; ii < II; ++ii) a_cur[ii] = a_nxt[ii];
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj) b_cur[jj] = b_nxt[jj];
+                for (int jj = 0; jj < JJ; ++jj) b_cur[jj] = b_nxt[jj];
             }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) words[jj][0] = next_words[jj][0], words[jj][1] = next_words[jj][1];
+        for (int jj = 0; jj < JJ; ++jj) words[jj][0] = next_words[jj][0], words[jj][1] = next_words[jj][1];
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
         buf ^= 1;
@@ -562,14 +570,16 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
     // One 64-row half of the wave's tile (rows row0 + [0, 64)); `return`
     // leaves only this lambda.
     const auto emit = [&](const int64_t row0) __attribute__((always_inline)) {
-        const int64_t col = n0 + 64 * wn + lane;
+        const int64_t col = n0 + 32 * JJ * wn + lane;
+        const bool lane_ok = lane < 32 * JJ;  // lanes past the wave's columns store nothing
+        const int p_lane = lane_ok ? lane : 0;  // and read a parked column of their own row
         const int rows = __builtin_amdgcn_readfirstlane(static_cast<int>(g.m - row0 < 64 ? g.m - row0 : 64));
         if (rows <= 0) return;  // the whole wave is past the last token
-        const bool col_ok = col < g.n;
+        const bool col_ok = lane_ok && col < g.n;
         if (g.partial) {
             if (!col_ok) return;
             float* dst = g.partial + static_cast<int64_t>(slice) * g.m * g.n;
-            for (int e = 0; e < rows; ++e) dst[(row0 + e) * g.n + col] = park[e * kParkStride + lane];
+            for (int e = 0; e < rows; ++e) dst[(row0 + e) * g.n + col] = park[e * kParkStride + p_lane];
             return;
         }
         // Every lane stays active up to the stores: lane e holds values of row
@@ -586,7 +596,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
         const int64_t salient = g.salient_count;
         float v[64];
 #pragma unroll
-        for (int e = 0; e < 64; ++e) v[e] = park[e * kParkStride + lane] * inv_of(e) * cs + bias;
+        for (int e = 0; e < 64; ++e) v[e] = park[e * kParkStride + p_lane] * inv_of(e) * cs + bias;
         // Salient columns (none for most layers): v[e] for the wave's 64 rows
         // stays in registers while the columns are added in index order, eight at
         // a time. Lane e loads x[row0 + e, idx_k] and the row loop takes it with
@@ -616,7 +626,7 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
             // the padding columns up to out_ld written as zeros (a 256-wide
             // block can reach past out_ld: those lanes store nothing).
             const float os_lane = g.out_scale[row0 + lane_row];
-            const bool in_row = col < g.out_ld;
+            const bool in_row = lane_ok && col < g.out_ld;
             _Float16* o = static_cast<_Float16*>(g.out) + row0 * g.out_ld + swizzle4(in_row ? col : 0);
 #pragma unroll
             for (int e = 0; e < 64; ++e) {
@@ -660,9 +670,9 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
     // out per half rather than as a loop: the accumulators must keep constant
     // register indices, and the compiler does not always unroll a loop around
     // two copies of emit.
-    const auto park_half = [&](const v16f (&a0)[2], const v16f (&a1)[2]) __attribute__((always_inline)) {
+    const auto park_half = [&](const v16f (&a0)[JJ], const v16f (&a1)[JJ]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
+        for (int jj = 0; jj < JJ; ++jj)
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 park[(8 * (q >> 2) + 4 * h + (q & 3)) * kParkStride + 32 * jj + r] = a0[jj][q];
@@ -671,12 +681,12 @@ __global__ __launch_bounds__(kBlock, 2) void k_sign_gemm(const GemmBatch batch) 
     };
     park_half(acc[0], acc[1]);
     __syncthreads();
-    emit(m0 + 64 * wm);
+    emit(m0 + 32 * II * wm);
     if constexpr (II == 4) {
         __syncthreads();  // the first half is read out of the park area
         park_half(acc[2], acc[3]);
         __syncthreads();
-        emit(m0 + 64 * wm + 64);
+        emit(m0 + 32 * II * wm + 64);
     }
 }
 
@@ -801,6 +811,8 @@ int64_t a256(int64_t n) { return (n + 255) & ~int64_t(255); }
 // partials' write and read (M x N x 4 bytes per slice, mostly served by the
 // last-level cache). Slices hold at least kMinSliceBlocks K blocks.
 constexpr int64_t kResident = 512;
+constexpr int64_t kResidentSmall = 1024;  // the 64 x 128 block: four per CU
+constexpr double kStepNsSmall = 500.0;    // half the MFMA and A work of a 128-row step
 constexpr int64_t kMinSliceBlocks = 2;
 constexpr double kStepNs = 1000.0;
 constexpr double kReduceNs = 3000.0;
@@ -810,7 +822,13 @@ struct Split {
     int64_t slices, k_per_split;
 };
 
+// Resident workgroups and K-step cost of the block tile used for `tokens`.
+int64_t resident_for(int64_t tokens) { return tokens <= kBM / 2 ? kResidentSmall : kResident; }
+double step_ns_for(int64_t tokens) { return tokens <= kBM / 2 ? kStepNsSmall : kStepNs; }
+
 Split split_for(int64_t tiles, int64_t k_blocks, int64_t tokens, int64_t n) {
+    const int64_t resident = resident_for(tokens);
+    const double step_ns = step_ns_for(tokens);
     Split best{1, k_blocks};
     double best_ns = -1.0;
     const int64_t most = k_blocks / kMinSliceBlocks > 1 ? k_blocks / kMinSliceBlocks : 1;
@@ -818,8 +836,8 @@ Split split_for(int64_t tiles, int64_t k_blocks, int64_t tokens, int64_t n) {
         Split s;
         s.k_per_split = (k_blocks + want - 1) / want;
         s.slices = (k_blocks + s.k_per_split - 1) / s.k_per_split;
-        const int64_t rounds = (tiles * s.slices + kResident - 1) / kResident;
-        double ns = static_cast<double>(rounds * (s.k_per_split + 1)) * kStepNs;
+        const int64_t rounds = (tiles * s.slices + resident - 1) / resident;
+        double ns = static_cast<double>(rounds * (s.k_per_split + 1)) * step_ns;
         if (s.slices > 1)
             ns += kReduceNs + 2.0 * static_cast<double>(s.slices * tokens * n * 4) / kPartialBytesPerNs;
         if (best_ns < 0.0 || ns < best_ns) best = s, best_ns = ns;
@@ -857,8 +875,8 @@ void batch_splits(int count, const int64_t* tiles, const int64_t* k_blocks, cons
             steps = cand[i].k_per_split > steps ? cand[i].k_per_split : steps;
             if (cand[i].slices > 1) partial_elems += cand[i].slices * tokens * n[i];
         }
-        const int64_t rounds = (wgs + kResident - 1) / kResident;
-        double ns = static_cast<double>(rounds * (steps + 1)) * kStepNs;
+        const int64_t rounds = (wgs + resident_for(tokens) - 1) / resident_for(tokens);
+        double ns = static_cast<double>(rounds * (steps + 1)) * step_ns_for(tokens);
         if (partial_elems > 0) ns += kReduceNs + 2.0 * static_cast<double>(partial_elems * 4) / kPartialBytesPerNs;
         if (best_ns < 0.0 || ns < best_ns) {
             best_ns = ns;
@@ -868,13 +886,14 @@ void batch_splits(int count, const int64_t* tiles, const int64_t* k_blocks, cons
 }
 
 // One launch of a phase's GEMMs (p[i].splits, k_per_split and partial set)
-// and, when any member's K is split, one launch of the reductions. The
-// 128 x 256 block tile (k_sign_gemm<1>) is used when no member is split and
-// the launch still has at least kResident blocks at that size; 128 x 128
-// otherwise.
+// and, when any member's K is split, one launch of the reductions. Up to 64
+// tokens take the 64 x 128 block tile; otherwise the 128 x 256 block tile is
+// used when no member is split and the launch still has at least kResident
+// blocks at that size, and 128 x 128 when not.
 void launch_phase(GemmArgs* p, int count, int64_t tokens, hipStream_t stream) {
     const int64_t mt = (tokens + kBM - 1) / kBM;
-    bool wide = true;
+    const bool small = tokens <= kBM / 2;  // one 64-row block holds every token
+    bool wide = !small;
     int64_t wide_blocks = 0;
     for (int i = 0; i < count; ++i) {
         wide = wide && p[i].splits == 1;
@@ -902,10 +921,12 @@ void launch_phase(GemmArgs* p, int count, int64_t tokens, hipStream_t stream) {
         }
     }
     const dim3 grid(static_cast<unsigned>(x), static_cast<unsigned>(mt));
-    if (wide)
-        hipLaunchKernelGGL(k_sign_gemm<1>, grid, dim3(kBlock), 0, stream, gb);
+    if (small)
+        hipLaunchKernelGGL((k_sign_gemm<1, 2, 1>), grid, dim3(kBlock), 0, stream, gb);
+    else if (wide)
+        hipLaunchKernelGGL((k_sign_gemm<1, 4, 2>), grid, dim3(kBlock), 0, stream, gb);
     else
-        hipLaunchKernelGGL(k_sign_gemm<2>, grid, dim3(kBlock), 0, stream, gb);
+        hipLaunchKernelGGL((k_sign_gemm<2, 2, 2>), grid, dim3(kBlock), 0, stream, gb);
     if (rx > 0) {
         const dim3 rgrid(static_cast<unsigned>(rx), static_cast<unsigned>(tokens < kRowsPerGridZ ? tokens : kRowsPerGridZ),
                          static_cast<unsigned>((tokens + kRowsPerGridZ - 1) / kRowsPerGridZ));
