@@ -345,12 +345,13 @@ def test_prefill_ragged_geometries(tokens, geometry):
     _check_shape(backend, state, tokens, seed=tokens)
 
 
-@pytest.mark.parametrize("geometry", [(1024, 64, 8200, 2), (512, 9000, 300, 0)])
+@pytest.mark.parametrize("geometry", [(1024, 64, 8000, 2), (512, 7990, 300, 0)])
 def test_prefill_wide_blocks(geometry):
-    """GEMMs large enough for the 128 x 256 block tile at M = 2048: a rank of
-    8200 puts it on the first GEMM (whose last block reaches past the padded
-    fp16 intermediate), an output of 9000 rows on the second (a partial last
-    block and partial tile)."""
+    """GEMMs that take the 128 x 256 block tile at M = 2048 (512 such blocks:
+    one resident round, against two of 128 x 128 blocks): a rank of 8000 puts
+    it on the first GEMM (whose last block reaches past the 8064-column padded
+    fp16 intermediate), an output of 7990 rows on the second (a partial last
+    block and a partial 16-row tile)."""
 
     in_f, out_f, rank, k = geometry
     backend = HipPackedBackend()
