@@ -70,6 +70,9 @@ def parse_args(argv=None):
     p.add_argument("--dominant-only", action="store_true",
                    help="only launch the dominant call (gate/up batch) of every layer eagerly --steps times "
                         "(per-dispatch counter collection) and exit")
+    p.add_argument("--stack-mode-only", default="", metavar="MODE",
+                   help="only time the M=1 decode stack in one launch grouping (one of --modes' names) "
+                        "and exit (kernel traces of one mode)")
     return p.parse_args(argv)
 
 
@@ -822,6 +825,15 @@ def dominant_only(args, device) -> int:
     return 0
 
 
+def stack_mode_only(args, device) -> int:
+    backend, stack = build_layers(args.layers, device)
+    fig = time_stack(backend, stack_io(stack, 1, device), args.stack_mode_only, args.steps, args.warmup)
+    print(json.dumps({"mode": args.stack_mode_only, "ms_per_step": fig["ms_per_step"],
+                      "step_bytes": fig["step_bytes"], "achieved_gbs": fig["achieved_gbs"],
+                      "frac_of_hbm_peak": fig["frac_of_hbm_peak"]}))
+    return 0
+
+
 def main(argv=None) -> int:
     args = parse_args(argv)
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -845,6 +857,8 @@ def main(argv=None) -> int:
     torch.cuda.set_device(device)
     if args.dominant_only:
         return dominant_only(args, device)
+    if args.stack_mode_only:
+        return stack_mode_only(args, device)
     wall0 = time.perf_counter()
     result: dict = {}
     c2, dom, backend, _ = (None, None, None, None)
