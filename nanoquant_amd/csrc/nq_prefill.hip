@@ -432,10 +432,10 @@ __global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const Gem
     // instruction j fills LDS rows 4 (NJ w + j) + [0, 4); lane l writes chunk
     // position p = l & 15 of row r, which holds the row's 16-byte column chunk
     // p ^ (r & 15): the A-fragment reads (32 rows at one chunk per
-    // instruction) then fall on distinct banks. Rows past M read the last
-    // valid row; an instruction whose four rows are all past M is skipped
-    // (those rows only feed accumulators whose outputs are never stored).
-    // Loads are unconditional otherwise: sign tiles past N read a valid tile.
+    // instruction) then fall on distinct banks. Every load is unconditional
+    // (no branch in the K loop): rows past M read the last valid row and sign
+    // tiles past N a valid tile; they only feed accumulators whose outputs are
+    // never stored.
     const int64_t nsc = g.nb, kpad = g.kpad;
     const int64_t a_rows = g.m - m0;  // valid rows of this block (>= 1)
     // Byte offsets from the block's first row (below 2^31: at most 128 rows
@@ -465,14 +465,14 @@ __global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const Gem
     // step ends with vmcnt(0) and a barrier before that buffer is read.
     typedef __attribute__((address_space(3))) void lds_void_t;
     const auto load_a = [&](int64_t sc, int buf) __attribute__((always_inline)) {
+        const char* base = a_blk + sc * (2 * kBK);  // wave-uniform: a scalar base, per-lane 32-bit offsets
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
-            if (4 * (NJ * wave + j) >= a_rows) continue;  // wave-uniform
             lds_void_t* dst = (lds_void_t*)(lds + buf * kABytes + (NJ * wave + j) * 1024);
             const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
-            const char* src = a_blk + sc * (2 * kBK) + a_src[j];
             // s_nop: one wait state between the M0 write and the LDS transfer.
-            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds_addr) : "memory");
+            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(a_src[j]), "s"(base), "{m0}"(lds_addr)
+                         : "memory");
         }
     };
     const auto load_words = [&](int64_t sc) __attribute__((always_inline)) {
@@ -504,9 +504,9 @@ __global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const Gem
     uint32_t sign_mask = 0x80008000u, fp16_one = 0x3C003C00u;
     asm volatile("" : "+v"(sign_mask), "+v"(fp16_one));  // keep them in VGPRs
     for (int64_t sc = k_begin; sc < k_end; ++sc) {
-        const bool more = sc + 1 < k_end;
-        if (more) load_a(sc + 1, buf ^ 1);
-        load_words(more ? sc + 1 : sc);
+        const int64_t nxt = sc + 1 < k_end ? sc + 1 : sc;  // the last step reloads its tile into the idle buffer
+        load_a(nxt, buf ^ 1);
+        load_words(nxt);
         // The sign words of the next step are issued here, ahead of the
         // MFMAs; left to itself the scheduler sinks them to the step's end,
         // where the wait before the barrier would take their whole latency.
