@@ -841,6 +841,204 @@ __global__ __launch_bounds__(kMfmaHeads * kWave) void k_decode_attention_mfma(
 }
 
 // ---------------------------------------------------------------------------
+// Prompt attention, pass 1 on MFMA (head_dim 128, four q heads per kv head,
+// 16-bit cache): workgroup (kv head g, tile of kPromptTile tokens, 64-row
+// cache block s); wave w computes q head 4g + w for the tile's tokens, the
+// same partial (m, l, acc) per (token, q head, block) as k_attention_blocks,
+// so k_attention_merge combines them unchanged.
+//   Scores S = Q K^T on v_mfma_f32_16x16x32 (bf16 / f16, the cache's type):
+//   A = the query rows (token i of the tile = row i), read from global memory
+//   and split into three 16-bit parts in registers (the rounding of q, of its
+//   remainder and of the remainder's remainder), all three accumulated into
+//   the same tile, so the product carries about 24 bits of the fp32 query; B =
+//   the block's K rows from LDS (exact). Four column tiles of 16 cache rows.
+//   Causal softmax per query row over the block (rows past the token's
+//   position weigh zero); the weights, split into three parts the same way,
+//   go through LDS into the A layout; O = P V with B = V staged transposed in
+//   LDS (one 16-byte read per lane), eight tiles of 16 dimensions.
+// Results differ from k_attention_blocks only by rounding.
+constexpr int kPromptTile = 16;                  // tokens per workgroup (A rows)
+constexpr int kPromptVStride = kSeqBlock + 8;    // halfs per transposed V row and per P row
+
+template <int CT>
+constexpr size_t prompt_attention_mfma_lds() {
+    // K block [64][row], V transposed [128][64 + 8], weight parts [3][4 waves][16][64 + 8].
+    return static_cast<size_t>(kSeqBlock) * k_row_bytes<128, CT>() + 128 * kPromptVStride * 2 +
+           3 * kMfmaHeads * kPromptTile * kPromptVStride * 2;
+}
+
+template <int CT>
+__global__ __launch_bounds__(kMfmaHeads * kWave) void k_prompt_attention_mfma(
+    const float* __restrict__ q, const char* __restrict__ k_cache, const char* __restrict__ v_cache, int64_t tokens,
+    int kv_heads, const int32_t* __restrict__ position, int64_t max_positions, float scaling,
+    float* __restrict__ part_ml, float* __restrict__ part_acc) {
+    constexpr int D = 128;
+    constexpr int G = kMfmaHeads;
+    constexpr int T = kPromptTile;
+    constexpr int RB = k_row_bytes<D, CT>();  // padded K row in LDS
+    constexpr int VRB = D * 2;                // row in the cache
+    constexpr int PIECES = VRB / 16;
+    constexpr int VS = kPromptVStride;
+    typedef typename Mfma16<CT>::v8 v8;
+    extern __shared__ float lds_raw[];
+    char* klds = reinterpret_cast<char*>(lds_raw);
+    uint16_t* vt = reinterpret_cast<uint16_t*>(klds + kSeqBlock * RB);  // [D][VS]
+    uint16_t* ps = vt + D * VS;                                         // [3][G][T][VS]
+
+    const int q_heads = kv_heads * G;
+    const int g = static_cast<int>(blockIdx.x) % kv_heads;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x / kv_heads) * T;
+    const int s = blockIdx.y;
+    const int blocks = gridDim.y;
+    const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t p0 = position[0];
+    const int64_t row0 = static_cast<int64_t>(s) * kSeqBlock;
+    const int64_t t_end = t0 + T < tokens ? t0 + T : tokens;
+    // Highest cache row any query of this workgroup may see.
+    int64_t last = p0 + t_end - 1;
+    if (last >= max_positions) last = max_positions - 1;
+    if (p0 < 0 || row0 > last) return;  // uniform: no query of this workgroup reaches row0
+    const int rows = static_cast<int>((last - row0 + 1) < kSeqBlock ? (last - row0 + 1) : kSeqBlock);
+
+    // Query operands: lane (kg, n) holds token row n, dimensions 32 st + 8 kg + [0, 8).
+    const int n = lane & 15, kg = lane >> 4;
+    const int h = g * G + w;
+    const int64_t tq = t0 + n < tokens ? t0 + n : tokens - 1;  // rows past the last token reuse it (not stored)
+    float qf[4][8];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const float4* src = reinterpret_cast<const float4*>(q + (tq * q_heads + h) * D + 32 * st + 8 * kg);
+        const float4 x0 = src[0], x1 = src[1];
+        qf[st][0] = x0.x; qf[st][1] = x0.y; qf[st][2] = x0.z; qf[st][3] = x0.w;
+        qf[st][4] = x1.x; qf[st][5] = x1.y; qf[st][6] = x1.z; qf[st][7] = x1.w;
+    }
+    // K rows [row0, row0 + rows) to LDS as stored, V transposed; rows past
+    // `rows` are zero (their weights are zero, and 0 * V must stay 0).
+    const int64_t head_row0 = static_cast<int64_t>(g) * max_positions + row0;
+    const char* kbase = k_cache + head_row0 * VRB;
+    const char* vbase = v_cache + head_row0 * VRB;
+    constexpr int PER_THREAD = kSeqBlock * PIECES / (G * kWave);
+    u32x4 kp[PER_THREAD], vp[PER_THREAD];
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int idx = static_cast<int>(threadIdx.x) + i * G * kWave;
+        const int r = idx % kSeqBlock, c = idx / kSeqBlock;
+        const int rr = r < rows ? r : rows - 1;
+        kp[i] = *reinterpret_cast<const u32x4*>(kbase + static_cast<int64_t>(rr) * VRB + 16 * c);
+        vp[i] = *reinterpret_cast<const u32x4*>(vbase + static_cast<int64_t>(rr) * VRB + 16 * c);
+    }
+#pragma unroll
+    for (int i = 0; i < PER_THREAD; ++i) {
+        const int idx = static_cast<int>(threadIdx.x) + i * G * kWave;
+        const int r = idx % kSeqBlock, c = idx / kSeqBlock;
+        const bool keep = r < rows;
+        const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(klds + r * RB + 16 * c) = keep ? kp[i] : zero;
+        const u32x4 vv = keep ? vp[i] : zero;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            vt[(8 * c + e) * VS + r] = static_cast<uint16_t>((vv[e >> 1] >> (16 * (e & 1))) & 0xffffu);
+    }
+    v8 qa[3][4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        union {
+            uint16_t h[8];
+            v8 v;
+        } part[3];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            uint16_t hh[3];
+            split3<CT>(qf[st][e], hh);
+#pragma unroll
+            for (int pp = 0; pp < 3; ++pp) part[pp].h[e] = hh[pp];
+        }
+#pragma unroll
+        for (int pp = 0; pp < 3; ++pp) qa[pp][st] = part[pp].v;
+    }
+    __syncthreads();
+
+    // Scores: sc[ct][j] = S[token row 4 kg + j][cache row 16 ct + n].
+    v4f_t sc[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+        sc[ct] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const v8 b = *reinterpret_cast<const v8*>(klds + (16 * ct + n) * RB + 2 * (32 * st + 8 * kg));
+#pragma unroll
+            for (int pp = 0; pp < 3; ++pp) sc[ct] = mfma16<CT>(qa[pp][st], b, sc[ct]);
+        }
+    }
+    // Causal softmax per token row over this block.
+    float mrow[4], lrow[4];
+    uint16_t* pw = ps + w * T * VS;  // this wave's [T][VS] for part 0; parts are G * T * VS apart
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = 4 * kg + j;  // token row of the tile
+        const int64_t pt = p0 + t0 + i;
+        float sv[4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const int cr = 16 * ct + n;
+            const bool valid = cr < rows && row0 + cr <= pt;
+            sv[ct] = valid ? sc[ct][j] * scaling : -INFINITY;
+            mx = fmaxf(mx, sv[ct]);
+        }
+        const float m = row16_max(mx);
+        const float msafe = m == -INFINITY ? 0.0f : m;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const float pv = sv[ct] == -INFINITY ? 0.0f : expf(sv[ct] - msafe);
+            lsum += pv;
+            uint16_t hh[3];
+            split3<CT>(pv, hh);
+#pragma unroll
+            for (int pp = 0; pp < 3; ++pp) pw[pp * G * T * VS + i * VS + 16 * ct + n] = hh[pp];
+        }
+        mrow[j] = m;
+        lrow[j] = row16_sum(lsum);
+    }
+    __syncthreads();
+
+    // O = P V: o[dt][j] = O[token row 4 kg + j][dimension 16 dt + n].
+    v4f_t o[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) o[dt] = v4f_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int kst = 0; kst < kSeqBlock / 32; ++kst) {
+        v8 pa[3];
+#pragma unroll
+        for (int pp = 0; pp < 3; ++pp)
+            pa[pp] = *reinterpret_cast<const v8*>(pw + pp * G * T * VS + n * VS + 32 * kst + 8 * kg);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const v8 b = *reinterpret_cast<const v8*>(vt + (16 * dt + n) * VS + 32 * kst + 8 * kg);
+#pragma unroll
+            for (int pp = 0; pp < 3; ++pp) o[dt] = mfma16<CT>(pa[pp], b, o[dt]);
+        }
+    }
+    // Partials of the tokens that reach this block (the merge reads block s of
+    // token t only when row0 <= position + t).
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t t = t0 + 4 * kg + j;
+        const int64_t pt = p0 + t;
+        if (t >= tokens || pt < row0 || pt >= max_positions) continue;
+        const int64_t pi = attn_part_index(t, h, s, q_heads, blocks);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) part_acc[pi * D + 16 * dt + n] = o[dt][j];
+        if (n == 0) {
+            part_ml[2 * pi] = mrow[j];
+            part_ml[2 * pi + 1] = lrow[j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // One-token decode attention with the q/k RMSNorm + RoPE + KV append fused in
 // (pass 1; k_attention_merge is pass 2). Workgroup (kv head g, 64-row cache
 // block s), one wave per q head of the group:
@@ -1195,8 +1393,23 @@ int launch_attention(const float* q, const void* kc, const void* vc, int64_t tok
                      const int32_t* position, int64_t max_positions, float scaling, void* out, int odt, float* ml,
                      float* acc, hipStream_t st) {
     const int group = q_heads / kv_heads;
-    const int qt = tokens == 1 ? 1 : 16;
     const int blocks = attention_blocks(max_positions);
+    if constexpr (D == 128 && CT != NQ_DTYPE_F32) {
+        if (group == kMfmaHeads && tokens > 1) {
+            const int64_t qblocks = (tokens + kPromptTile - 1) / kPromptTile;
+            if (qblocks * kv_heads > 0x7fffffff) return NQ_ERR_SHAPE;
+            dim3 grid(static_cast<unsigned>(qblocks * kv_heads), static_cast<unsigned>(blocks));
+            hipLaunchKernelGGL((k_prompt_attention_mfma<CT>), grid, dim3(kMfmaHeads * kWave),
+                               prompt_attention_mfma_lds<CT>(), st, q, static_cast<const char*>(kc),
+                               static_cast<const char*>(vc), tokens, kv_heads, position, max_positions, scaling, ml,
+                               acc);
+            if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+            hipLaunchKernelGGL(k_attention_merge<D>, dim3(q_heads, static_cast<unsigned>(tokens)), dim3(D), 0, st, ml,
+                               acc, q_heads, blocks, kSeqBlock, position, max_positions, out, odt);
+            return nq::launch_status();
+        }
+    }
+    const int qt = tokens == 1 ? 1 : 16;
     const int64_t qblocks = (tokens + qt - 1) / qt;
     const size_t lds = attention_lds<D, CT>(group);
     if (lds > 64 * 1024) return NQ_ERR_UNSUPPORTED;

@@ -127,6 +127,14 @@ def reference_attention(q, kc, vc, start, scaling):
         (37, 5, 32, 8, 128, torch.bfloat16),
         (512, 0, 32, 8, 128, torch.bfloat16),
         (100, 27, 8, 1, 64, torch.float32),
+        # MFMA prompt path (head_dim 128, four q heads per kv head, 16-bit cache):
+        # tile edges, the last cache rows, f16, other kv head counts
+        (16, 0, 32, 8, 128, torch.bfloat16),
+        (17, 63, 32, 8, 128, torch.bfloat16),
+        (2, 638, 32, 8, 128, torch.bfloat16),
+        (40, 600, 32, 8, 128, torch.float16),
+        (33, 100, 16, 4, 128, torch.bfloat16),
+        (70, 9, 8, 2, 128, torch.float16),
     ],
 )
 def test_attention(tokens, start, q_heads, kv_heads, head_dim, cache_dtype):
