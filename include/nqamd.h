@@ -250,8 +250,15 @@ typedef enum nq_input_kind {
     NQ_INPUT_RMSNORM = 1,   /* x is an fp32 residual h [in]; member i sees RMSNorm(h) * w
                                through col_scales[i] = w * s_in (fp32 [in], replacing
                                its s_in) and 1 / RMS(h) from norm_slots               */
-    NQ_INPUT_SILU_GATE = 2  /* x is the fp32 gate g [in], ups[i] the fp32 up u [in];
+    NQ_INPUT_SILU_GATE = 2, /* x is the fp32 gate g [in], ups[i] the fp32 up u [in];
                                member i sees silu(g) * u                              */
+    NQ_INPUT_ATTENTION = 3  /* x is the workspace of nq_decode_attention_partials
+                               (include/nqamd_shell.h) for a cache of
+                               attn_max_positions rows (at most 1024); input column k
+                               is dimension k % attn_head_dim of head k / attn_head_dim
+                               of the attention output, merged from the partials of
+                               the blocks up to *attn_position; in_features = heads *
+                               attn_head_dim <= 4096, heads * blocks even          */
 } nq_input_kind;
 
 /* Output forms of a fused one-token decode call (nq_linear_batch_fused). */
@@ -277,14 +284,18 @@ typedef struct nq_decode_fusion {
     float* const* out_slots;         /* with residuals: [count] fp32 [ceil(out / 16)]
                                         sums of the new residual's squares per tile     */
     int32_t output_kind;             /* nq_output_kind                                  */
+    const int32_t* attn_position;    /* ATTENTION: the token's cache row (device)       */
+    int32_t attn_head_dim;           /* ATTENTION: 64, 128 or 256                       */
+    int64_t attn_max_positions;      /* ATTENTION: rows of the cache                    */
 } nq_decode_fusion;
 
 /* One launch pair for `count` (1..8) packed linears of ONE token with the
  * decoder's neighbouring element-wise work fused in: the input RMSNorm (the
  * factor 1 / RMS(h) is applied to the rank intermediate, the weight is folded
- * into the column scale) or the SiLU-gated product, and the residual add of
+ * into the column scale), the SiLU-gated product or the merge of the decode
+ * attention's partial results (the attention's second pass), and the residual add of
  * the output with the per-tile sums of squares the next RMSNorm input needs.
- * x is fp32 for the RMSNORM and SILU_GATE inputs; scales fp16; ys[i] may be
+ * x_dtype is F32 for every input but PLAIN; scales fp16; ys[i] may be
  * NULL with residuals; no patch or row sidecar, and no salient columns with a
  * non-plain input. Workspaces as for nq_linear_batch with tokens = 1.
  * No reference counterpart: the reference decoder runs the norms,

@@ -85,12 +85,11 @@ int64_t nq_decode_attention_workspace_bytes(int32_t q_heads, int32_t kv_heads, i
                                             int32_t cache_dtype, int64_t max_positions);
 
 /* One decode token: nq_qk_norm_rope_cache followed by nq_attention with
- * tokens == 1, as one kernel per layer when head_dim * cache element bytes
- * <= 256 and q_heads / kv_heads is 1, 2, 4 or 8 (one workgroup per kv head
- * and 1024-row cache range rotates its q heads, appends k/v at row
- * position[0] when the range holds it, and attends over the range; ranges
- * beyond the first are merged by a second kernel), otherwise as the two
- * calls. q, k, v are the fp32 projection outputs [q_heads * head_dim],
+ * tokens == 1, as two kernels per layer when head_dim * cache element bytes
+ * <= 256 and q_heads / kv_heads is 1, 2, 4 or 8 (pass 1: one workgroup per kv
+ * head and 64-row cache block rotates its q heads, appends k/v at row
+ * position[0] when the block holds it, and attends over the block; pass 2
+ * merges the blocks' partial results), otherwise as the two calls. q, k, v are the fp32 projection outputs [q_heads * head_dim],
  * [kv_heads * head_dim] x2; out [q_heads * head_dim]. Replaces the pinned
  * one-token rope / cache update / attention sequence of the reference
  * (src/nanoquant/runtime/cuda_kernels.py:401-544,715-815). */
@@ -100,6 +99,22 @@ int nq_decode_attention(const float* q, const float* k, const float* v, int32_t 
                         int64_t max_positions, void* k_cache, void* v_cache, int32_t cache_dtype,
                         float scaling, void* out, int32_t out_dtype, void* workspace,
                         int64_t workspace_bytes, void* stream);
+
+/* Pass 1 of nq_decode_attention alone (the same arguments without the output;
+ * the same workspace size): the partial results of every 64-row cache block
+ * up to position[0] stay in the workspace, as fp32 (max, sum) pairs
+ * [q_heads][blocks][2] followed by the accumulators [q_heads][blocks][head_dim],
+ * blocks = ceil(max_positions / 64), for a projection whose input merges them
+ * (nq_linear_batch_fused with NQ_INPUT_ATTENTION). Only the one-pass form:
+ * head_dim * cache element bytes <= 256 and q_heads / kv_heads 1, 2, 4 or 8,
+ * otherwise NQ_ERR_UNSUPPORTED. No reference counterpart: the reference's
+ * attention returns its output (src/nanoquant/runtime/cuda_kernels.py:715-815). */
+int nq_decode_attention_partials(const float* q, const float* k, const float* v, int32_t q_heads,
+                                 int32_t kv_heads, int32_t head_dim, const void* q_norm, const void* k_norm,
+                                 int32_t norm_dtype, float eps, const float* cos_table, const float* sin_table,
+                                 const int32_t* position, int64_t max_positions, void* k_cache, void* v_cache,
+                                 int32_t cache_dtype, float scaling, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
 
 /* out[i] = silu(gate[i]) * up[i], gate and up fp32, out F32/F16/BF16,
  * n % 8 == 0. Replaces the activation of Qwen3MLP.forward. */

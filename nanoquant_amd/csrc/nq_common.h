@@ -51,6 +51,11 @@ __device__ __forceinline__ void store_f32_as(void* __restrict__ p, int dtype, in
 
 __host__ __device__ constexpr int64_t words_for(int64_t cols) { return (cols + 31) / 32; }
 
+// Cache rows per block of the one-token decode attention's pass 1: the grain of
+// its partial (max, sum, acc) results, which the merge and the O projection's
+// attention input kind read.
+constexpr int kAttnBlockRows = 64;
+
 inline bool is_float_dtype(int d) {
     return d == NQ_DTYPE_F32 || d == NQ_DTYPE_F16 || d == NQ_DTYPE_BF16;
 }

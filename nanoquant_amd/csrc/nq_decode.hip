@@ -207,10 +207,15 @@ int enqueue_stage1(const Batch& batch, const LaunchShape& s, hipStream_t stream)
         case kActF16: return enqueue_stage1_f16(batch, s, stream);
         case kActF32: return enqueue_stage1_f32(batch, s, stream);
         case kActNormF32:
-        case kActGatedF32: return enqueue_stage1_fused(batch, s, stream);
+        case kActGatedF32:
+        case kActAttn8:
+        case kActAttn16: return enqueue_stage1_fused(batch, s, stream);
         default: return enqueue_stage1_generic(batch, s, stream);
     }
 }
+
+// Cache blocks of the decode attention's pass 1 for a cache of max_positions rows.
+int64_t attn_blocks_of(int64_t max_positions) { return (max_positions + kAttnBlockRows - 1) / kAttnBlockRows; }
 
 // Fill member i's fusion fields; NQ_OK or an error status.
 int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, LinArgs& a) {
@@ -230,6 +235,23 @@ int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, L
         if (!f.ups || !f.ups[i]) return NQ_ERR_ARGUMENT;
         if (!aligned(f.ups[i], 16)) return NQ_ERR_ALIGNMENT;
         a.x2 = f.ups[i];
+    } else if (f.input_kind == NQ_INPUT_ATTENTION) {
+        // x (already in a.x) is the pass-1 workspace: (max, sum) pairs
+        // [heads][blocks][2], then the accumulators [heads][blocks][head_dim].
+        const int hd = f.attn_head_dim;
+        if (!f.attn_position || (hd != 64 && hd != 128 && hd != 256)) return NQ_ERR_ARGUMENT;
+        if (in % hd != 0 || f.attn_max_positions <= 0 || f.attn_max_positions > 0x7fffffff) return NQ_ERR_SHAPE;
+        const int64_t blocks = attn_blocks_of(f.attn_max_positions);
+        // One chunk per wave and at most eight waves; every block's partials in registers.
+        if (in > 8 * kChunkCols || blocks > attn_parts<kActAttn16>()) return NQ_ERR_UNSUPPORTED;
+        const int64_t heads = in / hd;
+        if ((heads * blocks) % 2 != 0 || !aligned(a.x, 16)) return NQ_ERR_ALIGNMENT;  // 16-byte accumulator rows
+        a.attn_ml = static_cast<const float*>(a.x);
+        a.x = static_cast<const float*>(a.x) + 2 * heads * blocks;
+        a.attn_pos = f.attn_position;
+        a.attn_blocks = static_cast<int>(blocks);
+        a.attn_hd_log2 = hd == 64 ? 6 : (hd == 128 ? 7 : 8);
+        a.attn_max_positions = f.attn_max_positions;
     } else if (f.input_kind != NQ_INPUT_PLAIN) {
         return NQ_ERR_ARGUMENT;
     }
@@ -391,7 +413,10 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
         if (fusion->input_kind != NQ_INPUT_PLAIN) {
             if (x_dtype != NQ_DTYPE_F32) return NQ_ERR_DTYPE;
             if (!vector_ok) return NQ_ERR_ALIGNMENT;
-            ak = fusion->input_kind == NQ_INPUT_RMSNORM ? kActNormF32 : kActGatedF32;
+            if (fusion->input_kind == NQ_INPUT_ATTENTION)
+                ak = attn_blocks_of(fusion->attn_max_positions) <= attn_parts<kActAttn8>() ? kActAttn8 : kActAttn16;
+            else
+                ak = fusion->input_kind == NQ_INPUT_RMSNORM ? kActNormF32 : kActGatedF32;
         }
     }
     return launch_batch(batch, tokens, ak, descs[0]->decode_launch == NQ_DECODE_FUSED, stream, pair);

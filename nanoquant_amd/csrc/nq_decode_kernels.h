@@ -201,6 +201,14 @@ struct LinArgs {
     float* slots_out;        // stage 2: sum of residual^2 per 16-row output tile
     int nslots;              // entries of slots_in
     float eps;               // normed input: RMSNorm epsilon
+    // Attention input (one token): x is the fp32 partial accumulators of the
+    // decode attention's pass 1, [heads][attn_blocks][head_dim] with heads =
+    // in / head_dim, and attn_ml their (max, sum) pairs [heads][attn_blocks][2].
+    const float* attn_ml;
+    const int32_t* attn_pos;    // the token's cache position
+    int attn_blocks;            // cache blocks of kAttnBlockRows rows
+    int attn_hd_log2;           // log2(head_dim)
+    int64_t attn_max_positions;
 };
 static_assert(sizeof(LinArgs) % 16 == 0, "LinArgs is read as 16-byte vectors");
 
@@ -277,6 +285,11 @@ __device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
     a.slots_out = s.slots_out;
     a.nslots = s.nslots;
     a.eps = s.eps;
+    a.attn_ml = s.attn_ml;
+    a.attn_pos = s.attn_pos;
+    a.attn_blocks = s.attn_blocks;
+    a.attn_hd_log2 = s.attn_hd_log2;
+    a.attn_max_positions = s.attn_max_positions;
     // One statement, so every field is waited for at the same point; it
     // redefines the integer fields, so no arithmetic on them can be hoisted
     // above it (the pointers are only read, so they stay known-global).
@@ -296,7 +309,18 @@ enum : int {
     kActGeneric = 3,   // any float x and s_in, element loads
     kActNormF32 = 4,   // fp32 x (a residual), fp32 col_scale (norm weight * s_in), RMS factor from slots_in
     kActGatedF32 = 5,  // silu(x) * x2 from fp32 gate x and up x2, fp16 s_in
+    kActAttn8 = 6,     // attention output merged from fp32 pass-1 partials of up to 8 cache blocks, fp16 s_in
+    kActAttn16 = 7,    // the same for up to 16 cache blocks
 };
+
+template <int AK>
+constexpr bool attn_kind() { return AK == kActAttn8 || AK == kActAttn16; }
+
+// Cache blocks whose partials one lane loads (the attention kinds).
+template <int AK>
+constexpr int attn_parts() { return AK == kActAttn16 ? 16 : 8; }
+
+using nq::kAttnBlockRows;
 
 // Column-scale dtype of a vector kind.
 template <int AK>
@@ -503,12 +527,35 @@ __device__ __forceinline__ int stage_col0(int c, int lane) {
 
 // Registers one stage-1 wave holds for one chunk: the activation runs of every
 // token, the s_in runs and the sign words of its TW tiles.
+// Attention kinds: a lane's partials for its eight columns (one head, eight
+// dimensions): acc of every cache block (two runs of four), the block's
+// (max, sum) pair, and the token's position.
+template <int NB>
+struct AttnParts {
+    v4u acc[NB][2];
+    v2u ml[NB];
+    int pos;
+};
+template <int AK>
+struct AttnRegsOf {
+    struct type {};
+};
+template <>
+struct AttnRegsOf<kActAttn8> {
+    using type = AttnParts<8>;
+};
+template <>
+struct AttnRegsOf<kActAttn16> {
+    using type = AttnParts<16>;
+};
+
 template <int AK, int TOK, int TW>
 struct S1Regs {
     Run<AK> x[TOK][2];
     Run<AK> x2[AK == kActGatedF32 ? TOK : 1][2];  // gated kind: up
     Run<AK> s[2];
     v4u w[TW];
+    typename AttnRegsOf<AK>::type at;
 };
 
 // Registers one stage-2 wave holds for one chunk: its A operands (8 per token
@@ -544,6 +591,30 @@ __device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const LinAr
     constexpr int DT = act_dtype<AK>();
     const int k0 = stage_col0(c, lane);
     const int in = static_cast<int>(a.in);
+    if constexpr (attn_kind<AK>()) {
+        // Every block's partials, issued before the position is known (the
+        // merge skips blocks past it); slots past the cache's blocks are not
+        // loaded. in is a multiple of 8 and of the head dimension.
+        constexpr int NB = attn_parts<AK>();
+        const int kk = k0 < in ? k0 : in - 8;
+        const int hd = a.attn_hd_log2;
+        const int blocks = a.attn_blocks;
+        const int64_t head = kk >> hd;
+        const float* acc = static_cast<const float*>(a.x) + ((head * blocks) << hd) + (kk & ((1 << hd) - 1));
+        const float* ml = a.attn_ml + head * blocks * 2;
+#pragma unroll
+        for (int s = 0; s < NB; ++s) {
+            if (s < blocks) {  // uniform
+                const float* p = acc + (static_cast<int64_t>(s) << hd);
+                r.at.acc[s][0] = *reinterpret_cast<const v4u*>(p);
+                r.at.acc[s][1] = *reinterpret_cast<const v4u*>(p + 4);
+                r.at.ml[s] = *reinterpret_cast<const v2u*>(ml + 2 * s);
+            }
+        }
+        r.at.pos = a.attn_pos[0];
+        load_runs<AK, NQ_DTYPE_F16>(r.s, a.s_in, a.scale_dtype, 0, 1, 0, k0, in);
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < TOK; ++t) load_runs<AK, DT>(r.x[t], a.x, a.x_dtype, t, a.tokens, in, k0, in);
     if constexpr (AK == kActGatedF32) {
@@ -666,6 +737,53 @@ __device__ __forceinline__ void gate_values(const S1Regs<AK, TOK, TW>& r, int t,
     }
 }
 
+// Attention kinds: the lane's eight columns of the attention output, merged
+// from the partials of the cache blocks up to the token's position, the order
+// of k_attention_merge's one round: M = max m_s, then sum_s acc_s e^(m_s - M)
+// over sum_s l_s e^(m_s - M). Blocks past the position are selected out (their
+// slots may hold anything); a position outside the cache gives zeros.
+template <int AK, int TOK, int TW>
+__device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, float (&mv)[2][4]) {
+    constexpr int NB = attn_parts<AK>();
+    const int64_t pos = r.at.pos;
+    const bool in_range = pos >= 0 && pos < a.attn_max_positions;  // uniform
+    const int nb = in_range ? static_cast<int>(pos / kAttnBlockRows) + 1 : 1;
+    float m = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NB; ++s) m = s < nb ? fmaxf(m, __uint_as_float(r.at.ml[s].x)) : m;
+    float l = 0.0f, acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NB; ++s) {
+        if (s < nb) {  // a select: slots past the position may hold anything
+            const float f = expf(__uint_as_float(r.at.ml[s].x) - m);
+            l = fmaf(__uint_as_float(r.at.ml[s].y), f, l);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[i] = fmaf(__uint_as_float(r.at.acc[s][0][i]), f, acc[i]);
+                acc[4 + i] = fmaf(__uint_as_float(r.at.acc[s][1][i]), f, acc[4 + i]);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mv[i >> 2][i & 3] = in_range ? acc[i] / l : 0.0f;
+}
+
+// One run's values of token t: the activations as read (with the gated kind's
+// product), or the attention kinds' merged values.
+template <int AK, int TOK, int TW>
+__device__ __forceinline__ void act_run(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int t, int run,
+                                        const float (&mv)[2][4], float (&v)[4]) {
+    if constexpr (attn_kind<AK>()) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = mv[run][i];
+    } else {
+        run_values<AK, act_dtype<AK>()>(r.x[t][run], a.x_dtype, v);
+        gate_values<AK, TOK, TW>(r, t, run, v);
+    }
+}
+
 // Bits that are set in the fma word of a non-finite staged value and clear in
 // every finite one (finite words have the top byte 0x4B, see stage_block).
 constexpr uint32_t kNonFiniteBits = 0x34000000u;
@@ -691,7 +809,6 @@ constexpr int kPoisonExp = 0x7fffffff;
 template <int AK, int TOK, int TW, int TPB>
 __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int c, int t_base,
                                             char* __restrict__ ops, int lane, int (&expo)[TPB], float (&cmax)[TPB]) {
-    constexpr int DT = act_dtype<AK>();
     const int m = lane >> 3, d = (lane >> 1) & 3, h = lane & 1;
     const int k0 = stage_col0(c, lane);
     const int in = static_cast<int>(a.in);
@@ -702,6 +819,8 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
     float sc[2][4];
     run_values<AK, col_scale_dtype<AK>()>(r.s[0], a.scale_dtype, sc[0]);
     run_values<AK, col_scale_dtype<AK>()>(r.s[1], a.scale_dtype, sc[1]);
+    float mv[2][4];  // attention kinds: the merged values (one token)
+    if constexpr (attn_kind<AK>()) attn_merge<AK, TOK, TW>(r, a, mv);
 #pragma unroll
     for (int u = 0; u < TPB; ++u) {
         const int t = t_base + u;
@@ -710,8 +829,7 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
         if (full_chunk && t < a.tokens) {  // uniform: every value is inside
 #pragma unroll
             for (int run = 0; run < 2; ++run) {
-                run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
-                gate_values<AK, TOK, TW>(r, t, run, v[run]);
+                act_run<AK, TOK, TW>(r, a, t, run, mv, v[run]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     v[run][i] *= sc[run][i];
@@ -721,8 +839,7 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
         } else {
 #pragma unroll
             for (int run = 0; run < 2; ++run) {
-                run_values<AK, DT>(r.x[t][run], a.x_dtype, v[run]);
-                gate_values<AK, TOK, TW>(r, t, run, v[run]);
+                act_run<AK, TOK, TW>(r, a, t, run, mv, v[run]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const bool ok = t < a.tokens && 4 * run + i < lim;
@@ -1163,6 +1280,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     const int fr0 = (t0 + f.tt) * kTileRows + f.n;
     const int fr = fr0 < out ? fr0 : out - 1;
     RawElem rs0, bias0, rs1;
+    float res0 = 0.0f;   // residual epilogue: residual[fr], loaded with the first pass
     bool stale = false;  // fused launch: the wait for stage 1 gave up
     // First-pass salient loads: weights i = threadIdx.x + n * nthreads of the
     // workgroup's block, and for threadIdx.x < tokens * ks one gathered x and scale.
@@ -1201,6 +1319,9 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
             rs0 = load_elem(a.s_out, a.scale_dtype, fr);
             // No branch on the optional bias: without one, s_out is loaded instead and ignored.
             bias0 = load_elem(a.bias ? a.bias : a.s_out, a.bias ? a.bias_dtype : a.scale_dtype, fr);
+            // Only this workgroup writes these rows, so the value read now is the
+            // one the epilogue adds to (in the fused launch, read after the wait).
+            if (TPB == 1 && a.residual != nullptr) res0 = a.residual[fr];
             if (sal_lds) {  // uniform
 #pragma unroll
                 for (int n = 0; n < kSalLoads; ++n) {
@@ -1335,7 +1456,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
             const bool ok = idx < outs && t0 + o.tt < nt && row < out;
             float sq = 0.0f;
             if (ok) {
-                const float h = a.residual[row] + value(idx, o, row);
+                const float h = res0 + value(idx, o, row);  // row == fr here
                 a.residual[row] = h;
                 sq = h * h;
             }

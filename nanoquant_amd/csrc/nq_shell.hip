@@ -19,7 +19,7 @@ using nq::f32_to_bf16_bits;
 
 constexpr int kWave = 64;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-constexpr int kSeqBlock = 64;           // cache rows per attention block
+constexpr int kSeqBlock = nq::kAttnBlockRows;  // cache rows per attention block
 constexpr int kRowThreads = 256;        // per-row kernels
 constexpr int kProjWaves = 4;           // output projection: waves per workgroup
 constexpr int kProjLoads = 32;          // 16-byte weight loads per lane in flight
@@ -1454,7 +1454,7 @@ template <int D, int CT, int G>
 int launch_decode_attention_g(const float* q, const float* k, const float* v, int kv_heads, const void* qn,
                               const void* kn, int ndt, float eps, const float* cs, const float* sn,
                               const int32_t* position, int64_t max_positions, void* kc, void* vc, float scaling,
-                              void* out, int odt, float* ml, float* acc, hipStream_t st) {
+                              void* out, int odt, float* ml, float* acc, bool merge, hipStream_t st) {
     const int blocks = attention_blocks(max_positions);
     if constexpr (D == 128 && G == kMfmaHeads && CT != NQ_DTYPE_F32) {
         hipLaunchKernelGGL((k_decode_attention_mfma<CT>), dim3(kv_heads, blocks), dim3(G * kWave),
@@ -1468,6 +1468,7 @@ int launch_decode_attention_g(const float* q, const float* k, const float* v, in
                            static_cast<char*>(vc), scaling, ml, acc);
     }
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
+    if (!merge) return NQ_OK;  // the partials stay in the workspace
     hipLaunchKernelGGL(k_attention_merge<D>, dim3(kv_heads * G, 1), dim3(D), 0, st, ml, acc, kv_heads * G, blocks,
                        kSeqBlock, position, max_positions, out, odt);
     return nq::launch_status();
@@ -1477,10 +1478,10 @@ template <int D, int CT>
 int launch_decode_attention_ct(int group, const float* q, const float* k, const float* v, int kv_heads, const void* qn,
                                const void* kn, int ndt, float eps, const float* cs, const float* sn,
                                const int32_t* position, int64_t max_positions, void* kc, void* vc, float scaling,
-                               void* out, int odt, float* ml, float* acc, hipStream_t st) {
+                               void* out, int odt, float* ml, float* acc, bool merge, hipStream_t st) {
 #define NQ_DA(G)                                                                                                   \
     return launch_decode_attention_g<D, CT, G>(q, k, v, kv_heads, qn, kn, ndt, eps, cs, sn, position, max_positions, \
-                                               kc, vc, scaling, out, odt, ml, acc, st)
+                                               kc, vc, scaling, out, odt, ml, acc, merge, st)
     switch (group) {
         case 1: NQ_DA(1);
         case 2: NQ_DA(2);
@@ -1663,15 +1664,18 @@ extern "C" int64_t nq_decode_attention_workspace_bytes(int32_t q_heads, int32_t 
     return attn < 0 ? -1 : round16(static_cast<int64_t>(q_heads) * head_dim * 4) + attn;
 }
 
-extern "C" int nq_decode_attention(const float* q, const float* k, const float* v, int32_t q_heads, int32_t kv_heads,
-                                   int32_t head_dim, const void* q_norm, const void* k_norm, int32_t norm_dtype,
-                                   float eps, const float* cos_table, const float* sin_table, const int32_t* position,
-                                   int64_t max_positions, void* k_cache, void* v_cache, int32_t cache_dtype,
-                                   float scaling, void* out, int32_t out_dtype, void* workspace,
-                                   int64_t workspace_bytes, void* stream) {
-    if (!q || !k || !v || !cos_table || !sin_table || !position || !k_cache || !v_cache || !out || !workspace)
+namespace {
+
+// nq_decode_attention (merge) and nq_decode_attention_partials (!merge: pass 1
+// only, out unused).
+int decode_attention(const float* q, const float* k, const float* v, int32_t q_heads, int32_t kv_heads,
+                     int32_t head_dim, const void* q_norm, const void* k_norm, int32_t norm_dtype, float eps,
+                     const float* cos_table, const float* sin_table, const int32_t* position, int64_t max_positions,
+                     void* k_cache, void* v_cache, int32_t cache_dtype, float scaling, void* out, int32_t out_dtype,
+                     bool merge, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (!q || !k || !v || !cos_table || !sin_table || !position || !k_cache || !v_cache || (merge && !out) || !workspace)
         return NQ_ERR_ARGUMENT;
-    if (((q_norm || k_norm) && !float_code(norm_dtype)) || !float_code(cache_dtype) || !float_code(out_dtype))
+    if (((q_norm || k_norm) && !float_code(norm_dtype)) || !float_code(cache_dtype) || (merge && !float_code(out_dtype)))
         return NQ_ERR_DTYPE;
     if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || max_positions <= 0 ||
         attention_blocks(max_positions) > 65535)
@@ -1685,6 +1689,7 @@ extern "C" int nq_decode_attention(const float* q, const float* k, const float* 
     hipStream_t st = as_stream(stream);
     const int group = q_heads / kv_heads;
     if (!decode_fast_path(head_dim, cache_dtype, group)) {
+        if (!merge) return NQ_ERR_UNSUPPORTED;  // the partials exist only in the one-pass form
         // Unfused: rotate q into the workspace and append k/v, then attend.
         float* q_rot = static_cast<float*>(workspace);
         char* attn_ws = static_cast<char*>(workspace) + round16(static_cast<int64_t>(q_heads) * head_dim * 4);
@@ -1701,7 +1706,7 @@ extern "C" int nq_decode_attention(const float* q, const float* k, const float* 
 #define NQ_DAC(D, CT)                                                                                             \
     return launch_decode_attention_ct<D, CT>(group, q, k, v, kv_heads, q_norm, k_norm, norm_dtype, eps, cos_table, \
                                              sin_table, position, max_positions, k_cache, v_cache, scaling, out,   \
-                                             out_dtype, ml, acc, st)
+                                             out_dtype, ml, acc, merge, st)
     if (head_dim == 64) {
         if (cache_dtype == NQ_DTYPE_F32) NQ_DAC(64, NQ_DTYPE_F32);
         if (cache_dtype == NQ_DTYPE_F16) NQ_DAC(64, NQ_DTYPE_F16);
@@ -1710,4 +1715,29 @@ extern "C" int nq_decode_attention(const float* q, const float* k, const float* 
     if (cache_dtype == NQ_DTYPE_F16) NQ_DAC(128, NQ_DTYPE_F16);
     NQ_DAC(128, NQ_DTYPE_BF16);
 #undef NQ_DAC
+}
+
+}  // namespace
+
+extern "C" int nq_decode_attention(const float* q, const float* k, const float* v, int32_t q_heads, int32_t kv_heads,
+                                   int32_t head_dim, const void* q_norm, const void* k_norm, int32_t norm_dtype,
+                                   float eps, const float* cos_table, const float* sin_table, const int32_t* position,
+                                   int64_t max_positions, void* k_cache, void* v_cache, int32_t cache_dtype,
+                                   float scaling, void* out, int32_t out_dtype, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+    return decode_attention(q, k, v, q_heads, kv_heads, head_dim, q_norm, k_norm, norm_dtype, eps, cos_table,
+                            sin_table, position, max_positions, k_cache, v_cache, cache_dtype, scaling, out, out_dtype,
+                            true, workspace, workspace_bytes, stream);
+}
+
+extern "C" int nq_decode_attention_partials(const float* q, const float* k, const float* v, int32_t q_heads,
+                                            int32_t kv_heads, int32_t head_dim, const void* q_norm,
+                                            const void* k_norm, int32_t norm_dtype, float eps,
+                                            const float* cos_table, const float* sin_table,
+                                            const int32_t* position, int64_t max_positions, void* k_cache,
+                                            void* v_cache, int32_t cache_dtype, float scaling, void* workspace,
+                                            int64_t workspace_bytes, void* stream) {
+    return decode_attention(q, k, v, q_heads, kv_heads, head_dim, q_norm, k_norm, norm_dtype, eps, cos_table,
+                            sin_table, position, max_positions, k_cache, v_cache, cache_dtype, scaling, nullptr,
+                            NQ_DTYPE_F32, false, workspace, workspace_bytes, stream);
 }

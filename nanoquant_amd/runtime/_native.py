@@ -64,6 +64,7 @@ EXPORTED_SYMBOLS = (
     "nq_attention",
     "nq_decode_attention_workspace_bytes",
     "nq_decode_attention",
+    "nq_decode_attention_partials",
     "nq_silu_mul",
     "nq_output_projection_workspace_bytes",
     "nq_output_projection",
@@ -131,7 +132,7 @@ class LinearDesc(ctypes.Structure):
 
 
 # nq_input_kind
-INPUT_PLAIN, INPUT_RMSNORM, INPUT_SILU_GATE = 0, 1, 2
+INPUT_PLAIN, INPUT_RMSNORM, INPUT_SILU_GATE, INPUT_ATTENTION = 0, 1, 2, 3
 # nq_output_kind
 OUTPUT_PLAIN, OUTPUT_SILU_PRODUCT = 0, 1
 
@@ -149,6 +150,9 @@ class DecodeFusion(ctypes.Structure):
         ("residuals", ctypes.POINTER(ctypes.c_void_p)),
         ("out_slots", ctypes.POINTER(ctypes.c_void_p)),
         ("output_kind", ctypes.c_int32),
+        ("attn_position", ctypes.c_void_p),
+        ("attn_head_dim", ctypes.c_int32),
+        ("attn_max_positions", ctypes.c_int64),
     ]
 
 
@@ -207,6 +211,10 @@ def _declare(lib: ctypes.CDLL) -> None:
             c_int,
             [vp, vp, vp, i32, i32, i32, vp, vp, i32, f32, vp, vp, vp, c_i64, vp, vp, i32, f32, vp, i32, vp,
              c_i64, vp],
+        ),
+        "nq_decode_attention_partials": (
+            c_int,
+            [vp, vp, vp, i32, i32, i32, vp, vp, i32, f32, vp, vp, vp, c_i64, vp, vp, i32, f32, vp, c_i64, vp],
         ),
         "nq_silu_mul": (c_int, [vp, vp, c_i64, vp, i32, vp]),
         "nq_output_projection_workspace_bytes": (c_i64, [c_i64, c_i64]),

@@ -12,14 +12,18 @@ shell built from this library's kernels instead:
   gate/up run as one batched call each: the decode stages for up to 16
   tokens, the MFMA prefill phases for a longer prompt;
 * embedding, residual add + RMSNorm, q/k RMSNorm + RoPE + KV append,
-  grouped-query attention (one fused kernel per layer for a decode token),
-  SiLU product, the bf16 output projection and greedy selection are the HIP
-  kernels of ``include/nqamd_shell.h``;
+  grouped-query attention (for a decode token one kernel per 64-row cache
+  block, then a merge), SiLU product, the bf16 output projection and greedy
+  selection are the HIP kernels of ``include/nqamd_shell.h``;
+* a decode token folds the norms, the SiLU product and the residual adds into
+  the packed calls (``linear_batch_fused``): 10 launches per layer (12 without
+  the fused calls), 9 when the attention's merge also folds into the O
+  projection's input (by default for caches of up to FOLD_MAX_BLOCKS blocks);
 * the KV cache is one device tensor per layer ``[kv_heads, max_positions,
   head_dim]``, and the token position lives in device memory, so one HIP graph
-  of the whole one-token step (12 launches per layer) replays for every
-  position with no host synchronisation; ``generate_greedy`` keeps the chosen
-  tokens on the device and synchronises once at the end.
+  of the whole one-token step replays for every position with no host
+  synchronisation; ``generate_greedy`` keeps the chosen tokens on the device
+  and synchronises once at the end.
 
 ``forward_step`` implements the reference's ``GenerationModel`` protocol for
 batch 1 (a prompt without padding), returning ``[1, 1, vocab]`` fp32 logits
@@ -39,6 +43,12 @@ from nanoquant_amd.runtime.hip_backend import HipPackedBackend
 from nanoquant_amd.runtime.packed import PackedLayerState
 
 ROLES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+# Cache blocks (64 rows each) up to which a decode token folds the attention's
+# merge into the O projection by default. Measured on the 36-layer Qwen3-8B
+# geometry, fused one-token steps: folded 543 vs 524 tok/s at 2 blocks, 539 vs
+# 523 at 4, 511 vs 517 at 10.
+FOLD_MAX_BLOCKS = 6
 
 
 class DecodeStep(NamedTuple):
@@ -220,6 +230,7 @@ class PackedDecoder:
         cache_dtype: torch.dtype = torch.bfloat16,
         history_capacity: int = 4096,
         fuse_decode: bool = True,
+        fold_attention_merge: bool | None = None,
     ) -> None:
         self.config = c = config
         self.device = torch.device(device)
@@ -257,6 +268,18 @@ class PackedDecoder:
                     self.backend.norm_column_scale(prepared[role], norm)
                     for role, norm in (("q_proj", in_norm), ("k_proj", in_norm), ("v_proj", in_norm),
                                        ("gate_proj", post_norm), ("up_proj", post_norm))))
+        # One-token steps with the fused calls can also fold the attention's
+        # second pass (the merge of its cache blocks) into the O projection's
+        # input (input_kind="attention"): one launch fewer per layer, but every
+        # O workgroup then reads all blocks' fp32 partials (blocks x 16 KB at
+        # 4096 columns). None chooses by the cache length: folded up to
+        # FOLD_MAX_BLOCKS blocks, where the saved launch outweighs the reads.
+        blocks = -(-self.max_positions // 64)
+        fold = blocks <= FOLD_MAX_BLOCKS if fold_attention_merge is None else bool(fold_attention_merge)
+        self.fold_attention_merge = (
+            fold and self.fuse_decode
+            and ops.decode_attention_partials_supported(c.q_heads, c.kv_heads, c.head_dim, cache_dtype)
+            and c.q_heads * c.head_dim <= 4096 and blocks <= 16 and (c.q_heads * blocks) % 2 == 0)
         cache_shape = (c.layers, c.kv_heads, self.max_positions, c.head_dim)
         self.k_cache = torch.zeros(cache_shape, dtype=cache_dtype, device=dev)
         self.v_cache = torch.zeros(cache_shape, dtype=cache_dtype, device=dev)
@@ -333,7 +356,13 @@ class PackedDecoder:
             else:
                 ops.launch_add_rmsnorm(b.residual, in_norm, c.eps, delta=b.down if i else None, out=b.xn)
                 self._linears([b.xn] * 3, qkv, [b.q, b.k, b.v], t)
-            if t == 1:
+            if t == 1 and fused and self.fold_attention_merge:
+                ops.launch_decode_attention_partials(
+                    b.q, b.k, b.v, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, q_norm=qn,
+                    k_norm=kn, eps=c.eps, cos=self.cos, sin=self.sin, position=self.position,
+                    k_cache=self.k_cache[i], v_cache=self.v_cache[i], scaling=self.scaling, workspace=b.attn_ws,
+                )
+            elif t == 1:
                 ops.launch_decode_attention(
                     b.q, b.k, b.v, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, q_norm=qn,
                     k_norm=kn, eps=c.eps, cos=self.cos, sin=self.sin, position=self.position,
@@ -349,8 +378,15 @@ class PackedDecoder:
                 ops.launch_attention(b.q_rot, self.k_cache[i], self.v_cache[i], position=self.position,
                                      scaling=self.scaling, out=b.attn, workspace=b.attn_ws)
             if fused:
-                self.backend.linear_batch_fused([b.attn.view(-1)], [prepared["o_proj"]], residuals=[b.residual[0]],
-                                                out_slots=[b.o_slots])
+                if self.fold_attention_merge:
+                    self.backend.linear_batch_fused(
+                        [b.attn_ws], [prepared["o_proj"]], input_kind="attention",
+                        attention_position=self.position, attention_head_dim=c.head_dim,
+                        attention_max_positions=self.max_positions, residuals=[b.residual[0]],
+                        out_slots=[b.o_slots])
+                else:
+                    self.backend.linear_batch_fused([b.attn.view(-1)], [prepared["o_proj"]],
+                                                    residuals=[b.residual[0]], out_slots=[b.o_slots])
                 # gate and up in one workgroup per output tile: the epilogue writes
                 # silu(gate) * up in the activation dtype, the down projection's input
                 self.backend.linear_batch_fused([b.residual[0]] * 2, [prepared["gate_proj"], prepared["up_proj"]],

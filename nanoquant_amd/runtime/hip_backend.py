@@ -341,6 +341,9 @@ class HipPackedBackend:
         outs: list[torch.Tensor] | None = None,
         output_dtype: torch.dtype = torch.float32,
         output_kind: str = "plain",
+        attention_position: torch.Tensor | None = None,
+        attention_head_dim: int = 0,
+        attention_max_positions: int = 0,
     ) -> list[torch.Tensor] | None:
         """One decode token through 1-8 prepared layers with the decoder's
         neighbouring element-wise work fused in (nq_linear_batch_fused):
@@ -350,6 +353,12 @@ class HipPackedBackend:
           and the per-16-row-tile sums of h^2 in ``norm_slots``;
         * ``input_kind="silu_gate"``: each value is the fp32 gate, ``ups[i]`` the
           fp32 up; member i sees silu(gate) * up;
+        * ``input_kind="attention"``: each value is the workspace that
+          ``shell_ops.launch_decode_attention_partials`` filled for a cache of
+          ``attention_max_positions`` rows; member i sees the attention output
+          (heads of ``attention_head_dim``) merged from the partials of the
+          cache blocks up to ``attention_position`` (int32 on the device), the
+          attention's second pass;
         * ``residuals`` / ``out_slots``: member i adds its output to
           ``residuals[i]`` (fp32) and writes the tile sums of the new residual's
           squares to ``out_slots[i]`` instead of producing an output tensor;
@@ -363,7 +372,7 @@ class HipPackedBackend:
         625-660)."""
 
         kinds = {"plain": _native.INPUT_PLAIN, "rmsnorm": _native.INPUT_RMSNORM,
-                 "silu_gate": _native.INPUT_SILU_GATE}
+                 "silu_gate": _native.INPUT_SILU_GATE, "attention": _native.INPUT_ATTENTION}
         if input_kind not in kinds:
             raise ValueError(f"unknown fused input kind {input_kind!r}")
         out_kinds = {"plain": _native.OUTPUT_PLAIN, "silu_product": _native.OUTPUT_SILU_PRODUCT}
@@ -380,14 +389,29 @@ class HipPackedBackend:
         if any(p.tiles is None for p in payloads):
             raise ValueError("HIP fused batch requires layers prepared with tiled decode")
         device = payloads[0].device
-        for value, layer in zip(values, layers):
-            _check_value(value, layer.spec, device)
-            if value.numel() != layer.spec.in_features:
-                raise ValueError("HIP fused batch runs exactly one token")
-        if input_kind != "plain" and any(v.dtype != torch.float32 for v in values):
-            raise ValueError("HIP fused rmsnorm / silu_gate inputs are fp32")
-        if len({v.dtype for v in values}) != 1:
-            raise ValueError("HIP fused batch members must share the input dtype")
+        if input_kind == "attention":
+            hd, rows = int(attention_head_dim), int(attention_max_positions)
+            if hd not in (64, 128, 256) or rows <= 0:
+                raise ValueError("attention input needs head_dim 64, 128 or 256 and a positive cache length")
+            if (attention_position is None or attention_position.device != device
+                    or attention_position.dtype != torch.int32 or attention_position.numel() < 1):
+                raise ValueError("attention input needs the int32 device position")
+            blocks = -(-rows // 64)
+            for value, layer in zip(values, layers):
+                heads, rem = divmod(layer.spec.in_features, hd)
+                if rem or value.device != device or not value.is_contiguous():
+                    raise ValueError("attention input: in_features must be heads * head_dim, one contiguous workspace")
+                if value.numel() * value.element_size() < (2 + hd) * heads * blocks * 4:
+                    raise ValueError("attention input workspace is smaller than the partials it holds")
+        else:
+            for value, layer in zip(values, layers):
+                _check_value(value, layer.spec, device)
+                if value.numel() != layer.spec.in_features:
+                    raise ValueError("HIP fused batch runs exactly one token")
+            if input_kind != "plain" and any(v.dtype != torch.float32 for v in values):
+                raise ValueError("HIP fused rmsnorm / silu_gate inputs are fp32")
+            if len({v.dtype for v in values}) != 1:
+                raise ValueError("HIP fused batch members must share the input dtype")
 
         def vec(t: torch.Tensor | None, length: int, what: str) -> torch.Tensor:
             if (t is None or t.device != device or t.dtype != torch.float32 or not t.is_contiguous()
@@ -403,6 +427,10 @@ class HipPackedBackend:
         fusion.output_kind = out_kinds[output_kind]
         fusion.eps = float(eps)
         keep: list = []
+        if input_kind == "attention":
+            fusion.attn_position = attention_position.data_ptr()
+            fusion.attn_head_dim = int(attention_head_dim)
+            fusion.attn_max_positions = int(attention_max_positions)
         if input_kind == "rmsnorm":
             if col_scales is None or len(col_scales) != n:
                 raise ValueError("rmsnorm input needs one column scale per member")
@@ -451,11 +479,12 @@ class HipPackedBackend:
         else:
             if output_dtype not in (torch.float32, torch.bfloat16, torch.float16):
                 raise ValueError(f"HIP packed output dtype is unsupported: {output_dtype}")
+            lead = [() if input_kind == "attention" else tuple(v.shape[:-1]) for v in values]
             if outs is None:
-                outs = [torch.empty((*v.shape[:-1], layer.spec.out_features), dtype=output_dtype, device=device)
-                        for v, layer in zip(values, layers)]
-            for out, value, layer in zip(outs, values, layers):
-                if (tuple(out.shape) != (*value.shape[:-1], layer.spec.out_features) or out.dtype != output_dtype
+                outs = [torch.empty((*ld, layer.spec.out_features), dtype=output_dtype, device=device)
+                        for ld, layer in zip(lead, layers)]
+            for out, ld, layer in zip(outs, lead, layers):
+                if (tuple(out.shape) != (*ld, layer.spec.out_features) or out.dtype != output_dtype
                         or not out.is_contiguous()):
                     raise ValueError("HIP packed output tensor shape, dtype or layout differs")
         lib = _native.load()
@@ -472,7 +501,9 @@ class HipPackedBackend:
         w_ptrs = (ctypes.c_void_p * n)(*[w.data_ptr() for w in workspaces])
         w_sizes = (ctypes.c_int64 * n)(*sizes)
         status = lib.nq_linear_batch_fused(
-            desc_ptrs, n, x_ptrs, _native.dtype_code(values[0].dtype), y_ptrs, _native.dtype_code(output_dtype),
+            desc_ptrs, n, x_ptrs,
+            _native.dtype_code(torch.float32 if input_kind == "attention" else values[0].dtype), y_ptrs,
+            _native.dtype_code(output_dtype),
             w_ptrs, w_sizes, ctypes.byref(fusion), _native.current_stream_handle(device),
         )
         _native.check("nq_linear_batch_fused", status)

@@ -215,6 +215,35 @@ def decode_attention_workspace_bytes(q_heads: int, kv_heads: int, head_dim: int,
         q_heads, kv_heads, head_dim, _native.dtype_code(cache_dtype), max_positions))
 
 
+def _decode_attention_checks(q, k, v, q_heads, kv_heads, head_dim, q_norm, k_norm, cos, sin, position, k_cache,
+                             v_cache, out, workspace) -> tuple[int, torch.Tensor]:
+    """Validate one-token attention operands; returns (max_positions, workspace)."""
+
+    device = q.device
+    for name, t, heads in (("q", q, q_heads), ("k", k, kv_heads), ("v", v, kv_heads)):
+        if t.dtype != torch.float32 or t.numel() != heads * head_dim:
+            raise ValueError(f"{name} must be fp32 [{heads} * {head_dim}] (one token)")
+    if (q_norm is None) != (k_norm is None):
+        raise ValueError("q_norm and k_norm must be given together")
+    if q_norm is not None and (q_norm.numel() != head_dim or k_norm.numel() != head_dim or q_norm.dtype != k_norm.dtype):
+        raise ValueError("q/k norm weights must be [head_dim] of one dtype")
+    _check_float("decode attention", q_norm, k_norm, k_cache)
+    _check_device("decode attention", device, q, k, v, q_norm, k_norm, cos, sin, position, k_cache, v_cache, out,
+                  workspace)
+    _position("decode attention", position, device)
+    max_positions = k_cache.shape[-2]
+    if tuple(k_cache.shape) != (kv_heads, max_positions, head_dim) or v_cache.shape != k_cache.shape or v_cache.dtype != k_cache.dtype:
+        raise ValueError("KV cache must be [kv_heads, max_positions, head_dim] for K and V")
+    if cos.dtype != torch.float32 or tuple(cos.shape) != (max_positions, head_dim // 2) or sin.shape != cos.shape:
+        raise ValueError("RoPE tables must be fp32 [max_positions, head_dim / 2]")
+    need = decode_attention_workspace_bytes(q_heads, kv_heads, head_dim, k_cache.dtype, max_positions)
+    if need < 0:
+        raise ValueError("decode attention geometry was rejected")
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    return max_positions, workspace
+
+
 def launch_decode_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -240,31 +269,12 @@ def launch_decode_attention(
     causal GQA attention, fused into one kernel where the geometry allows."""
 
     device = q.device
-    for name, t, heads in (("q", q, q_heads), ("k", k, kv_heads), ("v", v, kv_heads)):
-        if t.dtype != torch.float32 or t.numel() != heads * head_dim:
-            raise ValueError(f"{name} must be fp32 [{heads} * {head_dim}] (one token)")
-    if (q_norm is None) != (k_norm is None):
-        raise ValueError("q_norm and k_norm must be given together")
-    if q_norm is not None and (q_norm.numel() != head_dim or k_norm.numel() != head_dim or q_norm.dtype != k_norm.dtype):
-        raise ValueError("q/k norm weights must be [head_dim] of one dtype")
-    _check_float("decode attention", q_norm, k_norm, k_cache)
-    _check_device("decode attention", device, q, k, v, q_norm, k_norm, cos, sin, position, k_cache, v_cache, out,
-                  workspace)
-    _position("decode attention", position, device)
-    max_positions = k_cache.shape[-2]
-    if tuple(k_cache.shape) != (kv_heads, max_positions, head_dim) or v_cache.shape != k_cache.shape or v_cache.dtype != k_cache.dtype:
-        raise ValueError("KV cache must be [kv_heads, max_positions, head_dim] for K and V")
-    if cos.dtype != torch.float32 or tuple(cos.shape) != (max_positions, head_dim // 2) or sin.shape != cos.shape:
-        raise ValueError("RoPE tables must be fp32 [max_positions, head_dim / 2]")
+    max_positions, workspace = _decode_attention_checks(q, k, v, q_heads, kv_heads, head_dim, q_norm, k_norm, cos,
+                                                        sin, position, k_cache, v_cache, out, workspace)
     if out is None:
         out = torch.empty(q_heads * head_dim, dtype=out_dtype, device=device)
     elif out.numel() != q_heads * head_dim or out.dtype not in _FLOAT:
         raise ValueError("decode attention output geometry is incompatible")
-    need = decode_attention_workspace_bytes(q_heads, kv_heads, head_dim, k_cache.dtype, max_positions)
-    if need < 0:
-        raise ValueError("decode attention geometry was rejected")
-    if workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=device)
     status = _native.load().nq_decode_attention(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), q_heads, kv_heads, head_dim, _ptr(q_norm), _ptr(k_norm),
         _native.dtype_code(q_norm.dtype) if q_norm is not None else 0, float(eps), cos.data_ptr(), sin.data_ptr(),
@@ -274,6 +284,54 @@ def launch_decode_attention(
     )
     _native.check("nq_decode_attention", status)
     return out
+
+
+def decode_attention_partials_supported(q_heads: int, kv_heads: int, head_dim: int, cache_dtype: torch.dtype) -> bool:
+    """Whether one-token attention runs as pass 1 + merge (the form whose
+    partials ``launch_decode_attention_partials`` leaves in the workspace):
+    head_dim * cache element bytes <= 256 and 1, 2, 4 or 8 q heads per kv head."""
+
+    if q_heads <= 0 or kv_heads <= 0 or q_heads % kv_heads:
+        return False
+    element = 4 if cache_dtype == torch.float32 else 2
+    return head_dim in (64, 128, 256) and head_dim * element <= 256 and q_heads // kv_heads in (1, 2, 4, 8)
+
+
+def launch_decode_attention_partials(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    q_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    q_norm: torch.Tensor | None,
+    k_norm: torch.Tensor | None,
+    eps: float,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    position: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    scaling: float,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Pass 1 of ``launch_decode_attention`` alone (nq_decode_attention_partials):
+    returns the workspace, which holds every cache block's partial (max, sum,
+    acc) for a projection with ``input_kind="attention"`` to merge."""
+
+    device = q.device
+    max_positions, workspace = _decode_attention_checks(q, k, v, q_heads, kv_heads, head_dim, q_norm, k_norm, cos,
+                                                        sin, position, k_cache, v_cache, None, workspace)
+    status = _native.load().nq_decode_attention_partials(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), q_heads, kv_heads, head_dim, _ptr(q_norm), _ptr(k_norm),
+        _native.dtype_code(q_norm.dtype) if q_norm is not None else 0, float(eps), cos.data_ptr(), sin.data_ptr(),
+        position.data_ptr(), max_positions, k_cache.data_ptr(), v_cache.data_ptr(),
+        _native.dtype_code(k_cache.dtype), float(scaling),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream(device),
+    )
+    _native.check("nq_decode_attention_partials", status)
+    return workspace
 
 
 def launch_silu_mul(

@@ -1,7 +1,9 @@
 """Fused one-token decode calls (nq_linear_batch_fused) against the oracle's
 fp32 forward of the same element-wise chain: the RMSNorm-folded residual
 input, the SiLU-gated input and the residual epilogue with its per-tile sums
-of squares; and the fused decoder against the unfused one."""
+of squares; the attention input (the decode attention's merge folded into the
+O projection) against the attention's own merge followed by a plain call; and
+the fused decoder against the unfused one."""
 
 from __future__ import annotations
 
@@ -12,7 +14,9 @@ import torch
 
 from nanoquant_amd import synthetic as syn
 from nanoquant_amd.runtime import DecoderShellConfig, HipPackedBackend, PackedDecoder
+from nanoquant_amd.runtime import shell_ops as ops
 from nanoquant_amd.runtime._native import NativeCallError
+from oracle import decoder_shell as ods
 from oracle import nq_oracle as orc
 
 pytestmark = [
@@ -163,7 +167,120 @@ def test_fused_calls_reject_what_they_do_not_cover():
         backend.linear_batch_fused([torch.randn(2, 4096, device="cuda")], [layer])
 
 
+def _attention_operands(max_pos, p, cache_dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = (3 * torch.randn(32 * 128, generator=g)).cuda()
+    k = (3 * torch.randn(8 * 128, generator=g)).cuda()
+    v = torch.randn(8 * 128, generator=g).cuda()
+    cos, sin = ods.rope_tables(128, 1e6, max_pos)
+    caches = [torch.randn(8, max_pos, 128, generator=g).to(cache_dtype) for _ in range(2)]
+    common = dict(q_heads=32, kv_heads=8, head_dim=128, q_norm=(1 + 0.1 * torch.randn(128, generator=g)).cuda(),
+                  k_norm=(1 + 0.1 * torch.randn(128, generator=g)).cuda(), eps=EPS, cos=cos.cuda(), sin=sin.cuda(),
+                  position=torch.tensor([p], dtype=torch.int32, device="cuda"), scaling=128**-0.5)
+    return q, k, v, caches, common
+
+
+@pytest.mark.parametrize(
+    "max_pos,p,cache_dtype",
+    [
+        (640, 639, torch.bfloat16),  # 10 blocks (up-to-16 kind), last row
+        (640, 0, torch.bfloat16),    # one live block
+        (512, 300, torch.float16),   # 8 blocks (up-to-8 kind)
+        (1024, 1023, torch.bfloat16),  # 16 blocks
+        (100, 64, torch.float16),    # 2 blocks, first row of the second
+        (20, 7, torch.bfloat16),     # 1 block
+        (640, 640, torch.bfloat16),  # position outside the cache: zero input
+    ],
+)
+def test_attention_input_equals_merge_then_plain_call(max_pos, p, cache_dtype):
+    # With fp32 attention output, the merge kernel and the folded input compute
+    # the same values in the same order, so the O projection's results and the
+    # appended cache rows are identical, not just close.
+    backend = HipPackedBackend()
+    shape = syn.qwen3_8b_layer()[3]
+    _say("attention input", max_pos, p, cache_dtype)
+    (state,), (layer,) = _layers(backend, [shape], syn.BASE_SEED + 350)
+    q, k, v, caches, common = _attention_operands(max_pos, p, cache_dtype, 11)
+    r0 = 4 * torch.randn(4096, generator=torch.Generator().manual_seed(12))
+    results = []
+    for fold in (False, True):
+        kc, vc = (c.cuda() for c in caches)
+        r = r0.cuda()
+        slots = torch.full((256,), -1.0, device="cuda")
+        if fold:
+            ws = ops.launch_decode_attention_partials(q, k, v, k_cache=kc, v_cache=vc, **common)
+            ret = backend.linear_batch_fused([ws], [layer], input_kind="attention",
+                                             attention_position=common["position"], attention_head_dim=128,
+                                             attention_max_positions=max_pos, residuals=[r], out_slots=[slots])
+            assert ret is None
+        else:
+            attn = ops.launch_decode_attention(q, k, v, k_cache=kc, v_cache=vc, out_dtype=torch.float32, **common)
+            backend.linear_batch_fused([attn], [layer], residuals=[r], out_slots=[slots])
+            expected = orc.packed_forward(orc.operands_from_state(state), attn.cpu()[None])[0]
+            err = orc.relative_l2(r.cpu() - r0, expected)
+            assert err <= REL_L2, err
+        results.append((r, slots, kc, vc))
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+    if p >= max_pos:
+        assert torch.equal(results[1][0].cpu(), r0)  # zero input, no bias
+
+
+def test_attention_input_rejects_what_it_does_not_cover():
+    backend = HipPackedBackend()
+    (state,), (layer,) = _layers(backend, [syn.qwen3_8b_layer()[3]], syn.BASE_SEED + 351)
+    q, k, v, caches, common = _attention_operands(1100, 5, torch.bfloat16, 13)
+    kc, vc = (c.cuda() for c in caches)
+    ws = ops.launch_decode_attention_partials(q, k, v, k_cache=kc, v_cache=vc, **common)
+    kwargs = dict(input_kind="attention", attention_position=common["position"], attention_head_dim=128)
+    with pytest.raises(NativeCallError):  # 18 cache blocks: more than one register pass holds
+        backend.linear_batch_fused([ws], [layer], attention_max_positions=1100, **kwargs)
+    with pytest.raises(ValueError):  # workspace smaller than the partials of the cache length
+        backend.linear_batch_fused([ws[:1024]], [layer], attention_max_positions=1100, **kwargs)
+    with pytest.raises(ValueError):  # head_dim must divide in_features and be 64, 128 or 256
+        backend.linear_batch_fused([ws], [layer], input_kind="attention", attention_position=common["position"],
+                                   attention_head_dim=96, attention_max_positions=1100)
+    # head_dim 256 with a 16-bit cache is the unfused form: no partials to leave
+    g = torch.Generator().manual_seed(14)
+    kc2 = torch.randn(2, 64, 256, generator=g).to(torch.bfloat16).cuda()
+    cos, sin = ods.rope_tables(256, 1e6, 64)
+    with pytest.raises(NativeCallError):
+        ops.launch_decode_attention_partials(
+            torch.randn(8 * 256).cuda(), torch.randn(2 * 256).cuda(), torch.randn(2 * 256).cuda(), q_heads=8,
+            kv_heads=2, head_dim=256, q_norm=None, k_norm=None, eps=EPS, cos=cos.cuda(), sin=sin.cuda(),
+            position=torch.tensor([3], dtype=torch.int32, device="cuda"), k_cache=kc2, v_cache=kc2.clone(),
+            scaling=256**-0.5)
+
+
 SMALL = DecoderShellConfig(layers=3, hidden=256, intermediate=768, q_heads=4, kv_heads=2, head_dim=64, vocab=1000)
+
+
+@pytest.mark.parametrize("cache", [torch.float32, torch.bfloat16])
+def test_folded_attention_decoder_matches_unfolded(cache):
+    # 130 cache rows: three blocks; the unfolded decoder rounds the attention
+    # output to the activation dtype (fp32 here), the folded one merges in fp32.
+    weights = syn.synthetic_decoder(SMALL, seed=syn.BASE_SEED + 345, random_norms=True)
+    prompt = torch.randint(0, SMALL.vocab, (70,), generator=torch.Generator().manual_seed(10)).cuda()
+    runs = {}
+    for fold in (True, False):
+        decoder = PackedDecoder(SMALL, weights, device="cuda", max_positions=130, activation_dtype=torch.float32,
+                                cache_dtype=cache, fold_attention_merge=fold)
+        assert decoder.fuse_decode and decoder.fold_attention_merge == fold
+        runs[fold] = decoder.generate_greedy(prompt, 40).tolist()
+        decoder.reset()
+        decoder.prefill(prompt)
+        bufs = decoder._decode_bufs or decoder._buffers(1)
+        decoder._decode_bufs = bufs
+        logits = []
+        for token in runs[fold][:8]:
+            decoder.ids.fill_(token)
+            decoder._forward(decoder.ids, bufs)
+            decoder.position += 1
+            logits.append(decoder.logits.clone())
+        runs[(fold, "logits")] = logits
+    for a, b in zip(runs[(True, "logits")], runs[(False, "logits")]):
+        assert orc.relative_l2(a, b) <= 1e-5
+    assert runs[True][:8] == runs[False][:8]
 
 
 @pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
