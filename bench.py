@@ -16,7 +16,9 @@ Beside it, each with p10/p50/p90 over at least 10 repetitions:
   config3  the Llama-3-8B prefill sweep (64 to 2048 tokens, MFMA GEMMs);
   config4  Gemma-3-4B down 10240->2560 r1536 with a 26-entry int8 sidecar in
            column and row form at 1 and 8 tokens;
-  copy     the measured streaming ceiling of plain device copies and reads.
+  copy     the measured streaming ceiling of plain device copies and reads,
+           and the cost of one launch in a graph-replayed chain of minimal
+           launches (the floor each kernel of the decode step pays).
 Per-call figures rotate over replicas of the layer's weights (at least
 512 MB, twice the 256 MB Infinity Cache) so the bytes come from HBM.
 
@@ -70,6 +72,8 @@ def parse_args(argv=None):
     p.add_argument("--dominant-only", action="store_true",
                    help="only launch the dominant call (gate/up batch) of every layer eagerly --steps times "
                         "(per-dispatch counter collection) and exit")
+    p.add_argument("--launch-floor", type=int, default=0, metavar="N",
+                   help="only time a HIP graph of N back-to-back minimal launches and exit")
     p.add_argument("--stack-mode-only", default="", metavar="MODE",
                    help="only time the M=1 decode stack in one launch grouping (one of --modes' names) "
                         "and exit (kernel traces of one mode)")
@@ -272,7 +276,31 @@ def copy_ceiling(reps: int, warmup: int) -> dict:
         del srcs, dsts
         torch.cuda.empty_cache()
     return {"workload": "torch copy_ (read+write bytes) and nq_read_stream (read bytes) over distinct buffers, "
-                        "one HIP graph per size", "points": res}
+                        "one HIP graph per size", "points": res, "launch_floor": launch_floor(200, reps, warmup)}
+
+
+def launch_floor(launches: int, reps: int, warmup: int) -> dict:
+    """Cost of one launch in a chain of stream-ordered launches replayed from
+    a HIP graph, with next to no work in each: nq_read_stream over 4 KiB with
+    one workgroup. Each launch waits for the previous one to finish, as each
+    kernel of the decode step does, so this is the floor every kernel of that
+    chain pays before its own work."""
+
+    import torch
+
+    from nanoquant_amd.runtime import _native
+
+    lib = _native.load()
+    src = torch.ones(1024, dtype=torch.float32, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def chain():
+        stream = torch.cuda.current_stream().cuda_stream
+        for _ in range(launches):
+            _native.check("nq_read_stream", lib.nq_read_stream(src.data_ptr(), 4096, sink.data_ptr(), 1, stream))
+
+    d = pct([t / launches for t in graph_reps(chain, reps, warmup)])
+    return {"launches_per_graph": launches, "us_per_launch": _scaled(d, lambda ms: ms * 1e3, 3)}
 
 
 # --- config 2: the Qwen3-8B stack ----------------------------------------------------------
@@ -858,6 +886,9 @@ def main(argv=None) -> int:
     torch.cuda.set_device(device)
     if args.dominant_only:
         return dominant_only(args, device)
+    if args.launch_floor:
+        print(json.dumps(launch_floor(args.launch_floor, max(args.steps, 10), args.warmup)))
+        return 0
     if args.stack_mode_only:
         return stack_mode_only(args, device)
     wall0 = time.perf_counter()
