@@ -315,15 +315,28 @@ __device__ __forceinline__ uint32_t sign_pair(uint32_t w, int shift, uint32_t ma
     return ((w << shift) & mask) | one;
 }
 
+// 64-bit left shift as one instruction (a shift by a constant is otherwise
+// split into a 32-bit shift and an alignbit); the amount comes from an SGPR.
+__device__ __forceinline__ uint64_t shl64(uint64_t w, int s) {
+    uint64_t r;
+    asm("v_lshlrev_b64 %0, %1, %2" : "=v"(r) : "s"(s), "v"(w));
+    return r;
+}
+
+// The two words take the same shifts, so each shift moves both as one 64-bit
+// value (w1:w0): a shift s <= 15 carries bits of w0 only into bits below s of
+// the high half, never into its sign positions 15 and 31.
 __device__ __forceinline__ v8h expand_signs32(uint32_t w0, uint32_t w1, int m, uint32_t mask, uint32_t one) {
     union {
         uint32_t u[4];
         v8h v;
     } x;
-    x.u[0] = sign_pair(w0, 15 - m, mask, one);
-    x.u[1] = sign_pair(w0, 7 - m, mask, one);
-    x.u[2] = sign_pair(w1, 15 - m, mask, one);
-    x.u[3] = sign_pair(w1, 7 - m, mask, one);
+    const uint64_t w = (static_cast<uint64_t>(w1) << 32) | w0;
+    const uint64_t hi = shl64(w, 15 - m), lo = shl64(w, 7 - m);
+    x.u[0] = (static_cast<uint32_t>(hi) & mask) | one;
+    x.u[1] = (static_cast<uint32_t>(lo) & mask) | one;
+    x.u[2] = (static_cast<uint32_t>(hi >> 32) & mask) | one;
+    x.u[3] = (static_cast<uint32_t>(lo >> 32) & mask) | one;
     return x.v;
 }
 
