@@ -167,40 +167,47 @@ def test_fused_calls_reject_what_they_do_not_cover():
         backend.linear_batch_fused([torch.randn(2, 4096, device="cuda")], [layer])
 
 
-def _attention_operands(max_pos, p, cache_dtype, seed):
+def _attention_operands(max_pos, p, cache_dtype, seed, q_heads=32, kv_heads=8, head_dim=128):
     g = torch.Generator().manual_seed(seed)
-    q = (3 * torch.randn(32 * 128, generator=g)).cuda()
-    k = (3 * torch.randn(8 * 128, generator=g)).cuda()
-    v = torch.randn(8 * 128, generator=g).cuda()
-    cos, sin = ods.rope_tables(128, 1e6, max_pos)
-    caches = [torch.randn(8, max_pos, 128, generator=g).to(cache_dtype) for _ in range(2)]
-    common = dict(q_heads=32, kv_heads=8, head_dim=128, q_norm=(1 + 0.1 * torch.randn(128, generator=g)).cuda(),
-                  k_norm=(1 + 0.1 * torch.randn(128, generator=g)).cuda(), eps=EPS, cos=cos.cuda(), sin=sin.cuda(),
-                  position=torch.tensor([p], dtype=torch.int32, device="cuda"), scaling=128**-0.5)
+    q = (3 * torch.randn(q_heads * head_dim, generator=g)).cuda()
+    k = (3 * torch.randn(kv_heads * head_dim, generator=g)).cuda()
+    v = torch.randn(kv_heads * head_dim, generator=g).cuda()
+    cos, sin = ods.rope_tables(head_dim, 1e6, max_pos)
+    caches = [torch.randn(kv_heads, max_pos, head_dim, generator=g).to(cache_dtype) for _ in range(2)]
+    common = dict(q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
+                  q_norm=(1 + 0.1 * torch.randn(head_dim, generator=g)).cuda(),
+                  k_norm=(1 + 0.1 * torch.randn(head_dim, generator=g)).cuda(), eps=EPS, cos=cos.cuda(),
+                  sin=sin.cuda(), position=torch.tensor([p], dtype=torch.int32, device="cuda"),
+                  scaling=head_dim**-0.5)
     return q, k, v, caches, common
 
 
 @pytest.mark.parametrize(
-    "max_pos,p,cache_dtype",
+    "max_pos,p,cache_dtype,kv_heads,head_dim",
     [
-        (640, 639, torch.bfloat16),  # 10 blocks (up-to-16 kind), last row
-        (640, 0, torch.bfloat16),    # one live block
-        (512, 300, torch.float16),   # 8 blocks (up-to-8 kind)
-        (1024, 1023, torch.bfloat16),  # 16 blocks
-        (100, 64, torch.float16),    # 2 blocks, first row of the second
-        (20, 7, torch.bfloat16),     # 1 block
-        (640, 640, torch.bfloat16),  # position outside the cache: zero input
+        (640, 639, torch.bfloat16, 8, 128),  # 10 blocks (up-to-16 kind), last row; MFMA pass 1
+        (640, 0, torch.bfloat16, 8, 128),    # one live block
+        (512, 300, torch.float16, 8, 128),   # 8 blocks (up-to-8 kind)
+        (1024, 1023, torch.bfloat16, 8, 128),  # 16 blocks
+        (100, 64, torch.float16, 8, 128),    # 2 blocks, first row of the second
+        (20, 7, torch.bfloat16, 8, 128),     # 1 block
+        (640, 640, torch.bfloat16, 8, 128),  # position outside the cache: zero input
+        (640, 639, torch.float32, 32, 64),   # head dim 64, fp32 cache, two q heads per kv head
+        (130, 70, torch.bfloat16, 64, 64),   # head dim 64, one q head per kv head
+        (512, 511, torch.float16, 16, 64),   # head dim 64, four q heads per kv head
     ],
 )
-def test_attention_input_equals_merge_then_plain_call(max_pos, p, cache_dtype):
+def test_attention_input_equals_merge_then_plain_call(max_pos, p, cache_dtype, kv_heads, head_dim):
     # With fp32 attention output, the merge kernel and the folded input compute
     # the same values in the same order, so the O projection's results and the
-    # appended cache rows are identical, not just close.
+    # appended cache rows are identical, not just close (for the MFMA pass 1
+    # and for the other one-pass geometries alike).
     backend = HipPackedBackend()
     shape = syn.qwen3_8b_layer()[3]
-    _say("attention input", max_pos, p, cache_dtype)
+    q_heads = shape.in_features // head_dim
+    _say("attention input", max_pos, p, cache_dtype, f"{q_heads}/{kv_heads} x {head_dim}")
     (state,), (layer,) = _layers(backend, [shape], syn.BASE_SEED + 350)
-    q, k, v, caches, common = _attention_operands(max_pos, p, cache_dtype, 11)
+    q, k, v, caches, common = _attention_operands(max_pos, p, cache_dtype, 11, q_heads, kv_heads, head_dim)
     r0 = 4 * torch.randn(4096, generator=torch.Generator().manual_seed(12))
     results = []
     for fold in (False, True):
@@ -210,7 +217,7 @@ def test_attention_input_equals_merge_then_plain_call(max_pos, p, cache_dtype):
         if fold:
             ws = ops.launch_decode_attention_partials(q, k, v, k_cache=kc, v_cache=vc, **common)
             ret = backend.linear_batch_fused([ws], [layer], input_kind="attention",
-                                             attention_position=common["position"], attention_head_dim=128,
+                                             attention_position=common["position"], attention_head_dim=head_dim,
                                              attention_max_positions=max_pos, residuals=[r], out_slots=[slots])
             assert ret is None
         else:
