@@ -901,8 +901,8 @@ void batch_splits(int count, const int64_t* tiles, const int64_t* k_blocks, cons
 // One launch of a phase's GEMMs (p[i].splits, k_per_split and partial set)
 // and, when any member's K is split, one launch of the reductions. Up to 64
 // tokens take the 64 x 128 block tile; otherwise the 128 x 256 block tile is
-// used when no member is split and it is the cheaper of the two by the round
-// model below, and 128 x 128 when not.
+// used when it is the cheaper of the two by the round model below (K slices
+// count as blocks of their own), and 128 x 128 when not.
 constexpr double kWideStepCost = 1.65;
 void launch_phase(GemmArgs* p, int count, int64_t tokens, hipStream_t stream) {
     const int64_t mt = (tokens + kBM - 1) / kBM;
@@ -910,8 +910,7 @@ void launch_phase(GemmArgs* p, int count, int64_t tokens, hipStream_t stream) {
     bool wide = !small;
     int64_t wide_blocks = 0, narrow_blocks = 0, steps = 0;
     for (int i = 0; i < count; ++i) {
-        wide = wide && p[i].splits == 1;
-        wide_blocks += mt * ((p[i].n + 2 * kBN - 1) / (2 * kBN));
+        wide_blocks += mt * ((p[i].n + 2 * kBN - 1) / (2 * kBN)) * p[i].splits;
         narrow_blocks += mt * ((p[i].n + kBN - 1) / kBN) * p[i].splits;
         steps = p[i].k_per_split > steps ? p[i].k_per_split : steps;
     }

@@ -761,6 +761,23 @@ def test_prefill_batch_wide_blocks_at_2048():
         assert orc.relative_l2(y, backend.linear(x, layer)) <= 1e-4
 
 
+def test_prefill_wide_blocks_with_split_k_at_2048():
+    """Down of Llama-3-8B at M = 2048 (K = 14336): its first GEMM splits K
+    three ways and, by the round model, takes the 128 x 256 block tile, whose
+    partial sums the split reduction adds in slice order."""
+
+    backend = HipPackedBackend()
+    shape = syn.llama3_8b_layer()[6]
+    state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 97)
+    layer = backend.prepare(state, "cuda")
+    x = syn.synthetic_activations(2048, shape.in_features, seed=10, device="cuda")
+    _say("prefill down, split K, wide blocks", 2048)
+    y = backend.linear(x, layer)
+    err = orc.relative_l2(y, orc.packed_forward(orc.operands_from_state(state), x.cpu()))
+    assert err <= REL_L2, err
+    assert torch.equal(y, backend.linear(x, layer))
+
+
 def test_batch_rejects_mixed_launch_structures():
     state = syn.synthetic_packed_layer(syn.qwen3_8b_layer()[1], seed=3)
     split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
