@@ -56,6 +56,11 @@ __host__ __device__ constexpr int64_t words_for(int64_t cols) { return (cols + 3
 // attention input kind read.
 constexpr int kAttnBlockRows = 64;
 
+// e^x for the weights that merge attention blocks (x = a block's max minus the
+// running max, <= 0 or -inf): the hardware base-2 exponential of x * log2(e).
+// Every merge of block partials uses this one form, so they agree bit for bit.
+__device__ __forceinline__ float merge_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+
 inline bool is_float_dtype(int d) {
     return d == NQ_DTYPE_F32 || d == NQ_DTYPE_F16 || d == NQ_DTYPE_BF16;
 }

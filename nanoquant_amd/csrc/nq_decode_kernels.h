@@ -757,7 +757,7 @@ __device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const L
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
         if (s < nb) {  // a select: slots past the position may hold anything
-            const float f = expf(__uint_as_float(r.at.ml[s].x) - m);
+            const float f = nq::merge_exp(__uint_as_float(r.at.ml[s].x) - m);
             l = fmaf(__uint_as_float(r.at.ml[s].y), f, l);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {

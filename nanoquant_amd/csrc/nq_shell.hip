@@ -573,13 +573,13 @@ __global__ __launch_bounds__(D) void k_attention_merge(const float* __restrict__
         float mnew = mrun;
 #pragma unroll
         for (int i = 0; i < kMergeRound; ++i) mnew = b0 + i < nb ? fmaxf(mnew, mb[i]) : mnew;
-        const float keep = expf(mrun - mnew);  // 0 in the first round
+        const float keep = nq::merge_exp(mrun - mnew);  // 0 in the first round
         lsum *= keep;
         acc *= keep;
 #pragma unroll
         for (int i = 0; i < kMergeRound; ++i) {
             if (b0 + i < nb) {  // a select: slots past the position may hold anything
-                const float f = expf(mb[i] - mnew);
+                const float f = nq::merge_exp(mb[i] - mnew);
                 lsum = fmaf(lb[i], f, lsum);
                 acc = fmaf(ab[i], f, acc);
             }
