@@ -161,6 +161,10 @@ def test_attention(tokens, start, q_heads, kv_heads, head_dim, cache_dtype):
         (32, 8, 128, torch.bfloat16, 640, 577),
         (32, 8, 128, torch.bfloat16, 640, 639),
         (32, 8, 128, torch.bfloat16, 2500, 2300),  # 36 blocks: three merge rounds
+        (32, 8, 128, torch.bfloat16, 40, 39),  # one block
+        (32, 8, 128, torch.float16, 300, 299),  # five blocks, the last row
+        (32, 8, 128, torch.bfloat16, 1024, 1000),  # sixteen blocks
+        (32, 8, 128, torch.bfloat16, 1088, 1070),  # seventeen blocks: two merge rounds
         (16, 8, 128, torch.float16, 300, 130),
         (8, 8, 64, torch.float32, 200, 150),
         (64, 8, 128, torch.bfloat16, 1100, 1050),
