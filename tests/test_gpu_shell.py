@@ -374,13 +374,16 @@ def _check_against_oracle(config, act, cache, tol, prompt_len, new_tokens, seed)
     tokens, logits = _gpu_steps(decoder, prompt, new_tokens)
     oracle = _oracle(config, weights, act, cache, max_positions)
     expected = _teacher_forced(oracle, prompt, tokens)
+    worst = 0.0
     for step, (got, exp, token) in enumerate(zip(logits, expected, tokens)):
         err = relative_l2(got.cpu(), exp)
+        worst = max(worst, err)
         assert err <= tol, f"step {step}: rel_l2 {err:.3e} > {tol}"
         assert token == int(torch.argmax(got))
         top2 = torch.topk(exp, 2).values
         if float(top2[0] - top2[1]) > 4 * tol * float(exp.abs().max()):
             assert token == int(torch.argmax(exp)), f"step {step}: greedy token differs"
+    print(f"  logits worst-step rel_l2={worst:.2e} over {len(tokens)} tokens", flush=True)
     return decoder, prompt, tokens
 
 
