@@ -761,6 +761,28 @@ def test_prefill_batch_wide_blocks_at_2048():
         assert orc.relative_l2(y, backend.linear(x, layer)) <= 1e-4
 
 
+@pytest.mark.parametrize("tokens", [1800, 2048])
+def test_prefill_block_tile_does_not_change_results(tokens):
+    """Gate/up of Llama-3-8B at M = 1800 and 2048: batched, the first GEMM
+    runs as 128 x 256 blocks (300 / 320 of them); each linear alone runs it as
+    128 x 128 blocks (the round model's choice at 150 / 160 wide blocks). Both
+    tiles sum each output's K in the same order, so the batch equals each
+    linear called on its own exactly, and both match the oracle."""
+
+    backend = HipPackedBackend()
+    shapes = syn.llama3_8b_layer()[4:6]
+    states = [syn.synthetic_packed_layer(s, seed=syn.BASE_SEED + 93 + i) for i, s in enumerate(shapes)]
+    layers = [backend.prepare(st, "cuda") for st in states]
+    x = syn.synthetic_activations(tokens, 4096, seed=tokens, device="cuda")
+    _say("prefill gate/up batch against single calls", tokens)
+    ys = backend.linear_batch([x, x], layers)
+    for state, y, layer in zip(states, ys, layers):
+        assert torch.equal(y, backend.linear(x, layer)), state.spec.name
+        err = orc.relative_l2(y, orc.packed_forward(orc.operands_from_state(state), x.cpu()))
+        assert err <= REL_L2, (state.spec.name, err)
+    assert all(torch.equal(a, b) for a, b in zip(ys, backend.linear_batch([x, x], layers)))
+
+
 def test_prefill_wide_blocks_with_split_k_at_2048():
     """Down of Llama-3-8B at M = 2048 (K = 14336): its first GEMM splits K
     three ways and, by the round model, takes the 128 x 256 block tile, whose
