@@ -800,6 +800,62 @@ def test_prefill_wide_blocks_with_split_k_at_2048():
     assert torch.equal(y, backend.linear(x, layer))
 
 
+# --- exact properties at the benchmark sizes -------------------------------------------
+
+_PROPERTY_CASES = [
+    ("qwen3 gate decode", syn.qwen3_8b_layer()[4], 1),
+    ("qwen3 down decode", syn.qwen3_8b_layer()[6], 1),
+    ("qwen3 q decode", syn.qwen3_8b_layer()[0], 16),
+    ("llama gate prefill", syn.llama3_8b_layer()[4], 64),
+    ("llama down prefill, split K", syn.llama3_8b_layer()[6], 2048),
+]
+
+
+@pytest.mark.parametrize("case", _PROPERTY_CASES, ids=[c[0] for c in _PROPERTY_CASES])
+def test_power_of_two_input_scaling_is_exact(case):
+    """y(2^k x) == 2^k y(x) bit for bit on the tiled paths (no bias): decode
+    takes one power of two per activation chunk and prefill one per token
+    row, so scaling x by 2^k shifts those exponents and nothing else, and the
+    fp32 output comes out scaled exactly."""
+
+    name, shape, tokens = case
+    backend = HipPackedBackend()
+    layer = backend.prepare(syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 101), "cuda")
+    x = syn.synthetic_activations(tokens, shape.in_features, seed=11, device="cuda")
+    _say("power-of-two scaling", name, tokens)
+    y = backend.linear(x, layer)
+    for k in (-3, 5):
+        assert torch.equal(backend.linear(x * 2.0**k, layer), y * 2.0**k), (name, k)
+
+
+@pytest.mark.parametrize("case", _PROPERTY_CASES, ids=[c[0] for c in _PROPERTY_CASES])
+def test_one_sign_flip_in_u_moves_one_output_column(case):
+    """Flipping sign bit (o, r) of U changes output column o alone: every
+    other output stays bit-identical (column o' reads row o' of U only), and
+    column o moves by the oracle's difference, -2 sgn(U[o, r]) s_out[o] lm[r]
+    per token."""
+
+    name, shape, tokens = case
+    backend = HipPackedBackend()
+    state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 103)
+    o, r = shape.out_features // 3, shape.rank - 2
+    words = state.left_words.clone()
+    words.numpy().view(np.uint32)[o, r // 32] ^= np.uint32(1 << (r % 32))
+    flipped = replace(state, left_words=words)
+    x = syn.synthetic_activations(tokens, shape.in_features, seed=13, device="cuda")
+    _say("one sign flip in U", name, tokens, (o, r))
+    y = backend.linear(x, backend.prepare(state, "cuda"))
+    y2 = backend.linear(x, backend.prepare(flipped, "cuda"))
+    others = torch.ones(shape.out_features, dtype=torch.bool, device=y.device)
+    others[o] = False
+    assert torch.equal(y[:, others], y2[:, others]), name
+    got = (y2[:, o] - y[:, o]).cpu()
+    expected = (orc.packed_forward(orc.operands_from_state(flipped), x.cpu())[:, o]
+                - orc.packed_forward(orc.operands_from_state(state), x.cpu())[:, o])
+    assert float(expected.abs().min()) > 0.0
+    assert orc.relative_l2(got, expected) <= REL_L2, name
+
+
 def test_batch_rejects_mixed_launch_structures():
     state = syn.synthetic_packed_layer(syn.qwen3_8b_layer()[1], seed=3)
     split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
