@@ -323,14 +323,16 @@ def test_greedy_ties_take_the_lowest_index_and_advance_counters():
 # --------------------------------------------------------------------------- end to end
 SMALL = DecoderShellConfig(layers=3, hidden=256, intermediate=768, q_heads=4, kv_heads=2, head_dim=64, vocab=1000)
 QWEN_2L = DecoderShellConfig(layers=2, vocab=151936)
+QWEN_36L = DecoderShellConfig(layers=36, vocab=151936)
 
 
 def _oracle(config, weights, act, cache, max_positions):
     geometry = ods.ShellGeometry(config.layers, config.hidden, config.intermediate, config.q_heads,
                                  config.kv_heads, config.head_dim, config.vocab, config.eps, config.rope_theta)
+    host = lambda t: t.cpu()  # the oracle runs on the CPU whatever device the weights came from
     ow = ods.ShellWeights(
-        weights.embed, weights.lm_head, weights.final_norm,
-        [ods.LayerWeights(l.input_norm, l.post_norm, l.q_norm, l.k_norm,
+        host(weights.embed), host(weights.lm_head), host(weights.final_norm),
+        [ods.LayerWeights(host(l.input_norm), host(l.post_norm), host(l.q_norm), host(l.k_norm),
                           {r: operands_from_state(s) for r, s in l.linears.items()}) for l in weights.layers],
     )
     return ods.OracleDecoder(geometry, ow, max_positions=max_positions, activation_dtype=act, cache_dtype=cache)
@@ -365,8 +367,8 @@ def _gpu_steps(decoder, prompt, new_tokens):
     return tokens, logits
 
 
-def _check_against_oracle(config, act, cache, tol, prompt_len, new_tokens, seed):
-    weights = syn.synthetic_decoder(config, seed=seed, random_norms=True)
+def _check_against_oracle(config, act, cache, tol, prompt_len, new_tokens, seed, device="cpu"):
+    weights = syn.synthetic_decoder(config, seed=seed, random_norms=True, device=device)
     max_positions = prompt_len + new_tokens + 3
     decoder = PackedDecoder(config, weights, device=DEV, max_positions=max_positions, activation_dtype=act,
                             cache_dtype=cache)
@@ -397,6 +399,16 @@ def test_decoder_small_matches_oracle(act, cache, tol):
 def test_decoder_qwen3_8b_geometry_matches_oracle(act, cache, tol):
     # two layers of the Qwen3-8B geometry with its full vocabulary; prompt <= 16 uses the batched decode path
     _check_against_oracle(QWEN_2L, act, cache, tol, prompt_len=12, new_tokens=5, seed=syn.BASE_SEED + 62)
+
+
+@pytest.mark.parametrize("act,cache,tol", [(torch.float32, torch.float32, 1e-2), (torch.bfloat16, torch.bfloat16, 5e-2)])
+def test_decoder_qwen3_8b_full_size_matches_oracle(act, cache, tol):
+    # the benchmark's model at full size: 36 layers, full vocabulary, a 512-token prompt
+    # (the MFMA prefill and prompt attention over 8 cache blocks), then 6 greedy tokens
+    # teacher-forced through the oracle; weights generated on the device, copied for the oracle
+    _say("decoder, 36 layers, 512-token prompt", act, cache)
+    _check_against_oracle(QWEN_36L, act, cache, tol, prompt_len=512, new_tokens=6, seed=syn.BASE_SEED + 63,
+                          device=DEV)
 
 
 def test_graph_replay_matches_eager_and_forward_step():
