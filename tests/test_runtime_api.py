@@ -323,3 +323,31 @@ def test_projection_group_declines_layers_it_cannot_launch_together():
     assert prepare_hip_projection_group(tuple(foreign)) is None
     assert prepare_hip_projection_group(tuple(foreign[:1])) is None
     assert prepare_hip_projection_group(tuple(foreign * 3)) is None
+
+
+def test_linear_input_checks_follow_the_reference():
+    """HipPackedBackend.linear's input checks, each a ValueError raised before
+    any launch (src/nanoquant/runtime/cuda_backend.py:243-260): the layer's
+    device, a float dtype, last dimension == in_features, at least one token,
+    contiguous, no autograd."""
+
+    from nanoquant_amd.runtime.hip_backend import _check_value
+
+    spec = QuantizedLinearSpec("blocks.0.t", "nanoquant-v1", 8, 3, 4, "float32", "float16")
+    cpu = torch.device("cpu")
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        _check_value(torch.zeros(2, 8, dtype=dtype), spec, cpu)
+    _check_value(torch.zeros(3, 2, 8), spec, cpu)
+    cases = [
+        (torch.zeros(2, 8), torch.device("cuda", 0), "same device"),
+        (torch.zeros(2, 8, dtype=torch.int32), cpu, "dtype is unsupported"),
+        (torch.zeros(2, 7), cpu, "feature dimension"),
+        (torch.tensor(1.0), cpu, "feature dimension"),
+        (torch.zeros(0, 8), cpu, "at least one token"),
+        (torch.zeros(8, 2).t(), cpu, "contiguous"),
+        (torch.zeros(2, 16)[:, ::2], cpu, "contiguous"),
+        (torch.zeros(2, 8, requires_grad=True), cpu, "autograd"),
+    ]
+    for value, device, match in cases:
+        with pytest.raises(ValueError, match=match):
+            _check_value(value, spec, device)
