@@ -869,7 +869,7 @@ def main(argv=None) -> int:
     if args.gpus != 1 or world != 1:
         print(
             f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
-            "multi-GPU runs are not part of this build",
+            "the sharded path is described, not run, and this benchmark has no multi-GPU mode",
             file=sys.stderr,
         )
         return 2

@@ -49,7 +49,7 @@ typedef enum nq_status {
     NQ_ERR_WORKSPACE = -5,   /* workspace smaller than nq_linear_workspace_bytes */
     NQ_ERR_LAUNCH = -6,      /* hipLaunchKernel / hipGetLastError failure    */
     NQ_ERR_DEVICE = -7,      /* no HIP device or wrong architecture          */
-    NQ_ERR_UNSUPPORTED = -8, /* valid request this build does not implement  */
+    NQ_ERR_UNSUPPORTED = -8, /* valid request the library does not implement */
     NQ_ERR_SCRATCH = -9      /* nq_linear_static: the call needs more than
                                 NQ_STATIC_SCRATCH_BYTES of workspace         */
 } nq_status;

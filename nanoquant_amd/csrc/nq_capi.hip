@@ -15,7 +15,7 @@ extern "C" const char* nq_status_string(int status) {
         case NQ_ERR_WORKSPACE: return "workspace smaller than nq_linear_workspace_bytes";
         case NQ_ERR_LAUNCH: return "kernel launch failed";
         case NQ_ERR_DEVICE: return "no usable HIP device";
-        case NQ_ERR_UNSUPPORTED: return "request not implemented by this build";
+        case NQ_ERR_UNSUPPORTED: return "request not implemented by this library";
         case NQ_ERR_SCRATCH: return "request needs more workspace than the static scratch array (NQ_STATIC_SCRATCH_BYTES)";
         default: return "unknown status";
     }

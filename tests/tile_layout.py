@@ -1,6 +1,6 @@
 """numpy restatement of the GPU tile layout written by ``nq_prepare_tiles``.
 
-The layout is this build's own (not the reference's); the GPU tests compare
+The layout is this package's own (not the reference's); the GPU tests compare
 the device builder against this function word for word. A sign matrix
 [rows, cols] is cut into 16-row tiles and 512-column chunks (the last chunk
 128, 256, 384 or 512 columns wide). Lane ``l = 16*g + n`` of tile ``t`` owns row
