@@ -1,7 +1,7 @@
 """CPU oracle for the batch-1 decoder shell around the packed linears — TEST
 INFRASTRUCTURE ONLY.
 
-This module is the checker, never the product: only ``tests/``,
+This module checks the product and is never part of it: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.
 

@@ -1,6 +1,6 @@
 """CPU oracle for the packed binary low-rank linear — TEST INFRASTRUCTURE ONLY.
 
-This module is the checker, never the product: only ``tests/``,
+This module checks the product and is never part of it: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it. The shipped path (``nanoquant_amd``) never imports it and has no CPU
 fallback.
