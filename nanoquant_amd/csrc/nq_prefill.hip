@@ -828,16 +828,19 @@ constexpr int64_t kResidentSmall = 1024;  // the 64 x 128 block: four per CU
 constexpr double kStepNsSmall = 500.0;    // half the MFMA and A work of a 128-row step
 constexpr int64_t kMinSliceBlocks = 2;
 constexpr double kStepNs = 1000.0;
-constexpr double kReduceNs = 3000.0;
+constexpr double kReduceNsSmall = 3000.0;  // the reduce launch after 64 x 128 blocks
+constexpr double kReduceNs = 6000.0;       // and after 128-row blocks (measured: 2.5% faster at
+                                           // 256 tokens than 3000, the same above)
 constexpr double kPartialBytesPerNs = 8000.0;
 
 struct Split {
     int64_t slices, k_per_split;
 };
 
-// Resident workgroups and K-step cost of the block tile used for `tokens`.
+// Resident workgroups, K-step cost and reduce cost of the block tile used for `tokens`.
 int64_t resident_for(int64_t tokens) { return tokens <= kBM / 2 ? kResidentSmall : kResident; }
 double step_ns_for(int64_t tokens) { return tokens <= kBM / 2 ? kStepNsSmall : kStepNs; }
+double reduce_ns_for(int64_t tokens) { return tokens <= kBM / 2 ? kReduceNsSmall : kReduceNs; }
 
 Split split_for(int64_t tiles, int64_t k_blocks, int64_t tokens, int64_t n) {
     const int64_t resident = resident_for(tokens);
@@ -852,7 +855,7 @@ Split split_for(int64_t tiles, int64_t k_blocks, int64_t tokens, int64_t n) {
         const int64_t rounds = (tiles * s.slices + resident - 1) / resident;
         double ns = static_cast<double>(rounds * (s.k_per_split + 1)) * step_ns;
         if (s.slices > 1)
-            ns += kReduceNs + 2.0 * static_cast<double>(s.slices * tokens * n * 4) / kPartialBytesPerNs;
+            ns += reduce_ns_for(tokens) + 2.0 * static_cast<double>(s.slices * tokens * n * 4) / kPartialBytesPerNs;
         if (best_ns < 0.0 || ns < best_ns) best = s, best_ns = ns;
     }
     return best;
@@ -890,7 +893,8 @@ void batch_splits(int count, const int64_t* tiles, const int64_t* k_blocks, cons
         }
         const int64_t rounds = (wgs + resident_for(tokens) - 1) / resident_for(tokens);
         double ns = static_cast<double>(rounds * (steps + 1)) * step_ns_for(tokens);
-        if (partial_elems > 0) ns += kReduceNs + 2.0 * static_cast<double>(partial_elems * 4) / kPartialBytesPerNs;
+        if (partial_elems > 0)
+            ns += reduce_ns_for(tokens) + 2.0 * static_cast<double>(partial_elems * 4) / kPartialBytesPerNs;
         if (best_ns < 0.0 || ns < best_ns) {
             best_ns = ns;
             for (int i = 0; i < count; ++i) out[i] = cand[i];
