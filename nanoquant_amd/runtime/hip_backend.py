@@ -12,7 +12,7 @@ stream through the C ABI; it never synchronises, transfers or unpacks.
 from __future__ import annotations
 
 import ctypes
-from dataclasses import dataclass, field, replace
+from dataclasses import MISSING, dataclass, field, fields, replace
 
 import torch
 
@@ -61,6 +61,36 @@ class _HipPackedPayload:
 
 def _to_device(tensor: torch.Tensor | None, device: torch.device) -> torch.Tensor | None:
     return None if tensor is None else tensor.to(device=device).contiguous()
+
+
+_OWN_STATES = (RowSidecarLayerState, PackedLayerState, MixedVLayerState, ProductCodebookLayerState)
+# Tried in this order; no state kind carries all the required fields of another.
+_ADOPTABLE_STATES = (MixedVLayerState, ProductCodebookLayerState, PackedLayerState)
+
+
+def adopt_layer_state(state: object) -> RuntimeLayerState:
+    """This package's state object for ``state``.
+
+    The reference planner prepares layers with its own ``PackedLayerState``,
+    ``MixedVLayerState`` and ``ProductCodebookLayerState``
+    (src/nanoquant/runtime/planning.py:273-299 -> backend.prepare), whose
+    classes this package does not import. A state is recognised by the
+    reference's field names (src/nanoquant/runtime/packed.py:231-244,
+    mixed_v.py:169-187, product_codebook.py:147-164) and rebuilt as the
+    matching class here, which re-checks every invariant. The caller's ``spec``
+    object is kept, so ``PreparedLayer.spec`` compares equal to the state's
+    spec as the reference planner requires (planning.py:255-256). Objects
+    lacking a kind's required fields raise ``TypeError``."""
+
+    if isinstance(state, _OWN_STATES):
+        return state
+    for cls in _ADOPTABLE_STATES:
+        names = fields(cls)
+        required = [f.name for f in names if f.default is MISSING]
+        if all(hasattr(state, name) for name in required):
+            return cls(**{f.name: getattr(state, f.name, None) for f in names})
+    raise TypeError("HIP packed backend requires PackedLayerState, RowSidecarLayerState, MixedVLayerState "
+                    "or ProductCodebookLayerState (or an object with their fields)")
 
 
 def _device_arch(index: int) -> str:
@@ -163,9 +193,7 @@ class HipPackedBackend:
         right factors (mixed-V, product codebook) are expanded on the device, as
         the reference backend does for mixed-V (src/nanoquant/runtime/cuda_backend.py:199-241)."""
 
-        if not isinstance(state, (RowSidecarLayerState, PackedLayerState, MixedVLayerState, ProductCodebookLayerState)):
-            raise TypeError("HIP packed backend requires PackedLayerState, RowSidecarLayerState, MixedVLayerState "
-                            "or ProductCodebookLayerState")
+        state = adopt_layer_state(state)
         target = torch.device(device)
         if target.type != "cuda":
             raise ValueError("HIP packed backend preparation requires a CUDA (HIP) device")

@@ -427,6 +427,33 @@ def test_selection_and_module_on_gpu(backend):
     assert out.dtype == torch.bfloat16
 
 
+@pytest.mark.parametrize("tokens", [1, 4, 64])
+def test_reference_state_objects_run_through_prepare_and_linear(backend, tokens):
+    """States and specs of another class with the reference's field names
+    (src/nanoquant/runtime/packed.py:231-244, backend.py:27-73), as the
+    reference planner passes them to ``backend.prepare``
+    (src/nanoquant/runtime/planning.py:249-257): the prepared layer carries the
+    caller's spec, and ``linear`` matches the oracle and, bit for bit, the same
+    layer prepared from this package's own state."""
+
+    from foreign_state import foreign_copy
+
+    shape = syn.qwen3_8b_layer()[1]  # k_proj, rank 819 (word tail 19)
+    state = syn.synthetic_packed_layer(shape, seed=syn.BASE_SEED + 71, salient=5, salient_dtype=torch.int8,
+                                       bias=True)
+    foreign = foreign_copy(state)
+    _say("foreign state", shape.name, tokens, backend.name)
+    layer = backend.prepare(foreign, "cuda")
+    assert layer.spec == foreign.spec and layer.spec is foreign.spec
+    assert (layer.backend_name, layer.backend_version) == (backend.name, backend.version)
+    own = backend.prepare(state, "cuda")
+    x = syn.synthetic_activations(tokens, shape.in_features, seed=tokens).cuda()
+    y = backend.linear(x, layer)
+    assert torch.equal(y, backend.linear(x, own))
+    _assert_parity(backend, y, orc.packed_forward(orc.operands_from_state(foreign), x.cpu()),
+                   ("foreign", tokens))
+
+
 def test_hip_graph_capture_replays_match_eager(backend):
     shape = syn.qwen3_8b_layer()[1]
     state = syn.synthetic_packed_layer(shape, seed=7)

@@ -351,3 +351,96 @@ def test_linear_input_checks_follow_the_reference():
     for value, device, match in cases:
         with pytest.raises(ValueError, match=match):
             _check_value(value, spec, device)
+
+
+# --- the reference's own objects (stand-ins with its field names) -------------------
+
+
+def test_supports_reads_reference_spec_and_workload_objects(monkeypatch):
+    """``supports`` gives a spec and workload of another class (the
+    reference's field names, src/nanoquant/runtime/backend.py:27-91) the same
+    codes as this package's own, in the reference's order."""
+
+    from foreign_state import ForeignWorkload, foreign_spec
+
+    backend = HipPackedBackend()
+    own_work = WorkloadSpec("decode", "cuda", "bfloat16", 1, 1, deterministic=True)
+    work = ForeignWorkload("decode", "cuda", "bfloat16", 1, 1, deterministic=True)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    cases = [
+        (_spec(), work),
+        (_spec(), replace(work, device_type="cpu")),
+        (_spec(), replace(work, input_dtype="int8")),
+        (replace(_spec(), logical_format="x"), work),
+        (replace(_spec(), factor_dtype="float64"), work),
+        (replace(_spec(), outlier_value_dtype="float64"), work),
+        (_spec(), replace(work, kind="prefill", token_count=64)),
+    ]
+    codes = []
+    for spec, workload in cases:
+        own = backend.supports(spec, WorkloadSpec(**{k: getattr(workload, k) for k in WorkloadSpec.__slots__}))
+        got = backend.supports(foreign_spec(spec), workload)
+        assert got == own
+        codes.append(got.code)
+    assert codes == ["NQ-INF-DEVICE-UNAVAILABLE", "NQ-INF-DEVICE", "NQ-INF-INPUT-DTYPE", "NQ-INF-FORMAT",
+                     "NQ-INF-FACTOR-DTYPE", "NQ-INF-OUTLIER-DTYPE", "NQ-INF-DEVICE-UNAVAILABLE"]
+    monkeypatch.setattr(_native, "library_available", lambda: False)
+    assert backend.supports(foreign_spec(_spec()), work).code == "NQ-INF-HIP-KERNEL"
+    assert own_work.kind == work.kind
+
+
+def test_prepare_accepts_reference_state_objects():
+    """A state of another class with the reference's field names
+    (src/nanoquant/runtime/packed.py:231-244) passes the backend's type
+    check: on a CPU device ``prepare`` stops at the device check, as for this
+    package's own state. The adopted state keeps the caller's spec object,
+    which the reference planner compares with the prepared layer's spec
+    (src/nanoquant/runtime/planning.py:255-256)."""
+
+    from foreign_state import ForeignPackedLayerState, foreign_copy
+    from nanoquant_amd.runtime.hip_backend import adopt_layer_state
+
+    state = synthetic_packed_layer(qwen3_8b_layer()[1], seed=5)
+    foreign = foreign_copy(state)
+    assert not isinstance(foreign, PackedLayerState) and not isinstance(foreign.spec, QuantizedLinearSpec)
+    backend = HipPackedBackend()
+    for candidate in (state, foreign):
+        with pytest.raises(ValueError, match="requires a CUDA"):
+            backend.prepare(candidate, "cpu")
+    adopted = adopt_layer_state(foreign)
+    assert isinstance(adopted, PackedLayerState) and adopted.spec is foreign.spec
+    for name in ("left_words", "right_words", "scale_pre", "scale_mid", "scale_post"):
+        assert getattr(adopted, name) is getattr(foreign, name)
+    assert adopt_layer_state(state) is state
+    # an object without the reference's fields is still refused by type
+    for bad in (object(), {"spec": foreign.spec}, state.spec):
+        with pytest.raises(TypeError, match="requires PackedLayerState"):
+            backend.prepare(bad, "cpu")
+    # the invariants are checked again on adoption: s_in must be 0 at a salient column
+    salient = synthetic_packed_layer(qwen3_8b_layer()[1], seed=5, salient=3)
+    broken = foreign_copy(salient)
+    pre = broken.scale_pre.clone()
+    pre[int(broken.outlier_indices[0])] = 1.0
+    broken = ForeignPackedLayerState(**{**{k: getattr(broken, k) for k in broken.__slots__}, "scale_pre": pre})
+    with pytest.raises(ValueError, match="salient"):
+        adopt_layer_state(broken)
+
+
+def test_prepare_accepts_reference_mixed_v_state_objects():
+    """A mixed-V state of another class (src/nanoquant/runtime/mixed_v.py:169-187)
+    is adopted as this package's MixedVLayerState and expands to the same
+    packed words."""
+
+    from foreign_state import ForeignMixedVLayerState, foreign_copy
+    from nanoquant_amd.runtime.codecs import MixedVLayerState
+    from nanoquant_amd.runtime.hip_backend import adopt_layer_state
+
+    from test_codecs import _mixed_fixture
+
+    state = _mixed_fixture()[0]
+    foreign = foreign_copy(state, ForeignMixedVLayerState)
+    adopted = adopt_layer_state(foreign)
+    assert isinstance(adopted, MixedVLayerState) and adopted.spec is foreign.spec
+    assert torch.equal(adopted.to_packed().right_words, state.to_packed().right_words)
+    with pytest.raises(ValueError, match="requires a CUDA"):
+        HipPackedBackend().prepare(foreign, "cpu")
