@@ -88,8 +88,19 @@ int64_t lmq_bytes_for(const MatGeo& g2, int64_t tokens) {
     return lmq_bytes<4, 4>(g2);
 }
 
+int64_t round256(int64_t n) { return (n + 255) & ~int64_t(255); }
+
+// Several tokens: stage 0's operands of x * s_in (xq, sized for four token
+// blocks above four tokens) and its per-(chunk, token) exponents and maxima.
+int64_t xq_bytes_for(const MatGeo& g1, int64_t tokens) {
+    return tokens == 1 ? 0 : g1.nc * (tokens <= 4 ? 1 : 4) * Ops<4>::kBytes;
+}
+int64_t xe_bytes_for(const MatGeo& g1, int64_t tokens) { return tokens == 1 ? 0 : round256(g1.nc * kMaxTokens * 4); }
+
+// Workspace: [lmq][lme: 256 B][xq][xe][xm] (the last three for several tokens).
 int64_t scratch_bytes(const TilesGeometry& g, int64_t tokens) {
-    return ((lmq_bytes_for(g.g2, tokens) + 255) & ~int64_t(255)) + 256;
+    return round256(lmq_bytes_for(g.g2, tokens)) + 256 + round256(xq_bytes_for(g.g1, tokens)) +
+           2 * xe_bytes_for(g.g1, tokens);
 }
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -141,8 +152,17 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
     a.bias_dtype = d->bias_dtype;
     a.y = y;
     a.y_dtype = y_dtype;
-    a.lmq = static_cast<uint8_t*>(scratch);
-    a.lme = reinterpret_cast<int*>(static_cast<char*>(scratch) + ((lmq_bytes_for(g.g2, tokens) + 255) & ~int64_t(255)));
+    char* const ws = static_cast<char*>(scratch);
+    const int64_t lme_at = round256(lmq_bytes_for(g.g2, tokens));
+    const int64_t xq_at = lme_at + 256;
+    const int64_t xe_at = xq_at + round256(xq_bytes_for(g.g1, tokens));
+    a.lmq = reinterpret_cast<uint8_t*>(ws);
+    a.lme = reinterpret_cast<int*>(ws + lme_at);
+    if (tokens > 1) {
+        a.xq = reinterpret_cast<uint8_t*>(ws + xq_at);
+        a.xe = reinterpret_cast<int*>(ws + xe_at);
+        a.xm = reinterpret_cast<float*>(ws + xe_at + xe_bytes_for(g.g1, tokens));
+    }
     return NQ_OK;
 }
 
@@ -165,6 +185,19 @@ void pick_waves(int64_t nc, int tpb, int tb, int& nw, int& kc) {
         nw = static_cast<int>(nc < 8 ? nc : 8);
         kc = (tb == 1 && nc > 8) ? 2 : 1;
     }
+}
+
+// The same for the several-token stages of the split launch: at most eight
+// waves, two per chunk slot with four token blocks (blocks_per_wave); with one
+// token block two chunks per wave per pass when the slots would not cover the
+// chunks (a wave holding two blocks has no registers for a second chunk).
+void pick_waves_multi(int64_t nc, int tb, int& nw, int& kc) {
+    const int ng = tb > 2 ? 2 : 1;
+    const int64_t max_slots = 8 / ng;
+    kc = nc > max_slots && tb == 1 ? 2 : 1;
+    int64_t slots = (nc + kc - 1) / kc;
+    if (slots > max_slots) slots = max_slots;
+    nw = static_cast<int>(slots) * ng;
 }
 
 // Dynamic LDS of a stage: per-wave operand areas (stage 1), the partial sums
@@ -199,6 +232,27 @@ int pick_tiles(int stage, int64_t tiles, int nw, int kc, int tb, bool fused) {
     for (int tw = 1; tw < 4; ++tw)
         if (waves <= kStage2Waves * tw) return tw;
     return 4;
+}
+
+// Tokens from which the split launch stages x * s_in in a kernel of its own
+// (stage 0) instead of in every stage-1 workgroup. Measured on MI355X over the
+// Qwen3-8B decode stack (us per layer, in-kernel staging against stage 0):
+// 2 tokens 50.8 / 59.0, 4 tokens 50.1 / 59.3, 8 tokens 93.8 / 76.3,
+// 16 tokens 132.2 / 105.1: below two token blocks the extra launch costs more
+// than the staging it saves.
+constexpr int64_t kStage0Tokens = 5;
+bool stage0_path(int64_t tokens) { return tokens >= kStage0Tokens; }
+
+// Tiles per workgroup of the several-token stages: a wave's A operands (8 KB
+// per block of four tokens per chunk) are shared by its TW tiles, against
+// fewer waves. One token block (stage 2 after the in-kernel staging): four
+// tiles from 4096 waves, two from 2048. Two or four blocks (stage 0 path):
+// two tiles in both stages (measured best against one and four, per stage,
+// at 8 and 16 tokens).
+int pick_tiles_multi(int64_t tiles, int nw, int tb) {
+    if (tb > 1) return 2;
+    const int64_t waves = tiles * nw;
+    return waves >= 4 * 1024 ? 4 : (waves >= 2 * 1024 ? 2 : 1);
 }
 
 int enqueue_stage1(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
@@ -282,7 +336,8 @@ int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
     }
     LaunchShape s1{}, s2{};
     s1.tpb = s2.tpb = tokens == 1 ? 1 : 4;
-    s1.tb = s2.tb = tokens <= 4 ? 1 : 4;
+    // Blocks of four tokens: 1, 2 or 4 in the split launch, 1 or 4 fused.
+    s1.tb = s2.tb = tokens <= 4 ? 1 : (tokens <= 8 && !fused && stage0_path(tokens) ? 2 : 4);
     s1.ak = s2.ak = ak;
     if (fused) {
         int kc_unused = 0;
@@ -291,10 +346,23 @@ int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
         s1.kc2 = (s1.tb == 1 && nc2 > s1.nw) ? 2 : 1;
         s1.tw = 1;
     } else {
-        pick_waves(nc1, s1.tpb, s1.tb, s1.nw, s1.kc);
-        pick_waves(nc2, s2.tpb, s2.tb, s2.nw, s2.kc);
-        s1.tw = pick_tiles(1, tiles1, s1.nw, s1.kc, s1.tb, false);
-        s2.tw = pick_tiles(2, tiles2, s2.nw, s2.kc, s2.tb, false);
+        if (!stage0_path(tokens)) {
+            pick_waves(nc1, s1.tpb, s1.tb, s1.nw, s1.kc);
+            pick_waves(nc2, s2.tpb, s2.tb, s2.nw, s2.kc);
+            s1.tw = pick_tiles(1, tiles1, s1.nw, s1.kc, s1.tb, false);
+            s2.tw = tokens == 1 ? pick_tiles(2, tiles2, s2.nw, s2.kc, s2.tb, false)
+                                : pick_tiles_multi(tiles2, s2.nw, s2.tb);
+        } else {
+            pick_waves_multi(nc1, s1.tb, s1.nw, s1.kc);
+            pick_waves_multi(nc2, s2.tb, s2.nw, s2.kc);
+            s1.tw = pick_tiles_multi(tiles1, s1.nw, s1.tb);
+            s2.tw = pick_tiles_multi(tiles2, s2.nw, s2.tb);
+            // Partial sums within 64 KB of LDS.
+            while (s1.tw > 1 && nc1 * s1.tw * s1.tb * 256 + nc1 * kMaxTokens * 4 > 65536) s1.tw >>= 1;
+            while (s2.tw > 1 && static_cast<int64_t>(lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, s2.kc, nc2, ks,
+                                                               static_cast<int>(tokens))) > 65536)
+                s2.tw >>= 1;
+        }
     }
     batch.tw1 = s1.tw;
     batch.tw2 = fused ? 1 : s2.tw;
@@ -333,9 +401,21 @@ int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t s
         s1.grid = dim3(static_cast<unsigned>(max1 > max2 ? max1 : max2), 2 * count);
         return enqueue_fused(batch, s1, stream);
     }
-    s1.lds = lds_bytes(1, s1.tpb, s1.tb, s1.tw, s1.nw, s1.kc, nc1);
     s1.grid = dim3(xcd_grid(max1), count);
-    st = enqueue_stage1(batch, s1, stream);
+    if (stage0_path(tokens)) {
+        // Stage 0 stages x * s_in once per (chunk, token block); stage 1 reads
+        // its operands.
+        LaunchShape s0 = s1;
+        const int64_t items = nc1 * ((tokens + 3) / 4);
+        s0.grid = dim3(static_cast<unsigned>((items + 3) / 4), count);
+        st = enqueue_stage0(batch, s0, stream);
+        if (st != NQ_OK) return st;
+        s1.lds = static_cast<size_t>(nc1) * s1.tw * s1.tb * 64 * 4 + static_cast<size_t>(nc1) * kMaxTokens * 4;
+        st = enqueue_stage1m(batch, s1, stream);
+    } else {
+        s1.lds = lds_bytes(1, s1.tpb, s1.tb, s1.tw, s1.nw, s1.kc, nc1);
+        st = enqueue_stage1(batch, s1, stream);
+    }
     if (st != NQ_OK) return st;
     s2.lds = lds_bytes(2, s2.tpb, s2.tb, s2.tw, s2.nw, s2.kc, nc2, ks, static_cast<int>(tokens));
     if (pair) {

@@ -68,7 +68,10 @@
 // Launch structure (nq_linear_desc.decode_launch):
 //   split (default): kernel 1 runs the stage-1 tiles of every linear in the
 //     batch and writes the stage-2 operands; kernel 2 runs the stage-2 tiles. The kernel
-//     boundary is the grid-wide barrier.
+//     boundary is the grid-wide barrier. From five tokens a kernel 0 first
+//     stages x * s_in once per (chunk, token block) and kernel 1 loads those
+//     operands instead of staging them in every workgroup (k_decode_stage0,
+//     k_decode_stage1m below).
 //   fused: one kernel whose first grid rows are the stage-1 workgroups and
 //     the rest the stage-2 workgroups. Stage-1 workgroups store the operands
 //     at agent scope and then signal; stage-2 workgroups issue their U loads,
@@ -209,6 +212,14 @@ struct LinArgs {
     int attn_blocks;            // cache blocks of kAttnBlockRows rows
     int attn_hd_log2;           // log2(head_dim)
     int64_t attn_max_positions;
+    // Several tokens (split launch): stage 0 writes the stage-1 A operands of
+    // x * s_in here in the lmq layout (3 digit rows per token, the fourth
+    // zero), with the exponent and max |x s_in| of every (chunk, token) at
+    // [chunk * kMaxTokens + token].
+    uint8_t* xq;
+    int* xe;
+    float* xm;
+    void* pad_;
 };
 static_assert(sizeof(LinArgs) % 16 == 0, "LinArgs is read as 16-byte vectors");
 
@@ -290,6 +301,9 @@ __device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
     a.attn_blocks = s.attn_blocks;
     a.attn_hd_log2 = s.attn_hd_log2;
     a.attn_max_positions = s.attn_max_positions;
+    a.xq = s.xq;
+    a.xe = s.xe;
+    a.xm = s.xm;
     // One statement, so every field is waited for at the same point; it
     // redefines the integer fields, so no arithmetic on them can be hoisted
     // above it (the pointers are only read, so they stay known-global).
@@ -298,7 +312,7 @@ __device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
                    "+s"(a.g2.nt), "+s"(a.g2.nb), "+s"(a.g2.nc), "+s"(a.nwg1), "+s"(a.nwg2), "+s"(a.x_dtype),
                    "+s"(a.tokens), "+s"(a.scale_dtype), "+s"(a.bias_dtype), "+s"(a.nw1), "+s"(a.nw2)
                  : "s"(a.v_tiles), "s"(a.u_tiles), "s"(a.header), "s"(a.x), "s"(a.s_in), "s"(a.s_mid), "s"(a.s_out),
-                   "s"(a.bias), "s"(a.lmq), "s"(a.lme));
+                   "s"(a.bias), "s"(a.lmq), "s"(a.lme), "s"(a.xq), "s"(a.xe), "s"(a.xm));
     return a;
 }
 // Activation kinds (template parameter AK): how stage 1 reads a[t, k].
@@ -656,20 +670,13 @@ __device__ __forceinline__ void wave_lds_sync() {
 // wave's LDS area.
 constexpr int kS2SpreadBytes = 8 * 4 * 4 * 16;
 
+// (One token; several tokens load each MFMA's operand directly, in stage2_wg.)
 template <int TPB, int TB, int TW>
 __device__ __forceinline__ void load_s2_ops(S2Regs<TB, TW>& r, const LinArgs& a, int c, int lane) {
-    if constexpr (TPB == 1) {
-        const uint8_t* src = a.lmq + lmq_offset<1, TB>(c, 0, 0, 0, 0);
-        r.a[0][0] = *reinterpret_cast<const v4i*>(src + 16 * lane);
-        r.a[0][1] = *reinterpret_cast<const v4i*>(src + kS2SpreadBytes / 2 + 16 * lane);
-    } else {
-        const int row = lane & 15;
-#pragma unroll
-        for (int tb = 0; tb < TB; ++tb)
-#pragma unroll
-            for (int m = 0; m < 8; ++m)
-                r.a[tb][m] = *reinterpret_cast<const v4i*>(a.lmq + lmq_offset<TPB, TB>(c, tb, m, row, lane >> 4));
-    }
+    static_assert(TPB == 1 && TB == 1, "one token per launch");
+    const uint8_t* src = a.lmq + lmq_offset<1, TB>(c, 0, 0, 0, 0);
+    r.a[0][0] = *reinterpret_cast<const v4i*>(src + 16 * lane);
+    r.a[0][1] = *reinterpret_cast<const v4i*>(src + kS2SpreadBytes / 2 + 16 * lane);
 }
 
 // One token: the two loaded vectors through this wave's LDS area (kS2SpreadBytes)
@@ -923,6 +930,44 @@ __device__ __forceinline__ float tile_partial(const v4i (&A)[8], const v4i& S, v
               65536.0f * static_cast<float>(diff[2]);
     if (NDIG == 4) v += 16777216.0f * static_cast<float>(diff[3]);
     return v * scale;
+}
+
+// tile_partial for TB operand blocks (four tokens each) against one tile's
+// words: each sign-expansion AND feeds the blocks' MFMAs, so a block costs
+// eight MFMAs and its conversion. Every block is computed (a uniform guard
+// per block costs the compiler's register copies more than an unused
+// block's MFMAs); the caller stores the live ones. Integer results, and so
+// the partials, equal tile_partial's.
+template <int NDIG, int TB>
+__device__ __forceinline__ void tile_partials(const v4i (&A)[TB][8], const v4i (&S)[TB], v4u w, int dw,
+                                              const float (&scale)[TB], float (&out)[TB]) {
+    w[1] &= dw > 1 ? ~0u : 0u;
+    w[2] &= dw > 2 ? ~0u : 0u;
+    w[3] &= dw > 3 ? ~0u : 0u;
+    v4i t0[TB], t1[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) t0[tb] = t1[tb] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int m = 0; m < 8; m += 2) {
+        const uint32_t k0 = 0x01010101u << m, k1 = 0x01010101u << (m + 1);
+        const v4i b0 = v4i{static_cast<int>(w[0] & k0), static_cast<int>(w[1] & k0), static_cast<int>(w[2] & k0),
+                           static_cast<int>(w[3] & k0)};
+        const v4i b1 = v4i{static_cast<int>(w[0] & k1), static_cast<int>(w[1] & k1), static_cast<int>(w[2] & k1),
+                           static_cast<int>(w[3] & k1)};
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) {
+            t0[tb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tb][m], b0, t0[tb], 0, 0, 0);
+            t1[tb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[tb][m + 1], b1, t1[tb], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+        const v4i diff = S[tb] - 2 * (t0[tb] + t1[tb]);
+        float v = static_cast<float>(diff[0]) + 256.0f * static_cast<float>(diff[1]) +
+                  65536.0f * static_cast<float>(diff[2]);
+        if (NDIG == 4) v += 16777216.0f * static_cast<float>(diff[3]);
+        out[tb] = v * scale[tb];
+    }
 }
 
 __device__ __forceinline__ void hdr_store(uint32_t* header, int word, uint32_t v) {
@@ -1216,6 +1261,189 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
     }
 }
 
+// ---------------------------------------------------------------------------
+// Several tokens (2-16), split launch: stage 0 + stage 1 from operands.
+//
+// With several tokens the staging of x * s_in (about 110 VALU instructions per
+// token, chunk and wave) is repeated by every stage-1 workgroup, one per tile
+// group, and a stage-1 wave's A operands grow to 8 KB per block of four
+// tokens per chunk against 1 KB of sign words per tile. Stage 0 therefore
+// stages every (chunk, token block) once per call, with stage_block's
+// arithmetic, into xq (the lmq layout with TB blocks; each token's fourth
+// digit row zero) and records every (chunk, token)'s exponent (xe) and max
+// |x s_in| (xm). Stage 1 then loads its A operands like stage 2 and takes TW
+// tiles per wave, one sign expansion feeding every token block
+// (tile_partials). The digits, exponents, integer partials and their
+// chunk-order sums are those of stage1_wg, so the results are bit-identical.
+// ---------------------------------------------------------------------------
+
+// Element size of x for kind AK (the generic kind: its runtime dtype).
+template <int AK>
+__device__ __forceinline__ int act_elem_bytes(int x_dtype) {
+    if constexpr (AK == kActGeneric) return x_dtype == NQ_DTYPE_F32 ? 4 : 2;
+    else return act_dtype<AK>() == NQ_DTYPE_F32 ? 4 : 2;
+}
+
+// Stage 0 of (chunk c, token block tb) in a layout of tbl blocks: one wave.
+template <int AK>
+__device__ __forceinline__ void stage0_wave(const LinArgs& a, int c, int tb, int tbl, int lane) {
+    constexpr int TPB = 4;
+    LinArgs b = a;
+    b.x = static_cast<const char*>(a.x) +
+          static_cast<int64_t>(tb) * TPB * a.in * act_elem_bytes<AK>(a.x_dtype);
+    b.tokens = a.tokens - TPB * tb < TPB ? a.tokens - TPB * tb : TPB;
+    S1Regs<AK, TPB, 1> r;
+    load_s1_acts<AK, TPB, 1>(r, b, c, lane);
+    char* const ops = reinterpret_cast<char*>(a.xq) + (c * tbl + tb) * Ops<TPB>::kBytes;
+    int expo[TPB];
+    float cm[TPB];
+    stage_block<AK, TPB, 1, TPB>(r, b, c, 0, ops, lane, expo, cm);
+    const int m = lane >> 3, d = (lane >> 1) & 3, h = lane & 1;
+#pragma unroll
+    for (int u = 0; u < TPB; ++u)
+#pragma unroll
+        for (int run = 0; run < 2; ++run)
+            *reinterpret_cast<uint32_t*>(ops + ((m * Ops<TPB>::kRows + 4 * u + 3) * 4 + 2 * h + run) * 16 + 4 * d) = 0;
+    int e = expo[0];
+    float mx = cm[0];
+#pragma unroll
+    for (int u = 1; u < TPB; ++u) {
+        e = lane == u ? expo[u] : e;
+        mx = lane == u ? cm[u] : mx;
+    }
+    if (lane < TPB) {
+        a.xe[c * kMaxTokens + TPB * tb + lane] = e;
+        a.xm[c * kMaxTokens + TPB * tb + lane] = mx;
+    }
+}
+
+// Token blocks per wave and wave groups per chunk of the several-token
+// kernels: a wave holds the A operands of at most two token blocks (64
+// VGPRs per chunk), so with four blocks two waves share each chunk, wave w
+// taking blocks 2 (w % 2) and 2 (w % 2) + 1 of chunk slot w / 2.
+template <int TB>
+constexpr int blocks_per_wave() { return TB > 2 ? 2 : TB; }
+template <int TB>
+constexpr int wave_groups() { return TB / blocks_per_wave<TB>(); }
+
+// One stage-1 workgroup of the several-token path: tiles [t0, t0 + TW) of
+// linear `a`, operands from xq; TB blocks of four tokens in the layout.
+template <int TB, int TW, int KC>
+__device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __restrict__ lds) {
+    constexpr int TPB = 4;
+    constexpr int TBW = blocks_per_wave<TB>(), NG = wave_groups<TB>();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int grp = wave % NG, slot = wave / NG;
+    const int nw = a.nw1;
+    const int nslots = nw / NG;
+    const int nthreads = nw * 64;
+    const int tokens = a.tokens;
+    const int nblk = (tokens + TPB - 1) / TPB;
+    const int nwg = static_cast<int>(a.nwg1);
+    const bool dead = wg_in >= nwg;  // computes the last workgroup's tiles, stores nothing
+    const int wg = dead ? nwg - 1 : wg_in;
+    const int t0 = wg * TW;
+    const int nt = static_cast<int>(a.g1.nt), nb = static_cast<int>(a.g1.nb), nc = static_cast<int>(a.g1.nc);
+    const int rank = static_cast<int>(a.rank);
+    float* const red = reinterpret_cast<float*>(lds);
+    float* const cmx = red + nc * TW * TB * 64;  // [nc][kMaxTokens] max |x s_in|
+    const int nxm = nc * kMaxTokens;
+
+    const int outs = TW * tokens * kTileRows;
+    const OutIdx f = out_index<TPB>(threadIdx.x < outs ? threadIdx.x : 0, tokens);
+    const int fr = (t0 + f.tt) * kTileRows + f.n;
+    RawElem rs0;
+    float maxsm = 0.0f, xmv = 0.0f;
+
+    // This wave's token blocks are grp * TBW + i, i < gblk.
+    const int gblk0 = nblk - grp * TBW;
+    const int gblk = gblk0 < 0 ? 0 : (gblk0 > TBW ? TBW : gblk0);
+    const auto pass = [&](const int base, const bool first) __attribute__((always_inline)) {
+        const PassChunks<KC> pc = pass_chunks<KC>(base, slot, nslots, nc);
+        S2Regs<TBW, TW> r[KC];
+        int e[KC][TBW];
+#pragma unroll
+        for (int j = 0; j < KC; ++j) load_words(r[j].w, a.v_tiles, nt, nb, t0, pc.c[j], lane);
+        // Every block of the wave's group is loaded (xq holds TB blocks per
+        // chunk); blocks past the last token are computed and not stored.
+#pragma unroll
+        for (int j = 0; j < KC; ++j)
+#pragma unroll
+            for (int i = 0; i < TBW; ++i) {
+                const int tb = grp * TBW + i;
+#pragma unroll
+                for (int m = 0; m < 8; ++m)
+                    r[j].a[i][m] = *reinterpret_cast<const v4i*>(
+                        a.xq + lmq_offset<TPB, TB>(pc.c[j], tb, m, lane & 15, lane >> 4));
+                e[j][i] = a.xe[pc.c[j] * kMaxTokens + TPB * tb + (lane >> 4)];
+            }
+        if (first) {
+            const int frc = fr < rank ? fr : rank - 1;
+            rs0 = load_elem(a.s_mid, a.scale_dtype, frc);
+            maxsm = __uint_as_float(scalar_load(a.header + line_word(kMiscLine) + kMiscMaxMid));
+            xmv = a.xm[static_cast<int>(threadIdx.x) < nxm ? static_cast<int>(threadIdx.x) : 0];
+        }
+        __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+            if (!pc.live[j]) continue;  // uniform
+            const int c = pc.c[j];
+            const int dw = chunk_words32(nb, c);
+            v4i S[TBW];
+            float sc[TBW];
+#pragma unroll
+            for (int i = 0; i < TBW; ++i) {
+                S[i] = ones_mfma(r[j].a[i]);
+                sc[i] = exp2i(-e[j][i] - 7);
+            }
+#pragma unroll
+            for (int tt = 0; tt < TW; ++tt) {
+                float part[TBW];
+                tile_partials<3, TBW>(r[j].a, S, r[j].w[tt], dw, sc, part);
+#pragma unroll
+                for (int i = 0; i < TBW; ++i)
+                    if (i < gblk) red[((c * TW + tt) * TB + grp * TBW + i) * 64 + lane] = part[i];
+            }
+        }
+    };
+    const int step = nslots * KC;
+    pass(0, true);
+    for (int base = step; base < nc; base += step) pass(base, false);
+    if (static_cast<int>(threadIdx.x) < nxm) cmx[threadIdx.x] = xmv;
+    for (int i = static_cast<int>(threadIdx.x) + nthreads; i < nxm; i += nthreads) cmx[i] = a.xm[i];
+    __syncthreads();
+
+    if (dead) return;  // uniform, after the workgroup's only barrier
+
+    // Epilogue of stage1_wg (no input norm): lm = s_mid * Σ_chunks partial as
+    // stage-2 operands with the per-token exponent of max|s_mid| * Σ_c 512 * max_c.
+    for (int idx = threadIdx.x; idx < outs; idx += nthreads) {
+        const OutIdx o = out_index<TPB>(idx, tokens);
+        const int row = (t0 + o.tt) * kTileRows + o.n;
+        if (t0 + o.tt >= nt) continue;
+        float sum = 0.0f, bound = 0.0f;
+        for (int c = 0; c < nc; ++c) {
+            sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
+            bound += cmx[c * kMaxTokens + o.t];
+        }
+        const bool poison = !(bound <= 3.402823466e38f);
+        const int e = poison ? 0 : range_exponent(bound * (512.0f * maxsm), 21);
+        float v = 0.0f;
+        if (row < rank && !poison)
+            v = sum * elem_value(idx == static_cast<int>(threadIdx.x) ? rs0 : load_elem(a.s_mid, a.scale_dtype, row),
+                                 a.scale_dtype);
+        store_lmq<TPB, TB, false>(a.lmq, row, o.t, v, e);
+        if (wg == 0 && o.tt == 0 && o.n == 0) a.lme[o.t] = poison ? kPoisonExp : e;
+    }
+    if (t0 + TW >= nt) {
+        const int from = nt * kTileRows, to = static_cast<int>(a.g2.nc) * kChunkCols;
+        const int n = (to - from) * tokens;
+        for (int i = threadIdx.x; i < n; i += nthreads)
+            store_lmq<TPB, TB, false>(a.lmq, from + i / tokens, i % tokens, 0.0f, 0);
+    }
+}
+
 // Salient columns in the stage-2 epilogue. Up to kSalMax columns, the
 // workgroup's rows of W_sal (16 TW rows x k) and the gathered x[t, idx_k] *
 // scale_k of every token are loaded in the first pass, with the other
@@ -1252,11 +1480,21 @@ __device__ __forceinline__ float bits_value(uint32_t b, int dtype) {
 template <int TPB, int TB, int TW, int KC, bool FUSED, bool PAIR = false>
 __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __restrict__ lds,
                                           const LinArgs* pair = nullptr) {
+    // Split launch with four token blocks: two waves per chunk slot
+    // (blocks_per_wave); one token or the fused launch: one wave per slot.
+    constexpr int NG = (TPB == 4 && !FUSED) ? wave_groups<TB>() : 1;
+    constexpr int TBW = TB / NG;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int grp = wave % NG, slot = wave / NG;
     const int nw = a.nw2;
+    const int nslots = nw / NG;
     const int nthreads = nw * 64;  // the workgroup size (blockDim.x is a vector load of a hidden argument)
     const int tokens = a.tokens;
+    const int nblk = (tokens + TPB - 1) / TPB;
+    // This wave's token blocks are grp * TBW + i, i < gblk.
+    const int gblk0 = nblk - grp * TBW;
+    const int gblk = gblk0 < 0 ? 0 : (gblk0 > TBW ? TBW : gblk0);
     const int nwg = static_cast<int>(a.nwg2);
     const bool dead = wg_in >= nwg;  // computes the last workgroup's tiles, stores nothing
     const int wg = dead ? nwg - 1 : wg_in;
@@ -1296,23 +1534,38 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
     // workgroup issues both members' loads before either waits.
     struct PassRegs {
         PassChunks<KC> pc;
-        S2Regs<TB, TW> r[KC];
-        int e[TB];
+        S2Regs<TBW, TW> r[KC];
+        int e[TBW];
     };
     const auto load_pass = [&](const LinArgs& m, PassRegs& ps, const int base, const bool first)
                                __attribute__((always_inline)) {
-        ps.pc = pass_chunks<KC>(base, wave, nw, nc);
+        ps.pc = pass_chunks<KC>(base, slot, nslots, nc);
 #pragma unroll
         for (int j = 0; j < KC; ++j) load_words(ps.r[j].w, m.u_tiles, nt, nb, t0, ps.pc.c[j], lane);
         // The U words do not depend on stage 1; the fused launch waits for its
         // signal only now.
         if (FUSED && first) stale = wait_ready(m, t0, TW, wg, dead);
+        if constexpr (TPB == 1) {
 #pragma unroll
-        for (int j = 0; j < KC; ++j) load_s2_ops<TPB, TB, TW>(ps.r[j], m, ps.pc.c[j], lane);
+            for (int j = 0; j < KC; ++j) load_s2_ops<TPB, TB, TW>(ps.r[j], m, ps.pc.c[j], lane);
+            ps.e[0] = m.lme[0];
+        } else {
+            // Every block of the wave's group is loaded (the operand buffer
+            // holds TB blocks per chunk); blocks past the last token are
+            // computed and not stored.
 #pragma unroll
-        for (int tb = 0; tb < TB; ++tb) {
-            const int t = tb * TPB + (TPB == 1 ? 0 : (lane >> 4));
-            ps.e[tb] = m.lme[t < tokens ? t : tokens - 1];
+            for (int j = 0; j < KC; ++j)
+#pragma unroll
+                for (int i = 0; i < TBW; ++i)
+#pragma unroll
+                    for (int mm = 0; mm < 8; ++mm)
+                        ps.r[j].a[i][mm] = *reinterpret_cast<const v4i*>(
+                            m.lmq + lmq_offset<TPB, TB>(ps.pc.c[j], grp * TBW + i, mm, lane & 15, lane >> 4));
+#pragma unroll
+            for (int i = 0; i < TBW; ++i) {
+                const int t = (grp * TBW + i) * TPB + (lane >> 4);
+                ps.e[i] = m.lme[t < tokens ? t : tokens - 1];
+            }
         }
         if (PAIR && first && &m != &a) rs1 = load_elem(m.s_out, m.scale_dtype, fr);
         if (first && &m == &a) {
@@ -1341,21 +1594,34 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
             if (!ps.pc.live[j]) continue;  // uniform
             const int c = ps.pc.c[j];
             const int dw = chunk_words32(nb, c);
-            spread_s2_ops<TPB, TB, TW>(ps.r[j], spread + j * kS2SpreadBytes, lane);
-#pragma unroll
-            for (int tb = 0; tb < TB; ++tb) {
-                if (tb * TPB >= tokens) break;
-                const v4i S = ones_mfma(ps.r[j].a[tb]);
-                // A poisoned token (non-finite activations) yields NaN partials.
-                const float sc = ps.e[tb] == kPoisonExp ? __builtin_nanf("") : exp2i(-ps.e[tb] - 7);
+            // A poisoned token (non-finite activations) yields NaN partials.
+            if constexpr (TPB == 1) {
+                spread_s2_ops<TPB, TB, TW>(ps.r[j], spread + j * kS2SpreadBytes, lane);
+                const v4i S = ones_mfma(ps.r[j].a[0]);
+                const float sc = ps.e[0] == kPoisonExp ? __builtin_nanf("") : exp2i(-ps.e[0] - 7);
 #pragma unroll
                 for (int tt = 0; tt < TW; ++tt)
-                    redm[((c * TW + tt) * TB + tb) * 64 + lane] =
-                        tile_partial<4>(ps.r[j].a[tb], S, ps.r[j].w[tt], dw, sc);
+                    redm[(c * TW + tt) * 64 + lane] = tile_partial<4>(ps.r[j].a[0], S, ps.r[j].w[tt], dw, sc);
+            } else {
+                v4i S[TBW];
+                float sc[TBW];
+#pragma unroll
+                for (int i = 0; i < TBW; ++i) {
+                    S[i] = ones_mfma(ps.r[j].a[i]);
+                    sc[i] = ps.e[i] == kPoisonExp ? __builtin_nanf("") : exp2i(-ps.e[i] - 7);
+                }
+#pragma unroll
+                for (int tt = 0; tt < TW; ++tt) {
+                    float part[TBW];
+                    tile_partials<4, TBW>(ps.r[j].a, S, ps.r[j].w[tt], dw, sc, part);
+#pragma unroll
+                    for (int i = 0; i < TBW; ++i)
+                        if (i < gblk) redm[((c * TW + tt) * TB + grp * TBW + i) * 64 + lane] = part[i];
+                }
             }
         }
     };
-    const int step = nw * KC;
+    const int step = nslots * KC;
     {
         PassRegs pa;
         load_pass(a, pa, 0, true);
@@ -1493,6 +1759,30 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage1(const Batch batch) {
     stage1_wg<AK, TPB, TB, TW, KC, false>(a, xcd_block(blockIdx.x, nwg), lds);
 }
 
+// Stage 0 of the several-token path: grid (ceil(chunks * token blocks / 4),
+// members), four waves per workgroup, one (chunk, token block) per wave.
+template <int AK>
+__global__ __launch_bounds__(256) void k_decode_stage0(const Batch batch) {
+    const LinArgs a = load_args(batch, blockIdx.y);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int nblk = (a.tokens + 3) >> 2;
+    const int item = static_cast<int>(blockIdx.x) * 4 + wave;
+    if (item >= static_cast<int>(a.g1.nc) * nblk) return;  // uniform per wave
+    const int c = item / nblk;
+    stage0_wave<AK>(a, c, item - c * nblk, nblk > 2 ? 4 : nblk, lane);
+}
+
+// Stage 1 of the several-token path (split launch, grid as k_decode_stage1).
+template <int TB, int TW, int KC, int THREADS>
+__global__ __launch_bounds__(THREADS) void k_decode_stage1m(const Batch batch) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const LinArgs a = load_args(batch, blockIdx.y);
+    const int nwg = static_cast<int>(a.nwg1);
+    if (static_cast<int>(blockIdx.x) >= nwg) return;
+    stage1m_wg<TB, TW, KC>(a, xcd_block(blockIdx.x, nwg), lds);
+}
+
 template <int TPB, int TB, int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage2(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -1552,6 +1842,8 @@ int enqueue_stage1_generic(const Batch& batch, const LaunchShape& s, hipStream_t
 int enqueue_stage1_fused(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_stage2(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_stage2_pair(const Batch& batch, const LaunchShape& s, hipStream_t stream);
+int enqueue_stage0(const Batch& batch, const LaunchShape& s, hipStream_t stream);
+int enqueue_stage1m(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 int enqueue_fused(const Batch& batch, const LaunchShape& s, hipStream_t stream);
 
 }  // namespace nqdec

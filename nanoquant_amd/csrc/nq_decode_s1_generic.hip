@@ -28,8 +28,9 @@ int by_tiles(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
 
 int enqueue_stage1_generic(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     if (s.tpb == 1) return by_tiles<1>(batch, s, stream);
+    // Two to four tokens stage in the kernel; more take stage 0 + k_decode_stage1m (nq_decode_multi.hip).
     if (s.tb == 1) return by_tiles<4>(batch, s, stream);
-    return go<4, 4, 1, 1>(batch, s, stream);
+    return NQ_ERR_UNSUPPORTED;
 }
 
 }  // namespace nqdec

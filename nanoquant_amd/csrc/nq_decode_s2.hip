@@ -21,6 +21,15 @@ int by_tiles(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     return s.kc == 2 ? go<TPB, 1, 1, 2>(batch, s, stream) : go<TPB, 1, 1, 1>(batch, s, stream);
 }
 
+// Several token blocks (five tokens or more): one chunk per wave per pass.
+template <int TB>
+int by_tiles_blocks(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
+    if (s.kc != 1) return NQ_ERR_LAUNCH;
+    if (s.tw == 4) return go<4, TB, 4, 1>(batch, s, stream);
+    if (s.tw == 2) return go<4, TB, 2, 1>(batch, s, stream);
+    return go<4, TB, 1, 1>(batch, s, stream);
+}
+
 template <int TW, int KC>
 int go_pair(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     constexpr int kThreads = threads_for(1, KC);
@@ -41,7 +50,8 @@ int enqueue_stage2_pair(const Batch& batch, const LaunchShape& s, hipStream_t st
 int enqueue_stage2(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
     if (s.tpb == 1) return by_tiles<1>(batch, s, stream);
     if (s.tb == 1) return by_tiles<4>(batch, s, stream);
-    return go<4, 4, 1, 1>(batch, s, stream);
+    if (s.tb == 2) return by_tiles_blocks<2>(batch, s, stream);
+    return by_tiles_blocks<4>(batch, s, stream);
 }
 
 }  // namespace nqdec

@@ -450,8 +450,10 @@ def test_reference_state_objects_run_through_prepare_and_linear(backend, tokens)
     x = syn.synthetic_activations(tokens, shape.in_features, seed=tokens).cuda()
     y = backend.linear(x, layer)
     assert torch.equal(y, backend.linear(x, own))
-    _assert_parity(backend, y, orc.packed_forward(orc.operands_from_state(foreign), x.cpu()),
-                   ("foreign", tokens))
+    # Workload-sized: rel-L2 against the fp32 forward (the general fp32 path
+    # observes about 1e-6 at this size).
+    err = orc.relative_l2(y, orc.packed_forward(orc.operands_from_state(foreign), x.cpu()))
+    assert err <= (REL_L2 if _tiled(backend) else 1e-5), ("foreign", tokens, err)
 
 
 def test_hip_graph_capture_replays_match_eager(backend):
@@ -512,10 +514,14 @@ def test_qkv_and_layer_batches_match_oracle(tokens, launch):
     assert all(_sync_header_clean(layer) for layer in layers)
 
 
-@pytest.mark.parametrize("tokens", [1, 3, 16])
+@pytest.mark.parametrize("tokens", [1, 3, 5, 6, 9, 16])
 def test_split_and_fused_launches_are_bit_identical(tokens):
     """The two decode launch structures run the same tile arithmetic in the
-    same order, so their outputs agree bit for bit (including salient and bias)."""
+    same order, so their outputs agree bit for bit (including salient and bias).
+    From five tokens the split launch stages x * s_in in a kernel of its own
+    (two or four token blocks, two waves per chunk with four) where the fused
+    launch stages in every workgroup: the digits, and so the outputs, are the
+    same."""
 
     split, fused = HipPackedBackend(decode_launch="split"), HipPackedBackend(decode_launch="fused")
     for i, shape in enumerate(syn.qwen3_8b_layer()):
