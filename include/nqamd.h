@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define NQ_ABI_VERSION 2
+#define NQ_ABI_VERSION 3
 
 typedef enum nq_dtype {
     NQ_DTYPE_F32 = 0,
@@ -68,6 +68,19 @@ typedef enum nq_decode_launch {
     NQ_DECODE_SPLIT = 0,
     NQ_DECODE_FUSED = 1
 } nq_decode_launch;
+
+/* Operands of the prefill path's fp16 MFMA GEMMs (tokens > 16).
+ *   NQ_PREFILL_FP16: the row-scaled activations and the rank intermediate
+ *     rounded to fp16 (11 bits; about 3e-4 rel-L2 against the fp32 forward).
+ *   NQ_PREFILL_FP16_SPLIT: each as an fp16 high part plus an fp16 part of the
+ *     remainder (about 22 bits), two MFMAs per product, for callers whose
+ *     errors compound (a decoder's prompt pass).
+ * Batch members must agree. No reference counterpart (the reference's
+ * kernels compute in the activation dtype, cuda_kernels.py:65-162). */
+typedef enum nq_prefill_operands {
+    NQ_PREFILL_FP16 = 0,
+    NQ_PREFILL_FP16_SPLIT = 1
+} nq_prefill_operands;
 
 /* Device facts used by the backend's capability check.
  * Replaces the CUDA capability probe of CudaPackedBackend.supports
@@ -116,6 +129,7 @@ typedef struct nq_linear_desc {
     const void* tiles;            /* GPU layout from nq_prepare_tiles, or NULL */
     int64_t tiles_bytes;
     int32_t decode_launch;        /* nq_decode_launch; batch members must agree */
+    int32_t prefill_operands;     /* nq_prefill_operands; batch members must agree */
 } nq_linear_desc;
 
 /* Library ABI version (NQ_ABI_VERSION). No reference counterpart. */

@@ -34,8 +34,8 @@
 //   Stage 1 stages x * s_in per (wave, chunk, block of up to 4 tokens): lane L
 //     takes the 8 consecutive columns 512c + 128d + 16m + 8h + {0..7} of
 //     (m, d, h) = (L >> 3, (L >> 1) & 3, L & 1) (one 16-byte load of x and one
-//     of s_in for 16-bit x), the wave max gives E (|a 2^E| < 2^15, so
-//     w_m = rint(a 2^(E+7-m)) has three digits), and each lane writes its
+//     of s_in for 16-bit x), the wave max gives E (|a 2^E| < 2^23, so
+//     w_m = rint(a 2^(E+7-m)) has four digits), and each lane writes its
 //     digit bytes into the wave's LDS area A[m][row][g][16 B] (g = 2h, 2h + 1,
 //     byte 4d + b); each lane then reads its eight A operands (one 16-byte LDS
 //     read per MFMA).
@@ -43,7 +43,8 @@
 //     stage-2 operand layout in global memory as x_q = rint(lm 2^E) times
 //     2^(7-m) (four digits, |x_q| <= 2^22) with one exponent per token from a
 //     bound every stage-1 workgroup computes identically, |lm| <= max|s_mid| *
-//     Σ_chunks 512 * max_chunk|x s_in|; stage 2 loads a chunk's operands (one
+//     Σ_i |x_i s_in_i| (summed per chunk by the staging waves, then in chunk
+//     order); stage 2 loads a chunk's operands (one
 //     token: 2 KB, spread through LDS; more tokens: one 16-byte load each).
 // Chunk partials are summed in chunk order, so the result is the same for
 // every launch shape (waves or tiles per workgroup, split or fused launch).
@@ -213,8 +214,8 @@ struct LinArgs {
     int attn_hd_log2;           // log2(head_dim)
     int64_t attn_max_positions;
     // Several tokens (split launch): stage 0 writes the stage-1 A operands of
-    // x * s_in here in the lmq layout (3 digit rows per token, the fourth
-    // zero), with the exponent and max |x s_in| of every (chunk, token) at
+    // x * s_in here in the lmq layout (four digit rows per token), with the
+    // exponent and Σ |x s_in| of every (chunk, token) at
     // [chunk * kMaxTokens + token].
     uint8_t* xq;
     int* xe;
@@ -357,6 +358,15 @@ __host__ __device__ inline int lmq_offset(int c, int tb, int m, int row, int g) 
 
 template <int TPB, int TB>
 __host__ __device__ inline int64_t lmq_bytes(const MatGeo& g2) { return g2.nc * TB * Ops<TPB>::kBytes; }
+
+// Nearest integer of x (halves round up), |x| < 2^31: one instruction
+// (v_cvt_rpi_i32_f32 computes floor(x + 0.5)) where rintf and a conversion
+// take two.
+__device__ __forceinline__ int round_to_int(float x) {
+    int r;
+    asm("v_cvt_rpi_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+    return r;
+}
 
 // 2^e for an integer e in the fp32 normal range.
 __device__ __forceinline__ float exp2i(int e) { return __uint_as_float(static_cast<uint32_t>(e + 127) << 23); }
@@ -791,10 +801,6 @@ __device__ __forceinline__ void act_run(const S1Regs<AK, TOK, TW>& r, const LinA
     }
 }
 
-// Bits that are set in the fma word of a non-finite staged value and clear in
-// every finite one (finite words have the top byte 0x4B, see stage_block).
-constexpr uint32_t kNonFiniteBits = 0x34000000u;
-
 // Exponent a stage-1 epilogue writes for a token whose activations hold a
 // NaN or an infinity: stage 2 then stores NaN for every output of that token,
 // as the reference's fp32 forward yields (a non-finite activation reaches
@@ -802,20 +808,20 @@ constexpr uint32_t kNonFiniteBits = 0x34000000u;
 constexpr int kPoisonExp = 0x7fffffff;
 
 // Stage tokens [t_base, t_base + TPB) of chunk c into this wave's operand area
-// (three digit rows per token) and return each token's exponent E and the
-// chunk max |a| (uniform values).
+// (four digit rows per token) and return each token's exponent E and the
+// chunk's Σ |a| (uniform values; not finite when a staged value is not).
 //
 // MFMA m receives w = rint(a * 2^(E + 7 - m)) (m = 7: w = -rint(a * 2^E)), so
 // every product with its B bytes {0, 2^m} (m = 7: {0, -128}) is b times a
 // multiple of 2^-(E+7) and the eight MFMAs of a chunk share one accumulator.
-// |a * 2^E| < 2^15 gives |w| <= 2^22: adding 1.5 * 2^23 in one fma rounds to
-// the nearest integer (ties to even) and leaves y = 0x4B400000 + w in the
-// bits, from which the three signed base-256 digits of w are bytes of
-// y (digit 0), y + 128 (digit 1) and y + 128 + 128 * 256 - 0x400000 (digit 2):
-// digit j is the low byte of w_j with w_0 = w, w_{j+1} = (w_j + 128) >> 8.
+// |a * 2^E| < 2^23 gives |w| < 2^30, rounded once (halves up) from the
+// exact product, as four signed base-256 digits: digit j is the low byte of
+// w_j with w_0 = w, w_{j+1} = (w_j + 128) >> 8, i.e. byte j of w, w + 0x80,
+// w + 0x8080 and w + 0x808080. Every value keeps 24 bits relative to the
+// chunk's largest.
 template <int AK, int TOK, int TW, int TPB>
 __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int c, int t_base,
-                                            char* __restrict__ ops, int lane, int (&expo)[TPB], float (&cmax)[TPB]) {
+                                            char* __restrict__ ops, int lane, int (&expo)[TPB], float (&csum)[TPB]) {
     const int m = lane >> 3, d = (lane >> 1) & 3, h = lane & 1;
     const int k0 = stage_col0(c, lane);
     const int in = static_cast<int>(a.in);
@@ -832,7 +838,7 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
     for (int u = 0; u < TPB; ++u) {
         const int t = t_base + u;
         float v[2][4];
-        float mx = 0.0f;
+        float mx = 0.0f, sa = 0.0f;
         if (full_chunk && t < a.tokens) {  // uniform: every value is inside
 #pragma unroll
             for (int run = 0; run < 2; ++run) {
@@ -841,6 +847,7 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
                 for (int i = 0; i < 4; ++i) {
                     v[run][i] *= sc[run][i];
                     mx = fmaxf(mx, fabsf(v[run][i]));
+                    sa += fabsf(v[run][i]);
                 }
             }
         } else {
@@ -852,37 +859,36 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
                     const bool ok = t < a.tokens && 4 * run + i < lim;
                     v[run][i] = ok ? v[run][i] * sc[run][i] : 0.0f;
                     mx = fmaxf(mx, fabsf(v[run][i]));
+                    sa += fabsf(v[run][i]);
                 }
             }
         }
+        // fmaxf drops NaN, the sum does not: a NaN or an infinity makes the
+        // chunk sum, and so the token's bound in the epilogue, not finite.
         const float wmx = wave_max(mx);
-        const int e = range_exponent(wmx, 14);
+        csum[u] = wave_sum(sa);
+        const int e = range_exponent(wmx, 22);
         const float sm = m < 7 ? exp2i(e + 7 - m) : -exp2i(e);
-        uint32_t dig[3][2];
-        uint32_t seen = 0;  // OR of the fma words: flags a non-finite staged value
+        uint32_t dig[4][2];
 #pragma unroll
         for (int run = 0; run < 2; ++run) {
-            uint32_t y0[4], y1[4], y2[4];
+            uint32_t w0[4], w1[4], w2[4], w3[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const uint32_t y = __float_as_uint(__builtin_fmaf(v[run][i], sm, 12582912.0f));
-                seen |= y;
-                y0[i] = y;
-                y1[i] = y + 128u;
-                y2[i] = y + (32896u - 0x400000u);
+                const uint32_t w = static_cast<uint32_t>(round_to_int(v[run][i] * sm));
+                w0[i] = w;
+                w1[i] = w + 0x80u;
+                w2[i] = w + 0x8080u;
+                w3[i] = w + 0x808080u;
             }
-            dig[0][run] = bytes_at<0>(y0[0], y0[1], y0[2], y0[3]);
-            dig[1][run] = bytes_at<1>(y1[0], y1[1], y1[2], y1[3]);
-            dig[2][run] = bytes_at<2>(y2[0], y2[1], y2[2], y2[3]);
+            dig[0][run] = bytes_at<0>(w0[0], w0[1], w0[2], w0[3]);
+            dig[1][run] = bytes_at<1>(w1[0], w1[1], w1[2], w1[3]);
+            dig[2][run] = bytes_at<2>(w2[0], w2[1], w2[2], w2[3]);
+            dig[3][run] = bytes_at<3>(w3[0], w3[1], w3[2], w3[3]);
         }
         expo[u] = e;
-        // A finite value gives |w| <= 2^22, so its word lies in [2^23, 2^24]
-        // (top byte 0x4B); NaN and +-Inf give exponent bits 0xFF, which set
-        // bits the finite words never have. The chunk max then becomes +Inf,
-        // which makes the token's bound non-finite in the epilogue.
-        cmax[u] = __builtin_amdgcn_ballot_w64((seen & kNonFiniteBits) != 0) != 0 ? __builtin_inff() : wmx;
 #pragma unroll
-        for (int digit = 0; digit < 3; ++digit) {
+        for (int digit = 0; digit < 4; ++digit) {
             const int row = 4 * u + digit;
 #pragma unroll
             for (int run = 0; run < 2; ++run)
@@ -1126,7 +1132,7 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
     const int rank = static_cast<int>(a.rank);
     char* const ops = lds + wave * Ops<TPB>::kBytes;
     float* const red = reinterpret_cast<float*>(lds + nw * Ops<TPB>::kBytes);
-    float* const cmx = red + nc * TW * TB * 64;  // [nc][TOK] chunk max |x s_in|
+    float* const cmx = red + nc * TW * TB * 64;  // [nc][TOK] chunk Σ |x s_in|
 
     const int outs = TW * tokens * kTileRows;
     const OutIdx f = out_index<TPB>(threadIdx.x < outs ? threadIdx.x : 0, tokens);
@@ -1203,7 +1209,7 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
                 const float sc = exp2i(-e - 7);
 #pragma unroll
                 for (int tt = 0; tt < TW; ++tt)
-                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<3>(A, S, r[j].w[tt], dw, sc);
+                    red[((c * TW + tt) * TB + tb) * 64 + lane] = tile_partial<4>(A, S, r[j].w[tt], dw, sc);
                 if (lane == 0) {
 #pragma unroll
                     for (int u = 0; u < TPB; ++u) cmx[c * TOK + tb * TPB + u] = cm[u];
@@ -1220,7 +1226,8 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
     if (dead) return;  // uniform, after the workgroup's only barrier
 
     // Epilogue: lm = s_mid * Σ_chunks partial, written as stage-2 operands with
-    // the per-token exponent of the bound max|s_mid| * Σ_c 512 * max_c.
+    // the per-token exponent of the bound |lm| <= max|s_mid| * Σ_i |x_i s_in_i|
+    // (times 1/RMS for the normed kind).
     for (int idx = threadIdx.x; idx < outs; idx += nthreads) {
         const OutIdx o = out_index<TPB>(idx, tokens);
         const int row = (t0 + o.tt) * kTileRows + o.n;
@@ -1230,10 +1237,10 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
             sum += red[red_index<TPB, TB, TW>(c, o.tt, o.t, o.n)];
             bound += cmx[c * TOK + o.t];
         }
-        // Every workgroup sums the same chunk maxima in the same order, so all
+        // Every workgroup sums the same chunk sums in the same order, so all
         // agree on the exponent and on a poisoned (non-finite) token.
         const bool poison = !(bound <= 3.402823466e38f);
-        const int e = poison ? 0 : range_exponent(bound * rs * (512.0f * maxsm), 21);
+        const int e = poison ? 0 : range_exponent(bound * rs * maxsm, 21);
         float v = 0.0f;
         if (row < rank && !poison)
             v = sum * elem_value(idx == threadIdx.x ? rs0 : load_elem(a.s_mid, a.scale_dtype, row), a.scale_dtype) * rs;
@@ -1269,9 +1276,9 @@ __device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __r
 // group, and a stage-1 wave's A operands grow to 8 KB per block of four
 // tokens per chunk against 1 KB of sign words per tile. Stage 0 therefore
 // stages every (chunk, token block) once per call, with stage_block's
-// arithmetic, into xq (the lmq layout with TB blocks; each token's fourth
-// digit row zero) and records every (chunk, token)'s exponent (xe) and max
-// |x s_in| (xm). Stage 1 then loads its A operands like stage 2 and takes TW
+// arithmetic, into xq (the lmq layout with TB blocks) and records every
+// (chunk, token)'s exponent (xe) and Σ |x s_in| (xm). Stage 1 then loads its
+// A operands like stage 2 and takes TW
 // tiles per wave, one sign expansion feeding every token block
 // (tile_partials). The digits, exponents, integer partials and their
 // chunk-order sums are those of stage1_wg, so the results are bit-identical.
@@ -1298,12 +1305,6 @@ __device__ __forceinline__ void stage0_wave(const LinArgs& a, int c, int tb, int
     int expo[TPB];
     float cm[TPB];
     stage_block<AK, TPB, 1, TPB>(r, b, c, 0, ops, lane, expo, cm);
-    const int m = lane >> 3, d = (lane >> 1) & 3, h = lane & 1;
-#pragma unroll
-    for (int u = 0; u < TPB; ++u)
-#pragma unroll
-        for (int run = 0; run < 2; ++run)
-            *reinterpret_cast<uint32_t*>(ops + ((m * Ops<TPB>::kRows + 4 * u + 3) * 4 + 2 * h + run) * 16 + 4 * d) = 0;
     int e = expo[0];
     float mx = cm[0];
 #pragma unroll
@@ -1347,7 +1348,7 @@ __device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __
     const int nt = static_cast<int>(a.g1.nt), nb = static_cast<int>(a.g1.nb), nc = static_cast<int>(a.g1.nc);
     const int rank = static_cast<int>(a.rank);
     float* const red = reinterpret_cast<float*>(lds);
-    float* const cmx = red + nc * TW * TB * 64;  // [nc][kMaxTokens] max |x s_in|
+    float* const cmx = red + nc * TW * TB * 64;  // [nc][kMaxTokens] Σ |x s_in|
     const int nxm = nc * kMaxTokens;
 
     const int outs = TW * tokens * kTileRows;
@@ -1400,7 +1401,7 @@ __device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __
 #pragma unroll
             for (int tt = 0; tt < TW; ++tt) {
                 float part[TBW];
-                tile_partials<3, TBW>(r[j].a, S, r[j].w[tt], dw, sc, part);
+                tile_partials<4, TBW>(r[j].a, S, r[j].w[tt], dw, sc, part);
 #pragma unroll
                 for (int i = 0; i < TBW; ++i)
                     if (i < gblk) red[((c * TW + tt) * TB + grp * TBW + i) * 64 + lane] = part[i];
@@ -1417,7 +1418,7 @@ __device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __
     if (dead) return;  // uniform, after the workgroup's only barrier
 
     // Epilogue of stage1_wg (no input norm): lm = s_mid * Σ_chunks partial as
-    // stage-2 operands with the per-token exponent of max|s_mid| * Σ_c 512 * max_c.
+    // stage-2 operands with the per-token exponent of max|s_mid| * Σ |x s_in|.
     for (int idx = threadIdx.x; idx < outs; idx += nthreads) {
         const OutIdx o = out_index<TPB>(idx, tokens);
         const int row = (t0 + o.tt) * kTileRows + o.n;
@@ -1428,7 +1429,7 @@ __device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __
             bound += cmx[c * kMaxTokens + o.t];
         }
         const bool poison = !(bound <= 3.402823466e38f);
-        const int e = poison ? 0 : range_exponent(bound * (512.0f * maxsm), 21);
+        const int e = poison ? 0 : range_exponent(bound * maxsm, 21);
         float v = 0.0f;
         if (row < rank && !poison)
             v = sum * elem_value(idx == static_cast<int>(threadIdx.x) ? rs0 : load_elem(a.s_mid, a.scale_dtype, row),

@@ -394,6 +394,7 @@ int validate(const nq_linear_desc* d) {
     if (d->row_count > 0 && (!d->row_indices || !d->row_values || !d->row_scales))
         return NQ_ERR_ARGUMENT;
     if (d->decode_launch != NQ_DECODE_SPLIT && d->decode_launch != NQ_DECODE_FUSED) return NQ_ERR_ARGUMENT;
+    if (d->prefill_operands != NQ_PREFILL_FP16 && d->prefill_operands != NQ_PREFILL_FP16_SPLIT) return NQ_ERR_ARGUMENT;
     return NQ_OK;
 }
 

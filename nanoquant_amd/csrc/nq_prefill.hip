@@ -36,6 +36,15 @@
 // 16-column slices are software-pipelined: slice m's MFMAs issue while slice
 // m + 1's A fragments are read and its signs expanded.
 //
+// Split operands (nq_linear_desc.prefill_operands = NQ_PREFILL_FP16_SPLIT):
+// every prepared row and the rank intermediate carry, per 128-column block,
+// the fp16 values hi = fp16(v) and then the fp16 remainders lo = fp16(v - hi)
+// (v - hi is exact in fp32), so a row of K columns is 2K fp16 wide. Each K
+// step then moves both 128-column planes into LDS and issues every MFMA
+// twice, hi then lo into the same accumulator: about 22 bits per operand
+// instead of 11, against twice the MFMA and activation work (the signs are
+// expanded once).
+//
 // Split K: when a GEMM has too few (token, sign-row) tiles to fill the GPU,
 // its K blocks are split into slices of at least two, each workgroup writes
 // its raw fp32 accumulators to partial[slice][t][n], and k_reduce_splits, one
@@ -129,7 +138,8 @@ struct PrepArgs {
     int colscale_dtype;
     int vec;                         // 16-byte loads allowed (generic kernel)
     int64_t cols, cols_pad;
-    _Float16* out16;                 // [tokens, cols_pad]
+    _Float16* out16;                 // [tokens, cols_pad], or [tokens, 2 cols_pad] with split
+    int split;                       // split operands: hi and lo planes per 128-column block
     float* scale_out;                // [tokens]
     const uint32_t* max_mid_bits;    // fp32 bits of max|s_mid|, or null
     float* bound_scale_out;          // [tokens]
@@ -138,6 +148,35 @@ struct PrepArgs {
 struct PrepBatch {
     PrepArgs p[kPrefillBatch];
 };
+
+// Stores columns [c, c + 8) (c % 8 == 0) of prepared row t, v times `scale`,
+// into a buffer of rows of cols_pad columns: fp16 with columns 1 and 2 of
+// every group of four exchanged (swizzle4), one 16-byte store; with `split`
+// the rows are 2 cols_pad wide, block c / 128 holding its 128 high parts and
+// then their remainders: two stores.
+__device__ __forceinline__ void store_prepped(_Float16* __restrict__ out, int64_t t, int64_t cols_pad, int64_t c,
+                                              const float (&v)[8], float scale, bool split) {
+    union {
+        _Float16 h[8];
+        uint4 u;
+    } hi, lo;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float x = v[4 * g + (i == 1 ? 2 : (i == 2 ? 1 : i))] * scale;
+            hi.h[4 * g + i] = static_cast<_Float16>(x);
+            lo.h[4 * g + i] = static_cast<_Float16>(x - static_cast<float>(hi.h[4 * g + i]));
+        }
+    }
+    if (!split) {
+        *reinterpret_cast<uint4*>(out + t * cols_pad + c) = hi.u;
+        return;
+    }
+    _Float16* const row = out + t * 2 * cols_pad + (c >> 7) * 256 + (c & 127);
+    *reinterpret_cast<uint4*>(row) = hi.u;
+    *reinterpret_cast<uint4*>(row + 128) = lo.u;
+}
 
 // One workgroup per row: out16[t, swizzle4(c)] = fp16(a[t, c] * s[c] * scale_t)
 // for c < cols, zero for cols <= c < cols_pad; scale_out[t] = scale_t. Each
@@ -190,19 +229,7 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows(const PrepBatch batch, int
         else
 #pragma unroll
             for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-        union {
-            _Float16 h[8];
-            uint4 u;
-        } o;
-        // swizzle4 within each group of four: positions 1 and 2 exchanged.
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            o.h[4 * g + 0] = static_cast<_Float16>(v[4 * g + 0] * scale);
-            o.h[4 * g + 1] = static_cast<_Float16>(v[4 * g + 2] * scale);
-            o.h[4 * g + 2] = static_cast<_Float16>(v[4 * g + 1] * scale);
-            o.h[4 * g + 3] = static_cast<_Float16>(v[4 * g + 3] * scale);
-        }
-        *reinterpret_cast<uint4*>(out16 + t * cols_pad + c) = o.u;
+        store_prepped(out16, t, cols_pad, c, v, scale, pa.split != 0);
     }
     if (threadIdx.x == 0) scale_out[t] = scale;
 }
@@ -286,18 +313,7 @@ __global__ __launch_bounds__(kBlock) void k_prep_rows_vec(const PrepBatch batch)
     for (int k = 0; k < NCH; ++k) {
         const int64_t c = 8 * threadIdx.x + 8 * kBlock * k;
         if (c >= cols_pad) continue;
-        union {
-            _Float16 h[8];
-            uint4 u;
-        } o;
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-            o.h[4 * g + 0] = static_cast<_Float16>(v[k][4 * g + 0] * scale);
-            o.h[4 * g + 1] = static_cast<_Float16>(v[k][4 * g + 2] * scale);
-            o.h[4 * g + 2] = static_cast<_Float16>(v[k][4 * g + 1] * scale);
-            o.h[4 * g + 3] = static_cast<_Float16>(v[k][4 * g + 3] * scale);
-        }
-        *reinterpret_cast<uint4*>(out16 + t * cols_pad + c) = o.u;
+        store_prepped(out16, t, cols_pad, c, v[k], scale, pa.split != 0);
     }
     if (threadIdx.x == 0) scale_out[t] = scale;
 }
@@ -341,7 +357,7 @@ __device__ __forceinline__ v8h expand_signs32(uint32_t w0, uint32_t w1, int m, u
 }
 
 struct GemmArgs {
-    const _Float16* a;        // [M, kpad] fp16 activations (row-scaled)
+    const _Float16* a;        // [M, kpad] fp16 activations (row-scaled); [M, 2 kpad] with split
     int64_t m;                // tokens
     int64_t kpad;             // nb * 128
     const uint32_t* tiles;    // sign tiles [rt][nb * 64] (chunked, see above)
@@ -366,7 +382,9 @@ struct GemmArgs {
     int out_dtype;
     const float* out_scale;   // [M] or null: write fp16(v * out_scale[t]) at column
                               // swizzle4(c) of an out_ld-wide row, zero for n <= c < out_ld
+                              // (split: rows 2 out_ld wide, the prepared-row layout)
     int64_t out_ld;
+    int split;                // split operands (A, and the rank intermediate written)
     int64_t k_per_split;      // K blocks per K slice
     int64_t splits;           // K slices (1: no split)
     int64_t col_blocks;       // column blocks at the launch's block width
@@ -400,15 +418,17 @@ __device__ __forceinline__ int batch_member(const GemmBatch& b, int x) {
 // GPU at that size. (1, 2, 1): side by side, each 64 x 32 (block tile
 // 64 x 128), for at most 64 tokens: no MFMA or A read is spent on rows past
 // the last token.
-template <int WR, int II, int JJ>
+template <int WR, int II, int JJ, bool SPLIT>
 __global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const GemmBatch batch) {
     constexpr int BM = WR * 32 * II;      // token rows per block
     constexpr int BN = (4 / WR) * 32 * JJ;  // sign rows per block
-    constexpr int NJ = BM / 16;           // 1-KB LDS transfers per wave per K step
-    constexpr int kABytes = BM * kBK * 2;   // one activation tile, rows of 256 bytes
+    constexpr int NJ = BM / 16;           // 1-KB LDS transfers per wave per K step and plane
+    constexpr int kABytes = BM * kBK * 2;   // one activation plane, rows of 256 bytes
+    constexpr int kPlanes = SPLIT ? 2 : 1;  // split operands: the hi plane, then the lo plane
+    constexpr int kBufBytes = kPlanes * kABytes;
     constexpr int kParkStride = 32 * JJ + 1;  // floats per parked accumulator row
     constexpr int kParkBytes = 4 * 64 * kParkStride * 4;
-    constexpr int kLds = 2 * kABytes > kParkBytes ? 2 * kABytes : kParkBytes;  // double-buffered A
+    constexpr int kLds = 2 * kBufBytes > kParkBytes ? 2 * kBufBytes : kParkBytes;  // double-buffered A
     const int member = batch_member(batch, static_cast<int>(blockIdx.x));
     const GemmArgs& g = batch.p[member];
     const int local = static_cast<int>(blockIdx.x) - batch.begin[member];
@@ -449,18 +469,18 @@ __global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const Gem
     // (no branch in the K loop): rows past M read the last valid row and sign
     // tiles past N a valid tile; they only feed accumulators whose outputs are
     // never stored.
-    const int64_t nsc = g.nb, kpad = g.kpad;
+    const int64_t nsc = g.nb, lda = kPlanes * g.kpad;  // fp16 per activation row
     const int64_t a_rows = g.m - m0;  // valid rows of this block (>= 1)
     // Byte offsets from the block's first row (below 2^31: at most 128 rows
     // of a padded K that the host limits), added to a wave-uniform base.
-    const char* const a_blk = reinterpret_cast<const char*>(g.a + m0 * kpad);
+    const char* const a_blk = reinterpret_cast<const char*>(g.a + m0 * lda);
     uint32_t a_src[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int row = 4 * (NJ * wave + j) + (lane >> 4);
         const int chunk = (lane & 15) ^ (row & 15);
         const int64_t rr = row < a_rows ? row : a_rows - 1;
-        a_src[j] = static_cast<uint32_t>((rr * kpad + 8 * chunk) * 2);
+        a_src[j] = static_cast<uint32_t>((rr * lda + 8 * chunk) * 2);
     }
     const uint32_t* bt[JJ];
 #pragma unroll
@@ -478,15 +498,20 @@ __global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const Gem
     // step ends with vmcnt(0) and a barrier before that buffer is read.
     typedef __attribute__((address_space(3))) void lds_void_t;
     const auto load_a = [&](int64_t sc, int buf) __attribute__((always_inline)) {
-        const char* base = a_blk + sc * (2 * kBK);  // wave-uniform: a scalar base, per-lane 32-bit offsets
+        // wave-uniform: a scalar base, per-lane 32-bit offsets; plane q of
+        // block sc starts 256 q bytes after the hi plane.
+        const char* base = a_blk + sc * (2 * kBK * kPlanes);
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            lds_void_t* dst = (lds_void_t*)(lds + buf * kABytes + (NJ * wave + j) * 1024);
-            const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
-            // s_nop: one wait state between the M0 write and the LDS transfer.
-            asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(a_src[j]), "s"(base), "{m0}"(lds_addr)
-                         : "memory");
-        }
+        for (int q = 0; q < kPlanes; ++q)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                lds_void_t* dst = (lds_void_t*)(lds + buf * kBufBytes + q * kABytes + (NJ * wave + j) * 1024);
+                const uint32_t lds_addr = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(dst));
+                // s_nop: one wait state between the M0 write and the LDS transfer.
+                asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(a_src[j]), "s"(base + 2 * kBK * q),
+                             "{m0}"(lds_addr)
+                             : "memory");
+            }
     };
     const auto load_words = [&](int64_t sc) __attribute__((always_inline)) {
         const int64_t c_ = sc >> 2;
@@ -524,43 +549,48 @@ __global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const Gem
         // MFMAs; left to itself the scheduler sinks them to the step's end,
         // where the wait before the barrier would take their whole latency.
         __builtin_amdgcn_sched_barrier(0);
-        const char* a_lds = lds + buf * kABytes;
+        const char* a_lds = lds + buf * kBufBytes;
         // Software pipeline over the eight 16-column slices: slice m's MFMAs
         // issue while slice m + 1's A fragments are read from LDS and its
         // sign fragments expanded, so no MFMA waits on a read issued just
         // before it. Each slice is one scheduling region (sched_barrier) laid
-        // out as the reads, then MFMAs alternating with the expansion.
-        v8h a_cur[II], b_cur[JJ];
+        // out as the reads, then MFMAs alternating with the expansion. With
+        // split operands fragment II + ii is the lo plane of fragment ii.
+        constexpr int NA = kPlanes * II;
+        v8h a_cur[NA], b_cur[JJ];
 #pragma unroll
-        for (int ii = 0; ii < II; ++ii) a_cur[ii] = *reinterpret_cast<const v8h*>(a_lds + a_off[0] + 8192 * ii);
+        for (int ai = 0; ai < NA; ++ai)
+            a_cur[ai] = *reinterpret_cast<const v8h*>(a_lds + (ai / II) * kABytes + a_off[0] + 8192 * (ai % II));
 #pragma unroll
         for (int jj = 0; jj < JJ; ++jj) b_cur[jj] = expand_signs32(words[jj][0], words[jj][1], 0, sign_mask, fp16_one);
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
             __builtin_amdgcn_sched_barrier(0);
-            v8h a_nxt[II], b_nxt[JJ];
+            v8h a_nxt[NA], b_nxt[JJ];
             if (m < 7) {
 #pragma unroll
-                for (int ii = 0; ii < II; ++ii)
-                    a_nxt[ii] = *reinterpret_cast<const v8h*>(a_lds + a_off[m + 1] + 8192 * ii);
+                for (int ai = 0; ai < NA; ++ai)
+                    a_nxt[ai] = *reinterpret_cast<const v8h*>(a_lds + (ai / II) * kABytes + a_off[m + 1] +
+                                                              8192 * (ai % II));
 #pragma unroll
                 for (int jj = 0; jj < JJ; ++jj)
                     b_nxt[jj] = expand_signs32(words[jj][0], words[jj][1], m + 1, sign_mask, fp16_one);
             }
 #pragma unroll
-            for (int ii = 0; ii < II; ++ii)
+            for (int ai = 0; ai < NA; ++ai)
 #pragma unroll
                 for (int jj = 0; jj < JJ; ++jj)
-                    acc[ii][jj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[ii], b_cur[jj], acc[ii][jj], 0, 0, 0);
+                    acc[ai % II][jj] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[ai], b_cur[jj], acc[ai % II][jj], 0, 0, 0);
             if (m < 7) {
-                __builtin_amdgcn_sched_group_barrier(0x100, II, 0);  // LDS reads of slice m + 1
+                __builtin_amdgcn_sched_group_barrier(0x100, NA, 0);  // LDS reads of slice m + 1
 #pragma unroll
-                for (int q = 0; q < II * JJ; ++q) {
+                for (int q = 0; q < NA * JJ; ++q) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA of slice m
-                    __builtin_amdgcn_sched_group_barrier(0x002, 8 / II, 0);  // expansion of m + 1
+                    __builtin_amdgcn_sched_group_barrier(0x002, 8 / NA, 0);  // expansion of m + 1
                 }
 #pragma unroll
-                for (int ii = 0; ii < II; ++ii) a_cur[ii] = a_nxt[ii];
+                for (int ai = 0; ai < NA; ++ai) a_cur[ai] = a_nxt[ai];
 #pragma unroll
                 for (int jj = 0; jj < JJ; ++jj) b_cur[jj] = b_nxt[jj];
             }
@@ -637,15 +667,23 @@ __global__ __launch_bounds__(kBlock, JJ == 1 ? 4 : 2) void k_sign_gemm(const Gem
         if (g.out_scale) {
             // The rank intermediate for GEMM 2: fp16, row-scaled, swizzled, with
             // the padding columns up to out_ld written as zeros (a 256-wide
-            // block can reach past out_ld: those lanes store nothing).
+            // block can reach past out_ld: those lanes store nothing); split:
+            // the prepared-row layout, high parts and remainders.
             const float os_lane = g.out_scale[row0 + lane_row];
             const bool in_row = lane_ok && col < g.out_ld;
-            _Float16* o = static_cast<_Float16*>(g.out) + row0 * g.out_ld + swizzle4(in_row ? col : 0);
+            const int64_t cc = in_row ? col : 0;
+            const int64_t stride = kPlanes * g.out_ld;
+            _Float16* o = static_cast<_Float16*>(g.out) + row0 * stride + (cc >> 7) * (128 * kPlanes) +
+                          swizzle4(cc & 127);
 #pragma unroll
             for (int e = 0; e < 64; ++e) {
                 const float os = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(os_lane), e));
-                if (e < rows && in_row)
-                    o[e * g.out_ld] = col_ok ? static_cast<_Float16>(v[e] * os) : static_cast<_Float16>(0.0f);
+                if (e < rows && in_row) {
+                    const float x = col_ok ? v[e] * os : 0.0f;
+                    const _Float16 hi = static_cast<_Float16>(x);
+                    o[e * stride] = hi;
+                    if constexpr (SPLIT) o[e * stride + 128] = static_cast<_Float16>(x - static_cast<float>(hi));
+                }
             }
             return;
         }
@@ -752,6 +790,7 @@ __global__ __launch_bounds__(kBlock) void k_reduce_splits(const GemmBatch batch)
     g.bias = ga.bias;
     g.bias_dtype = ga.bias_dtype;
     g.salient_count = ga.salient_count;
+    g.split = ga.split;
     asm volatile("" ::"s"(g.m), "s"(g.n), "s"(g.out_ld), "s"(g.out_scale), "s"(g.out), "s"(g.out_dtype),
                  "s"(g.partial), "s"(g.row_scale), "s"(g.col_scale), "s"(g.col_scale_dtype), "s"(g.bias),
                  "s"(g.bias_dtype), "s"(g.salient_count), "s"(splits));
@@ -767,8 +806,15 @@ __global__ __launch_bounds__(kBlock) void k_reduce_splits(const GemmBatch batch)
     const int64_t t = static_cast<int64_t>(blockIdx.z) * kRowsPerGridZ + blockIdx.y;
     const int64_t width = g.out_scale ? g.out_ld : g.n;
     if (splits <= 1 || c >= width || t >= g.m) return;  // members without a split have no partials
+    // With out_scale: the rank intermediate's position of column c (split
+    // operands: the high part, its remainder 128 further).
+    const int64_t planes = g.split ? 2 : 1;
+    _Float16* const lm = g.out_scale ? static_cast<_Float16*>(g.out) + t * planes * g.out_ld +
+                                           (c >> 7) * (128 * planes) + swizzle4(c & 127)
+                                     : nullptr;
     if (c >= g.n) {  // only with out_scale: a padding column of the rank intermediate
-        static_cast<_Float16*>(g.out)[t * g.out_ld + swizzle4(c)] = static_cast<_Float16>(0.0f);
+        lm[0] = static_cast<_Float16>(0.0f);
+        if (g.split) lm[128] = static_cast<_Float16>(0.0f);
         return;
     }
     const int64_t plane = g.m * g.n;
@@ -790,10 +836,14 @@ __global__ __launch_bounds__(kBlock) void k_reduce_splits(const GemmBatch batch)
         if (g.salient_scales) w *= nq::load_f32(g.salient_scales, g.scale_dtype, k);
         v += w * nq::load_f32(g.x, g.x_dtype, t * g.in + g.salient_indices[k]);
     }
-    if (g.out_scale)
-        static_cast<_Float16*>(g.out)[t * g.out_ld + swizzle4(c)] = static_cast<_Float16>(v * g.out_scale[t]);
-    else
+    if (g.out_scale) {
+        const float x = v * g.out_scale[t];
+        const _Float16 hi = static_cast<_Float16>(x);
+        lm[0] = hi;
+        if (g.split) lm[128] = static_cast<_Float16>(x - static_cast<float>(hi));
+    } else {
         nq::store_f32_as(g.out, g.out_dtype, pi, v);
+    }
 }
 
 // Tile counts and 128-column block counts of V [rank, in] and U [out, rank]
@@ -945,12 +995,19 @@ void launch_phase(GemmArgs* p, int count, int64_t tokens, hipStream_t stream) {
         }
     }
     const dim3 grid(static_cast<unsigned>(x), static_cast<unsigned>(mt));
-    if (small)
-        hipLaunchKernelGGL((k_sign_gemm<1, 2, 1>), grid, dim3(kBlock), 0, stream, gb);
+    const bool split = p[0].split != 0;  // every member of a batch agrees (launch_prefill_batch)
+    if (small && split)
+        hipLaunchKernelGGL((k_sign_gemm<1, 2, 1, true>), grid, dim3(kBlock), 0, stream, gb);
+    else if (small)
+        hipLaunchKernelGGL((k_sign_gemm<1, 2, 1, false>), grid, dim3(kBlock), 0, stream, gb);
+    else if (wide && split)
+        hipLaunchKernelGGL((k_sign_gemm<1, 4, 2, true>), grid, dim3(kBlock), 0, stream, gb);
     else if (wide)
-        hipLaunchKernelGGL((k_sign_gemm<1, 4, 2>), grid, dim3(kBlock), 0, stream, gb);
+        hipLaunchKernelGGL((k_sign_gemm<1, 4, 2, false>), grid, dim3(kBlock), 0, stream, gb);
+    else if (split)
+        hipLaunchKernelGGL((k_sign_gemm<2, 2, 2, true>), grid, dim3(kBlock), 0, stream, gb);
     else
-        hipLaunchKernelGGL((k_sign_gemm<2, 2, 2>), grid, dim3(kBlock), 0, stream, gb);
+        hipLaunchKernelGGL((k_sign_gemm<2, 2, 2, false>), grid, dim3(kBlock), 0, stream, gb);
     if (rx > 0) {
         const dim3 rgrid(static_cast<unsigned>(rx), static_cast<unsigned>(tokens < kRowsPerGridZ ? tokens : kRowsPerGridZ),
                          static_cast<unsigned>((tokens + kRowsPerGridZ - 1) / kRowsPerGridZ));
@@ -970,10 +1027,11 @@ Scratch scratch_layout(const nq_linear_desc* d, int64_t tokens) {
     Scratch s{};
     s.s1 = split_for(mt * ((d->rank + kBN - 1) / kBN), g.nsc1, tokens, d->rank);
     s.s2 = split_for(mt * ((d->out_features + kBN - 1) / kBN), g.nsc2, tokens, d->out_features);
+    const int64_t planes = d->prefill_operands == NQ_PREFILL_FP16_SPLIT ? 2 : 1;
     s.xs16 = 0;
-    s.scale1 = s.xs16 + a256(tokens * g.nsc1 * kBK * 2);
+    s.scale1 = s.xs16 + a256(tokens * g.nsc1 * kBK * 2 * planes);
     s.lm16 = s.scale1 + a256(tokens * 4);
-    s.scale2 = s.lm16 + a256(tokens * g.nsc2 * kBK * 2);
+    s.scale2 = s.lm16 + a256(tokens * g.nsc2 * kBK * 2 * planes);
     s.partial = s.scale2 + a256(tokens * 4);
     const int64_t p1 = s.s1.slices > 1 ? s.s1.slices * tokens * d->rank : 0;
     const int64_t p2 = s.s2.slices > 1 ? s.s2.slices * tokens * d->out_features : 0;
@@ -1005,10 +1063,12 @@ int launch_prefill_batch(const nq_linear_desc* const* descs, int count, const vo
     PrepBatch pb{};
     bool all_vec = true;
     int64_t pad_max = 0;
+    const int split = descs[0]->prefill_operands == NQ_PREFILL_FP16_SPLIT ? 1 : 0;
     for (int i = 0; i < count; ++i) {
         const nq_linear_desc* d = descs[i];
         geo[i] = geometry(d);
         if (d->tiles_bytes < (header_words + geo[i].v_words + geo[i].u_words) * 4) return NQ_ERR_ARGUMENT;
+        if (d->prefill_operands != descs[0]->prefill_operands) return NQ_ERR_ARGUMENT;
         // The GEMMs read the fp16 staging buffers with 16-byte vector loads.
         if (!aligned(scratch[i], 16)) return NQ_ERR_ALIGNMENT;
         sl[i] = scratch_layout(d, tokens);
@@ -1023,6 +1083,7 @@ int launch_prefill_batch(const nq_linear_desc* const* descs, int count, const vo
         pa.cols = d->in_features;
         pa.cols_pad = geo[i].nsc1 * kBK;
         pa.out16 = reinterpret_cast<_Float16*>(ws + sl[i].xs16);
+        pa.split = split;
         pa.scale_out = reinterpret_cast<float*>(ws + sl[i].scale1);
         pa.max_mid_bits = static_cast<const uint32_t*>(d->tiles) + tiles_max_mid_word();
         pa.bound_scale_out = reinterpret_cast<float*>(ws + sl[i].scale2);
@@ -1083,6 +1144,7 @@ int launch_prefill_batch(const nq_linear_desc* const* descs, int count, const vo
         a.out_dtype = NQ_DTYPE_F16;
         a.out_scale = pb.p[i].bound_scale_out;
         a.out_ld = geo[i].nsc2 * kBK;  // GEMM 1's column blocks cover exactly this width
+        a.split = split;
         a.k_per_split = sp[i].k_per_split;
         a.splits = sp[i].slices;
         a.partial = sp[i].slices > 1 ? reinterpret_cast<float*>(ws + sl[i].partial) : nullptr;
@@ -1124,6 +1186,7 @@ int launch_prefill_batch(const nq_linear_desc* const* descs, int count, const vo
         a.bias_dtype = d->bias_dtype;
         a.out = ys[i];
         a.out_dtype = y_dtype;
+        a.split = split;
         a.k_per_split = sp[i].k_per_split;
         a.splits = sp[i].slices;
         a.partial = sp[i].slices > 1 ? reinterpret_cast<float*>(ws + sl[i].partial) : nullptr;

@@ -28,6 +28,9 @@ NQ_STATIC_SCRATCH_BYTES = 4 << 20
 
 NQ_DECODE_SPLIT = 0
 NQ_DECODE_FUSED = 1
+# nq_prefill_operands
+NQ_PREFILL_FP16 = 0
+NQ_PREFILL_FP16_SPLIT = 1
 
 DTYPE_CODES: dict[torch.dtype, int] = {
     torch.float32: 0,
@@ -128,6 +131,7 @@ class LinearDesc(ctypes.Structure):
         ("tiles", ctypes.c_void_p),
         ("tiles_bytes", ctypes.c_int64),
         ("decode_launch", ctypes.c_int32),
+        ("prefill_operands", ctypes.c_int32),
     ]
 
 

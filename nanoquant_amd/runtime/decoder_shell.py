@@ -245,7 +245,9 @@ class PackedDecoder:
         self.max_positions = int(max_positions)
         self.activation_dtype = activation_dtype
         self.cache_dtype = cache_dtype
-        self.backend = backend or HipPackedBackend()
+        # The prompt pass takes split prefill operands: its errors reach every
+        # later token through the KV cache and compound over the layers.
+        self.backend = backend or HipPackedBackend(prefill_operands="split")
         dev = self.device
         self.embed = weights.embed.to(dev, torch.bfloat16).contiguous()
         self.lm_head = weights.lm_head.to(dev, torch.bfloat16).contiguous()

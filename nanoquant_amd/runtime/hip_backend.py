@@ -134,6 +134,7 @@ def _describe(
 
 
 _DECODE_LAUNCH = {"split": _native.NQ_DECODE_SPLIT, "fused": _native.NQ_DECODE_FUSED}
+_PREFILL_OPERANDS = {"fp16": _native.NQ_PREFILL_FP16, "split": _native.NQ_PREFILL_FP16_SPLIT}
 
 
 class HipPackedBackend:
@@ -143,16 +144,25 @@ class HipPackedBackend:
     version = HIP_PACKED_BACKEND_VERSION
     packed_layout = PACKED_LAYOUT_VERSION
 
-    def __init__(self, *, tiled_decode: bool = True, decode_launch: str = "split") -> None:
+    def __init__(self, *, tiled_decode: bool = True, decode_launch: str = "split",
+                 prefill_operands: str = "fp16") -> None:
         """``tiled_decode`` prepares the MFMA tile layout (decode and prefill
         kernels); without it every call takes the canonical-word fp32 path.
         ``decode_launch``: ``"split"`` runs the two decode stages as two
-        kernels, ``"fused"`` as one kernel with an in-kernel grid handoff."""
+        kernels, ``"fused"`` as one kernel with an in-kernel grid handoff.
+        ``prefill_operands`` (above 16 tokens): ``"fp16"`` rounds the prefill
+        GEMMs' activations and rank intermediate to fp16 (about 3e-4 rel-L2
+        per linear); ``"split"`` carries each as an fp16 value plus an fp16
+        remainder (about 1e-6), at twice the MFMA work, for callers whose
+        errors compound through many layers."""
 
         if decode_launch not in _DECODE_LAUNCH:
             raise ValueError(f"decode_launch must be one of {sorted(_DECODE_LAUNCH)}")
+        if prefill_operands not in _PREFILL_OPERANDS:
+            raise ValueError(f"prefill_operands must be one of {sorted(_PREFILL_OPERANDS)}")
         self._tiled_decode = tiled_decode
         self._decode_launch = _DECODE_LAUNCH[decode_launch]
+        self._prefill_operands = _PREFILL_OPERANDS[prefill_operands]
 
     def capabilities(self) -> BackendCapabilities:
         return BackendCapabilities(
@@ -230,6 +240,7 @@ class HipPackedBackend:
         )
         _describe(payload, packed.spec, payload.desc)
         payload.desc.decode_launch = self._decode_launch
+        payload.desc.prefill_operands = self._prefill_operands
         spec = packed.spec
         size = int(lib.nq_tiles_bytes(spec.in_features, spec.out_features, spec.rank))
         if self._tiled_decode and size > 0:

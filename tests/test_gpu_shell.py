@@ -376,16 +376,31 @@ def _check_against_oracle(config, act, cache, tol, prompt_len, new_tokens, seed,
     tokens, logits = _gpu_steps(decoder, prompt, new_tokens)
     oracle = _oracle(config, weights, act, cache, max_positions)
     expected = _teacher_forced(oracle, prompt, tokens)
-    worst = 0.0
+    worst, worst_abs, decided = 0.0, 0.0, 0
     for step, (got, exp, token) in enumerate(zip(logits, expected, tokens)):
-        err = relative_l2(got.cpu(), exp)
-        worst = max(worst, err)
+        got = got.cpu()
+        err = relative_l2(got, exp)
+        abs_err = float((got - exp).abs().max())
+        worst, worst_abs = max(worst, err), max(worst_abs, abs_err)
         assert err <= tol, f"step {step}: rel_l2 {err:.3e} > {tol}"
         assert token == int(torch.argmax(got))
+        # The oracle's greedy token is decided at this step when its top-2
+        # gap exceeds twice the largest logit error measured here: the GPU's
+        # token must then be the oracle's.
         top2 = torch.topk(exp, 2).values
-        if float(top2[0] - top2[1]) > 4 * tol * float(exp.abs().max()):
-            assert token == int(torch.argmax(exp)), f"step {step}: greedy token differs"
-    print(f"  logits worst-step rel_l2={worst:.2e} over {len(tokens)} tokens", flush=True)
+        if float(top2[0] - top2[1]) > 2 * abs_err:
+            decided += 1
+            assert token == int(torch.argmax(exp)), f"step {step}: greedy token differs from the oracle's"
+    print(f"  logits worst-step rel_l2={worst:.2e} max|err|={worst_abs:.2e}; tokens checked against the oracle "
+          f"on {decided} of {len(tokens)} steps", flush=True)
+    # The check must bind. With fp32 activations the logit error is small
+    # enough to decide at least half the steps' tokens. With bf16 activations
+    # and cache every activation is rounded to 8 bits, and the GPU and the
+    # oracle round fp32 sums that differ in the last bits (summation order), so
+    # a rounding flips now and then and the logits drift apart through the
+    # layers: a quarter of the steps must still be decided.
+    need = (len(tokens) + 1) // 2 if act == torch.float32 else (len(tokens) + 3) // 4
+    assert decided >= need, f"only {decided} of {len(tokens)} greedy tokens were decided"
     return decoder, prompt, tokens
 
 
@@ -401,13 +416,14 @@ def test_decoder_qwen3_8b_geometry_matches_oracle(act, cache, tol):
     _check_against_oracle(QWEN_2L, act, cache, tol, prompt_len=12, new_tokens=5, seed=syn.BASE_SEED + 62)
 
 
-@pytest.mark.parametrize("act,cache,tol", [(torch.float32, torch.float32, 1e-2), (torch.bfloat16, torch.bfloat16, 5e-2)])
+@pytest.mark.parametrize("act,cache,tol", [(torch.float32, torch.float32, 2e-3), (torch.bfloat16, torch.bfloat16, 4e-2)])
 def test_decoder_qwen3_8b_full_size_matches_oracle(act, cache, tol):
     # the benchmark's model at full size: 36 layers, full vocabulary, a 512-token prompt
-    # (the MFMA prefill and prompt attention over 8 cache blocks), then 6 greedy tokens
-    # teacher-forced through the oracle; weights generated on the device, copied for the oracle
+    # (the MFMA prefill with split operands and prompt attention over 8 cache blocks), then
+    # 8 greedy tokens teacher-forced through the oracle; weights generated on the device,
+    # copied for the oracle. fp32 activations and cache at the per-linear bar of 2e-3.
     _say("decoder, 36 layers, 512-token prompt", act, cache)
-    _check_against_oracle(QWEN_36L, act, cache, tol, prompt_len=512, new_tokens=6, seed=syn.BASE_SEED + 63,
+    _check_against_oracle(QWEN_36L, act, cache, tol, prompt_len=512, new_tokens=8, seed=syn.BASE_SEED + 63,
                           device=DEV)
 
 

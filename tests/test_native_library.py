@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_only_entry_points():
     lib = _native.load()
-    assert lib.nq_abi_version() == 2
+    assert lib.nq_abi_version() == 3
     assert _native.status_text(-5).startswith("workspace smaller")
     # Argument validation happens before any device work.
     desc = _native.LinearDesc()
