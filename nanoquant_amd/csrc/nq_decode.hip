@@ -325,6 +325,23 @@ struct Shapes {
     int64_t nc1, nc2, ks, max1, max2;
 };
 
+// The stage-1 chunk count that most of a batch's stage-1 tiles have (ties:
+// the larger). A one-token batch plans its stage-1 waves for it; members with
+// more chunks run more passes. Measured on MI355X with the seven linears of a
+// Qwen3-8B layer in one batch (six of 8 chunks, down_proj of 24): 18.4 us per
+// layer against 23.5 us when planned for the widest member (12 waves of two
+// chunks, one 768-thread workgroup per CU).
+int64_t typical_chunks1(const Batch& batch) {
+    int64_t best = 0, best_tiles = -1;
+    for (int i = 0; i < batch.count; ++i) {
+        const int64_t nc = batch.p[i].g1.nc;
+        int64_t tiles = 0;
+        for (int j = 0; j < batch.count; ++j) tiles += batch.p[j].g1.nc == nc ? batch.p[j].g1.nt : 0;
+        if (tiles > best_tiles || (tiles == best_tiles && nc > best)) best = nc, best_tiles = tiles;
+    }
+    return best;
+}
+
 int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
     int64_t tiles1 = 0, tiles2 = 0, nc1 = 0, nc2 = 0, ks = 0;
     for (int i = 0; i < batch.count; ++i) {
@@ -347,7 +364,7 @@ int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
         s1.tw = 1;
     } else {
         if (!stage0_path(tokens)) {
-            pick_waves(nc1, s1.tpb, s1.tb, s1.nw, s1.kc);
+            pick_waves(tokens == 1 ? typical_chunks1(batch) : nc1, s1.tpb, s1.tb, s1.nw, s1.kc);
             pick_waves(nc2, s2.tpb, s2.tb, s2.nw, s2.kc);
             s1.tw = pick_tiles(1, tiles1, s1.nw, s1.kc, s1.tb, false);
             s2.tw = tokens == 1 ? pick_tiles(2, tiles2, s2.nw, s2.kc, s2.tb, false)
