@@ -709,6 +709,20 @@ __device__ __forceinline__ uint32_t pack_bytes(int a, int b, int c, int d) {
            ((static_cast<uint32_t>(c) & 0xffu) << 16) | (static_cast<uint32_t>(d) << 24);
 }
 
+// Byte j of a, b, c, d packed into out[j] (a in byte 0): a 4 x 4 byte
+// transpose in eight v_perm_b32 (result byte k = byte sel_k of {src0:src1},
+// bytes 0-3 from src1, 4-7 from src0).
+__device__ __forceinline__ void transpose_bytes(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (&out)[4]) {
+    const uint32_t ab_lo = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+    const uint32_t cd_lo = __builtin_amdgcn_perm(d, c, 0x05010400u);  // c0 d0 c1 d1
+    const uint32_t ab_hi = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+    const uint32_t cd_hi = __builtin_amdgcn_perm(d, c, 0x07030602u);  // c2 d2 c3 d3
+    out[0] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u);        // a0 b0 c0 d0
+    out[1] = __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u);        // a1 b1 c1 d1
+    out[2] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u);        // a2 b2 c2 d2
+    out[3] = __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u);        // a3 b3 c3 d3
+}
+
 // Signed base-256 digits of w: w = d0 + 256 d1 + 65536 d2 + ..., each digit in
 // [-128, 127]. The byte of d_j is the low byte of w_j with w_0 = w and
 // w_{j+1} = (w_j + 128) >> 8.
@@ -817,8 +831,11 @@ constexpr int kPoisonExp = 0x7fffffff;
 // |a * 2^E| < 2^23 gives |w| < 2^30, rounded once (halves up) from the
 // exact product, as four signed base-256 digits: digit j is the low byte of
 // w_j with w_0 = w, w_{j+1} = (w_j + 128) >> 8, i.e. byte j of w, w + 0x80,
-// w + 0x8080 and w + 0x808080. Every value keeps 24 bits relative to the
-// chunk's largest.
+// w + 0x8080 and w + 0x808080. Byte j of w + 0x808080 is digit j with its top
+// bit flipped for j < 3 (the +0x80 at byte j carries into byte j + 1 exactly
+// as digit j + 1 needs), so the bytes of (w + 0x808080) ^ 0x808080 are the
+// four digits: one add and one xor per value, then a byte transpose of four
+// values. Every value keeps 24 bits relative to the chunk's largest.
 template <int AK, int TOK, int TW, int TPB>
 __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int c, int t_base,
                                             char* __restrict__ ops, int lane, int (&expo)[TPB], float (&csum)[TPB]) {
@@ -872,19 +889,13 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
         uint32_t dig[4][2];
 #pragma unroll
         for (int run = 0; run < 2; ++run) {
-            uint32_t w0[4], w1[4], w2[4], w3[4];
+            uint32_t u[4], t[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t w = static_cast<uint32_t>(round_to_int(v[run][i] * sm));
-                w0[i] = w;
-                w1[i] = w + 0x80u;
-                w2[i] = w + 0x8080u;
-                w3[i] = w + 0x808080u;
-            }
-            dig[0][run] = bytes_at<0>(w0[0], w0[1], w0[2], w0[3]);
-            dig[1][run] = bytes_at<1>(w1[0], w1[1], w1[2], w1[3]);
-            dig[2][run] = bytes_at<2>(w2[0], w2[1], w2[2], w2[3]);
-            dig[3][run] = bytes_at<3>(w3[0], w3[1], w3[2], w3[3]);
+            for (int i = 0; i < 4; ++i)
+                u[i] = (static_cast<uint32_t>(round_to_int(v[run][i] * sm)) + 0x808080u) ^ 0x808080u;
+            transpose_bytes(u[0], u[1], u[2], u[3], t);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dig[j][run] = t[j];
         }
         expo[u] = e;
 #pragma unroll
