@@ -167,12 +167,15 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
 }
 
 // Waves per workgroup and chunks per wave per pass for a stage whose widest
-// member has nc chunks: one chunk per wave up to 16 waves (one token per
-// block) or 8 waves (four), otherwise two chunks per wave on at most 12 (or
-// 8) waves; blocks of several token groups keep one chunk (their activation
-// registers would not fit twice) and the pass loop covers the rest.
+// member has nc chunks. One block of up to four tokens: one chunk per wave up
+// to 16 waves, otherwise two chunks per wave on at most 12 waves (the 24
+// chunks of a 12288-wide input in one pass; measured on MI355X over the
+// Qwen3-8B stack at 2-4 tokens: 49.2 against 50.6 us per layer with at most
+// 8 waves and two passes). Several blocks (the fused launch from five tokens):
+// at most 8 waves of one chunk (their activation registers would not fit
+// twice) and the pass loop covers the rest.
 void pick_waves(int64_t nc, int tpb, int tb, int& nw, int& kc) {
-    if (tpb == 1) {
+    if (tpb == 1 || tb == 1) {
         if (nc <= 16) {
             nw = static_cast<int>(nc);
             kc = 1;

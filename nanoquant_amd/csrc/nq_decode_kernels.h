@@ -1833,7 +1833,7 @@ __global__ __launch_bounds__(THREADS) void k_decode_fused(const Batch batch) {
 }
 
 // Launch bound of a configuration (see k_decode_stage1).
-constexpr int threads_for(int tpb, int kc) { return tpb == 1 ? (kc == 1 ? 1024 : 768) : 512; }
+constexpr int threads_for(int tpb, int kc) { return kc == 1 ? 1024 : 768; }
 
 // Shape of one decode launch, chosen on the host (nq_decode.hip).
 struct LaunchShape {
