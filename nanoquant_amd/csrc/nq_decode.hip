@@ -360,8 +360,12 @@ int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
     s1.tb = s2.tb = tokens <= 4 ? 1 : (tokens <= 8 && !fused && stage0_path(tokens) ? 2 : 4);
     s1.ak = s2.ak = ak;
     if (fused) {
+        // The fused kernel keeps both stages' registers live: blocks of four
+        // tokens stay within 8 waves (512 threads) there.
         int kc_unused = 0;
-        pick_waves(nc1 > nc2 ? nc1 : nc2, s1.tpb, s1.tb, s1.nw, kc_unused);
+        const int64_t ncf = nc1 > nc2 ? nc1 : nc2;
+        pick_waves(ncf, s1.tpb, s1.tb, s1.nw, kc_unused);
+        if (s1.tpb > 1 && s1.nw > 8) s1.nw = 8;
         s1.kc = (s1.tb == 1 && nc1 > s1.nw) ? 2 : 1;
         s1.kc2 = (s1.tb == 1 && nc2 > s1.nw) ? 2 : 1;
         s1.tw = 1;

@@ -7,7 +7,7 @@ namespace {
 
 template <int TPB, int TB, int KC1, int KC2>
 int go(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
-    constexpr int kThreads = threads_for(TPB, KC1 > KC2 ? KC1 : KC2);
+    constexpr int kThreads = TPB == 1 ? threads_for(1, KC1 > KC2 ? KC1 : KC2) : 512;  // see plan_shapes
     if (64 * s.nw > kThreads) return NQ_ERR_LAUNCH;
     hipLaunchKernelGGL((k_decode_fused<TPB, TB, KC1, KC2, kThreads>), s.grid, dim3(64 * s.nw), s.lds, stream,
                        batch);

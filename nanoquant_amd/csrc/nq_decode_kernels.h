@@ -1832,8 +1832,11 @@ __global__ __launch_bounds__(THREADS) void k_decode_fused(const Batch batch) {
     }
 }
 
-// Launch bound of a configuration (see k_decode_stage1).
-constexpr int threads_for(int tpb, int kc) { return kc == 1 ? 1024 : 768; }
+// Launch bound of a configuration (see k_decode_stage1): blocks of up to four
+// tokens take up to 16 waves of one chunk or 12 of two; several token blocks
+// take at most 8 waves (their operand registers for two or four blocks would
+// spill under a bound of 16 waves).
+constexpr int threads_for(int tpb, int kc, int tb = 1) { return tb > 1 ? 512 : (kc == 1 ? 1024 : 768); }
 
 // Shape of one decode launch, chosen on the host (nq_decode.hip).
 struct LaunchShape {

@@ -7,7 +7,7 @@ namespace {
 
 template <int TPB, int TB, int TW, int KC>
 int go(const Batch& batch, const LaunchShape& s, hipStream_t stream) {
-    constexpr int kThreads = threads_for(TPB, KC);
+    constexpr int kThreads = threads_for(TPB, KC, TB);
     if (64 * s.nw > kThreads) return NQ_ERR_LAUNCH;
     hipLaunchKernelGGL((k_decode_stage2<TPB, TB, TW, KC, kThreads>), s.grid, dim3(64 * s.nw), s.lds, stream, batch);
     return nq::launch_status();
