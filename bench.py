@@ -77,6 +77,9 @@ def parse_args(argv=None):
     p.add_argument("--stack-mode-only", default="", metavar="MODE",
                    help="only time the M=1 decode stack in one launch grouping (one of --modes' names) "
                         "and exit (kernel traces of one mode)")
+    p.add_argument("--grouped-eager", type=int, default=0, metavar="M",
+                   help="only launch the 'grouped' decode stack at M tokens eagerly --steps times "
+                        "(per-dispatch traces and counters of one token count) and exit")
     return p.parse_args(argv)
 
 
@@ -854,6 +857,18 @@ def dominant_only(args, device) -> int:
     return 0
 
 
+def grouped_eager(args, device) -> int:
+    import torch
+
+    backend, stack = build_layers(args.layers, device)
+    calls = step_calls(stack_io(stack, args.grouped_eager, device), "grouped", backend)
+    for _ in range(args.steps):
+        run_calls(backend, calls)
+    torch.cuda.synchronize()
+    print(json.dumps({"tokens": args.grouped_eager, "calls": args.steps * len(calls)}))
+    return 0
+
+
 def stack_mode_only(args, device) -> int:
     backend, stack = build_layers(args.layers, device)
     fig = time_stack(backend, stack_io(stack, 1, device), args.stack_mode_only, args.steps, args.warmup)
@@ -891,6 +906,8 @@ def main(argv=None) -> int:
         return 0
     if args.stack_mode_only:
         return stack_mode_only(args, device)
+    if args.grouped_eager:
+        return grouped_eager(args, device)
     wall0 = time.perf_counter()
     result: dict = {}
     c2, dom, backend, _ = (None, None, None, None)
