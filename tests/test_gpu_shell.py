@@ -5,12 +5,16 @@ oracle/decoder_shell.py (itself pinned to transformers' Qwen3) or with plain
 torch fp32 on the same inputs. End-to-end tests run ``PackedDecoder`` against
 the oracle decoder on the same synthetic model, teacher-forced on the GPU's
 own greedy tokens:
-  * fp32 activations and KV cache: logits rel-L2 <= 2e-3 per step (the packed
-    linear's bar; the shell kernels themselves are fp32);
+  * fp32 activations and KV cache: logits rel-L2 <= 2e-3 per step at every
+    size, 36 layers included (the packed linear's bar; the shell kernels
+    themselves are fp32);
   * bf16 activations and KV cache (the deployed configuration) against an
-    oracle that rounds at the same points: rel-L2 <= 2e-2;
-  * the greedy token is the argmax of the returned logits and agrees with the
-    oracle's unless the oracle's top-2 gap is within the tolerance;
+    oracle that rounds at the same points: rel-L2 <= 2e-2 (two and three
+    layers), 4e-2 (36 layers: rounding flips add up with depth);
+  * the greedy token is the argmax of the returned logits, and equals the
+    oracle's at every step where the oracle's top-2 gap exceeds twice the
+    largest logit error of that step; at least half of the steps (fp32) or a
+    quarter (bf16) must be decided that way;
   * graph replay, eager steps and the ``forward_step`` protocol give identical tokens.
 """
 
