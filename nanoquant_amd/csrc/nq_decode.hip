@@ -88,16 +88,8 @@ int64_t lmq_bytes_for(const MatGeo& g2, int64_t tokens) {
     return lmq_bytes<4, 4>(g2);
 }
 
-int64_t round256(int64_t n) { return (n + 255) & ~int64_t(255); }
-
-// Several tokens: stage 0's operands of x * s_in (xq, sized for four token
-// blocks above four tokens) and its per-(chunk, token) exponents and maxima.
-int64_t xq_bytes_for(const MatGeo& g1, int64_t tokens) {
-    return tokens == 1 ? 0 : g1.nc * (tokens <= 4 ? 1 : 4) * Ops<4>::kBytes;
-}
-int64_t xe_bytes_for(const MatGeo& g1, int64_t tokens) { return tokens == 1 ? 0 : round256(g1.nc * kMaxTokens * 4); }
-
-// Workspace: [lmq][lme: 256 B][xq][xe][xm] (the last three for several tokens).
+// Workspace: [lmq][lme: 256 B][xq][xe][xm] (the last three for several
+// tokens, at the addresses multi_ws derives from lme).
 int64_t scratch_bytes(const TilesGeometry& g, int64_t tokens) {
     return round256(lmq_bytes_for(g.g2, tokens)) + 256 + round256(xq_bytes_for(g.g1, tokens)) +
            2 * xe_bytes_for(g.g1, tokens);
@@ -153,16 +145,8 @@ int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens
     a.y = y;
     a.y_dtype = y_dtype;
     char* const ws = static_cast<char*>(scratch);
-    const int64_t lme_at = round256(lmq_bytes_for(g.g2, tokens));
-    const int64_t xq_at = lme_at + 256;
-    const int64_t xe_at = xq_at + round256(xq_bytes_for(g.g1, tokens));
     a.lmq = reinterpret_cast<uint8_t*>(ws);
-    a.lme = reinterpret_cast<int*>(ws + lme_at);
-    if (tokens > 1) {
-        a.xq = reinterpret_cast<uint8_t*>(ws + xq_at);
-        a.xe = reinterpret_cast<int*>(ws + xe_at);
-        a.xm = reinterpret_cast<float*>(ws + xe_at + xe_bytes_for(g.g1, tokens));
-    }
+    a.lme = reinterpret_cast<int*>(ws + round256(lmq_bytes_for(g.g2, tokens)));
     return NQ_OK;
 }
 

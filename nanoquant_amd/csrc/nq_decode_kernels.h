@@ -213,14 +213,6 @@ struct LinArgs {
     int attn_blocks;            // cache blocks of kAttnBlockRows rows
     int attn_hd_log2;           // log2(head_dim)
     int64_t attn_max_positions;
-    // Several tokens (split launch): stage 0 writes the stage-1 A operands of
-    // x * s_in here in the lmq layout (four digit rows per token), with the
-    // exponent and Σ |x s_in| of every (chunk, token) at
-    // [chunk * kMaxTokens + token].
-    uint8_t* xq;
-    int* xe;
-    float* xm;
-    void* pad_;
 };
 static_assert(sizeof(LinArgs) % 16 == 0, "LinArgs is read as 16-byte vectors");
 
@@ -302,9 +294,6 @@ __device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
     a.attn_blocks = s.attn_blocks;
     a.attn_hd_log2 = s.attn_hd_log2;
     a.attn_max_positions = s.attn_max_positions;
-    a.xq = s.xq;
-    a.xe = s.xe;
-    a.xm = s.xm;
     // One statement, so every field is waited for at the same point; it
     // redefines the integer fields, so no arithmetic on them can be hoisted
     // above it (the pointers are only read, so they stay known-global).
@@ -313,7 +302,7 @@ __device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
                    "+s"(a.g2.nt), "+s"(a.g2.nb), "+s"(a.g2.nc), "+s"(a.nwg1), "+s"(a.nwg2), "+s"(a.x_dtype),
                    "+s"(a.tokens), "+s"(a.scale_dtype), "+s"(a.bias_dtype), "+s"(a.nw1), "+s"(a.nw2)
                  : "s"(a.v_tiles), "s"(a.u_tiles), "s"(a.header), "s"(a.x), "s"(a.s_in), "s"(a.s_mid), "s"(a.s_out),
-                   "s"(a.bias), "s"(a.lmq), "s"(a.lme), "s"(a.xq), "s"(a.xe), "s"(a.xm));
+                   "s"(a.bias), "s"(a.lmq), "s"(a.lme));
     return a;
 }
 // Activation kinds (template parameter AK): how stage 1 reads a[t, k].
@@ -358,6 +347,34 @@ __host__ __device__ inline int lmq_offset(int c, int tb, int m, int row, int g) 
 
 template <int TPB, int TB>
 __host__ __device__ inline int64_t lmq_bytes(const MatGeo& g2) { return g2.nc * TB * Ops<TPB>::kBytes; }
+
+// Several tokens (split launch from five tokens): stage 0 writes the stage-1 A
+// operands of x * s_in in the lmq layout (xq, one token block up to four
+// tokens, four above), with the exponent (xe) and Σ |x s_in| (xm) of every
+// (chunk, token) at [chunk * kMaxTokens + token]. They follow the 256-byte
+// exponent line lme in the workspace, each 256-byte aligned, so the kernels
+// derive their addresses from lme and the geometry. Measured on MI355X: the
+// three pointers as kernel arguments, loaded by every launch's load_args,
+// cost the one-token stack 1.0 us per Qwen3 layer (35.0 against 36.0) and
+// end-to-end decode 2.3% (523.3 against 511.5 tok/s).
+__host__ __device__ inline int64_t round256(int64_t n) { return (n + 255) & ~int64_t(255); }
+__host__ __device__ inline int64_t xq_bytes_for(const MatGeo& g1, int64_t tokens) {
+    return tokens == 1 ? 0 : g1.nc * (tokens <= 4 ? 1 : 4) * Ops<4>::kBytes;
+}
+__host__ __device__ inline int64_t xe_bytes_for(const MatGeo& g1, int64_t tokens) {
+    return tokens == 1 ? 0 : round256(g1.nc * kMaxTokens * 4);
+}
+struct MultiWs {
+    uint8_t* xq;
+    int* xe;
+    float* xm;
+};
+__host__ __device__ inline MultiWs multi_ws(int* lme, const MatGeo& g1, int64_t tokens) {
+    char* const xq = reinterpret_cast<char*>(lme) + 256;
+    char* const xe = xq + round256(xq_bytes_for(g1, tokens));
+    return MultiWs{reinterpret_cast<uint8_t*>(xq), reinterpret_cast<int*>(xe),
+                   reinterpret_cast<float*>(xe + xe_bytes_for(g1, tokens))};
+}
 
 // Nearest integer of x (halves round up), |x| < 2^31: one instruction
 // (v_cvt_rpi_i32_f32 computes floor(x + 0.5)) where rintf and a conversion
@@ -1312,7 +1329,8 @@ __device__ __forceinline__ void stage0_wave(const LinArgs& a, int c, int tb, int
     b.tokens = a.tokens - TPB * tb < TPB ? a.tokens - TPB * tb : TPB;
     S1Regs<AK, TPB, 1> r;
     load_s1_acts<AK, TPB, 1>(r, b, c, lane);
-    char* const ops = reinterpret_cast<char*>(a.xq) + (c * tbl + tb) * Ops<TPB>::kBytes;
+    const MultiWs ws = multi_ws(a.lme, a.g1, a.tokens);
+    char* const ops = reinterpret_cast<char*>(ws.xq) + (c * tbl + tb) * Ops<TPB>::kBytes;
     int expo[TPB];
     float cm[TPB];
     stage_block<AK, TPB, 1, TPB>(r, b, c, 0, ops, lane, expo, cm);
@@ -1324,8 +1342,8 @@ __device__ __forceinline__ void stage0_wave(const LinArgs& a, int c, int tb, int
         mx = lane == u ? cm[u] : mx;
     }
     if (lane < TPB) {
-        a.xe[c * kMaxTokens + TPB * tb + lane] = e;
-        a.xm[c * kMaxTokens + TPB * tb + lane] = mx;
+        ws.xe[c * kMaxTokens + TPB * tb + lane] = e;
+        ws.xm[c * kMaxTokens + TPB * tb + lane] = mx;
     }
 }
 
@@ -1361,6 +1379,7 @@ __device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __
     float* const red = reinterpret_cast<float*>(lds);
     float* const cmx = red + nc * TW * TB * 64;  // [nc][kMaxTokens] Σ |x s_in|
     const int nxm = nc * kMaxTokens;
+    const MultiWs ws = multi_ws(a.lme, a.g1, tokens);
 
     const int outs = TW * tokens * kTileRows;
     const OutIdx f = out_index<TPB>(threadIdx.x < outs ? threadIdx.x : 0, tokens);
@@ -1387,14 +1406,14 @@ __device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __
 #pragma unroll
                 for (int m = 0; m < 8; ++m)
                     r[j].a[i][m] = *reinterpret_cast<const v4i*>(
-                        a.xq + lmq_offset<TPB, TB>(pc.c[j], tb, m, lane & 15, lane >> 4));
-                e[j][i] = a.xe[pc.c[j] * kMaxTokens + TPB * tb + (lane >> 4)];
+                        ws.xq + lmq_offset<TPB, TB>(pc.c[j], tb, m, lane & 15, lane >> 4));
+                e[j][i] = ws.xe[pc.c[j] * kMaxTokens + TPB * tb + (lane >> 4)];
             }
         if (first) {
             const int frc = fr < rank ? fr : rank - 1;
             rs0 = load_elem(a.s_mid, a.scale_dtype, frc);
             maxsm = __uint_as_float(scalar_load(a.header + line_word(kMiscLine) + kMiscMaxMid));
-            xmv = a.xm[static_cast<int>(threadIdx.x) < nxm ? static_cast<int>(threadIdx.x) : 0];
+            xmv = ws.xm[static_cast<int>(threadIdx.x) < nxm ? static_cast<int>(threadIdx.x) : 0];
         }
         __builtin_amdgcn_sched_barrier(0);  // every load of the pass is issued before any use
 #pragma unroll
@@ -1423,7 +1442,7 @@ __device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __
     pass(0, true);
     for (int base = step; base < nc; base += step) pass(base, false);
     if (static_cast<int>(threadIdx.x) < nxm) cmx[threadIdx.x] = xmv;
-    for (int i = static_cast<int>(threadIdx.x) + nthreads; i < nxm; i += nthreads) cmx[i] = a.xm[i];
+    for (int i = static_cast<int>(threadIdx.x) + nthreads; i < nxm; i += nthreads) cmx[i] = ws.xm[i];
     __syncthreads();
 
     if (dead) return;  // uniform, after the workgroup's only barrier
