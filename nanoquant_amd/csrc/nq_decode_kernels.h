@@ -171,49 +171,61 @@ __device__ __forceinline__ int chunk_words32(int nb, int c) {
 // Decode kernels.
 // ---------------------------------------------------------------------------
 
-struct LinArgs {
+// One linear of a decode launch. The fields every kernel waits for before its
+// first load (load_args) fill the first three 64-byte lines; the epilogue,
+// sidecar and fusion fields follow. Members are 64-byte aligned, so a
+// launch's argument wait covers three scalar-cache lines per workgroup.
+struct alignas(64) LinArgs {
+    // line 0
     int64_t in, rank, out;
-    MatGeo g1, g2;           // V [rank, in], U [out, rank]
+    MatGeo g1;               // V [rank, in]
     int64_t nwg1, nwg2;      // workgroups of each stage (tiles / tiles per workgroup)
+    // line 1
+    MatGeo g2;               // U [out, rank]
     const uint32_t* v_tiles;
     const uint32_t* u_tiles;
     uint32_t* header;
     const void* x;
-    int x_dtype;
-    int tokens;
     const void* s_in;
+    // line 2
     const void* s_mid;
     const void* s_out;
+    const void* bias;
+    uint8_t* lmq;            // stage-2 A operands, see lmq_offset
+    int* lme;                // [tokens] exponent of lmq per token
+    int x_dtype;
+    int tokens;
     int scale_dtype;
+    int bias_dtype;
+    int nw1, nw2;            // waves per workgroup of each stage (the fused launch: both equal)
+    // line 3
+    void* y;
+    int y_dtype;
+    int salient_dtype;
     int64_t salient_count;
     const int32_t* salient_indices;
     const void* salient_values;
-    int salient_dtype;
     const void* salient_scales;
-    const void* bias;
-    int bias_dtype;
-    void* y;
-    int y_dtype;
-    uint8_t* lmq;            // stage-2 A operands, see lmq_offset
-    int* lme;                // [tokens] exponent of lmq per token
-    int nw1, nw2;            // waves per workgroup of each stage (the fused launch: both equal)
     // Decoder fusions (nq_linear_batch_fused, one token; null / zero otherwise).
     const void* x2;          // gated input: up [in] (fp32); x is the gate
     const float* col_scale;  // normed input: fp32 column scale replacing s_in
+    // line 4
     const float* slots_in;   // normed input: sums of squares of x per 16-row tile of its producer
     float* residual;         // stage 2: residual[o] += y (y is not written)
     float* slots_out;        // stage 2: sum of residual^2 per 16-row output tile
-    int nslots;              // entries of slots_in
-    float eps;               // normed input: RMSNorm epsilon
     // Attention input (one token): x is the fp32 partial accumulators of the
     // decode attention's pass 1, [heads][attn_blocks][head_dim] with heads =
     // in / head_dim, and attn_ml their (max, sum) pairs [heads][attn_blocks][2].
     const float* attn_ml;
     const int32_t* attn_pos;    // the token's cache position
+    int nslots;              // entries of slots_in
+    float eps;               // normed input: RMSNorm epsilon
     int attn_blocks;            // cache blocks of kAttnBlockRows rows
     int attn_hd_log2;           // log2(head_dim)
     int64_t attn_max_positions;
 };
+static_assert(sizeof(LinArgs) == 320 && offsetof(LinArgs, nw2) + 4 == 192 && offsetof(LinArgs, slots_in) == 256,
+              "the load_args fields fill lines 0-2");
 static_assert(sizeof(LinArgs) % 16 == 0, "LinArgs is read as 16-byte vectors");
 
 // ---------------------------------------------------------------------------
