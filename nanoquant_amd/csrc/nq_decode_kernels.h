@@ -257,11 +257,18 @@ struct Batch {
 };
 
 // A member's arguments, copied field by field from the kernel-argument segment
-// with every field then used by an empty asm: all the scalar loads are issued
-// together and complete at one point, instead of lazily (one dependent round
-// trip per uniform branch that needs a field). The copies stay typed loads, so
-// the pointers are still known to be global.
-__device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
+// (copy_args), with the fields a kernel needs before its first load then used
+// by one empty asm (pin_args): all those scalar loads are issued together and
+// complete at one point, instead of lazily (one dependent round trip per
+// uniform branch that needs a field). The copies stay typed loads, so the
+// pointers are still known to be global. The fused input kinds add the fields
+// they read first (kArgsNorm: the column scale and the producer's row sums;
+// kArgsGated: the up input; kArgsAttn: the attention partials and position)
+// to the same wait: left to the compiler, those loads were issued only after
+// it, a second scalar round trip before the kernel's first vector load.
+enum : int { kArgsPlain = 0, kArgsNorm = 1, kArgsGated = 2, kArgsAttn = 3 };
+
+__device__ __forceinline__ LinArgs copy_args(const Batch& batch, int member) {
     const LinArgs& s = batch.p[member];
     LinArgs a;
     a.in = s.in;
@@ -306,15 +313,64 @@ __device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
     a.attn_blocks = s.attn_blocks;
     a.attn_hd_log2 = s.attn_hd_log2;
     a.attn_max_positions = s.attn_max_positions;
-    // One statement, so every field is waited for at the same point; it
-    // redefines the integer fields, so no arithmetic on them can be hoisted
-    // above it (the pointers are only read, so they stay known-global).
-    asm volatile(""
-                 : "+s"(a.in), "+s"(a.rank), "+s"(a.out), "+s"(a.g1.nt), "+s"(a.g1.nb), "+s"(a.g1.nc),
-                   "+s"(a.g2.nt), "+s"(a.g2.nb), "+s"(a.g2.nc), "+s"(a.nwg1), "+s"(a.nwg2), "+s"(a.x_dtype),
-                   "+s"(a.tokens), "+s"(a.scale_dtype), "+s"(a.bias_dtype), "+s"(a.nw1), "+s"(a.nw2)
-                 : "s"(a.v_tiles), "s"(a.u_tiles), "s"(a.header), "s"(a.x), "s"(a.s_in), "s"(a.s_mid), "s"(a.s_out),
-                   "s"(a.bias), "s"(a.lmq), "s"(a.lme));
+    return a;
+}
+
+// One statement per use, so every field it names is waited for at the same
+// point; it redefines the integer fields, so no arithmetic on them can be
+// hoisted above it (the pointers are only read, so they stay known-global).
+// Each stage pins only what it reads (fewer live scalar registers: the
+// compiler otherwise reloads some fields after the wait), kPinStages both.
+enum : int { kPinStage1 = 1, kPinStage2 = 2, kPinStages = 3 };
+#define NQ_PIN1_OUT(a)                                                                                          \
+    "+s"(a.in), "+s"(a.rank), "+s"(a.g1.nt), "+s"(a.g1.nb), "+s"(a.g1.nc), "+s"(a.g2.nc), "+s"(a.nwg1),         \
+        "+s"(a.nw1), "+s"(a.x_dtype), "+s"(a.tokens), "+s"(a.scale_dtype)
+#define NQ_PIN1_IN(a) "s"(a.v_tiles), "s"(a.header), "s"(a.x), "s"(a.s_in), "s"(a.s_mid), "s"(a.lmq), "s"(a.lme)
+#define NQ_PIN2_OUT(a)                                                                                          \
+    "+s"(a.rank), "+s"(a.out), "+s"(a.g2.nt), "+s"(a.g2.nb), "+s"(a.g2.nc), "+s"(a.nwg2), "+s"(a.nw2),          \
+        "+s"(a.tokens), "+s"(a.scale_dtype), "+s"(a.bias_dtype)
+#define NQ_PIN2_IN(a) "s"(a.u_tiles), "s"(a.s_out), "s"(a.bias), "s"(a.lmq), "s"(a.lme)
+#define NQ_PIN_OUT(a)                                                                                           \
+    "+s"(a.in), "+s"(a.rank), "+s"(a.out), "+s"(a.g1.nt), "+s"(a.g1.nb), "+s"(a.g1.nc), "+s"(a.g2.nt),          \
+        "+s"(a.g2.nb), "+s"(a.g2.nc), "+s"(a.nwg1), "+s"(a.nwg2), "+s"(a.x_dtype), "+s"(a.tokens),               \
+        "+s"(a.scale_dtype), "+s"(a.bias_dtype), "+s"(a.nw1), "+s"(a.nw2)
+#define NQ_PIN_IN(a)                                                                                            \
+    "s"(a.v_tiles), "s"(a.u_tiles), "s"(a.header), "s"(a.x), "s"(a.s_in), "s"(a.s_mid), "s"(a.s_out),          \
+        "s"(a.bias), "s"(a.lmq), "s"(a.lme)
+template <int STAGE, int EXTRA>
+__device__ __forceinline__ void pin_args(LinArgs& a) {
+    if constexpr (STAGE == kPinStage2) {
+        asm volatile("" : NQ_PIN2_OUT(a) : NQ_PIN2_IN(a));
+    } else if constexpr (STAGE == kPinStages) {
+        asm volatile("" : NQ_PIN_OUT(a) : NQ_PIN_IN(a));
+    } else if constexpr (EXTRA == kArgsNorm) {
+        asm volatile("" : NQ_PIN1_OUT(a), "+s"(a.nslots), "+s"(a.eps) : NQ_PIN1_IN(a), "s"(a.col_scale), "s"(a.slots_in));
+    } else if constexpr (EXTRA == kArgsGated) {
+        asm volatile("" : NQ_PIN1_OUT(a) : NQ_PIN1_IN(a), "s"(a.x2));
+    } else if constexpr (EXTRA == kArgsAttn) {
+        asm volatile(""
+                     : NQ_PIN1_OUT(a), "+s"(a.attn_blocks), "+s"(a.attn_hd_log2), "+s"(a.attn_max_positions)
+                     : NQ_PIN1_IN(a), "s"(a.attn_ml), "s"(a.attn_pos));
+    } else {
+        asm volatile("" : NQ_PIN1_OUT(a) : NQ_PIN1_IN(a));
+    }
+}
+
+// Both members of a paired stage 2 in one statement: one wait for both.
+__device__ __forceinline__ void pin_args2(LinArgs& a, LinArgs& b) {
+    asm volatile("" : NQ_PIN2_OUT(a), NQ_PIN2_OUT(b) : NQ_PIN2_IN(a), NQ_PIN2_IN(b));
+}
+#undef NQ_PIN1_OUT
+#undef NQ_PIN1_IN
+#undef NQ_PIN2_OUT
+#undef NQ_PIN2_IN
+#undef NQ_PIN_OUT
+#undef NQ_PIN_IN
+
+template <int STAGE, int EXTRA = kArgsPlain>
+__device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
+    LinArgs a = copy_args(batch, member);
+    pin_args<STAGE, EXTRA>(a);
     return a;
 }
 // Activation kinds (template parameter AK): how stage 1 reads a[t, k].
@@ -1796,7 +1852,11 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
 template <int AK, int TPB, int TB, int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage1(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const LinArgs a = load_args(batch, blockIdx.y);
+    constexpr int kExtra = AK == kActNormF32    ? kArgsNorm
+                           : AK == kActGatedF32 ? kArgsGated
+                           : attn_kind<AK>()    ? kArgsAttn
+                                                : kArgsPlain;
+    const LinArgs a = load_args<kPinStage1, kExtra>(batch, blockIdx.y);
     const int nwg = static_cast<int>(a.nwg1);
     if (static_cast<int>(blockIdx.x) >= nwg) return;  // grid padding: the arguments are already loaded
     stage1_wg<AK, TPB, TB, TW, KC, false>(a, xcd_block(blockIdx.x, nwg), lds);
@@ -1806,7 +1866,7 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage1(const Batch batch) {
 // members), four waves per workgroup, one (chunk, token block) per wave.
 template <int AK>
 __global__ __launch_bounds__(256) void k_decode_stage0(const Batch batch) {
-    const LinArgs a = load_args(batch, blockIdx.y);
+    const LinArgs a = load_args<kPinStage1>(batch, blockIdx.y);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nblk = (a.tokens + 3) >> 2;
@@ -1820,7 +1880,7 @@ __global__ __launch_bounds__(256) void k_decode_stage0(const Batch batch) {
 template <int TB, int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage1m(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const LinArgs a = load_args(batch, blockIdx.y);
+    const LinArgs a = load_args<kPinStage1>(batch, blockIdx.y);
     const int nwg = static_cast<int>(a.nwg1);
     if (static_cast<int>(blockIdx.x) >= nwg) return;
     stage1m_wg<TB, TW, KC>(a, xcd_block(blockIdx.x, nwg), lds);
@@ -1829,7 +1889,7 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage1m(const Batch batch) {
 template <int TPB, int TB, int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage2(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const LinArgs a = load_args(batch, blockIdx.y);
+    const LinArgs a = load_args<kPinStage2>(batch, blockIdx.y);
     const int nwg = static_cast<int>(a.nwg2);
     if (static_cast<int>(blockIdx.x) >= nwg) return;  // grid padding: the arguments are already loaded
     stage2_wg<TPB, TB, TW, KC, false>(a, xcd_block(blockIdx.x, nwg), lds);
@@ -1839,8 +1899,9 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage2(const Batch batch) {
 template <int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage2_pair(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const LinArgs a = load_args(batch, 0);
-    const LinArgs b = load_args(batch, 1);
+    LinArgs a = copy_args(batch, 0);
+    LinArgs b = copy_args(batch, 1);
+    pin_args2(a, b);
     const int nwg = static_cast<int>(a.nwg2);
     if (static_cast<int>(blockIdx.x) >= nwg) return;
     stage2_wg<1, 1, TW, KC, false, true>(a, xcd_block(blockIdx.x, nwg), lds, &b);
@@ -1853,7 +1914,7 @@ __global__ __launch_bounds__(THREADS) void k_decode_fused(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int y = static_cast<int>(blockIdx.y);
     const int count = batch.count;
-    const LinArgs a = load_args(batch, y < count ? y : y - count);
+    const LinArgs a = load_args<kPinStages>(batch, y < count ? y : y - count);
     if (y < count) {
         if (blockIdx.x >= a.nwg1) return;
         stage1_wg<kActGeneric, TPB, TB, 1, KC1, true>(a, blockIdx.x, lds);

@@ -684,7 +684,9 @@ __global__ __launch_bounds__(kMfmaHeads * kWave) void k_decode_attention_mfma(
 
     const int g = blockIdx.x;
     const int s = blockIdx.y;
-    const int blocks = gridDim.y;
+    // gridDim.y, from an argument: gridDim is read from the hidden kernel
+    // arguments, one more scalar-cache line before the first load.
+    const int blocks = static_cast<int>((max_positions + kSeqBlock - 1) / kSeqBlock);
     const int q_heads = kv_heads * G;
     const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
     const int lane = threadIdx.x & (kWave - 1);
@@ -1081,7 +1083,9 @@ __global__ __launch_bounds__(G * kWave) void k_decode_attention(
 
     const int g = blockIdx.x;
     const int s = blockIdx.y;
-    const int blocks = gridDim.y;
+    // gridDim.y, from an argument: gridDim is read from the hidden kernel
+    // arguments, one more scalar-cache line before the first load.
+    const int blocks = static_cast<int>((max_positions + kSeqBlock - 1) / kSeqBlock);
     const int q_heads = kv_heads * G;
     const int w = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
