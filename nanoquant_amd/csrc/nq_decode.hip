@@ -81,12 +81,7 @@ TilesGeometry geometry(int64_t in, int64_t out, int64_t rank) {
     return g;
 }
 
-// Decode workspace: [stage-2 operands (lmq)][per-token exponents (lme)].
-int64_t lmq_bytes_for(const MatGeo& g2, int64_t tokens) {
-    if (tokens == 1) return lmq_bytes<1, 1>(g2);
-    if (tokens <= 4) return lmq_bytes<4, 1>(g2);
-    return lmq_bytes<4, 4>(g2);
-}
+static_assert(Ops<1>::kBytes == 2048 && Ops<4>::kBytes == 8192, "lmq_bytes_for's operand block sizes");
 
 // Workspace: [lmq][lme: 256 B][xq][xe][xm] (the last three for several
 // tokens, at the addresses multi_ws derives from lme).
@@ -108,13 +103,13 @@ bool offsets_fit(const TilesGeometry& g, int64_t in, int64_t out, int64_t tokens
 // Fill one linear of a batch; NQ_OK or an error status. `vector_ok` is cleared
 // when this member's x or s_in cannot take the vector-load kinds.
 int describe(const nq_linear_desc* d, const void* x, int x_dtype, int64_t tokens, void* y, int y_dtype,
-             void* scratch, LinArgs& a, bool& vector_ok) {
+             void* scratch, Lin& a, bool& vector_ok) {
     const TilesGeometry g = geometry(d->in_features, d->out_features, d->rank);
     if (!d->tiles) return NQ_ERR_ARGUMENT;
     if (d->tiles_bytes < tiles_bytes_of(g)) return NQ_ERR_ARGUMENT;
     if (!offsets_fit(g, d->in_features, d->out_features, tokens, d->salient_count)) return NQ_ERR_SHAPE;
     if (!aligned(d->tiles, 16) || !aligned(scratch, 16)) return NQ_ERR_ALIGNMENT;
-    a = LinArgs{};
+    a = Lin{};
     a.in = d->in_features;
     a.rank = d->rank;
     a.out = d->out_features;
@@ -259,7 +254,7 @@ int enqueue_stage1(const Batch& batch, const LaunchShape& s, hipStream_t stream)
 int64_t attn_blocks_of(int64_t max_positions) { return (max_positions + kAttnBlockRows - 1) / kAttnBlockRows; }
 
 // Fill member i's fusion fields; NQ_OK or an error status.
-int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, LinArgs& a) {
+int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, Lin& a) {
     const int64_t in = d->in_features;
     if (f.input_kind == NQ_INPUT_RMSNORM) {
         if (!f.col_scales || !f.col_scales[i] || !f.norm_slots) return NQ_ERR_ARGUMENT;
@@ -318,7 +313,7 @@ struct Shapes {
 // Qwen3-8B layer in one batch (six of 8 chunks, down_proj of 24): 18.4 us per
 // layer against 23.5 us when planned for the widest member (12 waves of two
 // chunks, one 768-thread workgroup per CU).
-int64_t typical_chunks1(const Batch& batch) {
+int64_t typical_chunks1(const HostBatch& batch) {
     int64_t best = 0, best_tiles = -1;
     for (int i = 0; i < batch.count; ++i) {
         const int64_t nc = batch.p[i].g1.nc;
@@ -329,7 +324,7 @@ int64_t typical_chunks1(const Batch& batch) {
     return best;
 }
 
-int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
+int plan_shapes(HostBatch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
     int64_t tiles1 = 0, tiles2 = 0, nc1 = 0, nc2 = 0, ks = 0;
     for (int i = 0; i < batch.count; ++i) {
         ks = batch.p[i].salient_count <= kSalMax && batch.p[i].salient_count > ks ? batch.p[i].salient_count : ks;
@@ -376,7 +371,7 @@ int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
     batch.tw2 = fused ? 1 : s2.tw;
     int64_t max1 = 0, max2 = 0;
     for (int i = 0; i < batch.count; ++i) {
-        LinArgs& a = batch.p[i];
+        Lin& a = batch.p[i];
         a.nw1 = s1.nw;
         a.nw2 = fused ? s1.nw : s2.nw;
         a.nwg1 = (a.g1.nt + batch.tw1 - 1) / batch.tw1;
@@ -394,10 +389,12 @@ int plan_shapes(Batch& batch, int64_t tokens, int ak, bool fused, Shapes& sh) {
 // XCDs round-robin in linear order).
 unsigned xcd_grid(int64_t workgroups) { return static_cast<unsigned>((workgroups + 7) & ~int64_t(7)); }
 
-int launch_batch(Batch& batch, int64_t tokens, int ak, bool fused, hipStream_t stream, bool pair = false) {
+int launch_batch(HostBatch& plan, int64_t tokens, int ak, bool fused, hipStream_t stream, bool pair = false) {
     Shapes sh{};
-    int st = plan_shapes(batch, tokens, ak, fused, sh);
+    int st = plan_shapes(plan, tokens, ak, fused, sh);
     if (st != NQ_OK) return st;
+    Batch batch;
+    pack_batch(plan, batch);
     LaunchShape s1 = sh.s1, s2 = sh.s2;
     const int64_t nc1 = sh.nc1, nc2 = sh.nc2, ks = sh.ks, max1 = sh.max1, max2 = sh.max2;
     const unsigned count = static_cast<unsigned>(batch.count);
@@ -466,7 +463,7 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
                         hipStream_t stream, const nq_decode_fusion* fusion) {
     if (count < 1 || count > kMaxBatch) return NQ_ERR_SHAPE;
     if (tokens < 1 || tokens > kMaxTokens) return NQ_ERR_SHAPE;
-    Batch batch{};
+    HostBatch batch{};
     batch.count = count;
     bool vector_ok = true;
     for (int i = 0; i < count; ++i) {

@@ -171,62 +171,156 @@ __device__ __forceinline__ int chunk_words32(int nb, int c) {
 // Decode kernels.
 // ---------------------------------------------------------------------------
 
-// One linear of a decode launch. The fields every kernel waits for before its
-// first load (load_args) fill the first three 64-byte lines; the epilogue,
-// sidecar and fusion fields follow. Members are 64-byte aligned, so a
-// launch's argument wait covers three scalar-cache lines per workgroup.
-struct alignas(64) LinArgs {
-    // line 0
+// One linear of a decode launch as the kernels and the host planning use it.
+struct Lin {
     int64_t in, rank, out;
-    MatGeo g1;               // V [rank, in]
+    MatGeo g1, g2;           // V [rank, in], U [out, rank]
     int64_t nwg1, nwg2;      // workgroups of each stage (tiles / tiles per workgroup)
-    // line 1
-    MatGeo g2;               // U [out, rank]
     const uint32_t* v_tiles;
     const uint32_t* u_tiles;
     uint32_t* header;
     const void* x;
-    const void* s_in;
-    // line 2
-    const void* s_mid;
-    const void* s_out;
-    const void* bias;
-    uint8_t* lmq;            // stage-2 A operands, see lmq_offset
-    int* lme;                // [tokens] exponent of lmq per token
     int x_dtype;
     int tokens;
+    const void* s_in;
+    const void* s_mid;
+    const void* s_out;
     int scale_dtype;
-    int bias_dtype;
-    int nw1, nw2;            // waves per workgroup of each stage (the fused launch: both equal)
-    // line 3
-    void* y;
-    int y_dtype;
-    int salient_dtype;
     int64_t salient_count;
     const int32_t* salient_indices;
     const void* salient_values;
+    int salient_dtype;
     const void* salient_scales;
+    const void* bias;
+    int bias_dtype;
+    void* y;
+    int y_dtype;
+    uint8_t* lmq;            // stage-2 A operands, see lmq_offset
+    int* lme;                // [tokens] exponent of lmq per token
+    int nw1, nw2;            // waves per workgroup of each stage (the fused launch: both equal)
     // Decoder fusions (nq_linear_batch_fused, one token; null / zero otherwise).
     const void* x2;          // gated input: up [in] (fp32); x is the gate
     const float* col_scale;  // normed input: fp32 column scale replacing s_in
-    // line 4
     const float* slots_in;   // normed input: sums of squares of x per 16-row tile of its producer
     float* residual;         // stage 2: residual[o] += y (y is not written)
     float* slots_out;        // stage 2: sum of residual^2 per 16-row output tile
+    int nslots;              // entries of slots_in
+    float eps;               // normed input: RMSNorm epsilon
     // Attention input (one token): x is the fp32 partial accumulators of the
     // decode attention's pass 1, [heads][attn_blocks][head_dim] with heads =
     // in / head_dim, and attn_ml their (max, sum) pairs [heads][attn_blocks][2].
     const float* attn_ml;
     const int32_t* attn_pos;    // the token's cache position
-    int nslots;              // entries of slots_in
-    float eps;               // normed input: RMSNorm epsilon
     int attn_blocks;            // cache blocks of kAttnBlockRows rows
     int attn_hd_log2;           // log2(head_dim)
     int64_t attn_max_positions;
 };
-static_assert(sizeof(LinArgs) == 320 && offsetof(LinArgs, nw2) + 4 == 192 && offsetof(LinArgs, slots_in) == 256,
-              "the load_args fields fill lines 0-2");
-static_assert(sizeof(LinArgs) % 16 == 0, "LinArgs is read as 16-byte vectors");
+
+// The kernel arguments of one linear: four 64-byte lines, each holding what
+// one use reads first, so a workgroup waits on one line before its first
+// vector load (stage 0, stage 1, stage 2) or two (the fused input kinds of
+// stage 1; the fused launch). load_args rebuilds the rest of a Lin: the
+// geometry from in / rank / out, the tiles header from the V tile pointer,
+// the exponent line from the operand pointer. Every scalar-cache line a
+// launch waits on before its first vector load lengthens it: measured on
+// MI355X, twelve scalar loads over five lines instead of six over three put
+// the end-to-end Qwen3-8B decode at 522.9 instead of 537.2 tok/s.
+struct alignas(64) LinArgs {
+    // line 0: stage 1 and stage 0
+    const uint32_t* v_tiles;
+    const void* x;
+    const void* s_in;
+    const void* s_mid;
+    uint8_t* lmq;
+    int32_t in, rank, nwg1;
+    uint32_t kinds1;         // x_dtype | scale_dtype << 8 | nw1 << 16 | tokens << 24
+    int32_t pad0_[2];
+    // line 1: stage 2
+    const uint32_t* u_tiles;
+    uint8_t* lmq2;           // lmq again
+    const void* s_out;
+    const void* bias;
+    void* y;
+    int32_t out, rank2, nwg2, salient_count;
+    uint32_t kinds2;         // tokens | scale_dtype << 8 | bias_dtype << 16 | nw2 << 24
+    uint32_t kinds3;         // y_dtype | salient_dtype << 8 | x_dtype << 16
+    // line 2: the fused input kinds of stage 1
+    const void* x2;
+    const float* col_scale;
+    const float* slots_in;
+    const float* attn_ml;
+    const int32_t* attn_pos;
+    int32_t nslots;
+    float eps;
+    int32_t attn_blocks, attn_hd_log2;
+    int64_t attn_max_positions;
+    // line 3: stage 2's epilogue (residual, salient columns)
+    float* residual;
+    float* slots_out;
+    const int32_t* salient_indices;
+    const void* salient_values;
+    const void* salient_scales;
+    const void* x_s2;        // x again
+    int32_t in2;             // in again
+    int32_t pad1_[3];
+};
+static_assert(sizeof(LinArgs) == 256 && offsetof(LinArgs, u_tiles) == 64 && offsetof(LinArgs, x2) == 128 &&
+                  offsetof(LinArgs, residual) == 192 && offsetof(LinArgs, kinds1) + 4 <= 64 &&
+                  offsetof(LinArgs, kinds3) + 4 == 128 && offsetof(LinArgs, attn_max_positions) + 8 == 192,
+              "one use per 64-byte line");
+
+// Stage-2 operand bytes of a [out, rank] U for `tokens` tokens (1: one block of
+// one token; 2-4: one block of four; 5-16: four blocks of four). A multiple of 256.
+__host__ __device__ inline int64_t lmq_bytes_for(const MatGeo& g2, int64_t tokens) {
+    return g2.nc * (tokens == 1 ? 2048 : (tokens <= 4 ? 8192 : 32768));
+}
+
+// The kernel arguments of a Lin (host side). The narrow fields were range
+// checked by the host (offsets below 2^31, at most 16 tokens and waves).
+inline LinArgs pack_args(const Lin& a) {
+    LinArgs p{};
+    p.v_tiles = a.v_tiles;
+    p.x = a.x;
+    p.s_in = a.s_in;
+    p.s_mid = a.s_mid;
+    p.lmq = a.lmq;
+    p.in = static_cast<int32_t>(a.in);
+    p.rank = static_cast<int32_t>(a.rank);
+    p.nwg1 = static_cast<int32_t>(a.nwg1);
+    p.kinds1 = static_cast<uint32_t>(a.x_dtype) | static_cast<uint32_t>(a.scale_dtype) << 8 |
+               static_cast<uint32_t>(a.nw1) << 16 | static_cast<uint32_t>(a.tokens) << 24;
+    p.u_tiles = a.u_tiles;
+    p.lmq2 = a.lmq;
+    p.s_out = a.s_out;
+    p.bias = a.bias;
+    p.y = a.y;
+    p.out = static_cast<int32_t>(a.out);
+    p.rank2 = p.rank;
+    p.nwg2 = static_cast<int32_t>(a.nwg2);
+    p.salient_count = static_cast<int32_t>(a.salient_count);
+    p.kinds2 = static_cast<uint32_t>(a.tokens) | static_cast<uint32_t>(a.scale_dtype) << 8 |
+               static_cast<uint32_t>(a.bias_dtype) << 16 | static_cast<uint32_t>(a.nw2) << 24;
+    p.kinds3 = static_cast<uint32_t>(a.y_dtype) | static_cast<uint32_t>(a.salient_dtype) << 8 |
+               static_cast<uint32_t>(a.x_dtype) << 16;
+    p.x2 = a.x2;
+    p.col_scale = a.col_scale;
+    p.slots_in = a.slots_in;
+    p.attn_ml = a.attn_ml;
+    p.attn_pos = a.attn_pos;
+    p.nslots = a.nslots;
+    p.eps = a.eps;
+    p.attn_blocks = a.attn_blocks;
+    p.attn_hd_log2 = a.attn_hd_log2;
+    p.attn_max_positions = a.attn_max_positions;
+    p.residual = a.residual;
+    p.slots_out = a.slots_out;
+    p.salient_indices = a.salient_indices;
+    p.salient_values = a.salient_values;
+    p.salient_scales = a.salient_scales;
+    p.x_s2 = a.x;
+    p.in2 = p.in;
+    return p;
+}
 
 // ---------------------------------------------------------------------------
 // XCD-contiguous workgroup order.
@@ -249,129 +343,212 @@ __host__ __device__ inline int xcd_block(int x, int nblocks) {
     return c * q + (c < r ? c : r) + (x >> 3);
 }
 
+// Kernel arguments of a launch: the members' lines first, so member i starts
+// at byte 256 i of the segment.
 struct Batch {
-    int count;
-    int tw1, tw2;            // tiles per workgroup of each stage
-    int pad_;
     LinArgs p[kMaxBatch];
+    int32_t count;           // members (the fused launch)
 };
 
-// A member's arguments, copied field by field from the kernel-argument segment
-// (copy_args), with the fields a kernel needs before its first load then used
-// by one empty asm (pin_args): all those scalar loads are issued together and
-// complete at one point, instead of lazily (one dependent round trip per
-// uniform branch that needs a field). The copies stay typed loads, so the
-// pointers are still known to be global. The fused input kinds add the fields
-// they read first (kArgsNorm: the column scale and the producer's row sums;
-// kArgsGated: the up input; kArgsAttn: the attention partials and position)
-// to the same wait: left to the compiler, those loads were issued only after
-// it, a second scalar round trip before the kernel's first vector load.
-enum : int { kArgsPlain = 0, kArgsNorm = 1, kArgsGated = 2, kArgsAttn = 3 };
+// A launch as the host plans it: its members as Lins and the tiles per
+// workgroup of each stage (the kernels take those as template arguments).
+struct HostBatch {
+    int count;
+    int tw1, tw2;
+    Lin p[kMaxBatch];
+};
 
-__device__ __forceinline__ LinArgs copy_args(const Batch& batch, int member) {
-    const LinArgs& s = batch.p[member];
-    LinArgs a;
-    a.in = s.in;
-    a.rank = s.rank;
-    a.out = s.out;
-    a.g1 = s.g1;
-    a.g2 = s.g2;
-    a.nwg1 = s.nwg1;
-    a.nwg2 = s.nwg2;
-    a.v_tiles = s.v_tiles;
-    a.u_tiles = s.u_tiles;
-    a.header = s.header;
-    a.x = s.x;
-    a.x_dtype = s.x_dtype;
-    a.tokens = s.tokens;
-    a.s_in = s.s_in;
-    a.s_mid = s.s_mid;
-    a.s_out = s.s_out;
-    a.scale_dtype = s.scale_dtype;
-    a.salient_count = s.salient_count;
-    a.salient_indices = s.salient_indices;
-    a.salient_values = s.salient_values;
-    a.salient_dtype = s.salient_dtype;
-    a.salient_scales = s.salient_scales;
-    a.bias = s.bias;
-    a.bias_dtype = s.bias_dtype;
-    a.y = s.y;
-    a.y_dtype = s.y_dtype;
-    a.lmq = s.lmq;
-    a.lme = s.lme;
-    a.nw1 = s.nw1;
-    a.nw2 = s.nw2;
-    a.x2 = s.x2;
-    a.col_scale = s.col_scale;
-    a.slots_in = s.slots_in;
-    a.residual = s.residual;
-    a.slots_out = s.slots_out;
-    a.nslots = s.nslots;
-    a.eps = s.eps;
-    a.attn_ml = s.attn_ml;
-    a.attn_pos = s.attn_pos;
-    a.attn_blocks = s.attn_blocks;
-    a.attn_hd_log2 = s.attn_hd_log2;
-    a.attn_max_positions = s.attn_max_positions;
-    return a;
+inline void pack_batch(const HostBatch& h, Batch& b) {
+    for (int i = 0; i < kMaxBatch; ++i) b.p[i] = i < h.count ? pack_args(h.p[i]) : LinArgs{};
+    b.count = h.count;
 }
 
-// One statement per use, so every field it names is waited for at the same
-// point; it redefines the integer fields, so no arithmetic on them can be
-// hoisted above it (the pointers are only read, so they stay known-global).
-// Each stage pins only what it reads (fewer live scalar registers: the
-// compiler otherwise reloads some fields after the wait), kPinStages both.
+// A member's arguments as a Lin (load_args): the fields of the line a use
+// reads first are copied from the kernel-argument segment and passed through
+// one empty asm (pin_line*), so all their scalar loads are issued together and
+// complete at one point instead of lazily (one dependent round trip per
+// uniform branch that needs a field); the derived fields are computed from
+// them after that point. Fields of the other lines are copied too and load
+// where a kernel first uses them. The copies stay typed loads, so the
+// pointers are still known to be global. The fused input kinds add the
+// fields of line 2 they read first (kArgsNorm: the column scale and the
+// producer's row sums; kArgsGated: the up input; kArgsAttn: the attention
+// partials and position) to the same wait: left to the compiler, those
+// loads were issued only after it, a second round trip before the kernel's
+// first vector load.
+enum : int { kArgsPlain = 0, kArgsNorm = 1, kArgsGated = 2, kArgsAttn = 3 };
 enum : int { kPinStage1 = 1, kPinStage2 = 2, kPinStages = 3 };
-#define NQ_PIN1_OUT(a)                                                                                          \
-    "+s"(a.in), "+s"(a.rank), "+s"(a.g1.nt), "+s"(a.g1.nb), "+s"(a.g1.nc), "+s"(a.g2.nc), "+s"(a.nwg1),         \
-        "+s"(a.nw1), "+s"(a.x_dtype), "+s"(a.tokens), "+s"(a.scale_dtype)
-#define NQ_PIN1_IN(a) "s"(a.v_tiles), "s"(a.header), "s"(a.x), "s"(a.s_in), "s"(a.s_mid), "s"(a.lmq), "s"(a.lme)
-#define NQ_PIN2_OUT(a)                                                                                          \
-    "+s"(a.rank), "+s"(a.out), "+s"(a.g2.nt), "+s"(a.g2.nb), "+s"(a.g2.nc), "+s"(a.nwg2), "+s"(a.nw2),          \
-        "+s"(a.tokens), "+s"(a.scale_dtype), "+s"(a.bias_dtype)
-#define NQ_PIN2_IN(a) "s"(a.u_tiles), "s"(a.s_out), "s"(a.bias), "s"(a.lmq), "s"(a.lme)
-#define NQ_PIN_OUT(a)                                                                                           \
-    "+s"(a.in), "+s"(a.rank), "+s"(a.out), "+s"(a.g1.nt), "+s"(a.g1.nb), "+s"(a.g1.nc), "+s"(a.g2.nt),          \
-        "+s"(a.g2.nb), "+s"(a.g2.nc), "+s"(a.nwg1), "+s"(a.nwg2), "+s"(a.x_dtype), "+s"(a.tokens),               \
-        "+s"(a.scale_dtype), "+s"(a.bias_dtype), "+s"(a.nw1), "+s"(a.nw2)
-#define NQ_PIN_IN(a)                                                                                            \
-    "s"(a.v_tiles), "s"(a.u_tiles), "s"(a.header), "s"(a.x), "s"(a.s_in), "s"(a.s_mid), "s"(a.s_out),          \
-        "s"(a.bias), "s"(a.lmq), "s"(a.lme)
-template <int STAGE, int EXTRA>
-__device__ __forceinline__ void pin_args(LinArgs& a) {
-    if constexpr (STAGE == kPinStage2) {
-        asm volatile("" : NQ_PIN2_OUT(a) : NQ_PIN2_IN(a));
-    } else if constexpr (STAGE == kPinStages) {
-        asm volatile("" : NQ_PIN_OUT(a) : NQ_PIN_IN(a));
-    } else if constexpr (EXTRA == kArgsNorm) {
-        asm volatile("" : NQ_PIN1_OUT(a), "+s"(a.nslots), "+s"(a.eps) : NQ_PIN1_IN(a), "s"(a.col_scale), "s"(a.slots_in));
+
+// Device-side geometry from 32-bit sizes (shifts only).
+__device__ __forceinline__ MatGeo mat_geo32(uint32_t rows, uint32_t cols) {
+    static_assert(kTileRows == 16 && kBlockCols == 128 && kChunkBlocks == 4, "shift forms below");
+    const uint32_t nb = (cols + kBlockCols - 1) >> 7;
+    MatGeo g;
+    g.nt = (rows + kTileRows - 1) >> 4;
+    g.nb = nb;
+    g.nc = (nb + kChunkBlocks - 1) >> 2;
+    return g;
+}
+
+// Line 0 (stage 1) and line 1 (stage 2), as loaded.
+struct Line0 {
+    const uint32_t* v_tiles;
+    const void* x;
+    const void* s_in;
+    const void* s_mid;
+    uint8_t* lmq;
+    uint32_t in, rank, nwg1, kinds1;
+};
+struct Line1 {
+    const uint32_t* u_tiles;
+    uint8_t* lmq;
+    const void* s_out;
+    const void* bias;
+    void* y;
+    uint32_t out, rank, nwg2, salient_count, kinds2, kinds3;
+};
+
+__device__ __forceinline__ Line0 copy_line0(const LinArgs& s) {
+    return Line0{s.v_tiles, s.x, s.s_in, s.s_mid, s.lmq, static_cast<uint32_t>(s.in), static_cast<uint32_t>(s.rank),
+                 static_cast<uint32_t>(s.nwg1), s.kinds1};
+}
+__device__ __forceinline__ Line1 copy_line1(const LinArgs& s) {
+    return Line1{s.u_tiles, s.lmq2, s.s_out, s.bias, s.y, static_cast<uint32_t>(s.out),
+                 static_cast<uint32_t>(s.rank2), static_cast<uint32_t>(s.nwg2),
+                 static_cast<uint32_t>(s.salient_count), s.kinds2, s.kinds3};
+}
+
+#define NQ_PIN0_OUT(l) "+s"(l.in), "+s"(l.rank), "+s"(l.nwg1), "+s"(l.kinds1)
+#define NQ_PIN0_IN(l) "s"(l.v_tiles), "s"(l.x), "s"(l.s_in), "s"(l.s_mid), "s"(l.lmq)
+#define NQ_PIN1_OUT(l) "+s"(l.out), "+s"(l.rank), "+s"(l.nwg2), "+s"(l.salient_count), "+s"(l.kinds2)
+#define NQ_PIN1_IN(l) "s"(l.u_tiles), "s"(l.lmq), "s"(l.s_out), "s"(l.bias)
+
+// Line 0, with the line-2 fields the input kind reads first.
+template <int EXTRA>
+__device__ __forceinline__ void pin_line0(Line0& l, const void*& x2, const float*& col_scale, const float*& slots_in,
+                                          const float*& attn_ml, const int32_t*& attn_pos, int& nslots, float& eps,
+                                          int& attn_blocks, int& attn_hd_log2, int64_t& attn_max_positions) {
+    if constexpr (EXTRA == kArgsNorm) {
+        asm volatile("" : NQ_PIN0_OUT(l), "+s"(nslots), "+s"(eps) : NQ_PIN0_IN(l), "s"(col_scale), "s"(slots_in));
     } else if constexpr (EXTRA == kArgsGated) {
-        asm volatile("" : NQ_PIN1_OUT(a) : NQ_PIN1_IN(a), "s"(a.x2));
+        asm volatile("" : NQ_PIN0_OUT(l) : NQ_PIN0_IN(l), "s"(x2));
     } else if constexpr (EXTRA == kArgsAttn) {
         asm volatile(""
-                     : NQ_PIN1_OUT(a), "+s"(a.attn_blocks), "+s"(a.attn_hd_log2), "+s"(a.attn_max_positions)
-                     : NQ_PIN1_IN(a), "s"(a.attn_ml), "s"(a.attn_pos));
+                     : NQ_PIN0_OUT(l), "+s"(attn_blocks), "+s"(attn_hd_log2), "+s"(attn_max_positions)
+                     : NQ_PIN0_IN(l), "s"(attn_ml), "s"(attn_pos));
     } else {
-        asm volatile("" : NQ_PIN1_OUT(a) : NQ_PIN1_IN(a));
+        asm volatile("" : NQ_PIN0_OUT(l) : NQ_PIN0_IN(l));
     }
 }
-
-// Both members of a paired stage 2 in one statement: one wait for both.
-__device__ __forceinline__ void pin_args2(LinArgs& a, LinArgs& b) {
-    asm volatile("" : NQ_PIN2_OUT(a), NQ_PIN2_OUT(b) : NQ_PIN2_IN(a), NQ_PIN2_IN(b));
+__device__ __forceinline__ void pin_line1(Line1& l) { asm volatile("" : NQ_PIN1_OUT(l) : NQ_PIN1_IN(l)); }
+// Both lines (the fused launch), or line 1 of two members (the paired stage 2):
+// one wait.
+__device__ __forceinline__ void pin_lines(Line0& l0, Line1& l1) {
+    asm volatile("" : NQ_PIN0_OUT(l0), NQ_PIN1_OUT(l1) : NQ_PIN0_IN(l0), NQ_PIN1_IN(l1));
 }
+__device__ __forceinline__ void pin_line1_pair(Line1& a, Line1& b) {
+    asm volatile("" : NQ_PIN1_OUT(a), NQ_PIN1_OUT(b) : NQ_PIN1_IN(a), NQ_PIN1_IN(b));
+}
+#undef NQ_PIN0_OUT
+#undef NQ_PIN0_IN
 #undef NQ_PIN1_OUT
 #undef NQ_PIN1_IN
-#undef NQ_PIN2_OUT
-#undef NQ_PIN2_IN
-#undef NQ_PIN_OUT
-#undef NQ_PIN_IN
+
+// The Lin of member s, from its (pinned) line 0 and line 1 and the lazily
+// loaded lines 2 and 3. FROM1: the fields both lines hold (rank, tokens, the
+// scale dtype, the operand pointer) are taken from line 1 (stage 2), else
+// from line 0.
+template <bool FROM1>
+__device__ __forceinline__ Lin build_lin(const LinArgs& s, const Line0& l0, const Line1& l1, const void* x2,
+                                         const float* col_scale, const float* slots_in, const float* attn_ml,
+                                         const int32_t* attn_pos, int nslots, float eps, int attn_blocks,
+                                         int attn_hd_log2, int64_t attn_max_positions) {
+    Lin a;
+    const uint32_t rank = FROM1 ? l1.rank : l0.rank;
+    const uint32_t in = FROM1 ? static_cast<uint32_t>(s.in2) : l0.in;
+    const int tokens = FROM1 ? static_cast<int>(l1.kinds2 & 0xff) : static_cast<int>(l0.kinds1 >> 24);
+    a.in = in;
+    a.rank = rank;
+    a.out = l1.out;
+    a.g1 = mat_geo32(rank, in);
+    a.g2 = mat_geo32(l1.out, rank);
+    a.nwg1 = l0.nwg1;
+    a.nwg2 = l1.nwg2;
+    a.v_tiles = l0.v_tiles;
+    a.u_tiles = l1.u_tiles;
+    a.header = const_cast<uint32_t*>(l0.v_tiles) - kHeaderWords;
+    a.x = FROM1 ? s.x_s2 : l0.x;
+    a.x_dtype = FROM1 ? static_cast<int>((l1.kinds3 >> 16) & 0xff) : static_cast<int>(l0.kinds1 & 0xff);
+    a.tokens = tokens;
+    a.s_in = l0.s_in;
+    a.s_mid = l0.s_mid;
+    a.s_out = l1.s_out;
+    a.scale_dtype = FROM1 ? static_cast<int>((l1.kinds2 >> 8) & 0xff) : static_cast<int>((l0.kinds1 >> 8) & 0xff);
+    a.salient_count = l1.salient_count;
+    a.salient_indices = s.salient_indices;
+    a.salient_values = s.salient_values;
+    a.salient_dtype = static_cast<int>((l1.kinds3 >> 8) & 0xff);
+    a.salient_scales = s.salient_scales;
+    a.bias = l1.bias;
+    a.bias_dtype = static_cast<int>((l1.kinds2 >> 16) & 0xff);
+    a.y = l1.y;
+    a.y_dtype = static_cast<int>(l1.kinds3 & 0xff);
+    a.lmq = FROM1 ? l1.lmq : l0.lmq;
+    a.lme = reinterpret_cast<int*>(a.lmq + lmq_bytes_for(a.g2, tokens));
+    a.nw1 = static_cast<int>((l0.kinds1 >> 16) & 0xff);
+    a.nw2 = static_cast<int>(l1.kinds2 >> 24);
+    a.x2 = x2;
+    a.col_scale = col_scale;
+    a.slots_in = slots_in;
+    a.residual = s.residual;
+    a.slots_out = s.slots_out;
+    a.nslots = nslots;
+    a.eps = eps;
+    a.attn_ml = attn_ml;
+    a.attn_pos = attn_pos;
+    a.attn_blocks = attn_blocks;
+    a.attn_hd_log2 = attn_hd_log2;
+    a.attn_max_positions = attn_max_positions;
+    return a;
+}
 
 template <int STAGE, int EXTRA = kArgsPlain>
-__device__ __forceinline__ LinArgs load_args(const Batch& batch, int member) {
-    LinArgs a = copy_args(batch, member);
-    pin_args<STAGE, EXTRA>(a);
-    return a;
+__device__ __forceinline__ Lin load_args(const Batch& batch, int member) {
+    const LinArgs& s = batch.p[member];
+    Line0 l0 = copy_line0(s);
+    Line1 l1 = copy_line1(s);
+    const void* x2 = s.x2;
+    const float* col_scale = s.col_scale;
+    const float* slots_in = s.slots_in;
+    const float* attn_ml = s.attn_ml;
+    const int32_t* attn_pos = s.attn_pos;
+    int nslots = s.nslots;
+    float eps = s.eps;
+    int attn_blocks = s.attn_blocks, attn_hd_log2 = s.attn_hd_log2;
+    int64_t attn_max_positions = s.attn_max_positions;
+    if constexpr (STAGE == kPinStage2) {
+        pin_line1(l1);
+    } else if constexpr (STAGE == kPinStages) {
+        pin_lines(l0, l1);
+    } else {
+        pin_line0<EXTRA>(l0, x2, col_scale, slots_in, attn_ml, attn_pos, nslots, eps, attn_blocks, attn_hd_log2,
+                         attn_max_positions);
+    }
+    return build_lin<STAGE == kPinStage2>(s, l0, l1, x2, col_scale, slots_in, attn_ml, attn_pos, nslots, eps,
+                                          attn_blocks, attn_hd_log2, attn_max_positions);
+}
+
+// Stage 2 of members 0 and 1 (the paired stage 2): one wait for both lines.
+__device__ __forceinline__ void load_args_pair(const Batch& batch, Lin& a, Lin& b) {
+    const LinArgs& s = batch.p[0];
+    const LinArgs& t = batch.p[1];
+    Line0 s0 = copy_line0(s), t0 = copy_line0(t);
+    Line1 s1 = copy_line1(s), t1 = copy_line1(t);
+    pin_line1_pair(s1, t1);
+    a = build_lin<true>(s, s0, s1, s.x2, s.col_scale, s.slots_in, s.attn_ml, s.attn_pos, s.nslots, s.eps,
+                        s.attn_blocks, s.attn_hd_log2, s.attn_max_positions);
+    b = build_lin<true>(t, t0, t1, t.x2, t.col_scale, t.slots_in, t.attn_ml, t.attn_pos, t.nslots, t.eps,
+                        t.attn_blocks, t.attn_hd_log2, t.attn_max_positions);
 }
 // Activation kinds (template parameter AK): how stage 1 reads a[t, k].
 enum : int {
@@ -696,7 +873,7 @@ __device__ __forceinline__ void load_runs(Run<AK> (&r)[2], const void* __restric
 }
 
 template <int AK, int TOK, int TW>
-__device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const LinArgs& a, int c, int lane) {
+__device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const Lin& a, int c, int lane) {
     constexpr int DT = act_dtype<AK>();
     const int k0 = stage_col0(c, lane);
     const int in = static_cast<int>(a.in);
@@ -767,7 +944,7 @@ constexpr int kS2SpreadBytes = 8 * 4 * 4 * 16;
 
 // (One token; several tokens load each MFMA's operand directly, in stage2_wg.)
 template <int TPB, int TB, int TW>
-__device__ __forceinline__ void load_s2_ops(S2Regs<TB, TW>& r, const LinArgs& a, int c, int lane) {
+__device__ __forceinline__ void load_s2_ops(S2Regs<TB, TW>& r, const Lin& a, int c, int lane) {
     static_assert(TPB == 1 && TB == 1, "one token per launch");
     const uint8_t* src = a.lmq + lmq_offset<1, TB>(c, 0, 0, 0, 0);
     r.a[0][0] = *reinterpret_cast<const v4i*>(src + 16 * lane);
@@ -859,7 +1036,7 @@ __device__ __forceinline__ void gate_values(const S1Regs<AK, TOK, TW>& r, int t,
 // over sum_s l_s e^(m_s - M). Blocks past the position are selected out (their
 // slots may hold anything); a position outside the cache gives zeros.
 template <int AK, int TOK, int TW>
-__device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, float (&mv)[2][4]) {
+__device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const Lin& a, float (&mv)[2][4]) {
     constexpr int NB = attn_parts<AK>();
     const int64_t pos = r.at.pos;
     const bool in_range = pos >= 0 && pos < a.attn_max_positions;  // uniform
@@ -889,7 +1066,7 @@ __device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const L
 // One run's values of token t: the activations as read (with the gated kind's
 // product), or the attention kinds' merged values.
 template <int AK, int TOK, int TW>
-__device__ __forceinline__ void act_run(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int t, int run,
+__device__ __forceinline__ void act_run(const S1Regs<AK, TOK, TW>& r, const Lin& a, int t, int run,
                                         const float (&mv)[2][4], float (&v)[4]) {
     if constexpr (attn_kind<AK>()) {
 #pragma unroll
@@ -922,7 +1099,7 @@ constexpr int kPoisonExp = 0x7fffffff;
 // four digits: one add and one xor per value, then a byte transpose of four
 // values. Every value keeps 24 bits relative to the chunk's largest.
 template <int AK, int TOK, int TW, int TPB>
-__device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const LinArgs& a, int c, int t_base,
+__device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const Lin& a, int c, int t_base,
                                             char* __restrict__ ops, int lane, int (&expo)[TPB], float (&csum)[TPB]) {
     const int m = lane >> 3, d = (lane >> 1) & 3, h = lane & 1;
     const int k0 = stage_col0(c, lane);
@@ -1089,7 +1266,7 @@ __device__ __forceinline__ uint64_t slot_count(int slot, int slots, int64_t coun
 
 // Fused launch, stage 1: thread 0 signals each of the workgroup's tiles once
 // the workgroup's operand stores are complete (the caller waits and barriers first).
-__device__ __forceinline__ void signal_ready(const LinArgs& a, int64_t t0, int tw) {
+__device__ __forceinline__ void signal_ready(const Lin& a, int64_t t0, int tw) {
     if (threadIdx.x != 0) return;
     const int64_t n1 = a.g1.nt;
     for (int tt = 0; tt < tw; ++tt) {
@@ -1115,7 +1292,7 @@ __device__ __forceinline__ void signal_ready(const LinArgs& a, int64_t t0, int t
 // when the bounded wait gave up: the stage-1 operands may then be stale, so
 // the caller stores NaN for the workgroup's outputs, and the sticky error
 // flag in the header records the event for the host.
-__device__ __forceinline__ bool wait_ready(const LinArgs& a, int64_t t0, int tw, int64_t wg, bool dead) {
+__device__ __forceinline__ bool wait_ready(const Lin& a, int64_t t0, int tw, int64_t wg, bool dead) {
     __shared__ int gave_up;
     if (threadIdx.x == 0) gave_up = 0;
     if (threadIdx.x == 0 && !dead) {
@@ -1211,7 +1388,7 @@ __device__ __forceinline__ void store_lmq(uint8_t* lmq, int r, int t, float v, i
 // One stage-1 workgroup: tiles [t0, t0 + TW) of linear `a`. TPB tokens per
 // block and TB blocks cover the launch's tokens; KC chunks per wave per pass.
 template <int AK, int TPB, int TB, int TW, int KC, bool FUSED>
-__device__ __forceinline__ void stage1_wg(const LinArgs& a, int wg_in, char* __restrict__ lds) {
+__device__ __forceinline__ void stage1_wg(const Lin& a, int wg_in, char* __restrict__ lds) {
     constexpr int TOK = TPB * TB;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -1389,9 +1566,9 @@ __device__ __forceinline__ int act_elem_bytes(int x_dtype) {
 
 // Stage 0 of (chunk c, token block tb) in a layout of tbl blocks: one wave.
 template <int AK>
-__device__ __forceinline__ void stage0_wave(const LinArgs& a, int c, int tb, int tbl, int lane) {
+__device__ __forceinline__ void stage0_wave(const Lin& a, int c, int tb, int tbl, int lane) {
     constexpr int TPB = 4;
-    LinArgs b = a;
+    Lin b = a;
     b.x = static_cast<const char*>(a.x) +
           static_cast<int64_t>(tb) * TPB * a.in * act_elem_bytes<AK>(a.x_dtype);
     b.tokens = a.tokens - TPB * tb < TPB ? a.tokens - TPB * tb : TPB;
@@ -1427,7 +1604,7 @@ constexpr int wave_groups() { return TB / blocks_per_wave<TB>(); }
 // One stage-1 workgroup of the several-token path: tiles [t0, t0 + TW) of
 // linear `a`, operands from xq; TB blocks of four tokens in the layout.
 template <int TB, int TW, int KC>
-__device__ __forceinline__ void stage1m_wg(const LinArgs& a, int wg_in, char* __restrict__ lds) {
+__device__ __forceinline__ void stage1m_wg(const Lin& a, int wg_in, char* __restrict__ lds) {
     constexpr int TPB = 4;
     constexpr int TBW = blocks_per_wave<TB>(), NG = wave_groups<TB>();
     const int lane = threadIdx.x & 63;
@@ -1577,8 +1754,8 @@ __device__ __forceinline__ float bits_value(uint32_t b, int dtype) {
 // one token, and the output silu(y_a) * y_b stored to a.y (the decoder's
 // SiLU-gated MLP product), so the down projection reads one plain input.
 template <int TPB, int TB, int TW, int KC, bool FUSED, bool PAIR = false>
-__device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __restrict__ lds,
-                                          const LinArgs* pair = nullptr) {
+__device__ __forceinline__ void stage2_wg(const Lin& a, int wg_in, char* __restrict__ lds,
+                                          const Lin* pair = nullptr) {
     // Split launch with four token blocks: two waves per chunk slot
     // (blocks_per_wave); one token or the fused launch: one wave per slot.
     constexpr int NG = (TPB == 4 && !FUSED) ? wave_groups<TB>() : 1;
@@ -1636,7 +1813,7 @@ __device__ __forceinline__ void stage2_wg(const LinArgs& a, int wg_in, char* __r
         S2Regs<TBW, TW> r[KC];
         int e[TBW];
     };
-    const auto load_pass = [&](const LinArgs& m, PassRegs& ps, const int base, const bool first)
+    const auto load_pass = [&](const Lin& m, PassRegs& ps, const int base, const bool first)
                                __attribute__((always_inline)) {
         ps.pc = pass_chunks<KC>(base, slot, nslots, nc);
 #pragma unroll
@@ -1856,7 +2033,7 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage1(const Batch batch) {
                            : AK == kActGatedF32 ? kArgsGated
                            : attn_kind<AK>()    ? kArgsAttn
                                                 : kArgsPlain;
-    const LinArgs a = load_args<kPinStage1, kExtra>(batch, blockIdx.y);
+    const Lin a = load_args<kPinStage1, kExtra>(batch, blockIdx.y);
     const int nwg = static_cast<int>(a.nwg1);
     if (static_cast<int>(blockIdx.x) >= nwg) return;  // grid padding: the arguments are already loaded
     stage1_wg<AK, TPB, TB, TW, KC, false>(a, xcd_block(blockIdx.x, nwg), lds);
@@ -1866,7 +2043,7 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage1(const Batch batch) {
 // members), four waves per workgroup, one (chunk, token block) per wave.
 template <int AK>
 __global__ __launch_bounds__(256) void k_decode_stage0(const Batch batch) {
-    const LinArgs a = load_args<kPinStage1>(batch, blockIdx.y);
+    const Lin a = load_args<kPinStage1>(batch, blockIdx.y);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
     const int nblk = (a.tokens + 3) >> 2;
@@ -1880,7 +2057,7 @@ __global__ __launch_bounds__(256) void k_decode_stage0(const Batch batch) {
 template <int TB, int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage1m(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const LinArgs a = load_args<kPinStage1>(batch, blockIdx.y);
+    const Lin a = load_args<kPinStage1>(batch, blockIdx.y);
     const int nwg = static_cast<int>(a.nwg1);
     if (static_cast<int>(blockIdx.x) >= nwg) return;
     stage1m_wg<TB, TW, KC>(a, xcd_block(blockIdx.x, nwg), lds);
@@ -1889,7 +2066,7 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage1m(const Batch batch) {
 template <int TPB, int TB, int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage2(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const LinArgs a = load_args<kPinStage2>(batch, blockIdx.y);
+    const Lin a = load_args<kPinStage2>(batch, blockIdx.y);
     const int nwg = static_cast<int>(a.nwg2);
     if (static_cast<int>(blockIdx.x) >= nwg) return;  // grid padding: the arguments are already loaded
     stage2_wg<TPB, TB, TW, KC, false>(a, xcd_block(blockIdx.x, nwg), lds);
@@ -1899,9 +2076,8 @@ __global__ __launch_bounds__(THREADS) void k_decode_stage2(const Batch batch) {
 template <int TW, int KC, int THREADS>
 __global__ __launch_bounds__(THREADS) void k_decode_stage2_pair(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    LinArgs a = copy_args(batch, 0);
-    LinArgs b = copy_args(batch, 1);
-    pin_args2(a, b);
+    Lin a, b;
+    load_args_pair(batch, a, b);
     const int nwg = static_cast<int>(a.nwg2);
     if (static_cast<int>(blockIdx.x) >= nwg) return;
     stage2_wg<1, 1, TW, KC, false, true>(a, xcd_block(blockIdx.x, nwg), lds, &b);
@@ -1914,7 +2090,7 @@ __global__ __launch_bounds__(THREADS) void k_decode_fused(const Batch batch) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int y = static_cast<int>(blockIdx.y);
     const int count = batch.count;
-    const LinArgs a = load_args<kPinStages>(batch, y < count ? y : y - count);
+    const Lin a = load_args<kPinStages>(batch, y < count ? y : y - count);
     if (y < count) {
         if (blockIdx.x >= a.nwg1) return;
         stage1_wg<kActGeneric, TPB, TB, 1, KC1, true>(a, blockIdx.x, lds);
