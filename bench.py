@@ -634,7 +634,7 @@ def config5(args, device, packed_us_per_layer: float | None) -> dict:
         prefill_ms.append(timing["prefill_ms"])
     d, pf = pct(decode_ms), pct(prefill_ms)
     per_layer = (9 if decoder.fold_attention_merge else 10) if decoder.fuse_decode else 12
-    kernels = args.layers * per_layer + (5 if decoder.fuse_decode else 4)
+    kernels = args.layers * per_layer + 4  # embedding, final norm, lm_head, greedy select
     res = {
         "workload": (f"qwen3-8b-shape random-init packed model, {args.layers} layers, vocab {config.vocab}, "
                      f"prompt {args.e2e_prompt} ids, {args.e2e_tokens} greedy tokens, batch 1, "

@@ -35,6 +35,18 @@ extern "C" {
 int nq_embedding(const int64_t* ids, int64_t tokens, const void* table, int32_t table_dtype,
                  int64_t vocab, int64_t hidden, const float* scale, float* out, void* stream);
 
+/* nq_embedding that also writes, for each output row, the sums of squares of
+ * its 16-column groups: slots [tokens][hidden / 16] fp32, hidden % 16 == 0.
+ * These are the row statistics the NQ_INPUT_RMSNORM input of
+ * nq_linear_batch_fused reads (norm_slots), so the first layer's projections
+ * take the embedding's output with the RMSNorm folded in, as later layers take
+ * the residual. No reference counterpart: the reference's embedding
+ * (src/nanoquant/runtime/cuda_kernels.py:620-681) is followed by a separate
+ * RMSNorm. */
+int nq_embedding_slots(const int64_t* ids, int64_t tokens, const void* table, int32_t table_dtype,
+                       int64_t vocab, int64_t hidden, const float* scale, float* out, float* slots,
+                       void* stream);
+
 /* Residual add and RMSNorm, one row per token:
  *   residual[t, :] += delta[t, :]                      (skipped when delta is NULL)
  *   out[t, :] = weight * (residual[t, :] * rsqrt(mean(residual[t, :]^2) + eps))

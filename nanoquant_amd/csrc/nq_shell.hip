@@ -125,7 +125,8 @@ __device__ __forceinline__ void store8(void* __restrict__ p, int dtype, int64_t 
 
 __global__ __launch_bounds__(kRowThreads) void k_embedding(const int64_t* __restrict__ ids, const void* __restrict__ table,
                                                            int dtype, int64_t vocab, int64_t hidden,
-                                                           const float* __restrict__ scale, float* __restrict__ out) {
+                                                           const float* __restrict__ scale, float* __restrict__ out,
+                                                           float* __restrict__ slots) {
     const int64_t t = blockIdx.x;
     const int64_t id = ids[t];
     const bool ok = id >= 0 && id < vocab;
@@ -141,6 +142,13 @@ __global__ __launch_bounds__(kRowThreads) void k_embedding(const int64_t* __rest
             for (int j = 0; j < 8; ++j) v[j] = __builtin_nanf("");
         }
         store8(out, NQ_DTYPE_F32, t * hidden + i, v);
+        if (slots) {  // uniform. hidden % 16 == 0: threads 2k and 2k + 1 hold the 16 columns of one slot
+            float sq = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sq = fmaf(v[j], v[j], sq);
+            const float pair = sq + __shfl_xor(sq, 1, kWave);
+            if ((threadIdx.x & 1) == 0) slots[t * (hidden / 16) + i / 16] = pair;
+        }
     }
 }
 
@@ -1344,9 +1352,24 @@ __global__ __launch_bounds__(1024) void k_greedy_select(const uint64_t* __restri
                                                         int64_t* __restrict__ token_out, int64_t* __restrict__ history,
                                                         int64_t history_capacity, int32_t* __restrict__ step,
                                                         int32_t* __restrict__ position) {
-    __shared__ uint64_t red[1024 / kWave];
+    constexpr int kThreads = 1024;  // the launch's block size
+    constexpr int kRound = 16;      // loads in flight per thread
+    __shared__ uint64_t red[kThreads / kWave];
+    // Rounds of kRound independent loads per thread (indices clamped to the
+    // last partial, whose repeats do not change the maximum), so a round
+    // costs one memory round trip: 9496 partials for a 151936-row vocabulary
+    // are one round instead of ten dependent loads.
     uint64_t key = 0;
-    for (int64_t i = threadIdx.x; i < count; i += blockDim.x) key = partial[i] > key ? partial[i] : key;
+    for (int64_t base = threadIdx.x; base < count; base += static_cast<int64_t>(kThreads) * kRound) {
+        uint64_t v[kRound];
+#pragma unroll
+        for (int j = 0; j < kRound; ++j) {
+            const int64_t i = base + static_cast<int64_t>(j) * kThreads;
+            v[j] = partial[i < count ? i : count - 1];
+        }
+#pragma unroll
+        for (int j = 0; j < kRound; ++j) key = v[j] > key ? v[j] : key;
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const uint32_t lo = __shfl_xor(static_cast<uint32_t>(key), o, kWave);
@@ -1358,7 +1381,7 @@ __global__ __launch_bounds__(1024) void k_greedy_select(const uint64_t* __restri
     __syncthreads();
     if (threadIdx.x == 0) {
         uint64_t b = red[0];
-        for (int i = 1; i < static_cast<int>(blockDim.x / kWave); ++i) b = red[i] > b ? red[i] : b;
+        for (int i = 1; i < kThreads / kWave; ++i) b = red[i] > b ? red[i] : b;
         const int64_t token = static_cast<int64_t>(0xffffffffu - static_cast<uint32_t>(b & 0xffffffffu));
         token_out[0] = token;
         if (history && step) {
@@ -1505,7 +1528,19 @@ extern "C" int nq_embedding(const int64_t* ids, int64_t tokens, const void* tabl
     if (tokens <= 0 || tokens > 0x7fffffff || vocab <= 0 || hidden <= 0 || hidden % 8) return NQ_ERR_SHAPE;
     if (!aligned16(table) || !aligned16(out)) return NQ_ERR_ALIGNMENT;
     hipLaunchKernelGGL(k_embedding, dim3(static_cast<unsigned>(tokens)), dim3(kRowThreads), 0, as_stream(stream), ids,
-                       table, table_dtype, vocab, hidden, scale, out);
+                       table, table_dtype, vocab, hidden, scale, out, nullptr);
+    return nq::launch_status();
+}
+
+extern "C" int nq_embedding_slots(const int64_t* ids, int64_t tokens, const void* table, int32_t table_dtype,
+                                  int64_t vocab, int64_t hidden, const float* scale, float* out, float* slots,
+                                  void* stream) {
+    if (!ids || !table || !out || !slots) return NQ_ERR_ARGUMENT;
+    if (!float_code(table_dtype)) return NQ_ERR_DTYPE;
+    if (tokens <= 0 || tokens > 0x7fffffff || vocab <= 0 || hidden <= 0 || hidden % 16) return NQ_ERR_SHAPE;
+    if (!aligned16(table) || !aligned16(out)) return NQ_ERR_ALIGNMENT;
+    hipLaunchKernelGGL(k_embedding, dim3(static_cast<unsigned>(tokens)), dim3(kRowThreads), 0, as_stream(stream), ids,
+                       table, table_dtype, vocab, hidden, scale, out, slots);
     return nq::launch_status();
 }
 

@@ -61,6 +61,7 @@ EXPORTED_SYMBOLS = (
     "nq_decode_product_codebook_words",
     "nq_transpose_signs",
     "nq_embedding",
+    "nq_embedding_slots",
     "nq_add_rmsnorm",
     "nq_qk_norm_rope_cache",
     "nq_attention_workspace_bytes",
@@ -201,6 +202,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "nq_decode_product_codebook_words": (c_int, [vp, c_i64, vp, c_i64, vp, vp, c_i64, c_i64, vp, vp]),
         "nq_transpose_signs": (c_int, [vp, c_i64, c_i64, vp, vp]),
         "nq_embedding": (c_int, [vp, c_i64, vp, i32, c_i64, c_i64, vp, vp, vp]),
+        "nq_embedding_slots": (c_int, [vp, c_i64, vp, i32, c_i64, c_i64, vp, vp, vp, vp]),
         "nq_add_rmsnorm": (c_int, [vp, vp, i32, vp, i32, f32, c_i64, c_i64, vp, i32, vp]),
         "nq_qk_norm_rope_cache": (
             c_int,

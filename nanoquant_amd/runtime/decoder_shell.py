@@ -19,6 +19,9 @@ shell built from this library's kernels instead:
   the packed calls (``linear_batch_fused``): 10 launches per layer (12 without
   the fused calls), 9 when the attention's merge also folds into the O
   projection's input (by default for caches of up to FOLD_MAX_BLOCKS blocks);
+  the embedding writes the row statistics the first layer's folded norm reads,
+  so a step is the layers, the embedding, the final norm, the output
+  projection and the greedy selection;
 * the KV cache is one device tensor per layer ``[kv_heads, max_positions,
   head_dim]``, and the token position lives in device memory, so one HIP graph
   of the whole one-token step replays for every position with no host
@@ -346,12 +349,14 @@ class PackedDecoder:
 
         c, t = self.config, b.tokens
         fused = t == 1 and self.fuse_decode
-        ops.launch_embedding(ids, self.embed, out=b.residual)
+        # The fused step's first layer reads the embedding's row sums of squares
+        # as later layers read the down projection's.
+        ops.launch_embedding(ids, self.embed, out=b.residual, slots=b.down_slots.view(1, -1) if fused else None)
         for i, prepared in enumerate(self.layers):
             in_norm, post_norm, qn, kn = self.norms[i]
             qkv = [prepared["q_proj"], prepared["k_proj"], prepared["v_proj"]]
-            if fused and i > 0:
-                # residual already holds the previous down-projection (its epilogue)
+            if fused:
+                # residual holds the embedding or the previous down projection (its epilogue)
                 self.backend.linear_batch_fused([b.residual[0]] * 3, qkv, input_kind="rmsnorm", eps=c.eps,
                                                 col_scales=list(self.col_scales[i][:3]), norm_slots=b.down_slots,
                                                 outs=[b.q[0], b.k[0], b.v[0]])

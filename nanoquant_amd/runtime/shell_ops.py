@@ -50,10 +50,14 @@ def _ptr(t: torch.Tensor | None) -> int | None:
 
 
 def launch_embedding(
-    ids: torch.Tensor, table: torch.Tensor, *, scale: torch.Tensor | None = None, out: torch.Tensor | None = None
+    ids: torch.Tensor, table: torch.Tensor, *, scale: torch.Tensor | None = None, out: torch.Tensor | None = None,
+    slots: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """fp32 rows ``table[ids]`` (``* scale``). Mirrors ``launch_bfloat16_embedding``
-    (src/nanoquant/runtime/cuda_kernels.py:644-681) for any float table."""
+    (src/nanoquant/runtime/cuda_kernels.py:644-681) for any float table. With
+    ``slots`` (fp32 ``[*ids, hidden / 16]``) it also writes each row's sums of
+    squares per 16 columns, the statistics a ``rmsnorm`` input kind of
+    ``linear_batch_fused`` reads."""
 
     if ids.dtype != torch.int64 or table.ndim != 2:
         raise ValueError("embedding requires int64 ids and a 2-D table")
@@ -66,11 +70,22 @@ def launch_embedding(
         out = torch.empty((*ids.shape, hidden), dtype=torch.float32, device=ids.device)
     elif out.dtype != torch.float32 or tuple(out.shape) != (*ids.shape, hidden):
         raise ValueError("embedding output must be fp32 [*ids, hidden]")
-    status = _native.load().nq_embedding(
+    if slots is None:
+        status = _native.load().nq_embedding(
+            ids.data_ptr(), ids.numel(), table.data_ptr(), _native.dtype_code(table.dtype), vocab, hidden,
+            _ptr(scale), out.data_ptr(), _stream(ids.device),
+        )
+        _native.check("nq_embedding", status)
+        return out
+    _check_device("embedding", ids.device, slots)
+    if hidden % 16 or slots.dtype != torch.float32 or tuple(slots.shape) != (*ids.shape, hidden // 16) \
+            or not slots.is_contiguous():
+        raise ValueError("embedding slots must be contiguous fp32 [*ids, hidden / 16] (hidden % 16 == 0)")
+    status = _native.load().nq_embedding_slots(
         ids.data_ptr(), ids.numel(), table.data_ptr(), _native.dtype_code(table.dtype), vocab, hidden,
-        _ptr(scale), out.data_ptr(), _stream(ids.device),
+        _ptr(scale), out.data_ptr(), slots.data_ptr(), _stream(ids.device),
     )
-    _native.check("nq_embedding", status)
+    _native.check("nq_embedding_slots", status)
     return out
 
 

@@ -53,6 +53,24 @@ def test_embedding_gathers_rows_exactly():
     assert torch.isnan(bad).all()
 
 
+@pytest.mark.parametrize("hidden", [4096, 1152])
+def test_embedding_slots_are_row_sums_of_squares(hidden):
+    """nq_embedding_slots: the same rows, plus each row's sums of squares per 16
+    columns (the statistics the folded RMSNorm input reads); an invalid id's
+    row and slots are NaN."""
+    table = (0.5 * torch.randn(1000, hidden, generator=_g(11))).to(torch.bfloat16)
+    ids = torch.tensor([3, 999, 3, 1000, 0])
+    slots = torch.full((5, hidden // 16), -1.0, device=DEV)
+    out = ops.launch_embedding(ids.to(DEV), table.to(DEV), slots=slots)
+    rows = table[ids.clamp(max=999)].double()
+    assert torch.equal(out.cpu()[[0, 1, 2, 4]], rows[[0, 1, 2, 4]].float())
+    expected = (rows * rows).view(5, hidden // 16, 16).sum(-1)
+    got = slots.cpu().double()
+    assert torch.allclose(got[[0, 1, 2, 4]], expected[[0, 1, 2, 4]], rtol=4e-6, atol=0)
+    assert torch.equal(got[0], got[2])  # same id, same order of additions
+    assert torch.isnan(out[3]).all() and torch.isnan(slots[3]).all()
+
+
 @pytest.mark.parametrize("rows,hidden,out_dtype", [(1, 4096, torch.bfloat16), (37, 1152, torch.float32)])
 def test_add_rmsnorm(rows, hidden, out_dtype):
     g = _g(2)
@@ -293,7 +311,8 @@ def test_silu_mul():
 
 
 @pytest.mark.parametrize("vocab,hidden,x_dtype", [(151936, 4096, torch.float32), (1000, 1152, torch.bfloat16),
-                                                 (77, 64, torch.float32), (5000, 8192, torch.float32)])
+                                                 (77, 64, torch.float32), (5000, 8192, torch.float32),
+                                                 (2_200_000, 64, torch.float32)])  # 17188 partials: two rounds
 def test_output_projection_and_greedy(vocab, hidden, x_dtype):
     g = _g(6)
     weight = (0.02 * torch.randn(vocab, hidden, generator=g)).to(torch.bfloat16).to(DEV)
