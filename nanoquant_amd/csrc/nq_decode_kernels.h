@@ -1113,62 +1113,76 @@ __device__ __forceinline__ void stage_block(const S1Regs<AK, TOK, TW>& r, const 
     run_values<AK, col_scale_dtype<AK>()>(r.s[1], a.scale_dtype, sc[1]);
     float mv[2][4];  // attention kinds: the merged values (one token)
     if constexpr (attn_kind<AK>()) attn_merge<AK, TOK, TW>(r, a, mv);
+    // A block whose token slots are all in the call stages them in one
+    // straight-line loop; one with slots past the call's tokens (uniform)
+    // stages only those in it: the other slots' digit rows keep what the
+    // operand area held, and every result of those rows is discarded (the
+    // epilogues store tokens < a.tokens only).
+    const auto stage_tokens = [&](auto skip) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < TPB; ++u) {
-        const int t = t_base + u;
-        float v[2][4];
-        float mx = 0.0f, sa = 0.0f;
-        if (full_chunk && t < a.tokens) {  // uniform: every value is inside
+        for (int u = 0; u < TPB; ++u) {
+            const int t = t_base + u;
+            if (decltype(skip)::value && t >= a.tokens) {
+                expo[u] = 0;
+                csum[u] = 0.0f;
+                continue;
+            }
+            float v[2][4];
+            float mx = 0.0f, sa = 0.0f;
+            if (full_chunk) {  // uniform: every value is inside
 #pragma unroll
-            for (int run = 0; run < 2; ++run) {
-                act_run<AK, TOK, TW>(r, a, t, run, mv, v[run]);
+                for (int run = 0; run < 2; ++run) {
+                    act_run<AK, TOK, TW>(r, a, t, run, mv, v[run]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[run][i] *= sc[run][i];
-                    mx = fmaxf(mx, fabsf(v[run][i]));
-                    sa += fabsf(v[run][i]);
+                    for (int i = 0; i < 4; ++i) {
+                        v[run][i] *= sc[run][i];
+                        mx = fmaxf(mx, fabsf(v[run][i]));
+                        sa += fabsf(v[run][i]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int run = 0; run < 2; ++run) {
+                    act_run<AK, TOK, TW>(r, a, t, run, mv, v[run]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const bool ok = 4 * run + i < lim;
+                        v[run][i] = ok ? v[run][i] * sc[run][i] : 0.0f;
+                        mx = fmaxf(mx, fabsf(v[run][i]));
+                        sa += fabsf(v[run][i]);
+                    }
                 }
             }
-        } else {
+            // fmaxf drops NaN, the sum does not: a NaN or an infinity makes the
+            // chunk sum, and so the token's bound in the epilogue, not finite.
+            const float wmx = wave_max(mx);
+            csum[u] = wave_sum(sa);
+            const int e = range_exponent(wmx, 22);
+            const float sm = m < 7 ? exp2i(e + 7 - m) : -exp2i(e);
+            uint32_t dig[4][2];
 #pragma unroll
             for (int run = 0; run < 2; ++run) {
-                act_run<AK, TOK, TW>(r, a, t, run, mv, v[run]);
+                uint32_t u[4], t[4];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool ok = t < a.tokens && 4 * run + i < lim;
-                    v[run][i] = ok ? v[run][i] * sc[run][i] : 0.0f;
-                    mx = fmaxf(mx, fabsf(v[run][i]));
-                    sa += fabsf(v[run][i]);
-                }
+                for (int i = 0; i < 4; ++i)
+                    u[i] = (static_cast<uint32_t>(round_to_int(v[run][i] * sm)) + 0x808080u) ^ 0x808080u;
+                transpose_bytes(u[0], u[1], u[2], u[3], t);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) dig[j][run] = t[j];
+            }
+            expo[u] = e;
+#pragma unroll
+            for (int digit = 0; digit < 4; ++digit) {
+                const int row = 4 * u + digit;
+#pragma unroll
+                for (int run = 0; run < 2; ++run)
+                    *reinterpret_cast<uint32_t*>(ops + ((m * Ops<TPB>::kRows + row) * 4 + 2 * h + run) * 16 + 4 * d) =
+                        dig[digit][run];
             }
         }
-        // fmaxf drops NaN, the sum does not: a NaN or an infinity makes the
-        // chunk sum, and so the token's bound in the epilogue, not finite.
-        const float wmx = wave_max(mx);
-        csum[u] = wave_sum(sa);
-        const int e = range_exponent(wmx, 22);
-        const float sm = m < 7 ? exp2i(e + 7 - m) : -exp2i(e);
-        uint32_t dig[4][2];
-#pragma unroll
-        for (int run = 0; run < 2; ++run) {
-            uint32_t u[4], t[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                u[i] = (static_cast<uint32_t>(round_to_int(v[run][i] * sm)) + 0x808080u) ^ 0x808080u;
-            transpose_bytes(u[0], u[1], u[2], u[3], t);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dig[j][run] = t[j];
-        }
-        expo[u] = e;
-#pragma unroll
-        for (int digit = 0; digit < 4; ++digit) {
-            const int row = 4 * u + digit;
-#pragma unroll
-            for (int run = 0; run < 2; ++run)
-                *reinterpret_cast<uint32_t*>(ops + ((m * Ops<TPB>::kRows + row) * 4 + 2 * h + run) * 16 + 4 * d) =
-                    dig[digit][run];
-        }
-    }
+    };
+    if (TPB == 1 || t_base + TPB <= a.tokens) stage_tokens(std::false_type{});
+    else stage_tokens(std::true_type{});
 }
 
 // S = 2^7 Σ x_q of one chunk and operand block: eight MFMAs against 0x01 << m.
