@@ -173,6 +173,89 @@ int main() {
         for (Buffer* b : wss) delete b;
     }
 
+    // The other entry points, each planned up to its launch with buffers of the
+    // sizes it checks (Qwen3-8B geometry where it has one).
+    {
+        Buffer big(64 << 20), ws(64 << 20), ids(64), pos(64), tok(64), hist(1024), stepb(64), counts(4096);
+        int st = nq_embedding(static_cast<const int64_t*>(ids.p), 1, big.p, NQ_DTYPE_BF16, 151936, 4096, nullptr,
+                              static_cast<float*>(ws.p), nullptr);
+        expect(launch_refused(st), "embedding", st);
+        st = nq_embedding_slots(static_cast<const int64_t*>(ids.p), 1, big.p, NQ_DTYPE_BF16, 151936, 4096, nullptr,
+                                static_cast<float*>(ws.p), static_cast<float*>(x.p), nullptr);
+        expect(launch_refused(st), "embedding slots", st);
+        st = nq_embedding_slots(static_cast<const int64_t*>(ids.p), 1, big.p, NQ_DTYPE_BF16, 10, 24, nullptr,
+                                static_cast<float*>(ws.p), static_cast<float*>(x.p), nullptr);
+        expect(st == NQ_ERR_SHAPE, "embedding slots hidden % 16", st);
+        for (int64_t t : {int64_t(1), int64_t(37)}) {
+            st = nq_add_rmsnorm(static_cast<float*>(big.p), x.p, NQ_DTYPE_F32, scales.p, NQ_DTYPE_BF16, 1e-6f, t, 4096,
+                                y.p, NQ_DTYPE_BF16, nullptr);
+            expect(launch_refused(st), "add_rmsnorm", st);
+        }
+        st = nq_silu_mul(static_cast<const float*>(x.p), static_cast<const float*>(y.p), 12288, ws.p, NQ_DTYPE_BF16,
+                         nullptr);
+        expect(launch_refused(st), "silu_mul", st);
+        const int64_t pw = nq_output_projection_workspace_bytes(151936, 4096);
+        st = nq_output_projection(x.p, NQ_DTYPE_F32, big.p, 151936, 4096, static_cast<float*>(y.p), ws.p, pw, nullptr);
+        expect(launch_refused(st), "output projection", st);
+        st = nq_greedy_select(ws.p, 151936, 4096, static_cast<int64_t*>(tok.p), static_cast<int64_t*>(hist.p), 128,
+                              static_cast<int32_t*>(stepb.p), static_cast<int32_t*>(pos.p), nullptr);
+        expect(launch_refused(st), "greedy select", st);
+        for (int64_t mp : {int64_t(128), int64_t(640), int64_t(1100)}) {
+            for (int hd : {64, 128}) {
+                const int64_t dw = nq_decode_attention_workspace_bytes(32, 8, hd, NQ_DTYPE_BF16, mp);
+                expect(dw > 0, "decode attention workspace", static_cast<int>(dw));
+                st = nq_decode_attention(static_cast<const float*>(x.p), static_cast<const float*>(x.p),
+                                         static_cast<const float*>(x.p), 32, 8, hd, scales.p, scales.p, NQ_DTYPE_BF16,
+                                         1e-6f, static_cast<const float*>(big.p), static_cast<const float*>(big.p),
+                                         static_cast<const int32_t*>(pos.p), mp, ws.p, y.p, NQ_DTYPE_BF16, 0.088f,
+                                         x.p, NQ_DTYPE_F32, words.p, dw, nullptr);
+                expect(launch_refused(st), "decode attention", st);
+                st = nq_decode_attention_partials(static_cast<const float*>(x.p), static_cast<const float*>(x.p),
+                                                  static_cast<const float*>(x.p), 32, 8, hd, scales.p, scales.p,
+                                                  NQ_DTYPE_BF16, 1e-6f, static_cast<const float*>(big.p),
+                                                  static_cast<const float*>(big.p), static_cast<const int32_t*>(pos.p),
+                                                  mp, ws.p, y.p, NQ_DTYPE_BF16, 0.088f, words.p, dw, nullptr);
+                expect(launch_refused(st), "decode attention partials", st);
+            }
+            for (int64_t t : {int64_t(1), int64_t(17), int64_t(64)}) {
+                const int64_t aw = nq_attention_workspace_bytes(t, 32, 128, mp);
+                st = nq_qk_norm_rope_cache(static_cast<const float*>(x.p), static_cast<const float*>(x.p),
+                                           static_cast<const float*>(x.p), t, 32, 8, 128, scales.p, scales.p,
+                                           NQ_DTYPE_BF16, 1e-6f, static_cast<const float*>(big.p),
+                                           static_cast<const float*>(big.p), static_cast<const int32_t*>(pos.p), mp,
+                                           static_cast<float*>(y.p), ws.p, words.p, NQ_DTYPE_BF16, nullptr);
+                expect(launch_refused(st), "qk norm rope cache", st);
+                st = nq_attention(static_cast<const float*>(x.p), ws.p, words.p, NQ_DTYPE_BF16, t, 32, 8, 128,
+                                  static_cast<const int32_t*>(pos.p), mp, 0.088f, y.p, NQ_DTYPE_BF16, big.p, aw,
+                                  nullptr);
+                expect(launch_refused(st), "attention", st);
+            }
+        }
+        st = nq_unpack_signs(static_cast<const int32_t*>(words.p), 3072, 819, 26, NQ_DTYPE_BF16, ws.p, nullptr);
+        expect(launch_refused(st), "unpack", st);
+        st = nq_count_bad_padding(static_cast<const int32_t*>(words.p), 3072, 819, 26,
+                                  static_cast<int32_t*>(counts.p), nullptr);
+        expect(launch_refused(st), "bad padding", st);
+        st = nq_transpose_signs(static_cast<const int32_t*>(words.p), 819, 3072, static_cast<int32_t*>(ws.p),
+                                nullptr);
+        expect(launch_refused(st) || st == NQ_OK, "transpose signs", st);
+        const int64_t tb = nq_tiles_bytes(4096, 1024, 819);
+        Buffer tiles(static_cast<size_t>(tb));
+        nq_linear_desc d = desc_for(4096, 1024, 819, words, scales, tiles, tb);
+        st = nq_prepare_tiles(&d, tiles.p, tb, nullptr);
+        expect(launch_refused(st), "prepare tiles", st);
+        for (int64_t t : {int64_t(1), int64_t(4), int64_t(16)}) {
+            st = nq_linear_static(&d, x.p, NQ_DTYPE_BF16, t, y.p, NQ_DTYPE_F32, nullptr);
+            expect(st != NQ_OK, "linear static", st);
+        }
+        st = nq_decode_mixed_v_words(nullptr, 0, nullptr, 0, nullptr, 819, 4096, nullptr, nullptr, nullptr);
+        expect(st != NQ_OK, "mixed-v null", st);
+        st = nq_decode_product_codebook_words(nullptr, 0, nullptr, 0, nullptr, nullptr, 819, 4096, nullptr, nullptr);
+        expect(st != NQ_OK, "product codebook null", st);
+        st = nq_read_stream(big.p, 1 << 20, static_cast<uint32_t*>(counts.p), 64, nullptr);
+        expect(launch_refused(st), "read stream", st);
+    }
+
     std::printf("%s: %d failed checks\n", failures ? "FAILED" : "ok", failures);
     return failures ? 1 : 0;
 }
