@@ -245,6 +245,7 @@ int enqueue_stage1(const Batch& batch, const LaunchShape& s, hipStream_t stream)
         case kActNormF32:
         case kActGatedF32:
         case kActAttn8:
+        case kActAttn12:
         case kActAttn16: return enqueue_stage1_fused(batch, s, stream);
         default: return enqueue_stage1_generic(batch, s, stream);
     }
@@ -498,10 +499,14 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
         if (fusion->input_kind != NQ_INPUT_PLAIN) {
             if (x_dtype != NQ_DTYPE_F32) return NQ_ERR_DTYPE;
             if (!vector_ok) return NQ_ERR_ALIGNMENT;
-            if (fusion->input_kind == NQ_INPUT_ATTENTION)
-                ak = attn_blocks_of(fusion->attn_max_positions) <= attn_parts<kActAttn8>() ? kActAttn8 : kActAttn16;
-            else
+            if (fusion->input_kind == NQ_INPUT_ATTENTION) {
+                // The fewest partial registers that hold every block.
+                const int64_t blocks = attn_blocks_of(fusion->attn_max_positions);
+                ak = blocks <= attn_parts<kActAttn8>() ? kActAttn8
+                                                       : (blocks <= attn_parts<kActAttn12>() ? kActAttn12 : kActAttn16);
+            } else {
                 ak = fusion->input_kind == NQ_INPUT_RMSNORM ? kActNormF32 : kActGatedF32;
+            }
         }
     }
     return launch_batch(batch, tokens, ak, descs[0]->decode_launch == NQ_DECODE_FUSED, stream, pair);

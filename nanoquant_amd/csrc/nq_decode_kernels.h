@@ -560,14 +560,15 @@ enum : int {
     kActGatedF32 = 5,  // silu(x) * x2 from fp32 gate x and up x2, fp16 s_in
     kActAttn8 = 6,     // attention output merged from fp32 pass-1 partials of up to 8 cache blocks, fp16 s_in
     kActAttn16 = 7,    // the same for up to 16 cache blocks
+    kActAttn12 = 8,    // the same for up to 12 cache blocks (fewer partial registers than kActAttn16)
 };
 
 template <int AK>
-constexpr bool attn_kind() { return AK == kActAttn8 || AK == kActAttn16; }
+constexpr bool attn_kind() { return AK == kActAttn8 || AK == kActAttn12 || AK == kActAttn16; }
 
 // Cache blocks whose partials one lane loads (the attention kinds).
 template <int AK>
-constexpr int attn_parts() { return AK == kActAttn16 ? 16 : 8; }
+constexpr int attn_parts() { return AK == kActAttn16 ? 16 : (AK == kActAttn12 ? 12 : 8); }
 
 using nq::kAttnBlockRows;
 
@@ -829,6 +830,10 @@ struct AttnRegsOf {
 template <>
 struct AttnRegsOf<kActAttn8> {
     using type = AttnParts<8>;
+};
+template <>
+struct AttnRegsOf<kActAttn12> {
+    using type = AttnParts<12>;
 };
 template <>
 struct AttnRegsOf<kActAttn16> {

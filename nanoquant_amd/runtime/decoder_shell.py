@@ -49,9 +49,10 @@ ROLES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_p
 
 # Cache blocks (64 rows each) up to which a decode token folds the attention's
 # merge into the O projection by default. Measured on the 36-layer Qwen3-8B
-# geometry, fused one-token steps: folded 543 vs 524 tok/s at 2 blocks, 539 vs
-# 523 at 4, 511 vs 517 at 10.
-FOLD_MAX_BLOCKS = 6
+# geometry, fused one-token steps, folded against unfolded: 567.5 / 555.0 tok/s
+# at 6 blocks, 561.6 / 553.6 at 8, 553.8 / 551.4 at 9, 550.9 / 550.9 at 10,
+# 544.4 / 549.3 at 12.
+FOLD_MAX_BLOCKS = 9
 
 
 class DecodeStep(NamedTuple):

@@ -185,9 +185,11 @@ def _attention_operands(max_pos, p, cache_dtype, seed, q_heads=32, kv_heads=8, h
 @pytest.mark.parametrize(
     "max_pos,p,cache_dtype,kv_heads,head_dim",
     [
-        (640, 639, torch.bfloat16, 8, 128),  # 10 blocks (up-to-16 kind), last row; MFMA pass 1
+        (640, 639, torch.bfloat16, 8, 128),  # 10 blocks (up-to-12 kind), last row; MFMA pass 1
         (640, 0, torch.bfloat16, 8, 128),    # one live block
         (512, 300, torch.float16, 8, 128),   # 8 blocks (up-to-8 kind)
+        (768, 767, torch.bfloat16, 8, 128),  # 12 blocks (up-to-12 kind, every slot)
+        (832, 777, torch.bfloat16, 8, 128),  # 13 blocks (up-to-16 kind)
         (1024, 1023, torch.bfloat16, 8, 128),  # 16 blocks
         (100, 64, torch.float16, 8, 128),    # 2 blocks, first row of the second
         (20, 7, torch.bfloat16, 8, 128),     # 1 block
