@@ -114,9 +114,11 @@ int nq_decode_attention(const float* q, const float* k, const float* v, int32_t 
 
 /* Pass 1 of nq_decode_attention alone (the same arguments without the output;
  * the same workspace size): the partial results of every 64-row cache block
- * up to position[0] stay in the workspace, as fp32 (max, sum) pairs
- * [q_heads][blocks][2] followed by the accumulators [q_heads][blocks][head_dim],
- * blocks = ceil(max_positions / 64), for a projection whose input merges them
+ * stay in the workspace, as fp32 (max, sum) pairs [q_heads][blocks][2]
+ * followed by the accumulators [q_heads][blocks][head_dim], blocks =
+ * ceil(max_positions / 64); a block past position[0] holds the neutral partial
+ * (max -inf, sum 0, accumulators 0), so a merge may run over every block.
+ * For a projection whose input merges them
  * (nq_linear_batch_fused with NQ_INPUT_ATTENTION). Only the one-pass form:
  * head_dim * cache element bytes <= 256 and q_heads / kv_heads 1, 2, 4 or 8,
  * otherwise NQ_ERR_UNSUPPORTED. No reference counterpart: the reference's

@@ -883,9 +883,10 @@ __device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const Lin& 
     const int k0 = stage_col0(c, lane);
     const int in = static_cast<int>(a.in);
     if constexpr (attn_kind<AK>()) {
-        // Every block's partials, issued before the position is known (the
-        // merge skips blocks past it); slots past the cache's blocks are not
-        // loaded. in is a multiple of 8 and of the head dimension.
+        // Every block's partials, issued before the position is known (pass 1
+        // stores a neutral partial for the blocks past the position); slots
+        // past the cache's blocks hold the neutral partial without a load. in
+        // is a multiple of 8 and of the head dimension.
         constexpr int NB = attn_parts<AK>();
         const int kk = k0 < in ? k0 : in - 8;
         const int hd = a.attn_hd_log2;
@@ -900,6 +901,10 @@ __device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const Lin& 
                 r.at.acc[s][0] = *reinterpret_cast<const v4u*>(p);
                 r.at.acc[s][1] = *reinterpret_cast<const v4u*>(p + 4);
                 r.at.ml[s] = *reinterpret_cast<const v2u*>(ml + 2 * s);
+            } else {
+                r.at.acc[s][0] = v4u{0u, 0u, 0u, 0u};
+                r.at.acc[s][1] = v4u{0u, 0u, 0u, 0u};
+                r.at.ml[s] = v2u{0xff800000u, 0u};  // (-inf, 0)
             }
         }
         r.at.pos = a.attn_pos[0];
@@ -1045,23 +1050,23 @@ __device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const L
     constexpr int NB = attn_parts<AK>();
     const int64_t pos = r.at.pos;
     const bool in_range = pos >= 0 && pos < a.attn_max_positions;  // uniform
-    const int nb = in_range ? static_cast<int>(pos / kAttnBlockRows) + 1 : 1;
+    // Every slot in block order: the slots past the position hold the neutral
+    // partial, whose weight exp(-inf - m) is 0 and whose terms fmaf(0, 0, s)
+    // leave the sums exactly as a merge of the live blocks alone.
     float m = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < NB; ++s) m = s < nb ? fmaxf(m, __uint_as_float(r.at.ml[s].x)) : m;
+    for (int s = 0; s < NB; ++s) m = fmaxf(m, __uint_as_float(r.at.ml[s].x));
     float l = 0.0f, acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
-        if (s < nb) {  // a select: slots past the position may hold anything
-            const float f = nq::merge_exp(__uint_as_float(r.at.ml[s].x) - m);
-            l = fmaf(__uint_as_float(r.at.ml[s].y), f, l);
+        const float f = nq::merge_exp(__uint_as_float(r.at.ml[s].x) - m);
+        l = fmaf(__uint_as_float(r.at.ml[s].y), f, l);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[i] = fmaf(__uint_as_float(r.at.acc[s][0][i]), f, acc[i]);
-                acc[4 + i] = fmaf(__uint_as_float(r.at.acc[s][1][i]), f, acc[4 + i]);
-            }
+        for (int i = 0; i < 4; ++i) {
+            acc[i] = fmaf(__uint_as_float(r.at.acc[s][0][i]), f, acc[i]);
+            acc[4 + i] = fmaf(__uint_as_float(r.at.acc[s][1][i]), f, acc[4 + i]);
         }
     }
 #pragma unroll

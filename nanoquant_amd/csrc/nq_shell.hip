@@ -837,16 +837,18 @@ __global__ __launch_bounds__(kMfmaHeads * kWave) void k_decode_attention_mfma(
             o[u] = mfma16<CT>(a, b.v, o[u]);
         }
     }
-    if (!live) return;
+    // A block past the token's row stores the neutral partial (max -inf, sum
+    // 0, accumulators 0), which adds nothing to a merge over every block.
     const int64_t pi = attn_part_index(0, g * G + kg, s, q_heads, blocks);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) part_acc[pi * D + 32 * w + 16 * u + n] = (o[u][0] + o[u][1]) + (o[u][2] + o[u][3]);
+    for (int u = 0; u < 2; ++u)
+        part_acc[pi * D + 32 * w + 16 * u + n] = live ? (o[u][0] + o[u][1]) + (o[u][2] + o[u][3]) : 0.0f;
     if (w == 0 && n == 0) {
         float l = 0.0f;
 #pragma unroll
         for (int i = 0; i < G; ++i) l += ls[kg * G + i];
-        part_ml[2 * pi] = M;
-        part_ml[2 * pi + 1] = l;
+        part_ml[2 * pi] = live ? M : -INFINITY;
+        part_ml[2 * pi + 1] = live ? l : 0.0f;
     }
 }
 
@@ -1223,15 +1225,16 @@ __global__ __launch_bounds__(G * kWave) void k_decode_attention(
     float acc[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) acc[e] = (acc4[0][e] + acc4[1][e]) + (acc4[2][e] + acc4[3][e]);
-    if (!live) return;
+    // A block past the token's row stores the neutral partial (max -inf, sum
+    // 0, accumulators 0), which adds nothing to a merge over every block.
     const int h = g * G + w;
     const int64_t pi = attn_part_index(0, h, s, q_heads, blocks);
     if (lane == 0) {
-        part_ml[2 * pi] = m;
-        part_ml[2 * pi + 1] = l;
+        part_ml[2 * pi] = live ? m : -INFINITY;
+        part_ml[2 * pi + 1] = live ? l : 0.0f;
     }
 #pragma unroll
-    for (int e = 0; e < E; ++e) part_acc[pi * D + lane * E + e] = acc[e];
+    for (int e = 0; e < E; ++e) part_acc[pi * D + lane * E + e] = live ? acc[e] : 0.0f;
 }
 
 // ---------------------------------------------------------------------------

@@ -50,9 +50,9 @@ ROLES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_p
 # Cache blocks (64 rows each) up to which a decode token folds the attention's
 # merge into the O projection by default. Measured on the 36-layer Qwen3-8B
 # geometry, fused one-token steps, folded against unfolded: 567.5 / 555.0 tok/s
-# at 6 blocks, 561.6 / 553.6 at 8, 553.8 / 551.4 at 9, 550.9 / 550.9 at 10,
-# 544.4 / 549.3 at 12.
-FOLD_MAX_BLOCKS = 9
+# at 6 blocks, 561.6 / 553.6 at 8, 556.6 / 552.4 at 9, 553.5 / 551.9 at 10,
+# 551.2 / 551.6 at 11, 547.4 / 549.9 at 12.
+FOLD_MAX_BLOCKS = 10
 
 
 class DecodeStep(NamedTuple):
