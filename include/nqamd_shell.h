@@ -115,9 +115,11 @@ int nq_decode_attention(const float* q, const float* k, const float* v, int32_t 
 /* Pass 1 of nq_decode_attention alone (the same arguments without the output;
  * the same workspace size): the partial results of every 64-row cache block
  * stay in the workspace, as fp32 (max, sum) pairs [q_heads][blocks][2]
- * followed by the accumulators [q_heads][blocks][head_dim], blocks =
- * ceil(max_positions / 64); a block past position[0] holds the neutral partial
- * (max -inf, sum 0, accumulators 0), so a merge may run over every block.
+ * followed by each block's output acc / sum in fp16 [q_heads][blocks][head_dim]
+ * (a block's output is a weighted mean of V rows: values beyond the fp16 range
+ * become infinite), blocks = ceil(max_positions / 64); a block past position[0]
+ * holds the neutral partial (max -inf, sum 0, output 0), so a merge may run
+ * over every block, weighting block s by sum_s * exp(max_s - max).
  * For a projection whose input merges them
  * (nq_linear_batch_fused with NQ_INPUT_ATTENTION). Only the one-pass form:
  * head_dim * cache element bytes <= 256 and q_heads / kv_heads 1, 2, 4 or 8,

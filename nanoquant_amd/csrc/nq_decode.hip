@@ -273,8 +273,8 @@ int describe_fusion(const nq_decode_fusion& f, int i, const nq_linear_desc* d, L
         if (!aligned(f.ups[i], 16)) return NQ_ERR_ALIGNMENT;
         a.x2 = f.ups[i];
     } else if (f.input_kind == NQ_INPUT_ATTENTION) {
-        // x (already in a.x) is the pass-1 workspace: (max, sum) pairs
-        // [heads][blocks][2], then the accumulators [heads][blocks][head_dim].
+        // x (already in a.x) is the pass-1 workspace: fp32 (max, sum) pairs
+        // [heads][blocks][2], then the fp16 block outputs [heads][blocks][head_dim].
         const int hd = f.attn_head_dim;
         if (!f.attn_position || (hd != 64 && hd != 128 && hd != 256)) return NQ_ERR_ARGUMENT;
         if (in % hd != 0 || f.attn_max_positions <= 0 || f.attn_max_positions > 0x7fffffff) return NQ_ERR_SHAPE;

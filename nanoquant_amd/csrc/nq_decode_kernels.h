@@ -206,9 +206,9 @@ struct Lin {
     float* slots_out;        // stage 2: sum of residual^2 per 16-row output tile
     int nslots;              // entries of slots_in
     float eps;               // normed input: RMSNorm epsilon
-    // Attention input (one token): x is the fp32 partial accumulators of the
-    // decode attention's pass 1, [heads][attn_blocks][head_dim] with heads =
-    // in / head_dim, and attn_ml their (max, sum) pairs [heads][attn_blocks][2].
+    // Attention input (one token): x is the fp16 block outputs (acc / sum) of
+    // the decode attention's pass 1, [heads][attn_blocks][head_dim] with heads =
+    // in / head_dim, and attn_ml their fp32 (max, sum) pairs [heads][attn_blocks][2].
     const float* attn_ml;
     const int32_t* attn_pos;    // the token's cache position
     int attn_blocks;            // cache blocks of kAttnBlockRows rows
@@ -558,7 +558,7 @@ enum : int {
     kActGeneric = 3,   // any float x and s_in, element loads
     kActNormF32 = 4,   // fp32 x (a residual), fp32 col_scale (norm weight * s_in), RMS factor from slots_in
     kActGatedF32 = 5,  // silu(x) * x2 from fp32 gate x and up x2, fp16 s_in
-    kActAttn8 = 6,     // attention output merged from fp32 pass-1 partials of up to 8 cache blocks, fp16 s_in
+    kActAttn8 = 6,     // attention output merged from pass-1 partials of up to 8 cache blocks, fp16 s_in
     kActAttn16 = 7,    // the same for up to 16 cache blocks
     kActAttn12 = 8,    // the same for up to 12 cache blocks (fewer partial registers than kActAttn16)
 };
@@ -819,7 +819,7 @@ __device__ __forceinline__ int stage_col0(int c, int lane) {
 // (max, sum) pair, and the token's position.
 template <int NB>
 struct AttnParts {
-    v4u acc[NB][2];
+    v4u out[NB];  // the block outputs of the lane's eight columns, fp16
     v2u ml[NB];
     int pos;
 };
@@ -886,24 +886,23 @@ __device__ __forceinline__ void load_s1_acts(S1Regs<AK, TOK, TW>& r, const Lin& 
         // Every block's partials, issued before the position is known (pass 1
         // stores a neutral partial for the blocks past the position); slots
         // past the cache's blocks hold the neutral partial without a load. in
-        // is a multiple of 8 and of the head dimension.
+        // is a multiple of 8 and of the head dimension. A block's output is
+        // fp16 (acc / sum; one 16-byte load for the lane's eight columns).
         constexpr int NB = attn_parts<AK>();
         const int kk = k0 < in ? k0 : in - 8;
         const int hd = a.attn_hd_log2;
         const int blocks = a.attn_blocks;
         const int64_t head = kk >> hd;
-        const float* acc = static_cast<const float*>(a.x) + ((head * blocks) << hd) + (kk & ((1 << hd) - 1));
+        const _Float16* outs =
+            static_cast<const _Float16*>(a.x) + ((head * blocks) << hd) + (kk & ((1 << hd) - 1));
         const float* ml = a.attn_ml + head * blocks * 2;
 #pragma unroll
         for (int s = 0; s < NB; ++s) {
             if (s < blocks) {  // uniform
-                const float* p = acc + (static_cast<int64_t>(s) << hd);
-                r.at.acc[s][0] = *reinterpret_cast<const v4u*>(p);
-                r.at.acc[s][1] = *reinterpret_cast<const v4u*>(p + 4);
+                r.at.out[s] = *reinterpret_cast<const v4u*>(outs + (static_cast<int64_t>(s) << hd));
                 r.at.ml[s] = *reinterpret_cast<const v2u*>(ml + 2 * s);
             } else {
-                r.at.acc[s][0] = v4u{0u, 0u, 0u, 0u};
-                r.at.acc[s][1] = v4u{0u, 0u, 0u, 0u};
+                r.at.out[s] = v4u{0u, 0u, 0u, 0u};
                 r.at.ml[s] = v2u{0xff800000u, 0u};  // (-inf, 0)
             }
         }
@@ -1050,9 +1049,9 @@ __device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const L
     constexpr int NB = attn_parts<AK>();
     const int64_t pos = r.at.pos;
     const bool in_range = pos >= 0 && pos < a.attn_max_positions;  // uniform
-    // Every slot in block order: the slots past the position hold the neutral
-    // partial, whose weight exp(-inf - m) is 0 and whose terms fmaf(0, 0, s)
-    // leave the sums exactly as a merge of the live blocks alone.
+    // Every slot in block order, block s weighted by sum_s * exp(m_s - m): the
+    // slots past the position hold the neutral partial, whose weight is
+    // 0 * exp(-inf - m) = 0, so they add nothing.
     float m = -INFINITY;
 #pragma unroll
     for (int s = 0; s < NB; ++s) m = fmaxf(m, __uint_as_float(r.at.ml[s].x));
@@ -1061,12 +1060,15 @@ __device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const L
     for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
 #pragma unroll
     for (int s = 0; s < NB; ++s) {
-        const float f = nq::merge_exp(__uint_as_float(r.at.ml[s].x) - m);
-        l = fmaf(__uint_as_float(r.at.ml[s].y), f, l);
+        const float wgt = __uint_as_float(r.at.ml[s].y) * nq::merge_exp(__uint_as_float(r.at.ml[s].x) - m);
+        l += wgt;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc[i] = fmaf(__uint_as_float(r.at.acc[s][0][i]), f, acc[i]);
-            acc[4 + i] = fmaf(__uint_as_float(r.at.acc[s][1][i]), f, acc[4 + i]);
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t pair = r.at.out[s][j];
+            const float lo = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair & 0xffffu)));
+            const float hi = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(pair >> 16)));
+            acc[2 * j] = fmaf(lo, wgt, acc[2 * j]);
+            acc[2 * j + 1] = fmaf(hi, wgt, acc[2 * j + 1]);
         }
     }
 #pragma unroll

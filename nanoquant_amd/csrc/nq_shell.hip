@@ -667,7 +667,7 @@ constexpr size_t decode_attention_mfma_lds() {
            kMfmaHeads * 4 * kSeqBlock * 2 + 2 * kMfmaHeads * kMfmaHeads * 4;
 }
 
-template <int CT>
+template <int CT, bool HALF>
 __global__ __launch_bounds__(kMfmaHeads * kWave) void k_decode_attention_mfma(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int kv_heads,
     const void* __restrict__ q_norm, const void* __restrict__ k_norm, int ndt, float eps,
@@ -839,14 +839,22 @@ __global__ __launch_bounds__(kMfmaHeads * kWave) void k_decode_attention_mfma(
     }
     // A block past the token's row stores the neutral partial (max -inf, sum
     // 0, accumulators 0), which adds nothing to a merge over every block.
+    // HALF: the block's output acc / sum as fp16 in place of the accumulators.
     const int64_t pi = attn_part_index(0, g * G + kg, s, q_heads, blocks);
+    float l = 0.0f;
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
-        part_acc[pi * D + 32 * w + 16 * u + n] = live ? (o[u][0] + o[u][1]) + (o[u][2] + o[u][3]) : 0.0f;
+    for (int i = 0; i < G; ++i) l += ls[kg * G + i];
+    const float inv = HALF && live ? 1.0f / l : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const float a = (o[u][0] + o[u][1]) + (o[u][2] + o[u][3]);
+        if constexpr (HALF)
+            reinterpret_cast<_Float16*>(part_acc)[pi * D + 32 * w + 16 * u + n] =
+                static_cast<_Float16>(live ? a * inv : 0.0f);
+        else
+            part_acc[pi * D + 32 * w + 16 * u + n] = live ? a : 0.0f;
+    }
     if (w == 0 && n == 0) {
-        float l = 0.0f;
-#pragma unroll
-        for (int i = 0; i < G; ++i) l += ls[kg * G + i];
         part_ml[2 * pi] = live ? M : -INFINITY;
         part_ml[2 * pi + 1] = live ? l : 0.0f;
     }
@@ -1072,7 +1080,7 @@ constexpr size_t decode_attention_lds() {
            static_cast<size_t>(kSeqBlock + 1) * D * cache_bytes<CT>() + static_cast<size_t>(G) * (D + kSeqBlock) * sizeof(float);
 }
 
-template <int D, int CT, int G>
+template <int D, int CT, int G, bool HALF>
 __global__ __launch_bounds__(G * kWave) void k_decode_attention(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v, int kv_heads,
     const void* __restrict__ q_norm, const void* __restrict__ k_norm, int ndt, float eps,
@@ -1227,14 +1235,22 @@ __global__ __launch_bounds__(G * kWave) void k_decode_attention(
     for (int e = 0; e < E; ++e) acc[e] = (acc4[0][e] + acc4[1][e]) + (acc4[2][e] + acc4[3][e]);
     // A block past the token's row stores the neutral partial (max -inf, sum
     // 0, accumulators 0), which adds nothing to a merge over every block.
+    // HALF: the block's output acc / sum as fp16 in place of the accumulators.
     const int h = g * G + w;
     const int64_t pi = attn_part_index(0, h, s, q_heads, blocks);
     if (lane == 0) {
         part_ml[2 * pi] = live ? m : -INFINITY;
         part_ml[2 * pi + 1] = live ? l : 0.0f;
     }
+    const float inv = HALF && live ? 1.0f / l : 0.0f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) part_acc[pi * D + lane * E + e] = live ? acc[e] : 0.0f;
+    for (int e = 0; e < E; ++e) {
+        if constexpr (HALF)
+            reinterpret_cast<_Float16*>(part_acc)[pi * D + lane * E + e] =
+                static_cast<_Float16>(live ? acc[e] * inv : 0.0f);
+        else
+            part_acc[pi * D + lane * E + e] = live ? acc[e] : 0.0f;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1486,16 +1502,30 @@ int launch_decode_attention_g(const float* q, const float* k, const float* v, in
                               const int32_t* position, int64_t max_positions, void* kc, void* vc, float scaling,
                               void* out, int odt, float* ml, float* acc, bool merge, hipStream_t st) {
     const int blocks = attention_blocks(max_positions);
+    // The partials form (no merge here) stores each block's output in fp16 for
+    // the projection input that merges them; the merge below reads fp32 sums.
     if constexpr (D == 128 && G == kMfmaHeads && CT != NQ_DTYPE_F32) {
-        hipLaunchKernelGGL((k_decode_attention_mfma<CT>), dim3(kv_heads, blocks), dim3(G * kWave),
-                           decode_attention_mfma_lds<CT>(), st, q, k, v, kv_heads, qn, kn, ndt, eps, cs, sn, position,
-                           max_positions, static_cast<char*>(kc), static_cast<char*>(vc), scaling, ml, acc);
+        if (merge)
+            hipLaunchKernelGGL((k_decode_attention_mfma<CT, false>), dim3(kv_heads, blocks), dim3(G * kWave),
+                               decode_attention_mfma_lds<CT>(), st, q, k, v, kv_heads, qn, kn, ndt, eps, cs, sn,
+                               position, max_positions, static_cast<char*>(kc), static_cast<char*>(vc), scaling, ml,
+                               acc);
+        else
+            hipLaunchKernelGGL((k_decode_attention_mfma<CT, true>), dim3(kv_heads, blocks), dim3(G * kWave),
+                               decode_attention_mfma_lds<CT>(), st, q, k, v, kv_heads, qn, kn, ndt, eps, cs, sn,
+                               position, max_positions, static_cast<char*>(kc), static_cast<char*>(vc), scaling, ml,
+                               acc);
     } else {
         const size_t lds = decode_attention_lds<D, CT, G>();
         if (lds > 64 * 1024) return NQ_ERR_UNSUPPORTED;
-        hipLaunchKernelGGL((k_decode_attention<D, CT, G>), dim3(kv_heads, blocks), dim3(G * kWave), lds, st, q, k, v,
-                           kv_heads, qn, kn, ndt, eps, cs, sn, position, max_positions, static_cast<char*>(kc),
-                           static_cast<char*>(vc), scaling, ml, acc);
+        if (merge)
+            hipLaunchKernelGGL((k_decode_attention<D, CT, G, false>), dim3(kv_heads, blocks), dim3(G * kWave), lds,
+                               st, q, k, v, kv_heads, qn, kn, ndt, eps, cs, sn, position, max_positions,
+                               static_cast<char*>(kc), static_cast<char*>(vc), scaling, ml, acc);
+        else
+            hipLaunchKernelGGL((k_decode_attention<D, CT, G, true>), dim3(kv_heads, blocks), dim3(G * kWave), lds,
+                               st, q, k, v, kv_heads, qn, kn, ndt, eps, cs, sn, position, max_positions,
+                               static_cast<char*>(kc), static_cast<char*>(vc), scaling, ml, acc);
     }
     if (hipGetLastError() != hipSuccess) return NQ_ERR_LAUNCH;
     if (!merge) return NQ_OK;  // the partials stay in the workspace

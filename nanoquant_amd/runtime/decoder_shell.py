@@ -277,11 +277,14 @@ class PackedDecoder:
         # One-token steps with the fused calls can also fold the attention's
         # second pass (the merge of its cache blocks) into the O projection's
         # input (input_kind="attention"): one launch fewer per layer, but every
-        # O workgroup then reads all blocks' fp32 partials (blocks x 16 KB at
-        # 4096 columns). None chooses by the cache length: folded up to
-        # FOLD_MAX_BLOCKS blocks, where the saved launch outweighs the reads.
+        # O workgroup then reads all blocks' partials (blocks x 8 KB of fp16
+        # outputs at 4096 columns). None chooses by the cache length: folded up
+        # to FOLD_MAX_BLOCKS blocks, where the saved launch outweighs the reads.
+        # The folded merge reads each block's output in fp16: by default only
+        # with a 16-bit cache, whose values the attention output already carries.
         blocks = -(-self.max_positions // 64)
-        fold = blocks <= FOLD_MAX_BLOCKS if fold_attention_merge is None else bool(fold_attention_merge)
+        fold = (blocks <= FOLD_MAX_BLOCKS and cache_dtype != torch.float32 if fold_attention_merge is None
+                else bool(fold_attention_merge))
         self.fold_attention_merge = (
             fold and self.fuse_decode
             and ops.decode_attention_partials_supported(c.q_heads, c.kv_heads, c.head_dim, cache_dtype)

@@ -200,10 +200,11 @@ def _attention_operands(max_pos, p, cache_dtype, seed, q_heads=32, kv_heads=8, h
     ],
 )
 def test_attention_input_equals_merge_then_plain_call(max_pos, p, cache_dtype, kv_heads, head_dim):
-    # With fp32 attention output, the merge kernel and the folded input compute
-    # the same values in the same order, so the O projection's results and the
-    # appended cache rows are identical, not just close (for the MFMA pass 1
-    # and for the other one-pass geometries alike).
+    # The folded input merges the blocks' fp16 outputs (acc / sum), the merge
+    # kernel their fp32 accumulators: the O projection's results agree to the
+    # fp16 rounding of a block output (unit roundoff 2^-11), within the 2e-3
+    # bar; the appended cache rows are identical (the same pass 1), and so is a
+    # zero input (for the MFMA pass 1 and for the other one-pass geometries).
     backend = HipPackedBackend()
     shape = syn.qwen3_8b_layer()[3]
     q_heads = shape.in_features // head_dim
@@ -229,10 +230,15 @@ def test_attention_input_equals_merge_then_plain_call(max_pos, p, cache_dtype, k
             err = orc.relative_l2(r.cpu() - r0, expected)
             assert err <= REL_L2, err
         results.append((r, slots, kc, vc))
-    for a, b in zip(*results):
-        assert torch.equal(a, b)
+    (r_m, s_m, kc_m, vc_m), (r_f, s_f, kc_f, vc_f) = results
+    assert torch.equal(kc_m, kc_f) and torch.equal(vc_m, vc_f)
     if p >= max_pos:
-        assert torch.equal(results[1][0].cpu(), r0)  # zero input, no bias
+        assert torch.equal(r_f.cpu(), r0) and torch.equal(r_m.cpu(), r0)  # zero input, no bias
+        return
+    err = orc.relative_l2(r_f.cpu() - r0, r_m.cpu() - r0)
+    _say("folded against merged, rel-L2", f"{err:.2e}")
+    assert err <= REL_L2, err
+    assert orc.relative_l2(s_f.cpu(), s_m.cpu()) <= REL_L2
 
 
 def test_attention_input_rejects_what_it_does_not_cover():
@@ -267,7 +273,8 @@ SMALL = DecoderShellConfig(layers=3, hidden=256, intermediate=768, q_heads=4, kv
 @pytest.mark.parametrize("cache", [torch.float32, torch.bfloat16])
 def test_folded_attention_decoder_matches_unfolded(cache):
     # 130 cache rows: three blocks; the unfolded decoder rounds the attention
-    # output to the activation dtype (fp32 here), the folded one merges in fp32.
+    # output to the activation dtype (fp32 here), the folded one merges the
+    # blocks' fp16 outputs: logits agree to that rounding, and so do the tokens.
     weights = syn.synthetic_decoder(SMALL, seed=syn.BASE_SEED + 345, random_norms=True)
     prompt = torch.randint(0, SMALL.vocab, (70,), generator=torch.Generator().manual_seed(10)).cuda()
     runs = {}
@@ -288,7 +295,9 @@ def test_folded_attention_decoder_matches_unfolded(cache):
             logits.append(decoder.logits.clone())
         runs[(fold, "logits")] = logits
     for a, b in zip(runs[(True, "logits")], runs[(False, "logits")]):
-        assert orc.relative_l2(a, b) <= 1e-5
+        err = orc.relative_l2(a, b)
+        _say("folded decoder logits against unfolded, rel-L2", f"{err:.2e}")
+        assert err <= 2e-3
     assert runs[True][:8] == runs[False][:8]
 
 
