@@ -49,10 +49,11 @@ ROLES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_p
 
 # Cache blocks (64 rows each) up to which a decode token folds the attention's
 # merge into the O projection by default. Measured on the 36-layer Qwen3-8B
-# geometry, fused one-token steps, folded against unfolded: 567.5 / 555.0 tok/s
-# at 6 blocks, 561.6 / 553.6 at 8, 556.6 / 552.4 at 9, 553.5 / 551.9 at 10,
-# 551.2 / 551.6 at 11, 547.4 / 549.9 at 12.
-FOLD_MAX_BLOCKS = 10
+# geometry, fused one-token steps with a bf16 cache, folded against unfolded:
+# 565.3 / 553.6 tok/s at 10 blocks, 566.1 / 553.4 at 11, 563.7 / 551.9 at 12,
+# 560.2 / 551.6 at 13, 558.5 / 550.9 at 14, 555.9 / 550.6 at 15, 547.9 / 549.7
+# at 16.
+FOLD_MAX_BLOCKS = 15
 
 
 class DecodeStep(NamedTuple):
