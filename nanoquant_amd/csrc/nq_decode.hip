@@ -246,7 +246,10 @@ int enqueue_stage1(const Batch& batch, const LaunchShape& s, hipStream_t stream)
         case kActGatedF32:
         case kActAttn8:
         case kActAttn12:
-        case kActAttn16: return enqueue_stage1_fused(batch, s, stream);
+        case kActAttn16:
+        case kActAttn8E:
+        case kActAttn12E:
+        case kActAttn16E: return enqueue_stage1_fused(batch, s, stream);
         default: return enqueue_stage1_generic(batch, s, stream);
     }
 }
@@ -500,10 +503,13 @@ int launch_decode_batch(const nq_linear_desc* const* descs, int count, const voi
             if (x_dtype != NQ_DTYPE_F32) return NQ_ERR_DTYPE;
             if (!vector_ok) return NQ_ERR_ALIGNMENT;
             if (fusion->input_kind == NQ_INPUT_ATTENTION) {
-                // The fewest partial registers that hold every block.
+                // The fewest partial registers that hold every block; paired
+                // (max, sum) loads for an even block count.
                 const int64_t blocks = attn_blocks_of(fusion->attn_max_positions);
-                ak = blocks <= attn_parts<kActAttn8>() ? kActAttn8
-                                                       : (blocks <= attn_parts<kActAttn12>() ? kActAttn12 : kActAttn16);
+                const bool even = blocks % 2 == 0;
+                ak = blocks <= attn_parts<kActAttn8>()    ? (even ? kActAttn8E : kActAttn8)
+                     : blocks <= attn_parts<kActAttn12>() ? (even ? kActAttn12E : kActAttn12)
+                                                          : (even ? kActAttn16E : kActAttn16);
             } else {
                 ak = fusion->input_kind == NQ_INPUT_RMSNORM ? kActNormF32 : kActGatedF32;
             }

@@ -2,7 +2,7 @@
 // (one token): the RMSNorm-folded fp32 residual (k_decode_stage1<kActNormF32,
 // ...>), the SiLU-gated fp32 gate/up pair (k_decode_stage1<kActGatedF32,
 // ...>) and the attention output merged from pass-1 partials
-// (k_decode_stage1<kActAttn8 / kActAttn12 / kActAttn16, ...>). The kernels are documented
+// (k_decode_stage1<kActAttn8 ... kActAttn16E, ...>). The kernels are documented
 // in nq_decode_kernels.h.
 #include "nq_decode_kernels.h"
 
@@ -50,6 +50,9 @@ int enqueue_stage1_fused(const Batch& batch, const LaunchShape& s, hipStream_t s
         case kActGatedF32: return by_tiles<kActGatedF32>(batch, s, stream);
         case kActAttn8: return attn_by_tiles<kActAttn8>(batch, s, stream);
         case kActAttn12: return attn_by_tiles<kActAttn12>(batch, s, stream);
+        case kActAttn8E: return attn_by_tiles<kActAttn8E>(batch, s, stream);
+        case kActAttn12E: return attn_by_tiles<kActAttn12E>(batch, s, stream);
+        case kActAttn16E: return attn_by_tiles<kActAttn16E>(batch, s, stream);
         case kActAttn16: return attn_by_tiles<kActAttn16>(batch, s, stream);
         default: return NQ_ERR_UNSUPPORTED;
     }
