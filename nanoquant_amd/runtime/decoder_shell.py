@@ -50,10 +50,10 @@ ROLES = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_p
 # Cache blocks (64 rows each) up to which a decode token folds the attention's
 # merge into the O projection by default. Measured on the 36-layer Qwen3-8B
 # geometry, fused one-token steps with a bf16 cache, folded against unfolded:
-# 565.3 / 553.6 tok/s at 10 blocks, 566.1 / 553.4 at 11, 563.7 / 551.9 at 12,
-# 560.2 / 551.6 at 13, 558.5 / 550.9 at 14, 555.9 / 550.6 at 15, 547.9 / 549.7
-# at 16.
-FOLD_MAX_BLOCKS = 15
+# 571.5 / 554.7 tok/s at 10 blocks, 566.1 / 553.4 at 11, 560.2 / 551.6 at 13,
+# 558.5 / 550.9 at 14, 555.9 / 550.6 at 15, 555.5 / 551.0 at 16, the most
+# blocks the folded input holds.
+FOLD_MAX_BLOCKS = 16
 
 
 class DecodeStep(NamedTuple):
