@@ -66,7 +66,7 @@ def parse_args(argv=None):
     p.add_argument("--prefill-tokens", default="64,256,512,2048", help="config-3 token counts ('' to skip)")
     p.add_argument("--e2e-tokens", type=int, default=128, help="greedy tokens of the config-5 run (0 to skip)")
     p.add_argument("--e2e-prompt", type=int, default=512)
-    p.add_argument("--skip", default="", help="comma-separated sections to skip: config1..config5,copy,cpu")
+    p.add_argument("--skip", default="", help="comma-separated sections to skip: config1..config5,copy,cpu,validate")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB 10 times (byte-counter calibration) and exit")
     p.add_argument("--dominant-only", action="store_true",
@@ -608,6 +608,157 @@ def config3(args, device) -> dict:
 # --- config 5 ---------------------------------------------------------------------------
 
 
+def _rel_l2(got, expected) -> float:
+    return float((got.double() - expected.double()).norm() / expected.double().norm().clamp_min(1e-300))
+
+
+def _dense_weight64(state, device):
+    """W = diag(s_out) U diag(s_mid) Vt diag(s_in) of a plain packed linear in
+    fp64 on the device, from its packed words unpacked by torch bit operations
+    (src/nanoquant/runtime/reference.py:122-138; this model has no sidecars)."""
+
+    import torch
+
+    from nanoquant_amd.runtime.packed import unpack_sign_matrix
+
+    spec = state.spec
+    if state.outlier_indices is not None or state.patch_left is not None or state.bias is not None:
+        raise ValueError(f"{spec.name}: the validation reconstructs plain packed linears only")
+    f64 = torch.float64
+    u = unpack_sign_matrix(state.left_words.to(device), spec.out_features, spec.rank, dtype=f64)
+    v = unpack_sign_matrix(state.right_words.to(device), spec.rank, spec.in_features, dtype=f64)
+    u.mul_(state.scale_post.to(device, f64)[:, None])
+    v.mul_(state.scale_mid.to(device, f64)[:, None]).mul_(state.scale_pre.to(device, f64)[None, :])
+    return u @ v
+
+
+def _transformers_qwen3(config, max_positions: int, device):
+    """transformers' Qwen3ForCausalLM of the decoder's geometry, fp32 on the
+    device, eager attention (the model shell the reference runs its packed
+    linears in: src/nanoquant/runtime/transformers_generation.py:84-114)."""
+
+    import torch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    hf_config = Qwen3Config(
+        vocab_size=config.vocab, hidden_size=config.hidden, intermediate_size=config.intermediate,
+        num_hidden_layers=config.layers, num_attention_heads=config.q_heads, num_key_value_heads=config.kv_heads,
+        head_dim=config.head_dim, rms_norm_eps=config.eps, rope_theta=config.rope_theta,
+        tie_word_embeddings=False, max_position_embeddings=max_positions, attention_bias=False,
+    )
+    hf_config._attn_implementation = "eager"
+    with torch.device(device):
+        model = Qwen3ForCausalLM(hf_config)
+    return model.float().eval()
+
+
+def validate_config5(decoder, weights, config, prompt, tokens: list[int], device) -> dict:
+    """The headline run checked against fp32/fp64 torch on the same GPU, in the
+    two ways the reference validates its CUDA runtime.
+
+    Every packed linear (tools/validate_cuda_packed_runtime.py:86-140): a seeded
+    bf16 input row through the prepared layer the decoder uses, twice (the
+    results must be bit-identical), against the fp64 reconstruction of the
+    packed words and scales; rel-L2 must stay within 2e-3.
+
+    The run's greedy tokens, teacher-forced: the prompt and the generated tokens
+    through transformers' Qwen3ForCausalLM in fp32 with those reconstructions as
+    weights, one causal pass, against the decoder's own logits of every step
+    (``forward_step``: the prompt pass, then a replay of the captured one-token
+    graph per token). Each step's logits must give the run's token as their
+    argmax; where the reference's top-2 gap exceeds twice that step's largest
+    logit error the token is decided and must be the reference's argmax. The
+    decoder computes in bf16 (activations and KV cache) and the reference in
+    fp32, so the logits differ by bf16 rounding carried through 36 layers:
+    each step's logits rel-L2 must stay within 5e-2 (the 36-layer bf16 bar of
+    the decoder's parity tests is 4e-2 against an oracle that rounds where the
+    decoder rounds)."""
+
+    import torch
+
+    from nanoquant_amd.runtime.decoder_shell import ROLES
+
+    t0 = time.perf_counter()
+    _say("config5: validation, building the fp32 transformers reference")
+    model = _transformers_qwen3(config, decoder.max_positions, device)
+    g = torch.Generator(device=device).manual_seed(20260715)
+    worst, worst_name, replay_ok = 0.0, "", True
+    with torch.no_grad():
+        model.model.embed_tokens.weight.copy_(weights.embed.float())
+        model.lm_head.weight.copy_(weights.lm_head.float())
+        model.model.norm.weight.copy_(weights.final_norm.float())
+        for block, layer, prepared in zip(model.model.layers, weights.layers, decoder.layers):
+            block.input_layernorm.weight.copy_(layer.input_norm.float())
+            block.post_attention_layernorm.weight.copy_(layer.post_norm.float())
+            block.self_attn.q_norm.weight.copy_(layer.q_norm.float())
+            block.self_attn.k_norm.weight.copy_(layer.k_norm.float())
+            for role in ROLES:
+                state = layer.linears[role]
+                w64 = _dense_weight64(state, device)
+                x = torch.randn(1, state.spec.in_features, generator=g, device=device).to(torch.bfloat16)
+                first = decoder.backend.linear(x, prepared[role])
+                again = decoder.backend.linear(x, prepared[role])
+                replay_ok &= bool(torch.equal(first, again))
+                err = _rel_l2(first, x.double() @ w64.T)
+                if err > worst:
+                    worst, worst_name = err, state.spec.name
+                module = getattr(block.self_attn if role in ("q_proj", "k_proj", "v_proj", "o_proj") else block.mlp,
+                                 role)
+                module.weight.copy_(w64.float())
+                del w64
+        linears_s = time.perf_counter() - t0
+
+        _say("config5: validation, teacher-forced reference pass")
+        n, p = len(tokens), int(prompt.numel())
+        ids = torch.cat([prompt.to(device), torch.tensor(tokens[:-1], device=device)])
+        reference = model(input_ids=ids[None], use_cache=False).logits[0, p - 1:p - 1 + n].float()
+        del model
+        torch.cuda.empty_cache()
+
+        _say("config5: validation, the decoder's logits step by step")
+        mask = torch.ones(1, decoder.max_positions, dtype=torch.int64, device=device)
+        step = decoder.forward_step(
+            input_ids=prompt.to(device)[None], attention_mask=mask[:, :p],
+            position_ids=torch.arange(p, device=device)[None], cache_position=torch.arange(p, device=device),
+            cache=None, max_cache_length=decoder.max_positions, workload="prefill", deterministic=True)
+        rows = [step.logits[0, 0]]
+        for i, token in enumerate(tokens[:-1]):
+            pos = p + i
+            step = decoder.forward_step(
+                input_ids=torch.tensor([[token]], device=device), attention_mask=mask[:, :pos + 1],
+                position_ids=torch.tensor([[pos]], device=device), cache_position=torch.tensor([pos], device=device),
+                cache=step.cache, max_cache_length=decoder.max_positions, workload="decode", deterministic=True)
+            rows.append(step.logits[0, 0])
+
+    errs, decided, agree, reproduced = [], 0, 0, 0
+    for got, exp, token in zip(rows, reference, tokens):
+        errs.append(_rel_l2(got, exp))
+        reproduced += int(int(torch.argmax(got)) == token)
+        abs_err = float((got - exp).abs().max())
+        top2 = torch.topk(exp, 2).values
+        if float(top2[0] - top2[1]) > 2 * abs_err:
+            decided += 1
+            agree += int(int(torch.argmax(exp)) == token)
+    errs.sort()
+    linears_ok = worst <= 2e-3 and replay_ok
+    passed = linears_ok and reproduced == n and agree == decided and errs[-1] <= 5e-2
+    res = {
+        "linears": {"count": len(weights.layers) * len(ROLES), "tokens": 1, "input": "bf16 N(0,1), seeded",
+                    "reference": "fp64 reconstruction from the packed words", "worst_rel_l2": float(f"{worst:.3e}"),
+                    "worst_layer": worst_name, "bar": 2e-3, "deterministic_replay": replay_ok},
+        "greedy": {"reference": "transformers Qwen3ForCausalLM, fp32, eager attention, teacher-forced",
+                   "steps": n, "argmax_reproduces_run": reproduced, "decided": decided, "agree": agree,
+                   "logits_rel_l2": {"p50": float(f"{errs[len(errs) // 2]:.3e}"), "max": float(f"{errs[-1]:.3e}"),
+                                     "bar": 5e-2}},
+        "passed": passed,
+        "seconds": round(time.perf_counter() - t0, 1),
+        "linears_seconds": round(linears_s, 1),
+    }
+    if not passed:
+        _say("config5: VALIDATION FAILED", json.dumps(res))
+    return res
+
+
 def config5(args, device, packed_us_per_layer: float | None) -> dict:
     import torch
 
@@ -618,7 +769,6 @@ def config5(args, device, packed_us_per_layer: float | None) -> dict:
     _say("config5: building the decoder")
     weights = syn.synthetic_decoder(config, seed=syn.BASE_SEED + 5, device=device)
     decoder = PackedDecoder(config, weights, device=device, max_positions=args.e2e_prompt + args.e2e_tokens)
-    del weights
     g = torch.Generator().manual_seed(syn.BASE_SEED + 5)
     prompt = torch.randint(0, config.vocab, (args.e2e_prompt,), generator=g).to(device)
     decoder.generate_greedy(prompt, args.e2e_tokens)  # capture + warm-up
@@ -655,7 +805,9 @@ def config5(args, device, packed_us_per_layer: float | None) -> dict:
     if packed_us_per_layer is not None:
         res["packed_linear_us_per_layer"] = round(packed_us_per_layer, 2)
         res["shell_us_per_token"] = round(d["p50"] * 1e3 - packed_us_per_layer * args.layers, 1)
-    del decoder
+    if "validate" not in {s for s in args.skip.split(",") if s}:
+        res["validation"] = validate_config5(decoder, weights, config, prompt, tokens, device)
+    del decoder, weights
     torch.cuda.empty_cache()
     return res
 
@@ -960,6 +1112,8 @@ def main(argv=None) -> int:
         "config": {"workload": workload, "value_is": unit_note, "global_batch": 1, "layers": args.layers,
                    "parallelism": "single-gpu"},
     })
+    if c5 is not None and "validation" in c5:
+        result["validated"] = c5["validation"]["passed"]
     if dom is not None:
         achieved = dom["achieved_gbs"]
         result["roofline"] = {
