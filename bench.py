@@ -806,7 +806,12 @@ def config5(args, device, packed_us_per_layer: float | None) -> dict:
         res["packed_linear_us_per_layer"] = round(packed_us_per_layer, 2)
         res["shell_us_per_token"] = round(d["p50"] * 1e3 - packed_us_per_layer * args.layers, 1)
     if "validate" not in {s for s in args.skip.split(",") if s}:
-        res["validation"] = validate_config5(decoder, weights, config, prompt, tokens, device)
+        try:
+            res["validation"] = validate_config5(decoder, weights, config, prompt, tokens, device)
+        except Exception as exc:  # recorded in the line: the timed figures stand, unvalidated
+            _say("config5: validation raised", repr(exc))
+            res["validation"] = {"passed": False, "error": repr(exc)}
+            torch.cuda.empty_cache()
     del decoder, weights
     torch.cuda.empty_cache()
     return res
