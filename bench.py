@@ -6,7 +6,7 @@ Headline (``value``): median greedy-decode tok/s of a random-init
 Qwen3-8B-shaped model (36 layers, hidden 4096, intermediate 12288, GQA 32/8
 x 128, vocab 151936; all 252 projections packed binary low-rank at ~1.0 bpw,
 bf16 N(0, 0.02) embeddings / untied lm_head / KV cache), 512-id prompt, 128
-greedy tokens, batch 1, each decode step one HIP-graph replay.
+greedy tokens, batch 1, decode steps replayed from HIP graphs of eight steps.
 
 Beside it, each with p10/p50/p90 over at least 10 repetitions:
   config1  Gemma-3-1B gate 1152->6912 r768, one token;
@@ -788,7 +788,7 @@ def config5(args, device, packed_us_per_layer: float | None) -> dict:
     res = {
         "workload": (f"qwen3-8b-shape random-init packed model, {args.layers} layers, vocab {config.vocab}, "
                      f"prompt {args.e2e_prompt} ids, {args.e2e_tokens} greedy tokens, batch 1, "
-                     "bf16 activations/KV, one HIP-graph replay per decode token"),
+                     "bf16 activations/KV, decode steps replayed from HIP graphs of eight steps"),
         "decode_tok_per_s": _scaled(d, lambda ms: 1000.0 / ms, 2),
         "decode_ms_per_token": _scaled(d, lambda v: v, 4),
         "prefill_ms": _scaled(pf, lambda v: v, 3),

@@ -476,3 +476,22 @@ def test_graph_replay_matches_eager_and_forward_step():
             workload="decode", deterministic=True)
         tokens.append(int(step.logits[0, -1].argmax()))
     assert tokens == graph_tokens
+
+@pytest.mark.parametrize("new_tokens", [2, 8, 9, 17, 26])
+def test_multi_step_graphs_match_eager(new_tokens):
+    # generate_greedy replays graphs of STEPS_PER_GRAPH decode steps and the
+    # one-step graph for the remainder: every split of the steps between them
+    # gives the eager launches' tokens, and the history holds them in order.
+    from nanoquant_amd.runtime.decoder_shell import STEPS_PER_GRAPH
+
+    assert STEPS_PER_GRAPH == 8
+    weights = syn.synthetic_decoder(SMALL, seed=syn.BASE_SEED + 64)
+    decoder = PackedDecoder(SMALL, weights, device=DEV, max_positions=128)
+    prompt = torch.randint(0, SMALL.vocab, (33,), generator=_g(64))
+    _say("multi-step graphs", new_tokens)
+    eager = decoder.generate_greedy(prompt.to(DEV), new_tokens, use_graph=False).tolist()
+    graph = decoder.generate_greedy(prompt.to(DEV), new_tokens).tolist()
+    again = decoder.generate_greedy(prompt.to(DEV), new_tokens).tolist()
+    assert len(eager) == new_tokens
+    assert graph == eager == again
+    assert int(decoder.position) == 33 + new_tokens - 1
