@@ -257,9 +257,14 @@ class PackedDecoder:
         self.max_positions = int(max_positions)
         self.activation_dtype = activation_dtype
         self.cache_dtype = cache_dtype
-        # The prompt pass takes split prefill operands: its errors reach every
-        # later token through the KV cache and compound over the layers.
-        self.backend = backend or HipPackedBackend(prefill_operands="split")
+        # The prompt pass's errors reach every later token through the KV cache
+        # and compound over the layers. With fp32 activations it takes split
+        # prefill operands (an fp16 value and its fp16 remainder, about 22
+        # bits); with 16-bit activations, which the shell rounds to 8 (bf16) or
+        # 11 (fp16) bits before every linear, one fp16 operand (11 bits) adds
+        # less than that rounding and halves the prompt's MFMA work.
+        operands = "split" if activation_dtype == torch.float32 else "fp16"
+        self.backend = backend or HipPackedBackend(prefill_operands=operands)
         dev = self.device
         self.embed = weights.embed.to(dev, torch.bfloat16).contiguous()
         self.lm_head = weights.lm_head.to(dev, torch.bfloat16).contiguous()
