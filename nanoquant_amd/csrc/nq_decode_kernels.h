@@ -1119,8 +1119,11 @@ __device__ __forceinline__ void attn_merge(const S1Regs<AK, TOK, TW>& r, const L
             acc[2 * j + 1] = fmaf(hi, wgt, acc[2 * j + 1]);
         }
     }
+    // One reciprocal for the lane's eight columns (eight divisions are about
+    // ten instructions each).
+    const float inv = 1.0f / l;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) mv[i >> 2][i & 3] = in_range ? acc[i] / l : 0.0f;
+    for (int i = 0; i < 8; ++i) mv[i >> 2][i & 3] = in_range ? acc[i] * inv : 0.0f;
 }
 
 // One run's values of token t: the activations as read (with the gated kind's
