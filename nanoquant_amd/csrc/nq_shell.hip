@@ -21,7 +21,7 @@ constexpr int kWave = 64;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kSeqBlock = nq::kAttnBlockRows;  // cache rows per attention block
 constexpr int kRowThreads = 256;        // per-row kernels
-constexpr int kProjWaves = 4;           // output projection: waves per workgroup
+constexpr int kProjWaves = 4;           // output projection: waves per workgroup (2 or 8: 13% slower)
 constexpr int kProjLoads = 32;          // 16-byte weight loads per lane in flight
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
